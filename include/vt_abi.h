@@ -1,0 +1,163 @@
+/*
+ * vt_abi.h -- C ABI of libvt_hip.so, the MI355X (gfx950) VoroTracing
+ * traversal library.
+ *
+ * Plain pointers and sizes only.  All array arguments are device pointers
+ * (HBM), contiguous, in the reference layouts noted per function.  `stream`
+ * is a hipStream_t (NULL = the null stream).  Every entry returns 0 on
+ * success or a VT_ERR_* code; vt_last_error() returns the calling thread's
+ * last message.  Entries enqueue work on `stream` and do not synchronise.
+ *
+ * Reference citations are to zenseact/VoroTracing (vorotracing/cuda/csrc).
+ */
+#ifndef VT_ABI_H
+#define VT_ABI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *vt_stream_t;
+
+enum {
+    VT_OK = 0,
+    VT_ERR_INVALID = 1,     /* bad argument (message names it) */
+    VT_ERR_HIP = 2,         /* HIP runtime / launch error */
+    VT_ERR_UNSUPPORTED = 3, /* e.g. texture resolution not compiled */
+    VT_ERR_NOMEM = 4
+};
+
+enum { VT_ATTR_F32 = 0, VT_ATTR_F16 = 1 };
+
+/* Per-ray walk statistics (debug / roofline accounting).  Filled only when a
+ * non-NULL `stats` array (one record per ray, in ray order) is passed. */
+typedef struct vt_ray_stats {
+    uint32_t n;          /* value returned by the walk (trace_octmap) */
+    uint32_t visits;     /* cells whose face list was searched */
+    uint32_t faces;      /* face records read */
+    uint32_t exits;      /* exit faces found (neighbour id + next site read) */
+    uint32_t integrated; /* integrate_cell calls (t1 > t0) */
+    uint32_t shaded;     /* cells whose textures were fetched */
+    uint64_t visit_hash; /* FNV-1a 64 over the visited cell ids */
+} vt_ray_stats;
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char *vt_last_error(void);
+/* ABI version (bumped on incompatible change). */
+int vt_abi_version(void);
+
+/*
+ * Prefetch of per-face site offsets.  Replaces _C.trace_vorotracing_prefetch_adj
+ * (tracing_octmap.cu:612-640, kernel :125-149).
+ *   points (num_points,3) f32; adjacency u32 (adjacency_size, including the
+ *   32-entry padding); offsets u32 (num_points+1).
+ *   adj_diff out: f16 (adjacency_size+32, 4) = half(site[adj[e]] - site[i]), w = 0.
+ *   Rows past offsets[num_points] are zero-filled.
+ */
+int vt_prefetch_adj(const float *points, uint32_t num_points, const uint32_t *adjacency, uint32_t adjacency_size,
+                    const uint32_t *offsets, uint16_t *adj_diff, vt_stream_t stream);
+
+/*
+ * fp16 inference render.  Replaces _C.trace_vorotracing_infer
+ * (tracing_octmap.cu:642-717, kernel :552-610).
+ *   diffuse/specular: Half4Texel maps, f16 (num_points, 4*R*R), R = diff_res /
+ *   spec_res in {4, 8}.  density f32 (num_points).  adj_diff from
+ *   vt_prefetch_adj.  rays f32 (num_rays, 6).  start_point u32 (num_rays).
+ *   ray_perm u32 (num_rays) or NULL: lane t renders ray ray_perm[t].
+ *   rgba out: f16 (num_rays, 4) in ray order.  stats: NULL or (num_rays).
+ */
+int vt_trace_infer_f16(const float *points, const uint16_t *diffuse, const uint16_t *specular, uint32_t diff_res,
+                       uint32_t spec_res, const float *density, const uint32_t *adjacency, const uint32_t *offsets,
+                       uint32_t num_points, const uint16_t *adj_diff, const float *rays, uint32_t num_rays,
+                       const uint32_t *start_point, const uint32_t *ray_perm, float weight_threshold,
+                       uint32_t max_intersections, float cell_skip_threshold, uint16_t *rgba, vt_ray_stats *stats,
+                       vt_stream_t stream);
+
+/*
+ * fp16 inference over image batches with in-kernel wave tiling: rays are
+ * (num_images, image_h, image_w, 6) and each 64-lane wave renders one
+ * tile_w x tile_h screen tile (tile_w * tile_h == 64), so no permutation
+ * buffer is read.  Results are identical to vt_trace_infer_f16 (the lane
+ * assignment never changes per-ray results, vorotracing.py:606-625).
+ */
+int vt_trace_infer_f16_tiled(const float *points, const uint16_t *diffuse, const uint16_t *specular,
+                             uint32_t diff_res, uint32_t spec_res, const float *density, const uint32_t *adjacency,
+                             const uint32_t *offsets, uint32_t num_points, const uint16_t *adj_diff,
+                             const float *rays, uint32_t num_images, uint32_t image_h, uint32_t image_w,
+                             uint32_t tile_h, uint32_t tile_w, const uint32_t *start_point, float weight_threshold,
+                             uint32_t max_intersections, float cell_skip_threshold, uint16_t *rgba,
+                             vt_ray_stats *stats, vt_stream_t stream);
+
+/*
+ * q8 inference render.  Replaces _C.trace_vorotracing_infer_q8
+ * (tracing_octmap.cu:781-854, kernel :723-779).
+ *   diffuse/specular u8 (num_points, 3*R*R); dequant = scale[c]*q + offset[c]
+ *   per RGB channel c (the reference's per-tensor pair = 3 equal values).
+ *   ray_perm: u32 or NULL (the reference has none; NULL reproduces it).
+ */
+int vt_trace_infer_q8(const float *points, const uint8_t *diffuse, const uint8_t *specular, uint32_t diff_res,
+                      uint32_t spec_res, const float diff_scale[3], const float diff_offset[3],
+                      const float spec_scale[3], const float spec_offset[3], const float *density,
+                      const uint32_t *adjacency, const uint32_t *offsets, uint32_t num_points,
+                      const uint16_t *adj_diff, const float *rays, uint32_t num_rays, const uint32_t *start_point,
+                      const uint32_t *ray_perm, float weight_threshold, uint32_t max_intersections,
+                      float cell_skip_threshold, uint16_t *rgba, vt_ray_stats *stats, vt_stream_t stream);
+
+/*
+ * Training forward.  Replaces _C.trace_vorotracing_fwd
+ * (tracing_octmap.cu:346-546, kernel :151-230).  Runs the prefetch into
+ * `adj_diff_workspace` ((adjacency_size+32)*4 halves) as the reference does
+ * on every call, then the traversal.
+ *   attr_dtype VT_ATTR_F32 / VT_ATTR_F16 for diffuse/specular (num_points,
+ *   3*R*R), rgba (num_rays,4) and contribution (num_points).
+ *   depth_quantiles f32 (num_rays, K) or NULL (K ignored); depth f32 and
+ *   depth_idx u32 (num_rays, K) outputs when quantiles are given.
+ *   contribution: NULL or zero-initialised (num_points), accumulated.
+ *   num_intersections u32, distortion/W_total/S_total/t_far f32 (num_rays).
+ */
+int vt_trace_fwd(int attr_dtype, const float *points, const void *diffuse, const void *specular, uint32_t diff_res,
+                 uint32_t spec_res, const float *density, const uint32_t *adjacency, uint32_t adjacency_size,
+                 const uint32_t *offsets, uint32_t num_points, const float *rays, uint32_t num_rays,
+                 const uint32_t *start_point, uint32_t num_quantiles, const float *depth_quantiles,
+                 float weight_threshold, uint32_t max_intersections, void *rgba, float *depth, uint32_t *depth_idx,
+                 void *contribution, uint32_t *num_intersections, float *distortion, float *W_total,
+                 float *S_total, float *t_far, uint16_t *adj_diff_workspace, vt_ray_stats *stats,
+                 vt_stream_t stream);
+
+/*
+ * Training backward.  Replaces _C.trace_vorotracing_bwd
+ * (tracing_octmap.cu:860-1103, kernel :232-340).  Prefetch into the
+ * workspace as in vt_trace_fwd, then the re-walk with gradient scatter.
+ *   rgba / rgba_grad: attr dtype (num_rays, 4).  depth_quantiles, depth_idx,
+ *   depth_grad (num_rays, K) or NULL.  ray_error: attr dtype (num_rays) or
+ *   NULL.  distortion, W_total, S_total, t_far: f32 (num_rays);
+ *   distortion_grad f32 (num_rays) or NULL.
+ *   Outputs (caller zero-initialises): points_grad f32 (num_points,3),
+ *   diffuse_grad / specular_grad attr dtype, density_grad f32 (num_points),
+ *   point_error attr dtype (num_points) or NULL.
+ */
+int vt_trace_bwd(int attr_dtype, const float *points, const void *diffuse, const void *specular, uint32_t diff_res,
+                 uint32_t spec_res, const float *density, const uint32_t *adjacency, uint32_t adjacency_size,
+                 const uint32_t *offsets, uint32_t num_points, const float *rays, uint32_t num_rays,
+                 const uint32_t *start_point, const void *rgba, const void *rgba_grad, uint32_t num_quantiles,
+                 const float *depth_quantiles, const uint32_t *depth_idx, const float *depth_grad,
+                 const void *ray_error, float contribution_alpha_grad, const float *distortion,
+                 const float *distortion_grad, const float *W_total, const float *S_total, const float *t_far,
+                 float weight_threshold, uint32_t max_intersections, float *points_grad, void *diffuse_grad,
+                 void *specular_grad, float *density_grad, void *point_error, uint16_t *adj_diff_workspace,
+                 vt_ray_stats *stats, vt_stream_t stream);
+
+/*
+ * Self-test of the device arithmetic shared by restatement with the CPU
+ * checker (no reference counterpart): op 0 = exp, 1 = log, 2 = f32->f16 bits
+ * (out as u16 in the low half of each u32), applied elementwise to n floats.
+ */
+int vt_math_probe(int op, const float *in, uint32_t *out, uint32_t n, vt_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,59 @@
+"""Shared test helpers: scenes as device tensors, oracle calls on the same inputs."""
+from __future__ import annotations
+
+import functools
+
+import numpy as np
+import torch
+
+from oracle import core, host_ops
+from vorotracing_amd import camera, scene
+
+
+@functools.lru_cache(maxsize=None)
+def c1_scene():
+    return scene.config1()
+
+
+@functools.lru_cache(maxsize=None)
+def mini_heightfield(n=40000, seed=3):
+    """Config-3 distribution at test size (same generator, 3% of the sites)."""
+    return scene.heightfield(seed=seed, n=n, name="mini_c3")
+
+
+@functools.lru_cache(maxsize=None)
+def small_random(n=600, seed=7, R=4, Rs=None, grid=None):
+    return scene.random_scene(n, seed=seed, R=R, Rs=Rs, grid=grid)
+
+
+def start_for(s, rays):
+    """Nearest site of each ray origin (brute force), as uint32 [...]."""
+    o = rays[..., :3].reshape(-1, 3)
+    uo, inv = np.unique(o, axis=0, return_inverse=True)
+    nn = host_ops.nearest_site(s.points, uo)
+    return nn[inv.reshape(-1)].astype(np.uint32).reshape(rays.shape[:-1])
+
+
+def to_dev(a, dev, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.to(dev)
+
+
+def f16_maps(s):
+    return (host_ops.pad_3to4(s.diffuse.astype(np.float16), s.diff_res),
+            host_ops.pad_3to4(s.specular.astype(np.float16), s.spec_res))
+
+
+def stats_np(t: torch.Tensor):
+    """(num_rays, 8) u32 device tensor -> numpy structured stats."""
+    a = t.cpu().numpy().view(np.uint32).reshape(-1, 8)
+    return np.ascontiguousarray(a).view(core.STATS_DTYPE).reshape(-1)
+
+
+def assert_stats_equal(got, want):
+    for k in ("n", "visits", "faces", "exits", "integrated", "shaded", "visit_hash"):
+        bad = np.nonzero(got[k] != want[k])[0]
+        assert bad.size == 0, f"stats field {k} differs on {bad.size} rays, first {bad[:5]}: " \
+                              f"{got[k][bad[:5]]} vs {want[k][bad[:5]]}"

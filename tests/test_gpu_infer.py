@@ -1,0 +1,188 @@
+"""GPU parity of the inference path against the CPU oracle (bit-exact).
+
+The device arithmetic restates the oracle's op for op, so visited-cell
+sequences (hash + counters), RGBA bits and per-ray statistics must be
+identical.  The north star's tolerance (2e-3 for fp16/q8) is asserted as
+well, so a failure of bit-exactness alone is distinguishable from a real
+error.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import core, host_ops
+from tests import helpers as H
+from vorotracing_amd import _C, camera, native
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev_scene(s, dev):
+    d4, s4 = H.f16_maps(s)
+    return dict(points=H.to_dev(s.points, dev), diffuse4=H.to_dev(d4, dev), specular4=H.to_dev(s4, dev),
+                density=H.to_dev(s.density.reshape(-1), dev), adjacency=H.to_dev(s.adjacency, dev),
+                offsets=H.to_dev(s.offsets, dev))
+
+
+def test_math_probe_exp_log_f16(gpu):
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.uniform(-110, 90, 1 << 20).astype(np.float32),
+                        (rng.standard_normal(1 << 18) * 3).astype(np.float32),
+                        np.array([0.0, -0.0, 1e-30, -1e-30, 88.7, 88.73, -87.3, -103.9, -104.0, np.inf, -np.inf,
+                                  np.nan], np.float32)])
+    xd = torch.from_numpy(x).to(gpu)
+    got = native.math_probe(0, xd).cpu().numpy().view(np.float32)
+    want = core.expf(x)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    xl = np.abs(x)
+    xl = np.concatenate([xl, rng.uniform(1e-38, 1e-30, 4096).astype(np.float32), np.float32([1e-44, 1.0, 2.0])])
+    got = native.math_probe(1, torch.from_numpy(xl).to(gpu)).cpu().numpy().view(np.float32)
+    want = core.logf(xl)
+    ok = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
+    assert ok.all()
+    xf = np.concatenate([x, rng.uniform(-70000, 70000, 1 << 16).astype(np.float32),
+                         (rng.standard_normal(1 << 16) * 1e-5).astype(np.float32)])
+    got = native.math_probe(2, torch.from_numpy(xf).to(gpu)).cpu().numpy().astype(np.uint16)
+    want = core.f32_to_f16_bits(xf)
+    nan = np.isnan(xf)
+    assert np.array_equal(got[~nan], want[~nan])
+
+
+@pytest.mark.parametrize("which", ["c1", "mini_c3"])
+def test_prefetch_bit_exact(gpu, which):
+    s = H.c1_scene() if which == "c1" else H.mini_heightfield()
+    d = _dev_scene(s, gpu)
+    got = _C.trace_vorotracing_prefetch_adj(d["points"], d["adjacency"], d["offsets"]).cpu().numpy()
+    want = core.prefetch_adj(s.points, s.adjacency, s.offsets)
+    m = s.num_faces
+    assert got.shape == (s.adjacency.shape[0] + 32, 4)
+    assert np.array_equal(got[:m].view(np.uint16), want[:m].view(np.uint16))
+    assert not got[m:].view(np.uint16).any()  # padding rows zero-filled
+
+
+def _c1_rays(W=128, Hh=128):
+    return camera.pinhole_rays(W, Hh, eye=(0.0, -4.0, 0.0))
+
+
+@pytest.mark.parametrize("mode", ["linear", "perm48", "perm88", "tiled88"])
+def test_infer_f16_c1_bit_exact(gpu, mode):
+    s = H.c1_scene()
+    rays = _c1_rays()
+    start = H.start_for(s, rays)
+    d = _dev_scene(s, gpu)
+    adj = native.prefetch(d["points"], d["adjacency"], d["offsets"])
+    d4, s4 = H.f16_maps(s)
+    want, wst, _ = core.trace_infer_f16(s.points, d4, s4, 4, 4, s.density, s.adjacency, s.offsets,
+                                        adj.cpu().numpy(), rays, start, weight_threshold=0.01, want_stats=True)
+    rays_d = H.to_dev(rays, gpu)
+    start_d = H.to_dev(start, gpu)
+    stats = native.new_stats(rays.shape[0] * rays.shape[1], gpu)
+    perm = None
+    tiled = None
+    if mode == "perm48":
+        perm = H.to_dev(host_ops.tile_perm(128, 128, 4, 8).view(np.uint32), gpu)
+    elif mode == "perm88":
+        perm = H.to_dev(host_ops.tile_perm(128, 128, 8, 8).view(np.uint32), gpu)
+    elif mode == "tiled88":
+        tiled = (8, 8)
+    got = native.infer_f16(d["points"], d["diffuse4"], d["specular4"], d["density"], d["adjacency"], d["offsets"],
+                           adj, rays_d, start_d, ray_perm=perm, weight_threshold=0.01, stats=stats, tiled=tiled)
+    torch.cuda.synchronize()
+    H.assert_stats_equal(H.stats_np(stats), wst)
+    g = got.cpu().numpy()
+    assert np.abs(g.astype(np.float32) - want.astype(np.float32)).max() <= 2e-3
+    assert np.array_equal(g.view(np.uint16), want.view(np.uint16))
+
+
+def test_infer_f16_reference_surface(gpu):
+    """_C.trace_vorotracing_infer with the reference arguments (int32 tile perm)."""
+    s = H.c1_scene()
+    rays = _c1_rays(96, 64)
+    start = H.start_for(s, rays)
+    d = _dev_scene(s, gpu)
+    adj = _C.trace_vorotracing_prefetch_adj(d["points"], d["adjacency"], d["offsets"])
+    perm = H.to_dev(host_ops.tile_perm(64, 96, 4, 8), gpu)
+    got = _C.trace_vorotracing_infer(d["points"], d["diffuse4"], d["specular4"], d["density"], d["adjacency"],
+                                     d["offsets"], H.to_dev(rays, gpu), H.to_dev(start, gpu), adj, perm, 0.01, 1024,
+                                     0.0)
+    d4, s4 = H.f16_maps(s)
+    want, _, _ = core.trace_infer_f16(s.points, d4, s4, 4, 4, s.density, s.adjacency, s.offsets,
+                                      adj.cpu().numpy(), rays, start, weight_threshold=0.01)
+    assert got.shape == (64, 96, 4) and got.dtype == torch.float16
+    assert np.array_equal(got.cpu().numpy().view(np.uint16), want.view(np.uint16))
+
+
+@pytest.mark.parametrize("R", [4, 8])
+def test_infer_f16_mini_c3_skip(gpu, R):
+    """Config-3 distribution (heightfield, skip gate 1e-3, thr 0.01) on two orbit poses."""
+    s = H.mini_heightfield() if R == 4 else H.small_random(3000, seed=11, R=8, Rs=4)
+    d = _dev_scene(s, gpu)
+    adj = native.prefetch(d["points"], d["adjacency"], d["offsets"])
+    d4, s4 = H.f16_maps(s)
+    adj_np = adj.cpu().numpy()
+    for k in (0, 9):
+        rays = camera.orbit_rays(k, 160, 120)
+        start = H.start_for(s, rays)
+        want, wst, _ = core.trace_infer_f16(s.points, d4, s4, s.diff_res, s.spec_res, s.density, s.adjacency,
+                                            s.offsets, adj_np, rays, start, weight_threshold=0.01,
+                                            cell_skip_threshold=1e-3, want_stats=True)
+        stats = native.new_stats(rays.shape[0] * rays.shape[1], gpu)
+        got = native.infer_f16(d["points"], d["diffuse4"], d["specular4"], d["density"], d["adjacency"],
+                               d["offsets"], adj, H.to_dev(rays, gpu), H.to_dev(start, gpu), weight_threshold=0.01,
+                               cell_skip_threshold=1e-3, stats=stats, tiled=(8, 8))
+        torch.cuda.synchronize()
+        H.assert_stats_equal(H.stats_np(stats), wst)
+        assert np.array_equal(got.cpu().numpy().view(np.uint16), want.view(np.uint16))
+
+
+@pytest.mark.parametrize("per_channel", [False, True])
+def test_infer_q8_bit_exact(gpu, per_channel):
+    s = H.mini_heightfield()
+    dq, dsc, dof = host_ops.quantize_u8(s.diffuse, per_channel)
+    sq, ssc, sof = host_ops.quantize_u8(s.specular, per_channel)
+    d = _dev_scene(s, gpu)
+    adj = native.prefetch(d["points"], d["adjacency"], d["offsets"])
+    rays = camera.orbit_rays(3, 128, 96)
+    start = H.start_for(s, rays)
+    want, wst = core.trace_infer_q8(s.points, dq, sq, 4, 4, dsc, dof, ssc, sof, s.density, s.adjacency, s.offsets,
+                                    adj.cpu().numpy(), rays, start, weight_threshold=0.01, cell_skip_threshold=1e-3,
+                                    want_stats=True)
+    stats = native.new_stats(rays.shape[0] * rays.shape[1], gpu)
+    got = native.infer_q8(d["points"], H.to_dev(dq, gpu), H.to_dev(sq, gpu),
+                          (np.broadcast_to(dsc, 3), np.broadcast_to(dof, 3), np.broadcast_to(ssc, 3),
+                           np.broadcast_to(sof, 3)),
+                          d["density"], d["adjacency"], d["offsets"], adj, H.to_dev(rays, gpu),
+                          H.to_dev(start, gpu), weight_threshold=0.01, cell_skip_threshold=1e-3, stats=stats)
+    torch.cuda.synchronize()
+    H.assert_stats_equal(H.stats_np(stats), wst)
+    assert np.array_equal(got.cpu().numpy().view(np.uint16), want.view(np.uint16))
+
+
+def test_infer_errors_reference_messages(gpu):
+    s = H.c1_scene()
+    d = _dev_scene(s, gpu)
+    rays = H.to_dev(_c1_rays(8, 8), gpu)
+    start = torch.zeros((8, 8), dtype=torch.uint32, device=gpu)
+    adj = _C.trace_vorotracing_prefetch_adj(d["points"], d["adjacency"], d["offsets"])
+    empty = torch.empty(0, dtype=torch.int32, device=gpu)
+    args = [d["points"], d["diffuse4"], d["specular4"], d["density"], d["adjacency"], d["offsets"], rays, start, adj,
+            empty, 0.01, 1024, 0.0]
+    bad = list(args)
+    bad[1] = d["diffuse4"].float()
+    with pytest.raises(RuntimeError, match="inference kernel requires float16 diffuse"):
+        _C.trace_vorotracing_infer(*bad)
+    bad = list(args)
+    bad[7] = start.to(torch.int32)
+    with pytest.raises(RuntimeError, match="start_point must have uint32 dtype"):
+        _C.trace_vorotracing_infer(*bad)
+    bad = list(args)
+    bad[5] = d["offsets"][:-1]
+    with pytest.raises(RuntimeError, match="point_adjacency_offsets must have num_points"):
+        _C.trace_vorotracing_infer(*bad)
+    bad = list(args)
+    bad[0] = d["points"].double()
+    with pytest.raises(RuntimeError, match="points had dtype Double, expected float32"):
+        _C.trace_vorotracing_infer(*bad)
+    # empty ray batch is a no-op (kernel_utils.cuh:31-34)
+    out = _C.trace_vorotracing_infer(*(args[:6] + [rays[:0], start[:0], adj, empty, 0.01, 1024, 0.0]))
+    assert out.shape == (0, 8, 4)

@@ -1,0 +1,438 @@
+"""The reference's ``_C`` operator module, backed by libvt_hip.so.
+
+Same functions, argument order, return tuples, validation order and error
+messages as vorotracing/cuda/csrc/ext.cpp:11-34 (declarations
+tracing_octmap.h:11-91, nn_bvh.h:4-16).  Inputs are made contiguous,
+outputs are allocated with torch on the input device, and kernels are
+enqueued on torch's current stream (the reference uses the legacy default
+stream, tracing_octmap.cu:460-461; under default usage the two coincide).
+Failed checks raise RuntimeError with the reference's message.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Sequence, Union
+
+import torch
+
+from . import _lib
+
+_C10_NAMES = {
+    torch.float32: "Float", torch.float64: "Double", torch.float16: "Half", torch.bfloat16: "BFloat16",
+    torch.int32: "Int", torch.int64: "Long", torch.int16: "Short", torch.int8: "Char", torch.uint8: "Byte",
+    torch.bool: "Bool", torch.uint32: "UInt32", torch.uint16: "UInt16", torch.uint64: "UInt64",
+}
+
+MAX_MAP_RES = (4, 8)
+
+
+def _assert(cond, msg):
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _is_gpu(t: torch.Tensor) -> bool:
+    return t.device.type == "cuda"
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def validate_scene_data(points, attributes, point_adjacency, point_adjacency_offsets):
+    """validations.h:17-66, same order and messages."""
+    if points.size(-1) != 3:
+        raise RuntimeError(f"points had dimension {points.size(-1)} along axis -1, expected 3")
+    if points.dtype != torch.float32:
+        raise RuntimeError(f"points had dtype {_C10_NAMES.get(points.dtype, str(points.dtype))}, expected float32")
+    if not _is_gpu(points):
+        raise RuntimeError("points must be on CUDA device")
+    num_points = points.numel() // 3
+    if not _is_gpu(attributes):
+        raise RuntimeError("attributes must be on CUDA device")
+    if point_adjacency_offsets.dtype != torch.uint32:
+        raise RuntimeError("point_adjacency_offsets must have uint32 dtype")
+    if not _is_gpu(point_adjacency_offsets):
+        raise RuntimeError("point_adjacency_offsets must be on CUDA device")
+    if point_adjacency_offsets.numel() != num_points + 1:
+        raise RuntimeError("point_adjacency_offsets must have num_points + 1 elements")
+    if point_adjacency.dtype != torch.uint32:
+        raise RuntimeError("point_adjacency must have uint32 dtype")
+    if not _is_gpu(point_adjacency):
+        raise RuntimeError("point_adjacency must be on CUDA device")
+
+
+def _map_res(width: int, channels: int, what: str) -> int:
+    r = int(round(math.sqrt(width / channels))) if width > 0 else 0
+    if r * r * channels != width or r not in MAX_MAP_RES:
+        raise RuntimeError(
+            f"{what} width {width} is not {channels}*R*R for a compiled octahedral resolution R in {MAX_MAP_RES}")
+    return r
+
+
+def _u32_view(t: torch.Tensor) -> torch.Tensor:
+    """int32 -> uint32 reinterpretation (the reference reads ray_perm int32 as u32)."""
+    if t.dtype == torch.int32:
+        return t.view(torch.uint32)
+    return t
+
+
+def trace_vorotracing_prefetch_adj(points_in, point_adjacency_in, point_adjacency_offsets_in):
+    """tracing_octmap.cu:612-640: f16 (adjacency_size + 32, 4) per-face site offsets."""
+    points = points_in.contiguous()
+    adjacency = point_adjacency_in.contiguous()
+    offsets = point_adjacency_offsets_in.contiguous()
+    num_points = points.size(0)
+    adjacency_size = adjacency.size(0)
+    adj_diff = torch.empty((adjacency_size + 32, 4), dtype=torch.float16, device=points.device)
+    with torch.cuda.device(points.device):
+        _lib.call("vt_prefetch_adj", points.data_ptr(), num_points, adjacency.data_ptr(), adjacency_size,
+                  offsets.data_ptr(), adj_diff.data_ptr(), _stream(points.device))
+    return adj_diff
+
+
+def _out_shape(rays, last):
+    return list(rays.shape[:-1]) + [last]
+
+
+def trace_vorotracing_infer(points_in, diffuse_in, specular_in, density_in, point_adjacency_in,
+                            point_adjacency_offsets_in, rays_in, start_point_in, adjacent_diff_in, ray_perm_in,
+                            weight_threshold: float, max_intersections: int, cell_skip_threshold: float):
+    """tracing_octmap.cu:642-717 (fp16 Half4Texel inference).  Returns f16 [..., 4]."""
+    points = points_in.contiguous()
+    ray_perm = _u32_view(ray_perm_in.contiguous())
+    diffuse = diffuse_in.contiguous()
+    specular = specular_in.contiguous()
+    density = density_in.contiguous()
+    adjacency = point_adjacency_in.contiguous()
+    offsets = point_adjacency_offsets_in.contiguous()
+    rays = rays_in.contiguous()
+    start_point = start_point_in.contiguous()
+    adjacent_diff = adjacent_diff_in.contiguous()
+    validate_scene_data(points_in, diffuse_in, point_adjacency_in, point_adjacency_offsets_in)
+    num_points = points.size(0)
+    num_rays = rays.numel() // 6
+    _assert(diffuse.dtype == torch.float16, "inference kernel requires float16 diffuse")
+    _assert(specular.dtype == torch.float16, "inference kernel requires float16 specular")
+    _assert(density.dtype == torch.float32, "density must have float32 dtype")
+    _assert(rays.dtype == torch.float32, "rays must have float32 dtype")
+    _assert(start_point.dtype == torch.uint32, "start_point must have uint32 dtype")
+    _check_infer_shapes(num_points, num_rays, diffuse, specular, density, start_point, adjacent_diff, adjacency)
+    rd = _map_res(diffuse.shape[-1], 4, "diffuse")
+    rs = _map_res(specular.shape[-1], 4, "specular")
+    if ray_perm.numel():
+        _assert(ray_perm.numel() == num_rays, "ray_perm must be empty or have one entry per ray")
+        _assert(ray_perm.dtype == torch.uint32, "ray_perm must have int32 or uint32 dtype")
+    out = torch.empty(_out_shape(rays, 4), dtype=torch.float16, device=rays.device)
+    if num_rays == 0:
+        return out
+    with torch.cuda.device(rays.device):
+        _lib.call("vt_trace_infer_f16", points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd, rs,
+                  density.data_ptr(), adjacency.data_ptr(), offsets.data_ptr(), num_points,
+                  adjacent_diff.data_ptr(), rays.data_ptr(), num_rays, start_point.data_ptr(),
+                  ray_perm.data_ptr() if ray_perm.numel() else None, float(weight_threshold),
+                  int(max_intersections), float(cell_skip_threshold), out.data_ptr(), None, _stream(rays.device))
+    return out
+
+
+def _check_infer_shapes(num_points, num_rays, diffuse, specular, density, start_point, adjacent_diff, adjacency):
+    # The reference does not check these (Appendix: the infer entries validate
+    # dtypes only); out-of-range sizes would read out of bounds, so they are
+    # checked here.
+    _assert(diffuse.size(0) == num_points and specular.size(0) == num_points and density.numel() == num_points,
+            "diffuse, specular, density must each have num_points rows")
+    _assert(start_point.numel() == num_rays, "start_point must have the same batch size as rays")
+    _assert(adjacent_diff.dim() == 2 and adjacent_diff.size(1) == 4 and adjacent_diff.dtype == torch.float16,
+            "adjacent_diff must be float16 (adjacency_size + 32, 4)")
+    _assert(adjacent_diff.size(0) >= adjacency.size(0) + 4, "adjacent_diff has fewer rows than adjacency + padding")
+    _assert(adjacency.numel() >= 4, "point_adjacency must carry the 32-entry padding")
+
+
+def trace_vorotracing_infer_q8(points_in, diffuse_in, specular_in, density_in, point_adjacency_in,
+                               point_adjacency_offsets_in, rays_in, start_point_in, adjacent_diff_in,
+                               diff_scale: Union[float, Sequence[float]], diff_offset, spec_scale, spec_offset,
+                               weight_threshold: float, max_intersections: int, cell_skip_threshold: float,
+                               ray_perm_in: Optional[torch.Tensor] = None):
+    """tracing_octmap.cu:781-854 (q8 inference).  Scale/offset may be floats
+    (the reference's per-tensor pair) or 3-sequences (per RGB channel).
+    ``ray_perm_in`` is an extension (the reference has none); None/empty
+    reproduces the reference."""
+    points = points_in.contiguous()
+    diffuse = diffuse_in.contiguous()
+    specular = specular_in.contiguous()
+    density = density_in.contiguous()
+    adjacency = point_adjacency_in.contiguous()
+    offsets = point_adjacency_offsets_in.contiguous()
+    rays = rays_in.contiguous()
+    start_point = start_point_in.contiguous()
+    adjacent_diff = adjacent_diff_in.contiguous()
+    validate_scene_data(points_in, diffuse_in, point_adjacency_in, point_adjacency_offsets_in)
+    num_points = points.size(0)
+    num_rays = rays.numel() // 6
+    _assert(diffuse.dtype == torch.uint8, "q8 inference kernel requires uint8 diffuse")
+    _assert(specular.dtype == torch.uint8, "q8 inference kernel requires uint8 specular")
+    _assert(density.dtype == torch.float32, "density must have float32 dtype")
+    _assert(rays.dtype == torch.float32, "rays must have float32 dtype")
+    _assert(start_point.dtype == torch.uint32, "start_point must have uint32 dtype")
+    _check_infer_shapes(num_points, num_rays, diffuse, specular, density, start_point, adjacent_diff, adjacency)
+    rd = _map_res(diffuse.shape[-1], 3, "diffuse")
+    rs = _map_res(specular.shape[-1], 3, "specular")
+    perm = None
+    if ray_perm_in is not None and ray_perm_in.numel():
+        perm = _u32_view(ray_perm_in.contiguous())
+        _assert(perm.numel() == num_rays and perm.dtype == torch.uint32, "ray_perm must have one entry per ray")
+
+    import ctypes as C
+
+    def v3(x):
+        vals = [float(x)] * 3 if isinstance(x, (int, float)) else [float(v) for v in torch.as_tensor(x).reshape(-1)]
+        _assert(len(vals) == 3, "dequantisation scale/offset must be a float or 3 values")
+        return (C.c_float * 3)(*vals)
+
+    ds, do, ss, so = v3(diff_scale), v3(diff_offset), v3(spec_scale), v3(spec_offset)
+    out = torch.empty(_out_shape(rays, 4), dtype=torch.float16, device=rays.device)
+    if num_rays == 0:
+        return out
+    with torch.cuda.device(rays.device):
+        _lib.call("vt_trace_infer_q8", points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd, rs,
+                  C.cast(ds, C.c_void_p), C.cast(do, C.c_void_p), C.cast(ss, C.c_void_p), C.cast(so, C.c_void_p),
+                  density.data_ptr(), adjacency.data_ptr(), offsets.data_ptr(), num_points,
+                  adjacent_diff.data_ptr(), rays.data_ptr(), num_rays, start_point.data_ptr(), _ptr(perm),
+                  float(weight_threshold), int(max_intersections), float(cell_skip_threshold), out.data_ptr(), None,
+                  _stream(rays.device))
+    return out
+
+
+def _check_train_common(points, diffuse, specular, density, rays, start_point, num_points, num_rays):
+    """tracing_octmap.cu:386-398 (fwd) / :903-915 (bwd)."""
+    _assert(diffuse.dtype == specular.dtype, "diffuse and specular must have the same dtype")
+    _assert(diffuse.size(0) == specular.size(0) and diffuse.size(0) == density.size(0)
+            and diffuse.size(0) == num_points, "diffuse, specular, density must each have num_points rows")
+    _assert(density.dtype == torch.float32, "density must have float32 dtype")
+    _assert(rays.size(-1) == 6, "rays must have 6 as the last dimension")
+    _assert(rays.dtype == torch.float32, "rays must have float32 dtype")
+    _assert(_is_gpu(rays), "rays must be on CUDA device")
+    _assert(start_point.numel() == num_rays, "start_point must have the same batch size as rays")
+    _assert(start_point.dtype == torch.uint32, "start_point must have uint32 dtype")
+    _assert(_is_gpu(start_point), "start_point must be on CUDA device")
+
+
+def _attr_code(dtype):
+    if dtype == torch.float32:
+        return 0
+    if dtype == torch.float16:
+        return 1
+    raise RuntimeError("Unsupported color dtype. Only float32 and float16 are supported.")
+
+
+def trace_vorotracing_fwd(points_in, diffuse_in, specular_in, density_in, point_adjacency_in,
+                          point_adjacency_offsets_in, rays_in, start_point_in, depth_quantiles_in,
+                          weight_threshold: float, max_intersections: int, return_contribution: bool):
+    """tracing_octmap.cu:346-546.  Returns (rgba, depth, depth_idx,
+    contribution, n, distortion, W_total, S_total, t_far); absent outputs are
+    None."""
+    points = points_in.contiguous()
+    diffuse = diffuse_in.contiguous()
+    specular = specular_in.contiguous()
+    density = density_in.contiguous()
+    adjacency = point_adjacency_in.contiguous()
+    offsets = point_adjacency_offsets_in.contiguous()
+    rays = rays_in.contiguous()
+    start_point = start_point_in.contiguous()
+    validate_scene_data(points_in, diffuse_in, point_adjacency_in, point_adjacency_offsets_in)
+    return_depth = depth_quantiles_in is not None
+    num_points = points.size(0)
+    adjacency_size = adjacency.size(0)
+    num_rays = rays.numel() // 6
+    K = 0
+    _check_train_common(points, diffuse, specular, density, rays, start_point, num_points, num_rays)
+    depth_quantiles = None
+    if return_depth:
+        depth_quantiles = depth_quantiles_in.contiguous()
+        K = depth_quantiles.size(-1)
+        _assert(depth_quantiles.dtype == torch.float32, "depth_quantiles must have float32 dtype")
+        _assert(_is_gpu(depth_quantiles), "depth_quantiles must be on CUDA device")
+        _assert(K > 0 and depth_quantiles.numel() // K == num_rays,
+                "depth_quantiles must have the same batch size as rays")
+    code = _attr_code(diffuse.dtype)
+    rd = _map_res(diffuse.shape[-1], 3, "diffuse")
+    rs = _map_res(specular.shape[-1], 3, "specular")
+    dev = rays.device
+    rgba = torch.empty(_out_shape(rays, 4), dtype=diffuse.dtype, device=dev)
+    n = torch.empty(_out_shape(rays, 1), dtype=torch.uint32, device=dev)
+    contribution = torch.zeros((num_points, 1), dtype=diffuse.dtype, device=dev) if return_contribution else None
+    depth = depth_idx = None
+    if return_depth:
+        depth = torch.zeros(_out_shape(rays, K), dtype=torch.float32, device=dev)
+        depth_idx = torch.zeros(_out_shape(rays, K), dtype=torch.uint32, device=dev)
+    f1 = _out_shape(rays, 1)
+    distortion = torch.empty(f1, dtype=torch.float32, device=dev)
+    W_total = torch.empty(f1, dtype=torch.float32, device=dev)
+    S_total = torch.empty(f1, dtype=torch.float32, device=dev)
+    t_far = torch.empty(f1, dtype=torch.float32, device=dev)
+    workspace = torch.empty((adjacency_size + 32, 4), dtype=torch.float16, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call("vt_trace_fwd", code, points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd, rs,
+                  density.data_ptr(), adjacency.data_ptr(), adjacency_size, offsets.data_ptr(), num_points,
+                  rays.data_ptr(), num_rays, start_point.data_ptr(), K, _ptr(depth_quantiles),
+                  float(weight_threshold), int(max_intersections), rgba.data_ptr(), _ptr(depth), _ptr(depth_idx),
+                  _ptr(contribution), n.data_ptr(), distortion.data_ptr(), W_total.data_ptr(), S_total.data_ptr(),
+                  t_far.data_ptr(), workspace.data_ptr(), None, _stream(dev))
+    return rgba, depth, depth_idx, contribution, n, distortion, W_total, S_total, t_far
+
+
+def trace_vorotracing_bwd(points_in, diffuse_in, specular_in, density_in, point_adjacency_in,
+                          point_adjacency_offsets_in, rays_in, start_point_in, rgb_out, rgb_grad_in,
+                          depth_quantiles_in, depth_indices_in, depth_grad_in, ray_error_in,
+                          contribution_alpha_grad: float, distortion_in, distortion_grad_in, W_total_in, S_total_in,
+                          t_far_in, weight_threshold: float, max_intersections: int):
+    """tracing_octmap.cu:860-1103.  Returns (points_grad, diffuse_grad,
+    specular_grad, density_grad, ray_grad, point_error).  ray_grad is zeros
+    (the reference returns it uninitialised and the autograd wrapper drops
+    it)."""
+    points = points_in.contiguous()
+    diffuse = diffuse_in.contiguous()
+    specular = specular_in.contiguous()
+    density = density_in.contiguous()
+    adjacency = point_adjacency_in.contiguous()
+    offsets = point_adjacency_offsets_in.contiguous()
+    rays = rays_in.contiguous()
+    start_point = start_point_in.contiguous()
+    validate_scene_data(points_in, diffuse_in, point_adjacency_in, point_adjacency_offsets_in)
+    return_depth = depth_quantiles_in is not None
+    return_error = ray_error_in is not None
+    num_points = points.size(0)
+    adjacency_size = adjacency.size(0)
+    num_rays = rays.numel() // 6
+    K = 0
+    _check_train_common(points, diffuse, specular, density, rays, start_point, num_points, num_rays)
+    rgb_grad = rgb_grad_in.contiguous()
+    _assert(rgb_grad.size(-1) == 4, "rgb_grad_in must have 4 as the last dimension")
+    _assert(rgb_grad.dtype == diffuse.dtype, "rgb_grad_in must have the same dtype as diffuse/specular")
+    _assert(_is_gpu(rgb_grad), "rgb_grad_in must be on CUDA device")
+    _assert(rgb_grad.numel() // 4 == num_rays, "rgb_grad_in must have the same batch size as rays")
+    rgb_out = rgb_out.contiguous()
+    _assert(rgb_out.dtype == diffuse.dtype and rgb_out.numel() == 4 * num_rays,
+            "rgb_out must be the forward rgba (same dtype as diffuse, 4 per ray)")
+    depth_quantiles = depth_indices = depth_grad = None
+    if return_depth:
+        depth_quantiles = depth_quantiles_in.contiguous()
+        K = depth_quantiles.size(-1)
+        _assert(depth_quantiles.dtype == torch.float32, "depth_quantiles must have float32 dtype")
+        _assert(_is_gpu(depth_quantiles), "depth_quantiles must be on CUDA device")
+        _assert(depth_quantiles.numel() == num_rays * K, "depth_quantiles must have the same batch size as rays")
+        _assert(depth_grad_in is not None, "depth_grad must be provided if depth_quantiles is provided")
+        _assert(depth_indices_in is not None, "depth_indices must be provided if depth_quantiles is provided")
+        depth_indices = depth_indices_in.contiguous()
+        _assert(depth_indices.dtype == torch.uint32, "depth_indices must have uint32 dtype")
+        _assert(_is_gpu(depth_indices), "depth_indices must be on CUDA device")
+        _assert(depth_indices.numel() == num_rays * K, "depth_indices must have the same batch size as rays")
+        depth_grad = depth_grad_in.contiguous()
+        _assert(depth_grad.size(-1) == K,
+                "depth_grad must have the same number of depth quantiles as depth_quantiles")
+        _assert(depth_grad.dtype == torch.float32, "depth_grad must have float32 dtype")
+        _assert(_is_gpu(depth_grad), "depth_grad must be on CUDA device")
+        _assert(depth_grad.numel() == num_rays * K, "depth_grad must have the same batch size as rays")
+    ray_error = point_error = None
+    dev = rays.device
+    if return_error:
+        ray_error = ray_error_in.contiguous()
+        _assert(ray_error.dtype == diffuse.dtype, "ray_error must have the same dtype as diffuse/specular")
+        _assert(_is_gpu(ray_error), "ray_error must be on CUDA device")
+        _assert(ray_error.numel() == num_rays, "ray_error must have the same batch size as rays")
+        point_error = torch.zeros((num_points, 1), dtype=diffuse.dtype, device=dev)
+    W_total = W_total_in.contiguous()
+    S_total = S_total_in.contiguous()
+    t_far = t_far_in.contiguous()
+    distortion = distortion_in.contiguous()
+    _assert(W_total.dtype == torch.float32, "W_total must have float32 dtype")
+    _assert(S_total.dtype == torch.float32, "S_total must have float32 dtype")
+    _assert(t_far.dtype == torch.float32, "t_far must have float32 dtype")
+    _assert(distortion.dtype == torch.float32, "distortion must have float32 dtype")
+    _assert(W_total.numel() == num_rays, "W_total must have the same batch size as rays")
+    _assert(S_total.numel() == num_rays, "S_total must have the same batch size as rays")
+    _assert(t_far.numel() == num_rays, "t_far must have the same batch size as rays")
+    _assert(distortion.numel() == num_rays, "distortion must have the same batch size as rays")
+    distortion_grad = None
+    if distortion_grad_in is not None:
+        distortion_grad = distortion_grad_in.contiguous()
+        _assert(distortion_grad.dtype == torch.float32, "distortion_grad must have float32 dtype")
+        _assert(distortion_grad.numel() == num_rays, "distortion_grad must have the same batch size as rays")
+    code = _attr_code(diffuse.dtype)
+    rd = _map_res(diffuse.shape[-1], 3, "diffuse")
+    rs = _map_res(specular.shape[-1], 3, "specular")
+    diffuse_grad = torch.zeros_like(diffuse)
+    specular_grad = torch.zeros_like(specular)
+    density_grad = torch.zeros_like(density, dtype=torch.float32)
+    points_grad = torch.zeros((num_points, 3), dtype=rays.dtype, device=dev)
+    ray_grad = torch.zeros_like(rays)
+    workspace = torch.empty((adjacency_size + 32, 4), dtype=torch.float16, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call("vt_trace_bwd", code, points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd, rs,
+                  density.data_ptr(), adjacency.data_ptr(), adjacency_size, offsets.data_ptr(), num_points,
+                  rays.data_ptr(), num_rays, start_point.data_ptr(), rgb_out.data_ptr(), rgb_grad.data_ptr(), K,
+                  _ptr(depth_quantiles), _ptr(depth_indices), _ptr(depth_grad), _ptr(ray_error),
+                  float(contribution_alpha_grad), distortion.data_ptr(), _ptr(distortion_grad),
+                  W_total.data_ptr(), S_total.data_ptr(), t_far.data_ptr(), float(weight_threshold),
+                  int(max_intersections), points_grad.data_ptr(), diffuse_grad.data_ptr(),
+                  specular_grad.data_ptr(), density_grad.data_ptr(), _ptr(point_error), workspace.data_ptr(), None,
+                  _stream(dev))
+    return points_grad, diffuse_grad, specular_grad, density_grad, ray_grad, point_error
+
+
+class NNBVH:
+    """nn_bvh.h:4-16 / nn_bvh.cu:43-117: exact nearest-site queries over a
+    Morton LBVH built on the GPU (replaces cuBQL).  query returns int32."""
+
+    def __init__(self):
+        import ctypes as C
+
+        self._h = C.c_void_p()
+        _lib.call("vt_bvh_create", C.byref(self._h))
+        self._built = False
+        self._n = 0
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            try:
+                _lib.load().vt_bvh_destroy(h)
+            except Exception:
+                pass
+            self._h = None
+
+    def build(self, points):
+        _assert(points.device.type == "cuda", "points must be on CUDA")
+        pts = points.detach().contiguous()
+        _assert(pts.dtype == torch.float32 and pts.dim() == 2 and pts.size(1) == 3, "points must be float32 (N, 3)")
+        with torch.cuda.device(pts.device):
+            _lib.call("vt_bvh_build", self._h, pts.data_ptr(), pts.size(0), _stream(pts.device))
+        self._built = True
+        self._n = pts.size(0)
+
+    def query(self, points, queries):
+        _assert(self._built, "BVH must be built before querying")
+        _assert(queries.device.type == "cuda", "queries must be on CUDA")
+        pts = points.detach().contiguous()
+        q = queries.detach().contiguous()
+        _assert(q.dtype == torch.float32, "queries must be float32")
+        _assert(pts.size(0) == self._n, "points must be the point set the BVH was built on")
+        nq = q.numel() // 3
+        out = torch.empty((nq,), dtype=torch.int32, device=q.device)
+        if nq == 0:
+            return out
+        with torch.cuda.device(q.device):
+            _lib.call("vt_bvh_query", self._h, pts.data_ptr(), pts.size(0), q.data_ptr(), nq, out.data_ptr(),
+                      _stream(q.device))
+        return out
+
+
+def nearest_neighbor_bvh(points, queries):
+    """nn_bvh.cu:111-117: one-off build + query."""
+    bvh = NNBVH()
+    bvh.build(points)
+    return bvh.query(points, queries)

@@ -1,0 +1,127 @@
+// vt_core.hip -- error state, the arithmetic self-test probe, and the
+// per-face offset prefetch (tracing_octmap.cu:125-149, host :612-640).
+#include "vt_internal.h"
+#include "vt_device.h"
+
+#include <cstring>
+
+namespace vt {
+
+static thread_local char g_err[1024];
+
+void set_error(const char *fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+}
+
+void clear_error() { g_err[0] = 0; }
+
+__global__ void math_probe_kernel(int op, const float *__restrict__ in, uint32_t *__restrict__ out, uint32_t n)
+{
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n)
+        return;
+    float x = in[i];
+    if (op == 0)
+        out[i] = f_bits(vt_expf(x));
+    else if (op == 1)
+        out[i] = f_bits(vt_logf(x));
+    else
+        out[i] = f2h(x);
+}
+
+// Prefetch: one block per 256 consecutive cells.  The block stages the
+// cells' CSR offsets in LDS, then its lanes sweep the block's face entries
+// with unit stride (coalesced adjacency reads and adj_diff writes), finding
+// the owning cell by binary search in LDS.  Value per entry e of cell i:
+// half(site[adj[e]] - site[i]) per axis (f32 subtract, RNE cast), w = 0.
+constexpr int PF_CELLS = 256;
+
+__global__ __launch_bounds__(PF_CELLS) void prefetch_kernel(const float *__restrict__ points, uint32_t num_points,
+                                                             const uint32_t *__restrict__ adjacency,
+                                                             const uint32_t *__restrict__ offsets,
+                                                             uint2 *__restrict__ adj_diff)
+{
+    __shared__ uint32_t off[PF_CELLS + 1];
+    uint32_t c0 = blockIdx.x * PF_CELLS;
+    uint32_t cnt = min((uint32_t)PF_CELLS, num_points - c0);
+    for (uint32_t i = threadIdx.x; i <= cnt; i += blockDim.x)
+        off[i] = offsets[c0 + i];
+    __syncthreads();
+    uint32_t e0 = off[0], e1 = off[cnt];
+    for (uint32_t e = e0 + threadIdx.x; e < e1; e += blockDim.x) {
+        // largest c with off[c] <= e (c < cnt)
+        uint32_t lo = 0, hi = cnt;
+        while (hi - lo > 1) {
+            uint32_t mid = (lo + hi) >> 1;
+            if (off[mid] <= e)
+                lo = mid;
+            else
+                hi = mid;
+        }
+        f3 p = load_site(points, c0 + lo);
+        f3 q = load_site(points, adjacency[e]);
+        f3 df = sub(q, p);
+        uint2 w;
+        w.x = (uint32_t)f2h(df.x) | ((uint32_t)f2h(df.y) << 16);
+        w.y = (uint32_t)f2h(df.z);
+        adj_diff[e] = w;
+    }
+}
+
+// zero the rows past the last face list (the reference leaves them
+// uninitialised; chunked face reads past a list end land here and are masked)
+__global__ void zero_tail_kernel(const uint32_t *__restrict__ offsets, uint32_t num_points, uint32_t rows,
+                                 uint2 *__restrict__ adj_diff)
+{
+    uint32_t start = offsets[num_points];
+    for (uint32_t e = start + blockIdx.x * blockDim.x + threadIdx.x; e < rows; e += gridDim.x * blockDim.x)
+        adj_diff[e] = make_uint2(0u, 0u);
+}
+
+int prefetch(const float *points, uint32_t num_points, const uint32_t *adjacency, uint32_t adjacency_size,
+             const uint32_t *offsets, uint16_t *adj_diff, hipStream_t stream)
+{
+    VT_REQUIRE(points && adjacency && offsets && adj_diff, "null pointer argument");
+    uint32_t rows = adjacency_size + 32;
+    if (num_points > 0) {
+        uint32_t blocks = (num_points + PF_CELLS - 1) / PF_CELLS;
+        prefetch_kernel<<<blocks, PF_CELLS, 0, stream>>>(points, num_points, adjacency, offsets,
+                                                         reinterpret_cast<uint2 *>(adj_diff));
+        VT_LAUNCH_CHECK("prefetch_kernel");
+    }
+    zero_tail_kernel<<<4, 256, 0, stream>>>(offsets, num_points, rows, reinterpret_cast<uint2 *>(adj_diff));
+    VT_LAUNCH_CHECK("zero_tail_kernel");
+    return VT_OK;
+}
+
+} // namespace vt
+
+using namespace vt;
+
+extern "C" const char *vt_last_error(void) { return g_err; }
+
+extern "C" int vt_abi_version(void) { return 1; }
+
+extern "C" int vt_math_probe(int op, const float *in, uint32_t *out, uint32_t n, vt_stream_t stream)
+{
+    clear_error();
+    VT_REQUIRE(op >= 0 && op <= 2, "op must be 0 (exp), 1 (log) or 2 (f16)");
+    if (n == 0)
+        return VT_OK;
+    VT_REQUIRE(in && out, "null pointer argument");
+    math_probe_kernel<<<(n + 255) / 256, 256, 0, as_stream(stream)>>>(op, in, out, n);
+    VT_LAUNCH_CHECK("math_probe_kernel");
+    return VT_OK;
+}
+
+extern "C" int vt_prefetch_adj(const float *points, uint32_t num_points, const uint32_t *adjacency,
+                               uint32_t adjacency_size, const uint32_t *offsets, uint16_t *adj_diff,
+                               vt_stream_t stream)
+{
+    clear_error();
+    return prefetch(points, num_points, adjacency, adjacency_size, offsets, adj_diff, as_stream(stream));
+}

@@ -1,0 +1,355 @@
+// vt_infer.hip -- inference traversal: fp16 Half4Texel and q8 attribute
+// integrators (ray_integrator_octmap.cuh:295-633), their kernels
+// (tracing_octmap.cu:552-610, :723-779) and C entry points.
+//
+// One lane per ray.  The integrators advance transmittance only for cells
+// with density > 1e-6, shade a cell only when its weight reaches the skip
+// threshold, and stop once T <= weight_threshold.
+#include "vt_internal.h"
+#include "vt_walk.h"
+
+namespace vt {
+
+// fp16 Half4Texel maps: texel = 8 bytes (r, g, b, pad) halves
+template <int RD, int RS> struct TexF16 {
+    const uint2 *__restrict__ diffuse;
+    const uint2 *__restrict__ specular;
+
+    __device__ __forceinline__ f3 sample_diffuse(uint32_t cell, const Bilinear &b) const
+    {
+        return sample(diffuse + (size_t)cell * (RD * RD), b);
+    }
+    __device__ __forceinline__ f3 sample_specular(uint32_t cell, const Bilinear &b) const
+    {
+        return sample(specular + (size_t)cell * (RS * RS), b);
+    }
+    __device__ __forceinline__ static f3 sample(const uint2 *__restrict__ m, const Bilinear &b)
+    {
+        uint2 a = m[b.i00], c = m[b.i10], e = m[b.i01], g = m[b.i11];
+        float r = bil_mix(b, h2f(a.x & 0xffffu), h2f(c.x & 0xffffu), h2f(e.x & 0xffffu), h2f(g.x & 0xffffu));
+        float gg = bil_mix(b, h2f(a.x >> 16), h2f(c.x >> 16), h2f(e.x >> 16), h2f(g.x >> 16));
+        float bl = bil_mix(b, h2f(a.y & 0xffffu), h2f(c.y & 0xffffu), h2f(e.y & 0xffffu), h2f(g.y & 0xffffu));
+        return mk(r, gg, bl);
+    }
+};
+
+// q8 maps: texel = 3 bytes, dequant = scale[c] * q + offset[c]
+template <int RD, int RS> struct TexQ8 {
+    const uint8_t *__restrict__ diffuse;
+    const uint8_t *__restrict__ specular;
+    float ds[3], dof[3], ss[3], sof[3];
+
+    __device__ __forceinline__ f3 sample_diffuse(uint32_t cell, const Bilinear &b) const
+    {
+        return sample(diffuse + (size_t)cell * (3 * RD * RD), b, ds, dof);
+    }
+    __device__ __forceinline__ f3 sample_specular(uint32_t cell, const Bilinear &b) const
+    {
+        return sample(specular + (size_t)cell * (3 * RS * RS), b, ss, sof);
+    }
+    __device__ __forceinline__ static f3 sample(const uint8_t *__restrict__ m, const Bilinear &b, const float *sc,
+                                                const float *of)
+    {
+        float v[3];
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            float a = fma_(sc[c], (float)m[b.i00 * 3 + c], of[c]);
+            float bb = fma_(sc[c], (float)m[b.i10 * 3 + c], of[c]);
+            float cc = fma_(sc[c], (float)m[b.i01 * 3 + c], of[c]);
+            float d = fma_(sc[c], (float)m[b.i11 * 3 + c], of[c]);
+            v[c] = bil_mix(b, a, bb, cc, d);
+        }
+        return mk(v[0], v[1], v[2]);
+    }
+};
+
+// RayIntegratorOctMapInfer / ...InferQ8 (ray_integrator_octmap.cuh:315-344,
+// :487-515, colour :437-460)
+template <int RD, int RS, class Tex> struct InferIntegrator {
+    f3 o, d;
+    const float *__restrict__ density;
+    Tex tex;
+    Bilinear spec;
+    float thr, skip;
+    f3 acc;
+    float T;
+
+    template <class S>
+    __device__ __forceinline__ bool integrate(uint32_t cell, float t0, float t1, f3 p, f3, S &st)
+    {
+        float s = density[cell];
+        if (s <= 1e-6f)
+            return T > thr;
+        float dt = __builtin_fmaxf(t1 - t0, 0.0f);
+        float alpha = 1.0f - vt_expf(-s * dt);
+        float w = T * alpha;
+        if (w >= skip) {
+            st.shade();
+            f3 pd = probe_dir(o, d, t0, p);
+            float u, v;
+            oct_encode<RD>(pd, u, v);
+            Bilinear db = bilinear_setup<RD>(u, v);
+            f3 a = tex.sample_diffuse(cell, db);
+            f3 b = tex.sample_specular(cell, spec);
+            f3 lg = add(a, b);
+            f3 rgb = mk(sigmoid(lg.x), sigmoid(lg.y), sigmoid(lg.z));
+            acc = vfma(w, rgb, acc);
+        }
+        T = T * (1.0f - alpha);
+        return T > thr;
+    }
+};
+
+struct InferArgs {
+    const float *points;
+    const void *diffuse;
+    const void *specular;
+    const float *density;
+    const uint32_t *adjacency;
+    const uint32_t *offsets;
+    const uint2 *adj_diff;
+    const float *rays;
+    uint32_t num_rays;
+    const uint32_t *start_point;
+    const uint32_t *ray_perm;
+    float thr, skip;
+    uint32_t max_steps;
+    uint16_t *rgba;
+    uint32_t *stats;
+    // tiled mode
+    uint32_t num_images, H, W, th, tw;
+    // q8
+    float ds[3], dof[3], ss[3], sof[3];
+};
+
+enum { MAP_LINEAR = 0, MAP_TILED = 1 };
+
+template <int RD, int RS, bool Q8, bool STATS, int MAP, int CHUNK>
+__global__ __launch_bounds__(256) void infer_kernel(InferArgs a)
+{
+    uint32_t lane_global = xcd_block() * blockDim.x + threadIdx.x;
+    uint32_t r;
+    if (MAP == MAP_TILED) {
+        r = tiled_ray(lane_global, a.num_images, a.H, a.W, a.th, a.tw);
+        if (r == NONE)
+            return;
+    } else {
+        if (lane_global >= a.num_rays)
+            return;
+        r = a.ray_perm ? a.ray_perm[lane_global] : lane_global;
+    }
+
+    using Tex = typename std::conditional<Q8, TexQ8<RD, RS>, TexF16<RD, RS>>::type;
+    InferIntegrator<RD, RS, Tex> integ;
+    load_ray(a.rays, r, integ.o, integ.d);
+    integ.density = a.density;
+    if constexpr (Q8) {
+        integ.tex.diffuse = (const uint8_t *)a.diffuse;
+        integ.tex.specular = (const uint8_t *)a.specular;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            integ.tex.ds[c] = a.ds[c];
+            integ.tex.dof[c] = a.dof[c];
+            integ.tex.ss[c] = a.ss[c];
+            integ.tex.sof[c] = a.sof[c];
+        }
+    } else {
+        integ.tex.diffuse = (const uint2 *)a.diffuse;
+        integ.tex.specular = (const uint2 *)a.specular;
+    }
+    float su, sv;
+    oct_encode<RS>(mk(-integ.d.x, -integ.d.y, -integ.d.z), su, sv);
+    integ.spec = bilinear_setup<RS>(su, sv);
+    integ.thr = a.thr;
+    integ.skip = a.skip;
+    integ.acc = mk(0.0f, 0.0f, 0.0f);
+    integ.T = 1.0f;
+
+    StatsAcc<STATS> st;
+    uint32_t n = walk<CHUNK>(integ.o, integ.d, a.points, a.adjacency, a.offsets, a.adj_diff, a.start_point[r],
+                             a.max_steps, integ, st);
+    uint2 out;
+    out.x = (uint32_t)f2h(integ.acc.x) | ((uint32_t)f2h(integ.acc.y) << 16);
+    out.y = (uint32_t)f2h(integ.acc.z) | ((uint32_t)f2h(1.0f - integ.T) << 16);
+    reinterpret_cast<uint2 *>(a.rgba)[r] = out;
+    st.store(a.stats, r, n);
+}
+
+constexpr int INFER_BLOCK = 256;
+constexpr int INFER_CHUNK = 4;
+
+template <int RD, int RS, bool Q8>
+static int launch_infer_rs(const InferArgs &a, bool stats, int map, hipStream_t stream, uint32_t lanes)
+{
+    dim3 grid((lanes + INFER_BLOCK - 1) / INFER_BLOCK), block(INFER_BLOCK);
+    if (map == MAP_TILED) {
+        if (stats)
+            infer_kernel<RD, RS, Q8, true, MAP_TILED, INFER_CHUNK><<<grid, block, 0, stream>>>(a);
+        else
+            infer_kernel<RD, RS, Q8, false, MAP_TILED, INFER_CHUNK><<<grid, block, 0, stream>>>(a);
+    } else {
+        if (stats)
+            infer_kernel<RD, RS, Q8, true, MAP_LINEAR, INFER_CHUNK><<<grid, block, 0, stream>>>(a);
+        else
+            infer_kernel<RD, RS, Q8, false, MAP_LINEAR, INFER_CHUNK><<<grid, block, 0, stream>>>(a);
+    }
+    VT_LAUNCH_CHECK("infer_kernel");
+    return VT_OK;
+}
+
+template <bool Q8>
+static int launch_infer(const InferArgs &a, uint32_t rd, uint32_t rs, bool stats, int map, hipStream_t stream,
+                        uint32_t lanes)
+{
+    if (lanes == 0)
+        return VT_OK;
+    if (rd == 4 && rs == 4)
+        return launch_infer_rs<4, 4, Q8>(a, stats, map, stream, lanes);
+    if (rd == 8 && rs == 8)
+        return launch_infer_rs<8, 8, Q8>(a, stats, map, stream, lanes);
+    if (rd == 8 && rs == 4)
+        return launch_infer_rs<8, 4, Q8>(a, stats, map, stream, lanes);
+    if (rd == 4 && rs == 8)
+        return launch_infer_rs<4, 8, Q8>(a, stats, map, stream, lanes);
+    set_error("unsupported octahedral map resolution (diffuse %u, specular %u); compiled: 4, 8", rd, rs);
+    return VT_ERR_UNSUPPORTED;
+}
+
+static int check_common(const void *points, const void *diffuse, const void *specular, const void *density,
+                        const void *adjacency, const void *offsets, const void *adj_diff, const void *rays,
+                        const void *start_point, const void *rgba)
+{
+    VT_REQUIRE(points && diffuse && specular && density && adjacency && offsets && adj_diff && rays &&
+                   start_point && rgba,
+               "null pointer argument");
+    return VT_OK;
+}
+
+} // namespace vt
+
+using namespace vt;
+
+extern "C" int vt_trace_infer_f16(const float *points, const uint16_t *diffuse, const uint16_t *specular,
+                                  uint32_t diff_res, uint32_t spec_res, const float *density,
+                                  const uint32_t *adjacency, const uint32_t *offsets, uint32_t num_points,
+                                  const uint16_t *adj_diff, const float *rays, uint32_t num_rays,
+                                  const uint32_t *start_point, const uint32_t *ray_perm, float weight_threshold,
+                                  uint32_t max_intersections, float cell_skip_threshold, uint16_t *rgba,
+                                  vt_ray_stats *stats, vt_stream_t stream)
+{
+    clear_error();
+    if (num_rays == 0)
+        return VT_OK;
+    int rc = check_common(points, diffuse, specular, density, adjacency, offsets, adj_diff, rays, start_point, rgba);
+    if (rc)
+        return rc;
+    (void)num_points;
+    InferArgs a{};
+    a.points = points;
+    a.diffuse = diffuse;
+    a.specular = specular;
+    a.density = density;
+    a.adjacency = adjacency;
+    a.offsets = offsets;
+    a.adj_diff = reinterpret_cast<const uint2 *>(adj_diff);
+    a.rays = rays;
+    a.num_rays = num_rays;
+    a.start_point = start_point;
+    a.ray_perm = ray_perm;
+    a.thr = weight_threshold;
+    a.skip = cell_skip_threshold;
+    a.max_steps = max_intersections;
+    a.rgba = rgba;
+    a.stats = reinterpret_cast<uint32_t *>(stats);
+    return launch_infer<false>(a, diff_res, spec_res, stats != nullptr, MAP_LINEAR, as_stream(stream), num_rays);
+}
+
+extern "C" int vt_trace_infer_f16_tiled(const float *points, const uint16_t *diffuse, const uint16_t *specular,
+                                        uint32_t diff_res, uint32_t spec_res, const float *density,
+                                        const uint32_t *adjacency, const uint32_t *offsets, uint32_t num_points,
+                                        const uint16_t *adj_diff, const float *rays, uint32_t num_images,
+                                        uint32_t image_h, uint32_t image_w, uint32_t tile_h, uint32_t tile_w,
+                                        const uint32_t *start_point, float weight_threshold,
+                                        uint32_t max_intersections, float cell_skip_threshold, uint16_t *rgba,
+                                        vt_ray_stats *stats, vt_stream_t stream)
+{
+    clear_error();
+    if (num_images == 0 || image_h == 0 || image_w == 0)
+        return VT_OK;
+    int rc = check_common(points, diffuse, specular, density, adjacency, offsets, adj_diff, rays, start_point, rgba);
+    if (rc)
+        return rc;
+    VT_REQUIRE(tile_h * tile_w == 64, "tile_h * tile_w must be 64 (one wave64 per tile), got %u x %u", tile_h,
+               tile_w);
+    (void)num_points;
+    uint64_t tiles = (uint64_t)((image_w + tile_w - 1) / tile_w) * ((image_h + tile_h - 1) / tile_h) * num_images;
+    VT_REQUIRE(tiles * 64 < (1ull << 32), "image batch too large");
+    VT_REQUIRE((uint64_t)num_images * image_h * image_w < (1ull << 32), "image batch too large");
+    InferArgs a{};
+    a.points = points;
+    a.diffuse = diffuse;
+    a.specular = specular;
+    a.density = density;
+    a.adjacency = adjacency;
+    a.offsets = offsets;
+    a.adj_diff = reinterpret_cast<const uint2 *>(adj_diff);
+    a.rays = rays;
+    a.num_rays = num_images * image_h * image_w;
+    a.start_point = start_point;
+    a.ray_perm = nullptr;
+    a.thr = weight_threshold;
+    a.skip = cell_skip_threshold;
+    a.max_steps = max_intersections;
+    a.rgba = rgba;
+    a.stats = reinterpret_cast<uint32_t *>(stats);
+    a.num_images = num_images;
+    a.H = image_h;
+    a.W = image_w;
+    a.th = tile_h;
+    a.tw = tile_w;
+    return launch_infer<false>(a, diff_res, spec_res, stats != nullptr, MAP_TILED, as_stream(stream),
+                               (uint32_t)(tiles * 64));
+}
+
+extern "C" int vt_trace_infer_q8(const float *points, const uint8_t *diffuse, const uint8_t *specular,
+                                 uint32_t diff_res, uint32_t spec_res, const float diff_scale[3],
+                                 const float diff_offset[3], const float spec_scale[3], const float spec_offset[3],
+                                 const float *density, const uint32_t *adjacency, const uint32_t *offsets,
+                                 uint32_t num_points, const uint16_t *adj_diff, const float *rays,
+                                 uint32_t num_rays, const uint32_t *start_point, const uint32_t *ray_perm,
+                                 float weight_threshold, uint32_t max_intersections, float cell_skip_threshold,
+                                 uint16_t *rgba, vt_ray_stats *stats, vt_stream_t stream)
+{
+    clear_error();
+    if (num_rays == 0)
+        return VT_OK;
+    int rc = check_common(points, diffuse, specular, density, adjacency, offsets, adj_diff, rays, start_point, rgba);
+    if (rc)
+        return rc;
+    VT_REQUIRE(diff_scale && diff_offset && spec_scale && spec_offset, "null dequantisation parameters");
+    (void)num_points;
+    InferArgs a{};
+    a.points = points;
+    a.diffuse = diffuse;
+    a.specular = specular;
+    a.density = density;
+    a.adjacency = adjacency;
+    a.offsets = offsets;
+    a.adj_diff = reinterpret_cast<const uint2 *>(adj_diff);
+    a.rays = rays;
+    a.num_rays = num_rays;
+    a.start_point = start_point;
+    a.ray_perm = ray_perm;
+    a.thr = weight_threshold;
+    a.skip = cell_skip_threshold;
+    a.max_steps = max_intersections;
+    a.rgba = rgba;
+    a.stats = reinterpret_cast<uint32_t *>(stats);
+    for (int c = 0; c < 3; ++c) {
+        a.ds[c] = diff_scale[c];
+        a.dof[c] = diff_offset[c];
+        a.ss[c] = spec_scale[c];
+        a.sof[c] = spec_offset[c];
+    }
+    return launch_infer<true>(a, diff_res, spec_res, stats != nullptr, MAP_LINEAR, as_stream(stream), num_rays);
+}

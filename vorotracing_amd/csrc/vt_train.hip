@@ -1,0 +1,624 @@
+// vt_train.hip -- training traversal: forward (ray_integrator_octmap.cuh:57-282,
+// kernel tracing_octmap.cu:151-230) and backward (ray_integrator_octmap.cuh:635-1027,
+// kernel :232-340), with f32 or f16 attribute storage.
+//
+// Attribute maps are (num_points, 3*R*R), texel-major / channel-minor.  The
+// backward scatters 28 gradient values per integrated cell with global
+// atomics (f32: hardware global_atomic_add_f32; f16: 32-bit CAS).
+#include "vt_internal.h"
+#include "vt_walk.h"
+
+namespace vt {
+
+// ---------------------------------------------------------------------------
+// attribute storage
+
+template <typename A> struct Attr;
+
+template <> struct Attr<float> {
+    __device__ __forceinline__ static float load(const float *p, size_t i) { return p[i]; }
+    __device__ __forceinline__ static void store(float *p, size_t i, float v) { p[i] = v; }
+    __device__ __forceinline__ static void add(float *p, size_t i, float v) { atomicAdd(p + i, v); }
+};
+
+// f16 stored as raw 16-bit words
+template <> struct Attr<uint16_t> {
+    __device__ __forceinline__ static float load(const uint16_t *p, size_t i) { return h2f(p[i]); }
+    __device__ __forceinline__ static void store(uint16_t *p, size_t i, float v) { p[i] = f2h(v); }
+    // atomicAdd on a half: add the half-rounded value into the containing
+    // aligned 32-bit word with compare-and-swap
+    __device__ __forceinline__ static void add(uint16_t *p, size_t i, float v)
+    {
+        uintptr_t addr = reinterpret_cast<uintptr_t>(p + i);
+        uint32_t *word = reinterpret_cast<uint32_t *>(addr & ~(uintptr_t)3);
+        uint32_t shift = (addr & 2) ? 16u : 0u;
+        float hv = h2f(f2h(v));
+        uint32_t old = *word, assumed;
+        do {
+            assumed = old;
+            uint16_t h = (uint16_t)(assumed >> shift);
+            uint16_t nh = f2h(h2f(h) + hv);
+            uint32_t nw = (assumed & ~(0xffffu << shift)) | ((uint32_t)nh << shift);
+            old = atomicCAS(word, assumed, nw);
+        } while (old != assumed);
+    }
+};
+
+template <typename A, int RD, int RS> struct TrainTex {
+    const A *__restrict__ diffuse;
+    const A *__restrict__ specular;
+
+    __device__ __forceinline__ static f3 sample(const A *__restrict__ m, const Bilinear &b)
+    {
+        float v[3];
+#pragma unroll
+        for (int c = 0; c < 3; ++c)
+            v[c] = bil_mix(b, Attr<A>::load(m, b.i00 * 3 + c), Attr<A>::load(m, b.i10 * 3 + c),
+                           Attr<A>::load(m, b.i01 * 3 + c), Attr<A>::load(m, b.i11 * 3 + c));
+        return mk(v[0], v[1], v[2]);
+    }
+    // sigmoid(diffuse(probe) + specular(spec taps)); diffuse taps out in db
+    __device__ __forceinline__ f3 color(uint32_t cell, f3 o, f3 d, float t0, f3 p, const Bilinear &spec,
+                                        Bilinear &db) const
+    {
+        f3 pd = probe_dir(o, d, t0, p);
+        float u, v;
+        oct_encode<RD>(pd, u, v);
+        db = bilinear_setup<RD>(u, v);
+        f3 a = sample(diffuse + (size_t)cell * (3 * RD * RD), db);
+        f3 b = sample(specular + (size_t)cell * (3 * RS * RS), spec);
+        f3 lg = add(a, b);
+        return mk(sigmoid(lg.x), sigmoid(lg.y), sigmoid(lg.z));
+    }
+};
+
+// ---------------------------------------------------------------------------
+// forward
+
+struct FwdArgs {
+    const float *points;
+    const void *diffuse, *specular;
+    const float *density;
+    const uint32_t *adjacency, *offsets;
+    const uint2 *adj_diff;
+    const float *rays;
+    uint32_t num_rays;
+    const uint32_t *start_point;
+    uint32_t K;
+    const float *quantiles;
+    float thr;
+    uint32_t max_steps;
+    void *rgba;
+    float *depth;
+    uint32_t *depth_idx;
+    void *contribution;
+    uint32_t *n_out;
+    float *distortion, *W_total, *S_total, *t_far;
+    uint32_t *stats;
+};
+
+// RayIntegratorOctMap::integrate_cell (ray_integrator_octmap.cuh:102-152)
+template <typename A, int RD, int RS> struct FwdIntegrator {
+    f3 o, d;
+    const float *__restrict__ density;
+    TrainTex<A, RD, RS> tex;
+    Bilinear spec;
+    float thr;
+    A *contribution;
+    const float *qthr;
+    uint32_t nq, qi;
+    float qval;
+    float *qdepth;
+    uint32_t *qidx;
+    f3 acc;
+    float T, W, S, D, self, tfar;
+
+    template <class St>
+    __device__ __forceinline__ bool integrate(uint32_t cell, float t0, float t1, f3 p, f3, St &st)
+    {
+        float sig = density[cell];
+        f3 rgb = mk(0.0f, 0.0f, 0.0f);
+        if (sig > 1e-6f) {
+            st.shade();
+            Bilinear db;
+            rgb = tex.color(cell, o, d, t0, p, spec, db);
+        }
+        float dt = __builtin_fmaxf(t1 - t0, 0.0f);
+        float alpha = 1.0f - vt_expf(-sig * dt);
+        float w = T * alpha;
+
+        float s0 = 1.0f - 1.0f / (1.0f + t0);
+        float s1 = 1.0f - 1.0f / (1.0f + t1);
+        float mid = 0.5f * (s0 + s1);
+        float ds = s1 - s0;
+        D = fma_(w, fma_(mid, W, -S), D);
+        self = fma_(w * w, ds, self);
+        W = W + w;
+        S = fma_(w, mid, S);
+        if (t1 > tfar)
+            tfar = t1;
+
+        if (contribution)
+            Attr<A>::add(contribution, cell, w);
+        acc = vfma(w, rgb, acc);
+
+        float nextT = T * (1.0f - alpha);
+        while (qi < nq && nextT < qval) {
+            qdepth[qi] = t0 + vt_logf(T / qval) / sig;
+            qidx[qi] = cell;
+            qi++;
+            if (qi < nq)
+                qval = qthr[qi];
+        }
+        T = nextT;
+        return T > thr;
+    }
+};
+
+template <typename A, int RD, int RS, bool STATS>
+__global__ __launch_bounds__(256) void fwd_kernel(FwdArgs a)
+{
+    uint32_t r = xcd_block() * blockDim.x + threadIdx.x;
+    if (r >= a.num_rays)
+        return;
+    FwdIntegrator<A, RD, RS> it;
+    load_ray(a.rays, r, it.o, it.d);
+    it.density = a.density;
+    it.tex.diffuse = (const A *)a.diffuse;
+    it.tex.specular = (const A *)a.specular;
+    float su, sv;
+    oct_encode<RS>(mk(-it.d.x, -it.d.y, -it.d.z), su, sv);
+    it.spec = bilinear_setup<RS>(su, sv);
+    it.thr = a.thr;
+    it.contribution = (A *)a.contribution;
+    uint32_t K = a.quantiles ? a.K : 0;
+    it.nq = K;
+    it.qi = 0;
+    it.qthr = K ? a.quantiles + (size_t)r * K : nullptr;
+    it.qval = K ? it.qthr[0] : 0.0f;
+    it.qdepth = K ? a.depth + (size_t)r * K : nullptr;
+    it.qidx = K ? a.depth_idx + (size_t)r * K : nullptr;
+    it.acc = mk(0.0f, 0.0f, 0.0f);
+    it.T = 1.0f;
+    it.W = it.S = it.D = it.self = it.tfar = 0.0f;
+    StatsAcc<STATS> st;
+    uint32_t n = walk<4>(it.o, it.d, a.points, a.adjacency, a.offsets, a.adj_diff, a.start_point[r], a.max_steps,
+                         it, st);
+    for (uint32_t i = it.qi; i < K; ++i) {
+        a.depth[(size_t)r * K + i] = -1.0f;
+        a.depth_idx[(size_t)r * K + i] = NONE;
+    }
+    A *rgba = (A *)a.rgba;
+    Attr<A>::store(rgba, 4 * (size_t)r + 0, it.acc.x);
+    Attr<A>::store(rgba, 4 * (size_t)r + 1, it.acc.y);
+    Attr<A>::store(rgba, 4 * (size_t)r + 2, it.acc.z);
+    Attr<A>::store(rgba, 4 * (size_t)r + 3, 1.0f - it.T);
+    if (a.n_out)
+        a.n_out[r] = n;
+    a.distortion[r] = fma_(2.0f, it.D, it.self / 3.0f);
+    a.W_total[r] = it.W;
+    a.S_total[r] = it.S;
+    a.t_far[r] = it.tfar;
+    st.store(a.stats, r, n);
+}
+
+// ---------------------------------------------------------------------------
+// backward
+
+struct BwdArgs {
+    const float *points;
+    const void *diffuse, *specular;
+    const float *density;
+    const uint32_t *adjacency, *offsets;
+    const uint2 *adj_diff;
+    const float *rays;
+    uint32_t num_rays;
+    const uint32_t *start_point;
+    const void *rgba, *rgba_grad;
+    uint32_t K;
+    const float *quantiles;
+    const uint32_t *depth_idx;
+    const float *depth_grad;
+    const void *ray_error;
+    float contribution_alpha_grad;
+    const float *distortion, *distortion_grad, *W_total, *S_total;
+    float thr;
+    uint32_t max_steps;
+    float *points_grad;
+    void *diffuse_grad, *specular_grad;
+    float *density_grad;
+    void *point_error;
+    uint32_t *stats;
+};
+
+// ray_integrator.cuh:39-53
+__device__ __forceinline__ f3 cell_intersection_grad(f3 prim, f3 opp, f3 o, f3 d)
+{
+    f3 fo = mk((prim.x + opp.x) * 0.5f, (prim.y + opp.y) * 0.5f, (prim.z + opp.z) * 0.5f);
+    f3 n = sub(opp, prim);
+    float num = dot(sub(fo, o), n);
+    float dp = dot(n, d);
+    f3 op = sub(o, prim);
+    f3 g = mk(fma_(num, d.x, dp * op.x), fma_(num, d.y, dp * op.y), fma_(num, d.z, dp * op.z));
+    return divs(g, dp * dp);
+}
+
+__device__ __forceinline__ void add_vec(float *pg, uint32_t idx, f3 v)
+{
+    float *q = pg + 3 * (size_t)idx;
+    atomicAdd(q + 0, v.x);
+    atomicAdd(q + 1, v.y);
+    atomicAdd(q + 2, v.z);
+}
+
+// RayIntegratorOctMapBackward::integrate_cell (ray_integrator_octmap.cuh:683-860)
+template <typename A, int RD, int RS> struct BwdIntegrator {
+    f3 o, d;
+    const float *__restrict__ density;
+    TrainTex<A, RD, RS> tex;
+    Bilinear spec;
+    float thr;
+    f3 acc;
+    float T;
+    float cur_depth_grad;
+    uint32_t qi, nq;
+    float qval;
+    const float *qthr, *depth_grad;
+    float *points_grad;
+    A *diffuse_grad, *specular_grad, *point_error;
+    float *density_grad;
+    f3 prev_geom, prev_grad, cur_grad, next_grad;
+    uint32_t prev_idx;
+    f3 fwd_rgb, fwd_rgb_grad;
+    float fwd_alpha, fwd_alpha_grad, ray_error;
+    float W_run, S_run, W_total, S_total, dist_grad, D_total, D_running;
+
+    template <class St>
+    __device__ __forceinline__ bool integrate(uint32_t cell, float t0, float t1, f3 p, f3 np, St &st)
+    {
+        float sig = density[cell];
+        f3 rgb = mk(0.0f, 0.0f, 0.0f);
+        Bilinear db;
+        bool has_color = false;
+        if (sig > 1e-6f) {
+            st.shade();
+            rgb = tex.color(cell, o, d, t0, p, spec, db);
+            has_color = true;
+        }
+        float dt = __builtin_fmaxf(t1 - t0, 0.0f);
+        float alpha = 1.0f - vt_expf(-sig * dt);
+        float w = T * alpha;
+        float da_ds = dt * (1.0f - alpha);
+        float da_ddt = 0.0f;
+        if (dt > 0.0f)
+            da_ddt = sig * (1.0f - alpha);
+
+        acc = vfma(w, rgb, acc);
+        if (point_error)
+            Attr<A>::add(point_error, cell, w * ray_error);
+
+        f3 dL_drgb = mk(fwd_rgb_grad.x * w, fwd_rgb_grad.y * w, fwd_rgb_grad.z * w);
+        f3 rest = divs(sub(fwd_rgb, acc), T * ((1.0f - alpha) + 1e-6f));
+        float dL_dalpha = T * dot(sub(rgb, rest), fwd_rgb_grad);
+        dL_dalpha = dL_dalpha + ((1.0f - fwd_alpha) * fwd_alpha_grad) / ((1.0f - alpha) + 1e-6f);
+
+        float dL_ds = dL_dalpha * da_ds;
+        float dL_ddt = dL_dalpha * da_ddt;
+        float dL_dt0 = 0.0f;
+
+        if (dist_grad != 0.0f) {
+            float s0 = 1.0f - 1.0f / (1.0f + t0);
+            float s1 = 1.0f - 1.0f / (1.0f + t1);
+            float mid = 0.5f * (s0 + s1);
+            float ds = s1 - s0;
+            float Wm = W_run;
+            float Sm = S_run;
+            float Wp = (W_total - Wm) - w;
+            float Sp = fma_(-w, mid, S_total - Sm);
+            float dL_dw_raw = fma_(2.0f / 3.0f * w, ds, fma_(2.0f, fma_(-mid, Wp, Sp), 2.0f * fma_(mid, Wm, -Sm)));
+            float dL_dw_outer = dL_dw_raw * dist_grad;
+            float dL_dw_w = dL_dw_outer * w;
+            float D_iplus = (D_total - D_running) - dL_dw_w;
+            dL_ds = dL_ds + fma_(-dt, D_iplus, (dL_dw_outer * T) * da_ds);
+            D_running = D_running + dL_dw_w;
+            W_run = W_run + w;
+            S_run = fma_(w, mid, S_run);
+        }
+
+        float nextT = T * (1.0f - alpha);
+        while (qi < nq && nextT < qval) {
+            float dg = depth_grad[qi] / sig;
+            dL_dt0 = dL_dt0 + dg;
+            dL_ds = dL_ds + (-dg * vt_logf(T / qval)) / sig;
+            cur_depth_grad = cur_depth_grad - dg;
+            qi++;
+            if (qi < nq)
+                qval = qthr[qi];
+        }
+        if (qi < nq) {
+            dL_ds = fma_(-dt, cur_depth_grad, dL_ds);
+            dL_ddt = fma_(-sig, cur_depth_grad, dL_ddt);
+        }
+        dL_dt0 = dL_dt0 + -dL_ddt;
+        float dL_dt1 = dL_ddt;
+
+        f3 dt0_dprev = mk(0.0f, 0.0f, 0.0f);
+        if (prev_idx != NONE)
+            dt0_dprev = cell_intersection_grad(prev_geom, p, o, d);
+        f3 dt1_dcur = cell_intersection_grad(p, np, o, d);
+        f3 dt0_dcur = cell_intersection_grad(p, prev_geom, o, d);
+        f3 dt1_dnext = cell_intersection_grad(np, p, o, d);
+
+        prev_grad = vfma(dL_dt0, dt0_dprev, prev_grad);
+        f3 cg = mk(fma_(dL_dt1, dt1_dcur.x, dL_dt0 * dt0_dcur.x), fma_(dL_dt1, dt1_dcur.y, dL_dt0 * dt0_dcur.y),
+                   fma_(dL_dt1, dt1_dcur.z, dL_dt0 * dt0_dcur.z));
+        cur_grad = add(cur_grad, cg);
+        next_grad = vfma(dL_dt1, dt1_dnext, next_grad);
+
+        if (prev_idx != NONE)
+            add_vec(points_grad, prev_idx, prev_grad);
+        prev_geom = p;
+        prev_idx = cell;
+        prev_grad = cur_grad;
+        cur_grad = next_grad;
+        next_grad = mk(0.0f, 0.0f, 0.0f);
+
+        T = nextT;
+
+        if (has_color) {
+            float gl[3];
+            gl[0] = (dL_drgb.x * rgb.x) * (1.0f - rgb.x);
+            gl[1] = (dL_drgb.y * rgb.y) * (1.0f - rgb.y);
+            gl[2] = (dL_drgb.z * rgb.z) * (1.0f - rgb.z);
+            A *dg = diffuse_grad + (size_t)cell * (3 * RD * RD);
+            A *sg = specular_grad + (size_t)cell * (3 * RS * RS);
+#pragma unroll
+            for (int c = 0; c < 3; ++c) {
+                Attr<A>::add(dg, db.i00 * 3 + c, db.w00 * gl[c]);
+                Attr<A>::add(dg, db.i10 * 3 + c, db.w10 * gl[c]);
+                Attr<A>::add(dg, db.i01 * 3 + c, db.w01 * gl[c]);
+                Attr<A>::add(dg, db.i11 * 3 + c, db.w11 * gl[c]);
+            }
+#pragma unroll
+            for (int c = 0; c < 3; ++c) {
+                Attr<A>::add(sg, spec.i00 * 3 + c, spec.w00 * gl[c]);
+                Attr<A>::add(sg, spec.i10 * 3 + c, spec.w10 * gl[c]);
+                Attr<A>::add(sg, spec.i01 * 3 + c, spec.w01 * gl[c]);
+                Attr<A>::add(sg, spec.i11 * 3 + c, spec.w11 * gl[c]);
+            }
+        }
+        atomicAdd(density_grad + cell, dL_ds);
+
+        if (T < thr) {
+            add_vec(points_grad, prev_idx, prev_grad);
+            return false;
+        }
+        return true;
+    }
+};
+
+template <typename A, int RD, int RS, bool STATS>
+__global__ __launch_bounds__(256) void bwd_kernel(BwdArgs a)
+{
+    uint32_t r = xcd_block() * blockDim.x + threadIdx.x;
+    if (r >= a.num_rays)
+        return;
+    BwdIntegrator<A, RD, RS> it;
+    load_ray(a.rays, r, it.o, it.d);
+    it.density = a.density;
+    it.tex.diffuse = (const A *)a.diffuse;
+    it.tex.specular = (const A *)a.specular;
+    float su, sv;
+    oct_encode<RS>(mk(-it.d.x, -it.d.y, -it.d.z), su, sv);
+    it.spec = bilinear_setup<RS>(su, sv);
+    it.thr = a.thr;
+    const A *rg = (const A *)a.rgba_grad;
+    const A *rv = (const A *)a.rgba;
+    float g[4], v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        g[i] = Attr<A>::load(rg, 4 * (size_t)r + i);
+        v[i] = Attr<A>::load(rv, 4 * (size_t)r + i);
+    }
+    g[3] = g[3] + a.contribution_alpha_grad;
+    it.ray_error = a.ray_error ? Attr<A>::load((const A *)a.ray_error, r) : 0.0f;
+    uint32_t K = a.quantiles ? a.K : 0;
+    float cdg = 0.0f;
+    for (uint32_t i = 0; i < K; ++i) {
+        uint32_t q = a.depth_idx[(size_t)r * K + i];
+        if (q != NONE)
+            cdg = cdg + a.depth_grad[(size_t)r * K + i] / a.density[q];
+    }
+    it.acc = mk(0.0f, 0.0f, 0.0f);
+    it.T = 1.0f;
+    it.cur_depth_grad = cdg;
+    it.qi = 0;
+    it.nq = K;
+    it.qthr = K ? a.quantiles + (size_t)r * K : nullptr;
+    it.depth_grad = K ? a.depth_grad + (size_t)r * K : nullptr;
+    it.qval = K ? it.qthr[0] : 0.0f;
+    it.points_grad = a.points_grad;
+    it.diffuse_grad = (A *)a.diffuse_grad;
+    it.specular_grad = (A *)a.specular_grad;
+    it.density_grad = a.density_grad;
+    it.point_error = (A *)a.point_error;
+    it.prev_geom = it.prev_grad = it.cur_grad = it.next_grad = mk(0.0f, 0.0f, 0.0f);
+    it.prev_idx = NONE;
+    it.fwd_rgb = mk(v[0], v[1], v[2]);
+    it.fwd_alpha = v[3];
+    it.fwd_rgb_grad = mk(g[0], g[1], g[2]);
+    it.fwd_alpha_grad = g[3];
+    it.W_run = it.S_run = it.D_running = 0.0f;
+    it.W_total = a.W_total ? a.W_total[r] : 0.0f;
+    it.S_total = a.S_total ? a.S_total[r] : 0.0f;
+    float fd = a.distortion ? a.distortion[r] : 0.0f;
+    it.dist_grad = a.distortion_grad ? a.distortion_grad[r] : 0.0f;
+    it.D_total = (2.0f * fd) * it.dist_grad;
+    StatsAcc<STATS> st;
+    uint32_t n = walk<4>(it.o, it.d, a.points, a.adjacency, a.offsets, a.adj_diff, a.start_point[r], a.max_steps,
+                         it, st);
+    st.store(a.stats, r, n);
+}
+
+int prefetch(const float *points, uint32_t num_points, const uint32_t *adjacency, uint32_t adjacency_size,
+             const uint32_t *offsets, uint16_t *adj_diff, hipStream_t stream);
+
+constexpr int TRAIN_BLOCK = 256;
+
+template <template <typename, int, int, bool> class K, typename Args, typename A, int RD, int RS>
+static int launch_train_rs(const Args &a, bool stats, hipStream_t s)
+{
+    dim3 grid((a.num_rays + TRAIN_BLOCK - 1) / TRAIN_BLOCK), block(TRAIN_BLOCK);
+    if (stats)
+        hipLaunchKernelGGL((K<A, RD, RS, true>::fn), grid, block, 0, s, a);
+    else
+        hipLaunchKernelGGL((K<A, RD, RS, false>::fn), grid, block, 0, s, a);
+    VT_LAUNCH_CHECK("training traversal kernel");
+    return VT_OK;
+}
+
+template <typename A, int RD, int RS, bool ST> struct FwdK {
+    static constexpr auto fn = fwd_kernel<A, RD, RS, ST>;
+};
+template <typename A, int RD, int RS, bool ST> struct BwdK {
+    static constexpr auto fn = bwd_kernel<A, RD, RS, ST>;
+};
+
+template <template <typename, int, int, bool> class K, typename Args, typename A>
+static int launch_train_a(const Args &a, uint32_t rd, uint32_t rs, bool stats, hipStream_t s)
+{
+    if (rd == 4 && rs == 4)
+        return launch_train_rs<K, Args, A, 4, 4>(a, stats, s);
+    if (rd == 8 && rs == 8)
+        return launch_train_rs<K, Args, A, 8, 8>(a, stats, s);
+    if (rd == 8 && rs == 4)
+        return launch_train_rs<K, Args, A, 8, 4>(a, stats, s);
+    if (rd == 4 && rs == 8)
+        return launch_train_rs<K, Args, A, 4, 8>(a, stats, s);
+    set_error("unsupported octahedral map resolution (diffuse %u, specular %u); compiled: 4, 8", rd, rs);
+    return VT_ERR_UNSUPPORTED;
+}
+
+template <template <typename, int, int, bool> class K, typename Args>
+static int launch_train(int attr_dtype, const Args &a, uint32_t rd, uint32_t rs, bool stats, hipStream_t s)
+{
+    if (a.num_rays == 0)
+        return VT_OK;
+    if (attr_dtype == VT_ATTR_F32)
+        return launch_train_a<K, Args, float>(a, rd, rs, stats, s);
+    if (attr_dtype == VT_ATTR_F16)
+        return launch_train_a<K, Args, uint16_t>(a, rd, rs, stats, s);
+    set_error("Unsupported color dtype. Only float32 and float16 are supported.");
+    return VT_ERR_INVALID;
+}
+
+} // namespace vt
+
+using namespace vt;
+
+extern "C" int vt_trace_fwd(int attr_dtype, const float *points, const void *diffuse, const void *specular,
+                            uint32_t diff_res, uint32_t spec_res, const float *density, const uint32_t *adjacency,
+                            uint32_t adjacency_size, const uint32_t *offsets, uint32_t num_points, const float *rays,
+                            uint32_t num_rays, const uint32_t *start_point, uint32_t num_quantiles,
+                            const float *depth_quantiles, float weight_threshold, uint32_t max_intersections,
+                            void *rgba, float *depth, uint32_t *depth_idx, void *contribution,
+                            uint32_t *num_intersections, float *distortion, float *W_total, float *S_total,
+                            float *t_far, uint16_t *adj_diff_workspace, vt_ray_stats *stats, vt_stream_t stream)
+{
+    clear_error();
+    VT_REQUIRE(points && diffuse && specular && density && adjacency && offsets && adj_diff_workspace,
+               "null scene pointer");
+    VT_REQUIRE(num_rays == 0 || (rays && start_point && rgba && distortion && W_total && S_total && t_far),
+               "null ray or output pointer");
+    VT_REQUIRE(!depth_quantiles || num_quantiles == 0 || (depth && depth_idx),
+               "depth outputs required when depth_quantiles is given");
+    hipStream_t s = as_stream(stream);
+    int rc = prefetch(points, num_points, adjacency, adjacency_size, offsets, adj_diff_workspace, s);
+    if (rc)
+        return rc;
+    FwdArgs a{};
+    a.points = points;
+    a.diffuse = diffuse;
+    a.specular = specular;
+    a.density = density;
+    a.adjacency = adjacency;
+    a.offsets = offsets;
+    a.adj_diff = reinterpret_cast<const uint2 *>(adj_diff_workspace);
+    a.rays = rays;
+    a.num_rays = num_rays;
+    a.start_point = start_point;
+    a.K = depth_quantiles ? num_quantiles : 0;
+    a.quantiles = (depth_quantiles && num_quantiles) ? depth_quantiles : nullptr;
+    a.thr = weight_threshold;
+    a.max_steps = max_intersections;
+    a.rgba = rgba;
+    a.depth = depth;
+    a.depth_idx = depth_idx;
+    a.contribution = contribution;
+    a.n_out = num_intersections;
+    a.distortion = distortion;
+    a.W_total = W_total;
+    a.S_total = S_total;
+    a.t_far = t_far;
+    a.stats = reinterpret_cast<uint32_t *>(stats);
+    return launch_train<FwdK>(attr_dtype, a, diff_res, spec_res, stats != nullptr, s);
+}
+
+extern "C" int vt_trace_bwd(int attr_dtype, const float *points, const void *diffuse, const void *specular,
+                            uint32_t diff_res, uint32_t spec_res, const float *density, const uint32_t *adjacency,
+                            uint32_t adjacency_size, const uint32_t *offsets, uint32_t num_points, const float *rays,
+                            uint32_t num_rays, const uint32_t *start_point, const void *rgba, const void *rgba_grad,
+                            uint32_t num_quantiles, const float *depth_quantiles, const uint32_t *depth_idx,
+                            const float *depth_grad, const void *ray_error, float contribution_alpha_grad,
+                            const float *distortion, const float *distortion_grad, const float *W_total,
+                            const float *S_total, const float *t_far, float weight_threshold,
+                            uint32_t max_intersections, float *points_grad, void *diffuse_grad, void *specular_grad,
+                            float *density_grad, void *point_error, uint16_t *adj_diff_workspace,
+                            vt_ray_stats *stats, vt_stream_t stream)
+{
+    clear_error();
+    (void)t_far;
+    VT_REQUIRE(points && diffuse && specular && density && adjacency && offsets && adj_diff_workspace,
+               "null scene pointer");
+    VT_REQUIRE(num_rays == 0 || (rays && start_point && rgba && rgba_grad), "null ray pointer");
+    VT_REQUIRE(points_grad && diffuse_grad && specular_grad && density_grad, "null gradient output");
+    VT_REQUIRE(!depth_quantiles || num_quantiles == 0 || (depth_idx && depth_grad),
+               "depth_idx and depth_grad required when depth_quantiles is given");
+    VT_REQUIRE(!ray_error || point_error, "point_error output required when ray_error is given");
+    hipStream_t s = as_stream(stream);
+    int rc = prefetch(points, num_points, adjacency, adjacency_size, offsets, adj_diff_workspace, s);
+    if (rc)
+        return rc;
+    BwdArgs a{};
+    a.points = points;
+    a.diffuse = diffuse;
+    a.specular = specular;
+    a.density = density;
+    a.adjacency = adjacency;
+    a.offsets = offsets;
+    a.adj_diff = reinterpret_cast<const uint2 *>(adj_diff_workspace);
+    a.rays = rays;
+    a.num_rays = num_rays;
+    a.start_point = start_point;
+    a.rgba = rgba;
+    a.rgba_grad = rgba_grad;
+    a.K = depth_quantiles ? num_quantiles : 0;
+    a.quantiles = (depth_quantiles && num_quantiles) ? depth_quantiles : nullptr;
+    a.depth_idx = depth_idx;
+    a.depth_grad = depth_grad;
+    a.ray_error = ray_error;
+    a.contribution_alpha_grad = contribution_alpha_grad;
+    a.distortion = distortion;
+    a.distortion_grad = distortion_grad;
+    a.W_total = W_total;
+    a.S_total = S_total;
+    a.thr = weight_threshold;
+    a.max_steps = max_intersections;
+    a.points_grad = points_grad;
+    a.diffuse_grad = diffuse_grad;
+    a.specular_grad = specular_grad;
+    a.density_grad = density_grad;
+    a.point_error = point_error;
+    a.stats = reinterpret_cast<uint32_t *>(stats);
+    return launch_train<BwdK>(attr_dtype, a, diff_res, spec_res, stats != nullptr, s);
+}

@@ -1,0 +1,104 @@
+"""Torch-tensor wrappers over the full C ABI (include/vt_abi.h), including
+options the reference surface does not expose: per-ray walk statistics,
+in-kernel wave tiling, explicit streams.  Used by the callers in infer.py,
+the benchmark and the tests.  No validation beyond what the library does:
+callers pass contiguous device tensors of the documented dtypes.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+STATS_WORDS = 8  # vt_ray_stats = 8 u32 words
+
+
+def _p(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _s(device, stream=None) -> int:
+    if stream is None:
+        stream = torch.cuda.current_stream(device)
+    return stream.cuda_stream
+
+
+def new_stats(num_rays: int, device) -> torch.Tensor:
+    return torch.zeros((num_rays, STATS_WORDS), dtype=torch.uint32, device=device)
+
+
+def map_res(width: int, channels: int) -> int:
+    import math
+
+    r = int(round(math.sqrt(width / channels)))
+    if r * r * channels != width:
+        raise ValueError(f"map width {width} is not {channels}*R*R")
+    return r
+
+
+def math_probe(op: int, x: torch.Tensor) -> torch.Tensor:
+    x = x.contiguous()
+    out = torch.empty(x.shape, dtype=torch.uint32, device=x.device)
+    _lib.call("vt_math_probe", op, x.data_ptr(), out.data_ptr(), x.numel(), _s(x.device))
+    return out
+
+
+def prefetch(points, adjacency, offsets, out=None, stream=None):
+    n = points.size(0)
+    m = adjacency.size(0)
+    if out is None:
+        out = torch.empty((m + 32, 4), dtype=torch.float16, device=points.device)
+    _lib.call("vt_prefetch_adj", points.data_ptr(), n, adjacency.data_ptr(), m, offsets.data_ptr(), out.data_ptr(),
+              _s(points.device, stream))
+    return out
+
+
+def infer_f16(points, diffuse4, specular4, density, adjacency, offsets, adj_diff, rays, start_point, ray_perm=None,
+              weight_threshold=0.001, max_intersections=1024, cell_skip_threshold=0.0, stats=None, out=None,
+              tiled=None, stream=None):
+    """fp16 inference.  ``tiled=(tile_h, tile_w)`` uses the in-kernel wave
+    tiling over rays shaped (B, H, W, 6) or (H, W, 6)."""
+    rd = map_res(diffuse4.shape[-1], 4)
+    rs = map_res(specular4.shape[-1], 4)
+    nr = rays.numel() // 6
+    if out is None:
+        out = torch.empty(list(rays.shape[:-1]) + [4], dtype=torch.float16, device=rays.device)
+    dev = rays.device
+    if tiled is not None:
+        shp = rays.shape[:-1]
+        if len(shp) == 2:
+            B, H, W = 1, shp[0], shp[1]
+        else:
+            B, H, W = shp[0], shp[1], shp[2]
+        _lib.call("vt_trace_infer_f16_tiled", points.data_ptr(), diffuse4.data_ptr(), specular4.data_ptr(), rd, rs,
+                  density.data_ptr(), adjacency.data_ptr(), offsets.data_ptr(), points.size(0), adj_diff.data_ptr(),
+                  rays.data_ptr(), B, H, W, tiled[0], tiled[1], start_point.data_ptr(), float(weight_threshold),
+                  int(max_intersections), float(cell_skip_threshold), out.data_ptr(), _p(stats), _s(dev, stream))
+    else:
+        _lib.call("vt_trace_infer_f16", points.data_ptr(), diffuse4.data_ptr(), specular4.data_ptr(), rd, rs,
+                  density.data_ptr(), adjacency.data_ptr(), offsets.data_ptr(), points.size(0), adj_diff.data_ptr(),
+                  rays.data_ptr(), nr, start_point.data_ptr(), _p(ray_perm), float(weight_threshold),
+                  int(max_intersections), float(cell_skip_threshold), out.data_ptr(), _p(stats), _s(dev, stream))
+    return out
+
+
+def infer_q8(points, diffuse_q8, specular_q8, scales, density, adjacency, offsets, adj_diff, rays, start_point,
+             ray_perm=None, weight_threshold=0.001, max_intersections=1024, cell_skip_threshold=0.0, stats=None,
+             out=None, stream=None):
+    """q8 inference; ``scales`` = (diff_scale[3], diff_offset[3], spec_scale[3], spec_offset[3])."""
+    rd = map_res(diffuse_q8.shape[-1], 3)
+    rs = map_res(specular_q8.shape[-1], 3)
+    nr = rays.numel() // 6
+    if out is None:
+        out = torch.empty(list(rays.shape[:-1]) + [4], dtype=torch.float16, device=rays.device)
+    arrs = [(C.c_float * 3)(*[float(v) for v in torch.as_tensor(x, dtype=torch.float32).reshape(-1).tolist()])
+            for x in scales]
+    _lib.call("vt_trace_infer_q8", points.data_ptr(), diffuse_q8.data_ptr(), specular_q8.data_ptr(), rd, rs,
+              *[C.cast(a, C.c_void_p) for a in arrs], density.data_ptr(), adjacency.data_ptr(), offsets.data_ptr(),
+              points.size(0), adj_diff.data_ptr(), rays.data_ptr(), nr, start_point.data_ptr(), _p(ray_perm),
+              float(weight_threshold), int(max_intersections), float(cell_skip_threshold), out.data_ptr(), _p(stats),
+              _s(rays.device, stream))
+    return out
