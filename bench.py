@@ -1,0 +1,271 @@
+"""Benchmark of the VoroTracing traversal hot path on one MI355X.
+
+Workload ("C3"): 1,048,576-site height-field scene
+(seed 0), Morton-sorted, 4x4 fp16 octahedral textures, 1237x822 pinhole orbit
+over 32 poses, weight threshold 0.01, cell-skip 1e-3, fp16 inference.  A
+step is one ``VoroTracingInfer.render`` of one pose (start-cell LBVH query +
+traversal kernel), as timed by the reference's benchmark_eval.py:137-158;
+``value`` = frames per second over ``--steps`` renders (rays resident in HBM).
+
+Also reported: the traversal kernel's duration from HIP events on its stream,
+its algorithmic bytes per frame (from the kernel's own per-ray walk counters)
+and the fraction of MI355X's 8 TB/s HBM peak; the CPU oracle on a bounded
+sample of the same frame; optionally (``--train``) the config-2 training step
+(fwd + bwd ms/step, 262,144 sites, 800x600 rays).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def b_alg(st, tex_bytes=64, per_ray_extra=0):
+    """Algorithmic bytes of the inference walk from per-ray counters (u32 (R,8) tensor).
+
+    per ray 24 (ray) + 4 (start) + 12 (start site) + 8 (rgba) ; per searched
+    cell 8 (offsets pair) + 8 per face record ; per exit 4 (neighbour id) + 12
+    (next site) ; per integrate_cell 4 (density) ; per shaded cell the two
+    maps' 4+4 texels (64 B fp16 Half4Texel, 24 B q8)."""
+    import torch
+
+    s = (st.view(torch.int32).to(torch.int64) & 0xffffffff).sum(0).tolist()
+    nr = st.shape[0]
+    return (48 + per_ray_extra) * nr + 8 * s[1] + 8 * s[2] + 16 * s[3] + 4 * s[4] + tex_bytes * s[5], s
+
+
+def cpu_info():
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return cores, model
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--poses", type=int, default=32)
+    ap.add_argument("--sites", type=int, default=1048576)
+    ap.add_argument("--width", type=int, default=1237)
+    ap.add_argument("--height", type=int, default=822)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU-baseline sample time")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--train", action="store_true", help="also time the config-2 fwd+bwd training step")
+    ap.add_argument("--profile", action="store_true", help="short run for rocprofv3 (no CPU leg, no stats)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is design-only (see DESIGN.md)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from vorotracing_amd import _lib, camera, native, scene
+    from vorotracing_amd.infer import VoroTracingInfer
+    from vorotracing_amd.model import VoroTracing
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    _lib.load()
+    dev = torch.device("cuda:0")
+
+    t0 = time.time()
+    log(f"building scene C3 ({args.sites} sites, qhull)")
+    sc = scene.cached(scene.heightfield, 0, args.sites, 4, name="c3")
+    log(f"scene ready in {time.time() - t0:.1f}s: N={sc.num_points} M={sc.num_faces}")
+    model = VoroTracing.from_scene(sc, device=dev)
+    inf = VoroTracingInfer(model, sort_morton=True, quantize="fp16")
+    torch.cuda.synchronize()
+    log(f"inference prep done ({time.time() - t0:.1f}s)")
+
+    W, H = args.width, args.height
+    poses = []
+    for k in range(args.poses):
+        poses.append(torch.from_numpy(camera.orbit_rays(k, W, H, n=args.poses)).to(dev))
+    torch.cuda.synchronize()
+    log(f"{args.poses} poses of {W}x{H} rays resident ({time.time() - t0:.1f}s)")
+    thr, skip = 0.01, 1e-3
+    stream = torch.cuda.current_stream(dev)
+
+    # warmup
+    for i in range(args.warmup):
+        inf.render(poses[i % args.poses], weight_threshold=thr, cell_skip_threshold=skip)
+    torch.cuda.synchronize()
+
+    # timed region: K renders, events around each traversal launch on its stream
+    K = args.steps
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
+    frames = []
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for i in range(K):
+        rays = poses[i % args.poses]
+        sp = inf.get_starting_point(rays)
+        ev[i][0].record(stream)
+        out = inf.render(rays, start_point=sp, weight_threshold=thr, cell_skip_threshold=skip)
+        ev[i][1].record(stream)
+        frames.append(out)
+    torch.cuda.synchronize()
+    t_total = time.perf_counter() - t_start
+    kern_ms = [a.elapsed_time(b) for a, b in ev]
+    ms_per_step = 1000.0 * t_total / K
+    fps = K / t_total
+    kernel_avg_ms = float(np.mean(kern_ms))
+    log(f"timed {K} frames: {ms_per_step:.3f} ms/frame, {fps:.1f} FPS, traversal kernel {kernel_avg_ms:.3f} ms")
+
+    result = {
+        "metric": "FPS @1237x822 1M cells fp16; fwd+bwd ms/step; achieved HBM GB/s",
+        "value": round(fps, 2),
+        "unit": "frames/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 storage, fp32 arithmetic",
+        "data": "synthetic (seeded height-field scene, BASELINE.json configs[2])",
+        "config": {"workload": "C3: fp16 inference render, 1,048,576 sites (Morton-sorted), 4x4 octahedral "
+                               "textures, 1237x822 pinhole orbit x32 poses, thr 0.01, skip 1e-3",
+                   "sites": sc.num_points, "faces": sc.num_faces, "width": W, "height": H, "poses": args.poses,
+                   "tiling": "8x8 wave64 tiles in-kernel", "parallelism": "single GPU"},
+    }
+
+    if not args.profile:
+        # algorithmic bytes from the kernel's walk counters (every pose once)
+        tot_b = 0
+        tot_s = np.zeros(6, np.int64)
+        nr = W * H
+        st = native.new_stats(nr, dev)
+        for k in range(args.poses):
+            inf.render(poses[k], weight_threshold=thr, cell_skip_threshold=skip, stats=st)
+            b, s = b_alg(st)
+            tot_b += b
+            tot_s += np.array(s[:6], np.int64)
+        torch.cuda.synchronize()
+        bytes_per_frame = tot_b / args.poses
+        achieved = bytes_per_frame / (kernel_avg_ms * 1e-3) / 1e9
+        result["roofline"] = {
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "bytes_per_launch": int(bytes_per_frame), "kernel_ms": round(kernel_avg_ms, 4),
+        }
+        result["walk"] = {
+            "rays_per_frame": nr,
+            "steps_per_ray": round(float(tot_s[1]) / (nr * args.poses), 2),
+            "faces_per_step": round(float(tot_s[2]) / max(tot_s[1], 1), 2),
+            "shaded_per_ray": round(float(tot_s[5]) / (nr * args.poses), 2),
+            "mrays_per_s": round(nr * fps / 1e6, 1),
+        }
+        log(f"B_alg {bytes_per_frame / 1e9:.3f} GB/frame -> {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%})")
+        prof = os.path.join(ROOT, "profiles", "traffic_infer_f16_c3.json")
+        if os.path.exists(prof):
+            with open(prof) as f:
+                tr = json.load(f)
+            result["roofline"]["traffic"] = tr.get("hbm_bytes_per_launch")
+            result["roofline"]["traffic_source"] = "profiles/traffic_infer_f16_c3.json (rocprofv3 --pmc)"
+
+    if not args.no_cpu and not args.profile:
+        from oracle import core as oc
+
+        cores, model_name = cpu_info()
+        pose = poses[0].cpu().numpy()
+        sp0 = inf.get_starting_point(poses[0]).cpu().numpy()
+        pts = inf.primal_points.cpu().numpy()
+        d4 = inf.diffuse_fp16.cpu().numpy()
+        s4 = inf.specular_fp16.cpu().numpy()
+        den = inf.density.reshape(-1).cpu().numpy()
+        adj = inf.point_adjacency.cpu().numpy()
+        off = inf.point_adjacency_offsets.cpu().numpy()
+        ad = inf.adjacent_diff.cpu().numpy()
+        # calibrate on a small row band, then size the sample to ~cpu-seconds
+        rows = 8
+        tc = time.perf_counter()
+        oc.trace_infer_f16(pts, d4, s4, 4, 4, den, adj, off, ad, pose[:rows], sp0[:rows], weight_threshold=thr,
+                           cell_skip_threshold=skip, threads=cores)
+        dt = time.perf_counter() - tc
+        per_row = dt / rows
+        rows = int(min(H, max(8, args.cpu_seconds / max(per_row, 1e-6))))
+        stride = max(1, H // rows)
+        sel = np.arange(0, H, stride)[:rows]
+        tc = time.perf_counter()
+        got, _, _ = oc.trace_infer_f16(pts, d4, s4, 4, 4, den, adj, off, ad, np.ascontiguousarray(pose[sel]),
+                                       np.ascontiguousarray(sp0[sel]), weight_threshold=thr,
+                                       cell_skip_threshold=skip, threads=cores)
+        dt = time.perf_counter() - tc
+        rays_s = len(sel) * W / dt
+        gpu_rows = frames[0].cpu().numpy()[sel]
+        same = bool(np.array_equal(gpu_rows.view(np.uint16), got.view(np.uint16)))
+        result["cpu_baseline"] = {
+            "value": round(rays_s / (W * H), 4), "unit": "frames/s", "cores": cores, "kind": "port",
+            "sample": f"{len(sel)} of {H} rows (every {stride}th) of pose 0, {len(sel) * W} rays, {dt:.1f}s; "
+                      f"oracle/oracle.c OpenMP on {model_name or 'host CPU'}",
+            "mrays_per_s": round(rays_s / 1e6, 3),
+            "bit_identical_to_gpu": same,
+        }
+        log(f"CPU oracle: {rays_s / 1e6:.3f} Mrays/s on {cores} threads; rows bit-identical to GPU: {same}")
+
+    if args.train:
+        result["train_c2"] = train_c2(dev, log)
+
+    print(json.dumps(result), flush=True)
+
+
+def train_c2(dev, log):
+    """Config-2 training step: TraceVoroTracing forward + backward (fp32), 262,144 sites, 800x600 rays."""
+    import numpy as np
+    import torch
+
+    from vorotracing_amd import camera, scene
+    from vorotracing_amd.model import VoroTracing
+
+    t0 = time.time()
+    sc = scene.cached(scene.config2, 0)
+    log(f"C2 scene {time.time() - t0:.1f}s")
+    model = VoroTracing.from_scene(sc, device=dev)
+    rays = torch.from_numpy(camera.pinhole_rays(800, 600, eye=(0.0, -4.0, 0.0))).to(dev)
+    g = torch.from_numpy(np.random.default_rng(0).normal(size=(600, 800, 4)).astype(np.float32)).to(dev)
+    g[..., 3] = 0
+    sp = model.get_starting_point(rays)
+
+    def step():
+        model.zero_grad(set_to_none=True)
+        rgba, _, _, _, _, dist = model(rays, start_point=sp, weight_threshold=0.001)
+        rgba.backward(g)
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    K = 10
+    t = time.perf_counter()
+    for _ in range(K):
+        step()
+    torch.cuda.synchronize()
+    ms = 1000 * (time.perf_counter() - t) / K
+    log(f"C2 fwd+bwd {ms:.2f} ms/step")
+    return {"fwd_bwd_ms_per_step": round(ms, 3), "rays": 480000, "sites": sc.num_points, "dtype": "fp32"}
+
+
+if __name__ == "__main__":
+    main()

@@ -107,6 +107,19 @@ int vt_trace_infer_q8(const float *points, const uint8_t *diffuse, const uint8_t
                       float cell_skip_threshold, uint16_t *rgba, vt_ray_stats *stats, vt_stream_t stream);
 
 /*
+ * q8 inference over image batches with in-kernel wave tiling (as
+ * vt_trace_infer_f16_tiled; per-ray results identical to vt_trace_infer_q8).
+ */
+int vt_trace_infer_q8_tiled(const float *points, const uint8_t *diffuse, const uint8_t *specular, uint32_t diff_res,
+                            uint32_t spec_res, const float diff_scale[3], const float diff_offset[3],
+                            const float spec_scale[3], const float spec_offset[3], const float *density,
+                            const uint32_t *adjacency, const uint32_t *offsets, uint32_t num_points,
+                            const uint16_t *adj_diff, const float *rays, uint32_t num_images, uint32_t image_h,
+                            uint32_t image_w, uint32_t tile_h, uint32_t tile_w, const uint32_t *start_point,
+                            float weight_threshold, uint32_t max_intersections, float cell_skip_threshold,
+                            uint16_t *rgba, vt_ray_stats *stats, vt_stream_t stream);
+
+/*
  * Training forward.  Replaces _C.trace_vorotracing_fwd
  * (tracing_octmap.cu:346-546, kernel :151-230).  Runs the prefetch into
  * `adj_diff_workspace` ((adjacency_size+32)*4 halves) as the reference does
@@ -149,6 +162,68 @@ int vt_trace_bwd(int attr_dtype, const float *points, const void *diffuse, const
                  float weight_threshold, uint32_t max_intersections, float *points_grad, void *diffuse_grad,
                  void *specular_grad, float *density_grad, void *point_error, uint16_t *adj_diff_workspace,
                  vt_ray_stats *stats, vt_stream_t stream);
+
+/*
+ * Start-cell lookup.  Replaces _C.NNBVH (nn_bvh.h:4-16, nn_bvh.cu:43-109):
+ * a Morton LBVH built on the GPU, exact nearest-site queries.
+ *   vt_bvh_create: new empty handle (host object owning device memory).
+ *   vt_bvh_build: (re)build over points (num_points, 3) f32 (nn_bvh.cu:63-89).
+ *   vt_bvh_query: out[i] = index of the site nearest to queries[i] (int32,
+ *   nn_bvh.cu:91-109); squared distance in fp32, ties to the lowest index.
+ *   `points` must be the array the handle was built on.
+ *   vt_bvh_destroy: free the handle (nn_bvh.cu:53-61).
+ */
+int vt_bvh_create(void **handle);
+int vt_bvh_destroy(void *handle);
+int vt_bvh_build(void *handle, const float *points, uint32_t num_points, vt_stream_t stream);
+int vt_bvh_query(void *handle, const float *points, uint32_t num_points, const float *queries, uint32_t num_queries,
+                 int32_t *out, vt_stream_t stream);
+int vt_bvh_num_nodes(void *handle);
+
+/*
+ * Morton reorder of cells.  Replaces VoroTracingInfer._reorder_by_morton
+ * (vorotracing.py:514-571): 10-bit-per-axis Morton keys of the sites in their
+ * bounding box, stable sort (the reference's argsort leaves ties unordered),
+ * perm[i] = old index of new cell i, sites gathered, neighbour ids remapped,
+ * face lists copied in their original order, new offsets; adjacency_out
+ * (adjacency_size entries) is zero past offsets_out[num_points].
+ * workspace: vt_morton_workspace_size() bytes.  Other per-cell rows
+ * (density, textures) follow with vt_permute_rows.
+ */
+size_t vt_morton_workspace_size(uint32_t num_points, uint32_t adjacency_size);
+int vt_morton_reorder(const float *points, uint32_t num_points, const uint32_t *adjacency, uint32_t adjacency_size,
+                      const uint32_t *offsets, uint32_t *perm, float *points_out, uint32_t *adjacency_out,
+                      uint32_t *offsets_out, void *workspace, vt_stream_t stream);
+/* dst row i = src row perm[i] (rows of row_bytes bytes; vorotracing.py:536-543) */
+int vt_permute_rows(const void *src, uint32_t rows, uint32_t row_bytes, const uint32_t *perm, void *dst,
+                    vt_stream_t stream);
+
+/*
+ * Screen-tile lane permutation.  Replaces VoroTracingInfer._tile_perm
+ * (vorotracing.py:606-625): perm (height*width) int32, lane t renders pixel
+ * perm[t], tiles of tile_h x tile_w in row-major tile order (the reference
+ * uses 4 x 8 for 32-wide warps; wave64 uses 8 x 8).
+ */
+int vt_tile_perm(uint32_t height, uint32_t width, uint32_t tile_h, uint32_t tile_w, int32_t *perm,
+                 vt_stream_t stream);
+
+/*
+ * q8 quantisation.  Replaces VoroTracingInfer._quantize_to_uint8
+ * (vorotracing.py:495-503): scale = fp32((vmax - vmin) / 255) (double
+ * arithmetic), offset = vmin, q = clamp(rint((x - offset) * fp32(1/scale)),
+ * 0, 255).  per_channel = 1 computes one (scale, offset) per RGB channel of
+ * the texel-major map (cols % 3 == 0).  params out (device): 9 floats =
+ * scale[3], offset[3], 1/scale[3] (all three equal when per-tensor).
+ * workspace: vt_quantize_workspace_size() bytes.
+ */
+size_t vt_quantize_workspace_size(void);
+int vt_quantize_u8(const float *x, uint32_t rows, uint32_t cols, int per_channel, uint8_t *q, float *params,
+                   void *workspace, vt_stream_t stream);
+
+/* fp16 Half4Texel padding.  Replaces VoroTracingInfer._pad_3to4 applied to
+ * .half() maps (vorotracing.py:477-482, :505-512): f32 (rows, 3*T) ->
+ * f16 (rows, 4*T), RNE cast, zero 4th channel. */
+int vt_pad_3to4_f16(const float *x, uint32_t rows, uint32_t texels_per_row, uint16_t *out, vt_stream_t stream);
 
 /*
  * Self-test of the device arithmetic shared by restatement with the CPU

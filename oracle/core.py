@@ -126,6 +126,13 @@ def oct_encode(d, R):
     return uv
 
 
+def cell_intersection_grad(prim, opp, o, d):
+    a = [_c(np.asarray(x), np.float32) for x in (prim, opp, o, d)]
+    out = np.empty(3, np.float32)
+    lib().or_cell_intersection_grad(*[_p(x) for x in a], _p(out))
+    return out
+
+
 # --------------------------------------------------------------------------
 # kernels
 

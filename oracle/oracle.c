@@ -1000,3 +1000,14 @@ void or_nearest_site(const float *points, uint32_t num_points, const float *quer
         out[qi] = bi;
     }
 }
+
+/* exported for tests: ray_integrator.cuh:39-53 */
+void or_cell_intersection_grad(const float prim[3], const float opp[3], const float o[3], const float d[3],
+                               float out[3])
+{
+    v3 g = cell_intersection_grad(mk(prim[0], prim[1], prim[2]), mk(opp[0], opp[1], opp[2]), mk(o[0], o[1], o[2]),
+                                  mk(d[0], d[1], d[2]));
+    out[0] = g.x;
+    out[1] = g.y;
+    out[2] = g.z;
+}

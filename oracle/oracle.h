@@ -109,6 +109,10 @@ void or_trace_bwd(int attr_f16, const float *points, const void *diffuse, const 
 void or_nearest_site(const float *points, uint32_t num_points, const float *queries, uint32_t num_queries,
                      int32_t *out, int num_threads);
 
+/* d t / d prim for the bisector plane of (prim, opp) (ray_integrator.cuh:39-53) */
+void or_cell_intersection_grad(const float prim[3], const float opp[3], const float o[3], const float d[3],
+                               float out[3]);
+
 #ifdef __cplusplus
 }
 #endif

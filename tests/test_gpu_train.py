@@ -1,0 +1,160 @@
+"""GPU parity of the training forward / backward against the CPU oracle.
+
+Forward outputs are deterministic and compared bit-for-bit (rgba, n, depth,
+depth_idx, distortion, W/S totals, t_far); atomically accumulated outputs
+(contribution, all gradients) are compared with the north star's 1e-3
+relative tolerance, measured against each tensor's largest magnitude (the
+GPU adds in a different order than the serial-per-ray CPU loop).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import core
+from tests import helpers as H
+from vorotracing_amd import _C, camera, ops
+from vorotracing_amd.model import VoroTracing
+
+pytestmark = pytest.mark.gpu
+
+GRAD_RTOL = 1e-3
+
+
+def _rel_err(got, want):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    scale = max(np.abs(want).max(), 1e-30)
+    return float(np.abs(got - want).max() / scale)
+
+
+def _scene_tensors(s, dev, f16):
+    adt = np.float16 if f16 else np.float32
+    return (H.to_dev(s.points, dev), H.to_dev(s.diffuse.astype(adt), dev), H.to_dev(s.specular.astype(adt), dev),
+            H.to_dev(s.density, dev), H.to_dev(s.adjacency, dev), H.to_dev(s.offsets, dev))
+
+
+def _case(which):
+    if which == "c1":
+        s = H.c1_scene()
+        rays = camera.pinhole_rays(64, 48, eye=(0.0, -4.0, 0.0))
+        thr = 0.01
+    elif which == "r8":
+        s = H.small_random(1500, seed=5, R=8, Rs=4)
+        rays = camera.pinhole_rays(48, 40, eye=(0.3, -3.2, 0.4))
+        thr = 0.001
+    else:
+        s = H.mini_heightfield()
+        rays = camera.orbit_rays(5, 64, 48)
+        thr = 0.001
+    return s, rays, H.start_for(s, rays), thr
+
+
+@pytest.mark.parametrize("which,f16", [("c1", False), ("r8", False), ("mini_c3", False), ("c1", True)])
+def test_fwd_parity(gpu, which, f16):
+    s, rays, start, thr = _case(which)
+    q = np.tile(np.array([0.9, 0.5, 0.1], np.float32), rays.shape[:-1] + (1,))
+    adt = np.float16 if f16 else np.float32
+    want = core.trace_fwd(s.points, s.diffuse.astype(adt), s.specular.astype(adt), s.diff_res, s.spec_res,
+                          s.density, s.adjacency, s.offsets, rays, start, depth_quantiles=q, weight_threshold=thr,
+                          return_contribution=True)
+    pts, dif, spe, den, adj, off = _scene_tensors(s, gpu, f16)
+    rgba, depth, depth_idx, contrib, n, dist, W, S, tf = _C.trace_vorotracing_fwd(
+        pts, dif, spe, den, adj, off, H.to_dev(rays, gpu), H.to_dev(start, gpu), H.to_dev(q, gpu), thr, 1024, True)
+    torch.cuda.synchronize()
+    assert rgba.dtype == (torch.float16 if f16 else torch.float32)
+    assert np.array_equal(n.cpu().numpy(), want["n"])
+    assert np.array_equal(rgba.cpu().numpy(), want["rgba"])
+    assert np.array_equal(depth_idx.cpu().numpy(), want["depth_idx"])
+    for got, key in ((depth, "depth"), (dist, "distortion"), (W, "W_total"), (S, "S_total"), (tf, "t_far")):
+        g = got.cpu().numpy()
+        assert np.array_equal(g.view(np.uint32), want[key].view(np.uint32)), key
+    # f16 storage: contribution is summed with half-precision atomics (as in the
+    # reference), so once a cell's sum is large, small weights are absorbed and
+    # the result depends on the add order; only f32 is held to a tight bound.
+    tol = 0.15 if f16 else 1e-5
+    assert _rel_err(contrib.cpu().numpy().astype(np.float32), want["contribution"].astype(np.float32)) <= tol
+
+
+@pytest.mark.parametrize("which,f16,extras", [("c1", False, True), ("r8", False, True), ("mini_c3", False, False),
+                                              ("c1", True, False)])
+def test_bwd_parity(gpu, which, f16, extras):
+    s, rays, start, thr = _case(which)
+    rng = np.random.default_rng(1)
+    adt = np.float16 if f16 else np.float32
+    q = np.tile(np.array([0.8, 0.3], np.float32), rays.shape[:-1] + (1,)) if extras else None
+    fw = core.trace_fwd(s.points, s.diffuse.astype(adt), s.specular.astype(adt), s.diff_res, s.spec_res, s.density,
+                        s.adjacency, s.offsets, rays, start, depth_quantiles=q, weight_threshold=thr)
+    g = rng.normal(size=rays.shape[:-1] + (4,)).astype(adt)
+    dg = rng.normal(size=rays.shape[:-1] + (2,)).astype(np.float32) * 0.1 if extras else None
+    distg = (rng.uniform(0, 1, size=rays.shape[:-1] + (1,)).astype(np.float32)) if extras else None
+    rerr = rng.uniform(0, 1, size=rays.shape[:-1]).astype(adt) if extras else None
+    cag = 0.25 if extras else 0.0
+    want = core.trace_bwd(s.points, s.diffuse.astype(adt), s.specular.astype(adt), s.diff_res, s.spec_res, s.density,
+                          s.adjacency, s.offsets, rays, start, fw["rgba"], g, depth_quantiles=q,
+                          depth_idx=fw["depth_idx"], depth_grad=dg, ray_error=rerr, contribution_alpha_grad=cag,
+                          distortion=fw["distortion"], distortion_grad=distg, W_total=fw["W_total"],
+                          S_total=fw["S_total"], t_far=fw["t_far"], weight_threshold=thr)
+    pts, dif, spe, den, adj, off = _scene_tensors(s, gpu, f16)
+    d = lambda a, dt=None: None if a is None else H.to_dev(a, gpu)  # noqa: E731
+    pg, dgd, sgd, deng, rayg, perr = _C.trace_vorotracing_bwd(
+        pts, dif, spe, den, adj, off, d(rays), d(start), d(fw["rgba"]), d(g), d(q), d(fw["depth_idx"]), d(dg),
+        d(rerr), cag, d(fw["distortion"]), d(distg), d(fw["W_total"]), d(fw["S_total"]), d(fw["t_far"]), thr, 1024)
+    torch.cuda.synchronize()
+    tol = 5e-2 if f16 else GRAD_RTOL  # f16 storage: each half-precision atomic add rounds, order-dependent
+    assert _rel_err(pg.cpu().numpy(), want["points_grad"]) <= GRAD_RTOL * (10 if f16 else 1)
+    assert _rel_err(deng.cpu().numpy(), want["density_grad"]) <= GRAD_RTOL * (10 if f16 else 1)
+    assert _rel_err(dgd.cpu().numpy().astype(np.float32), want["diffuse_grad"].astype(np.float32)) <= tol
+    assert _rel_err(sgd.cpu().numpy().astype(np.float32), want["specular_grad"].astype(np.float32)) <= tol
+    assert not rayg.cpu().numpy().any()
+    if extras:
+        assert _rel_err(perr.cpu().numpy(), want["point_error"]) <= GRAD_RTOL
+    else:
+        assert perr is None
+
+
+def test_autograd_model_forward_backward(gpu):
+    """VoroTracing.forward -> TraceVoroTracing -> loss.backward matches the oracle bwd."""
+    s, rays, start, thr = _case("c1")
+    model = VoroTracing.from_scene(s, device=gpu)
+    rays_d = H.to_dev(rays, gpu)
+    sp = model.get_starting_point(rays_d)
+    assert np.array_equal(sp.cpu().numpy(), start)
+    rgba, depth, contrib, n, errbox, dist = model(rays_d, start_point=sp, weight_threshold=thr)
+    gr = np.random.default_rng(2).normal(size=rgba.shape).astype(np.float32)
+    (rgba * torch.from_numpy(gr).to(gpu)).sum().backward()
+    dens = model._get_primal_density().detach().cpu().numpy()  # exp on the device, as the model feeds the kernel
+    fw = core.trace_fwd(s.points, s.diffuse, s.specular, 4, 4, dens, s.adjacency, s.offsets, rays, start,
+                        weight_threshold=thr)
+    want = core.trace_bwd(s.points, s.diffuse, s.specular, 4, 4, dens, s.adjacency, s.offsets, rays, start,
+                          fw["rgba"], gr, distortion=fw["distortion"], W_total=fw["W_total"], S_total=fw["S_total"],
+                          t_far=fw["t_far"], weight_threshold=thr)
+    assert np.array_equal(rgba.detach().cpu().numpy(), fw["rgba"])
+    assert _rel_err(model.primal_points.grad.cpu().numpy(), want["points_grad"]) <= GRAD_RTOL
+    assert _rel_err(model.att_diffuse.grad.cpu().numpy(), want["diffuse_grad"]) <= GRAD_RTOL
+    assert _rel_err(model.att_specular.grad.cpu().numpy(), want["specular_grad"]) <= GRAD_RTOL
+    # density enters through exp: d/draw = d/ds * s
+    ds = want["density_grad"] * dens
+    assert _rel_err(model.density.grad.cpu().numpy(), ds) <= GRAD_RTOL
+
+
+def test_train_errors_reference_messages(gpu):
+    s, rays, start, thr = _case("c1")
+    pts, dif, spe, den, adj, off = _scene_tensors(s, gpu, False)
+    r = H.to_dev(rays, gpu)
+    sp = H.to_dev(start, gpu)
+    with pytest.raises(RuntimeError, match="diffuse and specular must have the same dtype"):
+        _C.trace_vorotracing_fwd(pts, dif, spe.half(), den, adj, off, r, sp, None, thr, 1024, False)
+    with pytest.raises(RuntimeError, match="rays must have 6 as the last dimension"):
+        _C.trace_vorotracing_fwd(pts, dif, spe, den, adj, off, r[..., :5].contiguous(), sp, None, thr, 1024, False)
+    with pytest.raises(RuntimeError, match="start_point must have the same batch size as rays"):
+        _C.trace_vorotracing_fwd(pts, dif, spe, den, adj, off, r, sp[:3], None, thr, 1024, False)
+    with pytest.raises(RuntimeError, match="Unsupported color dtype"):
+        _C.trace_vorotracing_fwd(pts, dif.double(), spe.double(), den, adj, off, r, sp, None, thr, 1024, False)
+    out = _C.trace_vorotracing_fwd(pts, dif, spe, den, adj, off, r, sp, None, thr, 1024, False)
+    with pytest.raises(RuntimeError, match="rgb_grad_in must have 4 as the last dimension"):
+        _C.trace_vorotracing_bwd(pts, dif, spe, den, adj, off, r, sp, out[0], out[0][..., :3].contiguous(), None,
+                                 None, None, None, 0.0, out[5], None, out[6], out[7], out[8], thr, 1024)
+    with pytest.raises(RuntimeError, match="depth_grad must be provided if depth_quantiles is provided"):
+        qd = torch.full(rays.shape[:-1] + (1,), 0.5, device=gpu)
+        _C.trace_vorotracing_bwd(pts, dif, spe, den, adj, off, r, sp, out[0], out[0], qd, out[2], None, None, 0.0,
+                                 out[5], None, out[6], out[7], out[8], thr, 1024)

@@ -28,6 +28,9 @@ SIGNATURES = {
         [P, P, P, U32, U32, P, P, P, U32, P, P, U32, U32, U32, U32, U32, P, F32, U32, F32, P, P, P], C.c_int),
     "vt_trace_infer_q8": (
         [P, P, P, U32, U32, P, P, P, P, P, P, P, U32, P, P, U32, P, P, F32, U32, F32, P, P, P], C.c_int),
+    "vt_trace_infer_q8_tiled": (
+        [P, P, P, U32, U32, P, P, P, P, P, P, P, U32, P, P, U32, U32, U32, U32, U32, P, F32, U32, F32, P, P, P],
+        C.c_int),
     "vt_trace_fwd": (
         [I32, P, P, P, U32, U32, P, P, U32, P, U32, P, U32, P, U32, P, F32, U32, P, P, P, P, P, P, P, P, P, P, P, P],
         C.c_int),
@@ -42,7 +45,7 @@ SIGNATURES = {
     "vt_bvh_num_nodes": ([P], C.c_int),
     "vt_tile_perm": ([U32, U32, U32, U32, P, P], C.c_int),
     "vt_morton_workspace_size": ([U32, U32], C.c_size_t),
-    "vt_morton_reorder": ([P, U32, P, U32, P, P, P, U32, P, P, P, P, P, P, P], C.c_int),
+    "vt_morton_reorder": ([P, U32, P, U32, P, P, P, P, P, P, P], C.c_int),
     "vt_permute_rows": ([P, U32, U32, P, P, P], C.c_int),
     "vt_quantize_u8": ([P, U32, U32, I32, P, P, P, P], C.c_int),
     "vt_quantize_workspace_size": ([], C.c_size_t),

@@ -1,0 +1,353 @@
+// vt_bvh.hip -- start-cell lookup: a linear BVH over the sites (replaces the
+// cuBQL BinaryBVH of nn_bvh.cu:12-117) and an exact nearest-site query.
+//
+// Build: bounding box -> 30-bit Morton codes -> stable radix sort -> binary
+// radix tree over the sorted codes (Karras 2012, ties in the code broken by
+// sorted position) -> bottom-up refit.  Each internal node stores both
+// children's boxes, so a query tests two boxes per node fetch.
+// Query: depth-first, nearer child first, exact: squared distance
+// dot(q - p, q - p) (fma convention) and ties to the lowest site index, with
+// conservative box pruning so rounding can never drop a closer site.
+#include "vt_internal.h"
+#include "vt_prims.h"
+#include "vt_device.h"
+
+namespace vt {
+
+struct BvhNode {          // 64 bytes
+    float lo[2][3];       // child boxes: [0] = left, [1] = right
+    float hi[2][3];
+    uint32_t child[2];    // LEAF bit | sorted leaf position, or internal index
+    uint32_t parent, pad; // parent internal index (NONE for the root)
+};
+
+constexpr uint32_t LEAF = 0x80000000u;
+
+struct BvhHandle {
+    uint32_t n = 0, cap = 0;
+    BvhNode *nodes = nullptr;    // n-1 internal nodes
+    uint32_t *leaf_idx = nullptr; // sorted position -> site index
+    uint32_t *leaf_parent = nullptr;
+    uint32_t *flags = nullptr;
+    uint32_t *ws = nullptr;
+    size_t ws_words = 0;
+    float *bb = nullptr;
+};
+
+__device__ __forceinline__ int bvh_delta(const uint32_t *__restrict__ keys, uint32_t n, int i, int j)
+{
+    if (j < 0 || j >= (int)n)
+        return -1;
+    uint32_t a = keys[i], b = keys[j];
+    if (a != b)
+        return __builtin_clz(a ^ b);
+    return 32 + __builtin_clz((uint32_t)i ^ (uint32_t)j);
+}
+
+__global__ void bvh_keys_kernel(const float *__restrict__ points, uint32_t n, const float *__restrict__ bb,
+                                uint32_t *__restrict__ keys, uint32_t *__restrict__ vals)
+{
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n)
+        return;
+    f3 p = load_site(points, i);
+    float v[3] = {p.x, p.y, p.z};
+    uint32_t q[3];
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        float size = __builtin_fmaxf(bb[3 + c] - bb[c], 1e-30f);
+        float x = ((v[c] - bb[c]) / size) * 1023.0f;
+        q[c] = (uint32_t)__builtin_fminf(__builtin_fmaxf(x, 0.0f), 1023.0f);
+    }
+    uint32_t code = 0;
+#pragma unroll
+    for (int b = 0; b < 10; ++b)
+        code |= (((q[0] >> b) & 1u) << (3 * b + 2)) | (((q[1] >> b) & 1u) << (3 * b + 1)) |
+                (((q[2] >> b) & 1u) << (3 * b));
+    keys[i] = code;
+    vals[i] = i;
+}
+
+// Karras 2012, internal node i of n-1
+__global__ void bvh_hierarchy_kernel(const uint32_t *__restrict__ keys, uint32_t n, BvhNode *__restrict__ nodes,
+                                     uint32_t *__restrict__ leaf_parent, uint32_t *__restrict__ flags)
+{
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int)n - 1)
+        return;
+    flags[i] = 0;
+    int d = (bvh_delta(keys, n, i, i + 1) - bvh_delta(keys, n, i, i - 1)) >= 0 ? 1 : -1;
+    int dmin = bvh_delta(keys, n, i, i - d);
+    int lmax = 2;
+    while (bvh_delta(keys, n, i, i + lmax * d) > dmin)
+        lmax *= 2;
+    int l = 0;
+    for (int t = lmax / 2; t >= 1; t /= 2)
+        if (bvh_delta(keys, n, i, i + (l + t) * d) > dmin)
+            l += t;
+    int j = i + l * d;
+    int dnode = bvh_delta(keys, n, i, j);
+    int s = 0;
+    int div = 2;
+    int t = (l + div - 1) / div;
+    for (;;) {
+        if (bvh_delta(keys, n, i, i + (s + t) * d) > dnode)
+            s += t;
+        if (t == 1)
+            break;
+        div *= 2;
+        t = (l + div - 1) / div;
+    }
+    int gamma = i + s * d + min(d, 0);
+    int lo = min(i, j), hi = max(i, j);
+    uint32_t left = (lo == gamma) ? (LEAF | (uint32_t)gamma) : (uint32_t)gamma;
+    uint32_t right = (hi == gamma + 1) ? (LEAF | (uint32_t)(gamma + 1)) : (uint32_t)(gamma + 1);
+    nodes[i].child[0] = left;
+    nodes[i].child[1] = right;
+    if (left & LEAF)
+        leaf_parent[left & ~LEAF] = (uint32_t)i;
+    else
+        nodes[left].parent = (uint32_t)i;
+    if (right & LEAF)
+        leaf_parent[right & ~LEAF] = (uint32_t)i;
+    else
+        nodes[right].parent = (uint32_t)i;
+    if (i == 0)
+        nodes[0].parent = NONE;
+}
+
+// Bottom-up refit: each leaf writes its box into its parent's slot; the
+// second child to arrive at a node (atomic flag) merges and moves up.
+__global__ void bvh_refit_kernel(const float *__restrict__ points, const uint32_t *__restrict__ leaf_idx, uint32_t n,
+                                 BvhNode *nodes, const uint32_t *__restrict__ leaf_parent, uint32_t *flags)
+{
+    uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
+    if (k >= n)
+        return;
+    f3 p = load_site(points, leaf_idx[k]);
+    float lo[3] = {p.x, p.y, p.z}, hi[3] = {p.x, p.y, p.z};
+    uint32_t child = LEAF | k;
+    uint32_t node = leaf_parent[k];
+    while (node != NONE) {
+        int side = (nodes[node].child[0] == child) ? 0 : 1;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            __hip_atomic_store(&nodes[node].lo[side][c], lo[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&nodes[node].hi[side][c], hi[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __threadfence();
+        uint32_t prev = atomicAdd(&flags[node], 1u);
+        if (prev == 0)
+            return; // the sibling has not finished; it will continue upward
+        __threadfence();
+        int other = 1 - side;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            float olo = __hip_atomic_load(&nodes[node].lo[other][c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            float ohi = __hip_atomic_load(&nodes[node].hi[other][c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            lo[c] = __builtin_fminf(lo[c], olo);
+            hi[c] = __builtin_fmaxf(hi[c], ohi);
+        }
+        child = node;
+        node = nodes[node].parent;
+    }
+}
+
+__device__ __forceinline__ float box_d2(f3 q, const float *lo, const float *hi)
+{
+    float dx = __builtin_fmaxf(__builtin_fmaxf(lo[0] - q.x, 0.0f), q.x - hi[0]);
+    float dy = __builtin_fmaxf(__builtin_fmaxf(lo[1] - q.y, 0.0f), q.y - hi[1]);
+    float dz = __builtin_fmaxf(__builtin_fmaxf(lo[2] - q.z, 0.0f), q.z - hi[2]);
+    return fma_(dz, dz, fma_(dy, dy, dx * dx));
+}
+
+// prune a box only when its distance exceeds the best by more than the
+// rounding of either computation (relative 2^-16 margin)
+__device__ __forceinline__ bool box_may_hold(float bd2, float best) { return bd2 * 0.9999847f <= best; }
+
+constexpr int BVH_STACK = 64;
+
+__global__ __launch_bounds__(256) void bvh_query_kernel(const BvhNode *__restrict__ nodes,
+                                                        const uint32_t *__restrict__ leaf_idx, uint32_t n,
+                                                        const float *__restrict__ points,
+                                                        const float *__restrict__ queries, uint32_t nq,
+                                                        int32_t *__restrict__ out)
+{
+    uint32_t qi = xcd_block_linear();
+    if (qi >= nq)
+        return;
+    f3 q = load_site(queries, qi);
+    float best = __builtin_huge_valf();
+    uint32_t best_i = NONE;
+    auto visit_leaf = [&](uint32_t k) {
+        uint32_t idx = leaf_idx[k];
+        f3 df = sub(q, load_site(points, idx));
+        float d2 = dot(df, df);
+        if (d2 < best || (d2 == best && idx < best_i)) {
+            best = d2;
+            best_i = idx;
+        }
+    };
+    if (n == 1) {
+        visit_leaf(0);
+    } else {
+        uint32_t stack[BVH_STACK];
+        float sdist[BVH_STACK];
+        int sp = 0;
+        stack[sp] = 0;
+        sdist[sp] = 0.0f;
+        sp++;
+        while (sp > 0) {
+            sp--;
+            uint32_t node = stack[sp];
+            if (!box_may_hold(sdist[sp], best))
+                continue;
+            const BvhNode &nd = nodes[node];
+            float d0 = box_d2(q, nd.lo[0], nd.hi[0]);
+            float d1 = box_d2(q, nd.lo[1], nd.hi[1]);
+            uint32_t c0 = nd.child[0], c1 = nd.child[1];
+            // visit / push the farther child first so the nearer is expanded next
+            if (d1 < d0) {
+                uint32_t tc = c0;
+                c0 = c1;
+                c1 = tc;
+                float td = d0;
+                d0 = d1;
+                d1 = td;
+            }
+            if (box_may_hold(d1, best)) {
+                if (c1 & LEAF)
+                    visit_leaf(c1 & ~LEAF);
+                else if (sp < BVH_STACK) {
+                    stack[sp] = c1;
+                    sdist[sp] = d1;
+                    sp++;
+                }
+            }
+            if (box_may_hold(d0, best)) {
+                if (c0 & LEAF)
+                    visit_leaf(c0 & ~LEAF);
+                else if (sp < BVH_STACK) {
+                    stack[sp] = c0;
+                    sdist[sp] = d0;
+                    sp++;
+                }
+            }
+        }
+    }
+    out[qi] = (int32_t)best_i;
+}
+
+static int ensure_capacity(BvhHandle *h, uint32_t n)
+{
+    if (n <= h->cap && h->nodes)
+        return VT_OK;
+    hipFree(h->nodes);
+    hipFree(h->leaf_idx);
+    hipFree(h->leaf_parent);
+    hipFree(h->flags);
+    hipFree(h->ws);
+    hipFree(h->bb);
+    h->nodes = nullptr;
+    h->leaf_idx = h->leaf_parent = h->flags = h->ws = nullptr;
+    h->bb = nullptr;
+    h->cap = 0;
+    size_t ws_words = 2 * (size_t)n + radix_sort_workspace_words(n) + 16;
+    VT_HIP_CHECK(hipMalloc(&h->nodes, sizeof(BvhNode) * (size_t)(n > 1 ? n - 1 : 1)));
+    VT_HIP_CHECK(hipMalloc(&h->leaf_idx, 4 * (size_t)n));
+    VT_HIP_CHECK(hipMalloc(&h->leaf_parent, 4 * (size_t)n));
+    VT_HIP_CHECK(hipMalloc(&h->flags, 4 * (size_t)(n > 1 ? n - 1 : 1)));
+    VT_HIP_CHECK(hipMalloc(&h->ws, 4 * ws_words));
+    VT_HIP_CHECK(hipMalloc(&h->bb, 8 * sizeof(float)));
+    h->ws_words = ws_words;
+    h->cap = n;
+    return VT_OK;
+}
+
+} // namespace vt
+
+using namespace vt;
+
+extern "C" int vt_bvh_create(void **handle)
+{
+    clear_error();
+    VT_REQUIRE(handle, "null handle pointer");
+    *handle = new BvhHandle();
+    return VT_OK;
+}
+
+extern "C" int vt_bvh_destroy(void *handle)
+{
+    clear_error();
+    BvhHandle *h = (BvhHandle *)handle;
+    if (!h)
+        return VT_OK;
+    hipFree(h->nodes);
+    hipFree(h->leaf_idx);
+    hipFree(h->leaf_parent);
+    hipFree(h->flags);
+    hipFree(h->ws);
+    hipFree(h->bb);
+    delete h;
+    return VT_OK;
+}
+
+extern "C" int vt_bvh_build(void *handle, const float *points, uint32_t num_points, vt_stream_t stream)
+{
+    clear_error();
+    BvhHandle *h = (BvhHandle *)handle;
+    VT_REQUIRE(h, "null BVH handle");
+    VT_REQUIRE(points || num_points == 0, "null points");
+    VT_REQUIRE(num_points < 0x7fffffffu, "too many points");
+    hipStream_t s = as_stream(stream);
+    h->n = 0;
+    if (num_points == 0)
+        return VT_OK;
+    int rc = ensure_capacity(h, num_points);
+    if (rc)
+        return rc;
+    uint32_t n = num_points;
+    uint32_t *keys = h->ws;
+    uint32_t *sws = h->ws + n;
+    uint32_t *bbw = sws + radix_sort_workspace_words(n);
+    rc = bbox3(points, n, h->bb, bbw, s);
+    if (rc)
+        return rc;
+    bvh_keys_kernel<<<(n + 255) / 256, 256, 0, s>>>(points, n, h->bb, keys, h->leaf_idx);
+    VT_LAUNCH_CHECK("bvh_keys_kernel");
+    rc = radix_sort_pairs(keys, h->leaf_idx, n, 30, sws, s);
+    if (rc)
+        return rc;
+    if (n > 1) {
+        bvh_hierarchy_kernel<<<(n - 1 + 255) / 256, 256, 0, s>>>(keys, n, h->nodes, h->leaf_parent, h->flags);
+        VT_LAUNCH_CHECK("bvh_hierarchy_kernel");
+        bvh_refit_kernel<<<(n + 255) / 256, 256, 0, s>>>(points, h->leaf_idx, n, h->nodes, h->leaf_parent,
+                                                         h->flags);
+        VT_LAUNCH_CHECK("bvh_refit_kernel");
+    }
+    h->n = n;
+    return VT_OK;
+}
+
+extern "C" int vt_bvh_query(void *handle, const float *points, uint32_t num_points, const float *queries,
+                            uint32_t num_queries, int32_t *out, vt_stream_t stream)
+{
+    clear_error();
+    BvhHandle *h = (BvhHandle *)handle;
+    VT_REQUIRE(h, "null BVH handle");
+    VT_REQUIRE(h->n > 0, "BVH must be built before querying");
+    VT_REQUIRE(num_points == h->n, "points must be the point set the BVH was built on (%u vs %u)", num_points, h->n);
+    if (num_queries == 0)
+        return VT_OK;
+    VT_REQUIRE(points && queries && out, "null pointer argument");
+    bvh_query_kernel<<<(num_queries + 255) / 256, 256, 0, as_stream(stream)>>>(h->nodes, h->leaf_idx, h->n, points,
+                                                                             queries, num_queries, out);
+    VT_LAUNCH_CHECK("bvh_query_kernel");
+    return VT_OK;
+}
+
+extern "C" int vt_bvh_num_nodes(void *handle)
+{
+    BvhHandle *h = (BvhHandle *)handle;
+    return h ? (int)(h->n > 0 ? 2 * h->n - 1 : 0) : 0;
+}

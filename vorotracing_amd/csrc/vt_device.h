@@ -105,6 +105,19 @@ __device__ __forceinline__ float vt_logf(float x)
 
 __device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + vt_expf(-x)); }
 
+// Blocks are dispatched round-robin over the 8 XCDs of an MI355X, each with
+// its own L2.  Remap so that each XCD runs one contiguous range of logical
+// blocks (neighbouring rays -> neighbouring cells -> same L2).
+__device__ __forceinline__ uint32_t xcd_block()
+{
+    uint32_t G = gridDim.x, b = blockIdx.x;
+    uint32_t xcd = b & 7u, local = b >> 3;
+    uint32_t q = G >> 3, r = G & 7u;
+    return xcd < r ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
+}
+
+__device__ __forceinline__ uint32_t xcd_block_linear() { return xcd_block() * blockDim.x + threadIdx.x; }
+
 // ---------------------------------------------------------------------------
 // octahedral map (ray_integrator_octmap.cuh:17-55)
 

@@ -353,3 +353,57 @@ extern "C" int vt_trace_infer_q8(const float *points, const uint8_t *diffuse, co
     }
     return launch_infer<true>(a, diff_res, spec_res, stats != nullptr, MAP_LINEAR, as_stream(stream), num_rays);
 }
+
+extern "C" int vt_trace_infer_q8_tiled(const float *points, const uint8_t *diffuse, const uint8_t *specular,
+                                       uint32_t diff_res, uint32_t spec_res, const float diff_scale[3],
+                                       const float diff_offset[3], const float spec_scale[3],
+                                       const float spec_offset[3], const float *density, const uint32_t *adjacency,
+                                       const uint32_t *offsets, uint32_t num_points, const uint16_t *adj_diff,
+                                       const float *rays, uint32_t num_images, uint32_t image_h, uint32_t image_w,
+                                       uint32_t tile_h, uint32_t tile_w, const uint32_t *start_point,
+                                       float weight_threshold, uint32_t max_intersections, float cell_skip_threshold,
+                                       uint16_t *rgba, vt_ray_stats *stats, vt_stream_t stream)
+{
+    clear_error();
+    if (num_images == 0 || image_h == 0 || image_w == 0)
+        return VT_OK;
+    int rc = check_common(points, diffuse, specular, density, adjacency, offsets, adj_diff, rays, start_point, rgba);
+    if (rc)
+        return rc;
+    VT_REQUIRE(diff_scale && diff_offset && spec_scale && spec_offset, "null dequantisation parameters");
+    VT_REQUIRE(tile_h * tile_w == 64, "tile_h * tile_w must be 64 (one wave64 per tile), got %u x %u", tile_h,
+               tile_w);
+    (void)num_points;
+    uint64_t tiles = (uint64_t)((image_w + tile_w - 1) / tile_w) * ((image_h + tile_h - 1) / tile_h) * num_images;
+    VT_REQUIRE(tiles * 64 < (1ull << 32), "image batch too large");
+    VT_REQUIRE((uint64_t)num_images * image_h * image_w < (1ull << 32), "image batch too large");
+    InferArgs a{};
+    a.points = points;
+    a.diffuse = diffuse;
+    a.specular = specular;
+    a.density = density;
+    a.adjacency = adjacency;
+    a.offsets = offsets;
+    a.adj_diff = reinterpret_cast<const uint2 *>(adj_diff);
+    a.rays = rays;
+    a.num_rays = num_images * image_h * image_w;
+    a.start_point = start_point;
+    a.thr = weight_threshold;
+    a.skip = cell_skip_threshold;
+    a.max_steps = max_intersections;
+    a.rgba = rgba;
+    a.stats = reinterpret_cast<uint32_t *>(stats);
+    a.num_images = num_images;
+    a.H = image_h;
+    a.W = image_w;
+    a.th = tile_h;
+    a.tw = tile_w;
+    for (int c = 0; c < 3; ++c) {
+        a.ds[c] = diff_scale[c];
+        a.dof[c] = diff_offset[c];
+        a.ss[c] = spec_scale[c];
+        a.sof[c] = spec_offset[c];
+    }
+    return launch_infer<true>(a, diff_res, spec_res, stats != nullptr, MAP_TILED, as_stream(stream),
+                              (uint32_t)(tiles * 64));
+}

@@ -1,0 +1,369 @@
+// vt_prep.hip -- inference preparation on the GPU: Morton reorder of cells
+// with CSR rebuild (vorotracing.py:514-571), row permutation, screen-tile
+// permutation (vorotracing.py:606-625), q8 quantisation and fp16 4-channel
+// padding (vorotracing.py:495-512).
+#include "vt_internal.h"
+#include "vt_prims.h"
+#include "vt_device.h"
+
+namespace vt {
+
+// 10-bit-per-axis Morton code with the reference's quantisation
+// (vorotracing.py:519-530; same bit layout as geometry.h:271-283):
+// q = trunc(clamp((p - lo) / max(hi - lo, 1e-6) * 1023, 0, 1023)).
+__device__ __forceinline__ uint32_t morton10(f3 p, const float *bb)
+{
+    float v[3] = {p.x, p.y, p.z};
+    uint32_t q[3];
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        float size = __builtin_fmaxf(bb[3 + c] - bb[c], 1e-6f);
+        float x = ((v[c] - bb[c]) / size) * 1023.0f;
+        x = __builtin_fminf(__builtin_fmaxf(x, 0.0f), 1023.0f);
+        q[c] = (uint32_t)x;
+    }
+    uint32_t code = 0;
+#pragma unroll
+    for (int i = 0; i < 10; ++i) {
+        code |= ((q[0] >> i) & 1u) << (3 * i);
+        code |= ((q[1] >> i) & 1u) << (3 * i + 1);
+        code |= ((q[2] >> i) & 1u) << (3 * i + 2);
+    }
+    return code;
+}
+
+__global__ void morton_keys_kernel(const float *__restrict__ points, uint32_t n, const float *__restrict__ bb,
+                                   uint32_t *__restrict__ keys, uint32_t *__restrict__ vals)
+{
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n)
+        return;
+    keys[i] = morton10(load_site(points, i), bb);
+    vals[i] = i;
+}
+
+// new cell i = old cell perm[i]
+__global__ void morton_gather_kernel(const uint32_t *__restrict__ perm, uint32_t n, const float *__restrict__ points,
+                                     const uint32_t *__restrict__ offsets, float *__restrict__ points_out,
+                                     uint32_t *__restrict__ inv_perm, uint32_t *__restrict__ counts)
+{
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i > n)
+        return;
+    if (i == n) {
+        counts[n] = 0;
+        return;
+    }
+    uint32_t o = perm[i];
+    inv_perm[o] = i;
+    f3 p = load_site(points, o);
+    points_out[3 * (size_t)i + 0] = p.x;
+    points_out[3 * (size_t)i + 1] = p.y;
+    points_out[3 * (size_t)i + 2] = p.z;
+    counts[i] = offsets[o + 1] - offsets[o];
+}
+
+// Copy each face list to its new place, preserving intra-list order and
+// remapping neighbour ids through inv_perm.  One block per 256 new cells;
+// entries swept with unit stride, owner found by binary search in LDS.
+constexpr int CP_CELLS = 256;
+
+__global__ __launch_bounds__(CP_CELLS) void morton_copy_lists_kernel(
+    const uint32_t *__restrict__ perm, const uint32_t *__restrict__ inv_perm, uint32_t n,
+    const uint32_t *__restrict__ offsets, const uint32_t *__restrict__ adjacency,
+    const uint32_t *__restrict__ new_offsets, uint32_t *__restrict__ adjacency_out)
+{
+    __shared__ uint32_t off[CP_CELLS + 1];
+    __shared__ uint32_t src[CP_CELLS];
+    uint32_t c0 = blockIdx.x * CP_CELLS;
+    uint32_t cnt = min((uint32_t)CP_CELLS, n - c0);
+    for (uint32_t i = threadIdx.x; i <= cnt; i += blockDim.x)
+        off[i] = new_offsets[c0 + i];
+    for (uint32_t i = threadIdx.x; i < cnt; i += blockDim.x)
+        src[i] = offsets[perm[c0 + i]];
+    __syncthreads();
+    uint32_t e0 = off[0], e1 = off[cnt];
+    for (uint32_t e = e0 + threadIdx.x; e < e1; e += blockDim.x) {
+        uint32_t lo = 0, hi = cnt;
+        while (hi - lo > 1) {
+            uint32_t mid = (lo + hi) >> 1;
+            if (off[mid] <= e)
+                lo = mid;
+            else
+                hi = mid;
+        }
+        adjacency_out[e] = inv_perm[adjacency[src[lo] + (e - off[lo])]];
+    }
+}
+
+__global__ void zero_u32_from_kernel(const uint32_t *__restrict__ start_at, uint32_t end, uint32_t *__restrict__ a)
+{
+    uint32_t s = *start_at;
+    for (uint32_t e = s + blockIdx.x * blockDim.x + threadIdx.x; e < end; e += gridDim.x * blockDim.x)
+        a[e] = 0;
+}
+
+// dst row i = src row perm[i]; rows of `row_bytes` bytes
+__global__ void permute_rows_kernel(const uint8_t *__restrict__ src, uint32_t rows, uint32_t row_bytes,
+                                    const uint32_t *__restrict__ perm, uint8_t *__restrict__ dst, int vec)
+{
+    size_t total_units = (size_t)rows * (row_bytes / vec);
+    size_t units_per_row = row_bytes / vec;
+    for (size_t u = (size_t)blockIdx.x * blockDim.x + threadIdx.x; u < total_units;
+         u += (size_t)gridDim.x * blockDim.x) {
+        size_t r = u / units_per_row, k = u % units_per_row;
+        size_t so = (size_t)perm[r] * row_bytes + k * vec, dofs = r * row_bytes + k * vec;
+        if (vec == 16)
+            *reinterpret_cast<uint4 *>(dst + dofs) = *reinterpret_cast<const uint4 *>(src + so);
+        else if (vec == 4)
+            *reinterpret_cast<uint32_t *>(dst + dofs) = *reinterpret_cast<const uint32_t *>(src + so);
+        else
+            dst[dofs] = src[so];
+    }
+}
+
+// perm[rank] = pixel, rank = position of the pixel's key
+// ((y/TH)*ceil(W/TW) + x/TW)*TH*TW + (y%TH)*TW + x%TW among all keys
+// (vorotracing.py:618-623); partial edge tiles are compacted as argsort does.
+__global__ void tile_perm_kernel(uint32_t H, uint32_t W, uint32_t TH, uint32_t TW, int32_t *__restrict__ perm)
+{
+    uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= H * W)
+        return;
+    uint32_t y = p / W, x = p % W;
+    uint32_t ty = y / TH, tx = x / TW;
+    uint32_t h = min(TH, H - ty * TH), w = min(TW, W - tx * TW);
+    uint32_t rank = ty * TH * W + h * tx * TW + (y % TH) * w + (x % TW);
+    perm[rank] = (int32_t)p;
+}
+
+// --- q8 quantisation ---------------------------------------------------------
+
+// ws[0..2] min, ws[3..5] max (ordered ints), per channel or all in channel 0
+__global__ __launch_bounds__(256) void minmax_kernel(const float *__restrict__ x, size_t n, int per_channel,
+                                                     int32_t *ws)
+{
+    int32_t lo[3] = {0x7fffffff, 0x7fffffff, 0x7fffffff};
+    int32_t hi[3] = {(int32_t)0x80000000, (int32_t)0x80000000, (int32_t)0x80000000};
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        int c = per_channel ? (int)(i % 3) : 0;
+        int32_t o = f2ord(x[i]);
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            if (k == c) {
+                lo[k] = min(lo[k], o);
+                hi[k] = max(hi[k], o);
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            lo[k] = min(lo[k], __shfl_xor(lo[k], o, 64));
+            hi[k] = max(hi[k], __shfl_xor(hi[k], o, 64));
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            atomicMin(ws + k, lo[k]);
+            atomicMax(ws + 3 + k, hi[k]);
+        }
+    }
+}
+
+__global__ void minmax_init_kernel(int32_t *ws)
+{
+    if (threadIdx.x < 3)
+        ws[threadIdx.x] = 0x7fffffff;
+    else if (threadIdx.x < 6)
+        ws[threadIdx.x] = (int32_t)0x80000000;
+}
+
+// scale = fp32((double(vmax) - double(vmin)) / 255), offset = vmin
+// (vorotracing.py:498-501); params = {scale[3], offset[3], inv_scale[3]}
+__global__ void q8_params_kernel(const int32_t *ws, int per_channel, float *params)
+{
+    int c = threadIdx.x;
+    if (c >= 3)
+        return;
+    int k = per_channel ? c : 0;
+    float vmin = ord2f(ws[k]), vmax = ord2f(ws[3 + k]);
+    float scale = (float)(((double)vmax - (double)vmin) / 255.0);
+    params[c] = scale;
+    params[3 + c] = vmin;
+    params[6 + c] = 1.0f / scale;
+}
+
+// q = clamp(rint((x - offset) * fp32(1/scale)), 0, 255): torch's CUDA
+// true-division by a CPU scalar multiplies by the fp32 reciprocal
+__global__ void q8_apply_kernel(const float *__restrict__ x, size_t n, int per_channel,
+                                const float *__restrict__ params, uint8_t *__restrict__ q)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        int c = per_channel ? (int)(i % 3) : 0;
+        float scale = params[c];
+        float v = 0.0f;
+        if (scale != 0.0f) {
+            v = __builtin_rintf((x[i] - params[3 + c]) * params[6 + c]);
+            v = __builtin_fminf(__builtin_fmaxf(v, 0.0f), 255.0f);
+        }
+        q[i] = (uint8_t)v;
+    }
+}
+
+// (rows, 3*RR) f32 -> (rows, 4*RR) f16 with zero 4th channel (RNE cast)
+__global__ void pad34_kernel(const float *__restrict__ x, size_t texels, uint2 *__restrict__ out)
+{
+    for (size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x; t < texels; t += (size_t)gridDim.x * blockDim.x) {
+        const float *s = x + 3 * t;
+        uint2 w;
+        w.x = (uint32_t)f2h(s[0]) | ((uint32_t)f2h(s[1]) << 16);
+        w.y = (uint32_t)f2h(s[2]);
+        out[t] = w;
+    }
+}
+
+static uint32_t grid_for(size_t n, uint32_t block = 256, uint32_t cap = 8192)
+{
+    size_t g = (n + block - 1) / block;
+    return (uint32_t)(g < 1 ? 1 : (g > cap ? cap : g));
+}
+
+} // namespace vt
+
+using namespace vt;
+
+// words: keys n, vals n, inv n, counts n+1, sort ws, scan ws (n+1), bbox 6+6
+static size_t morton_ws_words(uint32_t n)
+{
+    return 4 * (size_t)n + 1 + radix_sort_workspace_words(n) + scan_workspace_words(n + 1) + 16;
+}
+
+extern "C" size_t vt_morton_workspace_size(uint32_t num_points, uint32_t adjacency_size)
+{
+    (void)adjacency_size;
+    return morton_ws_words(num_points) * 4;
+}
+
+extern "C" int vt_morton_reorder(const float *points, uint32_t num_points, const uint32_t *adjacency,
+                                 uint32_t adjacency_size, const uint32_t *offsets, uint32_t *perm,
+                                 float *points_out, uint32_t *adjacency_out, uint32_t *offsets_out,
+                                 void *workspace, vt_stream_t stream)
+{
+    clear_error();
+    VT_REQUIRE(points && adjacency && offsets && perm && points_out && adjacency_out && offsets_out && workspace,
+               "null pointer argument");
+    const uint32_t adj_out_size = adjacency_size;
+    hipStream_t s = as_stream(stream);
+    uint32_t n = num_points;
+    if (n == 0) {
+        zero_u32_from_kernel<<<1, 64, 0, s>>>(offsets, adj_out_size, adjacency_out);
+        VT_LAUNCH_CHECK("zero_u32_from_kernel");
+        VT_HIP_CHECK(hipMemcpyAsync(offsets_out, offsets, 4, hipMemcpyDeviceToDevice, s));
+        return VT_OK;
+    }
+    uint32_t *w = (uint32_t *)workspace;
+    uint32_t *keys = w;
+    uint32_t *vals = keys + n;
+    uint32_t *inv = vals + n;
+    uint32_t *counts = inv + n;
+    uint32_t *sws = counts + n + 1;
+    uint32_t *scan_ws = sws + radix_sort_workspace_words(n);
+    uint32_t *bbw = scan_ws + scan_workspace_words(n + 1);
+    float *bb = (float *)(bbw + 8);
+    int rc = bbox3(points, n, bb, bbw, s);
+    if (rc)
+        return rc;
+    morton_keys_kernel<<<(n + 255) / 256, 256, 0, s>>>(points, n, bb, keys, vals);
+    VT_LAUNCH_CHECK("morton_keys_kernel");
+    rc = radix_sort_pairs(keys, vals, n, 30, sws, s);
+    if (rc)
+        return rc;
+    VT_HIP_CHECK(hipMemcpyAsync(perm, vals, (size_t)n * 4, hipMemcpyDeviceToDevice, s));
+    morton_gather_kernel<<<(n + 1 + 255) / 256, 256, 0, s>>>(perm, n, points, offsets, points_out, inv, counts);
+    VT_LAUNCH_CHECK("morton_gather_kernel");
+    rc = exclusive_scan_u32(counts, offsets_out, n + 1, scan_ws, s);
+    if (rc)
+        return rc;
+    morton_copy_lists_kernel<<<(n + CP_CELLS - 1) / CP_CELLS, CP_CELLS, 0, s>>>(perm, inv, n, offsets, adjacency,
+                                                                               offsets_out, adjacency_out);
+    VT_LAUNCH_CHECK("morton_copy_lists_kernel");
+    zero_u32_from_kernel<<<4, 256, 0, s>>>(offsets_out + n, adj_out_size, adjacency_out);
+    VT_LAUNCH_CHECK("zero_u32_from_kernel");
+    return VT_OK;
+}
+
+extern "C" int vt_permute_rows(const void *src, uint32_t rows, uint32_t row_bytes, const uint32_t *perm, void *dst,
+                               vt_stream_t stream)
+{
+    clear_error();
+    if (rows == 0 || row_bytes == 0)
+        return VT_OK;
+    VT_REQUIRE(src && perm && dst && src != dst, "null or aliased pointer argument");
+    int vec = (row_bytes % 16 == 0 && ((uintptr_t)src % 16 == 0) && ((uintptr_t)dst % 16 == 0)) ? 16
+              : (row_bytes % 4 == 0 && ((uintptr_t)src % 4 == 0) && ((uintptr_t)dst % 4 == 0)) ? 4
+                                                                                                 : 1;
+    size_t units = (size_t)rows * (row_bytes / vec);
+    permute_rows_kernel<<<grid_for(units), 256, 0, as_stream(stream)>>>((const uint8_t *)src, rows, row_bytes, perm,
+                                                                        (uint8_t *)dst, vec);
+    VT_LAUNCH_CHECK("permute_rows_kernel");
+    return VT_OK;
+}
+
+extern "C" int vt_tile_perm(uint32_t height, uint32_t width, uint32_t tile_h, uint32_t tile_w, int32_t *perm,
+                            vt_stream_t stream)
+{
+    clear_error();
+    VT_REQUIRE(tile_h > 0 && tile_w > 0, "tile sizes must be positive");
+    VT_REQUIRE((uint64_t)height * width < (1ull << 31), "image too large");
+    if (height == 0 || width == 0)
+        return VT_OK;
+    VT_REQUIRE(perm, "null pointer argument");
+    uint32_t n = height * width;
+    tile_perm_kernel<<<(n + 255) / 256, 256, 0, as_stream(stream)>>>(height, width, tile_h, tile_w, perm);
+    VT_LAUNCH_CHECK("tile_perm_kernel");
+    return VT_OK;
+}
+
+extern "C" size_t vt_quantize_workspace_size(void) { return 64; }
+
+// x f32 (rows, cols) with cols % 3 == 0 when per_channel; params out (device,
+// 9 floats: scale[3], offset[3], 1/scale[3]); ws: vt_quantize_workspace_size bytes
+extern "C" int vt_quantize_u8(const float *x, uint32_t rows, uint32_t cols, int per_channel, uint8_t *q,
+                              float *params, void *workspace, vt_stream_t stream)
+{
+    clear_error();
+    VT_REQUIRE(x && q && params && workspace, "null pointer argument");
+    VT_REQUIRE(!per_channel || cols % 3 == 0, "per-channel quantisation needs RGB-interleaved columns");
+    hipStream_t s = as_stream(stream);
+    size_t n = (size_t)rows * cols;
+    int32_t *ws = (int32_t *)workspace;
+    minmax_init_kernel<<<1, 64, 0, s>>>(ws);
+    VT_LAUNCH_CHECK("minmax_init_kernel");
+    if (n > 0) {
+        minmax_kernel<<<grid_for(n, 256, 2048), 256, 0, s>>>(x, n, per_channel, ws);
+        VT_LAUNCH_CHECK("minmax_kernel");
+    }
+    q8_params_kernel<<<1, 64, 0, s>>>(ws, per_channel, params);
+    VT_LAUNCH_CHECK("q8_params_kernel");
+    if (n > 0) {
+        q8_apply_kernel<<<grid_for(n), 256, 0, s>>>(x, n, per_channel, params, q);
+        VT_LAUNCH_CHECK("q8_apply_kernel");
+    }
+    return VT_OK;
+}
+
+extern "C" int vt_pad_3to4_f16(const float *x, uint32_t rows, uint32_t texels_per_row, uint16_t *out,
+                               vt_stream_t stream)
+{
+    clear_error();
+    VT_REQUIRE(x && out, "null pointer argument");
+    size_t t = (size_t)rows * texels_per_row;
+    if (t == 0)
+        return VT_OK;
+    pad34_kernel<<<grid_for(t), 256, 0, as_stream(stream)>>>(x, t, reinterpret_cast<uint2 *>(out));
+    VT_LAUNCH_CHECK("pad34_kernel");
+    return VT_OK;
+}

@@ -66,17 +66,6 @@ __device__ __forceinline__ uint32_t walk(f3 o, f3 d, const float *__restrict__ p
     return n;
 }
 
-// Blocks are dispatched round-robin over the 8 XCDs of an MI355X, each with
-// its own L2.  Remap so that each XCD runs one contiguous range of logical
-// blocks (neighbouring rays -> neighbouring cells -> same L2).
-__device__ __forceinline__ uint32_t xcd_block()
-{
-    uint32_t G = gridDim.x, b = blockIdx.x;
-    uint32_t xcd = b & 7u, local = b >> 3;
-    uint32_t q = G >> 3, r = G & 7u;
-    return xcd < r ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
-}
-
 // Lane -> ray for a tiled image batch: one wave (64 lanes) per tile_w x
 // tile_h screen tile.  Returns NONE for lanes past the image edge.
 __device__ __forceinline__ uint32_t tiled_ray(uint32_t lane_global, uint32_t num_images, uint32_t H, uint32_t W,

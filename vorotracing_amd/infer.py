@@ -1,0 +1,238 @@
+"""Inference-side caller of the path: ``VoroTracingInfer``
+(vorotracing.py:439-683) with its preparation done by HIP kernels.
+
+Construction: density activation, fp16 Half4Texel padding
+(vt_pad_3to4_f16) or q8 quantisation (vt_quantize_u8), Morton reorder of the
+cells with CSR rebuild (vt_morton_reorder + vt_permute_rows), LBVH rebuild,
+and the per-face offset prefetch.  ``render`` picks start cells and launches
+the traversal; full images are rendered with in-kernel 8x8 wave tiling
+instead of the reference's 4x8 permutation buffer (the lane assignment never
+changes per-ray results).
+"""
+from __future__ import annotations
+
+from typing import Literal, Optional
+
+import torch
+
+from . import _C, _lib, native, ops
+
+
+class VoroTracingInfer:
+    """Lightweight inference wrapper (vorotracing.py:439-493).  ``model`` is a
+    ``vorotracing_amd.model.VoroTracing`` (or any object with its attributes)."""
+
+    TILE = (8, 8)
+
+    def __init__(self, model, sort_morton: bool = True, quantize: Literal["fp16", "q8"] = "fp16",
+                 per_channel_q8: bool = False):
+        self.primal_points = model.primal_points.detach().contiguous()
+        self.density = (model.config.activation_scale * torch.exp(model.density)).detach().contiguous()
+        self.point_adjacency = model.point_adjacency.clone()
+        self.point_adjacency_offsets = model.point_adjacency_offsets
+        self.bvh = model.bvh
+        self.device = self.primal_points.device
+        self.quantize = quantize
+        self.diff_res = model.config.oct_map_res
+        self.spec_res = model.config.spec_oct_map_res
+        self.diffuse_q8 = self.specular_q8 = None
+        self.diffuse_fp16 = self.specular_fp16 = None
+        if quantize == "q8":
+            self.diffuse_q8, self.diff_scale, self.diff_offset = self._quantize_to_uint8(
+                model.att_diffuse.detach(), per_channel_q8)
+            self.specular_q8, self.spec_scale, self.spec_offset = self._quantize_to_uint8(
+                model.att_specular.detach(), per_channel_q8)
+        elif quantize == "fp16":
+            self.diffuse_fp16 = self._pad_3to4(model.att_diffuse.detach(), self.diff_res)
+            self.specular_fp16 = self._pad_3to4(model.att_specular.detach(), self.spec_res)
+        else:
+            raise ValueError(f"Invalid quantization method: {quantize}")
+        if sort_morton:
+            self._reorder_by_morton()
+        self.adjacent_diff = ops.prefetch_octmap_adj(self.primal_points, self.point_adjacency,
+                                                     self.point_adjacency_offsets)
+
+    # -- preparation (HIP) ----------------------------------------------------
+
+    def _stream(self):
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def _quantize_to_uint8(self, tensor, per_channel=False):
+        """vorotracing.py:495-503 -> (q u8, scale, offset); per-channel returns 3-lists."""
+        x = tensor.float().contiguous()
+        q = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+        params = torch.empty(9, dtype=torch.float32, device=x.device)
+        ws = torch.empty(_lib.load().vt_quantize_workspace_size(), dtype=torch.uint8, device=x.device)
+        rows, cols = x.shape[0], x.numel() // max(x.shape[0], 1)
+        with torch.cuda.device(x.device):
+            _lib.call("vt_quantize_u8", x.data_ptr(), rows, cols, 1 if per_channel else 0, q.data_ptr(),
+                      params.data_ptr(), ws.data_ptr(), self._stream())
+        p = params.cpu().tolist()
+        if per_channel:
+            return q, p[0:3], p[3:6]
+        return q, p[0], p[3]
+
+    def _pad_3to4(self, tensor, R):
+        """vorotracing.py:505-512 on the .half() map (vorotracing.py:477-482)."""
+        x = tensor.float().contiguous()
+        n = x.shape[0]
+        out = torch.empty((n, 4 * R * R), dtype=torch.float16, device=x.device)
+        with torch.cuda.device(x.device):
+            _lib.call("vt_pad_3to4_f16", x.data_ptr(), n, R * R, out.data_ptr(), self._stream())
+        return out
+
+    def _permute(self, t: torch.Tensor, perm: torch.Tensor) -> torch.Tensor:
+        t = t.contiguous()
+        out = torch.empty_like(t)
+        row_bytes = t[0].numel() * t.element_size() if t.shape[0] else 0
+        _lib.call("vt_permute_rows", t.data_ptr(), t.shape[0], row_bytes, perm.data_ptr(), out.data_ptr(),
+                  self._stream())
+        return out
+
+    def _reorder_by_morton(self):
+        """vorotracing.py:514-571 on the GPU; ties in the key keep their index order."""
+        pts = self.primal_points
+        n = pts.shape[0]
+        adj = self.point_adjacency.contiguous()
+        off = self.point_adjacency_offsets.contiguous()
+        lib = _lib.load()
+        ws = torch.empty(lib.vt_morton_workspace_size(n, adj.numel()), dtype=torch.uint8, device=self.device)
+        perm = torch.empty(n, dtype=torch.uint32, device=self.device)
+        pts_out = torch.empty_like(pts)
+        adj_out = torch.empty_like(adj)
+        off_out = torch.empty_like(off)
+        with torch.cuda.device(self.device):
+            _lib.call("vt_morton_reorder", pts.data_ptr(), n, adj.data_ptr(), adj.numel(), off.data_ptr(),
+                      perm.data_ptr(), pts_out.data_ptr(), adj_out.data_ptr(), off_out.data_ptr(), ws.data_ptr(),
+                      self._stream())
+            self.density = self._permute(self.density, perm)
+            if self.quantize == "q8":
+                self.diffuse_q8 = self._permute(self.diffuse_q8, perm)
+                self.specular_q8 = self._permute(self.specular_q8, perm)
+            else:
+                self.diffuse_fp16 = self._permute(self.diffuse_fp16, perm)
+                self.specular_fp16 = self._permute(self.specular_fp16, perm)
+        self.morton_perm = perm
+        self.primal_points = pts_out
+        self.point_adjacency = adj_out
+        self.point_adjacency_offsets = off_out
+        # The reference rebuilds the model's shared BVH here (vorotracing.py:459,
+        # :571), which leaves the model's own start-cell queries running on a tree
+        # of the reordered sites; the reordered scene gets its own LBVH instead.
+        self.bvh = ops.NNBVH()
+        self.bvh.build(self.primal_points)
+
+    @classmethod
+    def from_pretrained(cls, pt_path, config, device=torch.device("cuda"), quantize="fp16",
+                        sort_morton: bool = True):
+        from .model import VoroTracing
+
+        return cls(VoroTracing.from_pretrained(pt_path, config, device=device), quantize=quantize,
+                   sort_morton=sort_morton)
+
+    # -- per frame ------------------------------------------------------------
+
+    def get_starting_point(self, rays):
+        """vorotracing.py:585-604: one LBVH query on the first ray's origin,
+        broadcast.  For an image batch (B, H, W, 6) each image gets its own
+        query (the reference's single-origin shortcut would be wrong there)."""
+        with torch.no_grad():
+            if rays.ndim == 1:
+                rays = rays[None, :]
+            lead = rays.shape[:-1]
+            if rays.ndim == 4:
+                origins = rays[:, 0, 0, :3].contiguous()
+                nn = self.bvh.query(self.primal_points, origins)
+                return nn.view(-1, 1, 1).expand(lead).contiguous().view(torch.uint32)
+            origin = rays.reshape(-1, rays.shape[-1])[:1, :3]
+            nn = self.bvh.query(self.primal_points, origin)
+            n = 1
+            for s in lead:
+                n *= s
+            return nn.expand(n).reshape(lead).contiguous().view(torch.uint32)
+
+    @torch.no_grad()
+    def _tile_perm(self, H, W, TH=8, TW=8):
+        """vorotracing.py:606-625 (int32, cached), from vt_tile_perm."""
+        cache = getattr(self, "_tile_perm_cache", None)
+        if cache is None:
+            cache = self._tile_perm_cache = {}
+        key = (int(H), int(W), TH, TW)
+        if key not in cache:
+            perm = torch.empty(H * W, dtype=torch.int32, device=self.device)
+            _lib.call("vt_tile_perm", H, W, TH, TW, perm.data_ptr(), self._stream())
+            cache[key] = perm
+        return cache[key]
+
+    def render(self, rays, start_point=None, weight_threshold=0.001, max_intersections=1024,
+               cell_skip_threshold=0.0, use_warp_perm: bool = True, stats: Optional[torch.Tensor] = None):
+        """vorotracing.py:627-683.  Returns f16 [..., 4]."""
+        if start_point is None:
+            start_point = self.get_starting_point(rays)
+        else:
+            start_point = torch.broadcast_to(start_point, rays.shape[:-1]).contiguous()
+        image = use_warp_perm and rays.ndim in (3, 4) and rays.shape[-1] == 6
+        if self.quantize == "q8":
+            if not image and stats is None:
+                return ops.trace_octmap_infer_q8(
+                    self.primal_points, self.diffuse_q8, self.specular_q8, self.density, self.point_adjacency,
+                    self.point_adjacency_offsets, rays, start_point, self.adjacent_diff, self.diff_scale,
+                    self.diff_offset, self.spec_scale, self.spec_offset, weight_threshold, max_intersections,
+                    cell_skip_threshold)
+            return self._render_q8_native(rays, start_point, weight_threshold, max_intersections,
+                                          cell_skip_threshold, image, stats)
+        if not image and stats is None:
+            empty = torch.empty(0, dtype=torch.int32, device=self.device)
+            return ops.trace_octmap_infer(self.primal_points, self.diffuse_fp16, self.specular_fp16, self.density,
+                                          self.point_adjacency, self.point_adjacency_offsets, rays, start_point,
+                                          self.adjacent_diff, empty, weight_threshold, max_intersections,
+                                          cell_skip_threshold)
+        rays = rays.contiguous()
+        _check_render_args(self, rays, start_point, self.diffuse_fp16)
+        return native.infer_f16(self.primal_points, self.diffuse_fp16, self.specular_fp16, self.density.reshape(-1),
+                                self.point_adjacency, self.point_adjacency_offsets, self.adjacent_diff, rays,
+                                start_point, weight_threshold=weight_threshold, max_intersections=max_intersections,
+                                cell_skip_threshold=cell_skip_threshold, stats=stats,
+                                tiled=self.TILE if image else None)
+
+    def _render_q8_native(self, rays, start_point, thr, max_int, skip, image, stats):
+        import ctypes as C
+
+        rays = rays.contiguous()
+        _check_render_args(self, rays, start_point, self.diffuse_q8)
+
+        def v3(x):
+            vals = [float(x)] * 3 if isinstance(x, (int, float)) else [float(v) for v in x]
+            return C.cast((C.c_float * 3)(*vals), C.c_void_p)
+
+        keep = [v3(self.diff_scale), v3(self.diff_offset), v3(self.spec_scale), v3(self.spec_offset)]
+        out = torch.empty(list(rays.shape[:-1]) + [4], dtype=torch.float16, device=rays.device)
+        rd = native.map_res(self.diffuse_q8.shape[-1], 3)
+        rs = native.map_res(self.specular_q8.shape[-1], 3)
+        sp = native._s(rays.device)
+        if image:
+            shp = rays.shape[:-1]
+            B, H, W = (1, shp[0], shp[1]) if len(shp) == 2 else (shp[0], shp[1], shp[2])
+            _lib.call("vt_trace_infer_q8_tiled", self.primal_points.data_ptr(), self.diffuse_q8.data_ptr(),
+                      self.specular_q8.data_ptr(), rd, rs, *keep, self.density.data_ptr(),
+                      self.point_adjacency.data_ptr(), self.point_adjacency_offsets.data_ptr(),
+                      self.primal_points.shape[0], self.adjacent_diff.data_ptr(), rays.data_ptr(), B, H, W,
+                      self.TILE[0], self.TILE[1], start_point.data_ptr(), float(thr), int(max_int), float(skip),
+                      out.data_ptr(), native._p(stats), sp)
+        else:
+            _lib.call("vt_trace_infer_q8", self.primal_points.data_ptr(), self.diffuse_q8.data_ptr(),
+                      self.specular_q8.data_ptr(), rd, rs, *keep, self.density.data_ptr(),
+                      self.point_adjacency.data_ptr(), self.point_adjacency_offsets.data_ptr(),
+                      self.primal_points.shape[0], self.adjacent_diff.data_ptr(), rays.data_ptr(),
+                      rays.numel() // 6, start_point.data_ptr(), None, float(thr), int(max_int), float(skip),
+                      out.data_ptr(), native._p(stats), sp)
+        return out
+
+
+def _check_render_args(inf, rays, start_point, diffuse):
+    """Shape/dtype checks of the native render paths (same rules as _C)."""
+    _C.validate_scene_data(inf.primal_points, diffuse, inf.point_adjacency, inf.point_adjacency_offsets)
+    if rays.dtype != torch.float32 or rays.shape[-1] != 6:
+        raise RuntimeError("rays must have float32 dtype and 6 as the last dimension")
+    if start_point.dtype != torch.uint32 or start_point.numel() != rays.numel() // 6:
+        raise RuntimeError("start_point must have uint32 dtype and the same batch size as rays")
