@@ -72,6 +72,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--train", action="store_true", help="also time the config-2 fwd+bwd training step")
     ap.add_argument("--profile", action="store_true", help="short run for rocprofv3 (no CPU leg, no stats)")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="only run 8 device copies of 1 GiB (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is design-only (see DESIGN.md)",
@@ -88,6 +90,14 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     _lib.load()
     dev = torch.device("cuda:0")
+    if args.copy_calib:
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB
+        dst = torch.empty_like(src)
+        for _ in range(8):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calib_bytes_per_dispatch": src.numel() * 4, "dispatches": 8}))
+        return
 
     t0 = time.time()
     log(f"building scene C3 ({args.sites} sites, qhull)")

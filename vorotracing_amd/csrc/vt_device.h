@@ -195,7 +195,7 @@ __device__ __forceinline__ f3 probe_dir(f3 o, f3 d, float t0, f3 site)
 // ---------------------------------------------------------------------------
 // loads
 
-__device__ __forceinline__ f3 load_site(const float *__restrict__ p, uint32_t i)
+__device__ __forceinline__ f3 load_site(const float *p, uint32_t i)
 {
     const float *q = p + 3 * (size_t)i;
     return mk(q[0], q[1], q[2]);
@@ -203,7 +203,7 @@ __device__ __forceinline__ f3 load_site(const float *__restrict__ p, uint32_t i)
 
 // Ray (camera.h:5-8) with the kernel's re-normalisation d /= |d|
 // (tracing_octmap.cu:180, :577)
-__device__ __forceinline__ void load_ray(const float *__restrict__ rays, uint32_t r, f3 &o, f3 &d)
+__device__ __forceinline__ void load_ray(const float *rays, uint32_t r, f3 &o, f3 &d)
 {
     const float *q = rays + 6 * (size_t)r;
     o = mk(q[0], q[1], q[2]);
@@ -213,7 +213,7 @@ __device__ __forceinline__ void load_ray(const float *__restrict__ rays, uint32_
 }
 
 // face record (half4 offset) -> f32 offset
-__device__ __forceinline__ f3 load_face(const uint2 *__restrict__ adj_diff, uint32_t e)
+__device__ __forceinline__ f3 load_face(const uint2 *adj_diff, uint32_t e)
 {
     uint2 w = adj_diff[e];
     return mk(h2f((uint16_t)(w.x & 0xffffu)), h2f((uint16_t)(w.x >> 16)), h2f((uint16_t)(w.y & 0xffffu)));

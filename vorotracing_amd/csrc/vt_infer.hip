@@ -12,8 +12,8 @@ namespace vt {
 
 // fp16 Half4Texel maps: texel = 8 bytes (r, g, b, pad) halves
 template <int RD, int RS> struct TexF16 {
-    const uint2 *__restrict__ diffuse;
-    const uint2 *__restrict__ specular;
+    const uint2 *diffuse;
+    const uint2 *specular;
 
     __device__ __forceinline__ f3 sample_diffuse(uint32_t cell, const Bilinear &b) const
     {
@@ -23,7 +23,7 @@ template <int RD, int RS> struct TexF16 {
     {
         return sample(specular + (size_t)cell * (RS * RS), b);
     }
-    __device__ __forceinline__ static f3 sample(const uint2 *__restrict__ m, const Bilinear &b)
+    __device__ __forceinline__ static f3 sample(const uint2 *m, const Bilinear &b)
     {
         uint2 a = m[b.i00], c = m[b.i10], e = m[b.i01], g = m[b.i11];
         float r = bil_mix(b, h2f(a.x & 0xffffu), h2f(c.x & 0xffffu), h2f(e.x & 0xffffu), h2f(g.x & 0xffffu));
@@ -35,8 +35,8 @@ template <int RD, int RS> struct TexF16 {
 
 // q8 maps: texel = 3 bytes, dequant = scale[c] * q + offset[c]
 template <int RD, int RS> struct TexQ8 {
-    const uint8_t *__restrict__ diffuse;
-    const uint8_t *__restrict__ specular;
+    const uint8_t *diffuse;
+    const uint8_t *specular;
     float ds[3], dof[3], ss[3], sof[3];
 
     __device__ __forceinline__ f3 sample_diffuse(uint32_t cell, const Bilinear &b) const
@@ -47,7 +47,7 @@ template <int RD, int RS> struct TexQ8 {
     {
         return sample(specular + (size_t)cell * (3 * RS * RS), b, ss, sof);
     }
-    __device__ __forceinline__ static f3 sample(const uint8_t *__restrict__ m, const Bilinear &b, const float *sc,
+    __device__ __forceinline__ static f3 sample(const uint8_t *m, const Bilinear &b, const float *sc,
                                                 const float *of)
     {
         float v[3];
@@ -67,7 +67,7 @@ template <int RD, int RS> struct TexQ8 {
 // :487-515, colour :437-460)
 template <int RD, int RS, class Tex> struct InferIntegrator {
     f3 o, d;
-    const float *__restrict__ density;
+    const float *density;
     Tex tex;
     Bilinear spec;
     float thr, skip;
@@ -124,24 +124,28 @@ struct InferArgs {
 
 enum { MAP_LINEAR = 0, MAP_TILED = 1 };
 
-template <int RD, int RS, bool Q8, bool STATS, int MAP, int CHUNK>
-__global__ __launch_bounds__(256) void infer_kernel(InferArgs a)
+// Lane s of a launch renders ray slot_to_ray(s): tiled, tile s/64 lane s%64
+// of the image batch; linear, ray s or ray_perm[s].
+__device__ __forceinline__ uint32_t slot_to_ray(const InferArgs &a, uint32_t s, int map)
 {
-    uint32_t lane_global = xcd_block() * blockDim.x + threadIdx.x;
-    uint32_t r;
-    if (MAP == MAP_TILED) {
-        r = tiled_ray(lane_global, a.num_images, a.H, a.W, a.th, a.tw);
-        if (r == NONE)
-            return;
-    } else {
-        if (lane_global >= a.num_rays)
-            return;
-        r = a.ray_perm ? a.ray_perm[lane_global] : lane_global;
-    }
+    if (map == MAP_TILED)
+        return tiled_ray(s, a.num_images, a.H, a.W, a.th, a.tw);
+    if (s >= a.num_rays)
+        return NONE;
+    return a.ray_perm ? a.ray_perm[s] : s;
+}
 
+template <int RD, int RS, bool Q8, bool STATS, int MAP, int CHUNK>
+__global__ __launch_bounds__(256) void infer_kernel(InferArgs a, uint32_t total_slots)
+{
+    uint32_t s = xcd_block() * blockDim.x + threadIdx.x;
+    if (s >= total_slots)
+        return;
+    uint32_t r = slot_to_ray(a, s, MAP);
+    if (r == NONE)
+        return;
     using Tex = typename std::conditional<Q8, TexQ8<RD, RS>, TexF16<RD, RS>>::type;
     InferIntegrator<RD, RS, Tex> integ;
-    load_ray(a.rays, r, integ.o, integ.d);
     integ.density = a.density;
     if constexpr (Q8) {
         integ.tex.diffuse = (const uint8_t *)a.diffuse;
@@ -157,14 +161,14 @@ __global__ __launch_bounds__(256) void infer_kernel(InferArgs a)
         integ.tex.diffuse = (const uint2 *)a.diffuse;
         integ.tex.specular = (const uint2 *)a.specular;
     }
+    integ.thr = a.thr;
+    integ.skip = a.skip;
+    load_ray(a.rays, r, integ.o, integ.d);
     float su, sv;
     oct_encode<RS>(mk(-integ.d.x, -integ.d.y, -integ.d.z), su, sv);
     integ.spec = bilinear_setup<RS>(su, sv);
-    integ.thr = a.thr;
-    integ.skip = a.skip;
     integ.acc = mk(0.0f, 0.0f, 0.0f);
     integ.T = 1.0f;
-
     StatsAcc<STATS> st;
     uint32_t n = walk<CHUNK>(integ.o, integ.d, a.points, a.adjacency, a.offsets, a.adj_diff, a.start_point[r],
                              a.max_steps, integ, st);
@@ -178,23 +182,23 @@ __global__ __launch_bounds__(256) void infer_kernel(InferArgs a)
 constexpr int INFER_BLOCK = 256;
 constexpr int INFER_CHUNK = 4;
 
+template <int RD, int RS, bool Q8, bool STATS, int MAP>
+static int launch_one(const InferArgs &a, hipStream_t stream, uint32_t slots)
+{
+    uint32_t blocks = (slots + INFER_BLOCK - 1) / INFER_BLOCK;
+    infer_kernel<RD, RS, Q8, STATS, MAP, INFER_CHUNK><<<blocks, INFER_BLOCK, 0, stream>>>(a, slots);
+    VT_LAUNCH_CHECK("infer_kernel");
+    return VT_OK;
+}
+
 template <int RD, int RS, bool Q8>
 static int launch_infer_rs(const InferArgs &a, bool stats, int map, hipStream_t stream, uint32_t lanes)
 {
-    dim3 grid((lanes + INFER_BLOCK - 1) / INFER_BLOCK), block(INFER_BLOCK);
-    if (map == MAP_TILED) {
-        if (stats)
-            infer_kernel<RD, RS, Q8, true, MAP_TILED, INFER_CHUNK><<<grid, block, 0, stream>>>(a);
-        else
-            infer_kernel<RD, RS, Q8, false, MAP_TILED, INFER_CHUNK><<<grid, block, 0, stream>>>(a);
-    } else {
-        if (stats)
-            infer_kernel<RD, RS, Q8, true, MAP_LINEAR, INFER_CHUNK><<<grid, block, 0, stream>>>(a);
-        else
-            infer_kernel<RD, RS, Q8, false, MAP_LINEAR, INFER_CHUNK><<<grid, block, 0, stream>>>(a);
-    }
-    VT_LAUNCH_CHECK("infer_kernel");
-    return VT_OK;
+    if (map == MAP_TILED)
+        return stats ? launch_one<RD, RS, Q8, true, MAP_TILED>(a, stream, lanes)
+                     : launch_one<RD, RS, Q8, false, MAP_TILED>(a, stream, lanes);
+    return stats ? launch_one<RD, RS, Q8, true, MAP_LINEAR>(a, stream, lanes)
+                 : launch_one<RD, RS, Q8, false, MAP_LINEAR>(a, stream, lanes);
 }
 
 template <bool Q8>

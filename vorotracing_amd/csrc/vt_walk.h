@@ -6,64 +6,131 @@
 
 namespace vt {
 
-// The cell walk.  Starting in `start` at t0 = 0, each step searches the
-// cell's face list for the nearest bisector plane with n.d > 0 (lowest face
-// index wins ties), hands the segment [t0, t1) to the integrator when
-// t1 > t0, and moves to the neighbour behind that face.  Faces are read in
-// chunks of CHUNK records; records past the list end stay inside the 32-row
-// padding and are masked, so the choice does not depend on CHUNK.  Returns the
-// reference's step count n (the breaking iteration included).
-template <int CHUNK, class Integrator, class StatsT>
-__device__ __forceinline__ uint32_t walk(f3 o, f3 d, const float *__restrict__ points,
-                                         const uint32_t *__restrict__ adjacency,
-                                         const uint32_t *__restrict__ offsets, const uint2 *__restrict__ adj_diff,
-                                         uint32_t start, uint32_t max_steps, Integrator &integ, StatsT &st)
+// Does a face (num, dp > 0) exit strictly before the current best (bnum,
+// bdp > 0), i.e. RN(num/dp) < RN(bnum/bdp) (RN(num/dp) < +inf while there is
+// no best)?  With both denominators positive, num/dp < bnum/bdp <=> num*bdp <
+// bnum*dp.  Each product is rounded once (relative error <= 2^-24), so a gap
+// larger than 2^-18 (|P| + |Q|) fixes the order of the exact quotients with a
+// margin of many ulps, hence of their rounded values, strictly.  Near-ties
+// and magnitudes outside [1e-30, 1e30] fall back to the two IEEE divisions,
+// so the choice is the reference's division-based one, bit for bit.
+__device__ __forceinline__ bool exit_before(float num, float dp, float bnum, float bdp, bool none)
 {
-    float t0 = 0.0f;
-    uint32_t n = 0;
-    uint32_t cur = start;
-    f3 p = load_site(points, cur);
-    for (;;) {
-        n++;
-        if (n > max_steps)
-            break;
-        uint32_t b = offsets[cur];
-        uint32_t e = offsets[cur + 1];
-        uint32_t nf = e - b;
-        st.visit(cur, nf);
-        float t1 = __builtin_huge_valf();
-        uint32_t best = NONE;
-        for (uint32_t i = 0; i < nf; i += CHUNK) {
-            f3 off[CHUNK];
+    if (none) {
+        if (__builtin_fabsf(num) < 1e30f && dp > 1e-8f)
+            return true;
+        return num / dp < __builtin_huge_valf();
+    }
+    float P = num * bdp;
+    float Q = bnum * dp;
+    float mag = __builtin_fabsf(P) + __builtin_fabsf(Q);
+    float gap = P - Q;
+    if (__builtin_fabsf(gap) > mag * 0x1p-18f && mag > 1e-30f && mag < 1e30f)
+        return gap < 0.0f;
+    return num / dp < bnum / bdp;
+}
+
+// State of one walk between steps: current cell and site, entry distance
+// t0, and the step count n of trace_octmap (tracing_octmap.cu:50-54).
+struct WalkState {
+    uint32_t cur;
+    f3 p;
+    float t0;
+    uint32_t n;
+};
+
+__device__ __forceinline__ void walk_begin(WalkState &w, const float *points, uint32_t start)
+{
+    w.cur = start;
+    w.p = load_site(points, start);
+    w.t0 = 0.0f;
+    w.n = 0;
+}
+
+// One iteration of the cell walk (tracing_octmap.cu:56-120): searches the
+// current cell's face list for the nearest bisector plane with n.d > 0
+// (lowest face index wins ties), hands [t0, t1) to the integrator when
+// t1 > t0, and moves to the neighbour behind that face.  Returns false when
+// the walk ends (step cap, no exit face, or the integrator stops it); w.n is
+// then the reference's return value.  Faces are read in chunks of CHUNK
+// records; records past the list end stay inside the 32-row padding and are
+// masked, so the choice does not depend on CHUNK.
+template <int CHUNK, class Integrator, class StatsT>
+__device__ __forceinline__ bool walk_step(WalkState &w, f3 o, f3 d, const float *points,
+                                          const uint32_t *adjacency,
+                                          const uint32_t *offsets, const uint2 *adj_diff,
+                                          uint32_t max_steps, Integrator &integ, StatsT &st)
+{
+    w.n++;
+    if (w.n > max_steps)
+        return false;
+    const f3 p = w.p;
+    uint32_t b = offsets[w.cur];
+    uint32_t e = offsets[w.cur + 1];
+    uint32_t nf = e - b;
+    st.visit(w.cur, nf);
+    const uint2 *fl = adj_diff + b;
+    // Exit face = lowest index j with dp_j > 0 minimising RN(num_j / dp_j),
+    // num_j = (p + off_j/2 - o) . off_j, dp_j = off_j . d.  The running
+    // minimum is kept as the pair (bnum, bdp) and candidates are ordered by
+    // cross products (face_order).
+    uint32_t best = NONE;
+    float bnum = 0.0f, bdp = 1.0f;
+    for (uint32_t i = 0; i < nf; i += CHUNK) {
+        f3 off[CHUNK];
 #pragma unroll
-            for (int j = 0; j < CHUNK; ++j)
-                off[j] = load_face(adj_diff, b + i + j);
+        for (int j = 0; j < CHUNK; ++j)
+            off[j] = load_face(fl, i + j);
 #pragma unroll
-            for (int j = 0; j < CHUNK; ++j) {
-                f3 fo = mk(p.x + off[j].x * 0.5f, p.y + off[j].y * 0.5f, p.z + off[j].z * 0.5f);
-                float dp = dot(off[j], d);
-                float t = dot(sub(fo, o), off[j]) / dp;
-                if (dp > 0.0f && t < t1 && (i + j) < nf) {
-                    t1 = t;
+        for (int j = 0; j < CHUNK; ++j) {
+            // p + off/2: off/2 is exact, so the fma rounds once like p + off*0.5
+            f3 fo = mk(fma_(off[j].x, 0.5f, p.x), fma_(off[j].y, 0.5f, p.y), fma_(off[j].z, 0.5f, p.z));
+            float dp = dot(off[j], d);
+            float num = dot(sub(fo, o), off[j]);
+            if (dp > 0.0f && (i + j) < nf) {
+                if (exit_before(num, dp, bnum, bdp, best == NONE)) {
+                    bnum = num;
+                    bdp = dp;
                     best = i + j;
                 }
             }
         }
-        if (best == NONE)
-            break;
-        st.exit();
-        uint32_t nxt = adjacency[b + best];
-        f3 np = load_site(points, nxt);
-        if (t1 > t0) {
-            st.integrate();
-            if (!integ.integrate(cur, t0, t1, p, np, st))
-                break;
-        }
-        t0 = __builtin_fmaxf(t0, t1);
-        cur = nxt;
-        p = np;
     }
-    return n;
+    if (best == NONE)
+        return false;
+    float t1 = bnum / bdp;
+    st.exit();
+    uint32_t nxt = adjacency[b + best];
+    f3 np = load_site(points, nxt);
+    // No early return inside the integrate branch: a divergent exit there made
+    // the control flow unstructured, and hipcc (packed FP32 disabled) then
+    // reused np's registers inside the shading code while np was still live,
+    // corrupting the next site of integrating lanes.  The state update below
+    // is harmless when the integrator ends the walk.
+    bool go = true;
+    if (t1 > w.t0) {
+        st.integrate();
+        go = integ.integrate(w.cur, w.t0, t1, p, np, st);
+    }
+    w.t0 = __builtin_fmaxf(w.t0, t1);
+    w.cur = nxt;
+    w.p = np;
+    return go;
+}
+
+// The whole walk of one ray (trace_octmap, tracing_octmap.cu:39-123).
+// Returns the reference's step count n (the breaking iteration included).
+template <int CHUNK, class Integrator, class StatsT>
+__device__ __forceinline__ uint32_t walk(f3 o, f3 d, const float *points,
+                                         const uint32_t *adjacency,
+                                         const uint32_t *offsets, const uint2 *adj_diff,
+                                         uint32_t start, uint32_t max_steps, Integrator &integ, StatsT &st)
+{
+    WalkState w;
+    walk_begin(w, points, start);
+    while (walk_step<CHUNK>(w, o, d, points, adjacency, offsets, adj_diff, max_steps, integ, st)) {
+    }
+    return w.n;
 }
 
 // Lane -> ray for a tiled image batch: one wave (64 lanes) per tile_w x
