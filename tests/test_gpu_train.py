@@ -112,6 +112,43 @@ def test_bwd_parity(gpu, which, f16, extras):
         assert perr is None
 
 
+def test_c5_shape_fisheye_rolling_shutter(gpu):
+    """Config-5 shape at test size: equidistant fisheye rays with a rolling
+    shutter (a different origin per image row), start cells from the LBVH for
+    every distinct origin (equal to brute force), forward bit for bit and
+    backward within tolerance against the oracle."""
+    s = H.mini_heightfield()
+    rays = camera.fisheye_rolling_rays(80, 53, eye=camera.orbit_eye(3))
+    assert len(np.unique(rays[..., :3].reshape(-1, 3), axis=0)) == rays.shape[0]  # one origin per row
+    thr = 0.001
+    model = VoroTracing.from_scene(s, device=gpu)
+    rays_d = H.to_dev(rays, gpu)
+    sp = model.get_starting_point(rays_d)
+    start = H.start_for(s, rays)
+    assert np.array_equal(sp.cpu().numpy(), start)
+    fw = core.trace_fwd(s.points, s.diffuse, s.specular, s.diff_res, s.spec_res, s.density, s.adjacency, s.offsets,
+                        rays, start, weight_threshold=thr)
+    pts, dif, spe, den, adj, off = _scene_tensors(s, gpu, False)
+    rgba, depth, depth_idx, contrib, n, dist, W, S, tf = _C.trace_vorotracing_fwd(
+        pts, dif, spe, den, adj, off, rays_d, sp, None, thr, 1024, False)
+    assert np.array_equal(n.cpu().numpy(), fw["n"])
+    assert np.array_equal(rgba.cpu().numpy().view(np.uint32), fw["rgba"].view(np.uint32))
+    assert np.array_equal(dist.cpu().numpy().view(np.uint32), fw["distortion"].view(np.uint32))
+    g = np.random.default_rng(4).normal(size=rays.shape[:-1] + (4,)).astype(np.float32)
+    want = core.trace_bwd(s.points, s.diffuse, s.specular, s.diff_res, s.spec_res, s.density, s.adjacency, s.offsets,
+                          rays, start, fw["rgba"], g, distortion=fw["distortion"], W_total=fw["W_total"],
+                          S_total=fw["S_total"], t_far=fw["t_far"], weight_threshold=thr)
+    d = lambda a: None if a is None else H.to_dev(a, gpu)  # noqa: E731
+    pg, dgd, sgd, deng, rayg, perr = _C.trace_vorotracing_bwd(
+        pts, dif, spe, den, adj, off, rays_d, sp, d(fw["rgba"]), d(g), None, None, None, None, 0.0,
+        d(fw["distortion"]), None, d(fw["W_total"]), d(fw["S_total"]), d(fw["t_far"]), thr, 1024)
+    torch.cuda.synchronize()
+    assert _rel_err(pg.cpu().numpy(), want["points_grad"]) <= GRAD_RTOL
+    assert _rel_err(deng.cpu().numpy(), want["density_grad"]) <= GRAD_RTOL
+    assert _rel_err(dgd.cpu().numpy(), want["diffuse_grad"]) <= GRAD_RTOL
+    assert _rel_err(sgd.cpu().numpy(), want["specular_grad"]) <= GRAD_RTOL
+
+
 def test_autograd_model_forward_backward(gpu):
     """VoroTracing.forward -> TraceVoroTracing -> loss.backward matches the oracle bwd."""
     s, rays, start, thr = _case("c1")

@@ -73,6 +73,61 @@ template <typename A, int RD, int RS> struct TrainTex {
 };
 
 // ---------------------------------------------------------------------------
+// Same-cell combining of gradient scatters.  Rays of one wave often integrate
+// the same cell in the same step (all rays of a camera share the start cell
+// and its neighbours), and hardware atomics to one address serialise.  Each
+// scatter therefore takes the cell of the first active lane as leader; when
+// at least AGG_MIN active lanes share it, those lanes add their values into
+// the wave's LDS slice (ds_add_f32) and the active lanes then flush the
+// slice with one global atomic per touched entry, zeroing it again.  Other
+// lanes scatter directly.  Only the order of the floating-point additions
+// changes (atomics have no defined order anyway).
+
+constexpr int TRAIN_BLOCK = 256;
+constexpr int TRAIN_WAVES = TRAIN_BLOCK / 64;
+constexpr int AGG_MIN = 4;
+
+// LDS floats per wave: diffuse + specular maps of one cell, density,
+// point_error, one point gradient
+template <int RD, int RS> constexpr int agg_floats() { return 3 * RD * RD + 3 * RS * RS + 5; }
+
+__device__ __forceinline__ void wave_lds_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+__device__ __forceinline__ uint32_t lane_rank(uint64_t m)
+{
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// Leader key of the active lanes, and whether this lane combines with it
+// (wave-uniform `comb`).
+struct AggVote {
+    uint32_t lead;
+    bool mine, comb;
+};
+
+__device__ __forceinline__ AggVote agg_vote(uint32_t key)
+{
+    AggVote v;
+    v.lead = __builtin_amdgcn_readfirstlane(key);
+    v.mine = key == v.lead;
+    v.comb = __popcll(__ballot(v.mine)) >= AGG_MIN;
+    return v;
+}
+
+// Zero this wave's slice before first use (all lanes of the wave, before any
+// lane leaves the kernel).
+__device__ __forceinline__ void agg_clear(float *agg, int n)
+{
+    for (int k = threadIdx.x & 63; k < n; k += 64)
+        agg[k] = 0.0f;
+    wave_lds_sync();
+}
+
+// ---------------------------------------------------------------------------
 // forward
 
 struct FwdArgs {
@@ -112,6 +167,26 @@ template <typename A, int RD, int RS> struct FwdIntegrator {
     uint32_t *qidx;
     f3 acc;
     float T, W, S, D, self, tfar;
+    float *agg; // this wave's LDS slot (one float)
+
+    // contribution[cell] += w, same-cell lanes of the wave combined first
+    __device__ __forceinline__ void scatter_contribution(uint32_t cell, float w)
+    {
+        AggVote v = agg_vote(cell);
+        if (v.comb) {
+            if (v.mine)
+                atomicAdd(agg, w);
+            wave_lds_sync();
+            if (lane_rank(__ballot(1)) == 0) {
+                float x = *agg;
+                *agg = 0.0f;
+                Attr<A>::add(contribution, v.lead, x);
+            }
+            wave_lds_sync();
+        }
+        if (!(v.comb && v.mine))
+            Attr<A>::add(contribution, cell, w);
+    }
 
     template <class St>
     __device__ __forceinline__ bool integrate(uint32_t cell, float t0, float t1, f3 p, f3, St &st)
@@ -139,7 +214,7 @@ template <typename A, int RD, int RS> struct FwdIntegrator {
             tfar = t1;
 
         if (contribution)
-            Attr<A>::add(contribution, cell, w);
+            scatter_contribution(cell, w);
         acc = vfma(w, rgb, acc);
 
         float nextT = T * (1.0f - alpha);
@@ -156,12 +231,16 @@ template <typename A, int RD, int RS> struct FwdIntegrator {
 };
 
 template <typename A, int RD, int RS, bool STATS>
-__global__ __launch_bounds__(256) void fwd_kernel(FwdArgs a)
+__global__ __launch_bounds__(TRAIN_BLOCK) void fwd_kernel(FwdArgs a)
 {
+    __shared__ float agg_lds[TRAIN_WAVES];
+    float *agg = agg_lds + threadIdx.x / 64;
+    agg_clear(agg, 1);
     uint32_t r = xcd_block() * blockDim.x + threadIdx.x;
     if (r >= a.num_rays)
         return;
     FwdIntegrator<A, RD, RS> it;
+    it.agg = agg;
     load_ray(a.rays, r, it.o, it.d);
     it.density = a.density;
     it.tex.diffuse = (const A *)a.diffuse;
@@ -272,6 +351,105 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
     f3 fwd_rgb, fwd_rgb_grad;
     float fwd_alpha, fwd_alpha_grad, ray_error;
     float W_run, S_run, W_total, S_total, dist_grad, D_total, D_running;
+    float *agg; // this wave's LDS slice, agg_floats<RD, RS>() floats
+
+    static constexpr int ND = 3 * RD * RD, NS = 3 * RS * RS;
+
+    // points_grad[idx] += g, same-idx lanes combined
+    __device__ __forceinline__ void scatter_point(uint32_t idx, f3 g)
+    {
+        AggVote v = agg_vote(idx);
+        if (v.comb) {
+            float *pb = agg + ND + NS + 2;
+            if (v.mine) {
+                atomicAdd(pb + 0, g.x);
+                atomicAdd(pb + 1, g.y);
+                atomicAdd(pb + 2, g.z);
+            }
+            wave_lds_sync();
+            uint32_t k = lane_rank(__ballot(1)); // >= AGG_MIN lanes are active
+            if (k < 3) {
+                float x = pb[k];
+                pb[k] = 0.0f;
+                if (x != 0.0f)
+                    atomicAdd(points_grad + 3 * (size_t)v.lead + k, x);
+            }
+            wave_lds_sync();
+        }
+        if (!(v.comb && v.mine))
+            add_vec(points_grad, idx, g);
+    }
+
+    // texture, density and point_error gradients of one integrated cell
+    __device__ __forceinline__ void scatter_cell(uint32_t cell, bool has_color, const Bilinear &db, const float *gl,
+                                                 float dL_ds, float perr)
+    {
+        AggVote v = agg_vote(cell);
+        if (v.comb) {
+            if (v.mine) {
+                if (has_color) {
+#pragma unroll
+                    for (int c = 0; c < 3; ++c) {
+                        atomicAdd(agg + db.i00 * 3 + c, db.w00 * gl[c]);
+                        atomicAdd(agg + db.i10 * 3 + c, db.w10 * gl[c]);
+                        atomicAdd(agg + db.i01 * 3 + c, db.w01 * gl[c]);
+                        atomicAdd(agg + db.i11 * 3 + c, db.w11 * gl[c]);
+                    }
+#pragma unroll
+                    for (int c = 0; c < 3; ++c) {
+                        atomicAdd(agg + ND + spec.i00 * 3 + c, spec.w00 * gl[c]);
+                        atomicAdd(agg + ND + spec.i10 * 3 + c, spec.w10 * gl[c]);
+                        atomicAdd(agg + ND + spec.i01 * 3 + c, spec.w01 * gl[c]);
+                        atomicAdd(agg + ND + spec.i11 * 3 + c, spec.w11 * gl[c]);
+                    }
+                }
+                atomicAdd(agg + ND + NS, dL_ds);
+                if (point_error)
+                    atomicAdd(agg + ND + NS + 1, perr);
+            }
+            wave_lds_sync();
+            uint64_t act = __ballot(1);
+            uint32_t nact = __popcll(act);
+            for (uint32_t k = lane_rank(act); k < (uint32_t)(ND + NS + 2); k += nact) {
+                float x = agg[k];
+                agg[k] = 0.0f;
+                if (x != 0.0f) {
+                    if (k < (uint32_t)ND)
+                        Attr<A>::add(diffuse_grad + (size_t)v.lead * ND, k, x);
+                    else if (k < (uint32_t)(ND + NS))
+                        Attr<A>::add(specular_grad + (size_t)v.lead * NS, k - ND, x);
+                    else if (k == (uint32_t)(ND + NS))
+                        atomicAdd(density_grad + v.lead, x);
+                    else
+                        Attr<A>::add(point_error, v.lead, x);
+                }
+            }
+            wave_lds_sync();
+        }
+        if (!(v.comb && v.mine)) {
+            if (has_color) {
+                A *dg = diffuse_grad + (size_t)cell * ND;
+                A *sg = specular_grad + (size_t)cell * NS;
+#pragma unroll
+                for (int c = 0; c < 3; ++c) {
+                    Attr<A>::add(dg, db.i00 * 3 + c, db.w00 * gl[c]);
+                    Attr<A>::add(dg, db.i10 * 3 + c, db.w10 * gl[c]);
+                    Attr<A>::add(dg, db.i01 * 3 + c, db.w01 * gl[c]);
+                    Attr<A>::add(dg, db.i11 * 3 + c, db.w11 * gl[c]);
+                }
+#pragma unroll
+                for (int c = 0; c < 3; ++c) {
+                    Attr<A>::add(sg, spec.i00 * 3 + c, spec.w00 * gl[c]);
+                    Attr<A>::add(sg, spec.i10 * 3 + c, spec.w10 * gl[c]);
+                    Attr<A>::add(sg, spec.i01 * 3 + c, spec.w01 * gl[c]);
+                    Attr<A>::add(sg, spec.i11 * 3 + c, spec.w11 * gl[c]);
+                }
+            }
+            atomicAdd(density_grad + cell, dL_ds);
+            if (point_error)
+                Attr<A>::add(point_error, cell, perr);
+        }
+    }
 
     template <class St>
     __device__ __forceinline__ bool integrate(uint32_t cell, float t0, float t1, f3 p, f3 np, St &st)
@@ -294,8 +472,6 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
             da_ddt = sig * (1.0f - alpha);
 
         acc = vfma(w, rgb, acc);
-        if (point_error)
-            Attr<A>::add(point_error, cell, w * ray_error);
 
         f3 dL_drgb = mk(fwd_rgb_grad.x * w, fwd_rgb_grad.y * w, fwd_rgb_grad.z * w);
         f3 rest = divs(sub(fwd_rgb, acc), T * ((1.0f - alpha) + 1e-6f));
@@ -356,7 +532,7 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
         next_grad = vfma(dL_dt1, dt1_dnext, next_grad);
 
         if (prev_idx != NONE)
-            add_vec(points_grad, prev_idx, prev_grad);
+            scatter_point(prev_idx, prev_grad);
         prev_geom = p;
         prev_idx = cell;
         prev_grad = cur_grad;
@@ -365,32 +541,16 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
 
         T = nextT;
 
+        float gl[3] = {0.0f, 0.0f, 0.0f};
         if (has_color) {
-            float gl[3];
             gl[0] = (dL_drgb.x * rgb.x) * (1.0f - rgb.x);
             gl[1] = (dL_drgb.y * rgb.y) * (1.0f - rgb.y);
             gl[2] = (dL_drgb.z * rgb.z) * (1.0f - rgb.z);
-            A *dg = diffuse_grad + (size_t)cell * (3 * RD * RD);
-            A *sg = specular_grad + (size_t)cell * (3 * RS * RS);
-#pragma unroll
-            for (int c = 0; c < 3; ++c) {
-                Attr<A>::add(dg, db.i00 * 3 + c, db.w00 * gl[c]);
-                Attr<A>::add(dg, db.i10 * 3 + c, db.w10 * gl[c]);
-                Attr<A>::add(dg, db.i01 * 3 + c, db.w01 * gl[c]);
-                Attr<A>::add(dg, db.i11 * 3 + c, db.w11 * gl[c]);
-            }
-#pragma unroll
-            for (int c = 0; c < 3; ++c) {
-                Attr<A>::add(sg, spec.i00 * 3 + c, spec.w00 * gl[c]);
-                Attr<A>::add(sg, spec.i10 * 3 + c, spec.w10 * gl[c]);
-                Attr<A>::add(sg, spec.i01 * 3 + c, spec.w01 * gl[c]);
-                Attr<A>::add(sg, spec.i11 * 3 + c, spec.w11 * gl[c]);
-            }
         }
-        atomicAdd(density_grad + cell, dL_ds);
+        scatter_cell(cell, has_color, db, gl, dL_ds, w * ray_error);
 
         if (T < thr) {
-            add_vec(points_grad, prev_idx, prev_grad);
+            scatter_point(prev_idx, prev_grad);
             return false;
         }
         return true;
@@ -398,12 +558,17 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
 };
 
 template <typename A, int RD, int RS, bool STATS>
-__global__ __launch_bounds__(256) void bwd_kernel(BwdArgs a)
+__global__ __launch_bounds__(TRAIN_BLOCK) void bwd_kernel(BwdArgs a)
 {
+    constexpr int NAGG = agg_floats<RD, RS>();
+    __shared__ float agg_lds[TRAIN_WAVES][NAGG];
+    float *agg = agg_lds[threadIdx.x / 64];
+    agg_clear(agg, NAGG);
     uint32_t r = xcd_block() * blockDim.x + threadIdx.x;
     if (r >= a.num_rays)
         return;
     BwdIntegrator<A, RD, RS> it;
+    it.agg = agg;
     load_ray(a.rays, r, it.o, it.d);
     it.density = a.density;
     it.tex.diffuse = (const A *)a.diffuse;
@@ -462,8 +627,6 @@ __global__ __launch_bounds__(256) void bwd_kernel(BwdArgs a)
 
 int prefetch(const float *points, uint32_t num_points, const uint32_t *adjacency, uint32_t adjacency_size,
              const uint32_t *offsets, uint16_t *adj_diff, hipStream_t stream);
-
-constexpr int TRAIN_BLOCK = 256;
 
 template <template <typename, int, int, bool> class K, typename Args, typename A, int RD, int RS>
 static int launch_train_rs(const Args &a, bool stats, hipStream_t s)

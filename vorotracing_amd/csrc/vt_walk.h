@@ -6,29 +6,48 @@
 
 namespace vt {
 
-// Does a face (num, dp > 0) exit strictly before the current best (bnum,
-// bdp > 0), i.e. RN(num/dp) < RN(bnum/bdp) (RN(num/dp) < +inf while there is
-// no best)?  With both denominators positive, num/dp < bnum/bdp <=> num*bdp <
-// bnum*dp.  Each product is rounded once (relative error <= 2^-24), so a gap
-// larger than 2^-18 (|P| + |Q|) fixes the order of the exact quotients with a
-// margin of many ulps, hence of their rounded values, strictly.  Near-ties
-// and magnitudes outside [1e-30, 1e30] fall back to the two IEEE divisions,
-// so the choice is the reference's division-based one, bit for bit.
-__device__ __forceinline__ bool exit_before(float num, float dp, float bnum, float bdp, bool none)
+// Exit-face order without a division per face.  For dp, bdp > 0,
+// num/dp < bnum/bdp <=> A < B with A = num*bdp, B = bnum*dp.  The search
+// forms Q = RN(B) and gap = RN(A - Q) (one fma).  When 2^18 |gap| > |Q| and
+// 1e-26 <= |Q| < inf, the exact quotients differ by more than 2^-18 of
+// |bnum/bdp| (Q and gap each carry one rounding, 2^-24 relative), which is
+// normal here because dp, bdp <= |f16 offset| < 2^17, so the rounded
+// quotients are strictly ordered like A and B: the face exits first iff
+// gap < 0.  Every other case (near-ties, zero, overflow, NaN) compares the
+// two IEEE quotients, so the choice is the reference's
+// RN(num/dp) < RN(bnum/bdp), bit for bit.  Before the first candidate the
+// best is the pair (2^64, 2^-64): its quotient 2^128 rounds to +inf, which
+// is the reference's initial t_1, and the same test then accepts a face iff
+// RN(num/dp) < inf.
+constexpr float FIRST_BNUM = 0x1p64f;
+constexpr float FIRST_BDP = 0x1p-64f;
+
+__device__ __forceinline__ bool exit_before(float num, float dp, float bnum, float bdp)
 {
-    if (none) {
-        if (__builtin_fabsf(num) < 1e30f && dp > 1e-8f)
-            return true;
-        return num / dp < __builtin_huge_valf();
-    }
-    float P = num * bdp;
     float Q = bnum * dp;
-    float mag = __builtin_fabsf(P) + __builtin_fabsf(Q);
-    float gap = P - Q;
-    if (__builtin_fabsf(gap) > mag * 0x1p-18f && mag > 1e-30f && mag < 1e30f)
+    float gap = fma_(num, bdp, -Q);
+    float aq = __builtin_fabsf(Q);
+    float h = fma_(__builtin_fabsf(gap), -0x1p18f, aq);
+    if (h < 0.0f && aq >= 1e-26f && aq < __builtin_huge_valf())
         return gap < 0.0f;
     return num / dp < bnum / bdp;
 }
+
+// -0.0f hidden from constant folding: fma(a, b, -0) == a*b exactly (also
+// for signed zeros), and keeping it an fma lets a half operand fold into
+// v_fma_mix_f32 instead of a separate conversion.
+__device__ __forceinline__ float opaque_neg_zero()
+{
+    uint32_t b;
+    asm("s_mov_b32 %0, 0x80000000" : "=s"(b));
+    return __builtin_bit_cast(float, b);
+}
+
+// f16 halves of a packed face record (x | y << 16, z | w << 16), widened
+// exactly; used directly as fma operands so the compiler can fold the
+// conversion into v_fma_mix_f32.
+__device__ __forceinline__ float half_lo(uint32_t w) { return h2f((uint16_t)(w & 0xffffu)); }
+__device__ __forceinline__ float half_hi(uint32_t w) { return h2f((uint16_t)(w >> 16)); }
 
 // State of one walk between steps: current cell and site, entry distance
 // t0, and the step count n of trace_octmap (tracing_octmap.cu:50-54).
@@ -73,22 +92,26 @@ __device__ __forceinline__ bool walk_step(WalkState &w, f3 o, f3 d, const float 
     // Exit face = lowest index j with dp_j > 0 minimising RN(num_j / dp_j),
     // num_j = (p + off_j/2 - o) . off_j, dp_j = off_j . d.  The running
     // minimum is kept as the pair (bnum, bdp) and candidates are ordered by
-    // cross products (face_order).
+    // exit_before.
     uint32_t best = NONE;
-    float bnum = 0.0f, bdp = 1.0f;
+    float bnum = FIRST_BNUM, bdp = FIRST_BDP;
+    const float nz = opaque_neg_zero();
     for (uint32_t i = 0; i < nf; i += CHUNK) {
-        f3 off[CHUNK];
+        uint2 rec[CHUNK];
 #pragma unroll
         for (int j = 0; j < CHUNK; ++j)
-            off[j] = load_face(fl, i + j);
+            rec[j] = fl[i + j];
 #pragma unroll
         for (int j = 0; j < CHUNK; ++j) {
+            float ox = half_lo(rec[j].x), oy = half_hi(rec[j].x), oz = half_lo(rec[j].y);
+            float dp = fma_(oz, d.z, fma_(oy, d.y, fma_(ox, d.x, nz)));
             // p + off/2: off/2 is exact, so the fma rounds once like p + off*0.5
-            f3 fo = mk(fma_(off[j].x, 0.5f, p.x), fma_(off[j].y, 0.5f, p.y), fma_(off[j].z, 0.5f, p.z));
-            float dp = dot(off[j], d);
-            float num = dot(sub(fo, o), off[j]);
+            float ex = fma_(ox, 0.5f, p.x) - o.x;
+            float ey = fma_(oy, 0.5f, p.y) - o.y;
+            float ez = fma_(oz, 0.5f, p.z) - o.z;
+            float num = fma_(ez, oz, fma_(ey, oy, fma_(ex, ox, nz)));
             if (dp > 0.0f && (i + j) < nf) {
-                if (exit_before(num, dp, bnum, bdp, best == NONE)) {
+                if (exit_before(num, dp, bnum, bdp)) {
                     bnum = num;
                     bdp = dp;
                     best = i + j;
