@@ -130,11 +130,16 @@ int vt_trace_infer_q8_tiled(const float *points, const uint8_t *diffuse, const u
  *   depth_idx u32 (num_rays, K) outputs when quantiles are given.
  *   contribution: NULL or zero-initialised (num_points), accumulated.
  *   num_intersections u32, distortion/W_total/S_total/t_far f32 (num_rays).
+ *   image_h, image_w: lane order only.  When both are non-zero and
+ *   image_h*image_w divides num_rays, the rays are row-major images of that
+ *   size and each wave traces one 8x8 screen tile (neighbouring rays share
+ *   cells, so same-cell gradient combining finds more partners); 0, 0 = ray
+ *   order.  Outputs do not depend on it beyond the order of atomic adds.
  */
 int vt_trace_fwd(int attr_dtype, const float *points, const void *diffuse, const void *specular, uint32_t diff_res,
                  uint32_t spec_res, const float *density, const uint32_t *adjacency, uint32_t adjacency_size,
                  const uint32_t *offsets, uint32_t num_points, const float *rays, uint32_t num_rays,
-                 const uint32_t *start_point, uint32_t num_quantiles, const float *depth_quantiles,
+                 uint32_t image_h, uint32_t image_w, const uint32_t *start_point, uint32_t num_quantiles, const float *depth_quantiles,
                  float weight_threshold, uint32_t max_intersections, void *rgba, float *depth, uint32_t *depth_idx,
                  void *contribution, uint32_t *num_intersections, float *distortion, float *W_total,
                  float *S_total, float *t_far, uint16_t *adj_diff_workspace, vt_ray_stats *stats,
@@ -151,11 +156,14 @@ int vt_trace_fwd(int attr_dtype, const float *points, const void *diffuse, const
  *   Outputs (caller zero-initialises): points_grad f32 (num_points,3),
  *   diffuse_grad / specular_grad attr dtype, density_grad f32 (num_points),
  *   point_error attr dtype (num_points) or NULL.
+ *   image_h, image_w: lane order, as for vt_trace_fwd.
+ *   Gradient scatters of lanes that integrate the same cell in the same step
+ *   are combined in LDS before the global atomics.
  */
 int vt_trace_bwd(int attr_dtype, const float *points, const void *diffuse, const void *specular, uint32_t diff_res,
                  uint32_t spec_res, const float *density, const uint32_t *adjacency, uint32_t adjacency_size,
                  const uint32_t *offsets, uint32_t num_points, const float *rays, uint32_t num_rays,
-                 const uint32_t *start_point, const void *rgba, const void *rgba_grad, uint32_t num_quantiles,
+                 uint32_t image_h, uint32_t image_w, const uint32_t *start_point, const void *rgba, const void *rgba_grad, uint32_t num_quantiles,
                  const float *depth_quantiles, const uint32_t *depth_idx, const float *depth_grad,
                  const void *ray_error, float contribution_alpha_grad, const float *distortion,
                  const float *distortion_grad, const float *W_total, const float *S_total, const float *t_far,

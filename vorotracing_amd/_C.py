@@ -221,6 +221,14 @@ def _check_train_common(points, diffuse, specular, density, rays, start_point, n
     _assert(_is_gpu(start_point), "start_point must be on CUDA device")
 
 
+def _image_dims(rays):
+    """(H, W) of image-shaped rays [..., H, W, 6] for the tiled lane order of
+    the training kernels; (0, 0) for flat ray batches."""
+    if rays.dim() >= 3 and rays.shape[-3] > 1 and rays.shape[-2] > 1:
+        return int(rays.shape[-3]), int(rays.shape[-2])
+    return 0, 0
+
+
 def _attr_code(dtype):
     if dtype == torch.float32:
         return 0
@@ -278,7 +286,7 @@ def trace_vorotracing_fwd(points_in, diffuse_in, specular_in, density_in, point_
     with torch.cuda.device(dev):
         _lib.call("vt_trace_fwd", code, points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd, rs,
                   density.data_ptr(), adjacency.data_ptr(), adjacency_size, offsets.data_ptr(), num_points,
-                  rays.data_ptr(), num_rays, start_point.data_ptr(), K, _ptr(depth_quantiles),
+                  rays.data_ptr(), num_rays, *_image_dims(rays), start_point.data_ptr(), K, _ptr(depth_quantiles),
                   float(weight_threshold), int(max_intersections), rgba.data_ptr(), _ptr(depth), _ptr(depth_idx),
                   _ptr(contribution), n.data_ptr(), distortion.data_ptr(), W_total.data_ptr(), S_total.data_ptr(),
                   t_far.data_ptr(), workspace.data_ptr(), None, _stream(dev))
@@ -374,7 +382,8 @@ def trace_vorotracing_bwd(points_in, diffuse_in, specular_in, density_in, point_
     with torch.cuda.device(dev):
         _lib.call("vt_trace_bwd", code, points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd, rs,
                   density.data_ptr(), adjacency.data_ptr(), adjacency_size, offsets.data_ptr(), num_points,
-                  rays.data_ptr(), num_rays, start_point.data_ptr(), rgb_out.data_ptr(), rgb_grad.data_ptr(), K,
+                  rays.data_ptr(), num_rays, *_image_dims(rays), start_point.data_ptr(), rgb_out.data_ptr(),
+                  rgb_grad.data_ptr(), K,
                   _ptr(depth_quantiles), _ptr(depth_indices), _ptr(depth_grad), _ptr(ray_error),
                   float(contribution_alpha_grad), distortion.data_ptr(), _ptr(distortion_grad),
                   W_total.data_ptr(), S_total.data_ptr(), t_far.data_ptr(), float(weight_threshold),

@@ -32,10 +32,10 @@ SIGNATURES = {
         [P, P, P, U32, U32, P, P, P, P, P, P, P, U32, P, P, U32, U32, U32, U32, U32, P, F32, U32, F32, P, P, P],
         C.c_int),
     "vt_trace_fwd": (
-        [I32, P, P, P, U32, U32, P, P, U32, P, U32, P, U32, P, U32, P, F32, U32, P, P, P, P, P, P, P, P, P, P, P, P],
+        [I32, P, P, P, U32, U32, P, P, U32, P, U32, P, U32, U32, U32, P, U32, P, F32, U32, P, P, P, P, P, P, P, P, P, P, P, P],
         C.c_int),
     "vt_trace_bwd": (
-        [I32, P, P, P, U32, U32, P, P, U32, P, U32, P, U32, P, P, P, U32, P, P, P, P, F32, P, P, P, P, P, F32, U32,
+        [I32, P, P, P, U32, U32, P, P, U32, P, U32, P, U32, U32, U32, P, P, P, U32, P, P, P, P, F32, P, P, P, P, P, F32, U32,
          P, P, P, P, P, P, P, P], C.c_int),
     "vt_math_probe": ([I32, P, P, U32, P], C.c_int),
     "vt_bvh_create": ([P], C.c_int),

@@ -75,10 +75,10 @@ template <typename A, int RD, int RS> struct TrainTex {
 // ---------------------------------------------------------------------------
 // Same-cell combining of gradient scatters.  Rays of one wave often integrate
 // the same cell in the same step (all rays of a camera share the start cell
-// and its neighbours), and hardware atomics to one address serialise.  Each
-// scatter therefore takes the cell of the first active lane as leader; when
-// at least AGG_MIN active lanes share it, those lanes add their values into
-// the wave's LDS slice (ds_add_f32) and the active lanes then flush the
+// and its neighbours), and hardware atomics to one address serialise.  A
+// scatter therefore groups the active lanes by cell, leader by leader (the
+// lowest pending lane); a group of at least AGG_MIN lanes adds its values
+// into the wave's LDS slice (ds_add_f32) and the active lanes then flush the
 // slice with one global atomic per touched entry, zeroing it again.  Other
 // lanes scatter directly.  Only the order of the floating-point additions
 // changes (atomics have no defined order anyway).
@@ -102,20 +102,37 @@ __device__ __forceinline__ uint32_t lane_rank(uint64_t m)
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
-// Leader key of the active lanes, and whether this lane combines with it
-// (wave-uniform `comb`).
-struct AggVote {
+constexpr int AGG_ROUNDS = 3;
+
+// One combining round over the lanes still pending: the key of the lowest
+// pending lane leads; `mine` marks its group and `comb` (wave-uniform) says
+// whether the group is large enough to combine.  Returns false when no lane
+// is pending.  Up to AGG_ROUNDS groups are combined per scatter; lanes of
+// smaller groups and lanes left over scatter directly.
+struct AggRound {
     uint32_t lead;
     bool mine, comb;
 };
 
-__device__ __forceinline__ AggVote agg_vote(uint32_t key)
+__device__ __forceinline__ bool agg_round(uint32_t key, bool pending, AggRound &g)
 {
-    AggVote v;
-    v.lead = __builtin_amdgcn_readfirstlane(key);
-    v.mine = key == v.lead;
-    v.comb = __popcll(__ballot(v.mine)) >= AGG_MIN;
-    return v;
+    uint64_t pm = __ballot(pending);
+    if (pm == 0)
+        return false;
+    g.lead = __builtin_amdgcn_readlane(key, (int)__builtin_ctzll(pm));
+    g.mine = pending && key == g.lead;
+    g.comb = __popcll(__ballot(g.mine)) >= AGG_MIN;
+    return true;
+}
+
+// Ray of lane slot s: 8x8 screen tiles of row-major images, or ray order.
+constexpr uint32_t TRAIN_TILE = 8;
+
+__device__ __forceinline__ uint32_t train_ray(uint32_t s, uint32_t num_rays, uint32_t ni, uint32_t h, uint32_t w)
+{
+    if (ni)
+        return tiled_ray(s, ni, h, w, TRAIN_TILE, TRAIN_TILE);
+    return s < num_rays ? s : NONE;
 }
 
 // Zero this wave's slice before first use (all lanes of the wave, before any
@@ -138,6 +155,7 @@ struct FwdArgs {
     const uint2 *adj_diff;
     const float *rays;
     uint32_t num_rays;
+    uint32_t num_images, img_h, img_w; // tiled lane order when num_images > 0
     const uint32_t *start_point;
     uint32_t K;
     const float *quantiles;
@@ -172,19 +190,28 @@ template <typename A, int RD, int RS> struct FwdIntegrator {
     // contribution[cell] += w, same-cell lanes of the wave combined first
     __device__ __forceinline__ void scatter_contribution(uint32_t cell, float w)
     {
-        AggVote v = agg_vote(cell);
-        if (v.comb) {
-            if (v.mine)
-                atomicAdd(agg, w);
-            wave_lds_sync();
-            if (lane_rank(__ballot(1)) == 0) {
-                float x = *agg;
-                *agg = 0.0f;
-                Attr<A>::add(contribution, v.lead, x);
+        bool pending = true, direct = false;
+        for (int round = 0; round < AGG_ROUNDS; ++round) {
+            AggRound g;
+            if (!agg_round(cell, pending, g))
+                break;
+            if (g.comb) {
+                if (g.mine)
+                    atomicAdd(agg, w);
+                wave_lds_sync();
+                if (lane_rank(__ballot(1)) == 0) {
+                    float x = *agg;
+                    *agg = 0.0f;
+                    Attr<A>::add(contribution, g.lead, x);
+                }
+                wave_lds_sync();
+            } else if (g.mine) {
+                direct = true;
             }
-            wave_lds_sync();
+            if (g.mine)
+                pending = false;
         }
-        if (!(v.comb && v.mine))
+        if (pending || direct)
             Attr<A>::add(contribution, cell, w);
     }
 
@@ -236,8 +263,8 @@ __global__ __launch_bounds__(TRAIN_BLOCK) void fwd_kernel(FwdArgs a)
     __shared__ float agg_lds[TRAIN_WAVES];
     float *agg = agg_lds + threadIdx.x / 64;
     agg_clear(agg, 1);
-    uint32_t r = xcd_block() * blockDim.x + threadIdx.x;
-    if (r >= a.num_rays)
+    uint32_t r = train_ray(xcd_block() * blockDim.x + threadIdx.x, a.num_rays, a.num_images, a.img_h, a.img_w);
+    if (r == NONE)
         return;
     FwdIntegrator<A, RD, RS> it;
     it.agg = agg;
@@ -292,6 +319,7 @@ struct BwdArgs {
     const uint2 *adj_diff;
     const float *rays;
     uint32_t num_rays;
+    uint32_t num_images, img_h, img_w; // tiled lane order when num_images > 0
     const uint32_t *start_point;
     const void *rgba, *rgba_grad;
     uint32_t K;
@@ -358,25 +386,34 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
     // points_grad[idx] += g, same-idx lanes combined
     __device__ __forceinline__ void scatter_point(uint32_t idx, f3 g)
     {
-        AggVote v = agg_vote(idx);
-        if (v.comb) {
-            float *pb = agg + ND + NS + 2;
-            if (v.mine) {
-                atomicAdd(pb + 0, g.x);
-                atomicAdd(pb + 1, g.y);
-                atomicAdd(pb + 2, g.z);
+        bool pending = true, direct = false;
+        for (int round = 0; round < AGG_ROUNDS; ++round) {
+            AggRound r;
+            if (!agg_round(idx, pending, r))
+                break;
+            if (r.comb) {
+                float *pb = agg + ND + NS + 2;
+                if (r.mine) {
+                    atomicAdd(pb + 0, g.x);
+                    atomicAdd(pb + 1, g.y);
+                    atomicAdd(pb + 2, g.z);
+                }
+                wave_lds_sync();
+                uint32_t k = lane_rank(__ballot(1)); // >= AGG_MIN lanes are active
+                if (k < 3) {
+                    float x = pb[k];
+                    pb[k] = 0.0f;
+                    if (x != 0.0f)
+                        atomicAdd(points_grad + 3 * (size_t)r.lead + k, x);
+                }
+                wave_lds_sync();
+            } else if (r.mine) {
+                direct = true;
             }
-            wave_lds_sync();
-            uint32_t k = lane_rank(__ballot(1)); // >= AGG_MIN lanes are active
-            if (k < 3) {
-                float x = pb[k];
-                pb[k] = 0.0f;
-                if (x != 0.0f)
-                    atomicAdd(points_grad + 3 * (size_t)v.lead + k, x);
-            }
-            wave_lds_sync();
+            if (r.mine)
+                pending = false;
         }
-        if (!(v.comb && v.mine))
+        if (pending || direct)
             add_vec(points_grad, idx, g);
     }
 
@@ -384,49 +421,58 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
     __device__ __forceinline__ void scatter_cell(uint32_t cell, bool has_color, const Bilinear &db, const float *gl,
                                                  float dL_ds, float perr)
     {
-        AggVote v = agg_vote(cell);
-        if (v.comb) {
-            if (v.mine) {
-                if (has_color) {
+        bool pending = true, direct = false;
+        for (int round = 0; round < AGG_ROUNDS; ++round) {
+            AggRound g;
+            if (!agg_round(cell, pending, g))
+                break;
+            if (g.comb) {
+                if (g.mine) {
+                    if (has_color) {
 #pragma unroll
-                    for (int c = 0; c < 3; ++c) {
-                        atomicAdd(agg + db.i00 * 3 + c, db.w00 * gl[c]);
-                        atomicAdd(agg + db.i10 * 3 + c, db.w10 * gl[c]);
-                        atomicAdd(agg + db.i01 * 3 + c, db.w01 * gl[c]);
-                        atomicAdd(agg + db.i11 * 3 + c, db.w11 * gl[c]);
+                        for (int c = 0; c < 3; ++c) {
+                            atomicAdd(agg + db.i00 * 3 + c, db.w00 * gl[c]);
+                            atomicAdd(agg + db.i10 * 3 + c, db.w10 * gl[c]);
+                            atomicAdd(agg + db.i01 * 3 + c, db.w01 * gl[c]);
+                            atomicAdd(agg + db.i11 * 3 + c, db.w11 * gl[c]);
+                        }
+#pragma unroll
+                        for (int c = 0; c < 3; ++c) {
+                            atomicAdd(agg + ND + spec.i00 * 3 + c, spec.w00 * gl[c]);
+                            atomicAdd(agg + ND + spec.i10 * 3 + c, spec.w10 * gl[c]);
+                            atomicAdd(agg + ND + spec.i01 * 3 + c, spec.w01 * gl[c]);
+                            atomicAdd(agg + ND + spec.i11 * 3 + c, spec.w11 * gl[c]);
+                        }
                     }
-#pragma unroll
-                    for (int c = 0; c < 3; ++c) {
-                        atomicAdd(agg + ND + spec.i00 * 3 + c, spec.w00 * gl[c]);
-                        atomicAdd(agg + ND + spec.i10 * 3 + c, spec.w10 * gl[c]);
-                        atomicAdd(agg + ND + spec.i01 * 3 + c, spec.w01 * gl[c]);
-                        atomicAdd(agg + ND + spec.i11 * 3 + c, spec.w11 * gl[c]);
+                    atomicAdd(agg + ND + NS, dL_ds);
+                    if (point_error)
+                        atomicAdd(agg + ND + NS + 1, perr);
+                }
+                wave_lds_sync();
+                uint64_t act = __ballot(1);
+                uint32_t nact = __popcll(act);
+                for (uint32_t k = lane_rank(act); k < (uint32_t)(ND + NS + 2); k += nact) {
+                    float x = agg[k];
+                    agg[k] = 0.0f;
+                    if (x != 0.0f) {
+                        if (k < (uint32_t)ND)
+                            Attr<A>::add(diffuse_grad + (size_t)g.lead * ND, k, x);
+                        else if (k < (uint32_t)(ND + NS))
+                            Attr<A>::add(specular_grad + (size_t)g.lead * NS, k - ND, x);
+                        else if (k == (uint32_t)(ND + NS))
+                            atomicAdd(density_grad + g.lead, x);
+                        else
+                            Attr<A>::add(point_error, g.lead, x);
                     }
                 }
-                atomicAdd(agg + ND + NS, dL_ds);
-                if (point_error)
-                    atomicAdd(agg + ND + NS + 1, perr);
+                wave_lds_sync();
+            } else if (g.mine) {
+                direct = true;
             }
-            wave_lds_sync();
-            uint64_t act = __ballot(1);
-            uint32_t nact = __popcll(act);
-            for (uint32_t k = lane_rank(act); k < (uint32_t)(ND + NS + 2); k += nact) {
-                float x = agg[k];
-                agg[k] = 0.0f;
-                if (x != 0.0f) {
-                    if (k < (uint32_t)ND)
-                        Attr<A>::add(diffuse_grad + (size_t)v.lead * ND, k, x);
-                    else if (k < (uint32_t)(ND + NS))
-                        Attr<A>::add(specular_grad + (size_t)v.lead * NS, k - ND, x);
-                    else if (k == (uint32_t)(ND + NS))
-                        atomicAdd(density_grad + v.lead, x);
-                    else
-                        Attr<A>::add(point_error, v.lead, x);
-                }
-            }
-            wave_lds_sync();
+            if (g.mine)
+                pending = false;
         }
-        if (!(v.comb && v.mine)) {
+        if (pending || direct) {
             if (has_color) {
                 A *dg = diffuse_grad + (size_t)cell * ND;
                 A *sg = specular_grad + (size_t)cell * NS;
@@ -564,8 +610,8 @@ __global__ __launch_bounds__(TRAIN_BLOCK) void bwd_kernel(BwdArgs a)
     __shared__ float agg_lds[TRAIN_WAVES][NAGG];
     float *agg = agg_lds[threadIdx.x / 64];
     agg_clear(agg, NAGG);
-    uint32_t r = xcd_block() * blockDim.x + threadIdx.x;
-    if (r >= a.num_rays)
+    uint32_t r = train_ray(xcd_block() * blockDim.x + threadIdx.x, a.num_rays, a.num_images, a.img_h, a.img_w);
+    if (r == NONE)
         return;
     BwdIntegrator<A, RD, RS> it;
     it.agg = agg;
@@ -628,10 +674,26 @@ __global__ __launch_bounds__(TRAIN_BLOCK) void bwd_kernel(BwdArgs a)
 int prefetch(const float *points, uint32_t num_points, const uint32_t *adjacency, uint32_t adjacency_size,
              const uint32_t *offsets, uint16_t *adj_diff, hipStream_t stream);
 
+template <typename Args> static void set_image_order(Args &a, uint32_t num_rays, uint32_t h, uint32_t w)
+{
+    a.num_images = 0;
+    a.img_h = a.img_w = 0;
+    uint64_t px = (uint64_t)h * w;
+    if (h && w && num_rays % px == 0) {
+        a.num_images = (uint32_t)(num_rays / px);
+        a.img_h = h;
+        a.img_w = w;
+    }
+}
+
 template <template <typename, int, int, bool> class K, typename Args, typename A, int RD, int RS>
 static int launch_train_rs(const Args &a, bool stats, hipStream_t s)
 {
-    dim3 grid((a.num_rays + TRAIN_BLOCK - 1) / TRAIN_BLOCK), block(TRAIN_BLOCK);
+    uint64_t slots = a.num_rays;
+    if (a.num_images)
+        slots = (uint64_t)a.num_images * ((a.img_h + TRAIN_TILE - 1) / TRAIN_TILE) *
+                ((a.img_w + TRAIN_TILE - 1) / TRAIN_TILE) * (TRAIN_TILE * TRAIN_TILE);
+    dim3 grid((uint32_t)((slots + TRAIN_BLOCK - 1) / TRAIN_BLOCK)), block(TRAIN_BLOCK);
     if (stats)
         hipLaunchKernelGGL((K<A, RD, RS, true>::fn), grid, block, 0, s, a);
     else
@@ -682,7 +744,8 @@ using namespace vt;
 extern "C" int vt_trace_fwd(int attr_dtype, const float *points, const void *diffuse, const void *specular,
                             uint32_t diff_res, uint32_t spec_res, const float *density, const uint32_t *adjacency,
                             uint32_t adjacency_size, const uint32_t *offsets, uint32_t num_points, const float *rays,
-                            uint32_t num_rays, const uint32_t *start_point, uint32_t num_quantiles,
+                            uint32_t num_rays, uint32_t image_h, uint32_t image_w,
+                            const uint32_t *start_point, uint32_t num_quantiles,
                             const float *depth_quantiles, float weight_threshold, uint32_t max_intersections,
                             void *rgba, float *depth, uint32_t *depth_idx, void *contribution,
                             uint32_t *num_intersections, float *distortion, float *W_total, float *S_total,
@@ -709,6 +772,7 @@ extern "C" int vt_trace_fwd(int attr_dtype, const float *points, const void *dif
     a.adj_diff = reinterpret_cast<const uint2 *>(adj_diff_workspace);
     a.rays = rays;
     a.num_rays = num_rays;
+    set_image_order(a, num_rays, image_h, image_w);
     a.start_point = start_point;
     a.K = depth_quantiles ? num_quantiles : 0;
     a.quantiles = (depth_quantiles && num_quantiles) ? depth_quantiles : nullptr;
@@ -730,7 +794,8 @@ extern "C" int vt_trace_fwd(int attr_dtype, const float *points, const void *dif
 extern "C" int vt_trace_bwd(int attr_dtype, const float *points, const void *diffuse, const void *specular,
                             uint32_t diff_res, uint32_t spec_res, const float *density, const uint32_t *adjacency,
                             uint32_t adjacency_size, const uint32_t *offsets, uint32_t num_points, const float *rays,
-                            uint32_t num_rays, const uint32_t *start_point, const void *rgba, const void *rgba_grad,
+                            uint32_t num_rays, uint32_t image_h, uint32_t image_w,
+                            const uint32_t *start_point, const void *rgba, const void *rgba_grad,
                             uint32_t num_quantiles, const float *depth_quantiles, const uint32_t *depth_idx,
                             const float *depth_grad, const void *ray_error, float contribution_alpha_grad,
                             const float *distortion, const float *distortion_grad, const float *W_total,
@@ -762,6 +827,7 @@ extern "C" int vt_trace_bwd(int attr_dtype, const float *points, const void *dif
     a.adj_diff = reinterpret_cast<const uint2 *>(adj_diff_workspace);
     a.rays = rays;
     a.num_rays = num_rays;
+    set_image_order(a, num_rays, image_h, image_w);
     a.start_point = start_point;
     a.rgba = rgba;
     a.rgba_grad = rgba_grad;
