@@ -9,9 +9,10 @@ traversal kernel), as timed by the reference's benchmark_eval.py:137-158;
 
 Also reported: the traversal kernel's duration from HIP events on its stream,
 its algorithmic bytes per frame (from the kernel's own per-ray walk counters)
-and the fraction of MI355X's 8 TB/s HBM peak; the CPU oracle on a bounded
-sample of the same frame; optionally (``--train``) the config-2 training step
-(fwd + bwd ms/step, 262,144 sites, 800x600 rays).
+and the fraction of MI355X's 8 TB/s HBM peak; the CPU oracle on whole frames
+of the same orbit (about ``--cpu-seconds`` of work, compared bit for bit);
+and, unless ``--no-train``, the config-2 training step (BASELINE.json
+fwd + bwd ms/step, 262,144 sites, 800x600 rays).
 """
 from __future__ import annotations
 
@@ -70,13 +71,14 @@ def main():
     ap.add_argument("--height", type=int, default=822)
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU-baseline sample time")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--train", action="store_true", help="also time the config-2 fwd+bwd training step")
+    ap.add_argument("--no-train", action="store_true", help="skip the config-2 fwd+bwd training step")
     ap.add_argument("--profile", action="store_true", help="short run for rocprofv3 (no CPU leg, no stats)")
+    ap.add_argument("--train-only", action="store_true", help="only the config-2 training step (profiling)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run 8 device copies of 1 GiB (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is design-only (see DESIGN.md)",
+        print(json.dumps({"error": "this build runs on one GPU; sharding across GPUs is a design, not a run mode",
                           "n_gpus": args.gpus}))
         sys.exit(2)
 
@@ -90,6 +92,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     _lib.load()
     dev = torch.device("cuda:0")
+    if args.train_only:
+        print(json.dumps({"train_c2": train_c2(dev, log)}), flush=True)
+        return
     if args.copy_calib:
         src = torch.ones(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB
         dst = torch.empty_like(src)
@@ -236,7 +241,7 @@ def main():
         log(f"CPU oracle: {rays_s / 1e6:.3f} Mrays/s on {cores} threads over {nframes} frames; "
             f"bit-identical to GPU: {same}")
 
-    if args.train:
+    if not args.no_train and not args.profile:
         result["train_c2"] = train_c2(dev, log)
 
     print(json.dumps(result), flush=True)
@@ -259,22 +264,36 @@ def train_c2(dev, log):
     g[..., 3] = 0
     sp = model.get_starting_point(rays)
 
-    def step():
+    stream = torch.cuda.current_stream(dev)
+
+    def step(ev=None):
         model.zero_grad(set_to_none=True)
+        if ev:
+            ev[0].record(stream)
         rgba, _, _, _, _, dist = model(rays, start_point=sp, weight_threshold=0.001)
+        if ev:
+            ev[1].record(stream)
         rgba.backward(g)
+        if ev:
+            ev[2].record(stream)
 
     for _ in range(3):
         step()
     torch.cuda.synchronize()
     K = 10
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(K)]
     t = time.perf_counter()
-    for _ in range(K):
-        step()
+    for i in range(K):
+        step(evs[i])
     torch.cuda.synchronize()
     ms = 1000 * (time.perf_counter() - t) / K
-    log(f"C2 fwd+bwd {ms:.2f} ms/step")
-    return {"fwd_bwd_ms_per_step": round(ms, 3), "rays": 480000, "sites": sc.num_points, "dtype": "fp32"}
+    fwd = float(np.mean([a.elapsed_time(b) for a, b, _ in evs]))
+    bwd = float(np.mean([b.elapsed_time(c) for _, b, c in evs]))
+    log(f"C2 fwd+bwd {ms:.2f} ms/step (forward {fwd:.2f} ms, backward {bwd:.2f} ms)")
+    return {"fwd_bwd_ms_per_step": round(ms, 3), "forward_ms": round(fwd, 3), "backward_ms": round(bwd, 3),
+            "rays": 480000, "sites": sc.num_points, "dtype": "fp32",
+            "workload": "C2: TraceVoroTracing forward + backward, 262,144 sites (torus + background), 4x4 fp32 "
+                        "textures, one 800x600 pinhole camera, upstream dL/dRGB ~ N(0,1), thr 0.001"}
 
 
 if __name__ == "__main__":

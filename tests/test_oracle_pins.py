@@ -438,3 +438,16 @@ def test_cell_intersection_grad_vs_central_differences():
             e[k] = 1e-6
             fd[k] = (_seg_t(O, D, P + e, Q) - _seg_t(O, D, P - e, Q)) / 2e-6
         assert np.allclose(got, fd, rtol=2e-3, atol=2e-3 * np.abs(fd).max())
+
+
+@pytest.mark.parametrize("R", [4, 8])
+def test_oct_wrap_edge_form_equals_general_on_tap_domain(R):
+    """The kernels use a reduced wrap valid for texel coordinates in [-1, R]
+    (every bilinear tap of an encoded direction): u mod R and one fold per
+    coordinate outside [0, R).  It must equal the general wrap there."""
+    for u in range(-1, R + 1):
+        for v in range(-1, R + 1):
+            wu, wv = u & (R - 1), v & (R - 1)
+            if (not 0 <= u < R) != (not 0 <= v < R):
+                wu, wv = R - 1 - wu, R - 1 - wv
+            assert wv * R + wu == core.oct_wrap_index(u, v, R), (u, v)

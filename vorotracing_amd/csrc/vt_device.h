@@ -121,21 +121,6 @@ __device__ __forceinline__ uint32_t xcd_block_linear() { return xcd_block() * bl
 // ---------------------------------------------------------------------------
 // octahedral map (ray_integrator_octmap.cuh:17-55)
 
-template <int R> __device__ __forceinline__ int oct_wrap(int u, int v)
-{
-    if (u >= 0 && u < R && v >= 0 && v < R)
-        return v * R + u;
-    int wu = ((u % R) + R) % R;
-    int wv = ((v % R) + R) % R;
-    int fu = abs(u / R) + (u < 0 ? 1 : 0);
-    int fv = abs(v / R) + (v < 0 ? 1 : 0);
-    if (((fu ^ fv) & 1) != 0) {
-        wu = R - 1 - wu;
-        wv = R - 1 - wv;
-    }
-    return wv * R + wu;
-}
-
 template <int R> __device__ __forceinline__ void oct_encode(f3 d, float &tu, float &tv)
 {
     float l1 = (__builtin_fabsf(d.x) + __builtin_fabsf(d.y)) + __builtin_fabsf(d.z);
@@ -157,6 +142,27 @@ struct Bilinear {
     float w00, w10, w01, w11;
 };
 
+// oct_wrap_index (ray_integrator_octmap.cuh:36-55) restricted to texel
+// coordinates in [-1, R] (R a power of two),
+// the only ones a bilinear tap of an encoded direction reaches: oct_encode
+// gives |u|, |v| <= 1 (|x| <= l1 after rounding, and x * RN(1/l1) rounds to
+// at most 1), so tex_u lies in [-0.5, R - 0.5], floor(tex_u) in [-1, R - 1]
+// and floor(tex_u) + 1 in [0, R].  There the general form reduces to
+// wrap = u mod R and one fold for each coordinate outside [0, R).
+template <int R> __device__ __forceinline__ int oct_wrap_edge(int u, int v)
+{
+    static_assert((R & (R - 1)) == 0, "R must be a power of two");
+    int wu = u & (R - 1);
+    int wv = v & (R - 1);
+    bool fu = (unsigned)u >= (unsigned)R;
+    bool fv = (unsigned)v >= (unsigned)R;
+    if (fu != fv) {
+        wu = R - 1 - wu;
+        wv = R - 1 - wv;
+    }
+    return wv * R + wu;
+}
+
 template <int R> __device__ __forceinline__ Bilinear bilinear_setup(float u, float v)
 {
     Bilinear b;
@@ -164,10 +170,10 @@ template <int R> __device__ __forceinline__ Bilinear bilinear_setup(float u, flo
     int v0 = (int)__builtin_floorf(v);
     float fu = u - (float)u0;
     float fv = v - (float)v0;
-    b.i00 = oct_wrap<R>(u0, v0);
-    b.i10 = oct_wrap<R>(u0 + 1, v0);
-    b.i01 = oct_wrap<R>(u0, v0 + 1);
-    b.i11 = oct_wrap<R>(u0 + 1, v0 + 1);
+    b.i00 = oct_wrap_edge<R>(u0, v0);
+    b.i10 = oct_wrap_edge<R>(u0 + 1, v0);
+    b.i01 = oct_wrap_edge<R>(u0, v0 + 1);
+    b.i11 = oct_wrap_edge<R>(u0 + 1, v0 + 1);
     b.w00 = (1.0f - fu) * (1.0f - fv);
     b.w10 = fu * (1.0f - fv);
     b.w01 = (1.0f - fu) * fv;

@@ -85,7 +85,7 @@ template <typename A, int RD, int RS> struct TrainTex {
 
 constexpr int TRAIN_BLOCK = 256;
 constexpr int TRAIN_WAVES = TRAIN_BLOCK / 64;
-constexpr int AGG_MIN = 4;
+constexpr int AGG_MIN = 2;
 
 // LDS floats per wave: diffuse + specular maps of one cell, density,
 // point_error, one point gradient
@@ -102,7 +102,7 @@ __device__ __forceinline__ uint32_t lane_rank(uint64_t m)
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
-constexpr int AGG_ROUNDS = 3;
+constexpr int AGG_ROUNDS = 32;
 
 // One combining round over the lanes still pending: the key of the lowest
 // pending lane leads; `mine` marks its group and `comb` (wave-uniform) says
@@ -399,8 +399,9 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
                     atomicAdd(pb + 2, g.z);
                 }
                 wave_lds_sync();
-                uint32_t k = lane_rank(__ballot(1)); // >= AGG_MIN lanes are active
-                if (k < 3) {
+                uint64_t act = __ballot(1);
+                uint32_t nact = __popcll(act);
+                for (uint32_t k = lane_rank(act); k < 3u; k += nact) {
                     float x = pb[k];
                     pb[k] = 0.0f;
                     if (x != 0.0f)

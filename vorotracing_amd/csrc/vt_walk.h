@@ -27,25 +27,16 @@ __device__ __forceinline__ bool exit_before(float num, float dp, float bnum, flo
     float Q = bnum * dp;
     float gap = fma_(num, bdp, -Q);
     float aq = __builtin_fabsf(Q);
+    // h < 0 <=> 2^18 |gap| > |Q| (sign of one rounding); false for NaN and
+    // for |Q| = inf, which therefore need no test of their own
     float h = fma_(__builtin_fabsf(gap), -0x1p18f, aq);
-    if (h < 0.0f && aq >= 1e-26f && aq < __builtin_huge_valf())
+    if (h < 0.0f && aq >= 1e-26f)
         return gap < 0.0f;
     return num / dp < bnum / bdp;
 }
 
-// -0.0f hidden from constant folding: fma(a, b, -0) == a*b exactly (also
-// for signed zeros), and keeping it an fma lets a half operand fold into
-// v_fma_mix_f32 instead of a separate conversion.
-__device__ __forceinline__ float opaque_neg_zero()
-{
-    uint32_t b;
-    asm("s_mov_b32 %0, 0x80000000" : "=s"(b));
-    return __builtin_bit_cast(float, b);
-}
-
 // f16 halves of a packed face record (x | y << 16, z | w << 16), widened
-// exactly; used directly as fma operands so the compiler can fold the
-// conversion into v_fma_mix_f32.
+// exactly.
 __device__ __forceinline__ float half_lo(uint32_t w) { return h2f((uint16_t)(w & 0xffffu)); }
 __device__ __forceinline__ float half_hi(uint32_t w) { return h2f((uint16_t)(w >> 16)); }
 
@@ -95,7 +86,6 @@ __device__ __forceinline__ bool walk_step(WalkState &w, f3 o, f3 d, const float 
     // exit_before.
     uint32_t best = NONE;
     float bnum = FIRST_BNUM, bdp = FIRST_BDP;
-    const float nz = opaque_neg_zero();
     for (uint32_t i = 0; i < nf; i += CHUNK) {
         uint2 rec[CHUNK];
 #pragma unroll
@@ -103,14 +93,19 @@ __device__ __forceinline__ bool walk_step(WalkState &w, f3 o, f3 d, const float 
             rec[j] = fl[i + j];
 #pragma unroll
         for (int j = 0; j < CHUNK; ++j) {
+            // Widen the halves once (v_cvt_f32_f16) and share them between
+            // dp and num: the empty asm keeps the compiler from folding the
+            // widening into v_fma_mix_f32 operands, which issue at a lower
+            // rate than a conversion plus plain fmas.
             float ox = half_lo(rec[j].x), oy = half_hi(rec[j].x), oz = half_lo(rec[j].y);
-            float dp = fma_(oz, d.z, fma_(oy, d.y, fma_(ox, d.x, nz)));
-            // p + off/2: off/2 is exact, so the fma rounds once like p + off*0.5
-            float ex = fma_(ox, 0.5f, p.x) - o.x;
-            float ey = fma_(oy, 0.5f, p.y) - o.y;
-            float ez = fma_(oz, 0.5f, p.z) - o.z;
-            float num = fma_(ez, oz, fma_(ey, oy, fma_(ex, ox, nz)));
+            asm("" : "+v"(ox), "+v"(oy), "+v"(oz));
+            float dp = fma_(oz, d.z, fma_(oy, d.y, ox * d.x));
             if (dp > 0.0f && (i + j) < nf) {
+                // p + off/2: off/2 is exact, so the fma rounds once like p + off*0.5
+                float ex = fma_(ox, 0.5f, p.x) - o.x;
+                float ey = fma_(oy, 0.5f, p.y) - o.y;
+                float ez = fma_(oz, 0.5f, p.z) - o.z;
+                float num = fma_(ez, oz, fma_(ey, oy, ex * ox));
                 if (exit_before(num, dp, bnum, bdp)) {
                     bnum = num;
                     bdp = dp;
