@@ -200,6 +200,8 @@ def main():
                 tr = json.load(f)
             result["roofline"]["traffic"] = tr.get("hbm_bytes_per_launch")
             result["roofline"]["traffic_source"] = "profiles/traffic_infer_f16_c3.json (rocprofv3 --pmc)"
+        result["roofline"]["stream_copy_gbs"] = round(stream_copy_gbs(dev), 1)
+        result["c4_q8"] = c4_q8(model, poses, dev, log, thr, skip)
 
     if not args.no_cpu and not args.profile:
         from oracle import core as oc
@@ -240,15 +242,95 @@ def main():
         }
         log(f"CPU oracle: {rays_s / 1e6:.3f} Mrays/s on {cores} threads over {nframes} frames; "
             f"bit-identical to GPU: {same}")
+        result["walk"].update(compulsory_bytes(oc, pts, d4, s4, den, adj, off, ad, poses[0], inf, thr, skip, cores))
+
 
     if not args.no_train and not args.profile:
-        result["train_c2"] = train_c2(dev, log)
+        result["train_c2"] = train_c2(dev, log, cpu=not args.no_cpu)
 
     print(json.dumps(result), flush=True)
 
 
-def train_c2(dev, log):
-    """Config-2 training step: TraceVoroTracing forward + backward (fp32), 262,144 sites, 800x600 rays."""
+def compulsory_bytes(oc, pts, d4, s4, den, adj, off, ad, rays, inf, thr, skip, cores):
+    """Lower bound on the bytes one frame (pose 0) must bring from memory:
+    every distinct cell on some ray's walk, counted once with its offsets
+    pair, face records, site and density (textures excluded).  The walk is
+    read from the CPU oracle's visit log, whose visit sequences equal the
+    GPU's (the frames are compared bit for bit above)."""
+    import numpy as np
+
+    rays_np = rays.cpu().numpy().reshape(-1, 6)
+    sp_np = inf.get_starting_point(rays).cpu().numpy().reshape(-1)
+    seen = np.zeros(pts.shape[0], bool)
+    chunk = 1 << 17
+    for a in range(0, rays_np.shape[0], chunk):
+        _, _, vl = oc.trace_infer_f16(pts, d4, s4, 4, 4, den, adj, off, ad, rays_np[a:a + chunk], sp_np[a:a + chunk],
+                                      weight_threshold=thr, cell_skip_threshold=skip, max_log=256, threads=cores)
+        v = vl[vl != 0xffffffff]
+        seen[v] = True
+    cells = np.nonzero(seen)[0]
+    faces = (off[cells + 1].astype(np.int64) - off[cells]).sum()
+    return {"distinct_cells_pose0": int(cells.size),
+            "compulsory_bytes_pose0": int(cells.size * (8 + 12 + 4) + 8 * faces),
+            "compulsory_note": "distinct cells on the walks of pose 0 x (offsets 8 + site 12 + density 4 + "
+                               "8 per face record); textures excluded; walks from the CPU oracle's visit log"}
+
+
+def stream_copy_gbs(dev):
+    """Measured device-copy bandwidth (read + write bytes / time) of a 1 GiB
+    torch copy: the box's practical HBM ceiling, reported beside the 8 TB/s
+    datasheet peak."""
+    import torch
+
+    src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(8):
+        dst.copy_(src)
+    b.record()
+    torch.cuda.synchronize()
+    per = a.elapsed_time(b) / 8 * 1e-3
+    del src, dst
+    return 2 * (1 << 30) / per / 1e9
+
+
+def c4_q8(model, poses, dev, log, thr, skip):
+    """Config-4 shape: q8 attributes with per-channel scale/offset, 8 cameras
+    (poses 0, 4, ..., 28) rendered in one launch with one start cell per camera."""
+    import numpy as np
+    import torch
+
+    from vorotracing_amd.infer import VoroTracingInfer
+
+    inf8 = VoroTracingInfer(model, sort_morton=True, quantize="q8", per_channel_q8=True)
+    batch = torch.stack([poses[k] for k in range(0, len(poses), 4)][:8]).contiguous()
+    sp = inf8.get_starting_point(batch)
+    for _ in range(3):
+        inf8.render(batch, start_point=sp, weight_threshold=thr, cell_skip_threshold=skip)
+    torch.cuda.synchronize()
+    K = 10
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(K):
+        inf8.render(batch, start_point=sp, weight_threshold=thr, cell_skip_threshold=skip)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / K
+    nr = batch.numel() // 6
+    log(f"C4 q8, {batch.shape[0]} cameras per launch: {ms:.3f} ms/launch, {nr / ms / 1e3:.1f} Mrays/s")
+    del inf8, batch
+    return {"ms_per_launch": round(ms, 3), "cameras": 8, "rays_per_launch": nr,
+            "mrays_per_s": round(nr / ms / 1e3, 1), "attributes": "u8, per-channel scale/offset",
+            "note": "BASELINE.json configs[3] shape; parity in tests/test_gpu_prep.py"}
+
+
+def train_c2(dev, log, cpu=False):
+    """Config-2 training step: TraceVoroTracing forward + backward (fp32), 262,144 sites, 800x600 rays.
+    With ``cpu``, the oracle also runs one forward + backward on the same inputs (the CPU baseline of this
+    config), checked against the GPU: forward bit for bit, gradients to 1e-3 of each tensor's scale."""
     import numpy as np
     import torch
 
@@ -290,10 +372,55 @@ def train_c2(dev, log):
     fwd = float(np.mean([a.elapsed_time(b) for a, b, _ in evs]))
     bwd = float(np.mean([b.elapsed_time(c) for _, b, c in evs]))
     log(f"C2 fwd+bwd {ms:.2f} ms/step (forward {fwd:.2f} ms, backward {bwd:.2f} ms)")
-    return {"fwd_bwd_ms_per_step": round(ms, 3), "forward_ms": round(fwd, 3), "backward_ms": round(bwd, 3),
-            "rays": 480000, "sites": sc.num_points, "dtype": "fp32",
-            "workload": "C2: TraceVoroTracing forward + backward, 262,144 sites (torus + background), 4x4 fp32 "
-                        "textures, one 800x600 pinhole camera, upstream dL/dRGB ~ N(0,1), thr 0.001"}
+    out = {"fwd_bwd_ms_per_step": round(ms, 3), "forward_ms": round(fwd, 3), "backward_ms": round(bwd, 3),
+           "rays": 480000, "sites": sc.num_points, "dtype": "fp32",
+           "workload": "C2: TraceVoroTracing forward + backward, 262,144 sites (torus + background), 4x4 fp32 "
+                       "textures, one 800x600 pinhole camera, upstream dL/dRGB ~ N(0,1), thr 0.001"}
+    if cpu:
+        out["cpu_baseline"] = train_c2_cpu(model, rays, sp, g, log)
+    return out
+
+
+def train_c2_cpu(model, rays, sp, g, log):
+    """One forward + backward of the CPU oracle on the config-2 step, timed, and compared with the GPU."""
+    import numpy as np
+    import torch
+
+    from oracle import core as oc
+
+    cores, model_name = cpu_info()
+    model.zero_grad(set_to_none=True)
+    rgba, _, _, _, _, _ = model(rays, start_point=sp, weight_threshold=0.001)
+    rgba.backward(g)
+    torch.cuda.synchronize()
+    dens = model._get_primal_density().detach().cpu().numpy()
+    args = (model.primal_points.detach().cpu().numpy(), model.att_diffuse.detach().cpu().numpy(),
+            model.att_specular.detach().cpu().numpy(), 4, 4, dens, model.point_adjacency.cpu().numpy(),
+            model.point_adjacency_offsets.cpu().numpy(), rays.cpu().numpy(), sp.cpu().numpy())
+    t = time.perf_counter()
+    fw = oc.trace_fwd(*args, weight_threshold=0.001, threads=cores)
+    t_fwd = time.perf_counter() - t
+    gn = g.cpu().numpy()
+    t = time.perf_counter()
+    bw = oc.trace_bwd(*args, fw["rgba"], gn, distortion=fw["distortion"], W_total=fw["W_total"],
+                      S_total=fw["S_total"], t_far=fw["t_far"], weight_threshold=0.001, threads=cores)
+    t_bwd = time.perf_counter() - t
+
+    def rel(got, want):
+        want = np.asarray(want, np.float64)
+        return float(np.abs(np.asarray(got, np.float64) - want).max() / max(np.abs(want).max(), 1e-30))
+
+    same = bool(np.array_equal(rgba.detach().cpu().numpy().view(np.uint32), fw["rgba"].view(np.uint32)))
+    errs = {"points": rel(model.primal_points.grad.cpu().numpy(), bw["points_grad"]),
+            "diffuse": rel(model.att_diffuse.grad.cpu().numpy(), bw["diffuse_grad"]),
+            "specular": rel(model.att_specular.grad.cpu().numpy(), bw["specular_grad"]),
+            "density": rel(model.density.grad.cpu().numpy(), bw["density_grad"] * dens)}
+    ms = 1000 * (t_fwd + t_bwd)
+    log(f"C2 CPU oracle: forward {t_fwd * 1e3:.0f} ms + backward {t_bwd * 1e3:.0f} ms on {cores} threads; "
+        f"rgba bit-identical {same}; max grad rel err {max(errs.values()):.2e}")
+    return {"value": round(ms, 1), "unit": "ms/step (fwd+bwd)", "cores": cores, "kind": "port",
+            "sample": f"one whole C2 step (480,000 rays); oracle/oracle.c OpenMP on {model_name or 'host CPU'}",
+            "rgba_bit_identical_to_gpu": same, "grad_rel_err_vs_gpu": {k: float(f"{v:.3g}") for k, v in errs.items()}}
 
 
 if __name__ == "__main__":

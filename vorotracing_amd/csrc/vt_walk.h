@@ -151,6 +151,16 @@ __device__ __forceinline__ uint32_t walk(f3 o, f3 d, const float *points,
     return w.n;
 }
 
+// Screen tiles are visited in vertical strips TILE_STRIP tiles wide (the last
+// strip takes the remainder), row by row inside a strip; 0 = row-major over
+// the whole image.  Consecutive waves, and hence the waves that run at the
+// same time on one XCD (one contiguous range of blocks, xcd_block), then
+// cover a compact screen region rather than an image-wide band.
+#ifndef VT_TILE_STRIP
+#define VT_TILE_STRIP 16
+#endif
+constexpr uint32_t TILE_STRIP = VT_TILE_STRIP;
+
 // Lane -> ray for a tiled image batch: one wave (64 lanes) per tile_w x
 // tile_h screen tile.  Returns NONE for lanes past the image edge.
 __device__ __forceinline__ uint32_t tiled_ray(uint32_t lane_global, uint32_t num_images, uint32_t H, uint32_t W,
@@ -163,8 +173,22 @@ __device__ __forceinline__ uint32_t tiled_ray(uint32_t lane_global, uint32_t num
     uint32_t tpi = tiles_x * tiles_y;
     uint32_t img = tile / tpi;
     uint32_t ti = tile % tpi;
-    uint32_t y = (ti / tiles_x) * th + within / tw;
-    uint32_t x = (ti % tiles_x) * tw + within % tw;
+    uint32_t tx, ty;
+    if (TILE_STRIP == 0 || TILE_STRIP >= tiles_x) {
+        ty = ti / tiles_x;
+        tx = ti % tiles_x;
+    } else {
+        uint32_t per_strip = TILE_STRIP * tiles_y;
+        uint32_t strip = ti / per_strip;
+        uint32_t r = ti % per_strip;
+        uint32_t w = TILE_STRIP;
+        if ((strip + 1) * TILE_STRIP > tiles_x)
+            w = tiles_x - strip * TILE_STRIP;
+        ty = r / w;
+        tx = strip * TILE_STRIP + r % w;
+    }
+    uint32_t y = ty * th + within / tw;
+    uint32_t x = tx * tw + within % tw;
     if (img >= num_images || x >= W || y >= H)
         return NONE;
     return (img * H + y) * W + x;
