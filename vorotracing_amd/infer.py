@@ -26,31 +26,69 @@ class VoroTracingInfer:
 
     def __init__(self, model, sort_morton: bool = True, quantize: Literal["fp16", "q8"] = "fp16",
                  per_channel_q8: bool = False):
-        self.primal_points = model.primal_points.detach().contiguous()
-        self.density = (model.config.activation_scale * torch.exp(model.density)).detach().contiguous()
-        self.point_adjacency = model.point_adjacency.clone()
-        self.point_adjacency_offsets = model.point_adjacency_offsets
-        self.bvh = model.bvh
+        self._setup(model.primal_points.detach().contiguous(),
+                    (model.config.activation_scale * torch.exp(model.density)).detach().contiguous(),
+                    model.point_adjacency.clone(), model.point_adjacency_offsets, model.bvh,
+                    model.att_diffuse.detach(), model.att_specular.detach(), model.config.oct_map_res,
+                    model.config.spec_oct_map_res, quantize, per_channel_q8, sort_morton)
+
+    def _setup(self, points, density, adjacency, offsets, bvh, diffuse, specular, diff_res, spec_res, quantize,
+               per_channel_q8, sort_morton):
+        self.primal_points = points
+        self.density = density
+        self.point_adjacency = adjacency
+        self.point_adjacency_offsets = offsets
+        self.bvh = bvh
         self.device = self.primal_points.device
         self.quantize = quantize
-        self.diff_res = model.config.oct_map_res
-        self.spec_res = model.config.spec_oct_map_res
+        self.diff_res = diff_res
+        self.spec_res = spec_res
         self.diffuse_q8 = self.specular_q8 = None
         self.diffuse_fp16 = self.specular_fp16 = None
         if quantize == "q8":
-            self.diffuse_q8, self.diff_scale, self.diff_offset = self._quantize_to_uint8(
-                model.att_diffuse.detach(), per_channel_q8)
-            self.specular_q8, self.spec_scale, self.spec_offset = self._quantize_to_uint8(
-                model.att_specular.detach(), per_channel_q8)
+            self.diffuse_q8, self.diff_scale, self.diff_offset = self._quantize_to_uint8(diffuse, per_channel_q8)
+            self.specular_q8, self.spec_scale, self.spec_offset = self._quantize_to_uint8(specular, per_channel_q8)
         elif quantize == "fp16":
-            self.diffuse_fp16 = self._pad_3to4(model.att_diffuse.detach(), self.diff_res)
-            self.specular_fp16 = self._pad_3to4(model.att_specular.detach(), self.spec_res)
+            self.diffuse_fp16 = self._pad_3to4(diffuse, self.diff_res)
+            self.specular_fp16 = self._pad_3to4(specular, self.spec_res)
         else:
             raise ValueError(f"Invalid quantization method: {quantize}")
         if sort_morton:
             self._reorder_by_morton()
+        if self.bvh is None:
+            self.bvh = ops.NNBVH()
+            self.bvh.build(self.primal_points)
         self.adjacent_diff = ops.prefetch_octmap_adj(self.primal_points, self.point_adjacency,
                                                      self.point_adjacency_offsets)
+
+    @classmethod
+    def from_foam(cls, path, device=torch.device("cuda"), quantize: Literal["fp16", "q8"] = "fp16",
+                  per_channel_q8: bool = False, sort_morton: bool = False):
+        """A scene from a ``.foam`` file (V3 or V4; vorotracing_amd.foam, the reference's
+        scripts/export_for_viewer.py format).  Cells are used in file order (the exporter writes a
+        Morton-sorted VoroTracingInfer); the file's density is already activated; adjacent_diff is
+        recomputed by the prefetch kernel.  A file without specular maps renders with zero specular
+        logits.  The file's header (thresholds, poses) is kept as ``self.foam``."""
+        import numpy as np
+
+        from . import foam
+
+        sc = foam.read_foam(path)
+        dev = torch.device(device)
+        n = sc.points.shape[0]
+
+        def t(a, dtype=None):
+            x = torch.from_numpy(np.ascontiguousarray(a))
+            return (x if dtype is None else x.to(dtype)).to(dev)
+
+        rs = sc.res_spec if sc.specular is not None else sc.res_diff
+        spec = sc.specular if sc.specular is not None else np.zeros((n, 3 * rs * rs), np.float16)
+        self = cls.__new__(cls)
+        self._setup(t(sc.points), t(sc.density).reshape(-1, 1), t(sc.adjacency), t(sc.offsets), None,
+                    t(sc.diffuse, torch.float32), t(spec, torch.float32), sc.res_diff, rs, quantize, per_channel_q8,
+                    sort_morton)
+        self.foam = sc
+        return self
 
     # -- preparation (HIP) ----------------------------------------------------
 
