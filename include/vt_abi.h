@@ -228,6 +228,29 @@ size_t vt_quantize_workspace_size(void);
 int vt_quantize_u8(const float *x, uint32_t rows, uint32_t cols, int per_channel, uint8_t *q, float *params,
                    void *workspace, vt_stream_t stream);
 
+/*
+ * Voronoi neighbours (the Delaunay adjacency) of a site set, built on the GPU.
+ * Replaces the adjacency step of vorotracing.cuda.build_voronoi_adjacency
+ * (cuda/__init__.py:16-46), which the reference delegates to Paragram.
+ *   vt_voronoi_build: points (num_points, 3) f32 -> offsets u32
+ *   (num_points+1) and *num_adjacency = offsets[num_points] (host).  Each
+ *   cell is clipped in fp64 from a bounding box by the bisector planes of
+ *   nearby sites; its neighbours are the sites whose planes keep a face, in
+ *   ascending order (the set equals qhull's Delaunay neighbours for points in
+ *   general position).  Synchronises `stream` (the host needs the total).
+ *   Fails with VT_ERR_INVALID if a cell exceeds the per-cell capacity or a
+ *   cut is degenerate (message gives the counts).
+ *   vt_voronoi_adjacency: writes the lists into adjacency (num_adjacency
+ *   entries; the caller adds any padding).
+ *   workspace: vt_voronoi_workspace_size(num_points) bytes, the same buffer
+ *   for both calls.
+ */
+size_t vt_voronoi_workspace_size(uint32_t num_points);
+int vt_voronoi_build(const float *points, uint32_t num_points, uint32_t *offsets, uint32_t *num_adjacency,
+                     void *workspace, vt_stream_t stream);
+int vt_voronoi_adjacency(uint32_t num_points, const uint32_t *offsets, uint32_t *adjacency, const void *workspace,
+                         vt_stream_t stream);
+
 /* fp16 Half4Texel padding.  Replaces VoroTracingInfer._pad_3to4 applied to
  * .half() maps (vorotracing.py:477-482, :505-512): f32 (rows, 3*T) ->
  * f16 (rows, 4*T), RNE cast, zero 4th channel. */

@@ -38,6 +38,9 @@ SIGNATURES = {
         [I32, P, P, P, U32, U32, P, P, U32, P, U32, P, U32, U32, U32, P, P, P, U32, P, P, P, P, F32, P, P, P, P, P, F32, U32,
          P, P, P, P, P, P, P, P], C.c_int),
     "vt_math_probe": ([I32, P, P, U32, P], C.c_int),
+    "vt_voronoi_workspace_size": ([U32], C.c_size_t),
+    "vt_voronoi_build": ([P, U32, P, P, P, P], C.c_int),
+    "vt_voronoi_adjacency": ([U32, P, P, P, P], C.c_int),
     "vt_bvh_create": ([P], C.c_int),
     "vt_bvh_destroy": ([P], C.c_int),
     "vt_bvh_build": ([P, P, U32, P], C.c_int),

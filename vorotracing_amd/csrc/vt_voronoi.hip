@@ -1,0 +1,835 @@
+// vt_voronoi.hip -- Voronoi neighbours (the Delaunay adjacency CSR) of a site
+// set, built on the GPU.  Replaces the adjacency step of
+// vorotracing.cuda.build_voronoi_adjacency (cuda/__init__.py:16-46, which
+// calls Paragram; the synthetic scenes of this build use host qhull).
+//
+// One wave per cell; the cell lives in LDS and is clipped in double
+// precision, in site-local coordinates:
+//   * it starts as a box around all sites (6 planes), 10^6 times their
+//     extent, so that the faces between convex-hull sites (unbounded in the
+//     Delaunay sense) keep a part inside it;
+//   * sites are taken from a uniform grid in distance bands [rho/2, rho)
+//     with rho doubling; a site q cuts the cell by its bisector plane
+//     d.x <= |d|^2/2 (d = q - p, exact in double for f32 inputs) when some
+//     vertex lies strictly outside it;
+//   * the walk stops once 2R <= rho (R: largest vertex distance; no farther
+//     site can cut the cell) or the bands have passed every site;
+//   * the neighbours are the sites whose planes keep a face, ascending.
+// The cell is kept as the triangulation of its dual (Ray, Sokolov, Lefebvre,
+// Levy, "Meshless Voronoi on the GPU", 2018): a vertex is a triangle of three
+// plane ids; a cut removes the vertices strictly outside the plane and closes
+// the hole with triangles (u, v, new plane) along the boundary edges (u, v).
+//
+// The scan is spread over the 64 lanes and pruned at three levels:
+//   * rows of grid cells: only the spherical shell of cells that can hold
+//     sites of the band;
+//   * grid cells (one per lane): skipped when no point x of the cell's box
+//     can satisfy x.v > |x|^2/2 for a vertex v, bounding max x.v by the
+//     bounding box of the near vertices and by each far (box) vertex;
+//   * candidates (one per lane, packed across the surviving grid cells of a
+//     row): the same test for the site itself, then the exact vertex test.
+// The planes that cut are applied one at a time, each cut spread over the
+// lanes.  A first pass runs every cell with small tables; the few cells that
+// overflow them run again with large ones.
+#include "vt_internal.h"
+#include "vt_prims.h"
+
+#include <algorithm>
+#include <cmath>
+
+namespace vt {
+
+constexpr uint32_t VOR_NONE = 0xffffffffu;
+constexpr int VOR_BLOCK = 64; // one wave
+
+// Per-cell capacities.  Plane ids are bytes, so P <= 255.
+template <int P_, int T_, int E_, int K_> struct VorCap {
+    static constexpr int P = P_;  // planes (6 box + bisectors)
+    static constexpr int T = T_;  // vertices
+    static constexpr int E = E_;  // directed edges of the region removed by one cut
+    static constexpr int K = K_;  // neighbours in the output
+};
+using VorSmall = VorCap<96, 192, 96, 64>;
+using VorLarge = VorCap<255, 510, 384, 192>;
+
+struct VorGrid {
+    float lo[3];
+    float h;       // cell side
+    uint32_t g[3]; // cells per axis
+    double box_lo[3], box_hi[3];
+    double far2;   // squared local distance beyond which a vertex counts as a box vertex
+};
+
+enum { VOR_OK = 0, VOR_FULL = 1, VOR_DEGENERATE = 2 };
+
+// fails[] words: failures, the retry count, big-list slots, work counters
+enum { F_FULL = 0, F_DEGENERATE = 1, F_RETRY = 2, F_BIG = 3, F_NEXT0 = 4, F_NEXT1 = 5, F_WORDS = 8 };
+
+__device__ __forceinline__ double4 cross_d(double4 a, double4 b)
+{
+    return make_double4(a.y * b.z - a.z * b.y, a.z * b.x - a.x * b.z, a.x * b.y - a.y * b.x, 0.0);
+}
+__device__ __forceinline__ double dot_d(double4 a, double4 b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
+
+// intersection of three planes n.x <= w; w of the result = |v|^2
+__device__ __forceinline__ double4 plane_vertex(double4 a, double4 b, double4 d)
+{
+    double4 bc = cross_d(b, d), ca = cross_d(d, a), ab = cross_d(a, b);
+    double det = dot_d(a, bc);
+    double s = 1.0 / det;
+    double4 v = make_double4((a.w * bc.x + b.w * ca.x + d.w * ab.x) * s, (a.w * bc.y + b.w * ca.y + d.w * ab.y) * s,
+                             (a.w * bc.z + b.w * ca.z + d.w * ab.z) * s, 0.0);
+    v.w = dot_d(v, v);
+    return v;
+}
+
+// The box planes 0..5 (+x, -x, +y, -y, +z, -z) and its 8 corners.  Corner
+// (sx, sy, sz) is the triangle of planes (X, Y, Z), ordered X, Y, Z when an
+// even number of them are "-" planes and X, Z, Y otherwise, so that every
+// edge of the closed triangulation appears once in each direction.
+__device__ __forceinline__ double4 box_plane(const VorGrid &g, double px, double py, double pz, int q)
+{
+    int a = q >> 1;
+    double p = a == 0 ? px : (a == 1 ? py : pz);
+    double4 pl = make_double4(0.0, 0.0, 0.0, (q & 1) ? p - g.box_lo[a] : g.box_hi[a] - p);
+    (&pl.x)[a] = (q & 1) ? -1.0 : 1.0;
+    return pl;
+}
+__device__ __forceinline__ uchar4 box_corner(int t)
+{
+    int sx = (t >> 2) & 1, sy = (t >> 1) & 1, sz = t & 1;
+    uint8_t X = (uint8_t)sx, Y = (uint8_t)(2 + sy), Z = (uint8_t)(4 + sz);
+    return ((sx + sy + sz) & 1) == 0 ? make_uchar4(X, Y, Z, 0) : make_uchar4(X, Z, Y, 0);
+}
+__device__ __forceinline__ double4 box_corner_pos(const VorGrid &g, double px, double py, double pz, int t)
+{
+    int sx = (t >> 2) & 1, sy = (t >> 1) & 1, sz = t & 1;
+    double4 v = make_double4(sx ? g.box_lo[0] - px : g.box_hi[0] - px, sy ? g.box_lo[1] - py : g.box_hi[1] - py,
+                             sz ? g.box_lo[2] - pz : g.box_hi[2] - pz, 0.0);
+    v.w = dot_d(v, v);
+    return v;
+}
+
+__device__ __forceinline__ int grid_coord(float x, float lo, float h, uint32_t g)
+{
+    int v = (int)floorf((x - lo) / h);
+    return v < 0 ? 0 : (v >= (int)g ? (int)g - 1 : v);
+}
+
+// Grid cells of the row (dy, dz), relative to the site's cell (cx, ., .),
+// that can hold sites at distances in [lo_g, hi_g) (grid units): up to two
+// x ranges, [a0, a1] and [b0, b1] (empty when first > last).  A site in the
+// cell at offset (dx, dy, dz) lies between (|dx|-1, |dy|-1, |dz|-1)+ and
+// (|dx|+1, |dy|+1, |dz|+1) grid units away per axis; cells entirely inside
+// lo_g were scanned by the earlier bands.  The margins of the callers cover
+// the rounding of grid_coord at cell borders.
+struct RowSpan {
+    int a0, a1, b0, b1;
+};
+__device__ __forceinline__ bool band_row(int dy, int dz, double lo_g, double hi_g, int rr, int cx, int gx, RowSpan &s)
+{
+    double my = (double)max(abs(dy) - 1, 0), mz = (double)max(abs(dz) - 1, 0);
+    double rem = hi_g * hi_g - my * my - mz * mz;
+    if (rem <= 0.0)
+        return false;
+    int ro = min((int)floor(sqrt(rem)) + 1, rr);
+    double py = (double)(abs(dy) + 1), pz = (double)(abs(dz) + 1);
+    double rin = lo_g * lo_g - py * py - pz * pz;
+    int si = rin > 0.0 ? (int)floor(sqrt(rin)) - 2 : -1;
+    int lo = max(cx - ro, 0), hi = min(cx + ro, gx - 1);
+    if (si < 0) {
+        s.a0 = lo;
+        s.a1 = hi;
+        s.b0 = 1;
+        s.b1 = 0;
+    } else {
+        s.a0 = lo;
+        s.a1 = min(cx - si - 1, hi);
+        s.b0 = max(cx + si + 1, lo);
+        s.b1 = hi;
+    }
+    return true;
+}
+
+template <class Cap> struct WaveCell {
+    double4 P[Cap::P];
+    double4 V[Cap::T]; // w = |v|^2
+    uint32_t nid[Cap::P];
+    uchar4 T[Cap::T];
+    uint16_t ed[Cap::E];  // directed edges (u | v << 8) of the removed vertices
+    uint16_t far[Cap::T]; // indices of the vertices beyond far2
+    uint32_t out[Cap::K];
+    uint32_t run_off[64]; // candidates of one row piece: first candidate of lane l's grid cell
+    uint32_t run_at[64];  // ... and where its sites start in the sorted order
+    uint32_t used[8];
+    uint8_t remap[Cap::P];
+    int np_shared;
+};
+
+__device__ __forceinline__ uint32_t lane_rank(uint64_t m)
+{
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+// maximum over the wave, returned in scalar registers
+__device__ __forceinline__ double wave_max(double x)
+{
+    for (int o = 32; o > 0; o >>= 1)
+        x = fmax(x, __shfl_xor(x, o));
+    const uint64_t b = (uint64_t)__double_as_longlong(x);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// Wave-uniform scalars of the cell (every lane holds the same values).
+struct WaveState {
+    int np, nt, nfar;
+    double R2, Rn2;          // squared radius of all vertices, of the near ones
+    double bmin[3], bmax[3]; // bounding box of the near vertices (0 when none)
+};
+
+// R2, the near radius and bounding box and the far list, after a change.
+template <class Cap> __device__ void wcell_radii(WaveCell<Cap> &c, WaveState &s, double far2, int lane)
+{
+    double r = 0.0, rn = 0.0;
+    double mn[3] = {INFINITY, INFINITY, INFINITY}, mx[3] = {-INFINITY, -INFINITY, -INFINITY};
+    int nf = 0;
+    for (int t0 = 0; t0 < s.nt; t0 += 64) {
+        const int t = t0 + lane;
+        bool f = false;
+        if (t < s.nt) {
+            const double4 v = c.V[t];
+            r = fmax(r, v.w);
+            f = v.w > far2;
+            if (!f) {
+                rn = fmax(rn, v.w);
+                mn[0] = fmin(mn[0], v.x);
+                mn[1] = fmin(mn[1], v.y);
+                mn[2] = fmin(mn[2], v.z);
+                mx[0] = fmax(mx[0], v.x);
+                mx[1] = fmax(mx[1], v.y);
+                mx[2] = fmax(mx[2], v.z);
+            }
+        }
+        uint64_t m = __ballot(f);
+        if (f)
+            c.far[nf + lane_rank(m)] = (uint16_t)t;
+        nf += __popcll(m);
+    }
+    s.R2 = wave_max(r);
+    s.Rn2 = wave_max(rn);
+    const bool any_near = nf < s.nt;
+    for (int a = 0; a < 3; ++a) {
+        s.bmin[a] = any_near ? -wave_max(-mn[a]) : 0.0;
+        s.bmax[a] = any_near ? wave_max(mx[a]) : 0.0;
+    }
+    s.nfar = nf;
+    __syncthreads();
+}
+
+// Marks the planes that some vertex uses in c.used.
+template <class Cap> __device__ void wcell_mark_used(WaveCell<Cap> &c, const WaveState &s, int lane)
+{
+    if (lane < 8)
+        c.used[lane] = 0;
+    __syncthreads();
+    for (int t = lane; t < s.nt; t += 64) {
+        uchar4 x = c.T[t];
+        atomicOr(&c.used[x.x >> 5], 1u << (x.x & 31));
+        atomicOr(&c.used[x.y >> 5], 1u << (x.y & 31));
+        atomicOr(&c.used[x.z >> 5], 1u << (x.z & 31));
+    }
+    __syncthreads();
+}
+
+// Drop bisector planes that no vertex uses any more (the 6 box planes stay),
+// renumbering the vertices' plane ids.  Called when the plane table is full.
+template <class Cap> __device__ void wcell_compact_planes(WaveCell<Cap> &c, WaveState &s, int lane)
+{
+    wcell_mark_used(c, s, lane);
+    if (lane == 0) {
+        int m = 6;
+        for (int q = 0; q < 6; ++q)
+            c.remap[q] = (uint8_t)q;
+        for (int q = 6; q < s.np; ++q) {
+            if (c.used[q >> 5] & (1u << (q & 31))) {
+                c.P[m] = c.P[q];
+                c.nid[m] = c.nid[q];
+                c.remap[q] = (uint8_t)m++;
+            }
+        }
+        c.np_shared = m;
+    }
+    __syncthreads();
+    for (int t = lane; t < s.nt; t += 64) {
+        uchar4 x = c.T[t];
+        c.T[t] = make_uchar4(c.remap[x.x], c.remap[x.y], c.remap[x.z], 0);
+    }
+    s.np = c.np_shared;
+    __syncthreads();
+}
+
+// Cut by n.x <= w, spread over the wave.  Returns a wave-uniform status
+// (VOR_OK also when the plane misses the cell).
+template <class Cap>
+__device__ int wcell_cut(WaveCell<Cap> &c, WaveState &s, double4 pl, uint32_t site, double far2, int lane)
+{
+    if (s.np >= Cap::P) {
+        wcell_compact_planes(c, s, lane);
+        if (s.np >= Cap::P)
+            return VOR_FULL;
+    }
+    // classify; gather the edges of the removed vertices
+    uint32_t outmask = 0; // bit b: vertex 64 b + lane is removed
+    int removed = 0;
+    for (int t0 = 0, b = 0; t0 < s.nt; t0 += 64, ++b) {
+        const int t = t0 + lane;
+        bool out = false;
+        uchar4 x = make_uchar4(0, 0, 0, 0);
+        if (t < s.nt) {
+            out = dot_d(pl, c.V[t]) > pl.w;
+            x = c.T[t];
+        }
+        uint64_t m = __ballot(out);
+        const int cnt = __popcll(m);
+        if (3 * (removed + cnt) > Cap::E)
+            return VOR_FULL;
+        if (out) {
+            const int e = 3 * (removed + (int)lane_rank(m));
+            c.ed[e] = (uint16_t)(x.x | (x.y << 8));
+            c.ed[e + 1] = (uint16_t)(x.y | (x.z << 8));
+            c.ed[e + 2] = (uint16_t)(x.z | (x.x << 8));
+            outmask |= 1u << b;
+        }
+        removed += cnt;
+    }
+    if (removed == 0)
+        return VOR_OK;
+    if (removed == s.nt)
+        return VOR_DEGENERATE; // the site's own half-space always keeps the site
+    const int ne = 3 * removed;
+    const int q = s.np++;
+    if (lane == 0) {
+        c.P[q] = pl;
+        c.nid[q] = site;
+    }
+    // compact the kept vertices (a chunk is read before it is written; the
+    // writes land below the next chunk)
+    int k = 0;
+    for (int t0 = 0, b = 0; t0 < s.nt; t0 += 64, ++b) {
+        const int t = t0 + lane;
+        const bool keep = t < s.nt && !((outmask >> b) & 1u);
+        uchar4 x = make_uchar4(0, 0, 0, 0);
+        double4 v = make_double4(0.0, 0.0, 0.0, 0.0);
+        if (keep) {
+            x = c.T[t];
+            v = c.V[t];
+        }
+        uint64_t m = __ballot(keep);
+        __syncthreads();
+        if (keep) {
+            const int d = k + (int)lane_rank(m);
+            c.T[d] = x;
+            c.V[d] = v;
+        }
+        k += __popcll(m);
+    }
+    __syncthreads(); // edges, plane q and kept vertices visible to all lanes
+    // boundary edges (u, v): their reverse belongs to a kept vertex; the new
+    // vertex (u, v, q) keeps the orientation.  A cut of a convex cell removes
+    // a disc, so the boundary is one cycle: every plane on it starts exactly
+    // one edge and ends exactly one.
+    int nb = 0;
+    for (int e0 = 0; e0 < ne; e0 += 64) {
+        const int e = e0 + lane;
+        bool bnd = false;
+        uint16_t ev = 0;
+        if (e < ne) {
+            ev = c.ed[e];
+            const uint16_t rev = (uint16_t)((ev >> 8) | ((ev & 0xff) << 8));
+            bool inner = false;
+            for (int f = 0; f < ne; ++f)
+                inner = inner || c.ed[f] == rev;
+            bnd = !inner;
+        }
+        uint64_t m = __ballot(bnd);
+        const int cnt = __popcll(m);
+        if (k + nb + cnt > Cap::T)
+            return VOR_FULL;
+        if (bnd)
+            c.T[k + nb + (int)lane_rank(m)] = make_uchar4((uint8_t)(ev & 0xff), (uint8_t)(ev >> 8), (uint8_t)q, 0);
+        nb += cnt;
+    }
+    if (nb < 3)
+        return VOR_DEGENERATE;
+    __syncthreads();
+    bool bad = false;
+    for (int a = k + lane; a < k + nb; a += 64) {
+        const uint8_t u = c.T[a].x;
+        int starts = 0, ends = 0;
+        for (int b = k; b < k + nb; ++b) {
+            const uchar4 y = c.T[b];
+            starts += y.x == u;
+            ends += y.y == u;
+        }
+        bad = bad || starts != 1 || ends != 1;
+    }
+    if (__ballot(bad))
+        return VOR_DEGENERATE;
+    for (int a = k + lane; a < k + nb; a += 64) {
+        const uchar4 x = c.T[a];
+        const double4 v = plane_vertex(c.P[x.x], c.P[x.y], c.P[x.z]);
+        bad = bad || !(v.w < 1e300); // a vertex of (nearly) parallel planes
+        c.V[a] = v;
+    }
+    if (__ballot(bad))
+        return VOR_DEGENERATE;
+    s.nt = k + nb;
+    __syncthreads();
+    wcell_radii(c, s, far2, lane);
+    return VOR_OK;
+}
+
+// max of x.v over x in [l, h] and v in [bmin, bmax], one axis
+__device__ __forceinline__ double axis_support(double l, double h, double bmin, double bmax)
+{
+    return fmax(fmax(l * bmin, l * bmax), fmax(h * bmin, h * bmax));
+}
+
+// Can a site in the box [lo, hi] (local, already widened by the grid
+// rounding margin) at a distance in [sqrt(lo2), sqrt(hi2)) cut the cell?
+template <class Cap>
+__device__ __forceinline__ bool wcell_box_may_cut(const WaveCell<Cap> &c, const WaveState &s, const double lo[3],
+                                                  const double hi[3], double lo2, double hi2)
+{
+    double mind2 = 0.0, maxd2 = 0.0;
+    for (int a = 0; a < 3; ++a) {
+        const double near = lo[a] > 0.0 ? lo[a] : (hi[a] < 0.0 ? -hi[a] : 0.0);
+        const double farc = fmax(-lo[a], hi[a]);
+        mind2 += near * near;
+        maxd2 += farc * farc;
+    }
+    if (mind2 >= hi2 || maxd2 < lo2 || mind2 >= 4.0 * s.R2)
+        return false;
+    double sb = axis_support(lo[0], hi[0], s.bmin[0], s.bmax[0]) + axis_support(lo[1], hi[1], s.bmin[1], s.bmax[1]) +
+                axis_support(lo[2], hi[2], s.bmin[2], s.bmax[2]);
+    for (int f = 0; f < s.nfar; ++f) {
+        const double4 v = c.V[c.far[f]];
+        sb = fmax(sb, fmax(lo[0] * v.x, hi[0] * v.x) + fmax(lo[1] * v.y, hi[1] * v.y) + fmax(lo[2] * v.z, hi[2] * v.z));
+    }
+    // a cut needs x.v > |x|^2 / 2 (slack for the rounding of the bound)
+    return sb >= 0.5 * mind2 * (1.0 - 1e-9);
+}
+
+// Does the plane of d (d.x <= |d|^2 / 2) cut the cell?
+template <class Cap>
+__device__ __forceinline__ bool wcell_hits(const WaveCell<Cap> &c, const WaveState &s, double dx, double dy,
+                                           double dz, double d2)
+{
+    const double w = 0.5 * d2;
+    bool hit = false;
+    for (int f = 0; f < s.nfar; ++f) {
+        const double4 v = c.V[c.far[f]];
+        hit = hit || dx * v.x + dy * v.y + dz * v.z > w;
+    }
+    if (!hit && d2 < 4.0 * s.Rn2) {
+        const double sb = fmax(dx * s.bmin[0], dx * s.bmax[0]) + fmax(dy * s.bmin[1], dy * s.bmax[1]) +
+                          fmax(dz * s.bmin[2], dz * s.bmax[2]);
+        if (sb * (1.0 + 1e-9) > w) {
+            for (int t = 0; t < s.nt; ++t) {
+                const double4 v = c.V[t];
+                hit = hit || dx * v.x + dy * v.y + dz * v.z > w;
+            }
+        }
+    }
+    return hit;
+}
+
+// Voronoi cell of site i; its m neighbours go to c.out[0..m) (unordered).
+template <class Cap>
+__device__ int wave_voronoi_cell(WaveCell<Cap> &c, uint32_t i, const float *__restrict__ points, const VorGrid &g,
+                                 const uint32_t *__restrict__ cell_start, const uint32_t *__restrict__ sorted,
+                                 int lane, int *m_out)
+{
+    const float pxf = points[3 * i], pyf = points[3 * i + 1], pzf = points[3 * i + 2];
+    const double px = pxf, py = pyf, pz = pzf;
+    WaveState s;
+    if (lane < 6) {
+        c.P[lane] = box_plane(g, px, py, pz, lane);
+        c.nid[lane] = VOR_NONE;
+    }
+    if (lane < 8) {
+        c.T[lane] = box_corner(lane);
+        c.V[lane] = box_corner_pos(g, px, py, pz, lane);
+    }
+    s.np = 6;
+    s.nt = 8;
+    __syncthreads();
+    wcell_radii(c, s, g.far2, lane);
+    const int cx = grid_coord(pxf, g.lo[0], g.h, g.g[0]);
+    const int cy = grid_coord(pyf, g.lo[1], g.h, g.g[1]);
+    const int cz = grid_coord(pzf, g.lo[2], g.h, g.g[2]);
+    const int gmax = (int)max(g.g[0], max(g.g[1], g.g[2]));
+    const double h = (double)g.h;
+    const double eps = 1e-3 * h; // grid rounding margin
+    const double diag2 = (double)(g.g[0] * g.g[0] + g.g[1] * g.g[1] + g.g[2] * g.g[2]) * h * h;
+    int status = VOR_OK;
+    double lo2 = 0.0;
+    for (double rho = 0.125 * h; status == VOR_OK; rho *= 2.0) {
+        const double hi2 = rho * rho;
+        const double hig = rho / h + 1e-3, log_ = fmax(sqrt(lo2) / h - 1e-3, 0.0);
+        const int rr = min((int)ceil(hig), gmax);
+        for (int dz = -rr; dz <= rr && status == VOR_OK; ++dz) {
+            const int z = cz + dz;
+            if (z < 0 || z >= (int)g.g[2])
+                continue;
+            for (int dy = -rr; dy <= rr && status == VOR_OK; ++dy) {
+                const int y = cy + dy;
+                RowSpan sp;
+                if (y < 0 || y >= (int)g.g[1] || !band_row(dy, dz, log_, hig, rr, cx, (int)g.g[0], sp))
+                    continue;
+                const uint32_t row = ((uint32_t)z * g.g[1] + (uint32_t)y) * g.g[0];
+                double blo[3], bhi[3];
+                blo[1] = (double)g.lo[1] + y * h - py - eps;
+                bhi[1] = blo[1] + h + 2.0 * eps;
+                blo[2] = (double)g.lo[2] + z * h - pz - eps;
+                bhi[2] = blo[2] + h + 2.0 * eps;
+                for (int part = 0; part < 2 && status == VOR_OK; ++part) {
+                    const int x0 = part ? sp.b0 : sp.a0, x1 = part ? sp.b1 : sp.a1;
+                    for (int xb = x0; xb <= x1 && status == VOR_OK; xb += 64) {
+                        // lane = grid cell of the row piece; surviving cells'
+                        // sites are packed into consecutive candidates
+                        const int x = xb + lane;
+                        uint32_t at = 0, cnt = 0;
+                        if (x <= x1) {
+                            blo[0] = (double)g.lo[0] + x * h - px - eps;
+                            bhi[0] = blo[0] + h + 2.0 * eps;
+                            if (wcell_box_may_cut(c, s, blo, bhi, lo2, hi2)) {
+                                at = cell_start[row + x];
+                                cnt = cell_start[row + x + 1] - at;
+                            }
+                        }
+                        uint32_t incl = cnt;
+                        for (int o = 1; o < 64; o <<= 1) {
+                            const uint32_t v = __shfl_up(incl, o);
+                            if (lane >= o)
+                                incl += v;
+                        }
+                        const uint32_t total = __shfl(incl, 63);
+                        if (total == 0)
+                            continue;
+                        c.run_off[lane] = incl - cnt;
+                        c.run_at[lane] = at;
+                        __syncthreads();
+                        for (uint32_t kb = 0; kb < total && status == VOR_OK; kb += 64) {
+                            const uint32_t kk = kb + (uint32_t)lane;
+                            bool cand = false;
+                            uint32_t j = 0;
+                            double ddx = 0.0, ddy = 0.0, ddz = 0.0, d2 = 0.0;
+                            if (kk < total) {
+                                int L = 0; // last lane whose run starts at or before kk
+                                for (int step = 32; step > 0; step >>= 1)
+                                    if (c.run_off[L + step] <= kk)
+                                        L += step;
+                                j = sorted[c.run_at[L] + (kk - c.run_off[L])];
+                                ddx = (double)points[3 * j] - px;
+                                ddy = (double)points[3 * j + 1] - py;
+                                ddz = (double)points[3 * j + 2] - pz;
+                                d2 = ddx * ddx + ddy * ddy + ddz * ddz;
+                                cand = j != i && d2 >= lo2 && d2 < hi2 && d2 < 4.0 * s.R2 &&
+                                       wcell_hits(c, s, ddx, ddy, ddz, d2);
+                            }
+                            uint64_t m = __ballot(cand);
+                            while (m && status == VOR_OK) {
+                                const int l = __ffsll((unsigned long long)m) - 1;
+                                m &= m - 1;
+                                const double4 pl = make_double4(__shfl(ddx, l), __shfl(ddy, l), __shfl(ddz, l),
+                                                                0.5 * __shfl(d2, l));
+                                status = wcell_cut(c, s, pl, (uint32_t)__shfl((int)j, l), g.far2, lane);
+                            }
+                        }
+                        __syncthreads(); // run_off / run_at are rewritten by the next piece
+                    }
+                }
+            }
+        }
+        if (status != VOR_OK || 4.0 * s.R2 <= hi2 || hi2 > diag2)
+            break;
+        lo2 = hi2;
+    }
+    int m = 0;
+    if (status == VOR_OK) {
+        wcell_mark_used(c, s, lane);
+        for (int q0 = 6; q0 < s.np; q0 += 64) {
+            const int q = q0 + lane;
+            const bool u = q < s.np && ((c.used[q >> 5] >> (q & 31)) & 1u);
+            uint64_t mm = __ballot(u);
+            if (m + __popcll(mm) > Cap::K) {
+                status = VOR_FULL;
+                break;
+            }
+            if (u)
+                c.out[m + (int)lane_rank(mm)] = c.nid[q];
+            m += __popcll(mm);
+        }
+        __syncthreads();
+    }
+    *m_out = status == VOR_OK ? m : 0;
+    return status;
+}
+
+// One wave per cell, cells taken in order from a work counter.  First pass
+// (LARGE false): every site, in grid order; cells that overflow the small
+// tables are queued in retry[].  Second pass (LARGE true): the queued cells;
+// a list longer than VorSmall::K goes to a slot of big_lists (big_slot[i]),
+// shorter lists to the cell's slot of lists.
+template <class Cap, bool LARGE>
+__global__ __launch_bounds__(VOR_BLOCK) __attribute__((amdgpu_waves_per_eu(3))) void voronoi_cells_kernel(
+    const float *__restrict__ points, VorGrid g, const uint32_t *__restrict__ cell_start,
+    const uint32_t *__restrict__ sorted, const uint32_t *__restrict__ cells, uint32_t ncells,
+    uint32_t *__restrict__ lists, uint32_t *__restrict__ big_lists, uint32_t big_cap, uint32_t *__restrict__ big_slot,
+    uint32_t *__restrict__ counts, uint32_t *__restrict__ retry, uint32_t *fails)
+{
+    __shared__ WaveCell<Cap> c;
+    __shared__ uint32_t pick;
+    const int lane = (int)threadIdx.x;
+    uint32_t *next = fails + (LARGE ? F_NEXT1 : F_NEXT0);
+    for (;;) {
+        if (lane == 0)
+            pick = atomicAdd(next, 1u);
+        __syncthreads();
+        const uint32_t r = pick;
+        __syncthreads();
+        if (r >= ncells)
+            break;
+        const uint32_t i = cells[r];
+        int m;
+        int status = wave_voronoi_cell<Cap>(c, i, points, g, cell_start, sorted, lane, &m);
+        uint32_t *dst = lists + (size_t)i * VorSmall::K;
+        if (LARGE && status == VOR_OK && m > VorSmall::K) {
+            if (lane == 0)
+                pick = atomicAdd(fails + F_BIG, 1u);
+            __syncthreads();
+            const uint32_t slot = pick;
+            __syncthreads();
+            if (slot < big_cap) {
+                dst = big_lists + (size_t)slot * VorLarge::K;
+                if (lane == 0)
+                    big_slot[i] = slot;
+            } else {
+                status = VOR_FULL;
+            }
+        }
+        if (status == VOR_OK) {
+            // ascending by rank (the ids are distinct)
+            for (int a = lane; a < m; a += 64) {
+                const uint32_t v = c.out[a];
+                int rank = 0;
+                for (int b = 0; b < m; ++b)
+                    rank += c.out[b] < v;
+                dst[rank] = v;
+            }
+        } else {
+            m = 0;
+            if (lane == 0) {
+                if (!LARGE && status == VOR_FULL)
+                    retry[atomicAdd(fails + F_RETRY, 1u)] = i; // at most n entries
+                else
+                    atomicAdd(fails + (status == VOR_FULL ? F_FULL : F_DEGENERATE), 1u);
+            }
+        }
+        if (lane == 0)
+            counts[i] = (uint32_t)m;
+        __syncthreads();
+    }
+}
+
+__global__ void voronoi_grid_keys_kernel(const float *__restrict__ points, uint32_t n, VorGrid g,
+                                         uint32_t *__restrict__ keys, uint32_t *__restrict__ vals,
+                                         uint32_t *__restrict__ cell_count)
+{
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n)
+        return;
+    int x = grid_coord(points[3 * i], g.lo[0], g.h, g.g[0]);
+    int y = grid_coord(points[3 * i + 1], g.lo[1], g.h, g.g[1]);
+    int z = grid_coord(points[3 * i + 2], g.lo[2], g.h, g.g[2]);
+    uint32_t cell = ((uint32_t)z * g.g[1] + (uint32_t)y) * g.g[0] + (uint32_t)x;
+    keys[i] = cell;
+    vals[i] = i;
+    atomicAdd(cell_count + cell, 1u);
+}
+
+__global__ void voronoi_copy_kernel(uint32_t n, const uint32_t *__restrict__ offsets,
+                                    const uint32_t *__restrict__ lists, const uint32_t *__restrict__ big_lists,
+                                    const uint32_t *__restrict__ big_slot, uint32_t *__restrict__ adjacency)
+{
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n)
+        return;
+    uint32_t b = offsets[i], m = offsets[i + 1] - b;
+    uint32_t slot = big_slot[i];
+    const uint32_t *src = slot == VOR_NONE ? lists + (size_t)i * VorSmall::K : big_lists + (size_t)slot * VorLarge::K;
+    for (uint32_t k = 0; k < m; ++k)
+        adjacency[b + k] = src[k];
+}
+
+__global__ void fill_u32_kernel(uint32_t *p, size_t n, uint32_t v)
+{
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n)
+        p[i] = v;
+}
+
+// workspace layout (u32 words)
+struct VorWs {
+    uint32_t *lists, *counts, *keys, *vals, *cell_start, *sort_ws, *scan_ws, *fails, *bbox_ws, *retry, *big_lists,
+        *big_slot;
+    float *bbox;
+};
+
+static uint32_t grid_cells_for(uint32_t n) { return n < 8 ? 8 : n; }
+// cells with more than VorSmall::K neighbours
+static uint32_t big_cap_for(uint32_t n) { return std::max<uint32_t>(256, n / 64); }
+
+static size_t ws_words(uint32_t n, VorWs *w, uint32_t *base)
+{
+    size_t cells = grid_cells_for(n) + 2 * 512 * 512; // slack for non-cubic boxes
+    size_t off = 0;
+    uint32_t *dummy;
+    auto take = [&](uint32_t **p, size_t words) {
+        *(w ? p : &dummy) = base + off;
+        off += (words + 63) & ~(size_t)63;
+    };
+    VorWs local{};
+    VorWs &x = w ? *w : local;
+    take(&x.lists, (size_t)n * VorSmall::K);
+    take(&x.counts, (size_t)n + 1);
+    take(&x.keys, n);
+    take(&x.vals, n);
+    take(&x.cell_start, cells + 1);
+    take(&x.sort_ws, radix_sort_workspace_words(n));
+    take(&x.scan_ws, scan_workspace_words((uint32_t)std::max<size_t>(cells + 1, (size_t)n + 1)));
+    take(&x.fails, F_WORDS);
+    take(&x.bbox_ws, 6);
+    uint32_t *bb;
+    take(&bb, 6);
+    x.bbox = reinterpret_cast<float *>(bb);
+    take(&x.retry, n);
+    take(&x.big_lists, (size_t)big_cap_for(n) * VorLarge::K);
+    take(&x.big_slot, n);
+    return off;
+}
+
+// enough waves to fill the chip (the LDS of a cell bounds them per CU)
+static uint32_t wave_blocks(uint32_t ncells) { return std::min<uint32_t>(ncells, 256u * 16u); }
+
+} // namespace vt
+
+using namespace vt;
+
+extern "C" size_t vt_voronoi_workspace_size(uint32_t num_points)
+{
+    return ws_words(num_points, nullptr, nullptr) * sizeof(uint32_t);
+}
+
+extern "C" int vt_voronoi_build(const float *points, uint32_t num_points, uint32_t *offsets,
+                                uint32_t *num_adjacency, void *workspace, vt_stream_t stream)
+{
+    clear_error();
+    VT_REQUIRE(points && offsets && num_adjacency && workspace, "null pointer argument");
+    VT_REQUIRE(num_points >= 2, "at least 2 sites are needed, got %u", num_points);
+    VT_REQUIRE(num_points <= (1u << 26), "too many sites (%u)", num_points);
+    hipStream_t s = as_stream(stream);
+    VorWs w{};
+    ws_words(num_points, &w, reinterpret_cast<uint32_t *>(workspace));
+    uint32_t n = num_points;
+    // bounding box -> grid of about one site per cell
+    int rc = bbox3(points, n, w.bbox, w.bbox_ws, s);
+    if (rc)
+        return rc;
+    float bb[6];
+    VT_HIP_CHECK(hipMemcpyAsync(bb, w.bbox, sizeof(bb), hipMemcpyDeviceToHost, s));
+    VT_HIP_CHECK(hipStreamSynchronize(s));
+    VorGrid g{};
+    double ext[3], vol = 1.0, maxext = 0.0;
+    for (int a = 0; a < 3; ++a) {
+        ext[a] = std::max((double)bb[3 + a] - (double)bb[a], 1e-6);
+        vol *= ext[a];
+        maxext = std::max(maxext, ext[a]);
+    }
+    double h = std::cbrt(vol / (double)n);
+    uint64_t cells = 1;
+    for (int a = 0; a < 3; ++a) {
+        g.g[a] = (uint32_t)std::max(1.0, std::min(512.0, std::ceil(ext[a] / h)));
+        cells *= g.g[a];
+    }
+    for (int a = 0; a < 3; ++a) {
+        g.lo[a] = bb[a];
+        g.box_lo[a] = (double)bb[a] - 1e6 * maxext;
+        g.box_hi[a] = (double)bb[3 + a] + 1e6 * maxext;
+    }
+    // vertices of bisector planes of sites in general position stay well
+    // inside 10^3 extents; beyond that a vertex lies on the box
+    g.far2 = (1e3 * maxext) * (1e3 * maxext);
+    g.h = (float)std::max({ext[0] / g.g[0], ext[1] / g.g[1], ext[2] / g.g[2]}) * 1.0000001f;
+    VT_REQUIRE(cells <= (uint64_t)grid_cells_for(n) + 2ull * 512 * 512, "grid too large");
+    uint32_t nc = (uint32_t)cells;
+    // bucket the sites by grid cell: counts -> starts; stable sort of (cell, site)
+    fill_u32_kernel<<<(nc + 1 + 255) / 256, 256, 0, s>>>(w.cell_start, (size_t)nc + 1, 0u);
+    fill_u32_kernel<<<1, 64, 0, s>>>(w.fails, F_WORDS, 0u);
+    fill_u32_kernel<<<(n + 255) / 256, 256, 0, s>>>(w.big_slot, n, VOR_NONE);
+    voronoi_grid_keys_kernel<<<(n + 255) / 256, 256, 0, s>>>(points, n, g, w.keys, w.vals, w.cell_start);
+    VT_LAUNCH_CHECK("voronoi_grid_keys_kernel");
+    rc = exclusive_scan_u32(w.cell_start, w.cell_start, nc + 1, w.scan_ws, s);
+    if (rc)
+        return rc;
+    int bits = 1;
+    while (bits < 32 && (1ull << bits) < nc)
+        ++bits;
+    rc = radix_sort_pairs(w.keys, w.vals, n, bits, w.sort_ws, s);
+    if (rc)
+        return rc;
+    const uint32_t bcap = big_cap_for(n);
+    voronoi_cells_kernel<VorSmall, false><<<wave_blocks(n), VOR_BLOCK, 0, s>>>(
+        points, g, w.cell_start, w.vals, w.vals, n, w.lists, w.big_lists, bcap, w.big_slot, w.counts, w.retry, w.fails);
+    VT_LAUNCH_CHECK("voronoi_cells_kernel (small)");
+    uint32_t f[F_WORDS];
+    VT_HIP_CHECK(hipMemcpyAsync(f, w.fails, sizeof(f), hipMemcpyDeviceToHost, s));
+    VT_HIP_CHECK(hipStreamSynchronize(s));
+    if (f[F_RETRY]) {
+        voronoi_cells_kernel<VorLarge, true><<<wave_blocks(f[F_RETRY]), VOR_BLOCK, 0, s>>>(
+            points, g, w.cell_start, w.vals, w.retry, f[F_RETRY], w.lists, w.big_lists, bcap, w.big_slot, w.counts,
+            w.retry, w.fails);
+        VT_LAUNCH_CHECK("voronoi_cells_kernel (large)");
+    }
+    rc = exclusive_scan_u32(w.counts, offsets, n + 1, w.scan_ws, s);
+    if (rc)
+        return rc;
+    uint32_t tail[3];
+    VT_HIP_CHECK(hipMemcpyAsync(tail, offsets + n, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+    VT_HIP_CHECK(hipMemcpyAsync(tail + 1, w.fails, 2 * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+    VT_HIP_CHECK(hipStreamSynchronize(s));
+    if (tail[1] || tail[2]) {
+        set_error("Voronoi build failed for %u cells over capacity (%d planes, %d vertices, %d neighbours, %u long "
+                  "lists) and %u degenerate cuts",
+                  tail[1], VorLarge::P, VorLarge::T, VorLarge::K, bcap, tail[2]);
+        return VT_ERR_INVALID;
+    }
+    *num_adjacency = tail[0];
+    return VT_OK;
+}
+
+extern "C" int vt_voronoi_adjacency(uint32_t num_points, const uint32_t *offsets, uint32_t *adjacency,
+                                    const void *workspace, vt_stream_t stream)
+{
+    clear_error();
+    VT_REQUIRE(offsets && adjacency && workspace, "null pointer argument");
+    hipStream_t s = as_stream(stream);
+    VorWs w{};
+    ws_words(num_points, &w, reinterpret_cast<uint32_t *>(const_cast<void *>(workspace)));
+    voronoi_copy_kernel<<<(num_points + 255) / 256, 256, 0, s>>>(num_points, offsets, w.lists, w.big_lists,
+                                                                 w.big_slot, adjacency);
+    VT_LAUNCH_CHECK("voronoi_copy_kernel");
+    return VT_OK;
+}

@@ -13,7 +13,7 @@ from __future__ import annotations
 import torch
 import torch.nn.functional as F
 
-from . import _C
+from . import _C, _lib
 
 NNBVH = _C.NNBVH
 nearest_neighbor_bvh = _C.nearest_neighbor_bvh
@@ -118,20 +118,30 @@ def trace_octmap_infer_q8(points, diffuse_q8, specular_q8, density, adjacency, o
 
 def build_voronoi_adjacency(points: torch.Tensor, *, debug: bool = False, initial_guesses=None,
                             initial_guesses_offsets=None, chunk_padding: int = 32):
-    """cuda/__init__.py:16-46: uint32 CSR (adjacency padded by
-    ``chunk_padding``, offsets) and a status tensor.  The Voronoi adjacency
-    comes from the host Delaunay triangulation (scipy/qhull) of the sites;
-    Paragram (the reference's GPU builder) is not available."""
+    """cuda/__init__.py:16-46: uint32 CSR (adjacency padded by ``chunk_padding``
+    zeros, offsets) and a status tensor, built on the GPU by vt_voronoi_build
+    (the reference calls Paragram).  Each neighbour list is ascending; the
+    sets are the Delaunay neighbours of the sites.  ``initial_guesses`` are
+    accepted for signature compatibility and not needed."""
     del debug, initial_guesses, initial_guesses_offsets
-    from .scene import delaunay_csr
+    import ctypes
 
-    pts = points.detach().float().cpu().numpy()
-    adj, off = delaunay_csr(pts, pad=0)
-    dev = points.device
-    adjacency = torch.from_numpy(adj.astype("int64"))
-    adjacency = F.pad(adjacency, (0, chunk_padding), mode="constant", value=0)
-    return (adjacency.to(device=dev, dtype=torch.uint32), torch.from_numpy(off).to(device=dev),
-            torch.zeros(1, dtype=torch.int32, device=dev))
+    pts = points.detach().to(torch.float32).contiguous()
+    dev = pts.device
+    if dev.type != "cuda":
+        raise RuntimeError("build_voronoi_adjacency needs the sites on the GPU")
+    n = pts.shape[0]
+    lib = _lib.load()
+    ws = torch.empty(lib.vt_voronoi_workspace_size(n), dtype=torch.uint8, device=dev)
+    offsets = torch.empty(n + 1, dtype=torch.uint32, device=dev)
+    m = ctypes.c_uint32(0)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    with torch.cuda.device(dev):
+        _lib.call("vt_voronoi_build", pts.data_ptr(), n, offsets.data_ptr(), ctypes.addressof(m), ws.data_ptr(),
+                  stream)
+        adjacency = torch.zeros(m.value + chunk_padding, dtype=torch.uint32, device=dev)
+        _lib.call("vt_voronoi_adjacency", n, offsets.data_ptr(), adjacency.data_ptr(), ws.data_ptr(), stream)
+    return adjacency, offsets, torch.zeros(1, dtype=torch.int32, device=dev)
 
 
 __all__ = [
