@@ -57,7 +57,7 @@ struct VorGrid {
     float h;       // cell side
     uint32_t g[3]; // cells per axis
     double box_lo[3], box_hi[3];
-    double far2;   // squared local distance beyond which a vertex counts as a box vertex
+    double far2;   // squared local distance beyond which a vertex counts as far
 };
 
 enum { VOR_OK = 0, VOR_FULL = 1, VOR_DEGENERATE = 2 };
@@ -156,12 +156,15 @@ template <class Cap> struct WaveCell {
     double4 V[Cap::T]; // w = |v|^2
     uint32_t nid[Cap::P];
     uchar4 T[Cap::T];
-    uint16_t ed[Cap::E];  // directed edges (u | v << 8) of the removed vertices
-    uint16_t far[Cap::T]; // indices of the vertices beyond far2
+    alignas(8) uint16_t ed[Cap::E + 4]; // directed edges (u | v << 8) of the removed vertices
+    uint16_t far[Cap::T];     // indices of the vertices beyond far2
+    uint16_t slabfar[Cap::T]; // ... whose ball meets the current slab of grid cells
+    uint16_t rowfar[Cap::T];  // ... and the current row
     uint32_t out[Cap::K];
     uint32_t run_off[64]; // candidates of one row piece: first candidate of lane l's grid cell
     uint32_t run_at[64];  // ... and where its sites start in the sorted order
     uint32_t used[8];
+    uint32_t starts[Cap::P], ends[Cap::P]; // boundary edges per plane during a cut (0 otherwise)
     uint8_t remap[Cap::P];
     int np_shared;
 };
@@ -170,11 +173,9 @@ __device__ __forceinline__ uint32_t lane_rank(uint64_t m)
 {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
-// maximum over the wave, returned in scalar registers
-__device__ __forceinline__ double wave_max(double x)
+// a value equal in every lane, moved to scalar registers
+__device__ __forceinline__ double wave_uniform(double x)
 {
-    for (int o = 32; o > 0; o >>= 1)
-        x = fmax(x, __shfl_xor(x, o));
     const uint64_t b = (uint64_t)__double_as_longlong(x);
     const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
     const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
@@ -184,6 +185,7 @@ __device__ __forceinline__ double wave_max(double x)
 // Wave-uniform scalars of the cell (every lane holds the same values).
 struct WaveState {
     int np, nt, nfar;
+    int gen;                 // effective cuts so far
     double R2, Rn2;          // squared radius of all vertices, of the near ones
     double bmin[3], bmax[3]; // bounding box of the near vertices (0 when none)
 };
@@ -216,12 +218,19 @@ template <class Cap> __device__ void wcell_radii(WaveCell<Cap> &c, WaveState &s,
             c.far[nf + lane_rank(m)] = (uint16_t)t;
         nf += __popcll(m);
     }
-    s.R2 = wave_max(r);
-    s.Rn2 = wave_max(rn);
+    // eight maxima over the wave, exchanged together
+    double red[8] = {r, rn, -mn[0], -mn[1], -mn[2], mx[0], mx[1], mx[2]};
+    for (int o = 32; o > 0; o >>= 1) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+            red[q] = fmax(red[q], __shfl_xor(red[q], o));
+    }
+    s.R2 = wave_uniform(red[0]);
+    s.Rn2 = wave_uniform(red[1]);
     const bool any_near = nf < s.nt;
     for (int a = 0; a < 3; ++a) {
-        s.bmin[a] = any_near ? -wave_max(-mn[a]) : 0.0;
-        s.bmax[a] = any_near ? wave_max(mx[a]) : 0.0;
+        s.bmin[a] = any_near ? -wave_uniform(red[2 + a]) : 0.0;
+        s.bmax[a] = any_near ? wave_uniform(red[5 + a]) : 0.0;
     }
     s.nfar = nf;
     __syncthreads();
@@ -313,6 +322,8 @@ __device__ int wcell_cut(WaveCell<Cap> &c, WaveState &s, double4 pl, uint32_t si
         c.P[q] = pl;
         c.nid[q] = site;
     }
+    if (lane < 4)
+        c.ed[ne + lane] = 0xffff; // plane ids are below 255
     // compact the kept vertices (a chunk is read before it is written; the
     // writes land below the next chunk)
     int k = 0;
@@ -346,11 +357,14 @@ __device__ int wcell_cut(WaveCell<Cap> &c, WaveState &s, double4 pl, uint32_t si
         uint16_t ev = 0;
         if (e < ne) {
             ev = c.ed[e];
-            const uint16_t rev = (uint16_t)((ev >> 8) | ((ev & 0xff) << 8));
-            bool inner = false;
-            for (int f = 0; f < ne; ++f)
-                inner = inner || c.ed[f] == rev;
-            bnd = !inner;
+            const uint64_t rev = (uint64_t)((ev >> 8) | ((ev & 0xff) << 8)) * 0x0001000100010001ull;
+            const uint64_t *e4 = reinterpret_cast<const uint64_t *>(c.ed);
+            uint64_t hit = 0;
+            for (int f = 0; f < ne; f += 4) {
+                const uint64_t x = e4[f >> 2] ^ rev; // a zero field: the reverse edge
+                hit |= (x - 0x0001000100010001ull) & ~x & 0x8000800080008000ull;
+            }
+            bnd = hit == 0;
         }
         uint64_t m = __ballot(bnd);
         const int cnt = __popcll(m);
@@ -363,16 +377,22 @@ __device__ int wcell_cut(WaveCell<Cap> &c, WaveState &s, double4 pl, uint32_t si
     if (nb < 3)
         return VOR_DEGENERATE;
     __syncthreads();
+    for (int a = k + lane; a < k + nb; a += 64) {
+        const uchar4 x = c.T[a];
+        atomicAdd(&c.starts[x.x], 1u);
+        atomicAdd(&c.ends[x.y], 1u);
+    }
+    __syncthreads();
     bool bad = false;
     for (int a = k + lane; a < k + nb; a += 64) {
         const uint8_t u = c.T[a].x;
-        int starts = 0, ends = 0;
-        for (int b = k; b < k + nb; ++b) {
-            const uchar4 y = c.T[b];
-            starts += y.x == u;
-            ends += y.y == u;
-        }
-        bad = bad || starts != 1 || ends != 1;
+        bad = bad || c.starts[u] != 1u || c.ends[u] != 1u;
+    }
+    __syncthreads();
+    for (int a = k + lane; a < k + nb; a += 64) {
+        const uchar4 x = c.T[a];
+        c.starts[x.x] = 0u;
+        c.ends[x.y] = 0u;
     }
     if (__ballot(bad))
         return VOR_DEGENERATE;
@@ -385,6 +405,7 @@ __device__ int wcell_cut(WaveCell<Cap> &c, WaveState &s, double4 pl, uint32_t si
     if (__ballot(bad))
         return VOR_DEGENERATE;
     s.nt = k + nb;
+    ++s.gen;
     __syncthreads();
     wcell_radii(c, s, far2, lane);
     return VOR_OK;
@@ -396,49 +417,93 @@ __device__ __forceinline__ double axis_support(double l, double h, double bmin, 
     return fmax(fmax(l * bmin, l * bmax), fmax(h * bmin, h * bmax));
 }
 
-// Can a site in the box [lo, hi] (local, already widened by the grid
-// rounding margin) at a distance in [sqrt(lo2), sqrt(hi2)) cut the cell?
+// A box of space (local coordinates, widened by the grid rounding margin):
+// the distances of its points from the site.
+struct VorBox {
+    double lo[3], hi[3];
+    double mind2, maxd2;
+    __device__ void finish()
+    {
+        mind2 = maxd2 = 0.0;
+        for (int a = 0; a < 3; ++a) {
+            const double near = lo[a] > 0.0 ? lo[a] : (hi[a] < 0.0 ? -hi[a] : 0.0);
+            const double farc = fmax(-lo[a], hi[a]);
+            mind2 += near * near;
+            maxd2 += farc * farc;
+        }
+    }
+    // Could a site of the band [lo2, hi2) in the box cut the cell at all?
+    __device__ bool in_reach(const WaveState &s, double lo2, double hi2) const
+    {
+        return mind2 < hi2 && maxd2 >= lo2 && mind2 < 4.0 * s.R2;
+    }
+    // Could a site in the box cut a near vertex?  A cut of v needs
+    // x.v > |x|^2 / 2; max x.v is bounded through the bounding box of the
+    // near vertices (slack for the rounding of the bound).
+    __device__ bool near_may_cut(const WaveState &s) const
+    {
+        if (s.nfar >= s.nt)
+            return false;
+        const double sb = axis_support(lo[0], hi[0], s.bmin[0], s.bmax[0]) +
+                          axis_support(lo[1], hi[1], s.bmin[1], s.bmax[1]) +
+                          axis_support(lo[2], hi[2], s.bmin[2], s.bmax[2]);
+        return sb >= 0.5 * mind2 * (1.0 - 1e-9);
+    }
+    // Could a site in the box cut vertex v: does the box meet the ball
+    // B(v, |v|) (the sites closer to v than the cell's own site)?
+    __device__ bool meets_ball(double4 v) const
+    {
+        const double ax = fmax(fmax(lo[0] - v.x, v.x - hi[0]), 0.0);
+        const double ay = fmax(fmax(lo[1] - v.y, v.y - hi[1]), 0.0);
+        const double az = fmax(fmax(lo[2] - v.z, v.z - hi[2]), 0.0);
+        return ax * ax + ay * ay + az * az < v.w * (1.0 + 1e-9);
+    }
+};
+
+// The far vertices of src[0..nsrc) whose ball meets the box go to dst
+// (spread over the lanes); returns their number.  The caller synchronises
+// before (dst may still be read) and after.
 template <class Cap>
-__device__ __forceinline__ bool wcell_box_may_cut(const WaveCell<Cap> &c, const WaveState &s, const double lo[3],
-                                                  const double hi[3], double lo2, double hi2)
+__device__ int collect_far(const WaveCell<Cap> &c, const uint16_t *src, int nsrc, uint16_t *dst, const VorBox &b,
+                           int lane)
 {
-    double mind2 = 0.0, maxd2 = 0.0;
-    for (int a = 0; a < 3; ++a) {
-        const double near = lo[a] > 0.0 ? lo[a] : (hi[a] < 0.0 ? -hi[a] : 0.0);
-        const double farc = fmax(-lo[a], hi[a]);
-        mind2 += near * near;
-        maxd2 += farc * farc;
+    int n = 0;
+    for (int f0 = 0; f0 < nsrc; f0 += 64) {
+        const int f = f0 + lane;
+        bool m = false;
+        uint16_t id = 0;
+        if (f < nsrc) {
+            id = src[f];
+            m = b.meets_ball(c.V[id]);
+        }
+        const uint64_t bm = __ballot(m);
+        if (m)
+            dst[n + (int)lane_rank(bm)] = id;
+        n += __popcll(bm);
     }
-    if (mind2 >= hi2 || maxd2 < lo2 || mind2 >= 4.0 * s.R2)
-        return false;
-    double sb = axis_support(lo[0], hi[0], s.bmin[0], s.bmax[0]) + axis_support(lo[1], hi[1], s.bmin[1], s.bmax[1]) +
-                axis_support(lo[2], hi[2], s.bmin[2], s.bmax[2]);
-    for (int f = 0; f < s.nfar; ++f) {
-        const double4 v = c.V[c.far[f]];
-        sb = fmax(sb, fmax(lo[0] * v.x, hi[0] * v.x) + fmax(lo[1] * v.y, hi[1] * v.y) + fmax(lo[2] * v.z, hi[2] * v.z));
-    }
-    // a cut needs x.v > |x|^2 / 2 (slack for the rounding of the bound)
-    return sb >= 0.5 * mind2 * (1.0 - 1e-9);
+    return n;
 }
 
-// Does the plane of d (d.x <= |d|^2 / 2) cut the cell?
+// Does the plane of d (d.x <= |d|^2 / 2) cut the cell?  Far vertices are
+// those of the list (the ones the site's row can reach).
 template <class Cap>
-__device__ __forceinline__ bool wcell_hits(const WaveCell<Cap> &c, const WaveState &s, double dx, double dy,
-                                           double dz, double d2)
+__device__ __forceinline__ bool wcell_hits(const WaveCell<Cap> &c, const WaveState &s, const uint16_t *far,
+                                           int nfar, double dx, double dy, double dz, double d2)
 {
     const double w = 0.5 * d2;
     bool hit = false;
-    for (int f = 0; f < s.nfar; ++f) {
-        const double4 v = c.V[c.far[f]];
-        hit = hit || dx * v.x + dy * v.y + dz * v.z > w;
+    for (int f = 0; f < nfar; ++f) {
+        const double4 v = c.V[far[f]];
+        hit |= dx * v.x + dy * v.y + dz * v.z > w;
     }
     if (!hit && d2 < 4.0 * s.Rn2) {
         const double sb = fmax(dx * s.bmin[0], dx * s.bmax[0]) + fmax(dy * s.bmin[1], dy * s.bmax[1]) +
                           fmax(dz * s.bmin[2], dz * s.bmax[2]);
         if (sb * (1.0 + 1e-9) > w) {
+#pragma unroll 4
             for (int t = 0; t < s.nt; ++t) {
                 const double4 v = c.V[t];
-                hit = hit || dx * v.x + dy * v.y + dz * v.z > w;
+                hit |= dx * v.x + dy * v.y + dz * v.z > w;
             }
         }
     }
@@ -462,8 +527,11 @@ __device__ int wave_voronoi_cell(WaveCell<Cap> &c, uint32_t i, const float *__re
         c.T[lane] = box_corner(lane);
         c.V[lane] = box_corner_pos(g, px, py, pz, lane);
     }
+    for (int q = lane; q < Cap::P; q += 64)
+        c.starts[q] = c.ends[q] = 0u;
     s.np = 6;
     s.nt = 8;
+    s.gen = 0;
     __syncthreads();
     wcell_radii(c, s, g.far2, lane);
     const int cx = grid_coord(pxf, g.lo[0], g.h, g.g[0]);
@@ -473,38 +541,83 @@ __device__ int wave_voronoi_cell(WaveCell<Cap> &c, uint32_t i, const float *__re
     const double h = (double)g.h;
     const double eps = 1e-3 * h; // grid rounding margin
     const double diag2 = (double)(g.g[0] * g.g[0] + g.g[1] * g.g[1] + g.g[2] * g.g[2]) * h * h;
+    // local box of the grid cells [x0, x1] x [y0, y1] x [z0, z1]
+    auto cells_box = [&](int x0, int x1, int y0, int y1, int z0, int z1) {
+        VorBox b;
+        b.lo[0] = (double)g.lo[0] + x0 * h - px - eps;
+        b.hi[0] = (double)g.lo[0] + (x1 + 1) * h - px + eps;
+        b.lo[1] = (double)g.lo[1] + y0 * h - py - eps;
+        b.hi[1] = (double)g.lo[1] + (y1 + 1) * h - py + eps;
+        b.lo[2] = (double)g.lo[2] + z0 * h - pz - eps;
+        b.hi[2] = (double)g.lo[2] + (z1 + 1) * h - pz + eps;
+        b.finish();
+        return b;
+    };
     int status = VOR_OK;
     double lo2 = 0.0;
     for (double rho = 0.125 * h; status == VOR_OK; rho *= 2.0) {
         const double hi2 = rho * rho;
         const double hig = rho / h + 1e-3, log_ = fmax(sqrt(lo2) / h - 1e-3, 0.0);
         const int rr = min((int)ceil(hig), gmax);
+        const int gx0 = max(cx - rr, 0), gx1 = min(cx + rr, (int)g.g[0] - 1);
+        const int gy0 = max(cy - rr, 0), gy1 = min(cy + rr, (int)g.g[1] - 1);
         for (int dz = -rr; dz <= rr && status == VOR_OK; ++dz) {
             const int z = cz + dz;
             if (z < 0 || z >= (int)g.g[2])
                 continue;
+            // the slab of the band at this z: its far vertices
+            const VorBox slab = cells_box(gx0, gx1, gy0, gy1, z, z);
+            if (!slab.in_reach(s, lo2, hi2))
+                continue;
+            int nsf = 0, nrf = 0;
+            auto refresh_slab = [&]() {
+                __syncthreads();
+                nsf = collect_far(c, c.far, s.nfar, c.slabfar, slab, lane);
+                __syncthreads();
+            };
+            refresh_slab();
+            if (nsf == 0 && !slab.near_may_cut(s))
+                continue;
+            int lgen = s.gen; // cut generation the lists belong to
             for (int dy = -rr; dy <= rr && status == VOR_OK; ++dy) {
                 const int y = cy + dy;
                 RowSpan sp;
                 if (y < 0 || y >= (int)g.g[1] || !band_row(dy, dz, log_, hig, rr, cx, (int)g.g[0], sp))
                     continue;
+                const int rx0 = sp.a0 <= sp.a1 ? sp.a0 : sp.b0, rx1 = sp.b0 <= sp.b1 ? sp.b1 : sp.a1;
+                if (rx0 > rx1)
+                    continue;
+                const VorBox rowb = cells_box(rx0, rx1, y, y, z, z);
+                if (!rowb.in_reach(s, lo2, hi2))
+                    continue;
+                // after a cut the vertex indices of the lists are stale
+                auto refresh_row = [&]() {
+                    if (lgen != s.gen) {
+                        refresh_slab();
+                        lgen = s.gen;
+                    }
+                    nrf = collect_far(c, c.slabfar, nsf, c.rowfar, rowb, lane);
+                    __syncthreads();
+                };
+                refresh_row();
+                if (nrf == 0 && !rowb.near_may_cut(s))
+                    continue;
                 const uint32_t row = ((uint32_t)z * g.g[1] + (uint32_t)y) * g.g[0];
-                double blo[3], bhi[3];
-                blo[1] = (double)g.lo[1] + y * h - py - eps;
-                bhi[1] = blo[1] + h + 2.0 * eps;
-                blo[2] = (double)g.lo[2] + z * h - pz - eps;
-                bhi[2] = blo[2] + h + 2.0 * eps;
                 for (int part = 0; part < 2 && status == VOR_OK; ++part) {
                     const int x0 = part ? sp.b0 : sp.a0, x1 = part ? sp.b1 : sp.a1;
                     for (int xb = x0; xb <= x1 && status == VOR_OK; xb += 64) {
+                        if (lgen != s.gen)
+                            refresh_row();
                         // lane = grid cell of the row piece; surviving cells'
                         // sites are packed into consecutive candidates
                         const int x = xb + lane;
                         uint32_t at = 0, cnt = 0;
                         if (x <= x1) {
-                            blo[0] = (double)g.lo[0] + x * h - px - eps;
-                            bhi[0] = blo[0] + h + 2.0 * eps;
-                            if (wcell_box_may_cut(c, s, blo, bhi, lo2, hi2)) {
+                            const VorBox cb = cells_box(x, x, y, y, z, z);
+                            bool may = cb.in_reach(s, lo2, hi2) && cb.near_may_cut(s);
+                            for (int f = 0; f < nrf && !may; ++f)
+                                may = cb.meets_ball(c.V[c.rowfar[f]]);
+                            if (may && cb.in_reach(s, lo2, hi2)) {
                                 at = cell_start[row + x];
                                 cnt = cell_start[row + x + 1] - at;
                             }
@@ -522,6 +635,8 @@ __device__ int wave_voronoi_cell(WaveCell<Cap> &c, uint32_t i, const float *__re
                         c.run_at[lane] = at;
                         __syncthreads();
                         for (uint32_t kb = 0; kb < total && status == VOR_OK; kb += 64) {
+                            if (lgen != s.gen)
+                                refresh_row();
                             const uint32_t kk = kb + (uint32_t)lane;
                             bool cand = false;
                             uint32_t j = 0;
@@ -537,7 +652,7 @@ __device__ int wave_voronoi_cell(WaveCell<Cap> &c, uint32_t i, const float *__re
                                 ddz = (double)points[3 * j + 2] - pz;
                                 d2 = ddx * ddx + ddy * ddy + ddz * ddz;
                                 cand = j != i && d2 >= lo2 && d2 < hi2 && d2 < 4.0 * s.R2 &&
-                                       wcell_hits(c, s, ddx, ddy, ddz, d2);
+                                       wcell_hits(c, s, c.rowfar, nrf, ddx, ddy, ddz, d2);
                             }
                             uint64_t m = __ballot(cand);
                             while (m && status == VOR_OK) {
@@ -584,7 +699,7 @@ __device__ int wave_voronoi_cell(WaveCell<Cap> &c, uint32_t i, const float *__re
 // a list longer than VorSmall::K goes to a slot of big_lists (big_slot[i]),
 // shorter lists to the cell's slot of lists.
 template <class Cap, bool LARGE>
-__global__ __launch_bounds__(VOR_BLOCK) __attribute__((amdgpu_waves_per_eu(3))) void voronoi_cells_kernel(
+__global__ __launch_bounds__(VOR_BLOCK) __attribute__((amdgpu_waves_per_eu(LARGE ? 1 : 3))) void voronoi_cells_kernel(
     const float *__restrict__ points, VorGrid g, const uint32_t *__restrict__ cell_start,
     const uint32_t *__restrict__ sorted, const uint32_t *__restrict__ cells, uint32_t ncells,
     uint32_t *__restrict__ lists, uint32_t *__restrict__ big_lists, uint32_t big_cap, uint32_t *__restrict__ big_slot,
@@ -769,10 +884,11 @@ extern "C" int vt_voronoi_build(const float *points, uint32_t num_points, uint32
         g.box_lo[a] = (double)bb[a] - 1e6 * maxext;
         g.box_hi[a] = (double)bb[3 + a] + 1e6 * maxext;
     }
-    // vertices of bisector planes of sites in general position stay well
-    // inside 10^3 extents; beyond that a vertex lies on the box
-    g.far2 = (1e3 * maxext) * (1e3 * maxext);
     g.h = (float)std::max({ext[0] / g.g[0], ext[1] / g.g[1], ext[2] / g.g[2]}) * 1.0000001f;
+    // vertices farther than 4 grid cells (box vertices, the long cells of
+    // convex-hull sites) are tested one by one rather than through the
+    // bounding box of the others
+    g.far2 = 16.0 * (double)g.h * (double)g.h;
     VT_REQUIRE(cells <= (uint64_t)grid_cells_for(n) + 2ull * 512 * 512, "grid too large");
     uint32_t nc = (uint32_t)cells;
     // bucket the sites by grid cell: counts -> starts; stable sort of (cell, site)
