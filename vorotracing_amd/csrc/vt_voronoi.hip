@@ -43,14 +43,16 @@ constexpr uint32_t VOR_NONE = 0xffffffffu;
 constexpr int VOR_BLOCK = 64; // one wave
 
 // Per-cell capacities.  Plane ids are bytes, so P <= 255.
-template <int P_, int T_, int E_, int K_> struct VorCap {
-    static constexpr int P = P_;  // planes (6 box + bisectors)
-    static constexpr int T = T_;  // vertices
-    static constexpr int E = E_;  // directed edges of the region removed by one cut
-    static constexpr int K = K_;  // neighbours in the output
+template <int P_, int T_, int E_> struct VorCap {
+    static constexpr int P = P_; // planes (6 box + bisectors), also bounds the neighbours
+    static constexpr int T = T_; // vertices
+    static constexpr int E = E_; // directed edges of the region removed by one cut
 };
-using VorSmall = VorCap<96, 192, 96, 64>;
-using VorLarge = VorCap<255, 510, 384, 192>;
+using VorSmall = VorCap<96, 192, 96>;
+using VorLarge = VorCap<255, 510, 384>;
+// Neighbour lists: LIST_K entries per site; longer lists in slots of BIG_K.
+constexpr int LIST_K = 64;
+constexpr int BIG_K = VorLarge::P;
 
 struct VorGrid {
     float lo[3];
@@ -160,7 +162,7 @@ template <class Cap> struct WaveCell {
     uint16_t far[Cap::T];     // indices of the vertices beyond far2
     uint16_t slabfar[Cap::T]; // ... whose ball meets the current slab of grid cells
     uint16_t rowfar[Cap::T];  // ... and the current row
-    uint32_t out[Cap::K];
+    uint32_t out[Cap::P];
     uint32_t run_off[64]; // candidates of one row piece: first candidate of lane l's grid cell
     uint32_t run_at[64];  // ... and where its sites start in the sorted order
     uint32_t used[8];
@@ -173,6 +175,33 @@ __device__ __forceinline__ uint32_t lane_rank(uint64_t m)
 {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
+// Cross-lane move of a double by a DPP pattern within rows of 16 lanes.
+template <int CTRL> __device__ __forceinline__ double dpp_d(double x)
+{
+    const uint64_t b = (uint64_t)__double_as_longlong(x);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, 0xf, 0xf, true);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, 0xf, 0xf, true);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+__device__ __forceinline__ double readlane_d(double x, int l)
+{
+    const uint64_t b = (uint64_t)__double_as_longlong(x);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+// Maximum over the wave (all lanes active): a butterfly within each row of
+// 16 lanes (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_ror 4, row_ror 8),
+// then the four row results.
+__device__ __forceinline__ double wave_max_dpp(double x)
+{
+    x = fmax(x, dpp_d<0xb1>(x));
+    x = fmax(x, dpp_d<0x4e>(x));
+    x = fmax(x, dpp_d<0x124>(x));
+    x = fmax(x, dpp_d<0x128>(x));
+    return fmax(fmax(readlane_d(x, 0), readlane_d(x, 16)), fmax(readlane_d(x, 32), readlane_d(x, 48)));
+}
+
 // a value equal in every lane, moved to scalar registers
 __device__ __forceinline__ double wave_uniform(double x)
 {
@@ -218,19 +247,12 @@ template <class Cap> __device__ void wcell_radii(WaveCell<Cap> &c, WaveState &s,
             c.far[nf + lane_rank(m)] = (uint16_t)t;
         nf += __popcll(m);
     }
-    // eight maxima over the wave, exchanged together
-    double red[8] = {r, rn, -mn[0], -mn[1], -mn[2], mx[0], mx[1], mx[2]};
-    for (int o = 32; o > 0; o >>= 1) {
-#pragma unroll
-        for (int q = 0; q < 8; ++q)
-            red[q] = fmax(red[q], __shfl_xor(red[q], o));
-    }
-    s.R2 = wave_uniform(red[0]);
-    s.Rn2 = wave_uniform(red[1]);
+    s.R2 = wave_uniform(wave_max_dpp(r));
+    s.Rn2 = wave_uniform(wave_max_dpp(rn));
     const bool any_near = nf < s.nt;
     for (int a = 0; a < 3; ++a) {
-        s.bmin[a] = any_near ? -wave_uniform(red[2 + a]) : 0.0;
-        s.bmax[a] = any_near ? wave_uniform(red[5 + a]) : 0.0;
+        s.bmin[a] = any_near ? -wave_uniform(wave_max_dpp(-mn[a])) : 0.0;
+        s.bmax[a] = any_near ? wave_uniform(wave_max_dpp(mx[a])) : 0.0;
     }
     s.nfar = nf;
     __syncthreads();
@@ -654,10 +676,17 @@ __device__ int wave_voronoi_cell(WaveCell<Cap> &c, uint32_t i, const float *__re
                                 cand = j != i && d2 >= lo2 && d2 < hi2 && d2 < 4.0 * s.R2 &&
                                        wcell_hits(c, s, c.rowfar, nrf, ddx, ddy, ddz, d2);
                             }
+                            // cut nearest first: the nearer planes make many
+                            // farther ones miss
                             uint64_t m = __ballot(cand);
                             while (m && status == VOR_OK) {
-                                const int l = __ffsll((unsigned long long)m) - 1;
-                                m &= m - 1;
+                                int l = __ffsll((unsigned long long)m) - 1;
+                                if (m & (m - 1)) {
+                                    const bool rem = (m >> lane) & 1u;
+                                    const double dmin = -wave_max_dpp(rem ? -d2 : -INFINITY);
+                                    l = __ffsll((unsigned long long)__ballot(rem && d2 == dmin)) - 1;
+                                }
+                                m &= ~(1ull << l);
                                 const double4 pl = make_double4(__shfl(ddx, l), __shfl(ddy, l), __shfl(ddz, l),
                                                                 0.5 * __shfl(d2, l));
                                 status = wcell_cut(c, s, pl, (uint32_t)__shfl((int)j, l), g.far2, lane);
@@ -679,10 +708,6 @@ __device__ int wave_voronoi_cell(WaveCell<Cap> &c, uint32_t i, const float *__re
             const int q = q0 + lane;
             const bool u = q < s.np && ((c.used[q >> 5] >> (q & 31)) & 1u);
             uint64_t mm = __ballot(u);
-            if (m + __popcll(mm) > Cap::K) {
-                status = VOR_FULL;
-                break;
-            }
             if (u)
                 c.out[m + (int)lane_rank(mm)] = c.nid[q];
             m += __popcll(mm);
@@ -694,9 +719,9 @@ __device__ int wave_voronoi_cell(WaveCell<Cap> &c, uint32_t i, const float *__re
 }
 
 // One wave per cell, cells taken in order from a work counter.  First pass
-// (LARGE false): every site, in grid order; cells that overflow the small
-// tables are queued in retry[].  Second pass (LARGE true): the queued cells;
-// a list longer than VorSmall::K goes to a slot of big_lists (big_slot[i]),
+// (LARGE false): every site, in the layer order; cells that overflow the small
+// tables are queued in retry[].  Second pass (LARGE true): the queued cells.
+// A list longer than LIST_K goes to a slot of big_lists (big_slot[i]),
 // shorter lists to the cell's slot of lists.
 template <class Cap, bool LARGE>
 __global__ __launch_bounds__(VOR_BLOCK) __attribute__((amdgpu_waves_per_eu(LARGE ? 1 : 3))) void voronoi_cells_kernel(
@@ -720,15 +745,15 @@ __global__ __launch_bounds__(VOR_BLOCK) __attribute__((amdgpu_waves_per_eu(LARGE
         const uint32_t i = cells[r];
         int m;
         int status = wave_voronoi_cell<Cap>(c, i, points, g, cell_start, sorted, lane, &m);
-        uint32_t *dst = lists + (size_t)i * VorSmall::K;
-        if (LARGE && status == VOR_OK && m > VorSmall::K) {
+        uint32_t *dst = lists + (size_t)i * LIST_K;
+        if (status == VOR_OK && m > LIST_K) {
             if (lane == 0)
                 pick = atomicAdd(fails + F_BIG, 1u);
             __syncthreads();
             const uint32_t slot = pick;
             __syncthreads();
             if (slot < big_cap) {
-                dst = big_lists + (size_t)slot * VorLarge::K;
+                dst = big_lists + (size_t)slot * BIG_K;
                 if (lane == 0)
                     big_slot[i] = slot;
             } else {
@@ -775,6 +800,22 @@ __global__ void voronoi_grid_keys_kernel(const float *__restrict__ points, uint3
     atomicAdd(cell_count + cell, 1u);
 }
 
+// Work order of the cells: by grid layer (distance of the grid cell from the
+// grid's boundary, outermost first: the long cells of convex-hull sites start
+// early instead of trailing the pass), grid order within a layer.
+__global__ void voronoi_layer_kernel(uint32_t *__restrict__ keys, const uint32_t *__restrict__ vals, uint32_t n,
+                                     VorGrid g, uint32_t *__restrict__ order)
+{
+    uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n)
+        return;
+    const uint32_t cell = keys[t];
+    const int x = (int)(cell % g.g[0]), y = (int)((cell / g.g[0]) % g.g[1]), z = (int)(cell / (g.g[0] * g.g[1]));
+    const int layer = min(min(min(x, (int)g.g[0] - 1 - x), min(y, (int)g.g[1] - 1 - y)), min(z, (int)g.g[2] - 1 - z));
+    keys[t] = (uint32_t)min(layer, 255);
+    order[t] = vals[t];
+}
+
 __global__ void voronoi_copy_kernel(uint32_t n, const uint32_t *__restrict__ offsets,
                                     const uint32_t *__restrict__ lists, const uint32_t *__restrict__ big_lists,
                                     const uint32_t *__restrict__ big_slot, uint32_t *__restrict__ adjacency)
@@ -784,7 +825,7 @@ __global__ void voronoi_copy_kernel(uint32_t n, const uint32_t *__restrict__ off
         return;
     uint32_t b = offsets[i], m = offsets[i + 1] - b;
     uint32_t slot = big_slot[i];
-    const uint32_t *src = slot == VOR_NONE ? lists + (size_t)i * VorSmall::K : big_lists + (size_t)slot * VorLarge::K;
+    const uint32_t *src = slot == VOR_NONE ? lists + (size_t)i * LIST_K : big_lists + (size_t)slot * BIG_K;
     for (uint32_t k = 0; k < m; ++k)
         adjacency[b + k] = src[k];
 }
@@ -799,12 +840,12 @@ __global__ void fill_u32_kernel(uint32_t *p, size_t n, uint32_t v)
 // workspace layout (u32 words)
 struct VorWs {
     uint32_t *lists, *counts, *keys, *vals, *cell_start, *sort_ws, *scan_ws, *fails, *bbox_ws, *retry, *big_lists,
-        *big_slot;
+        *big_slot, *order;
     float *bbox;
 };
 
 static uint32_t grid_cells_for(uint32_t n) { return n < 8 ? 8 : n; }
-// cells with more than VorSmall::K neighbours
+// cells with more than LIST_K neighbours
 static uint32_t big_cap_for(uint32_t n) { return std::max<uint32_t>(256, n / 64); }
 
 static size_t ws_words(uint32_t n, VorWs *w, uint32_t *base)
@@ -818,7 +859,7 @@ static size_t ws_words(uint32_t n, VorWs *w, uint32_t *base)
     };
     VorWs local{};
     VorWs &x = w ? *w : local;
-    take(&x.lists, (size_t)n * VorSmall::K);
+    take(&x.lists, (size_t)n * LIST_K);
     take(&x.counts, (size_t)n + 1);
     take(&x.keys, n);
     take(&x.vals, n);
@@ -831,8 +872,9 @@ static size_t ws_words(uint32_t n, VorWs *w, uint32_t *base)
     take(&bb, 6);
     x.bbox = reinterpret_cast<float *>(bb);
     take(&x.retry, n);
-    take(&x.big_lists, (size_t)big_cap_for(n) * VorLarge::K);
+    take(&x.big_lists, (size_t)big_cap_for(n) * BIG_K);
     take(&x.big_slot, n);
+    take(&x.order, n);
     return off;
 }
 
@@ -906,9 +948,14 @@ extern "C" int vt_voronoi_build(const float *points, uint32_t num_points, uint32
     rc = radix_sort_pairs(w.keys, w.vals, n, bits, w.sort_ws, s);
     if (rc)
         return rc;
+    voronoi_layer_kernel<<<(n + 255) / 256, 256, 0, s>>>(w.keys, w.vals, n, g, w.order);
+    VT_LAUNCH_CHECK("voronoi_layer_kernel");
+    rc = radix_sort_pairs(w.keys, w.order, n, 8, w.sort_ws, s);
+    if (rc)
+        return rc;
     const uint32_t bcap = big_cap_for(n);
     voronoi_cells_kernel<VorSmall, false><<<wave_blocks(n), VOR_BLOCK, 0, s>>>(
-        points, g, w.cell_start, w.vals, w.vals, n, w.lists, w.big_lists, bcap, w.big_slot, w.counts, w.retry, w.fails);
+        points, g, w.cell_start, w.vals, w.order, n, w.lists, w.big_lists, bcap, w.big_slot, w.counts, w.retry, w.fails);
     VT_LAUNCH_CHECK("voronoi_cells_kernel (small)");
     uint32_t f[F_WORDS];
     VT_HIP_CHECK(hipMemcpyAsync(f, w.fails, sizeof(f), hipMemcpyDeviceToHost, s));
@@ -927,9 +974,9 @@ extern "C" int vt_voronoi_build(const float *points, uint32_t num_points, uint32
     VT_HIP_CHECK(hipMemcpyAsync(tail + 1, w.fails, 2 * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
     VT_HIP_CHECK(hipStreamSynchronize(s));
     if (tail[1] || tail[2]) {
-        set_error("Voronoi build failed for %u cells over capacity (%d planes, %d vertices, %d neighbours, %u long "
-                  "lists) and %u degenerate cuts",
-                  tail[1], VorLarge::P, VorLarge::T, VorLarge::K, bcap, tail[2]);
+        set_error("Voronoi build failed for %u cells over capacity (%d planes, %d vertices, %u lists longer than %d) "
+                  "and %u degenerate cuts",
+                  tail[1], VorLarge::P, VorLarge::T, bcap, LIST_K, tail[2]);
         return VT_ERR_INVALID;
     }
     *num_adjacency = tail[0];
