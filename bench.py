@@ -74,6 +74,8 @@ def main():
     ap.add_argument("--no-train", action="store_true", help="skip the config-2 fwd+bwd training step")
     ap.add_argument("--profile", action="store_true", help="short run for rocprofv3 (no CPU leg, no stats)")
     ap.add_argument("--train-only", action="store_true", help="only the config-2 training step (profiling)")
+    ap.add_argument("--no-voronoi", action="store_true", help="skip the GPU Voronoi adjacency build of the C3 sites")
+    ap.add_argument("--voronoi-only", action="store_true", help="only the GPU Voronoi build (profiling)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run 8 device copies of 1 GiB (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
@@ -108,6 +110,9 @@ def main():
     log(f"building scene C3 ({args.sites} sites, qhull)")
     sc = scene.cached(scene.heightfield, 0, args.sites, 4, name="c3")
     log(f"scene ready in {time.time() - t0:.1f}s: N={sc.num_points} M={sc.num_faces}")
+    if args.voronoi_only:
+        print(json.dumps({"voronoi_c3": voronoi_c3(sc, dev, log)}), flush=True)
+        return
     model = VoroTracing.from_scene(sc, device=dev)
     inf = VoroTracingInfer(model, sort_morton=True, quantize="fp16")
     torch.cuda.synchronize()
@@ -247,6 +252,8 @@ def main():
 
     if not args.no_train and not args.profile:
         result["train_c2"] = train_c2(dev, log, cpu=not args.no_cpu)
+    if not args.no_voronoi and not args.profile:
+        result["voronoi_c3"] = voronoi_c3(sc, dev, log)
 
     print(json.dumps(result), flush=True)
 
@@ -274,6 +281,40 @@ def compulsory_bytes(oc, pts, d4, s4, den, adj, off, ad, rays, inf, thr, skip, c
             "compulsory_bytes_pose0": int(cells.size * (8 + 12 + 4) + 8 * faces),
             "compulsory_note": "distinct cells on the walks of pose 0 x (offsets 8 + site 12 + density 4 + "
                                "8 per face record); textures excluded; walks from the CPU oracle's visit log"}
+
+
+def voronoi_c3(sc, dev, log, reps=5):
+    """The Voronoi adjacency of the C3 sites built on the GPU (the step the
+    reference hands to Paragram, cuda/__init__.py:16-46): wall time of
+    ops.build_voronoi_adjacency from resident sites to the padded CSR, and
+    whether every neighbour set equals the scene's host-qhull CSR."""
+    import numpy as np
+    import torch
+    from vorotracing_amd import ops
+
+    pts = torch.from_numpy(sc.points).to(dev)
+    ops.build_voronoi_adjacency(pts)
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        adj, off, _ = ops.build_voronoi_adjacency(pts)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t)
+    adj, off = adj.cpu().numpy(), off.cpu().numpy().astype(np.int64)
+    qoff = sc.offsets.astype(np.int64)
+    qadj = sc.adjacency[:qoff[-1]].astype(np.int64)
+    rows = np.repeat(np.arange(qoff.size - 1), np.diff(qoff))
+    equal = bool(np.array_equal(off, qoff) and np.array_equal(adj[:off[-1]].astype(np.int64),
+                                                               qadj[np.lexsort((qadj, rows))]))
+    out = {"sites": int(pts.shape[0]), "faces": int(off[-1]), "ms": round(1000 * float(np.median(times)), 1),
+           "ms_min": round(1000 * min(times), 1), "equal_to_qhull": equal,
+           "note": "wall time of build_voronoi_adjacency (grid bucketing, cell clipping, CSR), median of "
+                   f"{reps}; sets compared with scipy/qhull Delaunay.vertex_neighbor_vertices"}
+    if "build_s" in sc.params:
+        out["host_qhull_scene_s"] = sc.params["build_s"]
+    log(f"voronoi C3: {out['ms']} ms, equal to qhull: {equal}")
+    return out
 
 
 def stream_copy_gbs(dev):

@@ -44,6 +44,21 @@ def test_mini_heightfield_sites(gpu):
     _check(H.mini_heightfield().points, gpu)
 
 
+def test_heightfield_131k(gpu):
+    """C3's site distribution at 131,072 sites: dense surface cells whose lists exceed the
+    64-entry slots, background cells next to the surface and the convex-hull cells of the cube."""
+    pts = scene._heightfield_sites(np.random.default_rng(3), 131072, 0.8, 4.0, 0.01).astype(np.float32)
+    _check(pts, gpu)
+
+
+def test_ellipsoid_surface(gpu):
+    """Every site on a convex surface is a convex-hull site, so every cell is unbounded.  An
+    ellipsoid (unlike a sphere) keeps 5 sites off a common sphere: general position."""
+    d = np.random.default_rng(5).normal(size=(3000, 3))
+    pts = (d / np.linalg.norm(d, axis=1, keepdims=True) * np.array([1.0, 0.7, 0.5])).astype(np.float32)
+    _check(pts, gpu)
+
+
 def test_model_scene_renders_the_same(gpu):
     """A scene whose adjacency comes from the GPU builder renders like the qhull one (same sets,
     ascending order; the walk's choice depends on the order only through exact ties)."""
