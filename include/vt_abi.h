@@ -120,6 +120,72 @@ int vt_trace_infer_q8_tiled(const float *points, const uint8_t *diffuse, const u
                             uint16_t *rgba, vt_ray_stats *stats, vt_stream_t stream);
 
 /*
+ * Cameras for in-kernel ray generation.  Replaces the rays buffer that the
+ * reference builds in torch before every render: vorotracing/utils/
+ * __init__.py:85-130 (generate_camera_rays) and datasets/datasets.py:126-136,
+ * :286-304 (pixel centres, cam_from_img, normalise, rotate by the pose).
+ * Pixel (u, v) of an H x W image samples (u + pixel_offset, v + pixel_offset)
+ * (datasets.py uses 0.5, generate_camera_rays 0):
+ *   mx = (u + pixel_offset - cx) / fx,  my = (v + pixel_offset - cy) / fy
+ *   pinhole: dir_cam = (mx, my, 1)
+ *   fisheye (OpenCV fisheye / equidistant): theta_d = |(mx, my)|, theta solves
+ *     theta (1 + k1 theta^2 + k2 theta^4 + k3 theta^6 + k4 theta^8) = theta_d
+ *     (12 Newton steps from theta_d, clamped to [0, pi]),
+ *     dir_cam = (mx sin(theta) / theta_d, my sin(theta) / theta_d, cos(theta))
+ *   dir_cam /= |dir_cam|; ray direction = R dir_cam (R row-major,
+ *   camera-to-world; the traversal normalises it again as it does any ray);
+ *   origin = t + (v / (H - 1)) * rolling (rolling shutter; zero for a
+ *   global shutter).
+ * The arithmetic is f32 with the library's convention (fused dot products,
+ * correctly rounded division and sqrt, own sin / cos polynomials).
+ */
+enum { VT_CAMERA_PINHOLE = 0, VT_CAMERA_FISHEYE = 1 }; /* other values render as pinhole */
+typedef struct vt_camera {
+    uint32_t model;     /* VT_CAMERA_* */
+    float fx, fy, cx, cy;
+    float pixel_offset;
+    float k[4];         /* fisheye distortion k1..k4 */
+    float R[9];         /* camera-to-world rotation, row-major */
+    float t[3];         /* camera centre */
+    float rolling[3];   /* origin shift at the last row */
+} vt_camera;
+
+/*
+ * Rays of num_images cameras (device array) for H x W images, written as
+ * f32 (num_images, H, W, 6): the rays the camera renders below trace.
+ * With W = 1 the origins are those of each row (start cells of
+ * rolling-shutter cameras).
+ */
+int vt_camera_rays(const vt_camera *cameras, uint32_t num_images, uint32_t image_h, uint32_t image_w, float *rays,
+                   vt_stream_t stream);
+
+/*
+ * fp16 / q8 inference of num_images cameras (device array), rays generated in
+ * the kernel: no rays buffer is read.  Per-ray results equal those of
+ * vt_trace_infer_f16_tiled / vt_trace_infer_q8_tiled on the rays of
+ * vt_camera_rays.  start_point: u32 start cell per image, or per image row
+ * ((num_images, image_h)) when start_per_row is non-zero (rolling shutter:
+ * every row has its own origin).  rgba (num_images, image_h, image_w, 4) f16;
+ * stats in the same ray order.
+ */
+int vt_trace_infer_f16_camera(const float *points, const uint16_t *diffuse, const uint16_t *specular,
+                              uint32_t diff_res, uint32_t spec_res, const float *density, const uint32_t *adjacency,
+                              const uint32_t *offsets, uint32_t num_points, const uint16_t *adj_diff,
+                              const vt_camera *cameras, uint32_t num_images, uint32_t image_h, uint32_t image_w,
+                              uint32_t tile_h, uint32_t tile_w, const uint32_t *start_point, int start_per_row,
+                              float weight_threshold, uint32_t max_intersections, float cell_skip_threshold,
+                              uint16_t *rgba, vt_ray_stats *stats, vt_stream_t stream);
+int vt_trace_infer_q8_camera(const float *points, const uint8_t *diffuse, const uint8_t *specular, uint32_t diff_res,
+                             uint32_t spec_res, const float diff_scale[3], const float diff_offset[3],
+                             const float spec_scale[3], const float spec_offset[3], const float *density,
+                             const uint32_t *adjacency, const uint32_t *offsets, uint32_t num_points,
+                             const uint16_t *adj_diff, const vt_camera *cameras, uint32_t num_images,
+                             uint32_t image_h, uint32_t image_w, uint32_t tile_h, uint32_t tile_w,
+                             const uint32_t *start_point, int start_per_row, float weight_threshold,
+                             uint32_t max_intersections, float cell_skip_threshold, uint16_t *rgba,
+                             vt_ray_stats *stats, vt_stream_t stream);
+
+/*
  * Training forward.  Replaces _C.trace_vorotracing_fwd
  * (tracing_octmap.cu:346-546, kernel :151-230).  Runs the prefetch into
  * `adj_diff_workspace` ((adjacency_size+32)*4 halves) as the reference does
@@ -259,7 +325,8 @@ int vt_pad_3to4_f16(const float *x, uint32_t rows, uint32_t texels_per_row, uint
 /*
  * Self-test of the device arithmetic shared by restatement with the CPU
  * checker (no reference counterpart): op 0 = exp, 1 = log, 2 = f32->f16 bits
- * (out as u16 in the low half of each u32), applied elementwise to n floats.
+ * (out as u16 in the low half of each u32), 3 = sin and 4 = cos of the camera
+ * generator (arguments in [0, pi]), applied elementwise to n floats.
  */
 int vt_math_probe(int op, const float *in, uint32_t *out, uint32_t n, vt_stream_t stream);
 

@@ -295,3 +295,24 @@ def b_alg_infer(stats, tex_bytes=64, perm=False):
     return int(per_ray * len(s) + 8 * s["visits"].sum(dtype=np.int64) + 8 * s["faces"].sum(dtype=np.int64)
                + 16 * s["exits"].sum(dtype=np.int64) + 4 * s["integrated"].sum(dtype=np.int64)
                + tex_bytes * s["shaded"].sum(dtype=np.int64))
+
+
+# --------------------------------------------------------------------------
+# camera rays
+
+
+def sincos(x, cos=False):
+    x = _c(np.atleast_1d(x), np.float32)
+    y = np.empty_like(x)
+    lib().or_sincos_many(_i(1 if cos else 0), _p(x), _p(y), _sz(x.size))
+    return y
+
+
+def camera_rays(packed: bytes, num_images: int, H: int, W: int):
+    """or_camera_rays over packed vt_camera records (100 bytes each): rays f32
+    (num_images, H, W, 6), direction not normalised."""
+    assert len(packed) == 100 * num_images
+    buf = C.create_string_buffer(packed, len(packed))
+    out = np.empty((num_images, H, W, 6), np.float32)
+    lib().or_camera_rays(C.cast(buf, C.c_void_p), _u(num_images), _u(H), _u(W), _p(out))
+    return out

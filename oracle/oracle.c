@@ -22,6 +22,8 @@
  *   vorotracing/cuda/csrc/tracing/ray_integrator.cuh:39-53  cell_intersection_grad
  *   vorotracing/cuda/csrc/utils/typing.cuh:18-24  f16 casts (RNE)
  *   vorotracing/cuda/csrc/utils/geometry.h:123-129 atomic_add_vec (atomics kept)
+ *   vorotracing/utils/__init__.py:85-130, vorotracing/datasets/datasets.py
+ *       :126-136, :286-304  camera rays                         -> or_camera_rays
  *
  * Parity pins (tests/test_oracle_*.py): f16 casts vs numpy.float16 (all
  * halves, random floats); or_expf/or_logf vs float64 libm (<= 2 ulp); walk vs
@@ -1010,4 +1012,118 @@ void or_cell_intersection_grad(const float prim[3], const float opp[3], const fl
     out[0] = g.x;
     out[1] = g.y;
     out[2] = g.z;
+}
+
+/* ------------------------------------------------------------------------- */
+/* camera rays                                                                 */
+/* ------------------------------------------------------------------------- */
+
+/* sin x and cos x for x in [0, pi]: reduced to [-pi/4, pi/4] against pi/2
+ * or pi, each held as hi + lo (hi - x is exact there by Sterbenz's lemma,
+ * so the reduced argument is rounded once), then the Taylor polynomials of
+ * degree 13 (sin) and 14 (cos) in Horner form in z = r^2 (truncation below
+ * 3e-14 on [-pi/4, pi/4]).  Same operations as vt_sinf / vt_cosf. */
+#define OR_PI_HI 0x1.921fb6p+1f
+#define OR_PI_LO (-0x1.777a5cp-24f)
+#define OR_PIO2_HI 0x1.921fb6p+0f
+#define OR_PIO2_LO (-0x1.777a5cp-25f)
+#define OR_PIO4 0.785398185f
+#define OR_PI3O4 2.35619450f
+
+static inline float sin_poly(float r)
+{
+    const float z = r * r;
+    float p = 1.0f / 6227020800.0f;
+    p = fmaf(p, z, -1.0f / 39916800.0f);
+    p = fmaf(p, z, 1.0f / 362880.0f);
+    p = fmaf(p, z, -1.0f / 5040.0f);
+    p = fmaf(p, z, 1.0f / 120.0f);
+    p = fmaf(p, z, -1.0f / 6.0f);
+    return fmaf(r * z, p, r);
+}
+
+static inline float cos_poly(float r)
+{
+    const float z = r * r;
+    float p = -1.0f / 87178291200.0f;
+    p = fmaf(p, z, 1.0f / 479001600.0f);
+    p = fmaf(p, z, -1.0f / 3628800.0f);
+    p = fmaf(p, z, 1.0f / 40320.0f);
+    p = fmaf(p, z, -1.0f / 720.0f);
+    p = fmaf(p, z, 1.0f / 24.0f);
+    p = fmaf(p, z, -0.5f);
+    return fmaf(z, p, 1.0f);
+}
+
+float or_sinf(float x)
+{
+    if (x <= OR_PIO4)
+        return sin_poly(x);
+    if (x <= OR_PI3O4)
+        return cos_poly((OR_PIO2_HI - x) + OR_PIO2_LO); /* sin x = cos(pi/2 - x) */
+    return sin_poly((OR_PI_HI - x) + OR_PI_LO);         /* sin x = sin(pi - x) */
+}
+
+float or_cosf(float x)
+{
+    if (x <= OR_PIO4)
+        return cos_poly(x);
+    if (x <= OR_PI3O4)
+        return sin_poly((OR_PIO2_HI - x) + OR_PIO2_LO); /* cos x = sin(pi/2 - x) */
+    return -cos_poly((OR_PI_HI - x) + OR_PI_LO);        /* cos x = -cos(pi - x) */
+}
+
+void or_sincos_many(int cos, const float *x, float *y, size_t n)
+{
+    for (size_t i = 0; i < n; ++i)
+        y[i] = cos ? or_cosf(x[i]) : or_sinf(x[i]);
+}
+
+/* Pixel (u, v): normalised image coordinates (pixel centre at +pixel_offset,
+ * datasets.py:128-131), through the camera model to a camera-frame
+ * direction, normalised (datasets.py:133-134), rotated by the pose
+ * (datasets.py:296-299), origin t (+ the rolling-shutter shift of row v). */
+static void camera_ray(const or_camera *c, uint32_t u, uint32_t v, uint32_t H, float *q)
+{
+    const float mx = ((float)u + c->pixel_offset - c->cx) / c->fx;
+    const float my = ((float)v + c->pixel_offset - c->cy) / c->fy;
+    v3 dc = mk(mx, my, 1.0f);
+    if (c->model == OR_CAMERA_FISHEYE) {
+        const float td = sqrtf(fmaf(my, my, mx * mx));
+        dc = mk(0.0f, 0.0f, 1.0f);
+        if (td > 0.0f) {
+            /* Newton on theta (1 + k1 theta^2 + k2 theta^4 + k3 theta^6 + k4 theta^8) = td */
+            float th = td;
+            for (int it = 0; it < 12; ++it) {
+                const float t2 = th * th;
+                const float p = fmaf(fmaf(fmaf(c->k[3], t2, c->k[2]), t2, c->k[1]), t2, c->k[0]);
+                const float qq =
+                    fmaf(fmaf(fmaf(9.0f * c->k[3], t2, 7.0f * c->k[2]), t2, 5.0f * c->k[1]), t2, 3.0f * c->k[0]);
+                const float g = fmaf(th * t2, p, th) - td;
+                const float dg = fmaf(t2, qq, 1.0f);
+                th = th - g / dg;
+            }
+            th = fminf(fmaxf(th, 0.0f), OR_PI_HI);
+            const float s = or_sinf(th) / td;
+            dc = mk(mx * s, my * s, or_cosf(th));
+        }
+    }
+    dc = vdivs(dc, sqrtf(vdot(dc, dc)));
+    const v3 d = mk(vdot(mk(c->R[0], c->R[1], c->R[2]), dc), vdot(mk(c->R[3], c->R[4], c->R[5]), dc),
+                    vdot(mk(c->R[6], c->R[7], c->R[8]), dc));
+    const float sv = H > 1 ? (float)v / (float)(H - 1) : 0.0f;
+    q[0] = fmaf(sv, c->rolling[0], c->t[0]);
+    q[1] = fmaf(sv, c->rolling[1], c->t[1]);
+    q[2] = fmaf(sv, c->rolling[2], c->t[2]);
+    q[3] = d.x;
+    q[4] = d.y;
+    q[5] = d.z;
+}
+
+void or_camera_rays(const or_camera *cams, uint32_t num_images, uint32_t H, uint32_t W, float *rays)
+{
+    for (uint32_t img = 0; img < num_images; ++img)
+        for (uint32_t v = 0; v < H; ++v)
+            for (uint32_t u = 0; u < W; ++u)
+                camera_ray(&cams[img], u, v, H, rays + 6 * (((size_t)img * H + v) * W + u));
 }

@@ -50,6 +50,27 @@ void or_f32_to_f16_many(const float *x, uint16_t *y, size_t n);
 int or_oct_wrap_index(int u, int v, int R);
 void or_oct_encode(const float dir[3], int R, float uv[2]);
 
+/* Camera ray generation (the rays the reference builds in torch:
+ * utils/__init__.py:85-130, datasets/datasets.py:126-136 and :286-304; the
+ * fisheye model is OpenCV's, which the reference reaches through pycolmap's
+ * cam_from_img).  Same layout and semantics as vt_camera in
+ * include/vt_abi.h. */
+enum { OR_CAMERA_PINHOLE = 0, OR_CAMERA_FISHEYE = 1 };
+typedef struct or_camera {
+    uint32_t model;
+    float fx, fy, cx, cy;
+    float pixel_offset;
+    float k[4];
+    float R[9];
+    float t[3];
+    float rolling[3];
+} or_camera;
+float or_sinf(float x); /* x in [0, pi] */
+float or_cosf(float x); /* x in [0, pi] */
+void or_sincos_many(int cos, const float *x, float *y, size_t n);
+/* rays f32 (num_images, H, W, 6); direction not normalised (the walk does). */
+void or_camera_rays(const or_camera *cams, uint32_t num_images, uint32_t H, uint32_t W, float *rays);
+
 /* tracing_octmap.cu:125-149; adj_diff has (adjacency_size + 32) * 4 halves,
  * the 32-row tail is left untouched (uninitialised in the reference). */
 void or_prefetch_adj(const float *points, uint32_t num_points, const uint32_t *adjacency,

@@ -26,7 +26,7 @@ def _declarations():
 
 def test_header_declarations_parsed():
     d = _declarations()
-    assert len(d) == 25, sorted(d)
+    assert len(d) == 28, sorted(d)
     for name in ("vt_trace_infer_f16", "vt_trace_fwd", "vt_trace_bwd", "vt_bvh_query", "vt_morton_reorder"):
         assert name in d
 
@@ -60,3 +60,41 @@ def test_argument_errors_need_no_gpu():
     assert b"null pointer" in lib.vt_last_error()
     with pytest.raises(_lib.VTError, match="null"):
         _lib.check(rc, "vt_trace_infer_f16_tiled")
+
+
+def test_every_device_kernel_has_its_host_launch_symbol(tmp_path):
+    """Each kernel in the library's gfx950 code objects must have a host-side kernel
+    symbol of exactly the same name, or its launches cannot find it.  Kernel
+    signatures whose types mangle differently in the host and the device
+    compilations (an unnamed enum in a template argument, for one) break this."""
+    import shutil
+    import subprocess
+
+    bundler = "/opt/rocm/llvm/bin/clang-offload-bundler"
+    readelf = "/opt/rocm/llvm/bin/llvm-readelf"
+    if not (shutil.which("objcopy") and os.path.exists(bundler) and os.path.exists(readelf)):
+        pytest.skip("objcopy / clang-offload-bundler / llvm-readelf not available")
+    lib = _lib.LIB_PATH
+    fat = tmp_path / "fatbin.bin"
+    subprocess.run(["objcopy", "--dump-section", f".hip_fatbin={fat}", lib], check=True)
+    data = fat.read_bytes()
+    magic = b"__CLANG_OFFLOAD_BUNDLE__"
+    starts = []
+    i = data.find(magic)
+    while i >= 0:
+        starts.append(i)
+        i = data.find(magic, i + 1)
+    assert starts, "no offload bundles in .hip_fatbin"
+    device = set()
+    for k, a in enumerate(starts):
+        part = tmp_path / f"bundle{k}.bin"
+        part.write_bytes(data[a:starts[k + 1] if k + 1 < len(starts) else len(data)])
+        co = tmp_path / f"co{k}.o"
+        subprocess.run([bundler, "--type=o", "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", f"--input={part}",
+                        f"--output={co}", "--unbundle"], check=True)
+        out = subprocess.run([readelf, "-s", "--wide", str(co)], check=True, capture_output=True, text=True).stdout
+        device |= {ln.split()[-1][:-3] for ln in out.splitlines() if ln.strip().endswith(".kd")}
+    host = set(subprocess.run(["nm", lib], check=True, capture_output=True, text=True).stdout.split())
+    assert len(device) > 40
+    missing = sorted(device - host)
+    assert not missing, f"{len(missing)} device kernels without a host symbol, e.g. {missing[:2]}"

@@ -31,6 +31,12 @@ SIGNATURES = {
     "vt_trace_infer_q8_tiled": (
         [P, P, P, U32, U32, P, P, P, P, P, P, P, U32, P, P, U32, U32, U32, U32, U32, P, F32, U32, F32, P, P, P],
         C.c_int),
+    "vt_camera_rays": ([P, U32, U32, U32, P, P], C.c_int),
+    "vt_trace_infer_f16_camera": (
+        [P, P, P, U32, U32, P, P, P, U32, P, P, U32, U32, U32, U32, U32, P, I32, F32, U32, F32, P, P, P], C.c_int),
+    "vt_trace_infer_q8_camera": (
+        [P, P, P, U32, U32, P, P, P, P, P, P, P, U32, P, P, U32, U32, U32, U32, U32, P, I32, F32, U32, F32, P, P, P],
+        C.c_int),
     "vt_trace_fwd": (
         [I32, P, P, P, U32, U32, P, P, U32, P, U32, P, U32, U32, U32, P, U32, P, F32, U32, P, P, P, P, P, P, P, P, P, P, P, P],
         C.c_int),

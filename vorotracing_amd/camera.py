@@ -1,4 +1,6 @@
-"""Ray generation for the benchmark cameras (host side, float64 then f32).
+"""Ray generation for the benchmark cameras (host side, float64 then f32),
+and ``Camera``, the record the in-kernel ray generation takes
+(``vt_camera`` in include/vt_abi.h).
 
 Rays are ``[..., 6]`` f32 = origin xyz + direction xyz, the layout of
 ``Ray`` (camera.h:5-8) the traversal reads.  Pinhole rays follow
@@ -7,7 +9,9 @@ forward; ``dir = R (x, y, 1)``, normalised) with pixel centres at +0.5.
 """
 from __future__ import annotations
 
+import dataclasses
 import math
+import struct
 
 import numpy as np
 
@@ -85,3 +89,79 @@ def fisheye_rolling_rays(width: int = 1558, height: int = 1039, eye=None, k1: fl
     shift = (v / (height - 1)) * shutter_shift
     o = np.asarray(eye, np.float64)[None, None, :] + shift[..., None] * Rcw[:, 0][None, None, :]
     return np.concatenate([o, dw], -1).astype(np.float32)
+
+
+_CAMERA_FMT = struct.Struct("<I5f4f9f3f3f")  # vt_camera, 100 bytes
+CAMERA_MODELS = {"pinhole": 0, "fisheye": 1}
+
+
+@dataclasses.dataclass
+class Camera:
+    """A camera for in-kernel ray generation (``vt_camera``).  Pixel (u, v)
+    samples (u + pixel_offset, v + pixel_offset); ``R`` is camera-to-world
+    (OpenCV axes: x right, y down, z forward), ``t`` the centre; ``k`` the
+    OpenCV fisheye distortion k1..k4; row v's origin is
+    ``t + v / (height - 1) * rolling`` (rolling shutter)."""
+
+    width: int
+    height: int
+    fx: float
+    fy: float
+    cx: float
+    cy: float
+    R: np.ndarray
+    t: np.ndarray
+    model: str = "pinhole"
+    k: tuple = (0.0, 0.0, 0.0, 0.0)
+    pixel_offset: float = 0.5
+    rolling: np.ndarray = dataclasses.field(default_factory=lambda: np.zeros(3))
+
+    @property
+    def rolling_shutter(self) -> bool:
+        return bool(np.any(np.asarray(self.rolling) != 0))
+
+    def pack(self) -> bytes:
+        """The 100-byte vt_camera record (f32 fields)."""
+        k = list(self.k) + [0.0] * (4 - len(self.k))
+        if self.model not in CAMERA_MODELS:
+            raise ValueError(f"unknown camera model {self.model!r} (known: {sorted(CAMERA_MODELS)})")
+        return _CAMERA_FMT.pack(CAMERA_MODELS[self.model], self.fx, self.fy, self.cx, self.cy, self.pixel_offset,
+                                *k[:4], *np.asarray(self.R, np.float64).reshape(9), *np.asarray(self.t).reshape(3),
+                                *np.asarray(self.rolling).reshape(3))
+
+    @classmethod
+    def look_at(cls, width: int, height: int, eye, target=(0.0, 0.0, 0.0), up=(0.0, 0.0, 1.0),
+                fov_y_deg: float = 60.0) -> "Camera":
+        """The pinhole camera of ``pinhole_rays``."""
+        f = (height / 2.0) / math.tan(math.radians(fov_y_deg) / 2.0)
+        return cls(width, height, f, f, width / 2.0, height / 2.0, look_at(eye, target, up),
+                   np.asarray(eye, np.float64))
+
+    @classmethod
+    def orbit(cls, k: int, width: int, height: int, n: int = 32, radius: float = 7.0, elevation_deg: float = 35.0,
+              fov_y_deg: float = 60.0) -> "Camera":
+        """Pose k of the config-3 orbit (``orbit_rays``)."""
+        return cls.look_at(width, height, orbit_eye(k, n, radius, elevation_deg), fov_y_deg=fov_y_deg)
+
+    @classmethod
+    def fisheye_rolling(cls, width: int = 1558, height: int = 1039, eye=None, k1: float = -0.1, k2: float = 0.01,
+                        diag_fov_deg: float = 180.0, shutter_shift: float = 0.05) -> "Camera":
+        """The config-5 camera of ``fisheye_rolling_rays``."""
+        if eye is None:
+            eye = orbit_eye(0)
+        Rcw = look_at(eye)
+        half_diag = math.hypot(width / 2.0, height / 2.0)
+        tmax = math.radians(diag_fov_deg) / 2.0
+        f = half_diag / (tmax * (1 + k1 * tmax ** 2 + k2 * tmax ** 4))
+        return cls(width, height, f, f, width / 2.0, height / 2.0, Rcw, np.asarray(eye, np.float64), "fisheye",
+                   (k1, k2, 0.0, 0.0), 0.5, shutter_shift * Rcw[:, 0])
+
+
+def pack_cameras(cameras) -> bytes:
+    """vt_camera array of a batch of cameras of one image size."""
+    cams = list(cameras)
+    if not cams:
+        raise ValueError("no cameras")
+    if any((c.width, c.height) != (cams[0].width, cams[0].height) for c in cams):
+        raise ValueError("all cameras of a batch must have the same image size")
+    return b"".join(c.pack() for c in cams)

@@ -2,6 +2,7 @@
 // per-face offset prefetch (tracing_octmap.cu:125-149, host :612-640).
 #include "vt_internal.h"
 #include "vt_device.h"
+#include "vt_camera.h"
 
 #include <cstring>
 
@@ -29,6 +30,10 @@ __global__ void math_probe_kernel(int op, const float *__restrict__ in, uint32_t
         out[i] = f_bits(vt_expf(x));
     else if (op == 1)
         out[i] = f_bits(vt_logf(x));
+    else if (op == 3)
+        out[i] = f_bits(vt_sinf(x));
+    else if (op == 4)
+        out[i] = f_bits(vt_cosf(x));
     else
         out[i] = f2h(x);
 }
@@ -109,7 +114,7 @@ extern "C" int vt_abi_version(void) { return 2; }
 extern "C" int vt_math_probe(int op, const float *in, uint32_t *out, uint32_t n, vt_stream_t stream)
 {
     clear_error();
-    VT_REQUIRE(op >= 0 && op <= 2, "op must be 0 (exp), 1 (log) or 2 (f16)");
+    VT_REQUIRE(op >= 0 && op <= 4, "op must be 0 (exp), 1 (log), 2 (f16), 3 (sin) or 4 (cos)");
     if (n == 0)
         return VT_OK;
     VT_REQUIRE(in && out, "null pointer argument");

@@ -7,6 +7,9 @@
 // threshold, and stop once T <= weight_threshold.
 #include "vt_internal.h"
 #include "vt_walk.h"
+#include "vt_camera.h"
+
+#include <algorithm>
 
 namespace vt {
 
@@ -120,15 +123,21 @@ struct InferArgs {
     uint32_t num_images, H, W, th, tw;
     // q8
     float ds[3], dof[3], ss[3], sof[3];
+    // camera renders: cameras of the images (device array); start cells per row
+    const vt_camera *cams;
+    uint32_t start_rows;
 };
 
-enum { MAP_LINEAR = 0, MAP_TILED = 1 };
+// MAP_CAMERA: tiled lanes whose rays come from cameras instead of a buffer.
+// (Named constants: a kernel signature must not depend on an unnamed type,
+// whose mangling differs between the host and the device compilation.)
+constexpr int MAP_LINEAR = 0, MAP_TILED = 1, MAP_CAMERA = 2;
 
 // Lane s of a launch renders ray slot_to_ray(s): tiled, tile s/64 lane s%64
 // of the image batch; linear, ray s or ray_perm[s].
 __device__ __forceinline__ uint32_t slot_to_ray(const InferArgs &a, uint32_t s, int map)
 {
-    if (map == MAP_TILED)
+    if (map == MAP_TILED || map == MAP_CAMERA)
         return tiled_ray(s, a.num_images, a.H, a.W, a.th, a.tw);
     if (s >= a.num_rays)
         return NONE;
@@ -163,15 +172,26 @@ __global__ __launch_bounds__(256) void infer_kernel(InferArgs a, uint32_t total_
     }
     integ.thr = a.thr;
     integ.skip = a.skip;
-    load_ray(a.rays, r, integ.o, integ.d);
+    uint32_t start;
+    if constexpr (MAP == MAP_CAMERA) {
+        // the ray of pixel (u, v) of image img, normalised as load_ray does
+        const uint32_t hw = a.H * a.W, img = r / hw, rem = r - img * hw, v = rem / a.W, u = rem - v * a.W;
+        f3 dd;
+        camera_ray(a.cams[img], u, v, a.H, integ.o, dd);
+        integ.d = divs(dd, __builtin_sqrtf(dot(dd, dd)));
+        start = a.start_point[a.start_rows ? img * a.H + v : img];
+    } else {
+        load_ray(a.rays, r, integ.o, integ.d);
+        start = a.start_point[r];
+    }
     float su, sv;
     oct_encode<RS>(mk(-integ.d.x, -integ.d.y, -integ.d.z), su, sv);
     integ.spec = bilinear_setup<RS>(su, sv);
     integ.acc = mk(0.0f, 0.0f, 0.0f);
     integ.T = 1.0f;
     StatsAcc<STATS> st;
-    uint32_t n = walk<CHUNK>(integ.o, integ.d, a.points, a.adjacency, a.offsets, a.adj_diff, a.start_point[r],
-                             a.max_steps, integ, st);
+    uint32_t n = walk<CHUNK>(integ.o, integ.d, a.points, a.adjacency, a.offsets, a.adj_diff, start, a.max_steps,
+                             integ, st);
     uint2 out;
     out.x = (uint32_t)f2h(integ.acc.x) | ((uint32_t)f2h(integ.acc.y) << 16);
     out.y = (uint32_t)f2h(integ.acc.z) | ((uint32_t)f2h(1.0f - integ.T) << 16);
@@ -194,6 +214,9 @@ static int launch_one(const InferArgs &a, hipStream_t stream, uint32_t slots)
 template <int RD, int RS, bool Q8>
 static int launch_infer_rs(const InferArgs &a, bool stats, int map, hipStream_t stream, uint32_t lanes)
 {
+    if (map == MAP_CAMERA)
+        return stats ? launch_one<RD, RS, Q8, true, MAP_CAMERA>(a, stream, lanes)
+                     : launch_one<RD, RS, Q8, false, MAP_CAMERA>(a, stream, lanes);
     if (map == MAP_TILED)
         return stats ? launch_one<RD, RS, Q8, true, MAP_TILED>(a, stream, lanes)
                      : launch_one<RD, RS, Q8, false, MAP_TILED>(a, stream, lanes);
@@ -410,4 +433,145 @@ extern "C" int vt_trace_infer_q8_tiled(const float *points, const uint8_t *diffu
     }
     return launch_infer<true>(a, diff_res, spec_res, stats != nullptr, MAP_TILED, as_stream(stream),
                               (uint32_t)(tiles * 64));
+}
+
+namespace vt {
+
+__global__ void camera_rays_kernel(const vt_camera *__restrict__ cams, uint32_t num_images, uint32_t H, uint32_t W,
+                                   float *__restrict__ rays)
+{
+    const uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t hw = (uint64_t)H * W;
+    if (r >= hw * num_images)
+        return;
+    const uint32_t img = (uint32_t)(r / hw), rem = (uint32_t)(r - img * hw), v = rem / W, u = rem - v * W;
+    f3 o, d;
+    camera_ray(cams[img], u, v, H, o, d);
+    float *q = rays + 6 * r;
+    q[0] = o.x;
+    q[1] = o.y;
+    q[2] = o.z;
+    q[3] = d.x;
+    q[4] = d.y;
+    q[5] = d.z;
+}
+
+// Camera renders of num_images images (one launch).
+template <bool Q8>
+static int render_cameras(const InferArgs &a, const vt_camera *cameras, uint32_t num_images, int start_per_row,
+                          uint32_t rd, uint32_t rs, bool stats, hipStream_t stream)
+{
+    VT_REQUIRE(a.th * a.tw == 64, "tile_h * tile_w must be 64 (one wave64 per tile), got %u x %u", a.th, a.tw);
+    const uint64_t tiles = (uint64_t)((a.W + a.tw - 1) / a.tw) * ((a.H + a.th - 1) / a.th) * num_images;
+    VT_REQUIRE(tiles * 64 < (1ull << 32) && (uint64_t)a.H * a.W * num_images < (1ull << 32), "image batch too large");
+    InferArgs c = a;
+    c.num_images = num_images;
+    c.num_rays = num_images * a.H * a.W;
+    c.cams = cameras;
+    c.start_rows = start_per_row ? 1u : 0u;
+    return launch_infer<Q8>(c, rd, rs, stats, MAP_CAMERA, stream, (uint32_t)(tiles * 64));
+}
+
+} // namespace vt
+
+extern "C" int vt_camera_rays(const vt_camera *cameras, uint32_t num_images, uint32_t image_h, uint32_t image_w,
+                              float *rays, vt_stream_t stream)
+{
+    clear_error();
+    if (num_images == 0 || image_h == 0 || image_w == 0)
+        return VT_OK;
+    VT_REQUIRE(cameras && rays, "null pointer argument");
+    const uint64_t total = (uint64_t)image_h * image_w * num_images;
+    VT_REQUIRE(total < (1ull << 40), "image batch too large");
+    camera_rays_kernel<<<(uint32_t)((total + 255) / 256), 256, 0, as_stream(stream)>>>(cameras, num_images, image_h,
+                                                                                        image_w, rays);
+    VT_LAUNCH_CHECK("camera_rays_kernel");
+    return VT_OK;
+}
+
+extern "C" int vt_trace_infer_f16_camera(const float *points, const uint16_t *diffuse, const uint16_t *specular,
+                                         uint32_t diff_res, uint32_t spec_res, const float *density,
+                                         const uint32_t *adjacency, const uint32_t *offsets, uint32_t num_points,
+                                         const uint16_t *adj_diff, const vt_camera *cameras, uint32_t num_images,
+                                         uint32_t image_h, uint32_t image_w, uint32_t tile_h, uint32_t tile_w,
+                                         const uint32_t *start_point, int start_per_row, float weight_threshold,
+                                         uint32_t max_intersections, float cell_skip_threshold, uint16_t *rgba,
+                                         vt_ray_stats *stats, vt_stream_t stream)
+{
+    clear_error();
+    if (num_images == 0 || image_h == 0 || image_w == 0)
+        return VT_OK;
+    int rc = check_common(points, diffuse, specular, density, adjacency, offsets, adj_diff, cameras, start_point,
+                          rgba);
+    if (rc)
+        return rc;
+    (void)num_points;
+    InferArgs a{};
+    a.points = points;
+    a.diffuse = diffuse;
+    a.specular = specular;
+    a.density = density;
+    a.adjacency = adjacency;
+    a.offsets = offsets;
+    a.adj_diff = reinterpret_cast<const uint2 *>(adj_diff);
+    a.start_point = start_point;
+    a.thr = weight_threshold;
+    a.skip = cell_skip_threshold;
+    a.max_steps = max_intersections;
+    a.rgba = rgba;
+    a.stats = reinterpret_cast<uint32_t *>(stats);
+    a.H = image_h;
+    a.W = image_w;
+    a.th = tile_h;
+    a.tw = tile_w;
+    return render_cameras<false>(a, cameras, num_images, start_per_row, diff_res, spec_res, stats != nullptr,
+                                 as_stream(stream));
+}
+
+extern "C" int vt_trace_infer_q8_camera(const float *points, const uint8_t *diffuse, const uint8_t *specular,
+                                        uint32_t diff_res, uint32_t spec_res, const float diff_scale[3],
+                                        const float diff_offset[3], const float spec_scale[3],
+                                        const float spec_offset[3], const float *density, const uint32_t *adjacency,
+                                        const uint32_t *offsets, uint32_t num_points, const uint16_t *adj_diff,
+                                        const vt_camera *cameras, uint32_t num_images, uint32_t image_h,
+                                        uint32_t image_w, uint32_t tile_h, uint32_t tile_w,
+                                        const uint32_t *start_point, int start_per_row, float weight_threshold,
+                                        uint32_t max_intersections, float cell_skip_threshold, uint16_t *rgba,
+                                        vt_ray_stats *stats, vt_stream_t stream)
+{
+    clear_error();
+    if (num_images == 0 || image_h == 0 || image_w == 0)
+        return VT_OK;
+    int rc = check_common(points, diffuse, specular, density, adjacency, offsets, adj_diff, cameras, start_point,
+                          rgba);
+    if (rc)
+        return rc;
+    VT_REQUIRE(diff_scale && diff_offset && spec_scale && spec_offset, "null dequantisation parameters");
+    (void)num_points;
+    InferArgs a{};
+    a.points = points;
+    a.diffuse = diffuse;
+    a.specular = specular;
+    a.density = density;
+    a.adjacency = adjacency;
+    a.offsets = offsets;
+    a.adj_diff = reinterpret_cast<const uint2 *>(adj_diff);
+    a.start_point = start_point;
+    a.thr = weight_threshold;
+    a.skip = cell_skip_threshold;
+    a.max_steps = max_intersections;
+    a.rgba = rgba;
+    a.stats = reinterpret_cast<uint32_t *>(stats);
+    a.H = image_h;
+    a.W = image_w;
+    a.th = tile_h;
+    a.tw = tile_w;
+    for (int c = 0; c < 3; ++c) {
+        a.ds[c] = diff_scale[c];
+        a.dof[c] = diff_offset[c];
+        a.ss[c] = spec_scale[c];
+        a.sof[c] = spec_offset[c];
+    }
+    return render_cameras<true>(a, cameras, num_images, start_per_row, diff_res, spec_res, stats != nullptr,
+                                as_stream(stream));
 }

@@ -13,6 +13,7 @@ from __future__ import annotations
 
 from typing import Literal, Optional
 
+import numpy as np
 import torch
 
 from . import _C, _lib, native, ops
@@ -232,6 +233,62 @@ class VoroTracingInfer:
                                 start_point, weight_threshold=weight_threshold, max_intersections=max_intersections,
                                 cell_skip_threshold=cell_skip_threshold, stats=stats,
                                 tiled=self.TILE if image else None)
+
+    def camera_start_points(self, cameras, camera_buffer=None):
+        """Start cells of a camera batch: one LBVH query on each camera's centre, or
+        on each row's origin for rolling shutters (vt_camera_rays with one column)."""
+        cams = list(cameras)
+        with torch.no_grad():
+            if any(c.rolling_shutter for c in cams):
+                origins = native.camera_rays(cams, self.device, width=1, camera_buffer=camera_buffer)
+                origins = origins[..., :3].reshape(-1, 3).contiguous()
+                return self.bvh.query(self.primal_points, origins).view(torch.uint32), True
+            origins = torch.tensor(np.stack([np.asarray(c.t, np.float32) for c in cams]), device=self.device)
+            return self.bvh.query(self.primal_points, origins).view(torch.uint32), False
+
+    def render_cameras(self, cameras, weight_threshold=0.001, max_intersections=1024, cell_skip_threshold=0.0,
+                       start_point=None, stats: Optional[torch.Tensor] = None, camera_buffer=None):
+        """``render`` of the rays of a batch of ``camera.Camera`` (one image size), with
+        the rays generated inside the traversal kernel (vt_trace_infer_*_camera): no
+        rays tensor is built or read.  Returns f16 (B, H, W, 4), the image ``render``
+        gives for ``native.camera_rays(cameras)``.  ``camera_buffer``: the cameras
+        already on the device (``native.upload_cameras``)."""
+        import ctypes as C
+
+        cams = list(cameras)
+        if camera_buffer is None:
+            camera_buffer = native.upload_cameras(cams, self.device)
+        B, H, W = len(cams), cams[0].height, cams[0].width
+        if start_point is None:
+            start_point, per_row = self.camera_start_points(cams, camera_buffer)
+        else:
+            per_row = start_point.numel() == B * H and any(c.rolling_shutter for c in cams)
+        out = torch.empty((B, H, W, 4), dtype=torch.float16, device=self.device)
+        sp = native._s(self.device)
+        common = (float(weight_threshold), int(max_intersections), float(cell_skip_threshold), out.data_ptr(),
+                  native._p(stats), sp)
+        if self.quantize == "q8":
+            def v3(x):
+                vals = [float(x)] * 3 if isinstance(x, (int, float)) else [float(v) for v in x]
+                return C.cast((C.c_float * 3)(*vals), C.c_void_p)
+
+            keep = [v3(self.diff_scale), v3(self.diff_offset), v3(self.spec_scale), v3(self.spec_offset)]
+            rd = native.map_res(self.diffuse_q8.shape[-1], 3)
+            rs = native.map_res(self.specular_q8.shape[-1], 3)
+            _lib.call("vt_trace_infer_q8_camera", self.primal_points.data_ptr(), self.diffuse_q8.data_ptr(),
+                      self.specular_q8.data_ptr(), rd, rs, *keep, self.density.data_ptr(),
+                      self.point_adjacency.data_ptr(), self.point_adjacency_offsets.data_ptr(),
+                      self.primal_points.shape[0], self.adjacent_diff.data_ptr(), camera_buffer.data_ptr(), B, H, W,
+                      self.TILE[0], self.TILE[1], start_point.data_ptr(), int(per_row), *common)
+        else:
+            rd = native.map_res(self.diffuse_fp16.shape[-1], 4)
+            rs = native.map_res(self.specular_fp16.shape[-1], 4)
+            _lib.call("vt_trace_infer_f16_camera", self.primal_points.data_ptr(), self.diffuse_fp16.data_ptr(),
+                      self.specular_fp16.data_ptr(), rd, rs, self.density.data_ptr(),
+                      self.point_adjacency.data_ptr(), self.point_adjacency_offsets.data_ptr(),
+                      self.primal_points.shape[0], self.adjacent_diff.data_ptr(), camera_buffer.data_ptr(), B, H, W,
+                      self.TILE[0], self.TILE[1], start_point.data_ptr(), int(per_row), *common)
+        return out
 
     def _render_q8_native(self, rays, start_point, thr, max_int, skip, image, stats):
         import ctypes as C

@@ -102,3 +102,26 @@ def infer_q8(points, diffuse_q8, specular_q8, scales, density, adjacency, offset
               float(weight_threshold), int(max_intersections), float(cell_skip_threshold), out.data_ptr(), _p(stats),
               _s(rays.device, stream))
     return out
+
+
+def upload_cameras(cameras, device) -> torch.Tensor:
+    """The vt_camera records of a batch of ``camera.Camera`` (one image size) as a
+    device buffer (u8), the form the camera entries of the C ABI take."""
+    from .camera import pack_cameras
+
+    blob = pack_cameras(list(cameras))
+    return torch.frombuffer(bytearray(blob), dtype=torch.uint8).to(device)
+
+
+def camera_rays(cameras, device, out=None, width=None, stream=None, camera_buffer=None):
+    """Rays (B, H, W, 6) f32 of a batch of ``camera.Camera`` (one image size),
+    generated on the GPU by vt_camera_rays: the rays the camera renders trace.
+    ``width=1`` gives each row's origin (start cells of rolling shutters)."""
+    cams = list(cameras)
+    if camera_buffer is None:
+        camera_buffer = upload_cameras(cams, device)
+    H, W = cams[0].height, cams[0].width if width is None else width
+    if out is None:
+        out = torch.empty((len(cams), H, W, 6), dtype=torch.float32, device=device)
+    _lib.call("vt_camera_rays", camera_buffer.data_ptr(), len(cams), H, W, out.data_ptr(), _s(device, stream))
+    return out
