@@ -417,9 +417,86 @@ def train_c2(dev, log, cpu=False):
            "rays": 480000, "sites": sc.num_points, "dtype": "fp32",
            "workload": "C2: TraceVoroTracing forward + backward, 262,144 sites (torus + background), 4x4 fp32 "
                        "textures, one 800x600 pinhole camera, upstream dL/dRGB ~ N(0,1), thr 0.001"}
+    out["full_step"] = train_step_c2(sc, dev, rays, sp, g, log)
     if cpu:
         out["cpu_baseline"] = train_c2_cpu(model, rays, sp, g, log)
     return out
+
+
+def train_step_c2(sc, dev, rays, sp, g, log, K=10):
+    """A whole C2 training step in the trainer's structure (trainer.py:231-265): forward, backward,
+    specular regulariser gradient, Adam (eps 1e-15) over the four groups, log-density clamp.  Once with
+    the reference's pieces (TraceVoroTracing + autograd's density chain, torch's fused Adam) and once
+    with the fused ones (FusedTraceVoroTracing's one-launch epilogue, FusedVoroAdam's one-launch step).
+    The optimizer part is also timed on its own with HIP events."""
+    import numpy as np
+    import torch
+
+    from vorotracing_amd.model import VoroTracing
+    from vorotracing_amd.train import FusedVoroAdam, fused_forward
+
+    names = ("primal_points", "density", "att_diffuse", "att_specular")
+    lr0 = (2e-4, 1e-1, 2e-2, 2e-2)  # train_configs.py:23-28
+    spec_w = 1e-2  # train_configs.py:41
+    ref = VoroTracing.from_scene(sc, device=dev)
+    fus = VoroTracing.from_scene(sc, device=dev)
+    topt = torch.optim.Adam([{"params": getattr(ref, n), "lr": lr, "name": n} for n, lr in zip(names, lr0)],
+                            eps=1e-15, fused=True)
+    fopt = FusedVoroAdam(fus, *lr0[:3], specular_reg_weight=spec_w)
+    stream = torch.cuda.current_stream(dev)
+
+    def ref_step(ev=None):
+        topt.zero_grad(set_to_none=True)
+        if ev:
+            ev[0].record(stream)
+        rgba = ref(rays, start_point=sp, weight_threshold=0.001)[0]
+        if ev:
+            ev[1].record(stream)
+        rgba.backward(g)
+        if ev:
+            ev[2].record(stream)
+        spec = ref.att_specular
+        spec.grad.add_(spec.data, alpha=2.0 * spec_w / spec.numel())
+        topt.step()
+        with torch.no_grad():
+            ref.density.clamp_(max=30.0)
+        if ev:
+            ev[3].record(stream)
+
+    def fused_step(ev=None):
+        fopt.zero_grad(set_to_none=True)
+        if ev:
+            ev[0].record(stream)
+        rgba = fused_forward(fus, rays, start_point=sp, weight_threshold=0.001)[0]
+        if ev:
+            ev[1].record(stream)
+        rgba.backward(g)
+        if ev:
+            ev[2].record(stream)
+        fopt.step()
+        if ev:
+            ev[3].record(stream)
+
+    res = {}
+    for name, fn in (("reference_pieces", ref_step), ("fused", fused_step)):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(K)]
+        t = time.perf_counter()
+        for i in range(K):
+            fn(evs[i])
+        torch.cuda.synchronize()
+        part = lambda j: round(float(np.mean([e[j].elapsed_time(e[j + 1]) for e in evs])), 3)
+        res[name] = {"ms_per_step": round(1000 * (time.perf_counter() - t) / K, 3), "forward_ms": part(0),
+                     "backward_ms": part(1), "optimizer_ms": part(2)}
+    log(f"C2 full step: reference pieces {res['reference_pieces']['ms_per_step']} ms "
+        f"(optimizer {res['reference_pieces']['optimizer_ms']} ms), fused {res['fused']['ms_per_step']} ms "
+        f"(optimizer {res['fused']['optimizer_ms']} ms)")
+    res["note"] = ("forward + backward + regulariser + Adam + clamp per step (wall clock, 10 steps); forward / "
+                   "backward / optimizer: HIP events between the parts (backward includes the gradient epilogue); "
+                   "parity in tests/test_gpu_train_fused.py")
+    return res
 
 
 def train_c2_cpu(model, rays, sp, g, log):

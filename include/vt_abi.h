@@ -295,6 +295,41 @@ int vt_quantize_u8(const float *x, uint32_t rows, uint32_t cols, int per_channel
                    void *workspace, vt_stream_t stream);
 
 /*
+ * Backward epilogue of the training traversal, fused.  Replaces the
+ * nan_to_num of the four gradients in TraceVoroTracing.backward
+ * (_wrapper.py:189-198) and autograd's chain through the density activation
+ * s = a * exp(raw) (vorotracing.py:346-347): in one pass,
+ *   points/diffuse/specular gradients: NaN and +-inf -> 0, in place;
+ *   density_grad_raw = (nan_to_num(density_grad_s) * a) * exp_raw
+ *   (the operations and order of torch's MulBackward and ExpBackward).
+ * exp_raw is exp(raw) as the forward computed it.  Counts are elements.
+ */
+int vt_grad_epilogue(float *points_grad, uint64_t points_n, float *diffuse_grad, uint64_t diffuse_n,
+                     float *specular_grad, uint64_t specular_n, const float *density_grad_s, const float *exp_raw,
+                     float activation_scale, uint32_t num_points, float *density_grad_raw, vt_stream_t stream);
+
+/*
+ * Optimizer step of the trainer, fused (trainer.py:233-265): the manual
+ * regulariser gradients (specular: g += 2 w_s / numel * p; diffuse mean pull:
+ * g += 2 w_d / numel * (p - mean over the cell's R*R texels, per channel)),
+ * Adam (torch.optim.Adam: betas, eps, bias correction at `step`, counted from
+ * 1; no weight decay) over the four parameter groups, then
+ * density = min(density, density_max).  Parameters, gradients and the two
+ * moment buffers of each group are f32 in the model's layouts (points
+ * (N,3), density (N,1), diffuse (N, 3*Rd*Rd), specular (N, 3*Rs*Rs),
+ * texel-major RGB).  lr: points, density, diffuse, specular (the trainer's
+ * group order).  lr and betas are doubles: 1 - beta, the bias corrections and
+ * lr / (1 - beta1^step) are formed in double and rounded once, as torch forms
+ * them from Python floats.  Gradients are read, not written.  diff_res: 4, 8.
+ */
+int vt_adam_voro(float *points, float *points_grad, float *points_m, float *points_v, float *density,
+                 float *density_grad, float *density_m, float *density_v, float *diffuse, float *diffuse_grad,
+                 float *diffuse_m, float *diffuse_v, uint32_t diff_res, float *specular, float *specular_grad,
+                 float *specular_m, float *specular_v, uint32_t spec_res, uint32_t num_points, const double lr[4],
+                 double beta1, double beta2, float eps, uint32_t step, float specular_reg_weight,
+                 float diffuse_mean_pull_weight, float density_max, vt_stream_t stream);
+
+/*
  * Voronoi neighbours (the Delaunay adjacency) of a site set, built on the GPU.
  * Replaces the adjacency step of vorotracing.cuda.build_voronoi_adjacency
  * (cuda/__init__.py:16-46), which the reference delegates to Paragram.

@@ -44,6 +44,9 @@ SIGNATURES = {
         [I32, P, P, P, U32, U32, P, P, U32, P, U32, P, U32, U32, U32, P, P, P, U32, P, P, P, P, F32, P, P, P, P, P, F32, U32,
          P, P, P, P, P, P, P, P], C.c_int),
     "vt_math_probe": ([I32, P, P, U32, P], C.c_int),
+    "vt_grad_epilogue": ([P, C.c_uint64, P, C.c_uint64, P, C.c_uint64, P, P, F32, U32, P, P], C.c_int),
+    "vt_adam_voro": ([P, P, P, P, P, P, P, P, P, P, P, P, U32, P, P, P, P, U32, U32, P, C.c_double, C.c_double, F32,
+                      U32, F32, F32, F32, P], C.c_int),
     "vt_voronoi_workspace_size": ([U32], C.c_size_t),
     "vt_voronoi_build": ([P, U32, P, P, P, P], C.c_int),
     "vt_voronoi_adjacency": ([U32, P, P, P, P], C.c_int),

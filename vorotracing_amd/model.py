@@ -5,8 +5,9 @@ Kept: the parameters (sites, raw log-density, diffuse / specular octahedral
 logit maps), the CSR adjacency, the start-cell lookup (NNBVH, vorotracing.py:
 323-344), ``forward`` (vorotracing.py:365-419), the checkpoint dict
 (vorotracing.py:421-436 / 242-271) and the triangulation refresh
-(vorotracing.py:310-321, host Delaunay standing in for Paragram).  The
-trainer, optimizer plumbing and viewer are out of scope.
+(vorotracing.py:310-321, on the GPU Voronoi builder standing in for
+Paragram).  The trainer and viewer are out of scope; the fused backward
+epilogue and optimizer step live in train.py.
 """
 from __future__ import annotations
 
