@@ -75,6 +75,8 @@ def main():
     ap.add_argument("--profile", action="store_true", help="short run for rocprofv3 (no CPU leg, no stats)")
     ap.add_argument("--train-only", action="store_true", help="only the config-2 training step (profiling)")
     ap.add_argument("--no-voronoi", action="store_true", help="skip the GPU Voronoi adjacency build of the C3 sites")
+    ap.add_argument("--no-c5", action="store_true", help="skip the config-5 fisheye rolling-shutter training step")
+    ap.add_argument("--c5-only", action="store_true", help="only the config-5 training step")
     ap.add_argument("--voronoi-only", action="store_true", help="only the GPU Voronoi build (profiling)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run 8 device copies of 1 GiB (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -96,6 +98,9 @@ def main():
     dev = torch.device("cuda:0")
     if args.train_only:
         print(json.dumps({"train_c2": train_c2(dev, log)}), flush=True)
+        return
+    if args.c5_only:
+        print(json.dumps({"train_c5": train_c5(dev, log, cpu=not args.no_cpu)}), flush=True)
         return
     if args.copy_calib:
         src = torch.ones(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB
@@ -254,6 +259,10 @@ def main():
         result["train_c2"] = train_c2(dev, log, cpu=not args.no_cpu)
     if not args.no_voronoi and not args.profile:
         result["voronoi_c3"] = voronoi_c3(sc, dev, log)
+    if not args.no_c5 and not args.profile:
+        del model, inf, poses
+        torch.cuda.empty_cache()
+        result["train_c5"] = train_c5(dev, log, cpu=not args.no_cpu)
 
     print(json.dumps(result), flush=True)
 
@@ -499,8 +508,86 @@ def train_step_c2(sc, dev, rays, sp, g, log, K=10):
     return res
 
 
+def train_c5(dev, log, cpu=False, K=5):
+    """Config-5 training step: 3,145,728 sites of the height-field distribution,
+    one 1558x1039 equidistant-fisheye camera (k1 -0.1, k2 0.01) with a rolling shutter (origin moving 0.05
+    along x_cam over the rows), forward + backward in fp32 with dL/dRGB ~ N(0,1).  The timed step includes the
+    start-cell lookup (LBVH query of every distinct ray origin, one per row).  The adjacency comes from the GPU
+    Voronoi builder: host qhull at 3.1M sites would take minutes."""
+    import numpy as np
+    import torch
+
+    from vorotracing_amd import camera, ops, scene
+    from vorotracing_amd.model import VoroTracing
+
+    t0 = time.time()
+    vor = {}
+
+    def gpu_csr(pts):
+        p = torch.from_numpy(pts).to(dev)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        adj, off, _ = ops.build_voronoi_adjacency(p)
+        torch.cuda.synchronize()
+        vor["ms"] = round(1000 * (time.perf_counter() - t), 1)
+        return adj.cpu().numpy(), off.cpu().numpy()
+
+    sc = scene.heightfield(0, 3145728, 4, name="c5", csr_fn=gpu_csr)
+    log(f"C5 scene {time.time() - t0:.1f}s (GPU Voronoi {vor['ms']} ms, M={sc.num_faces})")
+    model = VoroTracing.from_scene(sc, device=dev)
+    rays = torch.from_numpy(camera.fisheye_rolling_rays(1558, 1039)).to(dev)
+    g = torch.from_numpy(np.random.default_rng(5).normal(size=(1039, 1558, 4)).astype(np.float32)).to(dev)
+    g[..., 3] = 0
+    stream = torch.cuda.current_stream(dev)
+    holder = {}
+
+    def step(ev=None):
+        model.zero_grad(set_to_none=True)
+        if ev:
+            ev[0].record(stream)
+        sp = model.get_starting_point(rays)
+        if ev:
+            ev[1].record(stream)
+        rgba = model(rays, start_point=sp, weight_threshold=0.001)[0]
+        if ev:
+            ev[2].record(stream)
+        rgba.backward(g)
+        if ev:
+            ev[3].record(stream)
+        holder["sp"] = sp
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(K)]
+    t = time.perf_counter()
+    for i in range(K):
+        step(evs[i])
+    torch.cuda.synchronize()
+    ms = 1000 * (time.perf_counter() - t) / K
+    part = lambda j: round(float(np.mean([e[j].elapsed_time(e[j + 1]) for e in evs])), 3)
+    out = {"fwd_bwd_ms_per_step": round(ms, 3), "start_lookup_ms": part(0), "forward_ms": part(1),
+           "backward_ms": part(2), "rays": int(rays.numel() // 6), "sites": sc.num_points, "faces": sc.num_faces,
+           "distinct_origins": int(torch.unique(rays[..., :3].reshape(-1, 3), dim=0).shape[0]), "dtype": "fp32",
+           "adjacency": f"GPU Voronoi builder ({vor['ms']} ms)",
+           "workload": "C5: TraceVoroTracing forward + backward, 3,145,728 height-field sites, 4x4 fp32 textures, "
+                       "one 1558x1039 equidistant fisheye (k1 -0.1, k2 0.01) with a 0.05 rolling shutter, "
+                       "start cells per distinct origin, dL/dRGB ~ N(0,1), thr 0.001"}
+    log(f"C5 step {ms:.2f} ms (start lookup {out['start_lookup_ms']} ms, forward {out['forward_ms']} ms, "
+        f"backward {out['backward_ms']} ms)")
+    if cpu:
+        out["cpu_baseline"] = train_cpu_step(model, rays, holder["sp"], g, log, "C5",
+                                             "one whole C5 step (1,618,762 rays)")
+    return out
+
+
 def train_c2_cpu(model, rays, sp, g, log):
     """One forward + backward of the CPU oracle on the config-2 step, timed, and compared with the GPU."""
+    return train_cpu_step(model, rays, sp, g, log, "C2", "one whole C2 step (480,000 rays)")
+
+
+def train_cpu_step(model, rays, sp, g, log, label, sample):
+    """One forward + backward of the CPU oracle on a training step, timed, and compared with the GPU."""
     import numpy as np
     import torch
 
@@ -534,10 +621,10 @@ def train_c2_cpu(model, rays, sp, g, log):
             "specular": rel(model.att_specular.grad.cpu().numpy(), bw["specular_grad"]),
             "density": rel(model.density.grad.cpu().numpy(), bw["density_grad"] * dens)}
     ms = 1000 * (t_fwd + t_bwd)
-    log(f"C2 CPU oracle: forward {t_fwd * 1e3:.0f} ms + backward {t_bwd * 1e3:.0f} ms on {cores} threads; "
+    log(f"{label} CPU oracle: forward {t_fwd * 1e3:.0f} ms + backward {t_bwd * 1e3:.0f} ms on {cores} threads; "
         f"rgba bit-identical {same}; max grad rel err {max(errs.values()):.2e}")
     return {"value": round(ms, 1), "unit": "ms/step (fwd+bwd)", "cores": cores, "kind": "port",
-            "sample": f"one whole C2 step (480,000 rays); oracle/oracle.c OpenMP on {model_name or 'host CPU'}",
+            "sample": f"{sample}; oracle/oracle.c OpenMP on {model_name or 'host CPU'}",
             "rgba_bit_identical_to_gpu": same, "grad_rel_err_vs_gpu": {k: float(f"{v:.3g}") for k, v in errs.items()}}
 
 

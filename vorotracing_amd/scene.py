@@ -129,17 +129,19 @@ def config2(seed: int = 0, n: int = 262144, R: int = 4) -> Scene:
 
 
 def heightfield(seed: int = 0, n: int = 1048576, R: int = 4, extent: float = 4.0, name: str = "c3",
-                frac_surface: float = 0.8) -> Scene:
+                frac_surface: float = 0.8, csr_fn=None) -> Scene:
     """C3/C4/C5 scene: 80% near z = 0.3 sin(3x) cos(2y) (jitter N(0,0.01)),
     20% U([-4,4]^3); raw density N(3,1) within 0.02 of the surface, N(-4,1)
-    elsewhere; diffuse N(0,1) logits; specular N(0,0.1)."""
+    elsewhere; diffuse N(0,1) logits; specular N(0,0.1).  ``csr_fn(points)``
+    supplies (adjacency, offsets) instead of host qhull (the GPU builder)."""
     rng = np.random.default_rng(seed)
     pts = _heightfield_sites(rng, n, frac_surface, extent, 0.01)
     near = np.abs(pts[:, 2] - height(pts[:, 0], pts[:, 1])) < 0.02
     raw = np.where(near, rng.normal(3.0, 1.0, n), rng.normal(-4.0, 1.0, n)).reshape(n, 1)
     diff = rng.normal(0.0, 1.0, size=(n, 3 * R * R))
     spec = rng.normal(0.0, 0.1, size=(n, 3 * R * R))
-    return _finish(name, pts, raw, diff, spec, R, R, dict(config=name, seed=seed, n=n, R=R, extent=extent))
+    csr = None if csr_fn is None else csr_fn(np.ascontiguousarray(pts, np.float32))
+    return _finish(name, pts, raw, diff, spec, R, R, dict(config=name, seed=seed, n=n, R=R, extent=extent), csr)
 
 
 def config3(seed: int = 0, n: int = 1048576, R: int = 4) -> Scene:
