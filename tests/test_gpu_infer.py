@@ -186,3 +186,31 @@ def test_infer_errors_reference_messages(gpu):
     # empty ray batch is a no-op (kernel_utils.cuh:31-34)
     out = _C.trace_vorotracing_infer(*(args[:6] + [rays[:0], start[:0], adj, empty, 0.01, 1024, 0.0]))
     assert out.shape == (0, 8, 4)
+
+
+def test_infer_f16_origins_on_sites_ragged(gpu):
+    """Rays that start exactly on their start site: the first probe point is the
+    site itself, so the probe direction falls back to the ray direction (probe_dir's
+    |hit - site| <= 1e-8 branch).  1000 rays, not a multiple of the wave size,
+    with no skip gate so that every integrated cell is shaded."""
+    s = H.small_random(600, seed=5)
+    rng = np.random.default_rng(8)
+    n = 1000
+    idx = rng.integers(0, s.points.shape[0], n)
+    d = rng.normal(size=(n, 3))
+    d /= np.linalg.norm(d, axis=1, keepdims=True)
+    rays = np.concatenate([s.points[idx], d.astype(np.float32)], axis=1).astype(np.float32).reshape(1, n, 6)
+    start = idx.astype(np.uint32).reshape(1, n)
+    dd = _dev_scene(s, gpu)
+    adj = native.prefetch(dd["points"], dd["adjacency"], dd["offsets"])
+    d4, s4 = H.f16_maps(s)
+    want, wst, _ = core.trace_infer_f16(s.points, d4, s4, 4, 4, s.density, s.adjacency, s.offsets,
+                                        adj.cpu().numpy(), rays, start, weight_threshold=0.01, want_stats=True)
+    stats = native.new_stats(n, gpu)
+    got = native.infer_f16(dd["points"], dd["diffuse4"], dd["specular4"], dd["density"], dd["adjacency"],
+                           dd["offsets"], adj, H.to_dev(rays, gpu), H.to_dev(start, gpu), weight_threshold=0.01,
+                           stats=stats)
+    torch.cuda.synchronize()
+    H.assert_stats_equal(H.stats_np(stats), wst)
+    assert (H.stats_np(stats)["integrated"] > 0).all()
+    assert np.array_equal(got.cpu().numpy().view(np.uint16), want.view(np.uint16))

@@ -451,3 +451,18 @@ def test_oct_wrap_edge_form_equals_general_on_tap_domain(R):
             if (not 0 <= u < R) != (not 0 <= v < R):
                 wu, wv = R - 1 - wu, R - 1 - wv
             assert wv * R + wu == core.oct_wrap_index(u, v, R), (u, v)
+
+
+def test_probe_length_test_on_squared_length():
+    """The inference kernel replaces probe_dir's `sqrtf(x) > 1e-8f` by
+    `x > 0x1.cd2b2ap-54f` (vt_infer.hip PROBE_LEN2_MIN); numpy's float32 sqrt
+    is correctly rounded like the kernel's, so checking every float in a wide
+    band around the boundary, and the special values, shows the two agree."""
+    x0 = np.float32(float.fromhex("0x1.cd2b2ap-54"))
+    lo, hi = np.float32(x0 / 64).view(np.int32), np.float32(x0 * 64).view(np.int32)
+    x = np.arange(lo, hi, dtype=np.int32).view(np.float32)
+    t = np.float32(1e-8)
+    assert np.array_equal(np.sqrt(x) > t, x > x0)
+    sp = np.array([0.0, -0.0, np.inf, np.nan, 1e-45, 1.0, 3e38], np.float32)
+    with np.errstate(invalid="ignore"):
+        assert np.array_equal(np.sqrt(sp) > t, sp > x0)

@@ -105,6 +105,20 @@ __device__ __forceinline__ float vt_logf(float x)
 
 __device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + vt_expf(-x)); }
 
+// LDS writes of some lanes of a wave visible to the wave's other lanes (and
+// not reordered by the compiler across the point).
+__device__ __forceinline__ void wave_lds_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+// Number of set bits of m below the calling lane.
+__device__ __forceinline__ uint32_t lane_rank(uint64_t m)
+{
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
 // Blocks are dispatched round-robin over the 8 XCDs of an MI355X, each with
 // its own L2.  Remap so that each XCD runs one contiguous range of logical
 // blocks (neighbouring rays -> neighbouring cells -> same L2).

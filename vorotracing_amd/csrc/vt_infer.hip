@@ -5,6 +5,13 @@
 // One lane per ray.  The integrators advance transmittance only for cells
 // with density > 1e-6, shade a cell only when its weight reaches the skip
 // threshold, and stop once T <= weight_threshold.
+//
+// Shading is deferred: about half the lanes of a wave shade in a given step,
+// so shading in place would run its ~250 instructions at half the lanes.
+// The integrator queues (cell, weight, offset to the probe point) in the
+// wave's LDS ring instead; when 64 entries wait, every lane shades one, and
+// each ray then adds its results in queue order, i.e. in its own step order,
+// so the colour sums are the same operations in the same order as in place.
 #include "vt_internal.h"
 #include "vt_walk.h"
 #include "vt_camera.h"
@@ -66,13 +73,39 @@ template <int RD, int RS> struct TexQ8 {
     }
 };
 
+constexpr int INFER_BLOCK = 256;
+constexpr int INFER_CHUNK = 4;
+
+// sqrtf(x) > 1e-8f exactly when x > PROBE_LEN2_MIN (sqrt is correctly rounded
+// and monotone; the constant is the largest float whose root rounds to at
+// most 1e-8f), so probe_dir's length test needs no square root.
+constexpr float PROBE_LEN2_MIN = 0x1.cd2b2ap-54f;
+
+// The pending shades of one wave: a ring of SQ_RING entries.  Lanes append
+// from inside the integrator (at most 64 per walk step); the wave shades
+// 64 at a time at the uniform point after a step (an entry's colour then
+// replaces its dv).  Plus each lane's specular taps, fixed per ray.
+constexpr uint32_t SQ_RING = 128;
+struct ShadeQueue {
+    uint32_t cell[SQ_RING];
+    float w[SQ_RING], dvx[SQ_RING], dvy[SQ_RING], dvz[SQ_RING];
+    uint8_t owner[SQ_RING];          // owner lane | 0x80 when dv is already the direction
+    unsigned long long mask[64];     // per owner lane: its entries in the batch
+    uint8_t si[64][4];               // specular taps
+    float sw[64][4];
+    uint32_t tail;                   // entries appended so far (mod 2^32)
+};
+__shared__ ShadeQueue infer_queues[INFER_BLOCK / 64];
+
+__device__ __forceinline__ ShadeQueue &wave_queue() { return infer_queues[threadIdx.x >> 6]; }
+
 // RayIntegratorOctMapInfer / ...InferQ8 (ray_integrator_octmap.cuh:315-344,
-// :487-515, colour :437-460)
+// :487-515, colour :437-460).  A cell to shade goes to the wave's queue as
+// (cell, weight, probe offset); shade_batch computes its colour.
 template <int RD, int RS, class Tex> struct InferIntegrator {
     f3 o, d;
     const float *density;
     Tex tex;
-    Bilinear spec;
     float thr, skip;
     f3 acc;
     float T;
@@ -88,20 +121,77 @@ template <int RD, int RS, class Tex> struct InferIntegrator {
         float w = T * alpha;
         if (w >= skip) {
             st.shade();
-            f3 pd = probe_dir(o, d, t0, p);
-            float u, v;
-            oct_encode<RD>(pd, u, v);
-            Bilinear db = bilinear_setup<RD>(u, v);
-            f3 a = tex.sample_diffuse(cell, db);
-            f3 b = tex.sample_specular(cell, spec);
-            f3 lg = add(a, b);
-            f3 rgb = mk(sigmoid(lg.x), sigmoid(lg.y), sigmoid(lg.z));
-            acc = vfma(w, rgb, acc);
+            // probe_dir's test len > 1e-8 on the squared length (exact, see PROBE_LEN2_MIN)
+            const f3 dv = sub(mk(fma_(t0, d.x, o.x), fma_(t0, d.y, o.y), fma_(t0, d.z, o.z)), p);
+            const bool tiny = !(dot(dv, dv) > PROBE_LEN2_MIN);
+            // the lanes appending now are exactly the active ones
+            ShadeQueue &q = wave_queue();
+            const uint64_t m = __ballot(1);
+            const uint32_t rank = lane_rank(m), tail = q.tail;
+            const uint32_t k = (tail + rank) & (SQ_RING - 1);
+            q.cell[k] = cell;
+            q.w[k] = w;
+            // component selects: a select of the two structs would take their
+            // addresses and push the integrator into scratch memory
+            q.dvx[k] = tiny ? d.x : dv.x;
+            q.dvy[k] = tiny ? d.y : dv.y;
+            q.dvz[k] = tiny ? d.z : dv.z;
+            q.owner[k] = (uint8_t)((threadIdx.x & 63u) | (tiny ? 0x80u : 0u));
+            if (rank == 0)
+                q.tail = tail + (uint32_t)__popcll(m);
         }
         T = T * (1.0f - alpha);
         return T > thr;
     }
 };
+
+// Shade entries [head, head + nb) of the ring, one per lane (probe_dir,
+// octahedral lookup of the diffuse map, the ray's specular taps, sigmoid),
+// then each owner adds its entries' colours in ring order.
+template <int RD, int RS, class Integ>
+__device__ __forceinline__ void shade_batch(ShadeQueue &q, uint32_t head, uint32_t nb, Integ &integ, int lane)
+{
+    static_assert(RS * RS <= 256, "specular tap indices are stored as bytes");
+    if ((uint32_t)lane < nb) {
+        const uint32_t k = (head + (uint32_t)lane) & (SQ_RING - 1);
+        const uint32_t ob = q.owner[k], own = ob & 63u;
+        const f3 dv = mk(q.dvx[k], q.dvy[k], q.dvz[k]);
+        const float len = (ob & 0x80u) ? 1.0f : __builtin_sqrtf(dot(dv, dv));
+        const f3 pd = (ob & 0x80u) ? dv : divs(dv, len);
+        float u, v;
+        oct_encode<RD>(pd, u, v);
+        const Bilinear db = bilinear_setup<RD>(u, v);
+        Bilinear sb;
+        sb.i00 = q.si[own][0];
+        sb.i10 = q.si[own][1];
+        sb.i01 = q.si[own][2];
+        sb.i11 = q.si[own][3];
+        sb.w00 = q.sw[own][0];
+        sb.w10 = q.sw[own][1];
+        sb.w01 = q.sw[own][2];
+        sb.w11 = q.sw[own][3];
+        const uint32_t cell = q.cell[k];
+        const f3 a = integ.tex.sample_diffuse(cell, db);
+        const f3 b = integ.tex.sample_specular(cell, sb);
+        const f3 lg = add(a, b);
+        q.dvx[k] = sigmoid(lg.x);
+        q.dvy[k] = sigmoid(lg.y);
+        q.dvz[k] = sigmoid(lg.z);
+        atomicOr(&q.mask[own], 1ull << lane);
+    }
+    wave_lds_sync();
+    unsigned long long m = q.mask[lane];
+    if (m) {
+        q.mask[lane] = 0ull;
+        do {
+            const int i = __ffsll(m) - 1;
+            m &= m - 1;
+            const uint32_t k = (head + (uint32_t)i) & (SQ_RING - 1);
+            integ.acc = vfma(q.w[k], mk(q.dvx[k], q.dvy[k], q.dvz[k]), integ.acc);
+        } while (m);
+    }
+    wave_lds_sync();
+}
 
 struct InferArgs {
     const float *points;
@@ -144,15 +234,16 @@ __device__ __forceinline__ uint32_t slot_to_ray(const InferArgs &a, uint32_t s, 
     return a.ray_perm ? a.ray_perm[s] : s;
 }
 
+
 template <int RD, int RS, bool Q8, bool STATS, int MAP, int CHUNK>
-__global__ __launch_bounds__(256) void infer_kernel(InferArgs a, uint32_t total_slots)
+__global__ __launch_bounds__(INFER_BLOCK) void infer_kernel(InferArgs a, uint32_t total_slots)
 {
-    uint32_t s = xcd_block() * blockDim.x + threadIdx.x;
-    if (s >= total_slots)
-        return;
-    uint32_t r = slot_to_ray(a, s, MAP);
-    if (r == NONE)
-        return;
+    ShadeQueue &q = wave_queue();
+    const int lane = (int)(threadIdx.x & 63u);
+    // every lane stays in the wave's loop to the end (it shades for others)
+    const uint32_t s = xcd_block() * blockDim.x + threadIdx.x;
+    const uint32_t r = s < total_slots ? slot_to_ray(a, s, MAP) : NONE;
+    bool active = r != NONE;
     using Tex = typename std::conditional<Q8, TexQ8<RD, RS>, TexF16<RD, RS>>::type;
     InferIntegrator<RD, RS, Tex> integ;
     integ.density = a.density;
@@ -172,35 +263,62 @@ __global__ __launch_bounds__(256) void infer_kernel(InferArgs a, uint32_t total_
     }
     integ.thr = a.thr;
     integ.skip = a.skip;
-    uint32_t start;
-    if constexpr (MAP == MAP_CAMERA) {
-        // the ray of pixel (u, v) of image img, normalised as load_ray does
-        const uint32_t hw = a.H * a.W, img = r / hw, rem = r - img * hw, v = rem / a.W, u = rem - v * a.W;
-        f3 dd;
-        camera_ray(a.cams[img], u, v, a.H, integ.o, dd);
-        integ.d = divs(dd, __builtin_sqrtf(dot(dd, dd)));
-        start = a.start_point[a.start_rows ? img * a.H + v : img];
-    } else {
-        load_ray(a.rays, r, integ.o, integ.d);
-        start = a.start_point[r];
-    }
-    float su, sv;
-    oct_encode<RS>(mk(-integ.d.x, -integ.d.y, -integ.d.z), su, sv);
-    integ.spec = bilinear_setup<RS>(su, sv);
     integ.acc = mk(0.0f, 0.0f, 0.0f);
     integ.T = 1.0f;
     StatsAcc<STATS> st;
-    uint32_t n = walk<CHUNK>(integ.o, integ.d, a.points, a.adjacency, a.offsets, a.adj_diff, start, a.max_steps,
-                             integ, st);
+    WalkState w;
+    if (active) {
+        uint32_t start;
+        if constexpr (MAP == MAP_CAMERA) {
+            // the ray of pixel (u, v) of image img, normalised as load_ray does
+            const uint32_t hw = a.H * a.W, img = r / hw, rem = r - img * hw, v = rem / a.W, u = rem - v * a.W;
+            f3 dd;
+            camera_ray(a.cams[img], u, v, a.H, integ.o, dd);
+            integ.d = divs(dd, __builtin_sqrtf(dot(dd, dd)));
+            start = a.start_point[a.start_rows ? img * a.H + v : img];
+        } else {
+            load_ray(a.rays, r, integ.o, integ.d);
+            start = a.start_point[r];
+        }
+        float su, sv;
+        oct_encode<RS>(mk(-integ.d.x, -integ.d.y, -integ.d.z), su, sv);
+        const Bilinear sb = bilinear_setup<RS>(su, sv);
+        q.si[lane][0] = (uint8_t)sb.i00;
+        q.si[lane][1] = (uint8_t)sb.i10;
+        q.si[lane][2] = (uint8_t)sb.i01;
+        q.si[lane][3] = (uint8_t)sb.i11;
+        q.sw[lane][0] = sb.w00;
+        q.sw[lane][1] = sb.w10;
+        q.sw[lane][2] = sb.w01;
+        q.sw[lane][3] = sb.w11;
+        walk_begin(w, a.points, start);
+    }
+    q.mask[lane] = 0ull;
+    if (lane == 0)
+        q.tail = 0;
+    wave_lds_sync();
+    uint32_t head = 0; // wave-uniform: entries shaded so far
+    while (__ballot(active)) {
+        if (active)
+            active = walk_step<CHUNK>(w, integ.o, integ.d, a.points, a.adjacency, a.offsets, a.adj_diff,
+                                      a.max_steps, integ, st);
+        wave_lds_sync();
+        if (__builtin_amdgcn_readfirstlane(q.tail) - head >= 64u) {
+            shade_batch<RD, RS>(q, head, 64, integ, lane);
+            head += 64;
+        }
+    }
+    const uint32_t rest = __builtin_amdgcn_readfirstlane(q.tail) - head;
+    if (rest)
+        shade_batch<RD, RS>(q, head, rest, integ, lane);
+    if (r == NONE)
+        return;
     uint2 out;
     out.x = (uint32_t)f2h(integ.acc.x) | ((uint32_t)f2h(integ.acc.y) << 16);
     out.y = (uint32_t)f2h(integ.acc.z) | ((uint32_t)f2h(1.0f - integ.T) << 16);
     reinterpret_cast<uint2 *>(a.rgba)[r] = out;
-    st.store(a.stats, r, n);
+    st.store(a.stats, r, w.n);
 }
-
-constexpr int INFER_BLOCK = 256;
-constexpr int INFER_CHUNK = 4;
 
 template <int RD, int RS, bool Q8, bool STATS, int MAP>
 static int launch_one(const InferArgs &a, hipStream_t stream, uint32_t slots)

@@ -91,16 +91,6 @@ constexpr int AGG_MIN = 2;
 // point_error, one point gradient
 template <int RD, int RS> constexpr int agg_floats() { return 3 * RD * RD + 3 * RS * RS + 5; }
 
-__device__ __forceinline__ void wave_lds_sync()
-{
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-}
-
-__device__ __forceinline__ uint32_t lane_rank(uint64_t m)
-{
-    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-}
 
 constexpr int AGG_ROUNDS = 32;
 
