@@ -74,7 +74,7 @@ template <int RD, int RS> struct TexQ8 {
 };
 
 constexpr int INFER_BLOCK = 256;
-constexpr int INFER_CHUNK = 4;
+constexpr int INFER_CHUNK = 8;
 
 // sqrtf(x) > 1e-8f exactly when x > PROBE_LEN2_MIN (sqrt is correctly rounded
 // and monotone; the constant is the largest float whose root rounds to at

@@ -85,6 +85,7 @@ template <typename A, int RD, int RS> struct TrainTex {
 
 constexpr int TRAIN_BLOCK = 256;
 constexpr int TRAIN_WAVES = TRAIN_BLOCK / 64;
+constexpr int TRAIN_CHUNK = 8; // face records read together per exit-face step
 constexpr int AGG_MIN = 2;
 
 // LDS floats per wave: diffuse + specular maps of one cell, density,
@@ -278,7 +279,7 @@ __global__ __launch_bounds__(TRAIN_BLOCK) void fwd_kernel(FwdArgs a)
     it.T = 1.0f;
     it.W = it.S = it.D = it.self = it.tfar = 0.0f;
     StatsAcc<STATS> st;
-    uint32_t n = walk<4>(it.o, it.d, a.points, a.adjacency, a.offsets, a.adj_diff, a.start_point[r], a.max_steps,
+    uint32_t n = walk<TRAIN_CHUNK>(it.o, it.d, a.points, a.adjacency, a.offsets, a.adj_diff, a.start_point[r], a.max_steps,
                          it, st);
     for (uint32_t i = it.qi; i < K; ++i) {
         a.depth[(size_t)r * K + i] = -1.0f;
@@ -657,7 +658,7 @@ __global__ __launch_bounds__(TRAIN_BLOCK) void bwd_kernel(BwdArgs a)
     it.dist_grad = a.distortion_grad ? a.distortion_grad[r] : 0.0f;
     it.D_total = (2.0f * fd) * it.dist_grad;
     StatsAcc<STATS> st;
-    uint32_t n = walk<4>(it.o, it.d, a.points, a.adjacency, a.offsets, a.adj_diff, a.start_point[r], a.max_steps,
+    uint32_t n = walk<TRAIN_CHUNK>(it.o, it.d, a.points, a.adjacency, a.offsets, a.adj_diff, a.start_point[r], a.max_steps,
                          it, st);
     st.store(a.stats, r, n);
 }

@@ -84,6 +84,7 @@ __device__ __forceinline__ bool walk_step(WalkState &w, f3 o, f3 d, const float 
     // num_j = (p + off_j/2 - o) . off_j, dp_j = off_j . d.  The running
     // minimum is kept as the pair (bnum, bdp) and candidates are ordered by
     // exit_before.
+    static_assert(CHUNK >= 1 && CHUNK <= 32, "reads past a list end must stay inside the 32-row padding");
     uint32_t best = NONE;
     float bnum = FIRST_BNUM, bdp = FIRST_BDP;
     for (uint32_t i = 0; i < nf; i += CHUNK) {
