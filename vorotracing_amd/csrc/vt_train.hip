@@ -206,10 +206,14 @@ template <typename A, int RD, int RS> struct FwdIntegrator {
             Attr<A>::add(contribution, cell, w);
     }
 
+    float pdens; // density of the current cell, loaded by begin_cell
+
+    __device__ __forceinline__ void begin_cell(uint32_t cell) { pdens = density[cell]; }
+
     template <class St>
     __device__ __forceinline__ bool integrate(uint32_t cell, float t0, float t1, f3 p, f3, St &st)
     {
-        float sig = density[cell];
+        float sig = pdens;
         f3 rgb = mk(0.0f, 0.0f, 0.0f);
         if (sig > 1e-6f) {
             st.shade();
@@ -489,10 +493,14 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
         }
     }
 
+    float pdens; // density of the current cell, loaded by begin_cell
+
+    __device__ __forceinline__ void begin_cell(uint32_t cell) { pdens = density[cell]; }
+
     template <class St>
     __device__ __forceinline__ bool integrate(uint32_t cell, float t0, float t1, f3 p, f3 np, St &st)
     {
-        float sig = density[cell];
+        float sig = pdens;
         f3 rgb = mk(0.0f, 0.0f, 0.0f);
         Bilinear db;
         bool has_color = false;

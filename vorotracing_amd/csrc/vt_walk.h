@@ -41,18 +41,24 @@ __device__ __forceinline__ float half_lo(uint32_t w) { return h2f((uint16_t)(w &
 __device__ __forceinline__ float half_hi(uint32_t w) { return h2f((uint16_t)(w >> 16)); }
 
 // State of one walk between steps: current cell and site, entry distance
-// t0, and the step count n of trace_octmap (tracing_octmap.cu:50-54).
+// t0, and the step count n of trace_octmap (tracing_octmap.cu:50-54); plus
+// the current cell's face-list range [b, e), loaded with its site so that a
+// step starts with one dependent load fewer.
 struct WalkState {
     uint32_t cur;
     f3 p;
     float t0;
     uint32_t n;
+    uint32_t b, e;
 };
 
-__device__ __forceinline__ void walk_begin(WalkState &w, const float *points, uint32_t start)
+__device__ __forceinline__ void walk_begin(WalkState &w, const float *points, const uint32_t *offsets,
+                                           uint32_t start)
 {
     w.cur = start;
     w.p = load_site(points, start);
+    w.b = offsets[start];
+    w.e = offsets[start + 1];
     w.t0 = 0.0f;
     w.n = 0;
 }
@@ -64,7 +70,9 @@ __device__ __forceinline__ void walk_begin(WalkState &w, const float *points, ui
 // the walk ends (step cap, no exit face, or the integrator stops it); w.n is
 // then the reference's return value.  Faces are read in chunks of CHUNK
 // records; records past the list end stay inside the 32-row padding and are
-// masked, so the choice does not depend on CHUNK.
+// masked, so the choice does not depend on CHUNK.  The integrator's
+// begin_cell(cur) runs before the face search, so that loads it issues
+// (the cell's density) overlap the search.
 template <int CHUNK, class Integrator, class StatsT>
 __device__ __forceinline__ bool walk_step(WalkState &w, f3 o, f3 d, const float *points,
                                           const uint32_t *adjacency,
@@ -75,9 +83,9 @@ __device__ __forceinline__ bool walk_step(WalkState &w, f3 o, f3 d, const float 
     if (w.n > max_steps)
         return false;
     const f3 p = w.p;
-    uint32_t b = offsets[w.cur];
-    uint32_t e = offsets[w.cur + 1];
-    uint32_t nf = e - b;
+    const uint32_t b = w.b;
+    const uint32_t nf = w.e - b;
+    integ.begin_cell(w.cur); // the integrator's own loads for the cell, issued before the face loop
     st.visit(w.cur, nf);
     const uint2 *fl = adj_diff + b;
     // Exit face = lowest index j with dp_j > 0 minimising RN(num_j / dp_j),
@@ -121,6 +129,7 @@ __device__ __forceinline__ bool walk_step(WalkState &w, f3 o, f3 d, const float 
     st.exit();
     uint32_t nxt = adjacency[b + best];
     f3 np = load_site(points, nxt);
+    const uint32_t nb = offsets[nxt], ne = offsets[nxt + 1];
     // No early return inside the integrate branch: a divergent exit there made
     // the control flow unstructured, and hipcc (packed FP32 disabled) then
     // reused np's registers inside the shading code while np was still live,
@@ -134,6 +143,8 @@ __device__ __forceinline__ bool walk_step(WalkState &w, f3 o, f3 d, const float 
     w.t0 = __builtin_fmaxf(w.t0, t1);
     w.cur = nxt;
     w.p = np;
+    w.b = nb;
+    w.e = ne;
     return go;
 }
 
@@ -146,7 +157,7 @@ __device__ __forceinline__ uint32_t walk(f3 o, f3 d, const float *points,
                                          uint32_t start, uint32_t max_steps, Integrator &integ, StatsT &st)
 {
     WalkState w;
-    walk_begin(w, points, start);
+    walk_begin(w, points, offsets, start);
     while (walk_step<CHUNK>(w, o, d, points, adjacency, offsets, adj_diff, max_steps, integ, st)) {
     }
     return w.n;
