@@ -214,3 +214,41 @@ def test_infer_f16_origins_on_sites_ragged(gpu):
     H.assert_stats_equal(H.stats_np(stats), wst)
     assert (H.stats_np(stats)["integrated"] > 0).all()
     assert np.array_equal(got.cpu().numpy().view(np.uint16), want.view(np.uint16))
+
+
+@pytest.mark.parametrize("cap", [1, 5, 13])
+def test_infer_f16_step_cap(gpu, cap):
+    """max_intersections ends walks mid-scene (tracing_octmap.cu:58-62): the step
+    count, the cells integrated up to the cap, and the shades still queued when a
+    walk stops all match the oracle, tiled and linear."""
+    s = H.mini_heightfield()
+    d = _dev_scene(s, gpu)
+    adj = native.prefetch(d["points"], d["adjacency"], d["offsets"])
+    d4, s4 = H.f16_maps(s)
+    rays = camera.orbit_rays(5, 96, 64)
+    start = H.start_for(s, rays)
+    want, wst, _ = core.trace_infer_f16(s.points, d4, s4, s.diff_res, s.spec_res, s.density, s.adjacency, s.offsets,
+                                        adj.cpu().numpy(), rays, start, weight_threshold=0.01, max_intersections=cap,
+                                        cell_skip_threshold=1e-3, want_stats=True)
+    assert (wst["n"] == cap + 1).any()  # some walks do reach the cap
+    for tiled in (None, (8, 8)):
+        stats = native.new_stats(rays.shape[0] * rays.shape[1], gpu)
+        got = native.infer_f16(d["points"], d["diffuse4"], d["specular4"], d["density"], d["adjacency"],
+                               d["offsets"], adj, H.to_dev(rays, gpu), H.to_dev(start, gpu), weight_threshold=0.01,
+                               max_intersections=cap, cell_skip_threshold=1e-3, stats=stats, tiled=tiled)
+        torch.cuda.synchronize()
+        H.assert_stats_equal(H.stats_np(stats), wst)
+        assert np.array_equal(got.cpu().numpy().view(np.uint16), want.view(np.uint16))
+
+
+def test_infer_empty_batch(gpu):
+    """A batch of zero rays launches nothing and returns an empty image."""
+    s = H.c1_scene()
+    d = _dev_scene(s, gpu)
+    adj = native.prefetch(d["points"], d["adjacency"], d["offsets"])
+    rays = torch.empty((0, 6), dtype=torch.float32, device=gpu)
+    start = H.to_dev(np.zeros(0, np.uint32), gpu)
+    got = native.infer_f16(d["points"], d["diffuse4"], d["specular4"], d["density"], d["adjacency"], d["offsets"],
+                           adj, rays, start, weight_threshold=0.01)
+    torch.cuda.synchronize()
+    assert tuple(got.shape) == (0, 4)
