@@ -88,9 +88,14 @@ constexpr int TRAIN_WAVES = TRAIN_BLOCK / 64;
 constexpr int TRAIN_CHUNK = 8; // face records read together per exit-face step
 constexpr int AGG_MIN = 2;
 
-// LDS floats per wave: diffuse + specular maps of one cell, density,
-// point_error, one point gradient
-template <int RD, int RS> constexpr int agg_floats() { return 3 * RD * RD + 3 * RS * RS + 5; }
+// LDS floats per wave: copies of (diffuse + specular maps of one cell,
+// density, point_error), then copies of one point gradient.  Members of a
+// combining group add into AGG_COPIES copies of the slice
+// (member rank mod AGG_COPIES): lanes of one cell often hit the same texels,
+// and LDS atomics to one address serialise.
+constexpr int AGG_COPIES = 2;
+template <int RD, int RS> constexpr int agg_cell_floats() { return 3 * RD * RD + 3 * RS * RS + 2; }
+template <int RD, int RS> constexpr int agg_floats() { return AGG_COPIES * (agg_cell_floats<RD, RS>() + 3); }
 
 
 constexpr int AGG_ROUNDS = 32;
@@ -377,6 +382,7 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
     float *agg; // this wave's LDS slice, agg_floats<RD, RS>() floats
 
     static constexpr int ND = 3 * RD * RD, NS = 3 * RS * RS;
+    static constexpr int NC = agg_cell_floats<RD, RS>(); // floats of one copy of the cell slice
 
     // points_grad[idx] += g, same-idx lanes combined
     __device__ __forceinline__ void scatter_point(uint32_t idx, f3 g)
@@ -387,18 +393,23 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
             if (!agg_round(idx, pending, r))
                 break;
             if (r.comb) {
-                float *pb = agg + ND + NS + 2;
+                float *pb = agg + AGG_COPIES * NC; // [copy][3]
                 if (r.mine) {
-                    atomicAdd(pb + 0, g.x);
-                    atomicAdd(pb + 1, g.y);
-                    atomicAdd(pb + 2, g.z);
+                    float *q = pb + 3 * (lane_rank(__ballot(1)) % AGG_COPIES);
+                    atomicAdd(q + 0, g.x);
+                    atomicAdd(q + 1, g.y);
+                    atomicAdd(q + 2, g.z);
                 }
                 wave_lds_sync();
                 uint64_t act = __ballot(1);
                 uint32_t nact = __popcll(act);
                 for (uint32_t k = lane_rank(act); k < 3u; k += nact) {
-                    float x = pb[k];
-                    pb[k] = 0.0f;
+                    float x = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < AGG_COPIES; ++c) {
+                        x += pb[3 * c + k];
+                        pb[3 * c + k] = 0.0f;
+                    }
                     if (x != 0.0f)
                         atomicAdd(points_grad + 3 * (size_t)r.lead + k, x);
                 }
@@ -424,6 +435,7 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
                 break;
             if (g.comb) {
                 if (g.mine) {
+                    float *agg = this->agg + NC * (lane_rank(__ballot(1)) % AGG_COPIES);
                     if (has_color) {
 #pragma unroll
                         for (int c = 0; c < 3; ++c) {
@@ -448,8 +460,12 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
                 uint64_t act = __ballot(1);
                 uint32_t nact = __popcll(act);
                 for (uint32_t k = lane_rank(act); k < (uint32_t)(ND + NS + 2); k += nact) {
-                    float x = agg[k];
-                    agg[k] = 0.0f;
+                    float x = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < AGG_COPIES; ++c) {
+                        x += agg[NC * c + k];
+                        agg[NC * c + k] = 0.0f;
+                    }
                     if (x != 0.0f) {
                         if (k < (uint32_t)ND)
                             Attr<A>::add(diffuse_grad + (size_t)g.lead * ND, k, x);
