@@ -132,6 +132,21 @@ __device__ __forceinline__ uint32_t xcd_block()
 
 __device__ __forceinline__ uint32_t xcd_block_linear() { return xcd_block() * blockDim.x + threadIdx.x; }
 
+// Blocks dealt to the 8 XCDs in chunks of C consecutive logical blocks,
+// round-robin: each XCD still sees runs of C neighbouring blocks (neighbouring
+// screen tiles share cells in its L2), but every XCD gets a share of every
+// screen region, so that one XCD does not end up with all the expensive
+// tiles of a frame.  Blocks past the last full round of 8 C keep their index.
+template <uint32_t C> __device__ __forceinline__ uint32_t xcd_interleaved_block()
+{
+    constexpr uint32_t S = 8 * C;
+    const uint32_t b = blockIdx.x, full = gridDim.x / S * S;
+    if (b >= full)
+        return b;
+    const uint32_t local = b >> 3;
+    return (local / C) * S + (b & 7u) * C + local % C;
+}
+
 // ---------------------------------------------------------------------------
 // octahedral map (ray_integrator_octmap.cuh:17-55)
 

@@ -75,6 +75,9 @@ template <int RD, int RS> struct TexQ8 {
 
 constexpr int INFER_BLOCK = 256;
 constexpr int INFER_CHUNK = 8;
+// Blocks per XCD turn (xcd_interleaved_block): with contiguous ranges per XCD
+// (xcd_block) one XCD got the costliest screen region and finished last.
+constexpr uint32_t INFER_XCD_CHUNK = 8;
 
 // sqrtf(x) > 1e-8f exactly when x > PROBE_LEN2_MIN (sqrt is correctly rounded
 // and monotone; the constant is the largest float whose root rounds to at
@@ -249,7 +252,7 @@ void infer_kernel(InferArgs a, uint32_t total_slots)
     ShadeQueue &q = wave_queue();
     const int lane = (int)(threadIdx.x & 63u);
     // every lane stays in the wave's loop to the end (it shades for others)
-    const uint32_t s = xcd_block() * blockDim.x + threadIdx.x;
+    const uint32_t s = xcd_interleaved_block<INFER_XCD_CHUNK>() * blockDim.x + threadIdx.x;
     const uint32_t r = s < total_slots ? slot_to_ray(a, s, MAP) : NONE;
     bool active = r != NONE;
     using Tex = typename std::conditional<Q8, TexQ8<RD, RS>, TexF16<RD, RS>>::type;

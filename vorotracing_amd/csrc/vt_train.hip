@@ -86,6 +86,7 @@ template <typename A, int RD, int RS> struct TrainTex {
 constexpr int TRAIN_BLOCK = 256;
 constexpr int TRAIN_WAVES = TRAIN_BLOCK / 64;
 constexpr int TRAIN_CHUNK = 8; // face records read together per exit-face step
+constexpr uint32_t TRAIN_XCD_CHUNK = 8; // blocks per XCD turn (xcd_interleaved_block)
 constexpr int AGG_MIN = 2;
 
 // LDS floats per wave: copies of (diffuse + specular maps of one cell,
@@ -263,7 +264,8 @@ __global__ __launch_bounds__(TRAIN_BLOCK) void fwd_kernel(FwdArgs a)
     __shared__ float agg_lds[TRAIN_WAVES];
     float *agg = agg_lds + threadIdx.x / 64;
     agg_clear(agg, 1);
-    uint32_t r = train_ray(xcd_block() * blockDim.x + threadIdx.x, a.num_rays, a.num_images, a.img_h, a.img_w);
+    uint32_t r = train_ray(xcd_interleaved_block<TRAIN_XCD_CHUNK>() * blockDim.x + threadIdx.x, a.num_rays, a.num_images,
+                           a.img_h, a.img_w);
     if (r == NONE)
         return;
     FwdIntegrator<A, RD, RS> it;
@@ -626,7 +628,8 @@ __global__ __launch_bounds__(TRAIN_BLOCK) void bwd_kernel(BwdArgs a)
     __shared__ float agg_lds[TRAIN_WAVES][NAGG];
     float *agg = agg_lds[threadIdx.x / 64];
     agg_clear(agg, NAGG);
-    uint32_t r = train_ray(xcd_block() * blockDim.x + threadIdx.x, a.num_rays, a.num_images, a.img_h, a.img_w);
+    uint32_t r = train_ray(xcd_interleaved_block<TRAIN_XCD_CHUNK>() * blockDim.x + threadIdx.x, a.num_rays, a.num_images,
+                           a.img_h, a.img_w);
     if (r == NONE)
         return;
     BwdIntegrator<A, RD, RS> it;

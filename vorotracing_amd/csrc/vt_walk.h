@@ -165,11 +165,11 @@ __device__ __forceinline__ uint32_t walk(f3 o, f3 d, const float *points,
 
 // Screen tiles are visited in vertical strips TILE_STRIP tiles wide (the last
 // strip takes the remainder), row by row inside a strip; 0 = row-major over
-// the whole image.  Consecutive waves, and hence the waves that run at the
-// same time on one XCD (one contiguous range of blocks, xcd_block), then
-// cover a compact screen region rather than an image-wide band.
+// the whole image.  Consecutive waves then cover a compact screen region
+// rather than an image-wide band, and so do the runs of consecutive blocks
+// that one XCD takes in turn (xcd_interleaved_block).
 #ifndef VT_TILE_STRIP
-#define VT_TILE_STRIP 16
+#define VT_TILE_STRIP 4
 #endif
 constexpr uint32_t TILE_STRIP = VT_TILE_STRIP;
 
