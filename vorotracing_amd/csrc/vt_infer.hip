@@ -73,11 +73,14 @@ template <int RD, int RS> struct TexQ8 {
     }
 };
 
-constexpr int INFER_BLOCK = 256;
+// One wave per block: a block's LDS queue is freed as soon as its wave ends.
+// With 4-wave blocks the LDS of 8 blocks filled a CU, so a block whose other
+// waves had ended kept a new one from starting until its last wave ended.
+constexpr int INFER_BLOCK = 64;
 constexpr int INFER_CHUNK = 8;
 // Blocks per XCD turn (xcd_interleaved_block): with contiguous ranges per XCD
 // (xcd_block) one XCD got the costliest screen region and finished last.
-constexpr uint32_t INFER_XCD_CHUNK = 8;
+constexpr uint32_t INFER_XCD_CHUNK = 32;
 
 // sqrtf(x) > 1e-8f exactly when x > PROBE_LEN2_MIN (sqrt is correctly rounded
 // and monotone; the constant is the largest float whose root rounds to at

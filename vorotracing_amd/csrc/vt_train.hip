@@ -83,10 +83,10 @@ template <typename A, int RD, int RS> struct TrainTex {
 // lanes scatter directly.  Only the order of the floating-point additions
 // changes (atomics have no defined order anyway).
 
-constexpr int TRAIN_BLOCK = 256;
+constexpr int TRAIN_BLOCK = 64; // one wave per block: each wave's LDS is freed when it ends
 constexpr int TRAIN_WAVES = TRAIN_BLOCK / 64;
 constexpr int TRAIN_CHUNK = 8; // face records read together per exit-face step
-constexpr uint32_t TRAIN_XCD_CHUNK = 8; // blocks per XCD turn (xcd_interleaved_block)
+constexpr uint32_t TRAIN_XCD_CHUNK = 32; // blocks per XCD turn (xcd_interleaved_block)
 constexpr int AGG_MIN = 2;
 
 // LDS floats per wave: copies of (diffuse + specular maps of one cell,
