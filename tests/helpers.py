@@ -57,3 +57,26 @@ def assert_stats_equal(got, want):
         bad = np.nonzero(got[k] != want[k])[0]
         assert bad.size == 0, f"stats field {k} differs on {bad.size} rays, first {bad[:5]}: " \
                               f"{got[k][bad[:5]]} vs {want[k][bad[:5]]}"
+
+
+def assert_infer_rgba(got, want):
+    """fp16 RGBA of an inference kernel against the oracle.
+
+    Alpha is 1 - T, which the kernels compute exactly: bit-identical.  RGB is
+    shaded with hardware approximations (rsq, rcp, exp2), so each channel may
+    sit one fp16 ulp of the oracle's value away (the north star's bound is
+    2e-3); almost all values are identical, so the mean difference stays tiny.
+    """
+    g = np.asarray(got.cpu().numpy() if hasattr(got, "cpu") else got)
+    w = np.asarray(want)
+    assert g.shape == w.shape and g.dtype == np.float16 and w.dtype == np.float16
+    assert np.array_equal(g[..., 3].view(np.uint16), w[..., 3].view(np.uint16)), "alpha differs from the oracle"
+    gr, wr = g[..., :3].astype(np.float32), w[..., :3].astype(np.float32)
+    assert np.isnan(gr).sum() == 0 and np.isnan(wr).sum() == 0
+    d = np.abs(gr - wr)
+    ulp = np.spacing(np.abs(w[..., :3])).astype(np.float32)
+    bad = np.nonzero(d > ulp)
+    assert bad[0].size == 0, f"{bad[0].size} RGB values more than one fp16 ulp from the oracle, " \
+                             f"first {gr[bad][:5]} vs {wr[bad][:5]}"
+    assert d.max(initial=0.0) <= 2e-3
+    assert d.mean() <= 1e-4 if d.size else True, f"mean |rgb - oracle| = {d.mean()}"

@@ -109,7 +109,7 @@ def test_camera_render_equals_oracle(gpu):
                              start_point=torch.from_numpy(start_rows).to(gpu), stats=st)
     torch.cuda.synchronize()
     H.assert_stats_equal(H.stats_np(st), wst)
-    assert np.array_equal(got.cpu().numpy().view(np.uint16), want.view(np.uint16))
+    H.assert_infer_rgba(got.cpu().numpy(), want)
 
 
 def test_camera_render_argument_errors(gpu):

@@ -1,10 +1,10 @@
-"""GPU parity of the inference path against the CPU oracle (bit-exact).
+"""GPU parity of the inference path against the CPU oracle.
 
-The device arithmetic restates the oracle's op for op, so visited-cell
-sequences (hash + counters), RGBA bits and per-ray statistics must be
-identical.  The north star's tolerance (2e-3 for fp16/q8) is asserted as
-well, so a failure of bit-exactness alone is distinguishable from a real
-error.
+The walk's arithmetic restates the oracle's op for op, so visited-cell
+sequences (hash + counters), per-ray statistics and the alpha channel must be
+bit-identical.  The colour of a shaded cell uses hardware approximations
+(rsq, rcp, exp2), so RGB must lie within one fp16 ulp of the oracle's value,
+inside the north star's 2e-3 for fp16/q8 (tests.helpers.assert_infer_rgba).
 """
 import numpy as np
 import pytest
@@ -65,7 +65,7 @@ def _c1_rays(W=128, Hh=128):
 
 
 @pytest.mark.parametrize("mode", ["linear", "perm48", "perm88", "tiled88"])
-def test_infer_f16_c1_bit_exact(gpu, mode):
+def test_infer_f16_c1_parity(gpu, mode):
     s = H.c1_scene()
     rays = _c1_rays()
     start = H.start_for(s, rays)
@@ -90,8 +90,7 @@ def test_infer_f16_c1_bit_exact(gpu, mode):
     torch.cuda.synchronize()
     H.assert_stats_equal(H.stats_np(stats), wst)
     g = got.cpu().numpy()
-    assert np.abs(g.astype(np.float32) - want.astype(np.float32)).max() <= 2e-3
-    assert np.array_equal(g.view(np.uint16), want.view(np.uint16))
+    H.assert_infer_rgba(g, want)
 
 
 def test_infer_f16_reference_surface(gpu):
@@ -109,7 +108,7 @@ def test_infer_f16_reference_surface(gpu):
     want, _, _ = core.trace_infer_f16(s.points, d4, s4, 4, 4, s.density, s.adjacency, s.offsets,
                                       adj.cpu().numpy(), rays, start, weight_threshold=0.01)
     assert got.shape == (64, 96, 4) and got.dtype == torch.float16
-    assert np.array_equal(got.cpu().numpy().view(np.uint16), want.view(np.uint16))
+    H.assert_infer_rgba(got, want)
 
 
 @pytest.mark.parametrize("R", [4, 8])
@@ -132,11 +131,11 @@ def test_infer_f16_mini_c3_skip(gpu, R):
                                cell_skip_threshold=1e-3, stats=stats, tiled=(8, 8))
         torch.cuda.synchronize()
         H.assert_stats_equal(H.stats_np(stats), wst)
-        assert np.array_equal(got.cpu().numpy().view(np.uint16), want.view(np.uint16))
+        H.assert_infer_rgba(got, want)
 
 
 @pytest.mark.parametrize("per_channel", [False, True])
-def test_infer_q8_bit_exact(gpu, per_channel):
+def test_infer_q8_parity(gpu, per_channel):
     s = H.mini_heightfield()
     dq, dsc, dof = host_ops.quantize_u8(s.diffuse, per_channel)
     sq, ssc, sof = host_ops.quantize_u8(s.specular, per_channel)
@@ -155,7 +154,7 @@ def test_infer_q8_bit_exact(gpu, per_channel):
                           H.to_dev(start, gpu), weight_threshold=0.01, cell_skip_threshold=1e-3, stats=stats)
     torch.cuda.synchronize()
     H.assert_stats_equal(H.stats_np(stats), wst)
-    assert np.array_equal(got.cpu().numpy().view(np.uint16), want.view(np.uint16))
+    H.assert_infer_rgba(got, want)
 
 
 def test_infer_errors_reference_messages(gpu):
@@ -213,7 +212,7 @@ def test_infer_f16_origins_on_sites_ragged(gpu):
     torch.cuda.synchronize()
     H.assert_stats_equal(H.stats_np(stats), wst)
     assert (H.stats_np(stats)["integrated"] > 0).all()
-    assert np.array_equal(got.cpu().numpy().view(np.uint16), want.view(np.uint16))
+    H.assert_infer_rgba(got, want)
 
 
 @pytest.mark.parametrize("cap", [1, 5, 13])
@@ -238,7 +237,7 @@ def test_infer_f16_step_cap(gpu, cap):
                                max_intersections=cap, cell_skip_threshold=1e-3, stats=stats, tiled=tiled)
         torch.cuda.synchronize()
         H.assert_stats_equal(H.stats_np(stats), wst)
-        assert np.array_equal(got.cpu().numpy().view(np.uint16), want.view(np.uint16))
+        H.assert_infer_rgba(got, want)
 
 
 def test_infer_empty_batch(gpu):

@@ -129,4 +129,4 @@ def test_render_q8_batch_per_camera_start(gpu):
                                   inf.spec_scale, inf.spec_offset, inf.density.reshape(-1).cpu().numpy(),
                                   inf.point_adjacency.cpu().numpy(), inf.point_adjacency_offsets.cpu().numpy(),
                                   inf.adjacent_diff.cpu().numpy(), r0, sp, weight_threshold=0.01)
-    assert np.array_equal(out[0].cpu().numpy().view(np.uint16), want.view(np.uint16))
+    H.assert_infer_rgba(out[0].cpu().numpy(), want)

@@ -258,8 +258,10 @@ template <typename A, int RD, int RS> struct FwdIntegrator {
     }
 };
 
+// 6 waves per SIMD (80 VGPRs, 12 bytes spilled) beat the 5 that 86 VGPRs
+// allow: more waves hide more of the walk's load latency.
 template <typename A, int RD, int RS, bool STATS>
-__global__ __launch_bounds__(TRAIN_BLOCK) void fwd_kernel(FwdArgs a)
+__global__ __launch_bounds__(TRAIN_BLOCK) __attribute__((amdgpu_waves_per_eu(6))) void fwd_kernel(FwdArgs a)
 {
     __shared__ float agg_lds[TRAIN_WAVES];
     float *agg = agg_lds + threadIdx.x / 64;
