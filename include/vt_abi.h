@@ -361,7 +361,13 @@ int vt_pad_3to4_f16(const float *x, uint32_t rows, uint32_t texels_per_row, uint
  * Self-test of the device arithmetic shared by restatement with the CPU
  * checker (no reference counterpart): op 0 = exp, 1 = log, 2 = f32->f16 bits
  * (out as u16 in the low half of each u32), 3 = sin and 4 = cos of the camera
- * generator (arguments in [0, pi]), applied elementwise to n floats.
+ * generator (arguments in [0, pi]), applied elementwise to n floats; op 5 =
+ * the walk's exit-face order on n records (num, dp, bnum, bdp) of 4 floats
+ * (dp, bdp > 0): out = 1 iff RN(num/dp) < RN(bnum/bdp) as the walk decides it;
+ * op 6 = the walk's exit-face search on n rows of 26 floats (site, origin,
+ * unit direction, face count <= 8 as u32 bits, 8 half4 face records as 16
+ * u32; counts above 8 read as 8), out = 2 words per row: face index
+ * (0xffffffff = none) and t1 bits.
  */
 int vt_math_probe(int op, const float *in, uint32_t *out, uint32_t n, vt_stream_t stream);
 

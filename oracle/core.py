@@ -115,6 +115,18 @@ def f32_to_f16_bits(x):
     return y
 
 
+def exit_face_rows(rows):
+    """The walk's exit-face search (tracing_octmap.cu:73-100) on (n, 26)
+    float32 rows: site, origin, unit direction, face count (uint32 bits, at
+    most 8), 8 half4 face records as 16 words.  Returns (n, 2) uint32: face
+    index (0xffffffff = none) and the bits of t1."""
+    rows = _c(rows, np.float32)
+    assert rows.ndim == 2 and rows.shape[1] == 26
+    out = np.empty((rows.shape[0], 2), np.uint32)
+    lib().or_exit_face_many(_p(rows), _sz(rows.shape[0]), _p(out))
+    return out
+
+
 def oct_wrap_index(u, v, R):
     return lib().or_oct_wrap_index(int(u), int(v), int(R))
 

@@ -351,6 +351,46 @@ static inline void dbg_visit(walk_dbg_t *g, uint32_t cell)
     g->st.visit_hash = (g->st.visit_hash ^ (uint64_t)cell) * 1099511628211ull;
 }
 
+/* Exit face of a cell with face records fl[0, nf) (tracing_octmap.cu:73-100):
+ * the lowest j with dp > 0 minimising t = ((p + off/2 - o) . off) / dp, with
+ * the reference's strict t < t_1 from t_1 = +inf.  *t1 = that t. */
+static inline uint32_t exit_face(const uint16_t *fl, uint32_t nf, v3 p, v3 o, v3 d, float *t1_out)
+{
+    float t1 = INFINITY;
+    uint32_t best = OR_NONE;
+    for (uint32_t j = 0; j < nf; ++j) {
+        const uint16_t *h = fl + 4 * (size_t)j;
+        v3 off = mk(or_f16_to_f32(h[0]), or_f16_to_f32(h[1]), or_f16_to_f32(h[2]));
+        v3 fo = mk(p.x + off.x * 0.5f, p.y + off.y * 0.5f, p.z + off.z * 0.5f);
+        float dp = vdot(off, d);
+        float t = vdot(vsub(fo, o), off) / dp;
+        if (dp > 0.0f && t < t1) {
+            t1 = t;
+            best = j;
+        }
+    }
+    *t1_out = t1;
+    return best;
+}
+
+/* rows of 26 floats: site (3), origin (3), unit direction (3), face count
+ * (u32 bits; counts above 8 read as 8), 8 face records of 4 halves (16
+ * words); out: face index and t1 bits (0 when no face) per row. */
+void or_exit_face_many(const float *rows, size_t n, uint32_t *out)
+{
+    for (size_t i = 0; i < n; ++i) {
+        const float *r = rows + 26 * i;
+        uint32_t nf = f_bits(r[9]);
+        if (nf > 8)
+            nf = 8;
+        float t1 = 0.0f;
+        uint32_t best = exit_face((const uint16_t *)(r + 10), nf, mk(r[0], r[1], r[2]), mk(r[3], r[4], r[5]),
+                                  mk(r[6], r[7], r[8]), &t1);
+        out[2 * i] = best;
+        out[2 * i + 1] = best == OR_NONE ? 0u : f_bits(t1);
+    }
+}
+
 static inline uint32_t walk(v3 o, v3 d, const float *points, const uint32_t *adjacency, const uint32_t *offsets,
                             const uint16_t *adj_diff, uint32_t start, uint32_t max_steps, integrate_fn integrate,
                             void *state, walk_dbg_t *g)
@@ -368,19 +408,8 @@ static inline uint32_t walk(v3 o, v3 d, const float *points, const uint32_t *adj
         uint32_t nf = e - b;
         dbg_visit(g, cur);
         g->st.faces += nf;
-        float t1 = INFINITY;
-        uint32_t best = OR_NONE;
-        for (uint32_t j = 0; j < nf; ++j) {
-            const uint16_t *h = adj_diff + 4 * (size_t)(b + j);
-            v3 off = mk(or_f16_to_f32(h[0]), or_f16_to_f32(h[1]), or_f16_to_f32(h[2]));
-            v3 fo = mk(p.x + off.x * 0.5f, p.y + off.y * 0.5f, p.z + off.z * 0.5f);
-            float dp = vdot(off, d);
-            float t = vdot(vsub(fo, o), off) / dp;
-            if (dp > 0.0f && t < t1) {
-                t1 = t;
-                best = j;
-            }
-        }
+        float t1;
+        uint32_t best = exit_face(adj_diff + 4 * (size_t)b, nf, p, o, d, &t1);
         if (best == OR_NONE)
             break;
         g->st.exits += 1;

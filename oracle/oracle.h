@@ -47,6 +47,9 @@ float or_f16_to_f32(uint16_t h);
 void or_expf_many(const float *x, float *y, size_t n);
 void or_logf_many(const float *x, float *y, size_t n);
 void or_f32_to_f16_many(const float *x, uint16_t *y, size_t n);
+/* the walk's exit-face search on rows of 26 floats (site, origin, direction,
+ * face count as u32 bits, 8 half4 records); out: face index, t1 bits */
+void or_exit_face_many(const float *rows, size_t n, uint32_t *out);
 int or_oct_wrap_index(int u, int v, int R);
 void or_oct_encode(const float dir[3], int R, float uv[2]);
 

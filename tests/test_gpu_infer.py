@@ -17,6 +17,36 @@ from vorotracing_amd import _C, camera, native
 pytestmark = pytest.mark.gpu
 
 
+def test_exit_order_probe(gpu):
+    """exit_before, the walk's division-free face order, against IEEE float32
+    quotients on random rows, near-ties, exact ties, subnormal and overflowing
+    quotients and NaN.  Rows whose best quotient rounds to -inf are outside its
+    contract (the walk redoes that search with IEEE quotients; see
+    test_exit_face_probe)."""
+    from tests import exit_rows as X
+    a = X.order_cases(np.random.default_rng(7))
+    with np.errstate(all="ignore"):
+        keep = ~np.isneginf(a[:, 2] / a[:, 3])
+    a = np.ascontiguousarray(a[keep])
+    got = native.math_probe(5, torch.from_numpy(a).to(gpu)).cpu().numpy()
+    want = X.order_want(a)
+    bad = np.nonzero(got.astype(bool) != want)[0]
+    assert bad.size == 0, f"{bad.size} of {len(a)} rows differ, first {a[bad[:3]]}"
+
+
+def test_exit_face_probe(gpu):
+    """The walk's exit-face search (chunked reads, exit_before, the IEEE redo
+    for quotients rounding to -inf) equals the oracle's plain search: face
+    index and t1 bits, on random cells, duplicated faces and the -inf cases."""
+    from tests import exit_rows as X
+    rows = X.face_rows(np.random.default_rng(11))
+    got = native.math_probe(6, torch.from_numpy(rows).to(gpu)).cpu().numpy()
+    want = core.exit_face_rows(rows)
+    bad = np.nonzero((got != want).any(axis=1))[0]
+    assert bad.size == 0, f"{bad.size} of {len(rows)} rows differ, first {bad[:5]}: {got[bad[:5]]} vs {want[bad[:5]]}"
+    assert (want[-13:-1, 1] == np.float32(-np.inf).view(np.uint32)).all()
+
+
 def _dev_scene(s, dev):
     d4, s4 = H.f16_maps(s)
     return dict(points=H.to_dev(s.points, dev), diffuse4=H.to_dev(d4, dev), specular4=H.to_dev(s4, dev),

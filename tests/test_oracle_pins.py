@@ -466,3 +466,29 @@ def test_probe_length_test_on_squared_length():
     sp = np.array([0.0, -0.0, np.inf, np.nan, 1e-45, 1.0, 3e38], np.float32)
     with np.errstate(invalid="ignore"):
         assert np.array_equal(np.sqrt(sp) > t, sp > x0)
+
+
+def test_exit_face_rows_closed_forms():
+    """The oracle's exit-face search on hand-made cells: a unit cube seen from
+    inside exits through the face the ray points at; a duplicated face ties
+    to the lower index; faces behind the ray (dp <= 0) are skipped; quotients
+    that round to -inf keep the first such face (strict t < t_1)."""
+    from tests import exit_rows as X
+    cube = [(2, 0, 0), (-2, 0, 0), (0, 2, 0), (0, -2, 0), (0, 0, 2), (0, 0, -2)]
+    d = np.float32([0.0, 0.0, 1.0])
+    rows = np.stack([X._row((0, 0, 0), (0, 0, 0), d, cube),
+                     X._row((0, 0, 0), (0, 0, 0), np.float32([0.0, -1.0, 0.0]), cube),
+                     X._row((0, 0, 0), (0, 0, 0), d, cube[:4] + [(0, 0, 2), (0, 0, 2)]),
+                     X._row((0, 0, 0), (0, 0, 0), d, [(2, 0, 0), (0, 0, -2)])])
+    dn = np.array([1e-9, 1.0, 1e-9])
+    dn = (dn / np.linalg.norm(dn)).astype(np.float32)
+    rows = np.concatenate([rows, np.stack([X._row((0, 0, 0), (1e30, 0, 0), dn, [(1, 0, 1), (1, 0, 0)]),
+                                           X._row((0, 0, 0), (1e30, 0, 0), dn, [(0, 1, 0), (1, 0, 1), (1, 0, 0)])])])
+    out = core.exit_face_rows(rows)
+    t1 = out[:, 1].view(np.float32)
+    assert list(out[:4, 0]) == [4, 3, 4, 0xffffffff]
+    assert t1[0] == 1.0 and t1[1] == 1.0 and t1[2] == 1.0
+    assert list(out[4:, 0]) == [0, 1] and np.all(np.isneginf(t1[4:]))
+    # exactly: face 0 of row 4 is -5e38 and face 1 is -1e39, both below -FLT_MAX
+    x0 = (0.5 - 1e30) / dn[0].astype(np.float64) / 2
+    assert x0 < -np.finfo(np.float32).max

@@ -3,6 +3,7 @@
 #include "vt_internal.h"
 #include "vt_device.h"
 #include "vt_camera.h"
+#include "vt_walk.h"
 
 #include <cstring>
 
@@ -20,11 +21,33 @@ void set_error(const char *fmt, ...)
 
 void clear_error() { g_err[0] = 0; }
 
+// op 6 rows: site p (3), origin o (3), unit direction d (3), face count nf
+// (u32 bits; counts above 8 read as 8), then 8 face records (two u32 each)
+// read as one chunk
+constexpr int PROBE_FACE_ROW = 26;
+constexpr int INFER_PROBE_CHUNK = 8;
+
 __global__ void math_probe_kernel(int op, const float *__restrict__ in, uint32_t *__restrict__ out, uint32_t n)
 {
     uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n)
         return;
+    if (op == 5) { // in holds n records (num, dp, bnum, bdp)
+        const float *r = in + 4 * (size_t)i;
+        out[i] = exit_before(r[0], r[1], r[2], r[3]) ? 1u : 0u;
+        return;
+    }
+    if (op == 6) { // in holds n rows of PROBE_FACE_ROW floats; out 2 words per row
+        const float *r = in + PROBE_FACE_ROW * (size_t)i;
+        const uint32_t nf = min(f_bits(r[9]), 8u); // the row holds 8 records
+        float t1 = 0.0f;
+        const uint32_t best = exit_face<INFER_PROBE_CHUNK>(reinterpret_cast<const uint2 *>(r + 10), nf,
+                                                             mk(r[0], r[1], r[2]), mk(r[3], r[4], r[5]),
+                                                             mk(r[6], r[7], r[8]), t1);
+        out[2 * (size_t)i] = best;
+        out[2 * (size_t)i + 1] = best == NONE ? 0u : f_bits(t1);
+        return;
+    }
     float x = in[i];
     if (op == 0)
         out[i] = f_bits(vt_expf(x));
@@ -114,7 +137,8 @@ extern "C" int vt_abi_version(void) { return 2; }
 extern "C" int vt_math_probe(int op, const float *in, uint32_t *out, uint32_t n, vt_stream_t stream)
 {
     clear_error();
-    VT_REQUIRE(op >= 0 && op <= 4, "op must be 0 (exp), 1 (log), 2 (f16), 3 (sin) or 4 (cos)");
+    VT_REQUIRE(op >= 0 && op <= 6,
+               "op must be 0 (exp), 1 (log), 2 (f16), 3 (sin), 4 (cos), 5 (exit order) or 6 (exit face)");
     if (n == 0)
         return VT_OK;
     VT_REQUIRE(in && out, "null pointer argument");

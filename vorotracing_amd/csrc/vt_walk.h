@@ -8,17 +8,27 @@ namespace vt {
 
 // Exit-face order without a division per face.  For dp, bdp > 0,
 // num/dp < bnum/bdp <=> A < B with A = num*bdp, B = bnum*dp.  The search
-// forms Q = RN(B) and gap = RN(A - Q) (one fma).  When 2^18 |gap| > |Q| and
-// 1e-26 <= |Q| < inf, the exact quotients differ by more than 2^-18 of
-// |bnum/bdp| (Q and gap each carry one rounding, 2^-24 relative), which is
-// normal here because dp, bdp <= |f16 offset| < 2^17, so the rounded
-// quotients are strictly ordered like A and B: the face exits first iff
-// gap < 0.  Every other case (near-ties, zero, overflow, NaN) compares the
-// two IEEE quotients, so the choice is the reference's
-// RN(num/dp) < RN(bnum/bdp), bit for bit.  Before the first candidate the
-// best is the pair (2^64, 2^-64): its quotient 2^128 rounds to +inf, which
-// is the reference's initial t_1, and the same test then accepts a face iff
-// RN(num/dp) < inf.
+// forms Q = RN(B), gap = RN(A - Q) (one fma) and h = RN(|Q| - 2^18 |gap|)
+// (one fma).  When h < -c (c = 1e-26f; rounding is monotone, so then
+// 2^18 |gap| > |Q| + c exactly):
+//  - Q is off B by at most max(2^-24 |Q|, 2^-150) and gap off A - Q by
+//    2^-24 |gap|, both far below |gap| > 2^-18 (|Q| + c), so A - B has the
+//    sign of gap;
+//  - |A - B| >= 0.98 * 2^-18 (|Q| + c), so the quotients x = num/dp and
+//    y = bnum/bdp differ by at least 2^-19 |y| and, as dp, bdp <= |f16
+//    offset| < 2^17, by at least 2^-18 c / 2^34 > 2^-138.  Two reals that
+//    far apart cannot round to the same finite float (one normal rounding
+//    moves 2^-24 relative, a subnormal one 2^-150), so RN(x) < RN(y) iff
+//    gap < 0.  Overflow cannot turn an accept into a tie: the largest best
+//    is 2^128 (below), and x <= 2^128 (1 - 2^-19) rounds to a finite float.
+// Every other case (near-ties, overflow, NaN: h is then NaN or >= -c)
+// compares the two IEEE quotients, so the choice is the reference's
+// RN(num/dp) < RN(bnum/bdp), bit for bit, provided RN(bnum/bdp) > -inf:
+// below -2^128 two quotients that differ by 2^-19 both round to -inf and the
+// reference keeps the first, so exit_face redoes such a search with IEEE
+// quotients.  Before the first candidate the best is the pair (2^64, 2^-64):
+// its quotient 2^128 rounds to +inf, which is the reference's initial t_1,
+// and the same test then accepts a face iff RN(num/dp) < inf.
 constexpr float FIRST_BNUM = 0x1p64f;
 constexpr float FIRST_BDP = 0x1p-64f;
 
@@ -26,11 +36,9 @@ __device__ __forceinline__ bool exit_before(float num, float dp, float bnum, flo
 {
     float Q = bnum * dp;
     float gap = fma_(num, bdp, -Q);
-    float aq = __builtin_fabsf(Q);
-    // h < 0 <=> 2^18 |gap| > |Q| (sign of one rounding); false for NaN and
-    // for |Q| = inf, which therefore need no test of their own
-    float h = fma_(__builtin_fabsf(gap), -0x1p18f, aq);
-    if (h < 0.0f && aq >= 1e-26f)
+    // false for NaN and for |Q| = inf, which therefore need no test of their own
+    float h = fma_(__builtin_fabsf(gap), -0x1p18f, __builtin_fabsf(Q));
+    if (h < -1e-26f)
         return gap < 0.0f;
     return num / dp < bnum / bdp;
 }
@@ -40,58 +48,29 @@ __device__ __forceinline__ bool exit_before(float num, float dp, float bnum, flo
 __device__ __forceinline__ float half_lo(uint32_t w) { return h2f((uint16_t)(w & 0xffffu)); }
 __device__ __forceinline__ float half_hi(uint32_t w) { return h2f((uint16_t)(w >> 16)); }
 
-// State of one walk between steps: current cell and site, entry distance
-// t0, and the step count n of trace_octmap (tracing_octmap.cu:50-54); plus
-// the current cell's face-list range [b, e), loaded with its site so that a
-// step starts with one dependent load fewer.
-struct WalkState {
-    uint32_t cur;
-    f3 p;
-    float t0;
-    uint32_t n;
-    uint32_t b, e;
-};
-
-__device__ __forceinline__ void walk_begin(WalkState &w, const float *points, const uint32_t *offsets,
-                                           uint32_t start)
+// f16 face record -> offset (ox, oy, oz) and the plane terms of the walk:
+// dp = off . d and num = (p + off/2 - o) . off.
+__device__ __forceinline__ void face_terms(uint2 r, f3 p, f3 o, f3 d, float &num, float &dp)
 {
-    w.cur = start;
-    w.p = load_site(points, start);
-    w.b = offsets[start];
-    w.e = offsets[start + 1];
-    w.t0 = 0.0f;
-    w.n = 0;
+    const float ox = half_lo(r.x), oy = half_hi(r.x), oz = half_lo(r.y);
+    dp = fma_(oz, d.z, fma_(oy, d.y, ox * d.x));
+    const float ex = fma_(ox, 0.5f, p.x) - o.x;
+    const float ey = fma_(oy, 0.5f, p.y) - o.y;
+    const float ez = fma_(oz, 0.5f, p.z) - o.z;
+    num = fma_(ez, oz, fma_(ey, oy, ex * ox));
 }
 
-// One iteration of the cell walk (tracing_octmap.cu:56-120): searches the
-// current cell's face list for the nearest bisector plane with n.d > 0
-// (lowest face index wins ties), hands [t0, t1) to the integrator when
-// t1 > t0, and moves to the neighbour behind that face.  Returns false when
-// the walk ends (step cap, no exit face, or the integrator stops it); w.n is
-// then the reference's return value.  Faces are read in chunks of CHUNK
-// records; records past the list end stay inside the 32-row padding and are
-// masked, so the choice does not depend on CHUNK.  The integrator's
-// begin_cell(cur) runs before the face search, so that loads it issues
-// (the cell's density) overlap the search.
-template <int CHUNK, class Integrator, class StatsT>
-__device__ __forceinline__ bool walk_step(WalkState &w, f3 o, f3 d, const float *points,
-                                          const uint32_t *adjacency,
-                                          const uint32_t *offsets, const uint2 *adj_diff,
-                                          uint32_t max_steps, Integrator &integ, StatsT &st)
+// The exit face of a cell whose face records are fl[0, nf): the lowest index
+// j with dp_j > 0 minimising RN(num_j / dp_j) (tracing_octmap.cu:73-100), and
+// t1 = that quotient.  NONE when no face has dp > 0 (t1 is then not set).
+// Faces are read in chunks of CHUNK records; records past the list end stay
+// inside the 32-row padding and are masked, so the choice does not depend on
+// CHUNK.
+template <int CHUNK>
+__device__ __forceinline__ uint32_t exit_face(const uint2 *fl, uint32_t nf, f3 p, f3 o, f3 d, float &t1)
 {
-    w.n++;
-    if (w.n > max_steps)
-        return false;
-    const f3 p = w.p;
-    const uint32_t b = w.b;
-    const uint32_t nf = w.e - b;
-    integ.begin_cell(w.cur); // the integrator's own loads for the cell, issued before the face loop
-    st.visit(w.cur, nf);
-    const uint2 *fl = adj_diff + b;
-    // Exit face = lowest index j with dp_j > 0 minimising RN(num_j / dp_j),
-    // num_j = (p + off_j/2 - o) . off_j, dp_j = off_j . d.  The running
-    // minimum is kept as the pair (bnum, bdp) and candidates are ordered by
-    // exit_before.
+    // The running minimum is kept as the pair (bnum, bdp) and candidates are
+    // ordered by exit_before.
     static_assert(CHUNK >= 1 && CHUNK <= 32, "reads past a list end must stay inside the 32-row padding");
     uint32_t best = NONE;
     float bnum = FIRST_BNUM, bdp = FIRST_BDP;
@@ -124,8 +103,79 @@ __device__ __forceinline__ bool walk_step(WalkState &w, f3 o, f3 d, const float 
         }
     }
     if (best == NONE)
+        return NONE;
+    t1 = bnum / bdp;
+    if (t1 == -__builtin_huge_valf()) {
+        // A quotient rounded to -inf: the reference keeps the first face that
+        // reaches it, which exit_before cannot see (see above).  Redo the
+        // search with IEEE quotients.
+        float bt = __builtin_huge_valf();
+        best = NONE;
+        for (uint32_t j = 0; j < nf; ++j) {
+            float num, dp;
+            face_terms(fl[j], p, o, d, num, dp);
+            if (dp > 0.0f) {
+                const float t = num / dp;
+                if (t < bt) {
+                    bt = t;
+                    best = j;
+                }
+            }
+        }
+        t1 = bt;
+    }
+    return best;
+}
+
+// State of one walk between steps: current cell and site, entry distance
+// t0, and the step count n of trace_octmap (tracing_octmap.cu:50-54); plus
+// the current cell's face-list range [b, e), loaded with its site so that a
+// step starts with one dependent load fewer.
+struct WalkState {
+    uint32_t cur;
+    f3 p;
+    float t0;
+    uint32_t n;
+    uint32_t b, e;
+};
+
+__device__ __forceinline__ void walk_begin(WalkState &w, const float *points, const uint32_t *offsets,
+                                           uint32_t start)
+{
+    w.cur = start;
+    w.p = load_site(points, start);
+    w.b = offsets[start];
+    w.e = offsets[start + 1];
+    w.t0 = 0.0f;
+    w.n = 0;
+}
+
+// One iteration of the cell walk (tracing_octmap.cu:56-120): searches the
+// current cell's face list for the nearest bisector plane with n.d > 0
+// (lowest face index wins ties), hands [t0, t1) to the integrator when
+// t1 > t0, and moves to the neighbour behind that face.  Returns false when
+// the walk ends (step cap, no exit face, or the integrator stops it); w.n is
+// then the reference's return value.  The integrator's
+// begin_cell(cur) runs before the face search, so that loads it issues
+// (the cell's density) overlap the search.
+template <int CHUNK, class Integrator, class StatsT>
+__device__ __forceinline__ bool walk_step(WalkState &w, f3 o, f3 d, const float *points,
+                                          const uint32_t *adjacency,
+                                          const uint32_t *offsets, const uint2 *adj_diff,
+                                          uint32_t max_steps, Integrator &integ, StatsT &st)
+{
+    w.n++;
+    if (w.n > max_steps)
         return false;
-    float t1 = bnum / bdp;
+    const f3 p = w.p;
+    const uint32_t b = w.b;
+    const uint32_t nf = w.e - b;
+    integ.begin_cell(w.cur); // the integrator's own loads for the cell, issued before the face loop
+    st.visit(w.cur, nf);
+    float t1;
+    const uint32_t best = exit_face<CHUNK>(adj_diff + b, nf, p, o, d, t1);
+    if (best == NONE)
+        return false;
     st.exit();
     uint32_t nxt = adjacency[b + best];
     f3 np = load_site(points, nxt);

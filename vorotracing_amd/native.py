@@ -40,9 +40,26 @@ def map_res(width: int, channels: int) -> int:
 
 
 def math_probe(op: int, x: torch.Tensor) -> torch.Tensor:
+    """Elementwise device arithmetic (op 0-4); for op 5 the walk's exit-face
+    order on the rows (num, dp, bnum, bdp) of an (n, 4) float32 tensor; for
+    op 6 the walk's exit-face search on the rows of an (n, 26) float32 tensor
+    (site, origin, direction, face count as int32 bits, 8 half4 records as
+    16 words), giving (face index, t1 bits) per row."""
     x = x.contiguous()
-    out = torch.empty(x.shape, dtype=torch.uint32, device=x.device)
-    _lib.call("vt_math_probe", op, x.data_ptr(), out.data_ptr(), x.numel(), _s(x.device))
+    if op == 5:
+        if x.dim() != 2 or x.size(1) != 4 or x.dtype != torch.float32:
+            raise ValueError("op 5 takes an (n, 4) float32 tensor of (num, dp, bnum, bdp)")
+        n = x.size(0)
+        out = torch.empty(n, dtype=torch.uint32, device=x.device)
+    elif op == 6:
+        if x.dim() != 2 or x.size(1) != 26 or x.dtype != torch.float32:
+            raise ValueError("op 6 takes an (n, 26) float32 tensor of exit-face rows")
+        n = x.size(0)
+        out = torch.empty((n, 2), dtype=torch.uint32, device=x.device)
+    else:
+        n = x.numel()
+        out = torch.empty(x.shape, dtype=torch.uint32, device=x.device)
+    _lib.call("vt_math_probe", op, x.data_ptr(), out.data_ptr(), n, _s(x.device))
     return out
 
 
