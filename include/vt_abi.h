@@ -244,7 +244,11 @@ int vt_trace_bwd(int attr_dtype, const float *points, const void *diffuse, const
  *   vt_bvh_build: (re)build over points (num_points, 3) f32 (nn_bvh.cu:63-89).
  *   vt_bvh_query: out[i] = index of the site nearest to queries[i] (int32,
  *   nn_bvh.cu:91-109); squared distance in fp32, ties to the lowest index.
- *   `points` must be the array the handle was built on.
+ *   `points` must be the array the handle was built on.  Up to 2^26
+ *   query-site pairs (a frame's camera origins) a query scans all sites
+ *   instead of walking the tree (same distances, same answer), keeping
+ *   per-block partials in the handle's workspace: builds and queries of one
+ *   handle must be ordered on one stream.
  *   vt_bvh_destroy: free the handle (nn_bvh.cu:53-61).
  */
 int vt_bvh_create(void **handle);

@@ -14,7 +14,9 @@ from vorotracing_amd.model import VoroTracing
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("n,nq,seed", [(1, 5, 0), (2, 50, 1), (37, 300, 2), (5000, 20000, 3), (200000, 50000, 4)])
+# up to 2^26 query-site pairs the query scans all sites, above it walks the tree
+@pytest.mark.parametrize("n,nq,seed", [(1, 5, 0), (2, 50, 1), (37, 300, 2), (300000, 3, 5), (5000, 20000, 3),
+                                       (200000, 50000, 4)])
 def test_bvh_exact_nearest(gpu, n, nq, seed):
     rng = np.random.default_rng(seed)
     pts = rng.normal(size=(n, 3)).astype(np.float32) * rng.uniform(0.1, 3.0, size=(1, 3)).astype(np.float32)

@@ -238,6 +238,89 @@ __global__ __launch_bounds__(256) void bvh_query_kernel(const BvhNode *__restric
     out[qi] = (int32_t)best_i;
 }
 
+// Few queries (num_queries * num_points <= NN_SCAN_PAIRS, e.g. the one camera
+// origin of a pinhole frame): the tree walk is a chain of dependent loads on
+// one lane (about 37 us for 1M sites), while a scan of all sites by the whole
+// GPU reads 12 bytes per site once.  Same squared distance and the same
+// lowest-index rule as the tree, so the answer is the same site.
+constexpr uint64_t NN_SCAN_PAIRS = 1ull << 26;
+constexpr int NN_SCAN_BLOCK = 256;
+constexpr uint32_t NN_SCAN_BLOCKS = 256; // per query
+
+__device__ __forceinline__ bool nn_better(float d, uint32_t i, float bd, uint32_t bi)
+{
+    return d < bd || (d == bd && i < bi);
+}
+
+// partial[q * NN_SCAN_BLOCKS + block] = (squared distance bits, site) of the
+// nearest site among the sites this block strides over; grid (blocks, queries)
+__global__ __launch_bounds__(NN_SCAN_BLOCK) void nn_scan_kernel(const float *__restrict__ points, uint32_t n,
+                                                                const float *__restrict__ queries,
+                                                                uint2 *__restrict__ partial)
+{
+    __shared__ float sd[NN_SCAN_BLOCK / 64];
+    __shared__ uint32_t si[NN_SCAN_BLOCK / 64];
+    const uint32_t qi = blockIdx.y;
+    const f3 q = load_site(queries, qi);
+    float best = __builtin_huge_valf();
+    uint32_t bi = NONE;
+    for (uint32_t i = blockIdx.x * NN_SCAN_BLOCK + threadIdx.x; i < n; i += NN_SCAN_BLOCKS * NN_SCAN_BLOCK) {
+        const f3 df = sub(q, load_site(points, i));
+        const float d2 = dot(df, df);
+        if (d2 < best) { // i increases along the stride, so ties keep the lower index
+            best = d2;
+            bi = i;
+        }
+    }
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float od = __shfl_xor(best, o, 64);
+        const uint32_t oi = __shfl_xor(bi, o, 64);
+        if (nn_better(od, oi, best, bi)) {
+            best = od;
+            bi = oi;
+        }
+    }
+    const uint32_t wv = threadIdx.x >> 6;
+    if ((threadIdx.x & 63u) == 0) {
+        sd[wv] = best;
+        si[wv] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (uint32_t k = 1; k < NN_SCAN_BLOCK / 64; ++k)
+            if (nn_better(sd[k], si[k], best, bi)) {
+                best = sd[k];
+                bi = si[k];
+            }
+        partial[(size_t)qi * NN_SCAN_BLOCKS + blockIdx.x] = make_uint2(f_bits(best), bi);
+    }
+}
+
+// out[q] = the best of the query's NN_SCAN_BLOCKS partials; one wave per query
+__global__ __launch_bounds__(64) void nn_pick_kernel(const uint2 *__restrict__ partial, int32_t *__restrict__ out)
+{
+    const uint32_t qi = blockIdx.x;
+    float best = __builtin_huge_valf();
+    uint32_t bi = NONE;
+    for (uint32_t k = threadIdx.x; k < NN_SCAN_BLOCKS; k += 64) {
+        const uint2 p = partial[(size_t)qi * NN_SCAN_BLOCKS + k];
+        if (nn_better(bits_f(p.x), p.y, best, bi)) {
+            best = bits_f(p.x);
+            bi = p.y;
+        }
+    }
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float od = __shfl_xor(best, o, 64);
+        const uint32_t oi = __shfl_xor(bi, o, 64);
+        if (nn_better(od, oi, best, bi)) {
+            best = od;
+            bi = oi;
+        }
+    }
+    if (threadIdx.x == 0)
+        out[qi] = (int32_t)bi;
+}
+
 static int ensure_capacity(BvhHandle *h, uint32_t n)
 {
     if (n <= h->cap && h->nodes)
@@ -340,6 +423,19 @@ extern "C" int vt_bvh_query(void *handle, const float *points, uint32_t num_poin
     if (num_queries == 0)
         return VT_OK;
     VT_REQUIRE(points && queries && out, "null pointer argument");
+    if ((uint64_t)num_queries * h->n <= NN_SCAN_PAIRS && num_queries <= 65535u) {
+        // the partials live in the handle's workspace when it has room
+        const size_t need = (size_t)num_queries * NN_SCAN_BLOCKS * 2;
+        if (need <= h->ws_words) {
+            uint2 *partial = reinterpret_cast<uint2 *>(h->ws);
+            nn_scan_kernel<<<dim3(NN_SCAN_BLOCKS, num_queries), NN_SCAN_BLOCK, 0, as_stream(stream)>>>(
+                points, h->n, queries, partial);
+            VT_LAUNCH_CHECK("nn_scan_kernel");
+            nn_pick_kernel<<<num_queries, 64, 0, as_stream(stream)>>>(partial, out);
+            VT_LAUNCH_CHECK("nn_pick_kernel");
+            return VT_OK;
+        }
+    }
     bvh_query_kernel<<<(num_queries + 255) / 256, 256, 0, as_stream(stream)>>>(h->nodes, h->leaf_idx, h->n, points,
                                                                              queries, num_queries, out);
     VT_LAUNCH_CHECK("bvh_query_kernel");
