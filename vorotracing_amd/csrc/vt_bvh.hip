@@ -245,7 +245,7 @@ __global__ __launch_bounds__(256) void bvh_query_kernel(const BvhNode *__restric
 // lowest-index rule as the tree, so the answer is the same site.
 constexpr uint64_t NN_SCAN_PAIRS = 1ull << 26;
 constexpr int NN_SCAN_BLOCK = 256;
-constexpr uint32_t NN_SCAN_BLOCKS = 256; // per query
+constexpr uint32_t NN_SCAN_BLOCKS = 1024; // per query
 
 __device__ __forceinline__ bool nn_better(float d, uint32_t i, float bd, uint32_t bi)
 {
