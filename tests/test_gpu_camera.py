@@ -14,13 +14,6 @@ from vorotracing_amd.model import VoroTracing
 
 pytestmark = pytest.mark.gpu
 
-# The camera renders' launches aborted while the infer_kernel signature depended on an unnamed
-# enum (host and device mangled it differently, so the launch found no kernel).  The cause was
-# shown and fixed on the CPU (tests/test_abi.py::test_every_device_kernel_has_its_host_launch_symbol);
-# the renders stay off the GPU until a run that may test that fix.
-HELD_OFF = pytest.mark.skip(reason="camera render launches aborted before the kernel-name fix; held off the GPU "
-                                   "until a run that may test the fix")
-
 
 def _cams(kind, W, Hh):
     if kind == "orbit":
@@ -60,7 +53,6 @@ def _infer(gpu, quantize):
     return VoroTracingInfer(model, sort_morton=True, quantize=quantize)
 
 
-@HELD_OFF
 @pytest.mark.parametrize("quantize", ["fp16", "q8"])
 @pytest.mark.parametrize("kind", ["orbit", "fisheye_rolling", "many"])
 def test_camera_render_equals_buffer_render(gpu, quantize, kind):
@@ -85,7 +77,6 @@ def test_camera_render_equals_buffer_render(gpu, quantize, kind):
     assert (H.stats_np(st_cam)["integrated"] > 0).mean() > 0.3  # the cameras see the scene
 
 
-@HELD_OFF
 def test_camera_render_equals_oracle(gpu):
     """fp16 camera render of a fisheye rolling-shutter camera against the oracle
     rendering the oracle's own rays from the oracle's start cells."""
