@@ -80,3 +80,45 @@ def assert_infer_rgba(got, want):
                              f"first {gr[bad][:5]} vs {wr[bad][:5]}"
     assert d.max(initial=0.0) <= 2e-3
     assert d.mean() <= 1e-4 if d.size else True, f"mean |rgb - oracle| = {d.mean()}"
+
+
+def nn_tie_set(n=300000, seed=11):
+    """Sites and queries whose nearest sites tie, for the all-sites scan of the
+    start-cell lookup (1024 blocks x 256 lanes stride over the sites, so site i
+    and i + 262144 fall on one lane, i and i + 256 on two blocks, i and i + 64
+    on two waves of a block, i and i + 1 on two lanes of a wave).
+
+    Background sites lie in [5, 9]^3; tie groups sit near x in [-3, 3]:
+    exact duplicates at index pairs and triples of each spacing above, and
+    pairs exactly equidistant (offsets of +-0.25 along one axis, exact in
+    fp32) from their query.  Returns (points (n,3) f32, queries (q,3) f32)."""
+    rng = np.random.default_rng(seed)
+    pts = rng.uniform(5.0, 9.0, size=(n, 3)).astype(np.float32)
+    queries = []
+    spacings = [1, 64, 256, 256 * 1023, 262144, 7, 300]
+    base = 1000
+    g = 0
+    for sp in spacings:
+        for reps in (2, 3):
+            idx = [base + k * sp for k in range(reps)]
+            if idx[-1] >= n:
+                continue
+            c = np.array([-3.0 + 0.25 * g, 0.5, -0.5], np.float32)
+            for i in idx:
+                pts[i] = c
+            queries.append(c)                                   # distance 0 to every copy
+            queries.append(c + np.float32([0.0, 0.03125, 0.0]))  # equal distance to every copy
+            base += 17
+            g += 1
+    for e, sp in enumerate((1, 64, 256, 262144)):
+        lo, hi = base, base + sp
+        if hi >= n:
+            continue
+        c = np.array([-3.0 + 1.0 * e, -1.5, 1.0], np.float32)  # groups 1.0 apart: no site of one near another
+        off = np.float32([0.25, 0.0, 0.0])
+        # the higher index on the - side in every other group: the rule must not depend on the side
+        pts[lo], pts[hi] = (c + off, c - off) if g % 2 else (c - off, c + off)
+        queries.append(c)
+        base += 17
+        g += 1
+    return pts, np.stack(queries).astype(np.float32)

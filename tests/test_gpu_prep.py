@@ -50,6 +50,25 @@ def test_bvh_ties_lowest_index(gpu):
     assert np.array_equal(_C.nearest_neighbor_bvh(H.to_dev(pts2, gpu), H.to_dev(q, gpu)).cpu().numpy(), got)
 
 
+@pytest.mark.parametrize("path", ["scan", "tree"])
+def test_bvh_ties_across_strides_and_blocks(gpu, path):
+    """Duplicate and equidistant sites at index spacings of a lane, a wave, a
+    block and a whole scan stride (300,000 sites): the lowest index wins on the
+    all-sites scan (28 queries) and on the tree walk (the same queries repeated
+    past 2^26 query-site pairs)."""
+    pts, q = H.nn_tie_set()
+    if path == "tree":
+        q = np.tile(q, (10, 1))
+        assert q.shape[0] * pts.shape[0] > (1 << 26)
+    else:
+        assert q.shape[0] * pts.shape[0] <= (1 << 26)
+    bvh = ops.NNBVH()
+    pd = H.to_dev(pts, gpu)
+    bvh.build(pd)
+    got = bvh.query(pd, H.to_dev(q, gpu)).cpu().numpy()
+    assert np.array_equal(got, host_ops.nearest_site(pts, q))
+
+
 def test_morton_reorder_matches_restatement(gpu):
     s = H.mini_heightfield()
     model = VoroTracing.from_scene(s, device=gpu)
