@@ -259,6 +259,21 @@ int vt_bvh_query(void *handle, const float *points, uint32_t num_points, const f
 int vt_bvh_num_nodes(void *handle);
 
 /*
+ * Allocation-free nearest-site lookup.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops).  out[i] = index of the site nearest to
+ * queries[i] (int32), the answer vt_bvh_query gives (squared distance in
+ * fp32, ties to the lowest index), computed by a scan of all num_points sites
+ * without a handle.  At most 64 queries per call (512 KiB of per-block
+ * partials in a static device array that each GPU holds until the process
+ * ends); more is rejected with VT_ERR_INVALID.  No hipMalloc or hipFree.
+ * Every call on one GPU shares that array: calls that overlap on one GPU
+ * (concurrent streams, threads) race; order them on one stream.
+ */
+int vt_nearest_sites_noalloc(const float *points, uint32_t num_points, const float *queries, uint32_t num_queries,
+                             int32_t *out, vt_stream_t stream);
+
+/*
  * Morton reorder of cells.  Replaces VoroTracingInfer._reorder_by_morton
  * (vorotracing.py:514-571): 10-bit-per-axis Morton keys of the sites in their
  * bounding box, stable sort (the reference's argsort leaves ties unordered),

@@ -26,7 +26,7 @@ def _declarations():
 
 def test_header_declarations_parsed():
     d = _declarations()
-    assert len(d) == 30, sorted(d)
+    assert len(d) == 31, sorted(d)
     for name in ("vt_trace_infer_f16", "vt_trace_fwd", "vt_trace_bwd", "vt_bvh_query", "vt_morton_reorder"):
         assert name in d
 
@@ -60,6 +60,10 @@ def test_argument_errors_need_no_gpu():
     assert b"null pointer" in lib.vt_last_error()
     with pytest.raises(_lib.VTError, match="null"):
         _lib.check(rc, "vt_trace_infer_f16_tiled")
+    # the allocation-free lookup rejects more queries than its scratch holds before touching a device
+    rc = lib.vt_nearest_sites_noalloc(None, 1000, None, 65, None, None)
+    assert rc == 1
+    assert b"exceed its scratch capacity of 64" in lib.vt_last_error()
 
 
 def test_every_device_kernel_has_its_host_launch_symbol(tmp_path):

@@ -12,6 +12,8 @@
 #include "vt_prims.h"
 #include "vt_device.h"
 
+#include <mutex>
+
 namespace vt {
 
 struct BvhNode {          // 64 bytes
@@ -439,6 +441,69 @@ extern "C" int vt_bvh_query(void *handle, const float *points, uint32_t num_poin
     bvh_query_kernel<<<(num_queries + 255) / 256, 256, 0, as_stream(stream)>>>(h->nodes, h->leaf_idx, h->n, points,
                                                                              queries, num_queries, out);
     VT_LAUNCH_CHECK("bvh_query_kernel");
+    return VT_OK;
+}
+
+// ---- allocation-free nearest-site scan -------------------------------------
+//
+// The few-query path of vt_bvh_query (nn_scan_kernel + nn_pick_kernel) with
+// its per-block partials in a file-scope device array instead of a handle's
+// hipMalloc'd workspace, for callers that cannot allocate (code under HIP
+// graph capture, serving loops).  Every partial is written by the scan before
+// the pick reads it, so the array needs no clearing.  One array per GPU,
+// shared by every call on that GPU: calls that overlap on one GPU race.
+
+namespace vt {
+
+constexpr uint32_t NN_NOALLOC_MAX_QUERIES = 64;
+static __device__ __align__(256) uint2 scratch[NN_NOALLOC_MAX_QUERIES * NN_SCAN_BLOCKS]; // 512 KiB
+
+constexpr int NN_NOALLOC_MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static uint2 *g_scratch_ptr[NN_NOALLOC_MAX_DEVICES];
+
+// Device address of the current device's copy of `scratch`, looked up once
+// per device with that device current (host code never uses the symbol's
+// host-side name as an address).
+static int scratch_ptr_current_device(uint2 **out)
+{
+    int dev = -1;
+    VT_HIP_CHECK(hipGetDevice(&dev));
+    VT_REQUIRE(dev >= 0 && dev < NN_NOALLOC_MAX_DEVICES, "device ordinal %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        VT_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        VT_REQUIRE(p != nullptr, "scratch symbol has no device address");
+        g_scratch_ptr[dev] = reinterpret_cast<uint2 *>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return VT_OK;
+}
+
+} // namespace vt
+
+extern "C" int vt_nearest_sites_noalloc(const float *points, uint32_t num_points, const float *queries,
+                                        uint32_t num_queries, int32_t *out, vt_stream_t stream)
+{
+    clear_error();
+    if (num_queries == 0)
+        return VT_OK;
+    VT_REQUIRE(num_queries <= NN_NOALLOC_MAX_QUERIES,
+               "vt_nearest_sites_noalloc: %u queries exceed its scratch capacity of %u queries", num_queries,
+               NN_NOALLOC_MAX_QUERIES);
+    VT_REQUIRE(num_points > 0, "no points to search");
+    VT_REQUIRE(num_points < 0x7fffffffu, "too many points");
+    VT_REQUIRE(points && queries && out, "null pointer argument");
+    uint2 *partial = nullptr;
+    int rc = scratch_ptr_current_device(&partial);
+    if (rc)
+        return rc;
+    nn_scan_kernel<<<dim3(NN_SCAN_BLOCKS, num_queries), NN_SCAN_BLOCK, 0, as_stream(stream)>>>(points, num_points,
+                                                                                              queries, partial);
+    VT_LAUNCH_CHECK("nn_scan_kernel");
+    nn_pick_kernel<<<num_queries, 64, 0, as_stream(stream)>>>(partial, out);
+    VT_LAUNCH_CHECK("nn_pick_kernel");
     return VT_OK;
 }
 
