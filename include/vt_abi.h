@@ -257,6 +257,11 @@ int vt_bvh_build(void *handle, const float *points, uint32_t num_points, vt_stre
 int vt_bvh_query(void *handle, const float *points, uint32_t num_points, const float *queries, uint32_t num_queries,
                  int32_t *out, vt_stream_t stream);
 int vt_bvh_num_nodes(void *handle);
+/* Test hook (no reference counterpart): caps the tree walk's stack at `limit`
+ * entries (1..64; 0 restores 64) and, if force_tree, makes every query walk
+ * the tree.  A query whose stack would overflow answers by a scan of all
+ * sites (same distance and tie rule), so a capped stack reaches that path. */
+int vt_bvh_debug_stack_limit(void *handle, uint32_t limit, int force_tree);
 
 /*
  * Allocation-free nearest-site lookup.  No counterpart in the reference: it

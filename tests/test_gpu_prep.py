@@ -69,6 +69,52 @@ def test_bvh_ties_across_strides_and_blocks(gpu, path):
     assert np.array_equal(got, host_ops.nearest_site(pts, q))
 
 
+@pytest.mark.parametrize("limit", [1, 2, 5])
+def test_bvh_stack_overflow_answers_exactly(gpu, limit):
+    """A query whose traversal stack would overflow answers by a scan of all
+    sites instead of dropping a subtree.  The stack is capped from the host
+    (test hook) so the tree walk reaches that path on an ordinary tree."""
+    import ctypes as C
+
+    rng = np.random.default_rng(20 + limit)
+    pts = rng.normal(size=(20000, 3)).astype(np.float32)
+    pts[100:110] = pts[5000]  # duplicates: ties to the lowest index through the fallback too
+    q = np.concatenate([rng.normal(size=(700, 3)).astype(np.float32), pts[[5000, 100, 7]]])
+    pd, qd = H.to_dev(pts, gpu), H.to_dev(q, gpu)
+    h = C.c_void_p()
+    _lib.call("vt_bvh_create", C.byref(h))
+    try:
+        s = torch.cuda.current_stream(gpu).cuda_stream
+        _lib.call("vt_bvh_build", h, pd.data_ptr(), pts.shape[0], s)
+        _lib.call("vt_bvh_debug_stack_limit", h, limit, 1)
+        out = torch.full((q.shape[0],), -7, dtype=torch.int32, device=gpu)
+        _lib.call("vt_bvh_query", h, pd.data_ptr(), pts.shape[0], qd.data_ptr(), q.shape[0], out.data_ptr(), s)
+        torch.cuda.synchronize()
+        with pytest.raises(_lib.VTError, match="above the compiled 64"):
+            _lib.call("vt_bvh_debug_stack_limit", h, 65, 1)
+    finally:
+        _lib.load().vt_bvh_destroy(h)
+    assert np.array_equal(out.cpu().numpy(), host_ops.nearest_site(pts, q))
+
+
+def test_short_adjacent_diff_rejected(gpu):
+    """The walk reads face records 8 at a time past a list end: an adjacent_diff
+    shorter than the prefetch layout (adjacency rows + 32) is refused."""
+    s = H.small_random()
+    pts, adj, off = H.to_dev(s.points, gpu), H.to_dev(s.adjacency, gpu), H.to_dev(s.offsets, gpu)
+    ad = _C.trace_vorotracing_prefetch_adj(pts, adj, off)
+    assert ad.shape[0] == adj.shape[0] + 32
+    d4, s4 = (H.to_dev(m, gpu) for m in H.f16_maps(s))
+    rays = H.to_dev(camera.pinhole_rays(8, 8, eye=(0.0, -3.0, 0.2)), gpu)
+    sp = torch.zeros(rays.shape[:-1], dtype=torch.uint32, device=gpu)
+    dens = H.to_dev(s.density.reshape(-1), gpu)
+    empty = torch.empty(0, dtype=torch.int32, device=gpu)
+    with pytest.raises(RuntimeError, match="adjacency_size \\+ 32 rows"):
+        _C.trace_vorotracing_infer(pts, d4, s4, dens, adj, off, rays, sp, ad[:-1].contiguous(), empty, 0.01, 1024, 0.0)
+    _C.trace_vorotracing_infer(pts, d4, s4, dens, adj, off, rays, sp, ad, empty, 0.01, 1024, 0.0)
+    torch.cuda.synchronize()
+
+
 def test_morton_reorder_matches_restatement(gpu):
     s = H.mini_heightfield()
     model = VoroTracing.from_scene(s, device=gpu)

@@ -148,8 +148,12 @@ def _check_infer_shapes(num_points, num_rays, diffuse, specular, density, start_
     _assert(start_point.numel() == num_rays, "start_point must have the same batch size as rays")
     _assert(adjacent_diff.dim() == 2 and adjacent_diff.size(1) == 4 and adjacent_diff.dtype == torch.float16,
             "adjacent_diff must be float16 (adjacency_size + 32, 4)")
-    _assert(adjacent_diff.size(0) >= adjacency.size(0) + 4, "adjacent_diff has fewer rows than adjacency + padding")
-    _assert(adjacency.numel() >= 4, "point_adjacency must carry the 32-entry padding")
+    # The walk reads face records 8 at a time, up to 7 rows past the last
+    # list end (offsets[-1] <= adjacency rows); the reference's prefetch
+    # allocates adjacency rows + 32 (tracing_octmap.cu:623-624), which covers
+    # that reach without a device read of offsets[-1].
+    _assert(adjacent_diff.size(0) >= adjacency.size(0) + 32,
+            "adjacent_diff must have adjacency_size + 32 rows (the prefetch_adj layout)")
 
 
 def trace_vorotracing_infer_q8(points_in, diffuse_in, specular_in, density_in, point_adjacency_in,

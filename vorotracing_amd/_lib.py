@@ -55,6 +55,7 @@ SIGNATURES = {
     "vt_bvh_build": ([P, P, U32, P], C.c_int),
     "vt_bvh_query": ([P, P, U32, P, U32, P, P], C.c_int),
     "vt_bvh_num_nodes": ([P], C.c_int),
+    "vt_bvh_debug_stack_limit": ([P, U32, I32], C.c_int),
     "vt_nearest_sites_noalloc": ([P, U32, P, U32, P, P], C.c_int),
     "vt_tile_perm": ([U32, U32, U32, U32, P, P], C.c_int),
     "vt_morton_workspace_size": ([U32, U32], C.c_size_t),

@@ -34,6 +34,8 @@ struct BvhHandle {
     uint32_t *ws = nullptr;
     size_t ws_words = 0;
     float *bb = nullptr;
+    uint32_t stack_limit = 64; // traversal stack entries a query may use (test hook)
+    bool force_tree = false;   // queries always walk the tree (test hook)
 };
 
 __device__ __forceinline__ int bvh_delta(const uint32_t *__restrict__ keys, uint32_t n, int i, int j)
@@ -173,7 +175,7 @@ __global__ __launch_bounds__(256) void bvh_query_kernel(const BvhNode *__restric
                                                         const uint32_t *__restrict__ leaf_idx, uint32_t n,
                                                         const float *__restrict__ points,
                                                         const float *__restrict__ queries, uint32_t nq,
-                                                        int32_t *__restrict__ out)
+                                                        int32_t *__restrict__ out, uint32_t stack_limit)
 {
     uint32_t qi = xcd_block_linear();
     if (qi >= nq)
@@ -190,6 +192,7 @@ __global__ __launch_bounds__(256) void bvh_query_kernel(const BvhNode *__restric
             best_i = idx;
         }
     };
+    bool overflow = false;
     if (n == 1) {
         visit_leaf(0);
     } else {
@@ -220,20 +223,40 @@ __global__ __launch_bounds__(256) void bvh_query_kernel(const BvhNode *__restric
             if (box_may_hold(d1, best)) {
                 if (c1 & LEAF)
                     visit_leaf(c1 & ~LEAF);
-                else if (sp < BVH_STACK) {
+                else if (sp < (int)stack_limit) {
                     stack[sp] = c1;
                     sdist[sp] = d1;
                     sp++;
+                } else {
+                    overflow = true;
                 }
             }
             if (box_may_hold(d0, best)) {
                 if (c0 & LEAF)
                     visit_leaf(c0 & ~LEAF);
-                else if (sp < BVH_STACK) {
+                else if (sp < (int)stack_limit) {
                     stack[sp] = c0;
                     sdist[sp] = d0;
                     sp++;
+                } else {
+                    overflow = true;
                 }
+            }
+        }
+    }
+    if (overflow) {
+        // A subtree was not searched (stack full: cannot happen while the
+        // tree is at most 30 + 31 levels deep, i.e. n < 2^31, but a wrong
+        // start cell must never be returned): answer by a scan of all sites,
+        // with the same distance and tie rule.
+        best = __builtin_huge_valf();
+        best_i = NONE;
+        for (uint32_t k = 0; k < n; ++k) {
+            const f3 df = sub(q, load_site(points, k));
+            const float d2 = dot(df, df);
+            if (d2 < best) { // k increases, so ties keep the lowest index
+                best = d2;
+                best_i = k;
             }
         }
     }
@@ -425,7 +448,7 @@ extern "C" int vt_bvh_query(void *handle, const float *points, uint32_t num_poin
     if (num_queries == 0)
         return VT_OK;
     VT_REQUIRE(points && queries && out, "null pointer argument");
-    if ((uint64_t)num_queries * h->n <= NN_SCAN_PAIRS && num_queries <= 65535u) {
+    if (!h->force_tree && (uint64_t)num_queries * h->n <= NN_SCAN_PAIRS && num_queries <= 65535u) {
         // the partials live in the handle's workspace when it has room
         const size_t need = (size_t)num_queries * NN_SCAN_BLOCKS * 2;
         if (need <= h->ws_words) {
@@ -438,8 +461,9 @@ extern "C" int vt_bvh_query(void *handle, const float *points, uint32_t num_poin
             return VT_OK;
         }
     }
-    bvh_query_kernel<<<(num_queries + 255) / 256, 256, 0, as_stream(stream)>>>(h->nodes, h->leaf_idx, h->n, points,
-                                                                             queries, num_queries, out);
+    bvh_query_kernel<<<(num_queries + 255) / 256, 256, 0, as_stream(stream)>>>(
+        h->nodes, h->leaf_idx, h->n, points, queries, num_queries, out,
+        h->stack_limit < (uint32_t)BVH_STACK ? h->stack_limit : (uint32_t)BVH_STACK);
     VT_LAUNCH_CHECK("bvh_query_kernel");
     return VT_OK;
 }
@@ -504,6 +528,17 @@ extern "C" int vt_nearest_sites_noalloc(const float *points, uint32_t num_points
     VT_LAUNCH_CHECK("nn_scan_kernel");
     nn_pick_kernel<<<num_queries, 64, 0, as_stream(stream)>>>(partial, out);
     VT_LAUNCH_CHECK("nn_pick_kernel");
+    return VT_OK;
+}
+
+extern "C" int vt_bvh_debug_stack_limit(void *handle, uint32_t limit, int force_tree)
+{
+    clear_error();
+    BvhHandle *h = (BvhHandle *)handle;
+    VT_REQUIRE(h, "null BVH handle");
+    VT_REQUIRE(limit <= (uint32_t)BVH_STACK, "stack limit %u above the compiled %d", limit, BVH_STACK);
+    h->stack_limit = limit ? limit : (uint32_t)BVH_STACK;
+    h->force_tree = force_tree != 0;
     return VT_OK;
 }
 
