@@ -61,6 +61,32 @@ def lib():
     return _lib
 
 
+class plant:
+    """Context manager switching on one of oracle.h's planted mistakes
+    (OR_PLANT_*) for the pin tests: ``with core.plant(core.PLANT_SPEC_PLUS_D): ...``."""
+
+    def __init__(self, code: int):
+        self.code = int(code)
+
+    def __enter__(self):
+        lib().or_set_plant(C.c_int(self.code))
+        return self
+
+    def __exit__(self, *exc):
+        lib().or_set_plant(C.c_int(0))
+        return False
+
+
+PLANT_SPEC_PLUS_D = 1
+PLANT_INFER_NO_DENSITY_GATE = 2
+PLANT_SKIP_ON_ALPHA = 3
+PLANT_NO_FIRST_CELL_TERM = 4
+PLANT_FLUSH_CUR_ON_STOP = 5
+PLANT_POINT_ERROR_ALPHA = 6
+PLANT_IGNORE_CONTRIB_GRAD = 7
+PLANT_NO_DT0_PREV = 8
+
+
 def _p(a):
     if a is None:
         return None

@@ -43,6 +43,11 @@
 
 #define OR_NONE 0xffffffffu
 
+/* planted mistake for the pin tests (oracle.h); 0 in every other use */
+static int g_plant = OR_PLANT_NONE;
+void or_set_plant(int code) { g_plant = code; }
+int or_get_plant(void) { return g_plant; }
+
 /* ------------------------------------------------------------------------- */
 /* scalar math                                                                 */
 /* ------------------------------------------------------------------------- */
@@ -339,6 +344,7 @@ typedef struct {
     or_ray_stats st;
     uint32_t *log;
     uint32_t log_cap;
+    uint32_t next; /* the cell behind the exit face of the step being integrated */
 } walk_dbg_t;
 
 typedef int (*integrate_fn)(void *state, uint32_t cell, float t0, float t1, v3 p, v3 np);
@@ -417,6 +423,7 @@ static inline uint32_t walk(v3 o, v3 d, const float *points, const uint32_t *adj
         v3 np = ld3(points, nxt);
         if (t1 > t0) {
             g->st.integrated += 1;
+            g->next = nxt;
             if (!integrate(state, cur, t0, t1, p, np))
                 break;
         }
@@ -440,7 +447,10 @@ static inline void read_ray(const float *rays, uint32_t r, v3 *o, v3 *d)
 static inline void spec_setup(v3 d, int R, bil_t *b)
 {
     float u, v;
-    oct_encode(mk(-d.x, -d.y, -d.z), R, &u, &v);
+    if (g_plant == OR_PLANT_SPEC_PLUS_D)
+        oct_encode(d, R, &u, &v);
+    else
+        oct_encode(mk(-d.x, -d.y, -d.z), R, &u, &v);
     *b = bil_setup(u, v, R);
 }
 
@@ -510,12 +520,12 @@ static int infer_integrate(void *sp, uint32_t cell, float t0, float t1, v3 p, v3
     (void)np;
     infer_state *s = (infer_state *)sp;
     float sig = s->density[cell];
-    if (sig <= 1e-6f)
+    if (sig <= 1e-6f && g_plant != OR_PLANT_INFER_NO_DENSITY_GATE)
         return s->T > s->thr;
     float dt = fmaxf(t1 - t0, 0.0f);
     float alpha = 1.0f - or_expf(-sig * dt);
     float w = s->T * alpha;
-    if (w >= s->skip) {
+    if ((g_plant == OR_PLANT_SKIP_ON_ALPHA ? alpha : w) >= s->skip) {
         s->g->st.shaded += 1;
         v3 rgb = cell_color(&s->dm, &s->sm, &s->spec, cell, s->o, s->d, t0, p, NULL);
         s->acc = vfma(w, rgb, s->acc);
@@ -829,7 +839,7 @@ static int bwd_integrate(void *sp, uint32_t cell, float t0, float t1, v3 p, v3 n
 
     s->acc = vfma(w, rgb, s->acc);
     if (s->point_error)
-        attr_atomic_add(s->f16, s->point_error, cell, w * s->ray_error);
+        attr_atomic_add(s->f16, s->point_error, cell, (g_plant == OR_PLANT_POINT_ERROR_ALPHA ? alpha : w) * s->ray_error);
 
     v3 dL_drgb = mk(s->fwd_rgb_grad.x * w, s->fwd_rgb_grad.y * w, s->fwd_rgb_grad.z * w);
     v3 rest = vsub(s->fwd_rgb, s->acc);
@@ -878,10 +888,12 @@ static int bwd_integrate(void *sp, uint32_t cell, float t0, float t1, v3 p, v3 n
     float dL_dt1 = dL_ddt;
 
     v3 dt0_dprev = mk(0.0f, 0.0f, 0.0f);
-    if (s->prev_idx != OR_NONE)
+    if (s->prev_idx != OR_NONE && g_plant != OR_PLANT_NO_DT0_PREV)
         dt0_dprev = cell_intersection_grad(s->prev_geom, p, s->o, s->d);
     v3 dt1_dcur = cell_intersection_grad(p, np, s->o, s->d);
     v3 dt0_dcur = cell_intersection_grad(p, s->prev_geom, s->o, s->d);
+    if (g_plant == OR_PLANT_NO_FIRST_CELL_TERM && s->prev_idx == OR_NONE)
+        dt0_dcur = mk(0.0f, 0.0f, 0.0f);
     v3 dt1_dnext = cell_intersection_grad(np, p, s->o, s->d);
 
     s->prev_grad = vfma(dL_dt0, dt0_dprev, s->prev_grad);
@@ -925,6 +937,8 @@ static int bwd_integrate(void *sp, uint32_t cell, float t0, float t1, v3 p, v3 n
 
     if (s->T < s->thr) {
         add_vec_atomic(s->points_grad, s->prev_idx, s->prev_grad);
+        if (g_plant == OR_PLANT_FLUSH_CUR_ON_STOP)
+            add_vec_atomic(s->points_grad, s->g->next, s->cur_grad);
         return 0;
     }
     return 1;
@@ -965,7 +979,8 @@ void or_trace_bwd(int attr_f16, const float *points, const void *diffuse, const 
             rg[i] = attr_load(attr_f16, rgba_grad, 4 * (size_t)r + i);
             rv[i] = attr_load(attr_f16, rgba, 4 * (size_t)r + i);
         }
-        rg[3] = rg[3] + contribution_alpha_grad;
+        if (g_plant != OR_PLANT_IGNORE_CONTRIB_GRAD)
+            rg[3] = rg[3] + contribution_alpha_grad;
         s.ray_error = ray_error ? attr_load(attr_f16, ray_error, r) : 0.0f;
         float cdg = 0.0f;
         for (uint32_t i = 0; i < K; ++i) {

@@ -40,6 +40,23 @@ typedef struct or_ray_stats {
 } or_ray_stats;
 
 /* scalar helpers, exported so tests can pin them */
+/* Planted mistakes, for the pin tests only: a test switches one on to show
+ * that its check fails on that slip, then switches it back to 0 (none).  The
+ * switch is process-wide and read during each call. */
+enum {
+    OR_PLANT_NONE = 0,
+    OR_PLANT_SPEC_PLUS_D = 1,      /* specular sampled at oct_encode(+d), not (-d) */
+    OR_PLANT_INFER_NO_DENSITY_GATE = 2, /* inference updates T for density <= 1e-6 */
+    OR_PLANT_SKIP_ON_ALPHA = 3,    /* inference skip gate tests alpha, not the weight */
+    OR_PLANT_NO_FIRST_CELL_TERM = 4,    /* backward: first cell's t0 term against the zero site dropped */
+    OR_PLANT_FLUSH_CUR_ON_STOP = 5,     /* backward: opacity stop also flushes the next site's slot */
+    OR_PLANT_POINT_ERROR_ALPHA = 6,     /* backward: point_error accumulates alpha * error */
+    OR_PLANT_IGNORE_CONTRIB_GRAD = 7,   /* backward: contribution_alpha_grad not added */
+    OR_PLANT_NO_DT0_PREV = 8            /* backward: previous site's t0 term dropped */
+};
+void or_set_plant(int code);
+int or_get_plant(void);
+
 float or_expf(float x);
 float or_logf(float x);
 uint16_t or_f32_to_f16(float x);
