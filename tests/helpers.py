@@ -122,3 +122,20 @@ def nn_tie_set(n=300000, seed=11):
         base += 17
         g += 1
     return pts, np.stack(queries).astype(np.float32)
+
+
+def assert_grad_close(got, want, name="", rtol=1e-3, atol_frac=1e-6):
+    """Gradient parity: the largest difference within rtol of the tensor's
+    largest magnitude (atomics add in another order than the serial CPU
+    loop), and every element within rtol of its own value plus atol_frac of
+    that scale, so that a small element cannot be wrong by 100 % unnoticed."""
+    g = np.asarray(got, np.float64)
+    w = np.asarray(want, np.float64)
+    assert g.shape == w.shape, (name, g.shape, w.shape)
+    assert np.isfinite(g).all(), f"{name}: non-finite gradient"
+    scale = max(float(np.abs(w).max(initial=0.0)), 1e-30)
+    d = np.abs(g - w)
+    assert d.max(initial=0.0) <= rtol * scale, f"{name}: max |diff| {d.max():.3g} > {rtol} x scale {scale:.3g}"
+    bad = np.nonzero(d > rtol * np.abs(w) + atol_frac * scale)
+    assert bad[0].size == 0, (f"{name}: {bad[0].size} elements outside {rtol} x |want| + {atol_frac} x scale, first "
+                              f"{list(zip(g[bad][:4], w[bad][:4]))}")

@@ -1,0 +1,198 @@
+"""GPU parity at BASELINE.json's full sizes against the CPU oracle on the same
+inputs (the oracle finishes each in seconds on the box's cores).
+
+- C1: 4,096-site sphere scene, one 128x128 pinhole, fp32 forward (plus its
+  backward), forward bit for bit.
+- C2: 262,144-site torus scene, one 800x600 pinhole, fp32 forward + backward
+  with every optional input (quantile depths and their gradient, distortion
+  gradient, ray error, contribution_alpha_grad), upstream alpha gradient zero
+  and N(0, 1): forward bit for bit, gradients per element.
+- C3 / C4: the 1,048,576-site height field, Morton-sorted, fp16 and q8
+  inference of whole 1237x822 frames: walk statistics (visit hashes) and alpha
+  bit for bit, RGB to one fp16 ulp.
+- C5: 3,145,728 sites, one 1558x1039 fisheye rolling-shutter camera, start
+  cell per row from the LBVH, fp32 forward + backward.
+
+C3-C5 take their adjacency from the GPU Voronoi builder (neighbour sets equal
+to qhull's, tests/test_gpu_voronoi.py) instead of a minute of host qhull; the
+parity compared here is kernel against oracle on the same adjacency."""
+import functools
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import core, host_ops
+from tests import helpers as H
+from vorotracing_amd import _C, camera, native, ops, scene
+from vorotracing_amd.infer import VoroTracingInfer
+from vorotracing_amd.model import VoroTracing
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(f"[fullsize] {msg}", flush=True)
+
+
+def _gpu_csr(points):
+    adj, off, _ = ops.build_voronoi_adjacency(torch.from_numpy(points).to("cuda:0"))
+    torch.cuda.synchronize()
+    return adj.cpu().numpy(), off.cpu().numpy()
+
+
+@functools.lru_cache(maxsize=None)
+def _heightfield(n, name):
+    return scene.heightfield(0, n, 4, name=name, csr_fn=_gpu_csr)
+
+
+def _train_parity(s, rays, start, thr, gpu, extras, ga_random, label):
+    rng = np.random.default_rng(7)
+    nq = 2 if extras else 0
+    q = np.tile(np.float32([0.8, 0.35]), rays.shape[:-1] + (1,)) if extras else None
+    _say(f"{label}: oracle forward ({rays.size // 6} rays)")
+    fw = core.trace_fwd(s.points, s.diffuse, s.specular, s.diff_res, s.spec_res, s.density, s.adjacency, s.offsets,
+                        rays, start, depth_quantiles=q, weight_threshold=thr, return_contribution=True)
+    pts, dif, spe = H.to_dev(s.points, gpu), H.to_dev(s.diffuse, gpu), H.to_dev(s.specular, gpu)
+    den, adj, off = H.to_dev(s.density, gpu), H.to_dev(s.adjacency, gpu), H.to_dev(s.offsets, gpu)
+    rd, sd = H.to_dev(rays, gpu), H.to_dev(start, gpu)
+    _say(f"{label}: GPU forward")
+    rgba, depth, depth_idx, contrib, n, dist, W, S, tf = _C.trace_vorotracing_fwd(
+        pts, dif, spe, den, adj, off, rd, sd, None if q is None else H.to_dev(q, gpu), thr, 1024, True)
+    torch.cuda.synchronize()
+    assert np.array_equal(n.cpu().numpy(), fw["n"])
+    assert np.array_equal(rgba.cpu().numpy().view(np.uint32), fw["rgba"].view(np.uint32))
+    for got, key in ((dist, "distortion"), (W, "W_total"), (S, "S_total"), (tf, "t_far")):
+        assert np.array_equal(got.cpu().numpy().view(np.uint32), fw[key].view(np.uint32)), key
+    if extras:
+        assert np.array_equal(depth_idx.cpu().numpy(), fw["depth_idx"])
+        assert np.array_equal(depth.cpu().numpy().view(np.uint32), fw["depth"].view(np.uint32))
+    # contribution sums one weight (< 1) per ray and cell with f32 atomics, in
+    # any order on both sides.  Past 4096 every add rounds at 2^-12 or coarser,
+    # and C5's start region sums tens of thousands of weights per cell (up to
+    # 44,800), drifting by up to a few 1e-3 in either order: those sums get a
+    # 5e-3 bound, every other cell the 1e-3 one.
+    cg, cw = contrib.cpu().numpy().astype(np.float64), fw["contribution"].astype(np.float64)
+    big = np.abs(cw) > 4096.0
+    H.assert_grad_close(np.where(big, cw, cg), cw, "contribution")
+    assert (np.abs(cg - cw)[big] <= 5e-3 * np.abs(cw[big])).all()
+    assert (fw["n"] > 1).mean() > 0.3  # the camera sees the scene
+
+    g = rng.normal(size=rays.shape[:-1] + (4,)).astype(np.float32)
+    if not ga_random:
+        g[..., 3] = 0.0
+    dg = rng.normal(size=rays.shape[:-1] + (nq,)).astype(np.float32) * 0.1 if extras else None
+    distg = rng.uniform(0, 1, size=rays.shape[:-1] + (1,)).astype(np.float32) if extras else None
+    rerr = rng.uniform(0, 1, size=rays.shape[:-1]).astype(np.float32) if extras else None
+    cag = 0.25 if extras else 0.0
+    _say(f"{label}: oracle backward")
+    want = core.trace_bwd(s.points, s.diffuse, s.specular, s.diff_res, s.spec_res, s.density, s.adjacency, s.offsets,
+                          rays, start, fw["rgba"], g, depth_quantiles=q, depth_idx=fw["depth_idx"], depth_grad=dg,
+                          ray_error=rerr, contribution_alpha_grad=cag, distortion=fw["distortion"],
+                          distortion_grad=distg, W_total=fw["W_total"], S_total=fw["S_total"], t_far=fw["t_far"],
+                          weight_threshold=thr)
+    d = lambda a: None if a is None else H.to_dev(a, gpu)  # noqa: E731
+    _say(f"{label}: GPU backward")
+    pg, dgd, sgd, deng, rayg, perr = _C.trace_vorotracing_bwd(
+        pts, dif, spe, den, adj, off, rd, sd, rgba, d(g), d(q), depth_idx if extras else None, d(dg), d(rerr), cag,
+        dist, d(distg), W, S, tf, thr, 1024)
+    torch.cuda.synchronize()
+    H.assert_grad_close(pg.cpu().numpy(), want["points_grad"], "points_grad")
+    H.assert_grad_close(deng.cpu().numpy(), want["density_grad"], "density_grad")
+    H.assert_grad_close(dgd.cpu().numpy(), want["diffuse_grad"], "diffuse_grad")
+    H.assert_grad_close(sgd.cpu().numpy(), want["specular_grad"], "specular_grad")
+    assert not rayg.cpu().numpy().any()
+    if extras:
+        H.assert_grad_close(perr.cpu().numpy(), want["point_error"], "point_error")
+
+
+def test_c1_full_size(gpu):
+    s = H.c1_scene()
+    rays = camera.pinhole_rays(128, 128, eye=(0.0, -4.0, 0.0))
+    _train_parity(s, rays, H.start_for(s, rays), 0.01, gpu, extras=True, ga_random=True, label="C1")
+
+
+@pytest.mark.parametrize("ga_random", [False, True])
+def test_c2_full_size(gpu, ga_random):
+    _say("C2: scene (262,144 sites, host qhull)")
+    s = scene.cached(scene.config2, 0)
+    rays = camera.pinhole_rays(800, 600, eye=(0.0, -4.0, 0.0))
+    start = H.start_for(s, rays)
+    model = VoroTracing.from_scene(s, device=gpu)
+    assert np.array_equal(model.get_starting_point(H.to_dev(rays, gpu)).cpu().numpy(), start)
+    _train_parity(s, rays, start, 0.001, gpu, extras=ga_random, ga_random=ga_random, label="C2")
+
+
+@functools.lru_cache(maxsize=None)
+def _c3_infer(quantize):
+    s = _heightfield(1048576, "c3_gpu_csr")
+    model = VoroTracing.from_scene(s, device=torch.device("cuda:0"))
+    return VoroTracingInfer(model, sort_morton=True, quantize=quantize)
+
+
+def _oracle_args(inf):
+    return (inf.primal_points.cpu().numpy(), inf.density.reshape(-1).cpu().numpy(),
+            inf.point_adjacency.cpu().numpy(), inf.point_adjacency_offsets.cpu().numpy(),
+            inf.adjacent_diff.cpu().numpy())
+
+
+@pytest.mark.parametrize("pose", [0, 21])
+def test_c3_full_frame_fp16(gpu, pose):
+    _say(f"C3: 1M-site scene, pose {pose}")
+    inf = _c3_infer("fp16")
+    W, Hh = 1237, 822
+    rays = camera.orbit_rays(pose, W, Hh)
+    rd = H.to_dev(rays, gpu)
+    sp = inf.get_starting_point(rd)
+    pts, den, adj, off, ad = _oracle_args(inf)
+    assert int(sp.reshape(-1)[0]) == int(host_ops.nearest_site(pts, rays[0, 0, :3][None])[0])
+    st = native.new_stats(W * Hh, gpu)
+    got = inf.render(rd, start_point=sp, weight_threshold=0.01, cell_skip_threshold=1e-3, stats=st)
+    torch.cuda.synchronize()
+    _say("C3: oracle frame")
+    want, wst, _ = core.trace_infer_f16(pts, inf.diffuse_fp16.cpu().numpy(), inf.specular_fp16.cpu().numpy(), 4, 4,
+                                        den, adj, off, ad, rays, sp.cpu().numpy(), weight_threshold=0.01,
+                                        cell_skip_threshold=1e-3, want_stats=True)
+    H.assert_stats_equal(H.stats_np(st), wst)
+    H.assert_infer_rgba(got.cpu().numpy(), want)
+    assert (wst["integrated"] > 0).mean() > 0.5
+
+
+def test_c4_full_frames_q8(gpu):
+    """Two of C4's cameras (poses 0 and 16) in one q8 launch, per-channel
+    scale / offset, one start cell per image; visits equal the fp16 run's."""
+    _say("C4: q8, 2 cameras")
+    inf = _c3_infer("q8")
+    W, Hh = 1237, 822
+    rays = np.stack([camera.orbit_rays(k, W, Hh) for k in (0, 16)])
+    rd = H.to_dev(rays, gpu)
+    sp = inf.get_starting_point(rd)
+    st = native.new_stats(2 * W * Hh, gpu)
+    got = inf.render(rd, start_point=sp, weight_threshold=0.01, cell_skip_threshold=1e-3, stats=st)
+    torch.cuda.synchronize()
+    pts, den, adj, off, ad = _oracle_args(inf)
+    _say("C4: oracle frames")
+    want, wst = core.trace_infer_q8(pts, inf.diffuse_q8.cpu().numpy(), inf.specular_q8.cpu().numpy(), 4, 4,
+                                    inf.diff_scale, inf.diff_offset, inf.spec_scale, inf.spec_offset, den, adj, off,
+                                    ad, rays, sp.cpu().numpy(), weight_threshold=0.01, cell_skip_threshold=1e-3,
+                                    want_stats=True)
+    H.assert_stats_equal(H.stats_np(st), wst)
+    H.assert_infer_rgba(got.cpu().numpy(), want)
+    f16 = _c3_infer("fp16")
+    st16 = native.new_stats(2 * W * Hh, gpu)
+    f16.render(rd, start_point=sp, weight_threshold=0.01, cell_skip_threshold=1e-3, stats=st16)
+    torch.cuda.synchronize()
+    a, b = H.stats_np(st16), H.stats_np(st)
+    for k in ("n", "visits", "faces", "visit_hash"):
+        assert np.array_equal(a[k], b[k]), k
+
+
+def test_c5_full_size(gpu):
+    _say("C5: 3.1M-site scene (GPU Voronoi)")
+    s = _heightfield(3145728, "c5_gpu_csr")
+    rays = camera.fisheye_rolling_rays(1558, 1039)
+    model = VoroTracing.from_scene(s, device=gpu)
+    sp = model.get_starting_point(H.to_dev(rays, gpu)).cpu().numpy()
+    rows = host_ops.nearest_site(s.points, rays[:, 0, :3]).astype(np.uint32)
+    assert np.array_equal(sp, np.broadcast_to(rows[:, None], rays.shape[:-1]))
+    _train_parity(s, rays, sp, 0.001, gpu, extras=False, ga_random=False, label="C5")

@@ -3,8 +3,9 @@
 Forward outputs are deterministic and compared bit-for-bit (rgba, n, depth,
 depth_idx, distortion, W/S totals, t_far); atomically accumulated outputs
 (contribution, all gradients) are compared with the north star's 1e-3
-relative tolerance, measured against each tensor's largest magnitude (the
-GPU adds in a different order than the serial-per-ray CPU loop).
+relative tolerance, per element (helpers.assert_grad_close: within 1e-3 of
+the element plus 1e-6 of the tensor's largest magnitude; the GPU adds in a
+different order than the serial-per-ray CPU loop).
 """
 import numpy as np
 import pytest
@@ -100,14 +101,23 @@ def test_bwd_parity(gpu, which, f16, extras):
         pts, dif, spe, den, adj, off, d(rays), d(start), d(fw["rgba"]), d(g), d(q), d(fw["depth_idx"]), d(dg),
         d(rerr), cag, d(fw["distortion"]), d(distg), d(fw["W_total"]), d(fw["S_total"]), d(fw["t_far"]), thr, 1024)
     torch.cuda.synchronize()
-    tol = 5e-2 if f16 else GRAD_RTOL  # f16 storage: each half-precision atomic add rounds, order-dependent
-    assert _rel_err(pg.cpu().numpy(), want["points_grad"]) <= GRAD_RTOL * (10 if f16 else 1)
-    assert _rel_err(deng.cpu().numpy(), want["density_grad"]) <= GRAD_RTOL * (10 if f16 else 1)
-    assert _rel_err(dgd.cpu().numpy().astype(np.float32), want["diffuse_grad"].astype(np.float32)) <= tol
-    assert _rel_err(sgd.cpu().numpy().astype(np.float32), want["specular_grad"].astype(np.float32)) <= tol
     assert not rayg.cpu().numpy().any()
+    if not f16:
+        H.assert_grad_close(pg.cpu().numpy(), want["points_grad"], "points_grad")
+        H.assert_grad_close(deng.cpu().numpy(), want["density_grad"], "density_grad")
+        H.assert_grad_close(dgd.cpu().numpy(), want["diffuse_grad"], "diffuse_grad")
+        H.assert_grad_close(sgd.cpu().numpy(), want["specular_grad"], "specular_grad")
+    else:
+        # f16 storage (as in the reference): the texture gradients are summed
+        # with half-precision atomics, each add rounding to 11 bits, so once a
+        # texel's sum is large the result depends on the add order; points and
+        # density stay f32 atomics.
+        assert _rel_err(pg.cpu().numpy(), want["points_grad"]) <= GRAD_RTOL * 10
+        assert _rel_err(deng.cpu().numpy(), want["density_grad"]) <= GRAD_RTOL * 10
+        assert _rel_err(dgd.cpu().numpy().astype(np.float32), want["diffuse_grad"].astype(np.float32)) <= 5e-2
+        assert _rel_err(sgd.cpu().numpy().astype(np.float32), want["specular_grad"].astype(np.float32)) <= 5e-2
     if extras:
-        assert _rel_err(perr.cpu().numpy(), want["point_error"]) <= GRAD_RTOL
+        H.assert_grad_close(perr.cpu().numpy(), want["point_error"], "point_error")
     else:
         assert perr is None
 
@@ -143,10 +153,10 @@ def test_c5_shape_fisheye_rolling_shutter(gpu):
         pts, dif, spe, den, adj, off, rays_d, sp, d(fw["rgba"]), d(g), None, None, None, None, 0.0,
         d(fw["distortion"]), None, d(fw["W_total"]), d(fw["S_total"]), d(fw["t_far"]), thr, 1024)
     torch.cuda.synchronize()
-    assert _rel_err(pg.cpu().numpy(), want["points_grad"]) <= GRAD_RTOL
-    assert _rel_err(deng.cpu().numpy(), want["density_grad"]) <= GRAD_RTOL
-    assert _rel_err(dgd.cpu().numpy(), want["diffuse_grad"]) <= GRAD_RTOL
-    assert _rel_err(sgd.cpu().numpy(), want["specular_grad"]) <= GRAD_RTOL
+    H.assert_grad_close(pg.cpu().numpy(), want["points_grad"], "points_grad")
+    H.assert_grad_close(deng.cpu().numpy(), want["density_grad"], "density_grad")
+    H.assert_grad_close(dgd.cpu().numpy(), want["diffuse_grad"], "diffuse_grad")
+    H.assert_grad_close(sgd.cpu().numpy(), want["specular_grad"], "specular_grad")
 
 
 def test_autograd_model_forward_backward(gpu):
@@ -166,12 +176,12 @@ def test_autograd_model_forward_backward(gpu):
                           fw["rgba"], gr, distortion=fw["distortion"], W_total=fw["W_total"], S_total=fw["S_total"],
                           t_far=fw["t_far"], weight_threshold=thr)
     assert np.array_equal(rgba.detach().cpu().numpy(), fw["rgba"])
-    assert _rel_err(model.primal_points.grad.cpu().numpy(), want["points_grad"]) <= GRAD_RTOL
-    assert _rel_err(model.att_diffuse.grad.cpu().numpy(), want["diffuse_grad"]) <= GRAD_RTOL
-    assert _rel_err(model.att_specular.grad.cpu().numpy(), want["specular_grad"]) <= GRAD_RTOL
+    H.assert_grad_close(model.primal_points.grad.cpu().numpy(), want["points_grad"], "points_grad")
+    H.assert_grad_close(model.att_diffuse.grad.cpu().numpy(), want["diffuse_grad"], "diffuse_grad")
+    H.assert_grad_close(model.att_specular.grad.cpu().numpy(), want["specular_grad"], "specular_grad")
     # density enters through exp: d/draw = d/ds * s
     ds = want["density_grad"] * dens
-    assert _rel_err(model.density.grad.cpu().numpy(), ds) <= GRAD_RTOL
+    H.assert_grad_close(model.density.grad.cpu().numpy(), ds, "density")
 
 
 def test_train_errors_reference_messages(gpu):
