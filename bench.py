@@ -602,7 +602,7 @@ def train_cpu_step(model, rays, sp, g, log, label, sample):
     rgba, _, _, _, _, _ = model(rays, start_point=sp, weight_threshold=0.001)
     rgba.backward(g)
     torch.cuda.synchronize()
-    dens = model._get_primal_density().detach().cpu().numpy()
+    dens = model.activated_density().detach().cpu().numpy()
     args = (model.primal_points.detach().cpu().numpy(), model.att_diffuse.detach().cpu().numpy(),
             model.att_specular.detach().cpu().numpy(), 4, 4, dens, model.point_adjacency.cpu().numpy(),
             model.point_adjacency_offsets.cpu().numpy(), rays.cpu().numpy(), sp.cpu().numpy())

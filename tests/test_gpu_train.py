@@ -169,7 +169,7 @@ def test_autograd_model_forward_backward(gpu):
     rgba, depth, contrib, n, errbox, dist = model(rays_d, start_point=sp, weight_threshold=thr)
     gr = np.random.default_rng(2).normal(size=rgba.shape).astype(np.float32)
     (rgba * torch.from_numpy(gr).to(gpu)).sum().backward()
-    dens = model._get_primal_density().detach().cpu().numpy()  # exp on the device, as the model feeds the kernel
+    dens = model.activated_density().detach().cpu().numpy()  # exp on the device, as the model feeds the kernel
     fw = core.trace_fwd(s.points, s.diffuse, s.specular, 4, 4, dens, s.adjacency, s.offsets, rays, start,
                         weight_threshold=thr)
     want = core.trace_bwd(s.points, s.diffuse, s.specular, 4, 4, dens, s.adjacency, s.offsets, rays, start,

@@ -171,24 +171,18 @@ class VoroTracingInfer:
 
     # -- per frame ------------------------------------------------------------
 
+    @torch.no_grad()
     def get_starting_point(self, rays):
-        """vorotracing.py:585-604: one LBVH query on the first ray's origin,
-        broadcast.  For an image batch (B, H, W, 6) each image gets its own
-        query (the reference's single-origin shortcut would be wrong there)."""
-        with torch.no_grad():
-            if rays.ndim == 1:
-                rays = rays[None, :]
-            lead = rays.shape[:-1]
-            if rays.ndim == 4:
-                origins = rays[:, 0, 0, :3].contiguous()
-                nn = self.bvh.query(self.primal_points, origins)
-                return nn.view(-1, 1, 1).expand(lead).contiguous().view(torch.uint32)
-            origin = rays.reshape(-1, rays.shape[-1])[:1, :3]
-            nn = self.bvh.query(self.primal_points, origin)
-            n = 1
-            for s in lead:
-                n *= s
-            return nn.expand(n).reshape(lead).contiguous().view(torch.uint32)
+        """u32 start cells of a render, one LBVH query per camera: the origin
+        of a camera's first ray is every ray's origin for a pinhole image (the
+        reference queries the batch's first ray only, vorotracing.py:585-604).
+        An image batch (B, H, W, 6) is B cameras, any other shape one."""
+        lead = rays.shape[:-1]
+        cams = lead[0] if rays.dim() == 4 else 1
+        first = rays.reshape(cams, -1, 6)[:, 0, :3].contiguous()
+        cells = self.bvh.query(self.primal_points, first).view(torch.uint32)
+        spread = (cams,) + (1,) * (len(lead) - 1) if rays.dim() == 4 else (1,) * len(lead)
+        return cells.reshape(spread).expand(lead).contiguous()
 
     @torch.no_grad()
     def _tile_perm(self, H, W, TH=8, TW=8):

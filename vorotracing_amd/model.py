@@ -1,13 +1,17 @@
-"""Training-side caller of the path: ``VoroTracing`` (vorotracing.py:12-436),
-reduced to what the traversal needs.
+"""Training-side caller of the traversal: a Voronoi radiance field whose
+forward renders rays through ``ops.TraceVoroTracing``.  It plays the role of
+the reference's ``VoroTracing`` module (vorotracing.py:27-436) for the hot
+path; trainer, viewer and dataset code are out of scope.
 
-Kept: the parameters (sites, raw log-density, diffuse / specular octahedral
-logit maps), the CSR adjacency, the start-cell lookup (NNBVH, vorotracing.py:
-323-344), ``forward`` (vorotracing.py:365-419), the checkpoint dict
-(vorotracing.py:421-436 / 242-271) and the triangulation refresh
-(vorotracing.py:310-321, on the GPU Voronoi builder standing in for
-Paragram).  The trainer and viewer are out of scope; the fused backward
-epilogue and optimizer step live in train.py.
+State:
+- parameters ``primal_points`` (N, 3) sites, ``density`` (N, 1) raw
+  log-density (the kernels take s = a * exp(raw), vorotracing.py:346-347),
+  ``att_diffuse`` (N, 3 R^2) and ``att_specular`` (N, 3 Rs^2) octahedral
+  logit maps.  These names are what optimiser groups and checkpoints of the
+  reference refer to, so they are kept;
+- the Voronoi adjacency as a u32 CSR: ``point_adjacency`` (with 32 zero
+  padding entries) and ``point_adjacency_offsets`` (N + 1);
+- an LBVH over the sites (``bvh``) for start cells.
 """
 from __future__ import annotations
 
@@ -22,118 +26,135 @@ from . import ops
 
 @dataclass
 class VoroTracingConfig:
-    """vorotracing.py:12-24.  Resolutions 4 and 8 are compiled."""
+    """The reference's model configuration (vorotracing.py:12-24; same field
+    names, so its configs load).  Octahedral map sides 4 and 8 are compiled,
+    for diffuse and specular independently."""
     oct_map_res: int = 8
     spec_oct_map_res: int = 8
     activation_scale: float = 1.0
     up_direction: List[float] = field(default_factory=lambda: [0, 0, 0])
 
 
+def _float_param(value, rows: int, cols: int, device, what: str) -> nn.Parameter:
+    """A float32 (rows, cols) parameter holding ``value``, or zeros without one
+    (zero logits: grey diffuse, no specular; zero raw density: s = a)."""
+    if value is None:
+        return nn.Parameter(torch.zeros(rows, cols, dtype=torch.float32, device=device))
+    t = torch.as_tensor(value)
+    if t.dtype != torch.float32 or tuple(t.shape) != (rows, cols):
+        raise ValueError(f"{what}: expected float32 ({rows}, {cols}), got {t.dtype} {tuple(t.shape)}")
+    return nn.Parameter(t.to(device).contiguous())
+
+
 class VoroTracing(nn.Module):
-    def __init__(self, config: VoroTracingConfig, points: torch.Tensor, points_diffuse=None, points_specular=None,
+    """Sites, densities and octahedral maps of a Voronoi scene, rendered by
+    the HIP traversal.  Without an adjacency the constructor builds it on the
+    GPU (``update_triangulation``)."""
+
+    def __init__(self, config: VoroTracingConfig, points, points_diffuse=None, points_specular=None,
                  points_density=None, points_adjacency=None, points_adjacency_offsets=None,
                  device: torch.device = torch.device("cuda")):
         super().__init__()
+        sites = torch.as_tensor(points)
+        if sites.dim() != 2 or sites.shape[0] == 0:
+            raise ValueError(f"sites: expected a non-empty (N, 3) tensor, got shape {tuple(sites.shape)}")
+        n = sites.shape[0]
         self.config = config
         self.device = device
-        assert points is not None, "points must be provided"
-        assert points.shape[0] > 0, "points must have at least 1 point"
-        assert points.shape[1] == 3, "points must have 3 dimensions"
-        assert points.dtype == torch.float32, "points must be a float32 tensor"
-        n = points.shape[0]
-        dsz = 3 * config.oct_map_res ** 2
-        ssz = 3 * config.spec_oct_map_res ** 2
-        if points_diffuse is not None:
-            assert points_diffuse.shape == (n, dsz)
-            self.att_diffuse = nn.Parameter(points_diffuse.to(device))
-        else:
-            self.att_diffuse = nn.Parameter(torch.zeros(n, dsz, device=device, dtype=torch.float32))
-        if points_specular is not None:
-            assert points_specular.shape == (n, ssz)
-            self.att_specular = nn.Parameter(points_specular.to(device))
-        else:
-            self.att_specular = nn.Parameter(torch.zeros(n, ssz, device=device, dtype=torch.float32))
-        if points_density is not None:
-            assert points_density.shape[0] == n, "points and points_density must have the same number of points"
-            assert points_density.shape[1] == 1, "points_density must have 1 channel"
-            assert points_density.dtype == torch.float32, "points_density must be a float32 tensor"
-            self.density = nn.Parameter(points_density.to(device))
-        else:
-            self.density = nn.Parameter(torch.zeros(n, 1, device=device, dtype=torch.float32))
+        self.primal_points = _float_param(sites, n, 3, device, "sites")
+        self.density = _float_param(points_density, n, 1, device, "raw density")
+        self.att_diffuse = _float_param(points_diffuse, n, 3 * config.oct_map_res ** 2, device, "diffuse map")
+        self.att_specular = _float_param(points_specular, n, 3 * config.spec_oct_map_res ** 2, device, "specular map")
         self.bvh = ops.NNBVH()
-        if points_adjacency is not None and points_adjacency_offsets is not None:
-            assert points_adjacency_offsets.shape[0] == n + 1, \
-                "points_adjacency_offsets must have the same number of points + 1"
-            self.primal_points = nn.Parameter(points.to(device))
-            self.point_adjacency = points_adjacency.to(device, dtype=torch.uint32)
-            self.point_adjacency_offsets = points_adjacency_offsets.to(device, dtype=torch.uint32)
-            self.bvh.build(self.primal_points)
-        else:
-            self.primal_points = nn.Parameter(points.to(device))
+        if (points_adjacency is None) != (points_adjacency_offsets is None):
+            raise ValueError("the adjacency and its offsets are given together or not at all")
+        if points_adjacency is None:
             self.update_triangulation()
+        else:
+            self.set_adjacency(points_adjacency, points_adjacency_offsets)
+
+    # ---- construction and persistence
 
     @classmethod
     def from_scene(cls, s, device=torch.device("cuda")) -> "VoroTracing":
-        """Model from a synthetic scene (vorotracing_amd.scene.Scene)."""
+        """A model holding a synthetic scene (``vorotracing_amd.scene.Scene``)."""
         cfg = VoroTracingConfig(oct_map_res=s.diff_res, spec_oct_map_res=s.spec_res)
-        t = lambda a: torch.from_numpy(a.copy())  # noqa: E731
-        return cls(cfg, t(s.points), t(s.diffuse), t(s.specular), t(s.density_raw), t(s.adjacency.view("int32")),
-                   t(s.offsets.view("int32")), device=device)
+        return cls(cfg, torch.from_numpy(s.points.copy()), torch.from_numpy(s.diffuse.copy()),
+                   torch.from_numpy(s.specular.copy()), torch.from_numpy(s.density_raw.copy()),
+                   torch.from_numpy(s.adjacency.view("int32").copy()), torch.from_numpy(s.offsets.view("int32").copy()),
+                   device=device)
+
+    # checkpoint keys of the reference's files (vorotracing.py:421-436), so checkpoints move both ways
+    _CKPT = {"xyz": "primal_points", "density": "density", "color_diffuse": "att_diffuse",
+             "color_specular": "att_specular"}
 
     @classmethod
     def from_pretrained(cls, pt_path, config: VoroTracingConfig, device=torch.device("cuda")) -> "VoroTracing":
-        """vorotracing.py:242-271 (loads with weights_only=True)."""
+        """Load a checkpoint written by ``save_checkpoint`` or by the reference
+        (tensors only: ``torch.load(weights_only=True)``)."""
         d = torch.load(pt_path, map_location="cpu", weights_only=True)
-        return cls(config, d["xyz"], d["color_diffuse"], d["color_specular"], d["density"], d["adjacency"],
-                   d["adjacency_offsets"], device=device)
+        return cls(config, d["xyz"].float(), d["color_diffuse"].float(), d["color_specular"].float(),
+                   d["density"].float(), d["adjacency"], d["adjacency_offsets"], device=device)
 
     def save_checkpoint(self, out_path: str):
-        """vorotracing.py:421-436."""
-        torch.save({
-            "xyz": self.primal_points.detach().float().cpu(),
-            "density": self.density.detach().float().cpu(),
-            "adjacency": self.point_adjacency.cpu().long(),
-            "adjacency_offsets": self.point_adjacency_offsets.cpu().long(),
-            "color_diffuse": self.att_diffuse.detach().float().cpu(),
-            "color_specular": self.att_specular.detach().float().cpu(),
-        }, out_path)
+        state = {key: getattr(self, attr).detach().float().cpu() for key, attr in self._CKPT.items()}
+        state["adjacency"] = self.point_adjacency.cpu().long()
+        state["adjacency_offsets"] = self.point_adjacency_offsets.cpu().long()
+        torch.save(state, out_path)
 
-    def update_triangulation(self):
-        """vorotracing.py:310-321."""
-        if not self.primal_points.isfinite().all():
-            raise RuntimeError("NaN in points")
-        adjacency, offsets, _ = ops.build_voronoi_adjacency(self.primal_points.detach())
-        self.point_adjacency = adjacency
-        self.point_adjacency_offsets = offsets
+    # ---- geometry
+
+    @property
+    def num_sites(self) -> int:
+        return int(self.primal_points.shape[0])
+
+    def set_adjacency(self, adjacency, offsets):
+        """Install a Voronoi CSR (any integer dtype; stored as u32) and build
+        the start-cell LBVH over the current sites."""
+        off = torch.as_tensor(offsets).reshape(-1)
+        if off.numel() != self.num_sites + 1:
+            raise ValueError(f"adjacency offsets: expected {self.num_sites + 1} entries, got {off.numel()}")
+        self.point_adjacency = torch.as_tensor(adjacency).reshape(-1).to(self.device, dtype=torch.uint32)
+        self.point_adjacency_offsets = off.to(self.device, dtype=torch.uint32)
         self.bvh.build(self.primal_points)
 
-    def get_starting_point(self, rays):
-        """vorotracing.py:323-344: nearest site of each distinct ray origin."""
-        with torch.no_grad():
-            if rays.ndim == 1:
-                rays = rays[None, :]
-            origins = rays[..., :3]
-            lead = origins.shape[:-1]
-            flat = origins.reshape(-1, 3)
-            uniq, inv = torch.unique(flat, dim=0, return_inverse=True)
-            nn_inds = self.bvh.query(self.primal_points, uniq).long()
-            return nn_inds[inv].view(*lead).to(torch.uint32)
+    @torch.no_grad()
+    def update_triangulation(self):
+        """Rebuild the adjacency after the sites moved, on the GPU Voronoi
+        builder (the reference calls Paragram here, vorotracing.py:310-321),
+        and the start-cell LBVH."""
+        if not bool(torch.isfinite(self.primal_points).all()):
+            raise RuntimeError("update_triangulation: the sites hold NaN or inf")
+        adjacency, offsets, _ = ops.build_voronoi_adjacency(self.primal_points.detach())
+        self.set_adjacency(adjacency, offsets)
 
-    def _get_primal_density(self):
+    @torch.no_grad()
+    def get_starting_point(self, rays: torch.Tensor) -> torch.Tensor:
+        """u32 start cell of every ray: the nearest site of its origin, one LBVH
+        query per distinct origin (vorotracing.py:323-344)."""
+        lead = rays.shape[:-1]
+        origins, which = torch.unique(rays[..., :3].reshape(-1, 3), dim=0, return_inverse=True)
+        nearest = self.bvh.query(self.primal_points, origins)
+        return nearest[which].reshape(lead).view(torch.uint32)
+
+    def start_cells(self, rays: torch.Tensor, start_point: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """``start_point`` broadcast over the ray batch, or the nearest sites."""
+        if start_point is None:
+            return self.get_starting_point(rays)
+        return torch.broadcast_to(start_point, rays.shape[:-1])
+
+    # ---- rendering
+
+    def activated_density(self) -> torch.Tensor:
+        """The density the kernels take: s = a * exp(raw)."""
         return self.config.activation_scale * torch.exp(self.density)
-
-    def _get_trace_data(self):
-        return (self.primal_points, self.att_diffuse, self.att_specular, self._get_primal_density(),
-                self.point_adjacency, self.point_adjacency_offsets)
 
     def forward(self, rays: torch.Tensor, start_point: Optional[torch.Tensor] = None,
                 depth_quantiles: Optional[torch.Tensor] = None, weight_threshold: float = 0.001,
                 max_intersections: int = 1024, return_contribution: bool = False):
-        """vorotracing.py:365-419: (rgba, depth, contribution, n, errbox, distortion)."""
-        points, diffuse, specular, density, adjacency, offsets = self._get_trace_data()
-        if start_point is None:
-            start_point = self.get_starting_point(rays)
-        else:
-            start_point = torch.broadcast_to(start_point, rays.shape[:-1])
-        return ops.TraceVoroTracing.apply(points, diffuse, specular, density, adjacency, offsets, rays, start_point,
+        """Render ``rays`` (..., 6): (rgba, depth, contribution, n, error box,
+        distortion), the outputs of vorotracing.py:365-419; defaults as there."""
+        return ops.TraceVoroTracing.apply(self.primal_points, self.att_diffuse, self.att_specular,
+                                          self.activated_density(), self.point_adjacency,
+                                          self.point_adjacency_offsets, rays, self.start_cells(rays, start_point),
                                           depth_quantiles, weight_threshold, max_intersections, return_contribution)

@@ -5,95 +5,42 @@
 ``trace_octmap_infer`` / ``trace_octmap_infer_q8`` / ``prefetch_octmap_adj``
 the inference wrappers (_wrapper.py:234-307), ``NNBVH`` /
 ``nearest_neighbor_bvh`` the start-cell lookup (nn_bvh.h), and
-``build_voronoi_adjacency`` the CSR adapter (cuda/__init__.py:16-46) with the
-host Delaunay (qhull) standing in for Paragram.
+``build_voronoi_adjacency`` the CSR adapter (cuda/__init__.py:16-46), built by
+the GPU Voronoi builder where the reference calls Paragram.
 """
 from __future__ import annotations
 
 import torch
-import torch.nn.functional as F
 
-from . import _C, _lib
+from . import _C, _lib, autograd
+from .autograd import ErrorBox
 
 NNBVH = _C.NNBVH
 nearest_neighbor_bvh = _C.nearest_neighbor_bvh
 
 
-class ErrorBox:
-    def __init__(self):
-        self.ray_error = None
-        self.point_error = None
-        self.cell_distortion_gate = None
-
-
 class TraceVoroTracing(torch.autograd.Function):
-    """_wrapper.py:22-231: forward through _C.trace_vorotracing_fwd, backward
-    through _C.trace_vorotracing_bwd, gradients for points, diffuse,
-    specular and density (nan_to_num'd)."""
+    """Training traversal as an autograd Function (the operator of
+    _wrapper.py:22-231): inputs and the six outputs (rgba, depth,
+    contribution, n, error box, distortion) as the reference's; gradients
+    reach points, diffuse, specular and the activated density, NaN-cleaned.
+    The backward planning is ``autograd.scene_gradients``."""
 
     @staticmethod
-    def forward(ctx, _points, _diffuse, _specular, _density, _point_adjacency, _point_adjacency_offsets, rays,
-                start_point, depth_quantiles, weight_threshold: float, max_intersections: int,
-                return_contribution: bool):
-        ctx.rays = rays
-        ctx.start_point = start_point
-        ctx.depth_quantiles = depth_quantiles
-        ctx.weight_threshold = weight_threshold
-        ctx.max_intersections = max_intersections
-        ctx.points = _points
-        ctx.diffuse = _diffuse
-        ctx.specular = _specular
-        ctx.density = _density
-        ctx.point_adjacency = _point_adjacency
-        ctx.point_adjacency_offsets = _point_adjacency_offsets
-        (rgba, depth, depth_indices, contribution, num_intersections, distortion, W_total, S_total,
-         t_far) = _C.trace_vorotracing_fwd(_points, _diffuse, _specular, _density, _point_adjacency,
-                                          _point_adjacency_offsets, rays, start_point, depth_quantiles,
-                                          weight_threshold, max_intersections, return_contribution)
-        ctx.rgba = rgba
-        ctx.depth_indices = depth_indices
-        ctx.distortion = distortion
-        ctx.W_total = W_total
-        ctx.S_total = S_total
-        ctx.t_far = t_far
-        errbox = ErrorBox()
-        ctx.errbox = errbox
-        return rgba, depth, contribution, num_intersections, errbox, distortion
+    def forward(ctx, points, diffuse, specular, density, adjacency, offsets, rays, start_point, depth_quantiles,
+                weight_threshold: float, max_intersections: int, return_contribution: bool):
+        outputs, ctx.record = autograd.run_forward((points, diffuse, specular, density, adjacency, offsets), rays,
+                                                   start_point, depth_quantiles, weight_threshold, max_intersections,
+                                                   return_contribution)
+        return outputs
 
     @staticmethod
-    def backward(ctx, grad_rgba, grad_depth, grad_contribution, grad_num_intersections, errbox_grad,
-                 grad_distortion):
-        del grad_num_intersections, errbox_grad
-        contribution_alpha_grad = 0.0
-        if grad_contribution is not None:
-            contribution_alpha_grad = float(grad_contribution.detach().abs().max().item())
-
-        def _bwd(grad_rgba_, grad_depth_, ray_error_, contrib_, grad_distortion_):
-            return _C.trace_vorotracing_bwd(
-                ctx.points, ctx.diffuse, ctx.specular, ctx.density, ctx.point_adjacency,
-                ctx.point_adjacency_offsets, ctx.rays, ctx.start_point, ctx.rgba, grad_rgba_, ctx.depth_quantiles,
-                ctx.depth_indices, grad_depth_, ray_error_, contrib_, ctx.distortion, grad_distortion_,
-                ctx.W_total, ctx.S_total, ctx.t_far, ctx.weight_threshold, ctx.max_intersections)
-
-        if grad_rgba is None:
-            grad_rgba = torch.zeros_like(ctx.rgba)
-        cell_gate = getattr(ctx.errbox, "cell_distortion_gate", None)
-        if cell_gate is not None and grad_distortion is not None:
-            res_d = _bwd(torch.zeros_like(grad_rgba), None, None, 0.0, grad_distortion)
-            density_grad_dist = res_d[3]
-            points_grad, diffuse_grad, specular_grad, density_grad, _ray_grad, point_error = _bwd(
-                grad_rgba, grad_depth, ctx.errbox.ray_error, contribution_alpha_grad,
-                torch.zeros_like(grad_distortion))
-            torch.nan_to_num(density_grad_dist, nan=0.0, posinf=0.0, neginf=0.0, out=density_grad_dist)
-            density_grad = density_grad + cell_gate.reshape_as(density_grad) * density_grad_dist
-        else:
-            points_grad, diffuse_grad, specular_grad, density_grad, _ray_grad, point_error = _bwd(
-                grad_rgba, grad_depth, ctx.errbox.ray_error, contribution_alpha_grad, grad_distortion)
-        ctx.errbox.point_error = point_error
-        for g in (points_grad, diffuse_grad, specular_grad, density_grad):
-            torch.nan_to_num(g, nan=0.0, posinf=0.0, neginf=0.0, out=g)
-        return (points_grad, diffuse_grad, specular_grad, density_grad, None, None, None, None, None, None, None,
-                None)
+    def backward(ctx, grad_rgba, grad_depth, grad_contribution, _grad_n, _grad_box, grad_distortion):
+        rec = ctx.record
+        ctx.record = None  # the record holds the scene and the forward outputs: drop them with the graph
+        up = autograd.upstream_of(rec, grad_rgba, grad_depth, grad_contribution, grad_distortion)
+        grads = autograd.clean_(autograd.scene_gradients(rec, up))
+        return (*grads, None, None, None, None, None, None, None, None)
 
 
 def prefetch_octmap_adj(points, adjacency, offsets):

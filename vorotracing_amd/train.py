@@ -19,83 +19,50 @@ from typing import Optional
 
 import torch
 
-from . import _C, _lib, native
-from .ops import ErrorBox
+from . import _lib, autograd, native
 
 
 class FusedTraceVoroTracing(torch.autograd.Function):
-    """TraceVoroTracing with the raw log-density as input (same forward outputs)."""
+    """TraceVoroTracing on the raw log-density: the forward activates it as
+    s = a * exp(raw) (vorotracing.py:346-347, the same two torch operations,
+    so the kernel sees the same bits), the backward plans its launches with
+    ``autograd.scene_gradients`` and finishes all four gradients in one
+    launch: NaN cleaning plus d/draw = (dL/ds * a) * exp(raw)."""
 
     @staticmethod
     def forward(ctx, points, diffuse, specular, density_raw, activation_scale: float, adjacency, offsets, rays,
                 start_point, depth_quantiles, weight_threshold: float, max_intersections: int,
                 return_contribution: bool):
         e = torch.exp(density_raw)
-        density = activation_scale * e  # vorotracing.py:346-347, the same two torch operations
-        (rgba, depth, depth_indices, contribution, num_intersections, distortion, W_total, S_total,
-         t_far) = _C.trace_vorotracing_fwd(points, diffuse, specular, density, adjacency, offsets, rays, start_point,
-                                          depth_quantiles, weight_threshold, max_intersections, return_contribution)
-        ctx.save = (points, diffuse, specular, density, e, adjacency, offsets, rays, start_point, depth_quantiles,
-                    rgba, depth_indices, distortion, W_total, S_total, t_far)
+        density = activation_scale * e
+        outputs, ctx.record = autograd.run_forward((points, diffuse, specular, density, adjacency, offsets), rays,
+                                                   start_point, depth_quantiles, weight_threshold, max_intersections,
+                                                   return_contribution)
+        ctx.exp_raw = e
         ctx.activation_scale = float(activation_scale)
-        ctx.weight_threshold = weight_threshold
-        ctx.max_intersections = max_intersections
-        errbox = ErrorBox()
-        ctx.errbox = errbox
-        return rgba, depth, contribution, num_intersections, errbox, distortion
+        return outputs
 
     @staticmethod
-    def backward(ctx, grad_rgba, grad_depth, grad_contribution, grad_num_intersections, errbox_grad,
-                 grad_distortion):
-        (points, diffuse, specular, density, e, adjacency, offsets, rays, start_point, depth_quantiles, rgba,
-         depth_indices, distortion, W_total, S_total, t_far) = ctx.save
-        contribution_alpha_grad = 0.0
-        if grad_contribution is not None:
-            contribution_alpha_grad = float(grad_contribution.detach().abs().max().item())
-        if grad_rgba is None:
-            grad_rgba = torch.zeros_like(rgba)
-
-        def _bwd(grad_rgba_, grad_depth_, ray_error_, contrib_, grad_distortion_):
-            return _C.trace_vorotracing_bwd(points, diffuse, specular, density, adjacency, offsets, rays,
-                                            start_point, rgba, grad_rgba_, depth_quantiles, depth_indices,
-                                            grad_depth_, ray_error_, contrib_, distortion, grad_distortion_,
-                                            W_total, S_total, t_far, ctx.weight_threshold, ctx.max_intersections)
-
-        cell_gate = getattr(ctx.errbox, "cell_distortion_gate", None)
-        if cell_gate is not None and grad_distortion is not None:
-            res_d = _bwd(torch.zeros_like(grad_rgba), None, None, 0.0, grad_distortion)
-            density_grad_dist = res_d[3]
-            points_grad, diffuse_grad, specular_grad, density_grad, _ray_grad, point_error = _bwd(
-                grad_rgba, grad_depth, ctx.errbox.ray_error, contribution_alpha_grad,
-                torch.zeros_like(grad_distortion))
-            torch.nan_to_num(density_grad_dist, nan=0.0, posinf=0.0, neginf=0.0, out=density_grad_dist)
-            density_grad = density_grad + cell_gate.reshape_as(density_grad) * density_grad_dist
-        else:
-            points_grad, diffuse_grad, specular_grad, density_grad, _ray_grad, point_error = _bwd(
-                grad_rgba, grad_depth, ctx.errbox.ray_error, contribution_alpha_grad, grad_distortion)
-        ctx.errbox.point_error = point_error
+    def backward(ctx, grad_rgba, grad_depth, grad_contribution, _grad_n, _grad_box, grad_distortion):
+        rec, e = ctx.record, ctx.exp_raw
+        ctx.record = ctx.exp_raw = None
+        up = autograd.upstream_of(rec, grad_rgba, grad_depth, grad_contribution, grad_distortion)
+        pg, dg, sg, ds = autograd.scene_gradients(rec, up)
         raw_grad = torch.empty_like(e)
-        n = e.numel()
-        _lib.call("vt_grad_epilogue", points_grad.data_ptr(), points_grad.numel(), diffuse_grad.data_ptr(),
-                  diffuse_grad.numel(), specular_grad.data_ptr(), specular_grad.numel(),
-                  density_grad.contiguous().data_ptr(), e.data_ptr(), ctx.activation_scale, n,
+        _lib.call("vt_grad_epilogue", pg.data_ptr(), pg.numel(), dg.data_ptr(), dg.numel(), sg.data_ptr(),
+                  sg.numel(), ds.contiguous().data_ptr(), e.data_ptr(), ctx.activation_scale, e.numel(),
                   raw_grad.data_ptr(), native._s(e.device))
-        return (points_grad, diffuse_grad, specular_grad, raw_grad, None, None, None, None, None, None, None, None,
-                None)
+        return (pg, dg, sg, raw_grad, None, None, None, None, None, None, None, None, None)
 
 
 def fused_forward(model, rays, start_point=None, depth_quantiles=None, weight_threshold: float = 0.001,
                   max_intersections: int = 1024, return_contribution: bool = False):
     """``VoroTracing.forward`` (vorotracing.py:365-419) through FusedTraceVoroTracing:
     same outputs; the density gradient arrives at ``model.density`` (raw)."""
-    if start_point is None:
-        start_point = model.get_starting_point(rays)
-    else:
-        start_point = torch.broadcast_to(start_point, rays.shape[:-1])
     return FusedTraceVoroTracing.apply(model.primal_points, model.att_diffuse, model.att_specular, model.density,
                                        model.config.activation_scale, model.point_adjacency,
-                                       model.point_adjacency_offsets, rays, start_point, depth_quantiles,
-                                       weight_threshold, max_intersections, return_contribution)
+                                       model.point_adjacency_offsets, rays, model.start_cells(rays, start_point),
+                                       depth_quantiles, weight_threshold, max_intersections, return_contribution)
 
 
 class FusedVoroAdam:
