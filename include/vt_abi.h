@@ -257,6 +257,18 @@ int vt_bvh_build(void *handle, const float *points, uint32_t num_points, vt_stre
 int vt_bvh_query(void *handle, const float *points, uint32_t num_points, const float *queries, uint32_t num_queries,
                  int32_t *out, vt_stream_t stream);
 int vt_bvh_num_nodes(void *handle);
+/*
+ * The query of vt_bvh_query (nn_bvh.cu:91-109) without the handle's
+ * workspace: when the all-sites scan is the faster path (num_queries *
+ * num_points <= VT_NN_SCAN_PAIRS) its per-block partials go in `workspace`
+ * (8-byte aligned, vt_nearest_scan_workspace_size(num_queries) bytes; with
+ * less, or NULL, the tree is walked).  The handle is only read, so queries of
+ * one built handle may run on several streams at once.
+ */
+#define VT_NN_SCAN_PAIRS (1ull << 26)
+size_t vt_nearest_scan_workspace_size(uint32_t num_queries);
+int vt_bvh_query_ws(void *handle, const float *points, uint32_t num_points, const float *queries, uint32_t num_queries,
+                    int32_t *out, void *workspace, size_t workspace_bytes, vt_stream_t stream);
 /* Test hook (no reference counterpart): caps the tree walk's stack at `limit`
  * entries (1..64; 0 restores 64) and, if force_tree, makes every query walk
  * the tree.  A query whose stack would overflow answers by a scan of all

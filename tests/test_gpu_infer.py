@@ -13,6 +13,8 @@ import torch
 from oracle import core, host_ops
 from tests import helpers as H
 from vorotracing_amd import _C, camera, native
+from vorotracing_amd.infer import VoroTracingInfer
+from vorotracing_amd.model import VoroTracing
 
 pytestmark = pytest.mark.gpu
 
@@ -281,3 +283,20 @@ def test_infer_empty_batch(gpu):
                            adj, rays, start, weight_threshold=0.01)
     torch.cuda.synchronize()
     assert tuple(got.shape) == (0, 4)
+
+
+@pytest.mark.parametrize("in_flight", [2, 3])
+def test_render_frames_overlapped_equal_serial(gpu, in_flight):
+    """Frames rendered with several in flight on side streams (start-cell
+    queries included, each with its own scan workspace) equal serial renders
+    bit for bit."""
+    s = H.mini_heightfield()
+    model = VoroTracing.from_scene(s, device=gpu)
+    inf = VoroTracingInfer(model, sort_morton=True, quantize="fp16")
+    frames = [H.to_dev(camera.orbit_rays(k, 96, 64), gpu) for k in range(9)]
+    want = [inf.render(r, weight_threshold=0.01, cell_skip_threshold=1e-3) for r in frames]
+    got = inf.render_frames(frames, in_flight=in_flight, weight_threshold=0.01, cell_skip_threshold=1e-3)
+    torch.cuda.synchronize()
+    assert len(got) == len(want)
+    for a, b in zip(got, want):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))

@@ -438,9 +438,14 @@ class NNBVH:
         out = torch.empty((nq,), dtype=torch.int32, device=q.device)
         if nq == 0:
             return out
+        # The scan path's partials come from torch's stream-ordered allocator,
+        # not from the handle, so renders on several streams may query at once.
+        ws = None
+        if nq * self._n <= _lib.NN_SCAN_PAIRS:
+            ws = torch.empty(_lib.load().vt_nearest_scan_workspace_size(nq), dtype=torch.uint8, device=q.device)
         with torch.cuda.device(q.device):
-            _lib.call("vt_bvh_query", self._h, pts.data_ptr(), pts.size(0), q.data_ptr(), nq, out.data_ptr(),
-                      _stream(q.device))
+            _lib.call("vt_bvh_query_ws", self._h, pts.data_ptr(), pts.size(0), q.data_ptr(), nq, out.data_ptr(),
+                      None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), _stream(q.device))
         return out
 
 

@@ -55,6 +55,8 @@ SIGNATURES = {
     "vt_bvh_build": ([P, P, U32, P], C.c_int),
     "vt_bvh_query": ([P, P, U32, P, U32, P, P], C.c_int),
     "vt_bvh_num_nodes": ([P], C.c_int),
+    "vt_nearest_scan_workspace_size": ([U32], C.c_size_t),
+    "vt_bvh_query_ws": ([P, P, U32, P, U32, P, P, C.c_size_t, P], C.c_int),
     "vt_bvh_debug_stack_limit": ([P, U32, I32], C.c_int),
     "vt_nearest_sites_noalloc": ([P, U32, P, U32, P, P], C.c_int),
     "vt_tile_perm": ([U32, U32, U32, U32, P, P], C.c_int),
@@ -65,6 +67,11 @@ SIGNATURES = {
     "vt_quantize_workspace_size": ([], C.c_size_t),
     "vt_pad_3to4_f16": ([P, U32, U32, P, P], C.c_int),
 }
+
+
+# include/vt_abi.h VT_NN_SCAN_PAIRS: up to this many query-site pairs a start-cell
+# query scans all sites (vt_bvh_query_ws then needs its workspace)
+NN_SCAN_PAIRS = 1 << 26
 
 
 class VTError(RuntimeError):

@@ -437,35 +437,71 @@ extern "C" int vt_bvh_build(void *handle, const float *points, uint32_t num_poin
     return VT_OK;
 }
 
-extern "C" int vt_bvh_query(void *handle, const float *points, uint32_t num_points, const float *queries,
-                            uint32_t num_queries, int32_t *out, vt_stream_t stream)
+namespace vt {
+
+// The all-sites scan (nn_scan_kernel + nn_pick_kernel) into `partial`
+// (num_queries * NN_SCAN_BLOCKS entries).
+static int launch_scan(const float *points, uint32_t num_points, const float *queries, uint32_t num_queries,
+                       uint2 *partial, int32_t *out, hipStream_t stream)
 {
-    clear_error();
-    BvhHandle *h = (BvhHandle *)handle;
+    nn_scan_kernel<<<dim3(NN_SCAN_BLOCKS, num_queries), NN_SCAN_BLOCK, 0, stream>>>(points, num_points, queries,
+                                                                                   partial);
+    VT_LAUNCH_CHECK("nn_scan_kernel");
+    nn_pick_kernel<<<num_queries, 64, 0, stream>>>(partial, out);
+    VT_LAUNCH_CHECK("nn_pick_kernel");
+    return VT_OK;
+}
+
+static bool scan_is_faster(const BvhHandle *h, uint32_t num_queries)
+{
+    return !h->force_tree && (uint64_t)num_queries * h->n <= NN_SCAN_PAIRS && num_queries <= 65535u;
+}
+
+static int query_common(BvhHandle *h, const float *points, uint32_t num_points, const float *queries,
+                        uint32_t num_queries, int32_t *out, uint2 *partial, size_t partial_entries,
+                        hipStream_t stream)
+{
     VT_REQUIRE(h, "null BVH handle");
     VT_REQUIRE(h->n > 0, "BVH must be built before querying");
     VT_REQUIRE(num_points == h->n, "points must be the point set the BVH was built on (%u vs %u)", num_points, h->n);
     if (num_queries == 0)
         return VT_OK;
     VT_REQUIRE(points && queries && out, "null pointer argument");
-    if (!h->force_tree && (uint64_t)num_queries * h->n <= NN_SCAN_PAIRS && num_queries <= 65535u) {
-        // the partials live in the handle's workspace when it has room
-        const size_t need = (size_t)num_queries * NN_SCAN_BLOCKS * 2;
-        if (need <= h->ws_words) {
-            uint2 *partial = reinterpret_cast<uint2 *>(h->ws);
-            nn_scan_kernel<<<dim3(NN_SCAN_BLOCKS, num_queries), NN_SCAN_BLOCK, 0, as_stream(stream)>>>(
-                points, h->n, queries, partial);
-            VT_LAUNCH_CHECK("nn_scan_kernel");
-            nn_pick_kernel<<<num_queries, 64, 0, as_stream(stream)>>>(partial, out);
-            VT_LAUNCH_CHECK("nn_pick_kernel");
-            return VT_OK;
-        }
-    }
-    bvh_query_kernel<<<(num_queries + 255) / 256, 256, 0, as_stream(stream)>>>(
+    if (partial && scan_is_faster(h, num_queries) && (size_t)num_queries * NN_SCAN_BLOCKS <= partial_entries)
+        return launch_scan(points, h->n, queries, num_queries, partial, out, stream);
+    bvh_query_kernel<<<(num_queries + 255) / 256, 256, 0, stream>>>(
         h->nodes, h->leaf_idx, h->n, points, queries, num_queries, out,
         h->stack_limit < (uint32_t)BVH_STACK ? h->stack_limit : (uint32_t)BVH_STACK);
     VT_LAUNCH_CHECK("bvh_query_kernel");
     return VT_OK;
+}
+
+} // namespace vt
+
+extern "C" int vt_bvh_query(void *handle, const float *points, uint32_t num_points, const float *queries,
+                            uint32_t num_queries, int32_t *out, vt_stream_t stream)
+{
+    clear_error();
+    BvhHandle *h = (BvhHandle *)handle;
+    // the scan's partials live in the handle's workspace when it has room
+    return query_common(h, points, num_points, queries, num_queries, out,
+                        h ? reinterpret_cast<uint2 *>(h->ws) : nullptr, h ? h->ws_words / 2 : 0, as_stream(stream));
+}
+
+extern "C" size_t vt_nearest_scan_workspace_size(uint32_t num_queries)
+{
+    return (size_t)num_queries * NN_SCAN_BLOCKS * sizeof(uint2);
+}
+
+extern "C" int vt_bvh_query_ws(void *handle, const float *points, uint32_t num_points, const float *queries,
+                               uint32_t num_queries, int32_t *out, void *workspace, size_t workspace_bytes,
+                               vt_stream_t stream)
+{
+    clear_error();
+    VT_REQUIRE(!workspace_bytes || workspace, "null workspace with a nonzero size");
+    VT_REQUIRE(((uintptr_t)workspace & 7u) == 0, "workspace must be 8-byte aligned");
+    return query_common((BvhHandle *)handle, points, num_points, queries, num_queries, out,
+                        reinterpret_cast<uint2 *>(workspace), workspace_bytes / sizeof(uint2), as_stream(stream));
 }
 
 // ---- allocation-free nearest-site scan -------------------------------------
@@ -523,12 +559,7 @@ extern "C" int vt_nearest_sites_noalloc(const float *points, uint32_t num_points
     int rc = scratch_ptr_current_device(&partial);
     if (rc)
         return rc;
-    nn_scan_kernel<<<dim3(NN_SCAN_BLOCKS, num_queries), NN_SCAN_BLOCK, 0, as_stream(stream)>>>(points, num_points,
-                                                                                              queries, partial);
-    VT_LAUNCH_CHECK("nn_scan_kernel");
-    nn_pick_kernel<<<num_queries, 64, 0, as_stream(stream)>>>(partial, out);
-    VT_LAUNCH_CHECK("nn_pick_kernel");
-    return VT_OK;
+    return launch_scan(points, num_points, queries, num_queries, partial, out, as_stream(stream));
 }
 
 extern "C" int vt_bvh_debug_stack_limit(void *handle, uint32_t limit, int force_tree)

@@ -184,6 +184,37 @@ class VoroTracingInfer:
         spread = (cams,) + (1,) * (len(lead) - 1) if rays.dim() == 4 else (1,) * len(lead)
         return cells.reshape(spread).expand(lead).contiguous()
 
+    def render_frames(self, frames, in_flight: int = 2, **render_kw):
+        """``render`` of a sequence of frames (each a rays tensor as ``render``
+        takes, with ``render``'s keyword arguments) with up to ``in_flight``
+        frames on the GPU at once: frame k renders on side stream k mod
+        in_flight, so the end of one frame, when few waves are left, overlaps
+        the start of the next.  Every frame is a whole render (its own
+        start-cell query and traversal); outputs come back in order.  On
+        return the caller's stream is ordered after every frame, as after
+        ``render``.  Side streams keep the default priority."""
+        cur = torch.cuda.current_stream(self.device)
+        streams = self._side_streams(in_flight)
+        for s in streams:
+            s.wait_stream(cur)
+        outs = []
+        for k, rays in enumerate(frames):
+            with torch.cuda.stream(streams[k % len(streams)]):
+                out = self.render(rays, **render_kw)
+            out.record_stream(cur)  # allocated on the side stream, used on the caller's
+            outs.append(out)
+        for s in streams:
+            cur.wait_stream(s)
+        return outs
+
+    def _side_streams(self, n: int):
+        if n < 1:
+            raise ValueError("in_flight must be at least 1")
+        cache = getattr(self, "_streams", None)
+        if cache is None or len(cache) < n:
+            cache = self._streams = [torch.cuda.Stream(device=self.device) for _ in range(n)]
+        return cache[:n]
+
     @torch.no_grad()
     def _tile_perm(self, H, W, TH=8, TW=8):
         """vorotracing.py:606-625 (int32, cached), from vt_tile_perm."""
