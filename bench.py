@@ -26,6 +26,11 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+# Wave64 VALU instructions MI355X can issue per second: its 157.3 TFLOP/s FP32
+# vector peak is 256 CUs x 4 SIMDs x 32 lanes x 2 flops x 2.4 GHz, i.e. one
+# wave64 instruction per SIMD every 2 cycles.
+VALU_PEAK_PER_S = 256 * 4 * 2.4e9 / 2
+IN_FLIGHT = 2
 
 
 def log(*a):
@@ -44,6 +49,58 @@ def b_alg(st, tex_bytes=64, per_ray_extra=0):
     s = (st.view(torch.int32).to(torch.int64) & 0xffffffff).sum(0).tolist()
     nr = st.shape[0]
     return (48 + per_ray_extra) * nr + 8 * s[1] + 8 * s[2] + 16 * s[3] + 4 * s[4] + tex_bytes * s[5], s
+
+
+def train_bytes(st, fwd=True, attr_bytes=4):
+    """Logical bytes of a training walk from its per-ray counters (u32 (R,8)):
+    the walk's bytes as in b_alg, textures 2 maps x 4 taps x 3 channels x attr
+    bytes per shaded cell (96 f32).  Forward per ray: ray 24, start 4 + site
+    12, rgba 16, n 4, distortion/W/S/t_far 16.  Backward per ray: ray 24,
+    start 4, rgba and its gradient 32, distortion/W/S/t_far 16; per integrated
+    cell also 28 f32 atomic read-modify-writes (224 B)."""
+    import torch
+
+    s = (st.view(torch.int32).to(torch.int64) & 0xffffffff).sum(0).tolist()
+    nr = st.shape[0]
+    tex = 24 * attr_bytes
+    walk = 8 * s[1] + 8 * s[2] + 16 * s[3] + 4 * s[4] + tex * s[5]
+    if fwd:
+        return 76 * nr + walk
+    return 76 * nr + walk + 224 * s[4]
+
+
+def roofline_record(kernel_ms, logical_bytes, profile_name, kernel_key=None):
+    """Roofline of a traversal kernel against MI355X's 8 TB/s HBM: achieved =
+    the kernel's memory traffic per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE,
+    each scaled by what it reads for a 1 GiB copy; profiles/<profile_name>)
+    over its mean duration measured here.  The logical bytes (every record as
+    the walk reads it) are reported beside it: L2 and the MALL serve most of
+    them, so their rate is no fraction of the DRAM peak.  When the profile
+    holds the kernel's VALU instruction count, its issue rate is reported
+    against MI355X's VALU issue peak."""
+    sec = kernel_ms * 1e-3
+    rec = {"bound": "hbm", "achieved": None, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": None, "traffic": None,
+           "kernel_ms": round(kernel_ms, 4), "logical_bytes_per_launch": int(logical_bytes),
+           "logical_gbs": round(logical_bytes / sec / 1e9, 1)}
+    path = os.path.join(ROOT, "profiles", profile_name)
+    if not os.path.exists(path):
+        return rec
+    with open(path) as f:
+        tr = json.load(f)
+    if kernel_key:
+        tr = tr[kernel_key]
+    traffic = int(tr["hbm_bytes_per_launch"])
+    rec["traffic"] = traffic
+    rec["achieved"] = round(traffic / sec / 1e9, 1)
+    rec["frac"] = round(traffic / sec / 1e9 / HBM_PEAK_GBS, 4)
+    rec["traffic_source"] = f"profiles/{profile_name} (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)"
+    if "valu_insts_per_launch" in tr:
+        rate = tr["valu_insts_per_launch"] / sec
+        rec["valu"] = {"insts_per_launch": int(tr["valu_insts_per_launch"]), "issue_per_s": round(rate / 1e9, 1),
+                       "peak_per_s": round(VALU_PEAK_PER_S / 1e9, 1), "unit": "G wave64 instructions/s",
+                       "frac": round(rate / VALU_PEAK_PER_S, 4),
+                       "lanes_per_inst": tr.get("valu_lanes_per_inst")}
+    return rec
 
 
 def cpu_info():
@@ -137,8 +194,12 @@ def main():
         inf.render(poses[i % args.poses], weight_threshold=thr, cell_skip_threshold=skip)
     torch.cuda.synchronize()
 
-    # timed region: K renders, events around each traversal launch on its stream
+    kw = dict(weight_threshold=thr, cell_skip_threshold=skip)
     K = args.steps
+
+    # Serial frames, the reference's protocol (benchmark_eval.py:137-158): one
+    # render after the other on one stream.  HIP events on that stream around
+    # each traversal launch give the kernel's duration.
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
     frames = []
     torch.cuda.synchronize()
@@ -147,16 +208,32 @@ def main():
         rays = poses[i % args.poses]
         sp = inf.get_starting_point(rays)
         ev[i][0].record(stream)
-        out = inf.render(rays, start_point=sp, weight_threshold=thr, cell_skip_threshold=skip)
+        frames.append(inf.render(rays, start_point=sp, **kw))
         ev[i][1].record(stream)
-        frames.append(out)
+    torch.cuda.synchronize()
+    t_serial = time.perf_counter() - t_start
+    kernel_avg_ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
+    log(f"serial: {K} frames, {1000 * t_serial / K:.3f} ms/frame, {K / t_serial:.1f} FPS, "
+        f"traversal kernel {kernel_avg_ms:.3f} ms")
+
+    # The same frames with two in flight (VoroTracingInfer.render_frames): frame
+    # k renders (start-cell query and traversal) on side stream k mod 2, so the
+    # end of one frame, when few waves are left, overlaps the start of the
+    # next.  Every frame is a whole render, checked bit for bit against the
+    # serial frames.
+    seq = [poses[i % args.poses] for i in range(K)]
+    inf.render_frames(seq[:min(K, 8)], in_flight=IN_FLIGHT, **kw)
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    piped = inf.render_frames(seq, in_flight=IN_FLIGHT, **kw)
     torch.cuda.synchronize()
     t_total = time.perf_counter() - t_start
-    kern_ms = [a.elapsed_time(b) for a, b in ev]
+    same_frames = all(torch.equal(a.view(torch.int16), b.view(torch.int16)) for a, b in zip(piped, frames))
+    del piped
     ms_per_step = 1000.0 * t_total / K
     fps = K / t_total
-    kernel_avg_ms = float(np.mean(kern_ms))
-    log(f"timed {K} frames: {ms_per_step:.3f} ms/frame, {fps:.1f} FPS, traversal kernel {kernel_avg_ms:.3f} ms")
+    log(f"timed {K} frames, {IN_FLIGHT} in flight: {ms_per_step:.3f} ms/frame, {fps:.1f} FPS; "
+        f"frames bit-identical to the serial renders: {same_frames}")
 
     result = {
         "metric": "FPS @1237x822 1M cells fp16; fwd+bwd ms/step; achieved HBM GB/s",
@@ -174,7 +251,15 @@ def main():
         "config": {"workload": "C3: fp16 inference render, 1,048,576 sites (Morton-sorted), 4x4 octahedral "
                                "textures, 1237x822 pinhole orbit x32 poses, thr 0.01, skip 1e-3",
                    "sites": sc.num_points, "faces": sc.num_faces, "width": W, "height": H, "poses": args.poses,
-                   "tiling": "8x8 wave64 tiles in-kernel", "parallelism": "single GPU"},
+                   "tiling": "8x8 wave64 tiles in-kernel", "parallelism": "single GPU",
+                   "frames_in_flight": IN_FLIGHT,
+                   "timing": f"{K} whole renders (start-cell query + traversal each), frame k on side stream k mod "
+                             f"{IN_FLIGHT} (VoroTracingInfer.render_frames), wall clock between synchronizations; "
+                             "every frame complete and bit-identical to the serial render"},
+        "serial": {"fps": round(K / t_serial, 2), "ms_per_frame": round(1000 * t_serial / K, 4),
+                   "kernel_ms": round(kernel_avg_ms, 4),
+                   "note": "one render after the other on one stream (benchmark_eval.py:137-158)"},
+        "frames_identical_to_serial": same_frames,
     }
 
     if not args.profile:
@@ -184,18 +269,14 @@ def main():
         nr = W * H
         st = native.new_stats(nr, dev)
         for k in range(args.poses):
-            inf.render(poses[k], weight_threshold=thr, cell_skip_threshold=skip, stats=st)
+            inf.render(poses[k], stats=st, **kw)
             b, s = b_alg(st)
             tot_b += b
             tot_s += np.array(s[:6], np.int64)
         torch.cuda.synchronize()
         bytes_per_frame = tot_b / args.poses
-        achieved = bytes_per_frame / (kernel_avg_ms * 1e-3) / 1e9
-        result["roofline"] = {
-            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "bytes_per_launch": int(bytes_per_frame), "kernel_ms": round(kernel_avg_ms, 4),
-        }
+        result["roofline"] = roofline_record(kernel_avg_ms, bytes_per_frame, "traffic_infer_f16_c3.json")
+        result["roofline"]["stream_copy_gbs"] = round(stream_copy_gbs(dev), 1)
         result["walk"] = {
             "rays_per_frame": nr,
             "steps_per_ray": round(float(tot_s[1]) / (nr * args.poses), 2),
@@ -203,15 +284,10 @@ def main():
             "shaded_per_ray": round(float(tot_s[5]) / (nr * args.poses), 2),
             "mrays_per_s": round(nr * fps / 1e6, 1),
         }
-        log(f"B_alg {bytes_per_frame / 1e9:.3f} GB/frame -> {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%})")
-        prof = os.path.join(ROOT, "profiles", "traffic_infer_f16_c3.json")
-        if os.path.exists(prof):
-            with open(prof) as f:
-                tr = json.load(f)
-            result["roofline"]["traffic"] = tr.get("hbm_bytes_per_launch")
-            result["roofline"]["traffic_source"] = "profiles/traffic_infer_f16_c3.json (rocprofv3 --pmc)"
-        result["roofline"]["stream_copy_gbs"] = round(stream_copy_gbs(dev), 1)
-        result["c4_q8"] = c4_q8(model, poses, dev, log, thr, skip)
+        r = result["roofline"]
+        log(f"HBM {r['achieved']:.0f} GB/s ({r['frac']:.1%} of peak); logical bytes {bytes_per_frame / 1e9:.2f} "
+            f"GB/frame; VALU issue {r.get('valu', {}).get('frac', float('nan')):.1%}")
+        result["c4_q8"] = c4_q8(model, poses, dev, log, thr, skip, cpu=not args.no_cpu)
 
     if not args.no_cpu and not args.profile:
         from oracle import core as oc
@@ -259,6 +335,8 @@ def main():
         result["walk"].update(compulsory_bytes(oc, pts, d4, s4, den, adj, off, ad, poses[0], inf, thr, skip, cores))
 
 
+    if not args.profile:
+        result["c1_fwd"] = c1_forward(dev, log, cpu=not args.no_cpu)
     if not args.no_train and not args.profile:
         result["train_c2"] = train_c2(dev, log, cpu=not args.no_cpu)
     if not args.no_voronoi and not args.profile:
@@ -351,9 +429,11 @@ def stream_copy_gbs(dev):
     return 2 * (1 << 30) / per / 1e9
 
 
-def c4_q8(model, poses, dev, log, thr, skip):
+def c4_q8(model, poses, dev, log, thr, skip, cpu=False):
     """Config-4 shape: q8 attributes with per-channel scale/offset, 8 cameras
-    (poses 0, 4, ..., 28) rendered in one launch with one start cell per camera."""
+    (poses 0, 4, ..., 28) rendered in one launch with one start cell per camera.
+    With ``cpu``, the oracle renders camera 0 of the batch (1 of 8) as the CPU
+    baseline and is compared with the GPU's image: alpha bit for bit."""
     import numpy as np
     import torch
 
@@ -375,10 +455,89 @@ def c4_q8(model, poses, dev, log, thr, skip):
     ms = a.elapsed_time(b) / K
     nr = batch.numel() // 6
     log(f"C4 q8, {batch.shape[0]} cameras per launch: {ms:.3f} ms/launch, {nr / ms / 1e3:.1f} Mrays/s")
+    out = {"ms_per_launch": round(ms, 3), "cameras": 8, "rays_per_launch": nr,
+           "mrays_per_s": round(nr / ms / 1e3, 1), "attributes": "u8, per-channel scale/offset",
+           "note": "BASELINE.json configs[3] shape; parity in tests/test_gpu_fullsize.py, tests/test_gpu_prep.py"}
+    if cpu:
+        from oracle import core as oc
+
+        cores, model_name = cpu_info()
+        gpu = inf8.render(batch, start_point=sp, weight_threshold=thr, cell_skip_threshold=skip)[0].cpu().numpy()
+        r0 = batch[0].cpu().numpy()
+        sp0 = sp[0].cpu().numpy()
+        args = (inf8.primal_points.cpu().numpy(), inf8.diffuse_q8.cpu().numpy(), inf8.specular_q8.cpu().numpy(), 4, 4,
+                inf8.diff_scale, inf8.diff_offset, inf8.spec_scale, inf8.spec_offset,
+                inf8.density.reshape(-1).cpu().numpy(), inf8.point_adjacency.cpu().numpy(),
+                inf8.point_adjacency_offsets.cpu().numpy(), inf8.adjacent_diff.cpu().numpy(), r0, sp0)
+        t = time.perf_counter()
+        want, _ = oc.trace_infer_q8(*args, weight_threshold=thr, cell_skip_threshold=skip, threads=cores)
+        dt = time.perf_counter() - t
+        same = bool(np.array_equal(gpu[..., 3].view(np.uint16), want[..., 3].view(np.uint16)))
+        nr1 = r0.size // 6
+        out["cpu_baseline"] = {
+            "value": round(dt * 1000, 1), "unit": "ms per camera", "cores": cores, "kind": "port",
+            "sample": f"camera 0 of the 8 (1 of 8, {nr1} rays); oracle/oracle.c OpenMP on {model_name or 'host CPU'}",
+            "mrays_per_s": round(nr1 / dt / 1e6, 3), "alpha_bit_identical_to_gpu": same,
+            "rgb_max_abs_diff_vs_gpu": float(np.abs(gpu[..., :3].astype(np.float32)
+                                                    - want[..., :3].astype(np.float32)).max())}
+        log(f"C4 CPU oracle: {dt * 1000:.0f} ms for 1 of 8 cameras on {cores} threads; alpha identical: {same}")
     del inf8, batch
-    return {"ms_per_launch": round(ms, 3), "cameras": 8, "rays_per_launch": nr,
-            "mrays_per_s": round(nr / ms / 1e3, 1), "attributes": "u8, per-channel scale/offset",
-            "note": "BASELINE.json configs[3] shape; parity in tests/test_gpu_prep.py"}
+    return out
+
+
+def c1_forward(dev, log, cpu=False, K=20):
+    """Config 1: fp32 forward render of the 4,096-site
+    sphere scene through one 128x128 pinhole (radius 4, 60 deg), thr 0.01,
+    timed as the reference's protocol (10 warm-up, then K renders between HIP
+    events).  With ``cpu``, the oracle renders the same whole frame (repeated
+    for about a second of CPU work) and is compared bit for bit."""
+    import numpy as np
+    import torch
+
+    from vorotracing_amd import camera, scene
+    from vorotracing_amd.model import VoroTracing
+
+    sc = scene.cached(scene.config1, 0)
+    model = VoroTracing.from_scene(sc, device=dev)
+    rays = torch.from_numpy(camera.pinhole_rays(128, 128, eye=(0.0, -4.0, 0.0))).to(dev)
+    sp = model.get_starting_point(rays)
+    with torch.no_grad():
+        for _ in range(10):
+            model(rays, start_point=sp, weight_threshold=0.01)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(K):
+            rgba = model(rays, start_point=sp, weight_threshold=0.01)[0]
+        b.record()
+        torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / K
+    nr = rays.numel() // 6
+    out = {"ms_per_frame": round(ms, 4), "mrays_per_s": round(nr / ms / 1e3, 1), "rays": nr,
+           "sites": sc.num_points, "dtype": "fp32",
+           "workload": "C1: training forward only, 4,096 sites (sphere shell + background), 4x4 fp32 textures, "
+                       "one 128x128 pinhole, thr 0.01"}
+    log(f"C1 forward: {ms:.4f} ms/frame, {out['mrays_per_s']} Mrays/s")
+    if cpu:
+        from oracle import core as oc
+
+        cores, model_name = cpu_info()
+        args = (sc.points, sc.diffuse, sc.specular, 4, 4, model.activated_density().detach().cpu().numpy(),
+                sc.adjacency, sc.offsets, rays.cpu().numpy(), sp.cpu().numpy())
+        reps, dt = 0, 0.0
+        while dt < 1.0:
+            t = time.perf_counter()
+            want = oc.trace_fwd(*args, weight_threshold=0.01, threads=cores)
+            dt += time.perf_counter() - t
+            reps += 1
+        same = bool(np.array_equal(rgba.cpu().numpy().view(np.uint32), want["rgba"].view(np.uint32)))
+        out["cpu_baseline"] = {"value": round(1000 * dt / reps, 3), "unit": "ms/frame", "cores": cores,
+                               "kind": "port",
+                               "sample": f"the whole frame ({nr} rays), {reps} times; oracle/oracle.c OpenMP on "
+                                         f"{model_name or 'host CPU'}",
+                               "mrays_per_s": round(nr * reps / dt / 1e6, 3), "rgba_bit_identical_to_gpu": same}
+        log(f"C1 CPU oracle: {1000 * dt / reps:.2f} ms/frame on {cores} threads; rgba identical: {same}")
+    return out
 
 
 def train_c2(dev, log, cpu=False):
@@ -430,10 +589,59 @@ def train_c2(dev, log, cpu=False):
            "rays": 480000, "sites": sc.num_points, "dtype": "fp32",
            "workload": "C2: TraceVoroTracing forward + backward, 262,144 sites (torus + background), 4x4 fp32 "
                        "textures, one 800x600 pinhole camera, upstream dL/dRGB ~ N(0,1), thr 0.001"}
+    out["roofline_fwd"], out["roofline_bwd"] = train_rooflines(model, rays, sp, g, dev, log)
     out["full_step"] = train_step_c2(sc, dev, rays, sp, g, log)
     if cpu:
         out["cpu_baseline"] = train_c2_cpu(model, rays, sp, g, log)
     return out
+
+
+def train_rooflines(model, rays, sp, g, dev, log, R=10):
+    """Rooflines of fwd_kernel and bwd_kernel at C2.  Each _C entry runs the
+    face-offset prefetch and then its traversal kernel; both entries and the
+    prefetch alone are timed with HIP events on the launch stream (R calls
+    each), and the prefetch's time is subtracted.  Logical bytes come from the
+    kernels' own walk counters (train_bytes)."""
+    import numpy as np
+    import torch
+
+    from vorotracing_amd import _C, native
+
+    dens = model.activated_density().detach()
+    scn = (model.primal_points.detach(), model.att_diffuse.detach(), model.att_specular.detach(), dens,
+           model.point_adjacency, model.point_adjacency_offsets)
+    nr = rays.numel() // 6
+    st_f, st_b = native.new_stats(nr, dev), native.new_stats(nr, dev)
+    fw = _C.trace_vorotracing_fwd(*scn, rays, sp, None, 0.001, 1024, False, stats=st_f)
+
+    def bwd(stats=None):
+        return _C.trace_vorotracing_bwd(*scn, rays, sp, fw[0], g, None, None, None, None, 0.0, fw[5], None, fw[6],
+                                        fw[7], fw[8], 0.001, 1024, stats=stats)
+
+    bwd(st_b)
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(R):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / R
+
+    t_pre = timed(lambda: _C.trace_vorotracing_prefetch_adj(scn[0], scn[4], scn[5]))
+    t_fwd = timed(lambda: _C.trace_vorotracing_fwd(*scn, rays, sp, None, 0.001, 1024, False)) - t_pre
+    t_bwd = timed(bwd) - t_pre
+    rf = roofline_record(t_fwd, train_bytes(st_f, True), "traffic_train_c2.json", "fwd_kernel")
+    rb = roofline_record(t_bwd, train_bytes(st_b, False), "traffic_train_c2.json", "bwd_kernel")
+    for r in (rf, rb):
+        r["timing"] = "HIP events around the _C entry minus the face-offset prefetch timed alone"
+    log(f"C2 fwd_kernel {t_fwd:.3f} ms, bwd_kernel {t_bwd:.3f} ms (prefetch {t_pre:.3f} ms); HBM fractions "
+        f"{rf['frac']}, {rb['frac']}")
+    return rf, rb
 
 
 def train_step_c2(sc, dev, rays, sp, g, log, K=10):

@@ -243,10 +243,12 @@ def _attr_code(dtype):
 
 def trace_vorotracing_fwd(points_in, diffuse_in, specular_in, density_in, point_adjacency_in,
                           point_adjacency_offsets_in, rays_in, start_point_in, depth_quantiles_in,
-                          weight_threshold: float, max_intersections: int, return_contribution: bool):
+                          weight_threshold: float, max_intersections: int, return_contribution: bool,
+                          stats: Optional[torch.Tensor] = None):
     """tracing_octmap.cu:346-546.  Returns (rgba, depth, depth_idx,
     contribution, n, distortion, W_total, S_total, t_far); absent outputs are
-    None."""
+    None.  ``stats`` (an extension): None, or a u32 (num_rays, 8) tensor that
+    receives the per-ray walk counters (vt_ray_stats)."""
     points = points_in.contiguous()
     diffuse = diffuse_in.contiguous()
     specular = specular_in.contiguous()
@@ -293,19 +295,28 @@ def trace_vorotracing_fwd(points_in, diffuse_in, specular_in, density_in, point_
                   rays.data_ptr(), num_rays, *_image_dims(rays), start_point.data_ptr(), K, _ptr(depth_quantiles),
                   float(weight_threshold), int(max_intersections), rgba.data_ptr(), _ptr(depth), _ptr(depth_idx),
                   _ptr(contribution), n.data_ptr(), distortion.data_ptr(), W_total.data_ptr(), S_total.data_ptr(),
-                  t_far.data_ptr(), workspace.data_ptr(), None, _stream(dev))
+                  t_far.data_ptr(), workspace.data_ptr(), _stats_ptr(stats, num_rays), _stream(dev))
     return rgba, depth, depth_idx, contribution, n, distortion, W_total, S_total, t_far
+
+
+def _stats_ptr(stats: Optional[torch.Tensor], num_rays: int):
+    if stats is None:
+        return None
+    _assert(stats.is_contiguous() and stats.numel() * stats.element_size() == 32 * num_rays and _is_gpu(stats),
+            "stats must be a contiguous device tensor of num_rays 32-byte records")
+    return stats.data_ptr()
 
 
 def trace_vorotracing_bwd(points_in, diffuse_in, specular_in, density_in, point_adjacency_in,
                           point_adjacency_offsets_in, rays_in, start_point_in, rgb_out, rgb_grad_in,
                           depth_quantiles_in, depth_indices_in, depth_grad_in, ray_error_in,
                           contribution_alpha_grad: float, distortion_in, distortion_grad_in, W_total_in, S_total_in,
-                          t_far_in, weight_threshold: float, max_intersections: int):
+                          t_far_in, weight_threshold: float, max_intersections: int,
+                          stats: Optional[torch.Tensor] = None):
     """tracing_octmap.cu:860-1103.  Returns (points_grad, diffuse_grad,
     specular_grad, density_grad, ray_grad, point_error).  ray_grad is zeros
     (the reference returns it uninitialised and the autograd wrapper drops
-    it)."""
+    it).  ``stats`` as for trace_vorotracing_fwd (an extension)."""
     points = points_in.contiguous()
     diffuse = diffuse_in.contiguous()
     specular = specular_in.contiguous()
@@ -392,8 +403,8 @@ def trace_vorotracing_bwd(points_in, diffuse_in, specular_in, density_in, point_
                   float(contribution_alpha_grad), distortion.data_ptr(), _ptr(distortion_grad),
                   W_total.data_ptr(), S_total.data_ptr(), t_far.data_ptr(), float(weight_threshold),
                   int(max_intersections), points_grad.data_ptr(), diffuse_grad.data_ptr(),
-                  specular_grad.data_ptr(), density_grad.data_ptr(), _ptr(point_error), workspace.data_ptr(), None,
-                  _stream(dev))
+                  specular_grad.data_ptr(), density_grad.data_ptr(), _ptr(point_error), workspace.data_ptr(),
+                  _stats_ptr(stats, num_rays), _stream(dev))
     return points_grad, diffuse_grad, specular_grad, density_grad, ray_grad, point_error
 
 
