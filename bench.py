@@ -221,18 +221,21 @@ def main():
     # end of one frame, when few waves are left, overlaps the start of the
     # next.  Every frame is a whole render, checked bit for bit against the
     # serial frames.
+    # (--profile runs serial frames only, so that each traced dispatch runs alone
+    # and the kernel trace's mean duration is the one the roofline uses.)
     seq = [poses[i % args.poses] for i in range(K)]
-    inf.render_frames(seq[:min(K, 8)], in_flight=IN_FLIGHT, **kw)
+    in_flight = 1 if args.profile else IN_FLIGHT
+    inf.render_frames(seq[:min(K, 8)], in_flight=in_flight, **kw)
     torch.cuda.synchronize()
     t_start = time.perf_counter()
-    piped = inf.render_frames(seq, in_flight=IN_FLIGHT, **kw)
+    piped = inf.render_frames(seq, in_flight=in_flight, **kw)
     torch.cuda.synchronize()
     t_total = time.perf_counter() - t_start
     same_frames = all(torch.equal(a.view(torch.int16), b.view(torch.int16)) for a, b in zip(piped, frames))
     del piped
     ms_per_step = 1000.0 * t_total / K
     fps = K / t_total
-    log(f"timed {K} frames, {IN_FLIGHT} in flight: {ms_per_step:.3f} ms/frame, {fps:.1f} FPS; "
+    log(f"timed {K} frames, {in_flight} in flight: {ms_per_step:.3f} ms/frame, {fps:.1f} FPS; "
         f"frames bit-identical to the serial renders: {same_frames}")
 
     result = {
@@ -252,9 +255,9 @@ def main():
                                "textures, 1237x822 pinhole orbit x32 poses, thr 0.01, skip 1e-3",
                    "sites": sc.num_points, "faces": sc.num_faces, "width": W, "height": H, "poses": args.poses,
                    "tiling": "8x8 wave64 tiles in-kernel", "parallelism": "single GPU",
-                   "frames_in_flight": IN_FLIGHT,
+                   "frames_in_flight": in_flight,
                    "timing": f"{K} whole renders (start-cell query + traversal each), frame k on side stream k mod "
-                             f"{IN_FLIGHT} (VoroTracingInfer.render_frames), wall clock between synchronizations; "
+                             f"{in_flight} (VoroTracingInfer.render_frames), wall clock between synchronizations; "
                              "every frame complete and bit-identical to the serial render"},
         "serial": {"fps": round(K / t_serial, 2), "ms_per_frame": round(1000 * t_serial / K, 4),
                    "kernel_ms": round(kernel_avg_ms, 4),
