@@ -120,41 +120,75 @@ __global__ void bvh_hierarchy_kernel(const uint32_t *__restrict__ keys, uint32_t
         nodes[0].parent = NONE;
 }
 
-// Bottom-up refit: each leaf writes its box into its parent's slot; the
-// second child to arrive at a node (atomic flag) merges and moves up.
-__global__ void bvh_refit_kernel(const float *__restrict__ points, const uint32_t *__restrict__ leaf_idx, uint32_t n,
-                                 BvhNode *nodes, const uint32_t *__restrict__ leaf_parent, uint32_t *flags)
+// Bottom-up refit, one launch per tree level and no memory fences: a node
+// enters a level's list when the second of its two children has written its
+// box into the node's child slot (an atomic count per node), and the next
+// launch reads both boxes, which the kernel boundary has made visible on
+// every XCD.  A node's box goes into its parent's slot, and so on up to the
+// root.  The split prefix lengthens strictly from a node to its children
+// (delta 2..31 for distinct 30-bit codes, 33..63 for index ties), so no path
+// has more than 61 internal nodes; BVH_LEVELS launches cover every tree.
+constexpr int BVH_LEVELS = 64;
+
+__device__ __forceinline__ void put_child_box(BvhNode *nodes, uint32_t parent, uint32_t child, const float *lo,
+                                              const float *hi)
 {
-    uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
+    const int side = nodes[parent].child[0] == child ? 0 : 1;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        nodes[parent].lo[side][c] = lo[c];
+        nodes[parent].hi[side][c] = hi[c];
+    }
+}
+
+// the second child to arrive appends `node` to a level list
+__device__ __forceinline__ void arrive(uint32_t *flags, uint32_t node, uint32_t *list, uint32_t *count)
+{
+    if (atomicAdd(&flags[node], 1u) == 1u)
+        list[atomicAdd(count, 1u)] = node;
+}
+
+__global__ void bvh_leaf_boxes_kernel(const float *__restrict__ points, const uint32_t *__restrict__ leaf_idx,
+                                      uint32_t n, BvhNode *nodes, const uint32_t *__restrict__ leaf_parent,
+                                      uint32_t *flags, uint32_t *list0, uint32_t *counters)
+{
+    const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
     if (k >= n)
         return;
-    f3 p = load_site(points, leaf_idx[k]);
-    float lo[3] = {p.x, p.y, p.z}, hi[3] = {p.x, p.y, p.z};
-    uint32_t child = LEAF | k;
-    uint32_t node = leaf_parent[k];
-    while (node != NONE) {
-        int side = (nodes[node].child[0] == child) ? 0 : 1;
+    const f3 p = load_site(points, leaf_idx[k]);
+    const float b[3] = {p.x, p.y, p.z};
+    const uint32_t parent = leaf_parent[k];
+    put_child_box(nodes, parent, LEAF | k, b, b);
+    arrive(flags, parent, list0, &counters[0]);
+}
+
+// nodes of `in` (counters[level] of them): box = union of the two child
+// boxes, written into the parent's slot
+__global__ void bvh_level_kernel(BvhNode *nodes, uint32_t *flags, const uint32_t *__restrict__ in, uint32_t *out,
+                                 uint32_t *counters, int level)
+{
+    const uint32_t cnt = counters[level];
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < cnt; i += gridDim.x * blockDim.x) {
+        const uint32_t node = in[i];
+        const BvhNode nd = nodes[node];
+        if (nd.parent == NONE)
+            continue;
+        float lo[3], hi[3];
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
-            __hip_atomic_store(&nodes[node].lo[side][c], lo[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&nodes[node].hi[side][c], hi[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            lo[c] = __builtin_fminf(nd.lo[0][c], nd.lo[1][c]);
+            hi[c] = __builtin_fmaxf(nd.hi[0][c], nd.hi[1][c]);
         }
-        __threadfence();
-        uint32_t prev = atomicAdd(&flags[node], 1u);
-        if (prev == 0)
-            return; // the sibling has not finished; it will continue upward
-        __threadfence();
-        int other = 1 - side;
-#pragma unroll
-        for (int c = 0; c < 3; ++c) {
-            float olo = __hip_atomic_load(&nodes[node].lo[other][c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            float ohi = __hip_atomic_load(&nodes[node].hi[other][c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            lo[c] = __builtin_fminf(lo[c], olo);
-            hi[c] = __builtin_fmaxf(hi[c], ohi);
-        }
-        child = node;
-        node = nodes[node].parent;
+        put_child_box(nodes, nd.parent, node, lo, hi);
+        arrive(flags, nd.parent, out, &counters[level + 1]);
     }
+}
+
+__global__ void bvh_zero_kernel(uint32_t *p, uint32_t n)
+{
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n)
+        p[i] = 0u;
 }
 
 __device__ __forceinline__ float box_d2(f3 q, const float *lo, const float *hi)
@@ -429,9 +463,21 @@ extern "C" int vt_bvh_build(void *handle, const float *points, uint32_t num_poin
     if (n > 1) {
         bvh_hierarchy_kernel<<<(n - 1 + 255) / 256, 256, 0, s>>>(keys, n, h->nodes, h->leaf_parent, h->flags);
         VT_LAUNCH_CHECK("bvh_hierarchy_kernel");
-        bvh_refit_kernel<<<(n + 255) / 256, 256, 0, s>>>(points, h->leaf_idx, n, h->nodes, h->leaf_parent,
-                                                         h->flags);
-        VT_LAUNCH_CHECK("bvh_refit_kernel");
+        // level lists (n words each) and BVH_LEVELS + 1 counters in the sort
+        // workspace, free once the tree is built (ws_words >= 4n + 272)
+        uint32_t *lists[2] = {h->ws, h->ws + n};
+        uint32_t *counters = h->ws + 2 * (size_t)n;
+        bvh_zero_kernel<<<1, 128, 0, s>>>(counters, BVH_LEVELS + 1);
+        VT_LAUNCH_CHECK("bvh_zero_kernel");
+        bvh_leaf_boxes_kernel<<<(n + 255) / 256, 256, 0, s>>>(points, h->leaf_idx, n, h->nodes, h->leaf_parent,
+                                                              h->flags, lists[0], counters);
+        VT_LAUNCH_CHECK("bvh_leaf_boxes_kernel");
+        const uint32_t blocks = (uint32_t)(((size_t)n / 2 + 255) / 256 < 1024 ? ((size_t)n / 2 + 255) / 256 : 1024);
+        for (int level = 0; level < BVH_LEVELS; ++level) {
+            bvh_level_kernel<<<blocks ? blocks : 1, 256, 0, s>>>(h->nodes, h->flags, lists[level & 1],
+                                                                lists[(level + 1) & 1], counters, level);
+            VT_LAUNCH_CHECK("bvh_level_kernel");
+        }
     }
     h->n = n;
     return VT_OK;
