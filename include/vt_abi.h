@@ -385,6 +385,17 @@ int vt_adam_voro(float *points, float *points_grad, float *points_m, float *poin
 size_t vt_voronoi_workspace_size(uint32_t num_points);
 int vt_voronoi_build(const float *points, uint32_t num_points, uint32_t *offsets, uint32_t *num_adjacency,
                      void *workspace, vt_stream_t stream);
+/*
+ * vt_voronoi_build with a warm start: guess_offsets (num_points + 1) and
+ * guess_adjacency (u32 CSR, e.g. the adjacency before the sites moved, as the
+ * reference's training refresh can pass to Paragram: initial_guesses,
+ * cuda/__init__.py:16-37) cut each cell first; the result is the same
+ * neighbour sets as without guesses (out-of-range ids are ignored), found
+ * faster when the guesses are close.  NULL, NULL = vt_voronoi_build.
+ */
+int vt_voronoi_build_warm(const float *points, uint32_t num_points, const uint32_t *guess_offsets,
+                          const uint32_t *guess_adjacency, uint32_t *offsets, uint32_t *num_adjacency,
+                          void *workspace, vt_stream_t stream);
 int vt_voronoi_adjacency(uint32_t num_points, const uint32_t *offsets, uint32_t *adjacency, const void *workspace,
                          vt_stream_t stream);
 

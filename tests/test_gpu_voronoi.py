@@ -76,3 +76,44 @@ def test_model_scene_renders_the_same(gpu):
     b = m2(rays, weight_threshold=0.001)[0]
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("guess", ["previous", "shuffled", "junk"])
+def test_warm_start_equals_cold(gpu, guess):
+    """A warm-started build (initial_guesses, cuda/__init__.py:16-37) gives
+    the cold build's CSR and qhull's sets, whatever the guesses: the
+    adjacency before the sites moved (the training refresh), lists of other
+    sites, or ids out of range."""
+    rng = np.random.default_rng(17)
+    pts0 = scene._heightfield_sites(rng, 40000, 0.8, 4.0, 0.01).astype(np.float32)
+    adj0, off0, _ = ops.build_voronoi_adjacency(H.to_dev(pts0, gpu))
+    pts = (pts0 + rng.normal(0.0, 2e-3, size=pts0.shape)).astype(np.float32)  # the sites moved
+    g_adj, g_off = adj0, off0
+    if guess == "shuffled":
+        o64 = off0.to(torch.int64)
+        g_off = (o64[-1] - o64.flip(0)).to(torch.uint32).contiguous()  # other cells' list lengths and entries
+    elif guess == "junk":
+        g_adj = torch.full_like(adj0, 0xFFFFFFF0)
+        g_adj[::3] = torch.arange(0, g_adj[::3].numel(), device=gpu, dtype=torch.int64).to(torch.uint32)
+    pd = H.to_dev(pts, gpu)
+    cold = ops.build_voronoi_adjacency(pd)
+    warm = ops.build_voronoi_adjacency(pd, initial_guesses=g_adj, initial_guesses_offsets=g_off)
+    torch.cuda.synchronize()
+    assert torch.equal(warm[1], cold[1]) and torch.equal(warm[0], cold[0])
+    if guess == "previous":
+        _check(pts, gpu)
+
+
+def test_model_refresh_warm_start(gpu):
+    """VoroTracing.update_triangulation seeds the build with the current
+    adjacency; the refreshed CSR equals a cold build's."""
+    from vorotracing_amd.model import VoroTracing
+
+    s = H.small_random(3000, seed=21)
+    m = VoroTracing.from_scene(s, device=gpu)
+    with torch.no_grad():
+        m.primal_points.add_(torch.randn_like(m.primal_points) * 1e-3)
+    m.update_triangulation()
+    adj, off, _ = ops.build_voronoi_adjacency(m.primal_points)
+    torch.cuda.synchronize()
+    assert torch.equal(m.point_adjacency, adj) and torch.equal(m.point_adjacency_offsets, off)

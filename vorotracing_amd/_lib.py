@@ -49,6 +49,7 @@ SIGNATURES = {
                       U32, F32, F32, F32, P], C.c_int),
     "vt_voronoi_workspace_size": ([U32], C.c_size_t),
     "vt_voronoi_build": ([P, U32, P, P, P, P], C.c_int),
+    "vt_voronoi_build_warm": ([P, U32, P, P, P, P, P, P], C.c_int),
     "vt_voronoi_adjacency": ([U32, P, P, P, P], C.c_int),
     "vt_bvh_create": ([P], C.c_int),
     "vt_bvh_destroy": ([P], C.c_int),

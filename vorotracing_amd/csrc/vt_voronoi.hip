@@ -49,7 +49,10 @@ template <int P_, int T_, int E_> struct VorCap {
     static constexpr int E = E_; // directed edges of the region removed by one cut
 };
 using VorSmall = VorCap<96, 192, 96>;
-using VorLarge = VorCap<255, 510, 384>;
+// The large tier's edge table holds the edges of every vertex at once, so a
+// cut that removes most of a cell (a near site after many slivers of a dense
+// layer farther away) never overflows it.
+using VorLarge = VorCap<255, 510, 3 * 510>;
 // Neighbour lists: LIST_K entries per site; longer lists in slots of BIG_K.
 constexpr int LIST_K = 64;
 constexpr int BIG_K = VorLarge::P;
@@ -63,9 +66,21 @@ struct VorGrid {
 };
 
 enum { VOR_OK = 0, VOR_FULL = 1, VOR_DEGENERATE = 2 };
+// which table overflowed (bits of the fails[F_REASON] word)
+enum { FULL_PLANES = 1, FULL_EDGES = 2, FULL_VERTICES = 4, FULL_LISTS = 8 };
 
 // fails[] words: failures, the retry count, big-list slots, work counters
-enum { F_FULL = 0, F_DEGENERATE = 1, F_RETRY = 2, F_BIG = 3, F_NEXT0 = 4, F_NEXT1 = 5, F_WORDS = 8 };
+enum {
+    F_FULL = 0,
+    F_DEGENERATE = 1,
+    F_RETRY = 2,
+    F_BIG = 3,
+    F_NEXT0 = 4,
+    F_NEXT1 = 5,
+    F_FIRST_BAD = 6,
+    F_REASON = 7,
+    F_WORDS = 8
+};
 
 __device__ __forceinline__ double4 cross_d(double4 a, double4 b)
 {
@@ -214,6 +229,8 @@ __device__ __forceinline__ double wave_uniform(double x)
 // Wave-uniform scalars of the cell (every lane holds the same values).
 struct WaveState {
     int np, nt, nfar;
+    int full;                // FULL_* bits of a capacity failure
+    bool warm;               // guesses were cut in first (their sites come again)
     int gen;                 // effective cuts so far
     double R2, Rn2;          // squared radius of all vertices, of the near ones
     double bmin[3], bmax[3]; // bounding box of the near vertices (0 when none)
@@ -305,10 +322,22 @@ template <class Cap> __device__ void wcell_compact_planes(WaveCell<Cap> &c, Wave
 template <class Cap>
 __device__ int wcell_cut(WaveCell<Cap> &c, WaveState &s, double4 pl, uint32_t site, double far2, int lane)
 {
+    if (s.warm) {
+        // The band scan offers a guessed site again.  Its plane is already a
+        // face; a vertex on it may round to "outside", and cutting the same
+        // plane again would make a vertex of parallel planes.
+        bool dup = false;
+        for (int q = 6 + lane; q < s.np; q += 64)
+            dup = dup || c.nid[q] == site;
+        if (__ballot(dup))
+            return VOR_OK;
+    }
     if (s.np >= Cap::P) {
         wcell_compact_planes(c, s, lane);
-        if (s.np >= Cap::P)
+        if (s.np >= Cap::P) {
+            s.full |= FULL_PLANES;
             return VOR_FULL;
+        }
     }
     // classify; gather the edges of the removed vertices
     uint32_t outmask = 0; // bit b: vertex 64 b + lane is removed
@@ -323,8 +352,10 @@ __device__ int wcell_cut(WaveCell<Cap> &c, WaveState &s, double4 pl, uint32_t si
         }
         uint64_t m = __ballot(out);
         const int cnt = __popcll(m);
-        if (3 * (removed + cnt) > Cap::E)
+        if (3 * (removed + cnt) > Cap::E) {
+            s.full |= FULL_EDGES;
             return VOR_FULL;
+        }
         if (out) {
             const int e = 3 * (removed + (int)lane_rank(m));
             c.ed[e] = (uint16_t)(x.x | (x.y << 8));
@@ -390,8 +421,10 @@ __device__ int wcell_cut(WaveCell<Cap> &c, WaveState &s, double4 pl, uint32_t si
         }
         uint64_t m = __ballot(bnd);
         const int cnt = __popcll(m);
-        if (k + nb + cnt > Cap::T)
+        if (k + nb + cnt > Cap::T) {
+            s.full |= FULL_VERTICES;
             return VOR_FULL;
+        }
         if (bnd)
             c.T[k + nb + (int)lane_rank(m)] = make_uchar4((uint8_t)(ev & 0xff), (uint8_t)(ev >> 8), (uint8_t)q, 0);
         nb += cnt;
@@ -533,10 +566,65 @@ __device__ __forceinline__ bool wcell_hits(const WaveCell<Cap> &c, const WaveSta
 }
 
 // Voronoi cell of site i; its m neighbours go to c.out[0..m) (unordered).
+// Cuts of the candidates of `m` (bit l: lane l's plane, site j, offset d,
+// |d|^2 = d2), nearest first: the nearer planes make many farther ones miss.
+template <class Cap>
+__device__ __forceinline__ int cut_nearest_first(WaveCell<Cap> &c, WaveState &s, uint64_t m, uint32_t j, double ddx,
+                                                 double ddy, double ddz, double d2, double far2, int lane)
+{
+    int status = VOR_OK;
+    while (m && status == VOR_OK) {
+        int l = __ffsll((unsigned long long)m) - 1;
+        if (m & (m - 1)) {
+            const bool rem = (m >> lane) & 1u;
+            const double dmin = -wave_max_dpp(rem ? -d2 : -INFINITY);
+            l = __ffsll((unsigned long long)__ballot(rem && d2 == dmin)) - 1;
+        }
+        m &= ~(1ull << l);
+        const double4 pl = make_double4(__shfl(ddx, l), __shfl(ddy, l), __shfl(ddz, l), 0.5 * __shfl(d2, l));
+        status = wcell_cut(c, s, pl, (uint32_t)__shfl((int)j, l), far2, lane);
+    }
+    return status;
+}
+
+// Warm start: the cell is first cut by the guessed neighbours of site i
+// (gadj[gofs[i], gofs[i+1]), e.g. the adjacency before the sites moved),
+// nearest first.  Every bisector plane is a valid constraint of the cell, and the
+// band scan that follows still tests every site that could cut it, so the
+// result is the cell without guesses; with good guesses the scan meets a
+// cell that is already final (small R, few candidates that still cut).
+template <class Cap>
+__device__ int wave_guess_cuts(WaveCell<Cap> &c, WaveState &s, uint32_t i, const float *__restrict__ points,
+                               uint32_t n, const uint32_t *__restrict__ gofs, const uint32_t *__restrict__ gadj,
+                               double px, double py, double pz, double far2, int lane)
+{
+    const uint32_t gb = gofs[i], ge = gofs[i + 1];
+    int status = VOR_OK;
+    for (uint32_t kb = gb; kb < ge && status == VOR_OK; kb += 64) {
+        const uint32_t k = kb + (uint32_t)lane;
+        bool cand = false;
+        uint32_t j = 0;
+        double ddx = 0.0, ddy = 0.0, ddz = 0.0, d2 = 0.0;
+        if (k < ge) {
+            j = gadj[k];
+            if (j < n && j != i) {
+                ddx = (double)points[3 * j] - px;
+                ddy = (double)points[3 * j + 1] - py;
+                ddz = (double)points[3 * j + 2] - pz;
+                d2 = ddx * ddx + ddy * ddy + ddz * ddz;
+                cand = d2 > 0.0 && wcell_hits(c, s, c.far, s.nfar, ddx, ddy, ddz, d2);
+            }
+        }
+        status = cut_nearest_first(c, s, __ballot(cand), j, ddx, ddy, ddz, d2, far2, lane);
+    }
+    return status;
+}
+
 template <class Cap>
 __device__ int wave_voronoi_cell(WaveCell<Cap> &c, uint32_t i, const float *__restrict__ points, const VorGrid &g,
                                  const uint32_t *__restrict__ cell_start, const uint32_t *__restrict__ sorted,
-                                 int lane, int *m_out)
+                                 uint32_t n, const uint32_t *__restrict__ gofs, const uint32_t *__restrict__ gadj,
+                                 int lane, int *m_out, int *full_out)
 {
     const float pxf = points[3 * i], pyf = points[3 * i + 1], pzf = points[3 * i + 2];
     const double px = pxf, py = pyf, pz = pzf;
@@ -554,6 +642,8 @@ __device__ int wave_voronoi_cell(WaveCell<Cap> &c, uint32_t i, const float *__re
     s.np = 6;
     s.nt = 8;
     s.gen = 0;
+    s.full = 0;
+    s.warm = gofs != nullptr;
     __syncthreads();
     wcell_radii(c, s, g.far2, lane);
     const int cx = grid_coord(pxf, g.lo[0], g.h, g.g[0]);
@@ -576,6 +666,8 @@ __device__ int wave_voronoi_cell(WaveCell<Cap> &c, uint32_t i, const float *__re
         return b;
     };
     int status = VOR_OK;
+    if (gofs)
+        status = wave_guess_cuts(c, s, i, points, n, gofs, gadj, px, py, pz, g.far2, lane);
     double lo2 = 0.0;
     for (double rho = 0.125 * h; status == VOR_OK; rho *= 2.0) {
         const double hi2 = rho * rho;
@@ -583,7 +675,11 @@ __device__ int wave_voronoi_cell(WaveCell<Cap> &c, uint32_t i, const float *__re
         const int rr = min((int)ceil(hig), gmax);
         const int gx0 = max(cx - rr, 0), gx1 = min(cx + rr, (int)g.g[0] - 1);
         const int gy0 = max(cy - rr, 0), gy1 = min(cy + rr, (int)g.g[1] - 1);
-        for (int dz = -rr; dz <= rr && status == VOR_OK; ++dz) {
+        // rows nearest first (0, -1, +1, -2, +2, ...): their sites cut the
+        // cell early, so fewer planes of farther sites cut it only to be
+        // superseded (the cell does not depend on the order)
+        for (int zi = 0; zi <= 2 * rr && status == VOR_OK; ++zi) {
+            const int dz = (zi & 1) ? -((zi + 1) >> 1) : (zi >> 1);
             const int z = cz + dz;
             if (z < 0 || z >= (int)g.g[2])
                 continue;
@@ -601,7 +697,8 @@ __device__ int wave_voronoi_cell(WaveCell<Cap> &c, uint32_t i, const float *__re
             if (nsf == 0 && !slab.near_may_cut(s))
                 continue;
             int lgen = s.gen; // cut generation the lists belong to
-            for (int dy = -rr; dy <= rr && status == VOR_OK; ++dy) {
+            for (int yi = 0; yi <= 2 * rr && status == VOR_OK; ++yi) {
+                const int dy = (yi & 1) ? -((yi + 1) >> 1) : (yi >> 1);
                 const int y = cy + dy;
                 RowSpan sp;
                 if (y < 0 || y >= (int)g.g[1] || !band_row(dy, dz, log_, hig, rr, cx, (int)g.g[0], sp))
@@ -676,21 +773,8 @@ __device__ int wave_voronoi_cell(WaveCell<Cap> &c, uint32_t i, const float *__re
                                 cand = j != i && d2 >= lo2 && d2 < hi2 && d2 < 4.0 * s.R2 &&
                                        wcell_hits(c, s, c.rowfar, nrf, ddx, ddy, ddz, d2);
                             }
-                            // cut nearest first: the nearer planes make many
-                            // farther ones miss
-                            uint64_t m = __ballot(cand);
-                            while (m && status == VOR_OK) {
-                                int l = __ffsll((unsigned long long)m) - 1;
-                                if (m & (m - 1)) {
-                                    const bool rem = (m >> lane) & 1u;
-                                    const double dmin = -wave_max_dpp(rem ? -d2 : -INFINITY);
-                                    l = __ffsll((unsigned long long)__ballot(rem && d2 == dmin)) - 1;
-                                }
-                                m &= ~(1ull << l);
-                                const double4 pl = make_double4(__shfl(ddx, l), __shfl(ddy, l), __shfl(ddz, l),
-                                                                0.5 * __shfl(d2, l));
-                                status = wcell_cut(c, s, pl, (uint32_t)__shfl((int)j, l), g.far2, lane);
-                            }
+                            status = cut_nearest_first(c, s, __ballot(cand), j, ddx, ddy, ddz, d2, g.far2,
+                                                       lane);
                         }
                         __syncthreads(); // run_off / run_at are rewritten by the next piece
                     }
@@ -715,6 +799,7 @@ __device__ int wave_voronoi_cell(WaveCell<Cap> &c, uint32_t i, const float *__re
         __syncthreads();
     }
     *m_out = status == VOR_OK ? m : 0;
+    *full_out = s.full;
     return status;
 }
 
@@ -728,7 +813,8 @@ __global__ __launch_bounds__(VOR_BLOCK) __attribute__((amdgpu_waves_per_eu(LARGE
     const float *__restrict__ points, VorGrid g, const uint32_t *__restrict__ cell_start,
     const uint32_t *__restrict__ sorted, const uint32_t *__restrict__ cells, uint32_t ncells,
     uint32_t *__restrict__ lists, uint32_t *__restrict__ big_lists, uint32_t big_cap, uint32_t *__restrict__ big_slot,
-    uint32_t *__restrict__ counts, uint32_t *__restrict__ retry, uint32_t *fails)
+    uint32_t *__restrict__ counts, uint32_t *__restrict__ retry, uint32_t *fails, uint32_t n,
+    const uint32_t *__restrict__ gofs, const uint32_t *__restrict__ gadj)
 {
     __shared__ WaveCell<Cap> c;
     __shared__ uint32_t pick;
@@ -744,7 +830,15 @@ __global__ __launch_bounds__(VOR_BLOCK) __attribute__((amdgpu_waves_per_eu(LARGE
             break;
         const uint32_t i = cells[r];
         int m;
-        int status = wave_voronoi_cell<Cap>(c, i, points, g, cell_start, sorted, lane, &m);
+        // Guesses seed the first pass only, and only cells with at most 64 of
+        // them (one nearest-first group): a longer list cut group by group can
+        // hold more vertices on the way than the cold band order, and the
+        // retry with the large tables runs cold, so guesses never cause a
+        // capacity failure.
+        const bool warm = !LARGE && gofs && gofs[i + 1] - gofs[i] <= 64u;
+        int full = 0;
+        int status = wave_voronoi_cell<Cap>(c, i, points, g, cell_start, sorted, n, warm ? gofs : nullptr,
+                                            gadj, lane, &m, &full);
         uint32_t *dst = lists + (size_t)i * LIST_K;
         if (status == VOR_OK && m > LIST_K) {
             if (lane == 0)
@@ -758,6 +852,7 @@ __global__ __launch_bounds__(VOR_BLOCK) __attribute__((amdgpu_waves_per_eu(LARGE
                     big_slot[i] = slot;
             } else {
                 status = VOR_FULL;
+                full |= FULL_LISTS;
             }
         }
         if (status == VOR_OK) {
@@ -774,8 +869,11 @@ __global__ __launch_bounds__(VOR_BLOCK) __attribute__((amdgpu_waves_per_eu(LARGE
             if (lane == 0) {
                 if (!LARGE && status == VOR_FULL)
                     retry[atomicAdd(fails + F_RETRY, 1u)] = i; // at most n entries
-                else
+                else {
                     atomicAdd(fails + (status == VOR_FULL ? F_FULL : F_DEGENERATE), 1u);
+                    atomicMin(fails + F_FIRST_BAD, i);
+                    atomicOr(fails + F_REASON, (uint32_t)full);
+                }
             }
         }
         if (lane == 0)
@@ -893,8 +991,16 @@ extern "C" size_t vt_voronoi_workspace_size(uint32_t num_points)
 extern "C" int vt_voronoi_build(const float *points, uint32_t num_points, uint32_t *offsets,
                                 uint32_t *num_adjacency, void *workspace, vt_stream_t stream)
 {
+    return vt_voronoi_build_warm(points, num_points, nullptr, nullptr, offsets, num_adjacency, workspace, stream);
+}
+
+extern "C" int vt_voronoi_build_warm(const float *points, uint32_t num_points, const uint32_t *guess_offsets,
+                                     const uint32_t *guess_adjacency, uint32_t *offsets, uint32_t *num_adjacency,
+                                     void *workspace, vt_stream_t stream)
+{
     clear_error();
     VT_REQUIRE(points && offsets && num_adjacency && workspace, "null pointer argument");
+    VT_REQUIRE(!guess_offsets == !guess_adjacency, "guess offsets and adjacency are given together or not at all");
     VT_REQUIRE(num_points >= 2, "at least 2 sites are needed, got %u", num_points);
     VT_REQUIRE(num_points <= (1u << 26), "too many sites (%u)", num_points);
     hipStream_t s = as_stream(stream);
@@ -936,6 +1042,7 @@ extern "C" int vt_voronoi_build(const float *points, uint32_t num_points, uint32
     // bucket the sites by grid cell: counts -> starts; stable sort of (cell, site)
     fill_u32_kernel<<<(nc + 1 + 255) / 256, 256, 0, s>>>(w.cell_start, (size_t)nc + 1, 0u);
     fill_u32_kernel<<<1, 64, 0, s>>>(w.fails, F_WORDS, 0u);
+    fill_u32_kernel<<<1, 64, 0, s>>>(w.fails + F_FIRST_BAD, 1, VOR_NONE);
     fill_u32_kernel<<<(n + 255) / 256, 256, 0, s>>>(w.big_slot, n, VOR_NONE);
     voronoi_grid_keys_kernel<<<(n + 255) / 256, 256, 0, s>>>(points, n, g, w.keys, w.vals, w.cell_start);
     VT_LAUNCH_CHECK("voronoi_grid_keys_kernel");
@@ -955,7 +1062,8 @@ extern "C" int vt_voronoi_build(const float *points, uint32_t num_points, uint32
         return rc;
     const uint32_t bcap = big_cap_for(n);
     voronoi_cells_kernel<VorSmall, false><<<wave_blocks(n), VOR_BLOCK, 0, s>>>(
-        points, g, w.cell_start, w.vals, w.order, n, w.lists, w.big_lists, bcap, w.big_slot, w.counts, w.retry, w.fails);
+        points, g, w.cell_start, w.vals, w.order, n, w.lists, w.big_lists, bcap, w.big_slot, w.counts, w.retry, w.fails,
+        n, guess_offsets, guess_adjacency);
     VT_LAUNCH_CHECK("voronoi_cells_kernel (small)");
     uint32_t f[F_WORDS];
     VT_HIP_CHECK(hipMemcpyAsync(f, w.fails, sizeof(f), hipMemcpyDeviceToHost, s));
@@ -963,20 +1071,22 @@ extern "C" int vt_voronoi_build(const float *points, uint32_t num_points, uint32
     if (f[F_RETRY]) {
         voronoi_cells_kernel<VorLarge, true><<<wave_blocks(f[F_RETRY]), VOR_BLOCK, 0, s>>>(
             points, g, w.cell_start, w.vals, w.retry, f[F_RETRY], w.lists, w.big_lists, bcap, w.big_slot, w.counts,
-            w.retry, w.fails);
+            w.retry, w.fails, n, guess_offsets, guess_adjacency);
         VT_LAUNCH_CHECK("voronoi_cells_kernel (large)");
     }
     rc = exclusive_scan_u32(w.counts, offsets, n + 1, w.scan_ws, s);
     if (rc)
         return rc;
-    uint32_t tail[3];
+    uint32_t tail[1 + F_WORDS];
     VT_HIP_CHECK(hipMemcpyAsync(tail, offsets + n, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
-    VT_HIP_CHECK(hipMemcpyAsync(tail + 1, w.fails, 2 * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+    VT_HIP_CHECK(hipMemcpyAsync(tail + 1, w.fails, F_WORDS * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
     VT_HIP_CHECK(hipStreamSynchronize(s));
-    if (tail[1] || tail[2]) {
+    if (tail[1 + F_FULL] || tail[1 + F_DEGENERATE]) {
         set_error("Voronoi build failed for %u cells over capacity (%d planes, %d vertices, %u lists longer than %d) "
-                  "and %u degenerate cuts",
-                  tail[1], VorLarge::P, VorLarge::T, bcap, LIST_K, tail[2]);
+                  "and %u degenerate cuts; first failing site %u; full tables (1 planes, 2 edges, 4 vertices, "
+                  "8 lists): %u",
+                  tail[1 + F_FULL], VorLarge::P, VorLarge::T, bcap, LIST_K, tail[1 + F_DEGENERATE],
+                  tail[1 + F_FIRST_BAD], tail[1 + F_REASON]);
         return VT_ERR_INVALID;
     }
     *num_adjacency = tail[0];

@@ -119,13 +119,19 @@ class VoroTracing(nn.Module):
         self.bvh.build(self.primal_points)
 
     @torch.no_grad()
-    def update_triangulation(self):
+    def update_triangulation(self, warm_start: bool = True):
         """Rebuild the adjacency after the sites moved, on the GPU Voronoi
         builder (the reference calls Paragram here, vorotracing.py:310-321),
-        and the start-cell LBVH."""
+        and the start-cell LBVH.  With ``warm_start`` the current adjacency
+        (when it is over the same number of sites) seeds the build: same
+        result, found faster after small moves."""
         if not bool(torch.isfinite(self.primal_points).all()):
             raise RuntimeError("update_triangulation: the sites hold NaN or inf")
-        adjacency, offsets, _ = ops.build_voronoi_adjacency(self.primal_points.detach())
+        guess = {}
+        offs = getattr(self, "point_adjacency_offsets", None)
+        if warm_start and offs is not None and offs.numel() == self.num_sites + 1:
+            guess = dict(initial_guesses=self.point_adjacency, initial_guesses_offsets=offs)
+        adjacency, offsets, _ = ops.build_voronoi_adjacency(self.primal_points.detach(), **guess)
         self.set_adjacency(adjacency, offsets)
 
     @torch.no_grad()

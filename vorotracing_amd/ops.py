@@ -66,11 +66,13 @@ def trace_octmap_infer_q8(points, diffuse_q8, specular_q8, density, adjacency, o
 def build_voronoi_adjacency(points: torch.Tensor, *, debug: bool = False, initial_guesses=None,
                             initial_guesses_offsets=None, chunk_padding: int = 32):
     """cuda/__init__.py:16-46: uint32 CSR (adjacency padded by ``chunk_padding``
-    zeros, offsets) and a status tensor, built on the GPU by vt_voronoi_build
-    (the reference calls Paragram).  Each neighbour list is ascending; the
-    sets are the Delaunay neighbours of the sites.  ``initial_guesses`` are
-    accepted for signature compatibility and not needed."""
-    del debug, initial_guesses, initial_guesses_offsets
+    zeros, offsets) and a status tensor, built on the GPU by the Voronoi
+    builder (the reference calls Paragram).  Each neighbour list is
+    ascending; the sets are the Delaunay neighbours of the sites.
+    ``initial_guesses`` / ``initial_guesses_offsets`` (a CSR over the same
+    sites, e.g. the adjacency before the sites moved) warm-start the build;
+    the result is the same, found faster when the guesses are close."""
+    del debug
     import ctypes
 
     pts = points.detach().to(torch.float32).contiguous()
@@ -78,13 +80,27 @@ def build_voronoi_adjacency(points: torch.Tensor, *, debug: bool = False, initia
     if dev.type != "cuda":
         raise RuntimeError("build_voronoi_adjacency needs the sites on the GPU")
     n = pts.shape[0]
+    if (initial_guesses is None) != (initial_guesses_offsets is None):
+        raise ValueError("initial_guesses and initial_guesses_offsets are given together or not at all")
+    gofs = gadj = None
+    if initial_guesses is not None:
+        gofs = torch.as_tensor(initial_guesses_offsets, device=dev).reshape(-1)
+        gadj = torch.as_tensor(initial_guesses, device=dev).reshape(-1)
+        if gofs.numel() != n + 1:
+            raise ValueError(f"initial_guesses_offsets must have {n + 1} entries, got {gofs.numel()}")
+        gofs = gofs.to(torch.int64).to(torch.uint32).contiguous() if gofs.dtype != torch.uint32 else gofs.contiguous()
+        gadj = gadj.to(torch.int64).to(torch.uint32).contiguous() if gadj.dtype != torch.uint32 else gadj.contiguous()
+        last = int(gofs[-1].item())
+        if last > gadj.numel():
+            raise ValueError(f"initial_guesses has {gadj.numel()} entries, its offsets end at {last}")
     lib = _lib.load()
     ws = torch.empty(lib.vt_voronoi_workspace_size(n), dtype=torch.uint8, device=dev)
     offsets = torch.empty(n + 1, dtype=torch.uint32, device=dev)
     m = ctypes.c_uint32(0)
     stream = torch.cuda.current_stream(dev).cuda_stream
     with torch.cuda.device(dev):
-        _lib.call("vt_voronoi_build", pts.data_ptr(), n, offsets.data_ptr(), ctypes.addressof(m), ws.data_ptr(),
+        _lib.call("vt_voronoi_build_warm", pts.data_ptr(), n, None if gofs is None else gofs.data_ptr(),
+                  None if gadj is None else gadj.data_ptr(), offsets.data_ptr(), ctypes.addressof(m), ws.data_ptr(),
                   stream)
         adjacency = torch.zeros(m.value + chunk_padding, dtype=torch.uint32, device=dev)
         _lib.call("vt_voronoi_adjacency", n, offsets.data_ptr(), adjacency.data_ptr(), ws.data_ptr(), stream)
