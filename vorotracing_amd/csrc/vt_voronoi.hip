@@ -669,7 +669,17 @@ __device__ int wave_voronoi_cell(WaveCell<Cap> &c, uint32_t i, const float *__re
     if (gofs)
         status = wave_guess_cuts(c, s, i, points, n, gofs, gadj, px, py, pz, g.far2, lane);
     double lo2 = 0.0;
-    for (double rho = 0.125 * h; status == VOR_OK; rho *= 2.0) {
+    double rho0 = 0.125 * h;
+    if (gofs && status == VOR_OK) {
+        // The guesses usually leave the cell near its final shape: one shell
+        // of radius 2R (R = farthest vertex) then finishes the scan, where
+        // doubling from h/8 would visit the same rows several times.  Poor
+        // guesses (a large R) keep the doubling schedule.
+        const double r2 = 2.0 * sqrt(s.R2) * (1.0 + 1e-6);
+        if (r2 <= 4.0 * h)
+            rho0 = fmax(rho0, r2);
+    }
+    for (double rho = rho0; status == VOR_OK; rho *= 2.0) {
         const double hi2 = rho * rho;
         const double hig = rho / h + 1e-3, log_ = fmax(sqrt(lo2) / h - 1e-3, 0.0);
         const int rr = min((int)ceil(hig), gmax);
