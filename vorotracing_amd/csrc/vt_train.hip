@@ -5,6 +5,8 @@
 // Attribute maps are (num_points, 3*R*R), texel-major / channel-minor.  The
 // backward scatters 28 gradient values per integrated cell with global
 // atomics (f32: hardware global_atomic_add_f32; f16: 32-bit CAS).
+#include <type_traits>
+
 #include "vt_internal.h"
 #include "vt_walk.h"
 
@@ -89,14 +91,14 @@ constexpr int TRAIN_CHUNK = 8; // face records read together per exit-face step
 constexpr uint32_t TRAIN_XCD_CHUNK = 32; // blocks per XCD turn (xcd_interleaved_block)
 constexpr int AGG_MIN = 2;
 
-// LDS floats per wave: copies of (diffuse + specular maps of one cell,
-// density, point_error), then copies of one point gradient.  Members of a
-// combining group add into AGG_COPIES copies of the slice
-// (member rank mod AGG_COPIES): lanes of one cell often hit the same texels,
-// and LDS atomics to one address serialise.
+// LDS floats per wave: copies of one cell's slice (diffuse and specular
+// maps, density, point_error, point gradient).  Members of a combining group
+// add into AGG_COPIES copies of the slice (member rank mod AGG_COPIES): lanes
+// of one cell often hit the same texels, and LDS atomics to one address
+// serialise.
 constexpr int AGG_COPIES = 2;
-template <int RD, int RS> constexpr int agg_cell_floats() { return 3 * RD * RD + 3 * RS * RS + 2; }
-template <int RD, int RS> constexpr int agg_floats() { return AGG_COPIES * (agg_cell_floats<RD, RS>() + 3); }
+template <int RD, int RS> constexpr int agg_cell_floats() { return 3 * RD * RD + 3 * RS * RS + 2 + 3; }
+template <int RD, int RS> constexpr int agg_floats() { return AGG_COPIES * agg_cell_floats<RD, RS>(); }
 
 
 constexpr int AGG_ROUNDS = 32;
@@ -388,50 +390,69 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
     static constexpr int ND = 3 * RD * RD, NS = 3 * RS * RS;
     static constexpr int NC = agg_cell_floats<RD, RS>(); // floats of one copy of the cell slice
 
-    // points_grad[idx] += g, same-idx lanes combined
-    __device__ __forceinline__ void scatter_point(uint32_t idx, f3 g)
+    // The texture, density and point_error gradients of an integrated cell
+    // are held until the walk has integrated the next cell (or ends): the
+    // cell's point gradient is then complete, and both go out in one scatter
+    // keyed by the cell, so that one combining pass serves both.  Held: the
+    // four diffuse taps (texel indices < 256, 8 bits each; HELD_NO_COLOR when
+    // the cell was not shaded) with their weights, the logit gradient, dL/ds
+    // and the point_error term.
+    static constexpr uint32_t HELD_NO_COLOR = 0xffffffffu;
+    uint32_t held_taps;
+    float held_w[4], held_gl[3], held_ds, held_perr;
+
+    __device__ __forceinline__ void hold(bool has_color, const Bilinear &db, const float *gl, float dL_ds, float perr)
     {
-        bool pending = true, direct = false;
-        for (int round = 0; round < AGG_ROUNDS; ++round) {
-            AggRound r;
-            if (!agg_round(idx, pending, r))
-                break;
-            if (r.comb) {
-                float *pb = agg + AGG_COPIES * NC; // [copy][3]
-                if (r.mine) {
-                    float *q = pb + 3 * (lane_rank(__ballot(1)) % AGG_COPIES);
-                    atomicAdd(q + 0, g.x);
-                    atomicAdd(q + 1, g.y);
-                    atomicAdd(q + 2, g.z);
-                }
-                wave_lds_sync();
-                uint64_t act = __ballot(1);
-                uint32_t nact = __popcll(act);
-                for (uint32_t k = lane_rank(act); k < 3u; k += nact) {
-                    float x = 0.0f;
-#pragma unroll
-                    for (int c = 0; c < AGG_COPIES; ++c) {
-                        x += pb[3 * c + k];
-                        pb[3 * c + k] = 0.0f;
-                    }
-                    if (x != 0.0f)
-                        atomicAdd(points_grad + 3 * (size_t)r.lead + k, x);
-                }
-                wave_lds_sync();
-            } else if (r.mine) {
-                direct = true;
-            }
-            if (r.mine)
-                pending = false;
+        static_assert(RD * RD <= 256, "diffuse tap indices are packed in 8 bits");
+        held_taps = HELD_NO_COLOR;
+        if (has_color) { // db is set only for shaded cells
+            held_taps = (uint32_t)db.i00 | (uint32_t)db.i10 << 8 | (uint32_t)db.i01 << 16 | (uint32_t)db.i11 << 24;
+            held_w[0] = db.w00;
+            held_w[1] = db.w10;
+            held_w[2] = db.w01;
+            held_w[3] = db.w11;
         }
-        if (pending || direct)
-            add_vec(points_grad, idx, g);
+        held_gl[0] = gl[0];
+        held_gl[1] = gl[1];
+        held_gl[2] = gl[2];
+        held_ds = dL_ds;
+        held_perr = perr;
     }
 
-    // texture, density and point_error gradients of one integrated cell
-    __device__ __forceinline__ void scatter_cell(uint32_t cell, bool has_color, const Bilinear &db, const float *gl,
-                                                 float dL_ds, float perr)
+    // Global add of entry k of a cell's slice (k in [0, NC)).
+    __device__ __forceinline__ void slice_add(uint32_t cell, uint32_t k, float x)
     {
+        if (k == (uint32_t)(ND + NS + 1) && !point_error)
+            return; // no point_error output: its entry has no target
+        if constexpr (std::is_same<A, float>::value) {
+            // one atomic instruction for every target
+            float *q = k < (uint32_t)ND            ? diffuse_grad + (size_t)cell * ND + k
+                       : k < (uint32_t)(ND + NS)   ? specular_grad + (size_t)cell * NS + (k - ND)
+                       : k == (uint32_t)(ND + NS)  ? density_grad + cell
+                       : k == (uint32_t)(ND + NS + 1) ? point_error + cell
+                                                      : points_grad + 3 * (size_t)cell + (k - (ND + NS + 2));
+            atomicAdd(q, x);
+        } else {
+            if (k < (uint32_t)ND)
+                Attr<A>::add(diffuse_grad + (size_t)cell * ND, k, x);
+            else if (k < (uint32_t)(ND + NS))
+                Attr<A>::add(specular_grad + (size_t)cell * NS, k - ND, x);
+            else if (k == (uint32_t)(ND + NS))
+                atomicAdd(density_grad + cell, x);
+            else if (k == (uint32_t)(ND + NS + 1))
+                Attr<A>::add(point_error, cell, x);
+            else
+                atomicAdd(points_grad + 3 * (size_t)cell + (k - (ND + NS + 2)), x);
+        }
+    }
+
+    // Scatters the held gradients of `cell` and, when with_point, its point
+    // gradient pg; lanes of one cell combined first.
+    __device__ __forceinline__ void scatter(uint32_t cell, bool with_point, f3 pg)
+    {
+        const bool color = held_taps != HELD_NO_COLOR;
+        const int tap[4] = {(int)(held_taps & 0xffu), (int)((held_taps >> 8) & 0xffu), (int)((held_taps >> 16) & 0xffu),
+                            (int)(held_taps >> 24)};
         bool pending = true, direct = false;
         for (int round = 0; round < AGG_ROUNDS; ++round) {
             AggRound g;
@@ -439,47 +460,43 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
                 break;
             if (g.comb) {
                 if (g.mine) {
-                    float *agg = this->agg + NC * (lane_rank(__ballot(1)) % AGG_COPIES);
-                    if (has_color) {
+                    float *sl = agg + NC * (lane_rank(__ballot(1)) % AGG_COPIES);
+                    if (color) {
 #pragma unroll
                         for (int c = 0; c < 3; ++c) {
-                            atomicAdd(agg + db.i00 * 3 + c, db.w00 * gl[c]);
-                            atomicAdd(agg + db.i10 * 3 + c, db.w10 * gl[c]);
-                            atomicAdd(agg + db.i01 * 3 + c, db.w01 * gl[c]);
-                            atomicAdd(agg + db.i11 * 3 + c, db.w11 * gl[c]);
+#pragma unroll
+                            for (int t = 0; t < 4; ++t)
+                                atomicAdd(sl + tap[t] * 3 + c, held_w[t] * held_gl[c]);
                         }
 #pragma unroll
                         for (int c = 0; c < 3; ++c) {
-                            atomicAdd(agg + ND + spec.i00 * 3 + c, spec.w00 * gl[c]);
-                            atomicAdd(agg + ND + spec.i10 * 3 + c, spec.w10 * gl[c]);
-                            atomicAdd(agg + ND + spec.i01 * 3 + c, spec.w01 * gl[c]);
-                            atomicAdd(agg + ND + spec.i11 * 3 + c, spec.w11 * gl[c]);
+                            atomicAdd(sl + ND + spec.i00 * 3 + c, spec.w00 * held_gl[c]);
+                            atomicAdd(sl + ND + spec.i10 * 3 + c, spec.w10 * held_gl[c]);
+                            atomicAdd(sl + ND + spec.i01 * 3 + c, spec.w01 * held_gl[c]);
+                            atomicAdd(sl + ND + spec.i11 * 3 + c, spec.w11 * held_gl[c]);
                         }
                     }
-                    atomicAdd(agg + ND + NS, dL_ds);
+                    atomicAdd(sl + ND + NS, held_ds);
                     if (point_error)
-                        atomicAdd(agg + ND + NS + 1, perr);
+                        atomicAdd(sl + ND + NS + 1, held_perr);
+                    if (with_point) {
+                        atomicAdd(sl + ND + NS + 2, pg.x);
+                        atomicAdd(sl + ND + NS + 3, pg.y);
+                        atomicAdd(sl + ND + NS + 4, pg.z);
+                    }
                 }
                 wave_lds_sync();
                 uint64_t act = __ballot(1);
                 uint32_t nact = __popcll(act);
-                for (uint32_t k = lane_rank(act); k < (uint32_t)(ND + NS + 2); k += nact) {
+                for (uint32_t k = lane_rank(act); k < (uint32_t)NC; k += nact) {
                     float x = 0.0f;
 #pragma unroll
                     for (int c = 0; c < AGG_COPIES; ++c) {
                         x += agg[NC * c + k];
                         agg[NC * c + k] = 0.0f;
                     }
-                    if (x != 0.0f) {
-                        if (k < (uint32_t)ND)
-                            Attr<A>::add(diffuse_grad + (size_t)g.lead * ND, k, x);
-                        else if (k < (uint32_t)(ND + NS))
-                            Attr<A>::add(specular_grad + (size_t)g.lead * NS, k - ND, x);
-                        else if (k == (uint32_t)(ND + NS))
-                            atomicAdd(density_grad + g.lead, x);
-                        else
-                            Attr<A>::add(point_error, g.lead, x);
-                    }
+                    if (x != 0.0f)
+                        slice_add(g.lead, k, x);
                 }
                 wave_lds_sync();
             } else if (g.mine) {
@@ -489,28 +506,38 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
                 pending = false;
         }
         if (pending || direct) {
-            if (has_color) {
+            if (color) {
                 A *dg = diffuse_grad + (size_t)cell * ND;
                 A *sg = specular_grad + (size_t)cell * NS;
 #pragma unroll
                 for (int c = 0; c < 3; ++c) {
-                    Attr<A>::add(dg, db.i00 * 3 + c, db.w00 * gl[c]);
-                    Attr<A>::add(dg, db.i10 * 3 + c, db.w10 * gl[c]);
-                    Attr<A>::add(dg, db.i01 * 3 + c, db.w01 * gl[c]);
-                    Attr<A>::add(dg, db.i11 * 3 + c, db.w11 * gl[c]);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        Attr<A>::add(dg, tap[t] * 3 + c, held_w[t] * held_gl[c]);
                 }
 #pragma unroll
                 for (int c = 0; c < 3; ++c) {
-                    Attr<A>::add(sg, spec.i00 * 3 + c, spec.w00 * gl[c]);
-                    Attr<A>::add(sg, spec.i10 * 3 + c, spec.w10 * gl[c]);
-                    Attr<A>::add(sg, spec.i01 * 3 + c, spec.w01 * gl[c]);
-                    Attr<A>::add(sg, spec.i11 * 3 + c, spec.w11 * gl[c]);
+                    Attr<A>::add(sg, spec.i00 * 3 + c, spec.w00 * held_gl[c]);
+                    Attr<A>::add(sg, spec.i10 * 3 + c, spec.w10 * held_gl[c]);
+                    Attr<A>::add(sg, spec.i01 * 3 + c, spec.w01 * held_gl[c]);
+                    Attr<A>::add(sg, spec.i11 * 3 + c, spec.w11 * held_gl[c]);
                 }
             }
-            atomicAdd(density_grad + cell, dL_ds);
+            atomicAdd(density_grad + cell, held_ds);
             if (point_error)
-                Attr<A>::add(point_error, cell, perr);
+                Attr<A>::add(point_error, cell, held_perr);
+            if (with_point)
+                add_vec(points_grad, cell, pg);
         }
+    }
+
+    // After the walk: a walk that ended without the transmittance stop
+    // (no exit face, step cap) still owes its last cell's held gradients;
+    // that cell's point gradient is not scattered (its exit term never came).
+    __device__ __forceinline__ void finish()
+    {
+        if (prev_idx != NONE)
+            scatter(prev_idx, false, mk(0.0f, 0.0f, 0.0f));
     }
 
     float pdens; // density of the current cell, loaded by begin_cell
@@ -597,8 +624,9 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
         cur_grad = add(cur_grad, cg);
         next_grad = vfma(dL_dt1, dt1_dnext, next_grad);
 
+        // the previous cell's held gradients and its now complete point gradient
         if (prev_idx != NONE)
-            scatter_point(prev_idx, prev_grad);
+            scatter(prev_idx, true, prev_grad);
         prev_geom = p;
         prev_idx = cell;
         prev_grad = cur_grad;
@@ -613,10 +641,11 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
             gl[1] = (dL_drgb.y * rgb.y) * (1.0f - rgb.y);
             gl[2] = (dL_drgb.z * rgb.z) * (1.0f - rgb.z);
         }
-        scatter_cell(cell, has_color, db, gl, dL_ds, w * ray_error);
+        hold(has_color, db, gl, dL_ds, w * ray_error);
 
         if (T < thr) {
-            scatter_point(prev_idx, prev_grad);
+            scatter(cell, true, prev_grad);
+            prev_idx = NONE; // nothing held any more
             return false;
         }
         return true;
@@ -624,7 +653,7 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
 };
 
 template <typename A, int RD, int RS, bool STATS>
-__global__ __launch_bounds__(TRAIN_BLOCK) void bwd_kernel(BwdArgs a)
+__global__ __launch_bounds__(TRAIN_BLOCK) __attribute__((amdgpu_waves_per_eu(4))) void bwd_kernel(BwdArgs a)
 {
     constexpr int NAGG = agg_floats<RD, RS>();
     __shared__ float agg_lds[TRAIN_WAVES][NAGG];
@@ -689,6 +718,7 @@ __global__ __launch_bounds__(TRAIN_BLOCK) void bwd_kernel(BwdArgs a)
     StatsAcc<STATS> st;
     uint32_t n = walk<TRAIN_CHUNK>(it.o, it.d, a.points, a.adjacency, a.offsets, a.adj_diff, a.start_point[r], a.max_steps,
                          it, st);
+    it.finish();
     st.store(a.stats, r, n);
 }
 
@@ -779,6 +809,7 @@ extern "C" int vt_trace_fwd(int attr_dtype, const float *points, const void *dif
                "null ray or output pointer");
     VT_REQUIRE(!depth_quantiles || num_quantiles == 0 || (depth && depth_idx),
                "depth outputs required when depth_quantiles is given");
+    VT_REQUIRE(num_rays == 0 || num_points > 0, "rays need at least one site");
     hipStream_t s = as_stream(stream);
     int rc = prefetch(points, num_points, adjacency, adjacency_size, offsets, adj_diff_workspace, s);
     if (rc)
@@ -834,6 +865,7 @@ extern "C" int vt_trace_bwd(int attr_dtype, const float *points, const void *dif
     VT_REQUIRE(!depth_quantiles || num_quantiles == 0 || (depth_idx && depth_grad),
                "depth_idx and depth_grad required when depth_quantiles is given");
     VT_REQUIRE(!ray_error || point_error, "point_error output required when ray_error is given");
+    VT_REQUIRE(num_rays == 0 || num_points > 0, "rays need at least one site");
     hipStream_t s = as_stream(stream);
     int rc = prefetch(points, num_points, adjacency, adjacency_size, offsets, adj_diff_workspace, s);
     if (rc)
