@@ -33,7 +33,10 @@ enum {
 enum { VT_ATTR_F32 = 0, VT_ATTR_F16 = 1 };
 
 /* Per-ray walk statistics (debug / roofline accounting).  Filled only when a
- * non-NULL `stats` array (one record per ray, in ray order) is passed. */
+ * non-NULL `stats` array (one record per ray, in ray order) is passed.  The
+ * first VT_STATS_LOG visited cells locate the first step at which two walks
+ * part; the hash covers the whole walk.  128 bytes per ray. */
+#define VT_STATS_LOG 24
 typedef struct vt_ray_stats {
     uint32_t n;          /* value returned by the walk (trace_octmap) */
     uint32_t visits;     /* cells whose face list was searched */
@@ -42,6 +45,7 @@ typedef struct vt_ray_stats {
     uint32_t integrated; /* integrate_cell calls (t1 > t0) */
     uint32_t shaded;     /* cells whose textures were fetched */
     uint64_t visit_hash; /* FNV-1a 64 over the visited cell ids */
+    uint32_t first_cells[VT_STATS_LOG]; /* visited cells in walk order; 0xffffffff past the walk's end */
 } vt_ray_stats;
 
 /* Message of the calling thread's last failed call ("" if none). */

@@ -25,9 +25,10 @@ STATS_DTYPE = np.dtype(
         ("integrated", "<u4"),
         ("shaded", "<u4"),
         ("visit_hash", "<u8"),
+        ("first_cells", "<u4", (24,)),  # OR_STATS_LOG
     ]
 )
-assert STATS_DTYPE.itemsize == 32
+assert STATS_DTYPE.itemsize == 128
 
 
 def build(force: bool = False) -> str:

@@ -353,6 +353,8 @@ static inline void dbg_visit(walk_dbg_t *g, uint32_t cell)
 {
     if (g->log && g->st.visits < g->log_cap)
         g->log[g->st.visits] = cell;
+    if (g->st.visits < OR_STATS_LOG)
+        g->st.first_cells[g->st.visits] = cell;
     g->st.visits += 1;
     g->st.visit_hash = (g->st.visit_hash ^ (uint64_t)cell) * 1099511628211ull;
 }
@@ -458,6 +460,8 @@ static void init_dbg(walk_dbg_t *g, uint32_t *log, uint32_t cap)
 {
     memset(&g->st, 0, sizeof(g->st));
     g->st.visit_hash = 1469598103934665603ull;
+    for (int i = 0; i < OR_STATS_LOG; ++i)
+        g->st.first_cells[i] = OR_NONE;
     g->log = log;
     g->log_cap = cap;
     if (log)

@@ -28,7 +28,9 @@
 extern "C" {
 #endif
 
-/* Per-ray walk statistics; same layout as vt_ray_stats in include/vt_abi.h. */
+/* Per-ray walk statistics; same layout as vt_ray_stats in include/vt_abi.h
+ * (OR_STATS_LOG = VT_STATS_LOG). */
+#define OR_STATS_LOG 24
 typedef struct or_ray_stats {
     uint32_t n;          /* value returned by the walk */
     uint32_t visits;     /* cells whose face list was searched */
@@ -37,6 +39,7 @@ typedef struct or_ray_stats {
     uint32_t integrated; /* integrate_cell calls (t1 > t0) */
     uint32_t shaded;     /* cells whose textures were fetched */
     uint64_t visit_hash; /* FNV-1a 64 over the visited cell ids */
+    uint32_t first_cells[OR_STATS_LOG]; /* visited cells in walk order; 0xffffffff past the walk's end */
 } or_ray_stats;
 
 /* scalar helpers, exported so tests can pin them */

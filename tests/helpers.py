@@ -7,7 +7,7 @@ import numpy as np
 import torch
 
 from oracle import core, host_ops
-from vorotracing_amd import camera, scene
+from vorotracing_amd import camera, native, scene
 
 
 @functools.lru_cache(maxsize=None)
@@ -47,14 +47,15 @@ def f16_maps(s):
 
 
 def stats_np(t: torch.Tensor):
-    """(num_rays, 8) u32 device tensor -> numpy structured stats."""
-    a = t.cpu().numpy().view(np.uint32).reshape(-1, 8)
+    """(num_rays, native.STATS_WORDS) u32 device tensor -> numpy structured stats."""
+    a = t.cpu().numpy().view(np.uint32).reshape(-1, native.STATS_WORDS)
     return np.ascontiguousarray(a).view(core.STATS_DTYPE).reshape(-1)
 
 
 def assert_stats_equal(got, want):
-    for k in ("n", "visits", "faces", "exits", "integrated", "shaded", "visit_hash"):
-        bad = np.nonzero(got[k] != want[k])[0]
+    for k in ("n", "visits", "faces", "exits", "integrated", "shaded", "visit_hash", "first_cells"):
+        diff = got[k] != want[k]
+        bad = np.nonzero(diff.reshape(diff.shape[0], -1).any(axis=1))[0]
         assert bad.size == 0, f"stats field {k} differs on {bad.size} rays, first {bad[:5]}: " \
                               f"{got[k][bad[:5]]} vs {want[k][bad[:5]]}"
 

@@ -183,7 +183,7 @@ def test_c4_full_frames_q8(gpu):
     f16.render(rd, start_point=sp, weight_threshold=0.01, cell_skip_threshold=1e-3, stats=st16)
     torch.cuda.synchronize()
     a, b = H.stats_np(st16), H.stats_np(st)
-    for k in ("n", "visits", "faces", "visit_hash"):
+    for k in ("n", "visits", "faces", "visit_hash", "first_cells"):
         assert np.array_equal(a[k], b[k]), k
 
 

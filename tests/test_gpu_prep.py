@@ -186,7 +186,7 @@ def test_render_q8_batch_per_camera_start(gpu):
         one = inf.render(bd[i], weight_threshold=0.01, cell_skip_threshold=0.0)
         assert np.array_equal(one.cpu().numpy().view(np.uint16), out[i].cpu().numpy().view(np.uint16))
     a, b = H.stats_np(st), H.stats_np(st16)
-    for k in ("n", "visits", "visit_hash", "integrated"):
+    for k in ("n", "visits", "visit_hash", "integrated", "first_cells"):
         assert np.array_equal(a[k], b[k])
     # oracle on the first camera
     r0 = batch[0]

@@ -13,6 +13,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/vt_abi.h"
+
 namespace vt {
 
 constexpr uint32_t NONE = 0xffffffffu;
@@ -260,7 +262,11 @@ struct Stats {
     uint64_t hash;
 };
 
+constexpr uint32_t STATS_WORDS = sizeof(vt_ray_stats) / 4;
+static_assert(sizeof(vt_ray_stats) == 4 * (8 + VT_STATS_LOG), "vt_ray_stats is 8 counter words and the log");
+
 template <bool ON> struct StatsAcc {
+    __device__ __forceinline__ void begin(void *, uint32_t) {}
     __device__ __forceinline__ void visit(uint32_t, uint32_t) {}
     __device__ __forceinline__ void exit() {}
     __device__ __forceinline__ void integrate() {}
@@ -270,8 +276,17 @@ template <bool ON> struct StatsAcc {
 
 template <> struct StatsAcc<true> {
     Stats s{0, 0, 0, 0, 0, 0, 1469598103934665603ull};
+    uint32_t *log = nullptr; // first_cells of this ray's record
+    // the record of ray r (NONE: no record)
+    __device__ __forceinline__ void begin(void *out, uint32_t r)
+    {
+        if (out && r != NONE)
+            log = (uint32_t *)out + STATS_WORDS * (size_t)r + 8;
+    }
     __device__ __forceinline__ void visit(uint32_t cell, uint32_t nf)
     {
+        if (log && s.visits < VT_STATS_LOG)
+            log[s.visits] = cell;
         s.visits++;
         s.faces += nf;
         s.hash = (s.hash ^ (uint64_t)cell) * 1099511628211ull;
@@ -281,7 +296,9 @@ template <> struct StatsAcc<true> {
     __device__ __forceinline__ void shade() { s.shaded++; }
     __device__ __forceinline__ void store(void *out, uint32_t r, uint32_t n)
     {
-        uint32_t *o = (uint32_t *)out + 8 * (size_t)r;
+        uint32_t *o = (uint32_t *)out + STATS_WORDS * (size_t)r;
+        for (uint32_t k = s.visits; k < VT_STATS_LOG; ++k)
+            o[8 + k] = NONE;
         o[0] = n;
         o[1] = s.visits;
         o[2] = s.faces;

@@ -314,6 +314,7 @@ void infer_kernel(InferArgs a, uint32_t total_slots)
     integ.acc = mk(0.0f, 0.0f, 0.0f);
     integ.T = 1.0f;
     StatsAcc<STATS> st;
+    st.begin(a.stats, r);
     WalkState w;
     if (active) {
         uint32_t start;

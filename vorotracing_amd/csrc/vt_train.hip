@@ -294,6 +294,7 @@ __global__ __launch_bounds__(TRAIN_BLOCK) __attribute__((amdgpu_waves_per_eu(6))
     it.T = 1.0f;
     it.W = it.S = it.D = it.self = it.tfar = 0.0f;
     StatsAcc<STATS> st;
+    st.begin(a.stats, r);
     uint32_t n = walk<TRAIN_CHUNK>(it.o, it.d, a.points, a.adjacency, a.offsets, a.adj_diff, a.start_point[r], a.max_steps,
                          it, st);
     for (uint32_t i = it.qi; i < K; ++i) {
@@ -716,6 +717,7 @@ __global__ __launch_bounds__(TRAIN_BLOCK) __attribute__((amdgpu_waves_per_eu(4))
     it.dist_grad = a.distortion_grad ? a.distortion_grad[r] : 0.0f;
     it.D_total = (2.0f * fd) * it.dist_grad;
     StatsAcc<STATS> st;
+    st.begin(a.stats, r);
     uint32_t n = walk<TRAIN_CHUNK>(it.o, it.d, a.points, a.adjacency, a.offsets, a.adj_diff, a.start_point[r], a.max_steps,
                          it, st);
     it.finish();

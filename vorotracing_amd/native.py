@@ -13,7 +13,7 @@ import torch
 
 from . import _lib
 
-STATS_WORDS = 8  # vt_ray_stats = 8 u32 words
+STATS_WORDS = 32  # vt_ray_stats: 8 counter words and the first 24 visited cells
 
 
 def _p(t: Optional[torch.Tensor]):
