@@ -5,7 +5,9 @@ Workload ("C3"): 1,048,576-site height-field scene
 over 32 poses, weight threshold 0.01, cell-skip 1e-3, fp16 inference.  A
 step is one ``VoroTracingInfer.render`` of one pose (start-cell LBVH query +
 traversal kernel), as timed by the reference's benchmark_eval.py:137-158;
-``value`` = frames per second over ``--steps`` renders (rays resident in HBM).
+``value`` = frames per second over ``--steps`` whole renders (rays resident in
+HBM) with two frames in flight on side streams, every frame checked
+bit-identical to its serial render; the serial protocol is reported beside it.
 
 Also reported: the traversal kernel's duration from HIP events on its stream,
 its algorithmic bytes per frame (from the kernel's own per-ray walk counters)
@@ -38,7 +40,8 @@ def log(*a):
 
 
 def b_alg(st, tex_bytes=64, per_ray_extra=0):
-    """Algorithmic bytes of the inference walk from per-ray counters (u32 (R,8) tensor).
+    """Algorithmic bytes of the inference walk from per-ray walk statistics (u32 (R, 32): the counters, then
+    the visit log, which is not summed).
 
     per ray 24 (ray) + 4 (start) + 12 (start site) + 8 (rgba) ; per searched
     cell 8 (offsets pair) + 8 per face record ; per exit 4 (neighbour id) + 12
@@ -52,7 +55,7 @@ def b_alg(st, tex_bytes=64, per_ray_extra=0):
 
 
 def train_bytes(st, fwd=True, attr_bytes=4):
-    """Logical bytes of a training walk from its per-ray counters (u32 (R,8)):
+    """Logical bytes of a training walk from its per-ray walk statistics (u32 (R, 32)):
     the walk's bytes as in b_alg, textures 2 maps x 4 taps x 3 channels x attr
     bytes per shaded cell (96 f32).  Forward per ray: ray 24, start 4 + site
     12, rgba 16, n 4, distortion/W/S/t_far 16.  Backward per ray: ray 24,
@@ -291,6 +294,7 @@ def main():
         log(f"HBM {r['achieved']:.0f} GB/s ({r['frac']:.1%} of peak); logical bytes {bytes_per_frame / 1e9:.2f} "
             f"GB/frame; VALU issue {r.get('valu', {}).get('frac', float('nan')):.1%}")
         result["c4_q8"] = c4_q8(model, poses, dev, log, thr, skip, cpu=not args.no_cpu)
+        result["c3_camera"] = c3_camera(inf, W, H, args.poses, kw, dev, log)
 
     if not args.no_cpu and not args.profile:
         from oracle import core as oc
@@ -430,6 +434,40 @@ def stream_copy_gbs(dev):
     per = a.elapsed_time(b) / 8 * 1e-3
     del src, dst
     return 2 * (1 << 30) / per / 1e9
+
+
+def c3_camera(inf, W, H, n_poses, kw, dev, log, K=64):
+    """C3 rendered from camera records instead of a rays tensor: each lane
+    generates its pixel's ray inside the traversal kernel
+    (vt_trace_infer_f16_camera), so no 24 MB rays buffer is written or read per
+    frame.  The orbit's poses as pinhole cameras, one camera per launch, one
+    render after the other (start cell per camera from its centre).  Pose 0 is
+    checked bit for bit against render() of the same cameras' generated rays."""
+    import numpy as np
+    import torch
+
+    from vorotracing_amd import camera, native
+
+    cams = [camera.Camera.orbit(k, W, H, n=n_poses) for k in range(n_poses)]
+    bufs = [native.upload_cameras([c], dev) for c in cams]
+    starts = [inf.camera_start_points([c], b)[0] for c, b in zip(cams, bufs)]
+    ref = inf.render(native.camera_rays([cams[0]], dev), start_point=starts[0].reshape(1, 1, 1), **kw)
+    got = inf.render_cameras([cams[0]], start_point=starts[0], camera_buffer=bufs[0], **kw)
+    same = bool(torch.equal(ref.view(torch.int16), got.view(torch.int16)))
+    for k in range(min(K, 8)):
+        inf.render_cameras([cams[k % n_poses]], camera_buffer=bufs[k % n_poses], **kw)
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for k in range(K):
+        inf.render_cameras([cams[k % n_poses]], camera_buffer=bufs[k % n_poses], **kw)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t
+    log(f"C3 camera renders: {1000 * dt / K:.3f} ms/frame, {K / dt:.1f} FPS; pose 0 identical to the buffer "
+        f"render of its generated rays: {same}")
+    return {"fps": round(K / dt, 2), "ms_per_frame": round(1000 * dt / K, 4), "frames": K,
+            "identical_to_buffer_render": same,
+            "note": "serial renders from vt_camera records (whole renders: start-cell query + traversal), no rays "
+                    "buffer; compare serial.ms_per_frame"}
 
 
 def c4_q8(model, poses, dev, log, thr, skip, cpu=False):
