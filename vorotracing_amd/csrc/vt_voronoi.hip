@@ -319,10 +319,10 @@ template <class Cap> __device__ void wcell_compact_planes(WaveCell<Cap> &c, Wave
 
 // Cut by n.x <= w, spread over the wave.  Returns a wave-uniform status
 // (VOR_OK also when the plane misses the cell).
-template <class Cap>
+template <class Cap, bool WARM>
 __device__ int wcell_cut(WaveCell<Cap> &c, WaveState &s, double4 pl, uint32_t site, double far2, int lane)
 {
-    if (s.warm) {
+    if (WARM && s.warm) {
         // The band scan offers a guessed site again.  Its plane is already a
         // face; a vertex on it may round to "outside", and cutting the same
         // plane again would make a vertex of parallel planes.
@@ -568,7 +568,7 @@ __device__ __forceinline__ bool wcell_hits(const WaveCell<Cap> &c, const WaveSta
 // Voronoi cell of site i; its m neighbours go to c.out[0..m) (unordered).
 // Cuts of the candidates of `m` (bit l: lane l's plane, site j, offset d,
 // |d|^2 = d2), nearest first: the nearer planes make many farther ones miss.
-template <class Cap>
+template <class Cap, bool WARM>
 __device__ __forceinline__ int cut_nearest_first(WaveCell<Cap> &c, WaveState &s, uint64_t m, uint32_t j, double ddx,
                                                  double ddy, double ddz, double d2, double far2, int lane)
 {
@@ -582,7 +582,7 @@ __device__ __forceinline__ int cut_nearest_first(WaveCell<Cap> &c, WaveState &s,
         }
         m &= ~(1ull << l);
         const double4 pl = make_double4(__shfl(ddx, l), __shfl(ddy, l), __shfl(ddz, l), 0.5 * __shfl(d2, l));
-        status = wcell_cut(c, s, pl, (uint32_t)__shfl((int)j, l), far2, lane);
+        status = wcell_cut<Cap, WARM>(c, s, pl, (uint32_t)__shfl((int)j, l), far2, lane);
     }
     return status;
 }
@@ -615,12 +615,12 @@ __device__ int wave_guess_cuts(WaveCell<Cap> &c, WaveState &s, uint32_t i, const
                 cand = d2 > 0.0 && wcell_hits(c, s, c.far, s.nfar, ddx, ddy, ddz, d2);
             }
         }
-        status = cut_nearest_first(c, s, __ballot(cand), j, ddx, ddy, ddz, d2, far2, lane);
+        status = cut_nearest_first<Cap, true>(c, s, __ballot(cand), j, ddx, ddy, ddz, d2, far2, lane);
     }
     return status;
 }
 
-template <class Cap>
+template <class Cap, bool WARM>
 __device__ int wave_voronoi_cell(WaveCell<Cap> &c, uint32_t i, const float *__restrict__ points, const VorGrid &g,
                                  const uint32_t *__restrict__ cell_start, const uint32_t *__restrict__ sorted,
                                  uint32_t n, const uint32_t *__restrict__ gofs, const uint32_t *__restrict__ gadj,
@@ -666,11 +666,13 @@ __device__ int wave_voronoi_cell(WaveCell<Cap> &c, uint32_t i, const float *__re
         return b;
     };
     int status = VOR_OK;
-    if (gofs)
-        status = wave_guess_cuts(c, s, i, points, n, gofs, gadj, px, py, pz, g.far2, lane);
+    if constexpr (WARM) {
+        if (gofs)
+            status = wave_guess_cuts(c, s, i, points, n, gofs, gadj, px, py, pz, g.far2, lane);
+    }
     double lo2 = 0.0;
     double rho0 = 0.125 * h;
-    if (gofs && status == VOR_OK) {
+    if (WARM && gofs && status == VOR_OK) {
         // The guesses usually leave the cell near its final shape: one shell
         // of radius 2R (R = farthest vertex) then finishes the scan, where
         // doubling from h/8 would visit the same rows several times.  Poor
@@ -783,7 +785,7 @@ __device__ int wave_voronoi_cell(WaveCell<Cap> &c, uint32_t i, const float *__re
                                 cand = j != i && d2 >= lo2 && d2 < hi2 && d2 < 4.0 * s.R2 &&
                                        wcell_hits(c, s, c.rowfar, nrf, ddx, ddy, ddz, d2);
                             }
-                            status = cut_nearest_first(c, s, __ballot(cand), j, ddx, ddy, ddz, d2, g.far2,
+                            status = cut_nearest_first<Cap, WARM>(c, s, __ballot(cand), j, ddx, ddy, ddz, d2, g.far2,
                                                        lane);
                         }
                         __syncthreads(); // run_off / run_at are rewritten by the next piece
@@ -818,7 +820,7 @@ __device__ int wave_voronoi_cell(WaveCell<Cap> &c, uint32_t i, const float *__re
 // tables are queued in retry[].  Second pass (LARGE true): the queued cells.
 // A list longer than LIST_K goes to a slot of big_lists (big_slot[i]),
 // shorter lists to the cell's slot of lists.
-template <class Cap, bool LARGE>
+template <class Cap, bool LARGE, bool WARM>
 __global__ __launch_bounds__(VOR_BLOCK) __attribute__((amdgpu_waves_per_eu(LARGE ? 1 : 3))) void voronoi_cells_kernel(
     const float *__restrict__ points, VorGrid g, const uint32_t *__restrict__ cell_start,
     const uint32_t *__restrict__ sorted, const uint32_t *__restrict__ cells, uint32_t ncells,
@@ -845,10 +847,10 @@ __global__ __launch_bounds__(VOR_BLOCK) __attribute__((amdgpu_waves_per_eu(LARGE
         // hold more vertices on the way than the cold band order, and the
         // retry with the large tables runs cold, so guesses never cause a
         // capacity failure.
-        const bool warm = !LARGE && gofs && gofs[i + 1] - gofs[i] <= 64u;
+        const bool warm = WARM && !LARGE && gofs[i + 1] - gofs[i] <= 64u;
         int full = 0;
-        int status = wave_voronoi_cell<Cap>(c, i, points, g, cell_start, sorted, n, warm ? gofs : nullptr,
-                                            gadj, lane, &m, &full);
+        int status = wave_voronoi_cell<Cap, WARM>(c, i, points, g, cell_start, sorted, n, warm ? gofs : nullptr,
+                                                  gadj, lane, &m, &full);
         uint32_t *dst = lists + (size_t)i * LIST_K;
         if (status == VOR_OK && m > LIST_K) {
             if (lane == 0)
@@ -1071,17 +1073,24 @@ extern "C" int vt_voronoi_build_warm(const float *points, uint32_t num_points, c
     if (rc)
         return rc;
     const uint32_t bcap = big_cap_for(n);
-    voronoi_cells_kernel<VorSmall, false><<<wave_blocks(n), VOR_BLOCK, 0, s>>>(
-        points, g, w.cell_start, w.vals, w.order, n, w.lists, w.big_lists, bcap, w.big_slot, w.counts, w.retry, w.fails,
-        n, guess_offsets, guess_adjacency);
+    // cold builds run an instantiation without any of the warm-start code
+    if (guess_offsets)
+        voronoi_cells_kernel<VorSmall, false, true><<<wave_blocks(n), VOR_BLOCK, 0, s>>>(
+            points, g, w.cell_start, w.vals, w.order, n, w.lists, w.big_lists, bcap, w.big_slot, w.counts, w.retry,
+            w.fails, n, guess_offsets, guess_adjacency);
+    else
+        voronoi_cells_kernel<VorSmall, false, false><<<wave_blocks(n), VOR_BLOCK, 0, s>>>(
+            points, g, w.cell_start, w.vals, w.order, n, w.lists, w.big_lists, bcap, w.big_slot, w.counts, w.retry,
+            w.fails, n, nullptr, nullptr);
     VT_LAUNCH_CHECK("voronoi_cells_kernel (small)");
     uint32_t f[F_WORDS];
     VT_HIP_CHECK(hipMemcpyAsync(f, w.fails, sizeof(f), hipMemcpyDeviceToHost, s));
     VT_HIP_CHECK(hipStreamSynchronize(s));
     if (f[F_RETRY]) {
-        voronoi_cells_kernel<VorLarge, true><<<wave_blocks(f[F_RETRY]), VOR_BLOCK, 0, s>>>(
+        // the retry pass runs cold (guesses never cause a capacity failure)
+        voronoi_cells_kernel<VorLarge, true, false><<<wave_blocks(f[F_RETRY]), VOR_BLOCK, 0, s>>>(
             points, g, w.cell_start, w.vals, w.retry, f[F_RETRY], w.lists, w.big_lists, bcap, w.big_slot, w.counts,
-            w.retry, w.fails, n, guess_offsets, guess_adjacency);
+            w.retry, w.fails, n, nullptr, nullptr);
         VT_LAUNCH_CHECK("voronoi_cells_kernel (large)");
     }
     rc = exclusive_scan_u32(w.counts, offsets, n + 1, w.scan_ws, s);
