@@ -761,6 +761,39 @@ def train_step_c2(sc, dev, rays, sp, g, log, K=10):
     return res
 
 
+def adjacency_refresh(model, dev, log, sigma=1e-4, reps=3):
+    """The trainer's adjacency refresh (trainer.py:354-360) at the model's scale: the sites moved by
+    N(0, sigma), then the Voronoi CSR rebuilt warm-started from the current adjacency (what
+    VoroTracing.update_triangulation does) and cold, median of ``reps`` each; the two CSRs must be equal."""
+    import numpy as np
+    import torch
+
+    from vorotracing_amd import ops
+
+    g = torch.Generator(device=dev).manual_seed(7)
+    moved = (model.primal_points.detach() + sigma * torch.randn(model.primal_points.shape, generator=g,
+                                                                device=dev)).contiguous()
+    guess = dict(initial_guesses=model.point_adjacency, initial_guesses_offsets=model.point_adjacency_offsets)
+
+    def timed(**kw):
+        ts, res = [], None
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            res = ops.build_voronoi_adjacency(moved, **kw)
+            torch.cuda.synchronize()
+            ts.append(1000 * (time.perf_counter() - t))
+        return float(np.median(ts)), res
+
+    cold_ms, cold = timed()
+    warm_ms, warm = timed(**guess)
+    same = bool(torch.equal(cold[0], warm[0]) and torch.equal(cold[1], warm[1]))
+    log(f"adjacency refresh after N(0, {sigma}) moves: warm {warm_ms:.1f} ms, cold {cold_ms:.1f} ms, CSR equal: {same}")
+    return {"warm_ms": round(warm_ms, 1), "cold_ms": round(cold_ms, 1), "csr_identical": same, "sigma": sigma,
+            "note": "VoroTracing.update_triangulation's warm start (initial_guesses = the adjacency before the move) "
+                    "against a cold build of the same moved sites; median of 3"}
+
+
 def train_c5(dev, log, cpu=False, K=5):
     """Config-5 training step: 3,145,728 sites of the height-field distribution,
     one 1558x1039 equidistant-fisheye camera (k1 -0.1, k2 0.01) with a rolling shutter (origin moving 0.05
@@ -828,6 +861,7 @@ def train_c5(dev, log, cpu=False, K=5):
                        "start cells per distinct origin, dL/dRGB ~ N(0,1), thr 0.001"}
     log(f"C5 step {ms:.2f} ms (start lookup {out['start_lookup_ms']} ms, forward {out['forward_ms']} ms, "
         f"backward {out['backward_ms']} ms)")
+    out["adjacency_refresh"] = adjacency_refresh(model, dev, log)
     if cpu:
         out["cpu_baseline"] = train_cpu_step(model, rays, holder["sp"], g, log, "C5",
                                              "one whole C5 step (1,618,762 rays)")
