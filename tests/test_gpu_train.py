@@ -13,7 +13,7 @@ import torch
 
 from oracle import core
 from tests import helpers as H
-from vorotracing_amd import _C, camera, ops
+from vorotracing_amd import _C, camera, native, ops
 from vorotracing_amd.model import VoroTracing
 
 pytestmark = pytest.mark.gpu
@@ -57,11 +57,14 @@ def test_fwd_parity(gpu, which, f16):
     adt = np.float16 if f16 else np.float32
     want = core.trace_fwd(s.points, s.diffuse.astype(adt), s.specular.astype(adt), s.diff_res, s.spec_res,
                           s.density, s.adjacency, s.offsets, rays, start, depth_quantiles=q, weight_threshold=thr,
-                          return_contribution=True)
+                          return_contribution=True, want_stats=True)
     pts, dif, spe, den, adj, off = _scene_tensors(s, gpu, f16)
+    st = native.new_stats(rays.size // 6, gpu)
     rgba, depth, depth_idx, contrib, n, dist, W, S, tf = _C.trace_vorotracing_fwd(
-        pts, dif, spe, den, adj, off, H.to_dev(rays, gpu), H.to_dev(start, gpu), H.to_dev(q, gpu), thr, 1024, True)
+        pts, dif, spe, den, adj, off, H.to_dev(rays, gpu), H.to_dev(start, gpu), H.to_dev(q, gpu), thr, 1024, True,
+        stats=st)
     torch.cuda.synchronize()
+    H.assert_stats_equal(H.stats_np(st), want["stats"])  # the walk record through the _C entry
     assert rgba.dtype == (torch.float16 if f16 else torch.float32)
     assert np.array_equal(n.cpu().numpy(), want["n"])
     assert np.array_equal(rgba.cpu().numpy(), want["rgba"])
@@ -94,13 +97,16 @@ def test_bwd_parity(gpu, which, f16, extras):
                           s.adjacency, s.offsets, rays, start, fw["rgba"], g, depth_quantiles=q,
                           depth_idx=fw["depth_idx"], depth_grad=dg, ray_error=rerr, contribution_alpha_grad=cag,
                           distortion=fw["distortion"], distortion_grad=distg, W_total=fw["W_total"],
-                          S_total=fw["S_total"], t_far=fw["t_far"], weight_threshold=thr)
+                          S_total=fw["S_total"], t_far=fw["t_far"], weight_threshold=thr, want_stats=True)
     pts, dif, spe, den, adj, off = _scene_tensors(s, gpu, f16)
     d = lambda a, dt=None: None if a is None else H.to_dev(a, gpu)  # noqa: E731
+    st = native.new_stats(rays.size // 6, gpu)
     pg, dgd, sgd, deng, rayg, perr = _C.trace_vorotracing_bwd(
         pts, dif, spe, den, adj, off, d(rays), d(start), d(fw["rgba"]), d(g), d(q), d(fw["depth_idx"]), d(dg),
-        d(rerr), cag, d(fw["distortion"]), d(distg), d(fw["W_total"]), d(fw["S_total"]), d(fw["t_far"]), thr, 1024)
+        d(rerr), cag, d(fw["distortion"]), d(distg), d(fw["W_total"]), d(fw["S_total"]), d(fw["t_far"]), thr, 1024,
+        stats=st)
     torch.cuda.synchronize()
+    H.assert_stats_equal(H.stats_np(st), want["stats"])
     assert not rayg.cpu().numpy().any()
     if not f16:
         H.assert_grad_close(pg.cpu().numpy(), want["points_grad"], "points_grad")

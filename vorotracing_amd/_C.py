@@ -15,7 +15,7 @@ from typing import Optional, Sequence, Union
 
 import torch
 
-from . import _lib
+from . import _lib, native
 
 _C10_NAMES = {
     torch.float32: "Float", torch.float64: "Double", torch.float16: "Half", torch.bfloat16: "BFloat16",
@@ -247,8 +247,9 @@ def trace_vorotracing_fwd(points_in, diffuse_in, specular_in, density_in, point_
                           stats: Optional[torch.Tensor] = None):
     """tracing_octmap.cu:346-546.  Returns (rgba, depth, depth_idx,
     contribution, n, distortion, W_total, S_total, t_far); absent outputs are
-    None.  ``stats`` (an extension): None, or a u32 (num_rays, 8) tensor that
-    receives the per-ray walk counters (vt_ray_stats)."""
+    None.  ``stats`` (an extension): None, or a u32 (num_rays,
+    native.STATS_WORDS) tensor that receives the per-ray walk statistics
+    (vt_ray_stats)."""
     points = points_in.contiguous()
     diffuse = diffuse_in.contiguous()
     specular = specular_in.contiguous()
@@ -302,8 +303,9 @@ def trace_vorotracing_fwd(points_in, diffuse_in, specular_in, density_in, point_
 def _stats_ptr(stats: Optional[torch.Tensor], num_rays: int):
     if stats is None:
         return None
-    _assert(stats.is_contiguous() and stats.numel() * stats.element_size() == 32 * num_rays and _is_gpu(stats),
-            "stats must be a contiguous device tensor of num_rays 32-byte records")
+    rec = 4 * native.STATS_WORDS  # sizeof(vt_ray_stats)
+    _assert(stats.is_contiguous() and stats.numel() * stats.element_size() == rec * num_rays and _is_gpu(stats),
+            f"stats must be a contiguous device tensor of num_rays {rec}-byte records")
     return stats.data_ptr()
 
 

@@ -448,65 +448,68 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
     }
 
     // Scatters the held gradients of `cell` and, when with_point, its point
-    // gradient pg; lanes of one cell combined first.
+    // gradient pg; lanes of one cell combined first.  The pending lanes and
+    // each group are wave-uniform masks (scalar registers), so the leader loop
+    // is scalar work and a group's members are picked by their mask bit.
     __device__ __forceinline__ void scatter(uint32_t cell, bool with_point, f3 pg)
     {
         const bool color = held_taps != HELD_NO_COLOR;
         const int tap[4] = {(int)(held_taps & 0xffu), (int)((held_taps >> 8) & 0xffu), (int)((held_taps >> 16) & 0xffu),
                             (int)(held_taps >> 24)};
-        bool pending = true, direct = false;
-        for (int round = 0; round < AGG_ROUNDS; ++round) {
-            AggRound g;
-            if (!agg_round(cell, pending, g))
-                break;
-            if (g.comb) {
-                if (g.mine) {
-                    float *sl = agg + NC * (lane_rank(__ballot(1)) % AGG_COPIES);
-                    if (color) {
-#pragma unroll
-                        for (int c = 0; c < 3; ++c) {
-#pragma unroll
-                            for (int t = 0; t < 4; ++t)
-                                atomicAdd(sl + tap[t] * 3 + c, held_w[t] * held_gl[c]);
-                        }
-#pragma unroll
-                        for (int c = 0; c < 3; ++c) {
-                            atomicAdd(sl + ND + spec.i00 * 3 + c, spec.w00 * held_gl[c]);
-                            atomicAdd(sl + ND + spec.i10 * 3 + c, spec.w10 * held_gl[c]);
-                            atomicAdd(sl + ND + spec.i01 * 3 + c, spec.w01 * held_gl[c]);
-                            atomicAdd(sl + ND + spec.i11 * 3 + c, spec.w11 * held_gl[c]);
-                        }
-                    }
-                    atomicAdd(sl + ND + NS, held_ds);
-                    if (point_error)
-                        atomicAdd(sl + ND + NS + 1, held_perr);
-                    if (with_point) {
-                        atomicAdd(sl + ND + NS + 2, pg.x);
-                        atomicAdd(sl + ND + NS + 3, pg.y);
-                        atomicAdd(sl + ND + NS + 4, pg.z);
-                    }
-                }
-                wave_lds_sync();
-                uint64_t act = __ballot(1);
-                uint32_t nact = __popcll(act);
-                for (uint32_t k = lane_rank(act); k < (uint32_t)NC; k += nact) {
-                    float x = 0.0f;
-#pragma unroll
-                    for (int c = 0; c < AGG_COPIES; ++c) {
-                        x += agg[NC * c + k];
-                        agg[NC * c + k] = 0.0f;
-                    }
-                    if (x != 0.0f)
-                        slice_add(g.lead, k, x);
-                }
-                wave_lds_sync();
-            } else if (g.mine) {
-                direct = true;
+        const uint32_t lane = threadIdx.x & 63u;
+        // the scattering lanes and the groups as wave-uniform masks
+        const uint64_t act = __ballot(1);
+        const uint32_t nact = (uint32_t)__popcll(act), arank = lane_rank(act);
+        uint64_t pend = act, direct = 0;
+        for (int round = 0; round < AGG_ROUNDS && pend; ++round) {
+            const uint32_t lead = __builtin_amdgcn_readlane(cell, (int)__builtin_ctzll(pend));
+            const uint64_t mem = __ballot(cell == lead) & pend;
+            pend &= ~mem;
+            if (__popcll(mem) < AGG_MIN) {
+                direct |= mem;
+                continue;
             }
-            if (g.mine)
-                pending = false;
+            if ((mem >> lane) & 1u) {
+                float *sl = agg + NC * (lane_rank(mem) % AGG_COPIES);
+                if (color) {
+#pragma unroll
+                    for (int c = 0; c < 3; ++c) {
+#pragma unroll
+                        for (int t = 0; t < 4; ++t)
+                            atomicAdd(sl + tap[t] * 3 + c, held_w[t] * held_gl[c]);
+                    }
+#pragma unroll
+                    for (int c = 0; c < 3; ++c) {
+                        atomicAdd(sl + ND + spec.i00 * 3 + c, spec.w00 * held_gl[c]);
+                        atomicAdd(sl + ND + spec.i10 * 3 + c, spec.w10 * held_gl[c]);
+                        atomicAdd(sl + ND + spec.i01 * 3 + c, spec.w01 * held_gl[c]);
+                        atomicAdd(sl + ND + spec.i11 * 3 + c, spec.w11 * held_gl[c]);
+                    }
+                }
+                atomicAdd(sl + ND + NS, held_ds);
+                if (point_error)
+                    atomicAdd(sl + ND + NS + 1, held_perr);
+                if (with_point) {
+                    atomicAdd(sl + ND + NS + 2, pg.x);
+                    atomicAdd(sl + ND + NS + 3, pg.y);
+                    atomicAdd(sl + ND + NS + 4, pg.z);
+                }
+            }
+            wave_lds_sync();
+            for (uint32_t k = arank; k < (uint32_t)NC; k += nact) {
+                float x = 0.0f;
+#pragma unroll
+                for (int c = 0; c < AGG_COPIES; ++c) {
+                    x += agg[NC * c + k];
+                    agg[NC * c + k] = 0.0f;
+                }
+                if (x != 0.0f)
+                    slice_add(lead, k, x);
+            }
+            wave_lds_sync();
         }
-        if (pending || direct) {
+        direct |= pend; // groups beyond AGG_ROUNDS
+        if ((direct >> lane) & 1u) {
             if (color) {
                 A *dg = diffuse_grad + (size_t)cell * ND;
                 A *sg = specular_grad + (size_t)cell * NS;
