@@ -219,6 +219,11 @@ __device__ __forceinline__ float bil_mix(const Bilinear &b, float a, float bb, f
 }
 
 // direction of the diffuse probe: normalize(o + t0 d - site), or d
+// sqrtf(x) > 1e-8f exactly when x > PROBE_LEN2_MIN (sqrt is correctly rounded
+// and monotone; the constant is the largest float whose root rounds to at
+// most 1e-8f), so probe_dir's length test needs no square root.
+constexpr float PROBE_LEN2_MIN = 0x1.cd2b2ap-54f;
+
 __device__ __forceinline__ f3 probe_dir(f3 o, f3 d, float t0, f3 site)
 {
     f3 hit = mk(fma_(t0, d.x, o.x), fma_(t0, d.y, o.y), fma_(t0, d.z, o.z));

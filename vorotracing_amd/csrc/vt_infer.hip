@@ -83,10 +83,6 @@ constexpr int INFER_CHUNK = 8;
 // (xcd_block) one XCD got the costliest screen region and finished last.
 constexpr uint32_t INFER_XCD_CHUNK = 32;
 
-// sqrtf(x) > 1e-8f exactly when x > PROBE_LEN2_MIN (sqrt is correctly rounded
-// and monotone; the constant is the largest float whose root rounds to at
-// most 1e-8f), so probe_dir's length test needs no square root.
-constexpr float PROBE_LEN2_MIN = 0x1.cd2b2ap-54f;
 
 // The pending shades of one wave: a ring of SQ_RING entries.  Lanes append
 // from inside the integrator (at most 64 per walk step); the wave shades
