@@ -211,3 +211,19 @@ def test_train_errors_reference_messages(gpu):
         qd = torch.full(rays.shape[:-1] + (1,), 0.5, device=gpu)
         _C.trace_vorotracing_bwd(pts, dif, spe, den, adj, off, r, sp, out[0], out[0], qd, out[2], None, None, 0.0,
                                  out[5], None, out[6], out[7], out[8], thr, 1024)
+
+
+def test_start_cells_any_ray_order(gpu):
+    """VoroTracing.get_starting_point queries one origin per run of equal
+    consecutive origins; rays of three cameras shuffled together (short runs,
+    origins repeated out of order) still get each origin's nearest site."""
+    s = H.small_random(3000, seed=13)
+    model = VoroTracing.from_scene(s, device=gpu)
+    eyes = ((0.0, -3.0, 0.5), (2.5, 1.0, -0.4), (0.3, 0.2, 0.1))
+    rays = np.concatenate([camera.pinhole_rays(20, 12, eye=e).reshape(-1, 6) for e in eyes])
+    rays = rays[np.random.default_rng(3).permutation(rays.shape[0])]
+    got = model.get_starting_point(H.to_dev(rays, gpu)).cpu().numpy()
+    assert np.array_equal(got, H.start_for(s, rays))
+    # an image in order: one run per image
+    img = camera.pinhole_rays(20, 12, eye=eyes[1])
+    assert np.array_equal(model.get_starting_point(H.to_dev(img, gpu)).cpu().numpy(), H.start_for(s, img))

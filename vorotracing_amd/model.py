@@ -136,12 +136,20 @@ class VoroTracing(nn.Module):
 
     @torch.no_grad()
     def get_starting_point(self, rays: torch.Tensor) -> torch.Tensor:
-        """u32 start cell of every ray: the nearest site of its origin, one LBVH
-        query per distinct origin (vorotracing.py:323-344)."""
+        """u32 start cell of every ray: the nearest site of its origin
+        (vorotracing.py:323-344), one LBVH query per run of equal consecutive
+        origins.  Rays of an image share one origin, or one per row under a
+        rolling shutter, so the runs are the distinct origins without sorting
+        them; any order of rays gives the same cells."""
         lead = rays.shape[:-1]
-        origins, which = torch.unique(rays[..., :3].reshape(-1, 3), dim=0, return_inverse=True)
-        nearest = self.bvh.query(self.primal_points, origins)
-        return nearest[which].reshape(lead).view(torch.uint32)
+        o = rays[..., :3].reshape(-1, 3)
+        if o.shape[0] == 0:
+            return torch.empty(lead, dtype=torch.uint32, device=rays.device)
+        new = torch.ones(o.shape[0], dtype=torch.bool, device=o.device)
+        new[1:] = (o[1:] != o[:-1]).any(dim=1)
+        run = torch.cumsum(new, 0) - 1
+        nearest = self.bvh.query(self.primal_points, o[new].contiguous())
+        return nearest[run].reshape(lead).view(torch.uint32)
 
     def start_cells(self, rays: torch.Tensor, start_point: Optional[torch.Tensor] = None) -> torch.Tensor:
         """``start_point`` broadcast over the ray batch, or the nearest sites."""
