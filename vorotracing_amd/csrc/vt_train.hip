@@ -75,33 +75,32 @@ template <typename A, int RD, int RS> struct TrainTex {
 };
 
 // ---------------------------------------------------------------------------
-// Same-cell combining of gradient scatters.  Rays of one wave often integrate
-// the same cell in the same step (all rays of a camera share the start cell
-// and its neighbours), and hardware atomics to one address serialise.  A
-// scatter therefore groups the active lanes by cell, leader by leader (the
-// lowest pending lane); a group of at least AGG_MIN lanes adds its values
-// into the wave's LDS slice (ds_add_f32) and the active lanes then flush the
-// slice with one global atomic per touched entry, zeroing it again.  Other
-// lanes scatter directly.  Only the order of the floating-point additions
-// changes (atomics have no defined order anyway).
+// Same-cell combining of scatters.  Rays of one wave often integrate the same
+// cell in the same step (all rays of a camera share the start cell and its
+// neighbours), and hardware atomics to one address serialise.  A scatter
+// therefore groups the active lanes by cell, leader by leader (the lowest
+// pending lane).  The forward's contribution adds a group of at least AGG_MIN
+// lanes in one LDS word and sends it with one atomic; the backward's records
+// go through a per-wave LDS row table (BwdIntegrator::scatter).  Only the
+// order of the floating-point additions changes (atomics have no defined
+// order anyway).
 
 constexpr int TRAIN_BLOCK = 64; // one wave per block: each wave's LDS is freed when it ends
 constexpr int TRAIN_WAVES = TRAIN_BLOCK / 64;
 constexpr int TRAIN_CHUNK = 8; // face records read together per exit-face step
 constexpr uint32_t TRAIN_XCD_CHUNK = 32; // blocks per XCD turn (xcd_interleaved_block)
-constexpr int AGG_MIN = 2;
+constexpr int AGG_MIN = 2;     // forward contribution: smallest group combined
+constexpr int AGG_ROUNDS = 32; // forward contribution: groups combined per scatter
 
-// LDS floats per wave: copies of one cell's slice (diffuse and specular
-// maps, density, point_error, point gradient).  Members of a combining group
-// add into AGG_COPIES copies of the slice (member rank mod AGG_COPIES): lanes
-// of one cell often hit the same texels, and LDS atomics to one address
-// serialise.
-constexpr int AGG_COPIES = 2;
-template <int RD, int RS> constexpr int agg_cell_floats() { return 3 * RD * RD + 3 * RS * RS + 2 + 3; }
-template <int RD, int RS> constexpr int agg_floats() { return AGG_COPIES * agg_cell_floats<RD, RS>(); }
-
-
-constexpr int AGG_ROUNDS = 32;
+// The backward's scatter record of one lane: 12 diffuse and 12 specular
+// values (tap-major, 3 channels each), dL/ds, the point_error term and the
+// point gradient.  Each scattering lane writes its record as one row of the
+// wave's LDS table; ROW_STRIDE keeps rows 16-byte aligned and puts 8
+// consecutive lanes' 16-byte stores on distinct banks.  Row 64 stays zero
+// and is read in place of absent group members.
+constexpr int REC_COLS = 29;
+constexpr int ROW_STRIDE = 36;
+constexpr int ROW_TABLE_FLOATS = 65 * ROW_STRIDE;
 
 // One combining round over the lanes still pending: the key of the lowest
 // pending lane leads; `mine` marks its group and `comb` (wave-uniform) says
@@ -357,14 +356,6 @@ __device__ __forceinline__ f3 cell_intersection_grad(f3 prim, f3 opp, f3 o, f3 d
     return divs(g, dp * dp);
 }
 
-__device__ __forceinline__ void add_vec(float *pg, uint32_t idx, f3 v)
-{
-    float *q = pg + 3 * (size_t)idx;
-    atomicAdd(q + 0, v.x);
-    atomicAdd(q + 1, v.y);
-    atomicAdd(q + 2, v.z);
-}
-
 // RayIntegratorOctMapBackward::integrate_cell (ray_integrator_octmap.cuh:683-860)
 template <typename A, int RD, int RS> struct BwdIntegrator {
     f3 o, d;
@@ -386,10 +377,10 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
     f3 fwd_rgb, fwd_rgb_grad;
     float fwd_alpha, fwd_alpha_grad, ray_error;
     float W_run, S_run, W_total, S_total, dist_grad, D_total, D_running;
-    float *agg; // this wave's LDS slice, agg_floats<RD, RS>() floats
+    float *rows;        // this wave's LDS row table, ROW_TABLE_FLOATS floats
+    uint32_t spec_taps; // the ray's four specular taps, 8 bits each
 
     static constexpr int ND = 3 * RD * RD, NS = 3 * RS * RS;
-    static constexpr int NC = agg_cell_floats<RD, RS>(); // floats of one copy of the cell slice
 
     // The texture, density and point_error gradients of an integrated cell
     // are held until the walk has integrated the next cell (or ends): the
@@ -420,119 +411,184 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
         held_perr = perr;
     }
 
-    // Global add of entry k of a cell's slice (k in [0, NC)).
-    __device__ __forceinline__ void slice_add(uint32_t cell, uint32_t k, float x)
+    // Global add of column k of a combined record (k in [0, REC_COLS)) of
+    // `cell`; for a texture column, `tap` is the texel of the column's tap.
+    __device__ __forceinline__ void column_add(uint32_t cell, uint32_t k, uint32_t tap, float x)
     {
-        if (k == (uint32_t)(ND + NS + 1) && !point_error)
-            return; // no point_error output: its entry has no target
+        if (k == 25u && !point_error)
+            return; // no point_error output: its column has no target
+        if (k < 24u && tap >= (uint32_t)(k < 12u ? RD * RD : RS * RS))
+            return; // an unshaded cell: texture columns zero, taps unset
+        const uint32_t kt = k < 12u ? k : k - 12u;
+        const uint32_t texel = tap * 3u + (kt - 3u * (kt / 3u));
         if constexpr (std::is_same<A, float>::value) {
             // one atomic instruction for every target
-            float *q = k < (uint32_t)ND            ? diffuse_grad + (size_t)cell * ND + k
-                       : k < (uint32_t)(ND + NS)   ? specular_grad + (size_t)cell * NS + (k - ND)
-                       : k == (uint32_t)(ND + NS)  ? density_grad + cell
-                       : k == (uint32_t)(ND + NS + 1) ? point_error + cell
-                                                      : points_grad + 3 * (size_t)cell + (k - (ND + NS + 2));
+            float *q = k < 12u    ? diffuse_grad + (size_t)cell * ND + texel
+                       : k < 24u  ? specular_grad + (size_t)cell * NS + texel
+                       : k == 24u ? density_grad + cell
+                       : k == 25u ? point_error + cell
+                                  : points_grad + 3 * (size_t)cell + (k - 26u);
             atomicAdd(q, x);
         } else {
-            if (k < (uint32_t)ND)
-                Attr<A>::add(diffuse_grad + (size_t)cell * ND, k, x);
-            else if (k < (uint32_t)(ND + NS))
-                Attr<A>::add(specular_grad + (size_t)cell * NS, k - ND, x);
-            else if (k == (uint32_t)(ND + NS))
+            if (k < 12u)
+                Attr<A>::add(diffuse_grad + (size_t)cell * ND, texel, x);
+            else if (k < 24u)
+                Attr<A>::add(specular_grad + (size_t)cell * NS, texel, x);
+            else if (k == 24u)
                 atomicAdd(density_grad + cell, x);
-            else if (k == (uint32_t)(ND + NS + 1))
+            else if (k == 25u)
                 Attr<A>::add(point_error, cell, x);
             else
-                atomicAdd(points_grad + 3 * (size_t)cell + (k - (ND + NS + 2)), x);
+                atomicAdd(points_grad + 3 * (size_t)cell + (k - 26u), x);
+        }
+    }
+
+    // What a lane needs to send column k of a combined record: the tap it
+    // reads (a byte of the diffuse or specular tap word; none for the other
+    // columns) and, for f32 outputs, the target as base + cell * stride +
+    // 3 * tap + off.  Set once per scatter, not per group.
+    struct Column {
+        uint32_t k, sh, tmask;
+        bool diffuse_taps, on;
+        float *base;
+        uint32_t stride, off, taps; // taps: texels of the map (1 for other columns)
+    };
+
+    __device__ __forceinline__ Column column(uint32_t k) const
+    {
+        Column c;
+        const uint32_t kt = k < 12u ? k : k - 12u;
+        c.k = k;
+        c.sh = k < 24u ? 8u * (kt / 3u) : 0u;
+        c.tmask = k < 24u ? 0xffu : 0u;
+        c.diffuse_taps = k < 12u;
+        c.on = k != 25u || point_error;
+        c.base = nullptr;
+        c.stride = 0;
+        c.off = 0;
+        c.taps = k < 12u ? RD * RD : k < 24u ? RS * RS : 1u;
+        if constexpr (std::is_same<A, float>::value) {
+            c.base = k < 12u    ? diffuse_grad
+                     : k < 24u  ? specular_grad
+                     : k == 24u ? density_grad
+                     : k == 25u ? point_error
+                                : points_grad;
+            c.stride = k < 12u ? (uint32_t)ND : k < 24u ? (uint32_t)NS : k < 26u ? 1u : 3u;
+            c.off = k < 24u ? kt - 3u * (kt / 3u) : k < 26u ? 0u : k - 26u;
+        }
+        return c;
+    }
+
+    __device__ __forceinline__ void column_send(const Column &c, uint32_t cell, uint32_t tap, float x)
+    {
+        if constexpr (std::is_same<A, float>::value) {
+            if (c.on && tap < c.taps)
+                atomicAdd(c.base + (size_t)cell * c.stride + 3u * tap + c.off, x);
+        } else {
+            column_add(cell, c.k, tap, x);
+        }
+    }
+
+    // The combining passes of one scatter; ONE: every column has its own
+    // lane (at least REC_COLS lanes scatter), so the column is set up once.
+    template <bool ONE>
+    __device__ __forceinline__ void combine(uint32_t cell, uint64_t act, uint32_t nact, uint32_t arank, uint32_t lane)
+    {
+        Column c1;
+        if (ONE)
+            c1 = column(arank);
+        uint64_t pend = act;
+        while (pend) { // one group per pass, at most 64
+            const int ll = (int)__builtin_ctzll(pend);
+            const uint32_t lead = __builtin_amdgcn_readlane(cell, ll);
+            const uint32_t ldt = __builtin_amdgcn_readlane(held_taps, ll);
+            const uint32_t lst = __builtin_amdgcn_readlane(spec_taps, ll);
+            const uint64_t mem = __ballot(cell == lead) & pend;
+            pend &= ~mem;
+            // do all members share the leader's taps? (the usual case)
+            const bool uniform =
+                (mem & (mem - 1)) == 0 || __ballot(((mem >> lane) & 1u) && (held_taps != ldt || spec_taps != lst)) == 0;
+            for (uint32_t k = arank; k < (uint32_t)REC_COLS; k += nact) {
+                const Column c = ONE ? c1 : column(k);
+                const float *col = rows + k;
+                float acc = 0.0f;
+                uint64_t m = mem;
+                if (uniform) {
+                    do { // four members per pass; the zero row stands in for absent ones
+                        const int s0 = (int)__builtin_ctzll(m);
+                        m &= m - 1;
+                        const int s1 = m ? (int)__builtin_ctzll(m) : 64;
+                        m &= m - 1;
+                        const int s2 = m ? (int)__builtin_ctzll(m) : 64;
+                        m &= m - 1;
+                        const int s3 = m ? (int)__builtin_ctzll(m) : 64;
+                        m &= m - 1;
+                        const float x0 = col[s0 * ROW_STRIDE], x1 = col[s1 * ROW_STRIDE];
+                        const float x2 = col[s2 * ROW_STRIDE], x3 = col[s3 * ROW_STRIDE];
+                        acc += (x0 + x1) + (x2 + x3);
+                    } while (m);
+                    if (acc != 0.0f)
+                        column_send(c, lead, ((c.diffuse_taps ? ldt : lst) >> c.sh) & c.tmask, acc);
+                    continue;
+                }
+                // members in lane order; a texture column sends its sum
+                // whenever its tap changes
+                uint32_t cur = 0xffffffffu;
+                do {
+                    const int s0 = (int)__builtin_ctzll(m);
+                    m &= m - 1;
+                    const float x = col[s0 * ROW_STRIDE];
+                    const uint32_t dt = __builtin_amdgcn_readlane(held_taps, s0);
+                    const uint32_t st = __builtin_amdgcn_readlane(spec_taps, s0);
+                    const uint32_t tap = ((c.diffuse_taps ? dt : st) >> c.sh) & c.tmask;
+                    if (tap != cur) {
+                        if (acc != 0.0f)
+                            column_send(c, lead, cur, acc);
+                        cur = tap;
+                        acc = 0.0f;
+                    }
+                    acc += x;
+                } while (m);
+                if (acc != 0.0f)
+                    column_send(c, lead, cur, acc);
+            }
         }
     }
 
     // Scatters the held gradients of `cell` and, when with_point, its point
-    // gradient pg; lanes of one cell combined first.  The pending lanes and
-    // each group are wave-uniform masks (scalar registers), so the leader loop
-    // is scalar work and a group's members are picked by their mask bit.
+    // gradient pg.  Lanes with the same cell are combined: every scattering
+    // lane writes its record as a row of the LDS table, and for each group
+    // (wave-uniform masks, lowest pending lane leading) the active lanes take
+    // one column each, add it down the members' rows and send the sum with a
+    // global atomic (a texture column once per run of members sharing its
+    // tap).  A lone lane goes the same way: its record then leaves as one
+    // atomic per column, spread over the active lanes.
     __device__ __forceinline__ void scatter(uint32_t cell, bool with_point, f3 pg)
     {
         const bool color = held_taps != HELD_NO_COLOR;
-        const int tap[4] = {(int)(held_taps & 0xffu), (int)((held_taps >> 8) & 0xffu), (int)((held_taps >> 16) & 0xffu),
-                            (int)(held_taps >> 24)};
         const uint32_t lane = threadIdx.x & 63u;
-        // the scattering lanes and the groups as wave-uniform masks
+        {
+            float4 *row = reinterpret_cast<float4 *>(rows + lane * ROW_STRIDE);
+            const float g0 = color ? held_gl[0] : 0.0f, g1 = color ? held_gl[1] : 0.0f,
+                        g2 = color ? held_gl[2] : 0.0f;
+            // diffuse taps 0-3, then specular taps 0-3, three channels each
+            row[0] = make_float4(held_w[0] * g0, held_w[0] * g1, held_w[0] * g2, held_w[1] * g0);
+            row[1] = make_float4(held_w[1] * g1, held_w[1] * g2, held_w[2] * g0, held_w[2] * g1);
+            row[2] = make_float4(held_w[2] * g2, held_w[3] * g0, held_w[3] * g1, held_w[3] * g2);
+            row[3] = make_float4(spec.w00 * g0, spec.w00 * g1, spec.w00 * g2, spec.w10 * g0);
+            row[4] = make_float4(spec.w10 * g1, spec.w10 * g2, spec.w01 * g0, spec.w01 * g1);
+            row[5] = make_float4(spec.w01 * g2, spec.w11 * g0, spec.w11 * g1, spec.w11 * g2);
+            row[6] = make_float4(held_ds, held_perr, with_point ? pg.x : 0.0f, with_point ? pg.y : 0.0f);
+            rows[lane * ROW_STRIDE + 28] = with_point ? pg.z : 0.0f;
+        }
+        wave_lds_sync();
         const uint64_t act = __ballot(1);
         const uint32_t nact = (uint32_t)__popcll(act), arank = lane_rank(act);
-        uint64_t pend = act, direct = 0;
-        for (int round = 0; round < AGG_ROUNDS && pend; ++round) {
-            const uint32_t lead = __builtin_amdgcn_readlane(cell, (int)__builtin_ctzll(pend));
-            const uint64_t mem = __ballot(cell == lead) & pend;
-            pend &= ~mem;
-            if (__popcll(mem) < AGG_MIN) {
-                direct |= mem;
-                continue;
-            }
-            if ((mem >> lane) & 1u) {
-                float *sl = agg + NC * (lane_rank(mem) % AGG_COPIES);
-                if (color) {
-#pragma unroll
-                    for (int c = 0; c < 3; ++c) {
-#pragma unroll
-                        for (int t = 0; t < 4; ++t)
-                            atomicAdd(sl + tap[t] * 3 + c, held_w[t] * held_gl[c]);
-                    }
-#pragma unroll
-                    for (int c = 0; c < 3; ++c) {
-                        atomicAdd(sl + ND + spec.i00 * 3 + c, spec.w00 * held_gl[c]);
-                        atomicAdd(sl + ND + spec.i10 * 3 + c, spec.w10 * held_gl[c]);
-                        atomicAdd(sl + ND + spec.i01 * 3 + c, spec.w01 * held_gl[c]);
-                        atomicAdd(sl + ND + spec.i11 * 3 + c, spec.w11 * held_gl[c]);
-                    }
-                }
-                atomicAdd(sl + ND + NS, held_ds);
-                if (point_error)
-                    atomicAdd(sl + ND + NS + 1, held_perr);
-                if (with_point) {
-                    atomicAdd(sl + ND + NS + 2, pg.x);
-                    atomicAdd(sl + ND + NS + 3, pg.y);
-                    atomicAdd(sl + ND + NS + 4, pg.z);
-                }
-            }
-            wave_lds_sync();
-            for (uint32_t k = arank; k < (uint32_t)NC; k += nact) {
-                float x = 0.0f;
-#pragma unroll
-                for (int c = 0; c < AGG_COPIES; ++c) {
-                    x += agg[NC * c + k];
-                    agg[NC * c + k] = 0.0f;
-                }
-                if (x != 0.0f)
-                    slice_add(lead, k, x);
-            }
-            wave_lds_sync();
-        }
-        direct |= pend; // groups beyond AGG_ROUNDS
-        if ((direct >> lane) & 1u) {
-            if (color) {
-                A *dg = diffuse_grad + (size_t)cell * ND;
-                A *sg = specular_grad + (size_t)cell * NS;
-#pragma unroll
-                for (int c = 0; c < 3; ++c) {
-#pragma unroll
-                    for (int t = 0; t < 4; ++t)
-                        Attr<A>::add(dg, tap[t] * 3 + c, held_w[t] * held_gl[c]);
-                }
-#pragma unroll
-                for (int c = 0; c < 3; ++c) {
-                    Attr<A>::add(sg, spec.i00 * 3 + c, spec.w00 * held_gl[c]);
-                    Attr<A>::add(sg, spec.i10 * 3 + c, spec.w10 * held_gl[c]);
-                    Attr<A>::add(sg, spec.i01 * 3 + c, spec.w01 * held_gl[c]);
-                    Attr<A>::add(sg, spec.i11 * 3 + c, spec.w11 * held_gl[c]);
-                }
-            }
-            atomicAdd(density_grad + cell, held_ds);
-            if (point_error)
-                Attr<A>::add(point_error, cell, held_perr);
-            if (with_point)
-                add_vec(points_grad, cell, pg);
-        }
+        if (nact >= (uint32_t)REC_COLS)
+            combine<true>(cell, act, nact, arank, lane);
+        else
+            combine<false>(cell, act, nact, arank, lane);
+        wave_lds_sync(); // the rows are read before the next scatter rewrites them
     }
 
     // After the walk: a walk that ended without the transmittance stop
@@ -659,16 +715,17 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
 template <typename A, int RD, int RS, bool STATS>
 __global__ __launch_bounds__(TRAIN_BLOCK) __attribute__((amdgpu_waves_per_eu(4))) void bwd_kernel(BwdArgs a)
 {
-    constexpr int NAGG = agg_floats<RD, RS>();
-    __shared__ float agg_lds[TRAIN_WAVES][NAGG];
-    float *agg = agg_lds[threadIdx.x / 64];
-    agg_clear(agg, NAGG);
+    __shared__ __align__(16) float rows_lds[TRAIN_WAVES][ROW_TABLE_FLOATS];
+    float *rows = rows_lds[threadIdx.x / 64];
+    if ((threadIdx.x & 63u) < (uint32_t)ROW_STRIDE)
+        rows[64 * ROW_STRIDE + (threadIdx.x & 63u)] = 0.0f; // the zero row
+    wave_lds_sync();
     uint32_t r = train_ray(xcd_interleaved_block<TRAIN_XCD_CHUNK>() * blockDim.x + threadIdx.x, a.num_rays, a.num_images,
                            a.img_h, a.img_w);
     if (r == NONE)
         return;
     BwdIntegrator<A, RD, RS> it;
-    it.agg = agg;
+    it.rows = rows;
     load_ray(a.rays, r, it.o, it.d);
     it.density = a.density;
     it.tex.diffuse = (const A *)a.diffuse;
@@ -676,6 +733,11 @@ __global__ __launch_bounds__(TRAIN_BLOCK) __attribute__((amdgpu_waves_per_eu(4))
     float su, sv;
     oct_encode<RS>(mk(-it.d.x, -it.d.y, -it.d.z), su, sv);
     it.spec = bilinear_setup<RS>(su, sv);
+    static_assert(RS * RS <= 256, "specular tap indices are packed in 8 bits");
+    it.spec_taps = (uint32_t)it.spec.i00 | (uint32_t)it.spec.i10 << 8 | (uint32_t)it.spec.i01 << 16 |
+                   (uint32_t)it.spec.i11 << 24;
+    // a record of an unshaded cell writes held_w * 0 into the row
+    it.held_w[0] = it.held_w[1] = it.held_w[2] = it.held_w[3] = 0.0f;
     it.thr = a.thr;
     const A *rg = (const A *)a.rgba_grad;
     const A *rv = (const A *)a.rgba;
