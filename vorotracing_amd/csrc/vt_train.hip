@@ -94,11 +94,13 @@ constexpr int AGG_ROUNDS = 32; // forward contribution: groups combined per scat
 
 // The backward's scatter record of one lane: 12 diffuse and 12 specular
 // values (tap-major, 3 channels each), dL/ds, the point_error term and the
-// point gradient.  Each scattering lane writes its record as one row of the
-// wave's LDS table; ROW_STRIDE keeps rows 16-byte aligned and puts 8
-// consecutive lanes' 16-byte stores on distinct banks.  Row 64 stays zero
-// and is read in place of absent group members.
+// point gradient, then the diffuse and specular tap words (words 29, 30).
+// Each scattering lane writes its record as one row of the wave's LDS table;
+// ROW_STRIDE keeps rows 16-byte aligned and puts 8 consecutive lanes'
+// 16-byte stores on distinct banks.  Row 64 stays zero and is read in place
+// of absent group members.
 constexpr int REC_COLS = 29;
+constexpr int REC_DTAPS = 29, REC_STAPS = 30;
 constexpr int ROW_STRIDE = 36;
 constexpr int ROW_TABLE_FLOATS = 65 * ROW_STRIDE;
 
@@ -490,7 +492,10 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
     }
 
     // The combining passes of one scatter; ONE: every column has its own
-    // lane (at least REC_COLS lanes scatter), so the column is set up once.
+    // lane (at least REC_COLS lanes scatter), so the column is set up once;
+    // otherwise a lane takes several columns.  (Two lanes per column, each
+    // adding half the members, ran slower: two lanes adding to one address
+    // in one atomic instruction serialise.)
     template <bool ONE>
     __device__ __forceinline__ void combine(uint32_t cell, uint64_t act, uint32_t nact, uint32_t arank, uint32_t lane)
     {
@@ -511,6 +516,7 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
             for (uint32_t k = arank; k < (uint32_t)REC_COLS; k += nact) {
                 const Column c = ONE ? c1 : column(k);
                 const float *col = rows + k;
+                const uint32_t t0 = ((c.diffuse_taps ? ldt : lst) >> c.sh) & c.tmask;
                 float acc = 0.0f;
                 uint64_t m = mem;
                 if (uniform) {
@@ -528,29 +534,46 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
                         acc += (x0 + x1) + (x2 + x3);
                     } while (m);
                     if (acc != 0.0f)
-                        column_send(c, lead, ((c.diffuse_taps ? ldt : lst) >> c.sh) & c.tmask, acc);
+                        column_send(c, lead, t0, acc);
                     continue;
                 }
-                // members in lane order; a texture column sends its sum
-                // whenever its tap changes
-                uint32_t cur = 0xffffffffu;
+                // taps differ between members: each column keeps two sums, for
+                // the leader's tap and for one other; a third tap sends the
+                // second sum and takes its place
+                const float *tw = rows + (c.diffuse_taps ? REC_DTAPS : REC_STAPS);
+                uint32_t t1 = 0xffffffffu;
+                float acc1 = 0.0f;
                 do {
-                    const int s0 = (int)__builtin_ctzll(m);
-                    m &= m - 1;
-                    const float x = col[s0 * ROW_STRIDE];
-                    const uint32_t dt = __builtin_amdgcn_readlane(held_taps, s0);
-                    const uint32_t st = __builtin_amdgcn_readlane(spec_taps, s0);
-                    const uint32_t tap = ((c.diffuse_taps ? dt : st) >> c.sh) & c.tmask;
-                    if (tap != cur) {
-                        if (acc != 0.0f)
-                            column_send(c, lead, cur, acc);
-                        cur = tap;
-                        acc = 0.0f;
+                    int sm[4];
+                    float x[4];
+                    uint32_t w[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        sm[j] = m ? (int)__builtin_ctzll(m) : 64;
+                        m &= m - 1;
+                        x[j] = col[sm[j] * ROW_STRIDE];
+                        w[j] = __float_as_uint(tw[sm[j] * ROW_STRIDE]);
                     }
-                    acc += x;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        if (sm[j] == 64)
+                            break; // no more members (wave-uniform)
+                        const uint32_t tap = (w[j] >> c.sh) & c.tmask;
+                        const bool in0 = tap == t0, in1 = tap == t1;
+                        acc += in0 ? x[j] : 0.0f;
+                        acc1 += in1 ? x[j] : 0.0f;
+                        if (!in0 && !in1) {
+                            if (acc1 != 0.0f)
+                                column_send(c, lead, t1, acc1);
+                            t1 = tap;
+                            acc1 = x[j];
+                        }
+                    }
                 } while (m);
                 if (acc != 0.0f)
-                    column_send(c, lead, cur, acc);
+                    column_send(c, lead, t0, acc);
+                if (acc1 != 0.0f)
+                    column_send(c, lead, t1, acc1);
             }
         }
     }
@@ -579,7 +602,7 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
             row[4] = make_float4(spec.w10 * g1, spec.w10 * g2, spec.w01 * g0, spec.w01 * g1);
             row[5] = make_float4(spec.w01 * g2, spec.w11 * g0, spec.w11 * g1, spec.w11 * g2);
             row[6] = make_float4(held_ds, held_perr, with_point ? pg.x : 0.0f, with_point ? pg.y : 0.0f);
-            rows[lane * ROW_STRIDE + 28] = with_point ? pg.z : 0.0f;
+            row[7] = make_float4(with_point ? pg.z : 0.0f, __uint_as_float(held_taps), __uint_as_float(spec_taps), 0.0f);
         }
         wave_lds_sync();
         const uint64_t act = __ballot(1);
