@@ -491,11 +491,69 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
         }
     }
 
+    // Sum of column c (column k of the row table) over the members `mem` of
+    // one cell's group (ll: the lowest member; uniform: every member has the
+    // leader's taps).  acc is the sum for tap t0, the leader's; when taps
+    // differ, acc1 is the sum for one other tap t1, and a third tap sends
+    // acc1 and takes its place.
+    __device__ __forceinline__ void column_sum(const Column &c, uint32_t k, uint32_t lead, uint64_t mem, int ll,
+                                               bool uniform, uint32_t t0, float &acc, uint32_t &t1, float &acc1)
+    {
+        const float *col = rows + k;
+        uint64_t m = mem;
+        if (uniform) {
+            if ((mem & (mem - 1)) == 0) { // a lone lane: its own row
+                acc = col[ll * ROW_STRIDE];
+                return;
+            }
+            do { // four members per pass; the zero row stands in for absent ones
+                const int s0 = (int)__builtin_ctzll(m);
+                m &= m - 1;
+                const int s1 = m ? (int)__builtin_ctzll(m) : 64;
+                m &= m - 1;
+                const int s2 = m ? (int)__builtin_ctzll(m) : 64;
+                m &= m - 1;
+                const int s3 = m ? (int)__builtin_ctzll(m) : 64;
+                m &= m - 1;
+                const float x0 = col[s0 * ROW_STRIDE], x1 = col[s1 * ROW_STRIDE];
+                const float x2 = col[s2 * ROW_STRIDE], x3 = col[s3 * ROW_STRIDE];
+                acc += (x0 + x1) + (x2 + x3);
+            } while (m);
+            return;
+        }
+        const float *tw = rows + (c.diffuse_taps ? REC_DTAPS : REC_STAPS);
+        do {
+            int sm[4];
+            float x[4];
+            uint32_t w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                sm[j] = m ? (int)__builtin_ctzll(m) : 64;
+                m &= m - 1;
+                x[j] = col[sm[j] * ROW_STRIDE];
+                w[j] = __float_as_uint(tw[sm[j] * ROW_STRIDE]);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (sm[j] == 64)
+                    break; // no more members (wave-uniform)
+                const uint32_t tap = (w[j] >> c.sh) & c.tmask;
+                const bool in0 = tap == t0, in1 = tap == t1;
+                acc += in0 ? x[j] : 0.0f;
+                acc1 += in1 ? x[j] : 0.0f;
+                if (!in0 && !in1) {
+                    if (acc1 != 0.0f)
+                        column_send(c, lead, t1, acc1);
+                    t1 = tap;
+                    acc1 = x[j];
+                }
+            }
+        } while (m);
+    }
+
     // The combining passes of one scatter; ONE: every column has its own
     // lane (at least REC_COLS lanes scatter), so the column is set up once;
-    // otherwise a lane takes several columns.  (Two lanes per column, each
-    // adding half the members, ran slower: two lanes adding to one address
-    // in one atomic instruction serialise.)
+    // otherwise a lane takes several columns.
     template <bool ONE>
     __device__ __forceinline__ void combine(uint32_t cell, uint64_t act, uint32_t nact, uint32_t arank, uint32_t lane)
     {
@@ -515,61 +573,10 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
                 (mem & (mem - 1)) == 0 || __ballot(((mem >> lane) & 1u) && (held_taps != ldt || spec_taps != lst)) == 0;
             for (uint32_t k = arank; k < (uint32_t)REC_COLS; k += nact) {
                 const Column c = ONE ? c1 : column(k);
-                const float *col = rows + k;
                 const uint32_t t0 = ((c.diffuse_taps ? ldt : lst) >> c.sh) & c.tmask;
-                float acc = 0.0f;
-                uint64_t m = mem;
-                if (uniform) {
-                    do { // four members per pass; the zero row stands in for absent ones
-                        const int s0 = (int)__builtin_ctzll(m);
-                        m &= m - 1;
-                        const int s1 = m ? (int)__builtin_ctzll(m) : 64;
-                        m &= m - 1;
-                        const int s2 = m ? (int)__builtin_ctzll(m) : 64;
-                        m &= m - 1;
-                        const int s3 = m ? (int)__builtin_ctzll(m) : 64;
-                        m &= m - 1;
-                        const float x0 = col[s0 * ROW_STRIDE], x1 = col[s1 * ROW_STRIDE];
-                        const float x2 = col[s2 * ROW_STRIDE], x3 = col[s3 * ROW_STRIDE];
-                        acc += (x0 + x1) + (x2 + x3);
-                    } while (m);
-                    if (acc != 0.0f)
-                        column_send(c, lead, t0, acc);
-                    continue;
-                }
-                // taps differ between members: each column keeps two sums, for
-                // the leader's tap and for one other; a third tap sends the
-                // second sum and takes its place
-                const float *tw = rows + (c.diffuse_taps ? REC_DTAPS : REC_STAPS);
                 uint32_t t1 = 0xffffffffu;
-                float acc1 = 0.0f;
-                do {
-                    int sm[4];
-                    float x[4];
-                    uint32_t w[4];
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        sm[j] = m ? (int)__builtin_ctzll(m) : 64;
-                        m &= m - 1;
-                        x[j] = col[sm[j] * ROW_STRIDE];
-                        w[j] = __float_as_uint(tw[sm[j] * ROW_STRIDE]);
-                    }
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        if (sm[j] == 64)
-                            break; // no more members (wave-uniform)
-                        const uint32_t tap = (w[j] >> c.sh) & c.tmask;
-                        const bool in0 = tap == t0, in1 = tap == t1;
-                        acc += in0 ? x[j] : 0.0f;
-                        acc1 += in1 ? x[j] : 0.0f;
-                        if (!in0 && !in1) {
-                            if (acc1 != 0.0f)
-                                column_send(c, lead, t1, acc1);
-                            t1 = tap;
-                            acc1 = x[j];
-                        }
-                    }
-                } while (m);
+                float acc = 0.0f, acc1 = 0.0f;
+                column_sum(c, k, lead, mem, ll, uniform, t0, acc, t1, acc1);
                 if (acc != 0.0f)
                     column_send(c, lead, t0, acc);
                 if (acc1 != 0.0f)
