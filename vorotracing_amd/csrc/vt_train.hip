@@ -3,8 +3,9 @@
 // kernel :232-340), with f32 or f16 attribute storage.
 //
 // Attribute maps are (num_points, 3*R*R), texel-major / channel-minor.  The
-// backward scatters 28 gradient values per integrated cell with global
-// atomics (f32: hardware global_atomic_add_f32; f16: 32-bit CAS).
+// backward scatters 28 gradient values per integrated cell (29 with
+// point_error), lanes of one cell combined in LDS first, with global atomics
+// (f32: hardware global_atomic_add_f32; f16: 32-bit CAS).
 #include <type_traits>
 
 #include "vt_internal.h"
