@@ -128,6 +128,41 @@ def test_bwd_parity(gpu, which, f16, extras):
         assert perr is None
 
 
+@pytest.mark.parametrize("n", [23, 87])
+def test_bwd_parity_partial_waves(gpu, n):
+    """Flat ray batches keep ray order: 23 rays make one wave of 23 lanes, 87
+    a full wave and one of 23.  Fewer scattering lanes than the record's 29
+    columns make each lane sum several columns; consecutive pixels of one
+    row share cells, so the groups are real.  point_error on."""
+    s, rays, _, thr = _case("r8")
+    flat = rays[20, 8:8 + n].reshape(-1, 6) if n <= 40 else np.concatenate(
+        [rays[20, 4:44], rays[21, 4:44], rays[22, 4:4 + n - 80]]).reshape(-1, 6)
+    flat = np.ascontiguousarray(flat, np.float32)
+    assert flat.shape == (n, 6)
+    start = H.start_for(s, flat)
+    rng = np.random.default_rng(3)
+    dif32, spe32 = s.diffuse.astype(np.float32), s.specular.astype(np.float32)
+    fw = core.trace_fwd(s.points, dif32, spe32, s.diff_res, s.spec_res, s.density, s.adjacency, s.offsets,
+                        flat, start, weight_threshold=thr)
+    g = rng.normal(size=(n, 4)).astype(np.float32)
+    rerr = rng.uniform(0, 1, size=(n,)).astype(np.float32)
+    want = core.trace_bwd(s.points, dif32, spe32, s.diff_res, s.spec_res, s.density, s.adjacency,
+                          s.offsets, flat, start, fw["rgba"], g, ray_error=rerr, distortion=fw["distortion"],
+                          W_total=fw["W_total"], S_total=fw["S_total"], t_far=fw["t_far"], weight_threshold=thr)
+    pts, dif, spe, den, adj, off = _scene_tensors(s, gpu, False)
+    d = lambda a: None if a is None else H.to_dev(a, gpu)  # noqa: E731
+    pg, dgd, sgd, deng, _, perr = _C.trace_vorotracing_bwd(
+        pts, dif, spe, den, adj, off, d(flat), d(start), d(fw["rgba"]), d(g), None, None, None, d(rerr), 0.0,
+        d(fw["distortion"]), None, d(fw["W_total"]), d(fw["S_total"]), d(fw["t_far"]), thr, 1024)
+    torch.cuda.synchronize()
+    H.assert_grad_close(pg.cpu().numpy(), want["points_grad"], "points_grad")
+    H.assert_grad_close(deng.cpu().numpy(), want["density_grad"], "density_grad")
+    H.assert_grad_close(dgd.cpu().numpy(), want["diffuse_grad"], "diffuse_grad")
+    H.assert_grad_close(sgd.cpu().numpy(), want["specular_grad"], "specular_grad")
+    H.assert_grad_close(perr.cpu().numpy(), want["point_error"], "point_error")
+    assert np.abs(want["diffuse_grad"]).max() > 0 and np.abs(want["point_error"]).max() > 0
+
+
 def test_c5_shape_fisheye_rolling_shutter(gpu):
     """Config-5 shape at test size: equidistant fisheye rays with a rolling
     shutter (a different origin per image row), start cells from the LBVH for
