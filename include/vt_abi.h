@@ -227,6 +227,10 @@ int vt_trace_fwd(int attr_dtype, const float *points, const void *diffuse, const
  *   diffuse_grad / specular_grad attr dtype, density_grad f32 (num_points),
  *   point_error attr dtype (num_points) or NULL.
  *   image_h, image_w: lane order, as for vt_trace_fwd.
+ *   cell_workspace: f32 (num_points, 4), 16-byte aligned, any contents (an
+ *   extension, ABI version 4): the call accumulates each cell's point and
+ *   density gradients there, in one 16-byte slot per cell, and adds the
+ *   slots into points_grad and density_grad at its end.
  *   Gradient scatters of lanes that integrate the same cell in the same step
  *   are combined in LDS before the global atomics.
  */
@@ -239,7 +243,7 @@ int vt_trace_bwd(int attr_dtype, const float *points, const void *diffuse, const
                  const float *distortion_grad, const float *W_total, const float *S_total, const float *t_far,
                  float weight_threshold, uint32_t max_intersections, float *points_grad, void *diffuse_grad,
                  void *specular_grad, float *density_grad, void *point_error, uint16_t *adj_diff_workspace,
-                 vt_ray_stats *stats, vt_stream_t stream);
+                 float *cell_workspace, vt_ray_stats *stats, vt_stream_t stream);
 
 /*
  * Start-cell lookup.  Replaces _C.NNBVH (nn_bvh.h:4-16, nn_bvh.cu:43-109):

@@ -396,6 +396,7 @@ def trace_vorotracing_bwd(points_in, diffuse_in, specular_in, density_in, point_
     points_grad = torch.zeros((num_points, 3), dtype=rays.dtype, device=dev)
     ray_grad = torch.zeros_like(rays)
     workspace = torch.empty((adjacency_size + 32, 4), dtype=torch.float16, device=dev)
+    cell_workspace = torch.empty((num_points, 4), dtype=torch.float32, device=dev)
     with torch.cuda.device(dev):
         _lib.call("vt_trace_bwd", code, points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd, rs,
                   density.data_ptr(), adjacency.data_ptr(), adjacency_size, offsets.data_ptr(), num_points,
@@ -406,7 +407,7 @@ def trace_vorotracing_bwd(points_in, diffuse_in, specular_in, density_in, point_
                   W_total.data_ptr(), S_total.data_ptr(), t_far.data_ptr(), float(weight_threshold),
                   int(max_intersections), points_grad.data_ptr(), diffuse_grad.data_ptr(),
                   specular_grad.data_ptr(), density_grad.data_ptr(), _ptr(point_error), workspace.data_ptr(),
-                  _stats_ptr(stats, num_rays), _stream(dev))
+                  cell_workspace.data_ptr(), _stats_ptr(stats, num_rays), _stream(dev))
     return points_grad, diffuse_grad, specular_grad, density_grad, ray_grad, point_error
 
 

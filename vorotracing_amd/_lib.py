@@ -42,7 +42,7 @@ SIGNATURES = {
         C.c_int),
     "vt_trace_bwd": (
         [I32, P, P, P, U32, U32, P, P, U32, P, U32, P, U32, U32, U32, P, P, P, U32, P, P, P, P, F32, P, P, P, P, P, F32, U32,
-         P, P, P, P, P, P, P, P], C.c_int),
+         P, P, P, P, P, P, P, P, P], C.c_int),
     "vt_math_probe": ([I32, P, P, U32, P], C.c_int),
     "vt_grad_epilogue": ([P, C.c_uint64, P, C.c_uint64, P, C.c_uint64, P, P, F32, U32, P, P], C.c_int),
     "vt_adam_voro": ([P, P, P, P, P, P, P, P, P, P, P, P, U32, P, P, P, P, U32, U32, P, C.c_double, C.c_double, F32,

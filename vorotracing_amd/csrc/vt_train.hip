@@ -340,9 +340,8 @@ struct BwdArgs {
     const float *distortion, *distortion_grad, *W_total, *S_total;
     float thr;
     uint32_t max_steps;
-    float *points_grad;
+    float *cell_grad; // (num_points, 4): point gradient, density gradient
     void *diffuse_grad, *specular_grad;
-    float *density_grad;
     void *point_error;
     uint32_t *stats;
 };
@@ -372,9 +371,8 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
     uint32_t qi, nq;
     float qval;
     const float *qthr, *depth_grad;
-    float *points_grad;
+    float *cell_grad; // per cell (point gradient x, y, z, density gradient)
     A *diffuse_grad, *specular_grad, *point_error;
-    float *density_grad;
     f3 prev_geom, prev_grad, cur_grad, next_grad;
     uint32_t prev_idx;
     f3 fwd_rgb, fwd_rgb_grad;
@@ -428,9 +426,9 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
             // one atomic instruction for every target
             float *q = k < 12u    ? diffuse_grad + (size_t)cell * ND + texel
                        : k < 24u  ? specular_grad + (size_t)cell * NS + texel
-                       : k == 24u ? density_grad + cell
+                       : k == 24u ? cell_grad + 4 * (size_t)cell + 3
                        : k == 25u ? point_error + cell
-                                  : points_grad + 3 * (size_t)cell + (k - 26u);
+                                  : cell_grad + 4 * (size_t)cell + (k - 26u);
             atomicAdd(q, x);
         } else {
             if (k < 12u)
@@ -438,11 +436,11 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
             else if (k < 24u)
                 Attr<A>::add(specular_grad + (size_t)cell * NS, texel, x);
             else if (k == 24u)
-                atomicAdd(density_grad + cell, x);
+                atomicAdd(cell_grad + 4 * (size_t)cell + 3, x);
             else if (k == 25u)
                 Attr<A>::add(point_error, cell, x);
             else
-                atomicAdd(points_grad + 3 * (size_t)cell + (k - 26u), x);
+                atomicAdd(cell_grad + 4 * (size_t)cell + (k - 26u), x);
         }
     }
 
@@ -473,11 +471,10 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
         if constexpr (std::is_same<A, float>::value) {
             c.base = k < 12u    ? diffuse_grad
                      : k < 24u  ? specular_grad
-                     : k == 24u ? density_grad
                      : k == 25u ? point_error
-                                : points_grad;
-            c.stride = k < 12u ? (uint32_t)ND : k < 24u ? (uint32_t)NS : k < 26u ? 1u : 3u;
-            c.off = k < 24u ? kt - 3u * (kt / 3u) : k < 26u ? 0u : k - 26u;
+                                : cell_grad;
+            c.stride = k < 12u ? (uint32_t)ND : k < 24u ? (uint32_t)NS : k == 25u ? 1u : 4u;
+            c.off = k < 24u ? kt - 3u * (kt / 3u) : k == 24u ? 3u : k == 25u ? 0u : k - 26u;
         }
         return c;
     }
@@ -795,10 +792,9 @@ __global__ __launch_bounds__(TRAIN_BLOCK) __attribute__((amdgpu_waves_per_eu(4))
     it.qthr = K ? a.quantiles + (size_t)r * K : nullptr;
     it.depth_grad = K ? a.depth_grad + (size_t)r * K : nullptr;
     it.qval = K ? it.qthr[0] : 0.0f;
-    it.points_grad = a.points_grad;
+    it.cell_grad = a.cell_grad;
     it.diffuse_grad = (A *)a.diffuse_grad;
     it.specular_grad = (A *)a.specular_grad;
-    it.density_grad = a.density_grad;
     it.point_error = (A *)a.point_error;
     it.prev_geom = it.prev_grad = it.cur_grad = it.next_grad = mk(0.0f, 0.0f, 0.0f);
     it.prev_idx = NONE;
@@ -941,6 +937,30 @@ extern "C" int vt_trace_fwd(int attr_dtype, const float *points, const void *dif
     return launch_train<FwdK>(attr_dtype, a, diff_res, spec_res, stats != nullptr, s);
 }
 
+// The backward adds each cell's point and density gradients into one
+// 16-byte slot (x, y, z, density) of the caller's workspace, so that a
+// combined group's four sums there touch one cache line instead of one in
+// points_grad and one in density_grad; the slots are then added into those
+// outputs (caller zero-initialised, so the sums arrive unchanged).
+__global__ void cell_grad_clear_kernel(float4 *g, uint32_t n)
+{
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n)
+        g[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+}
+
+__global__ void cell_grad_out_kernel(const float4 *g, float *points_grad, float *density_grad, uint32_t n)
+{
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        const float4 v = g[i];
+        points_grad[3 * (size_t)i + 0] += v.x;
+        points_grad[3 * (size_t)i + 1] += v.y;
+        points_grad[3 * (size_t)i + 2] += v.z;
+        density_grad[i] += v.w;
+    }
+}
+
 extern "C" int vt_trace_bwd(int attr_dtype, const float *points, const void *diffuse, const void *specular,
                             uint32_t diff_res, uint32_t spec_res, const float *density, const uint32_t *adjacency,
                             uint32_t adjacency_size, const uint32_t *offsets, uint32_t num_points, const float *rays,
@@ -952,7 +972,7 @@ extern "C" int vt_trace_bwd(int attr_dtype, const float *points, const void *dif
                             const float *S_total, const float *t_far, float weight_threshold,
                             uint32_t max_intersections, float *points_grad, void *diffuse_grad, void *specular_grad,
                             float *density_grad, void *point_error, uint16_t *adj_diff_workspace,
-                            vt_ray_stats *stats, vt_stream_t stream)
+                            float *cell_workspace, vt_ray_stats *stats, vt_stream_t stream)
 {
     clear_error();
     (void)t_far;
@@ -960,6 +980,8 @@ extern "C" int vt_trace_bwd(int attr_dtype, const float *points, const void *dif
                "null scene pointer");
     VT_REQUIRE(num_rays == 0 || (rays && start_point && rgba && rgba_grad), "null ray pointer");
     VT_REQUIRE(points_grad && diffuse_grad && specular_grad && density_grad, "null gradient output");
+    VT_REQUIRE(cell_workspace && reinterpret_cast<uintptr_t>(cell_workspace) % 16 == 0,
+               "cell_workspace must be a 16-byte aligned (num_points, 4) float array");
     VT_REQUIRE(!depth_quantiles || num_quantiles == 0 || (depth_idx && depth_grad),
                "depth_idx and depth_grad required when depth_quantiles is given");
     VT_REQUIRE(!ray_error || point_error, "point_error output required when ray_error is given");
@@ -994,11 +1016,21 @@ extern "C" int vt_trace_bwd(int attr_dtype, const float *points, const void *dif
     a.S_total = S_total;
     a.thr = weight_threshold;
     a.max_steps = max_intersections;
-    a.points_grad = points_grad;
+    a.cell_grad = cell_workspace;
     a.diffuse_grad = diffuse_grad;
     a.specular_grad = specular_grad;
-    a.density_grad = density_grad;
     a.point_error = point_error;
     a.stats = reinterpret_cast<uint32_t *>(stats);
-    return launch_train<BwdK>(attr_dtype, a, diff_res, spec_res, stats != nullptr, s);
+    if (num_rays == 0)
+        return VT_OK;
+    const uint32_t cblocks = (num_points + 255) / 256;
+    cell_grad_clear_kernel<<<cblocks, 256, 0, s>>>(reinterpret_cast<float4 *>(cell_workspace), num_points);
+    VT_LAUNCH_CHECK("cell_grad_clear_kernel");
+    rc = launch_train<BwdK>(attr_dtype, a, diff_res, spec_res, stats != nullptr, s);
+    if (rc)
+        return rc;
+    cell_grad_out_kernel<<<cblocks, 256, 0, s>>>(reinterpret_cast<const float4 *>(cell_workspace), points_grad,
+                                                  density_grad, num_points);
+    VT_LAUNCH_CHECK("cell_grad_out_kernel");
+    return VT_OK;
 }
