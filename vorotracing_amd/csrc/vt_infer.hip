@@ -94,8 +94,8 @@ struct ShadeQueue {
     float w[SQ_RING], dvx[SQ_RING], dvy[SQ_RING], dvz[SQ_RING];
     uint8_t owner[SQ_RING];          // owner lane | 0x80 when dv is already the direction
     unsigned long long mask[64];     // per owner lane: its entries in the batch
-    uint8_t si[64][4];               // specular taps
-    float sw[64][4];
+    uint32_t si[64];                 // specular taps, 8 bits each
+    float sw[4][64];                 // specular weights (tap-major: lanes of different owners on different banks)
     uint32_t tail;                   // entries appended so far (mod 2^32)
 };
 __shared__ ShadeQueue infer_queues[INFER_BLOCK / 64];
@@ -201,14 +201,15 @@ __device__ __forceinline__ void shade_batch(ShadeQueue &q, uint32_t head, uint32
         shade_oct_encode<RD>(pd, u, v);
         const Bilinear db = bilinear_setup<RD>(u, v);
         Bilinear sb;
-        sb.i00 = q.si[own][0];
-        sb.i10 = q.si[own][1];
-        sb.i01 = q.si[own][2];
-        sb.i11 = q.si[own][3];
-        sb.w00 = q.sw[own][0];
-        sb.w10 = q.sw[own][1];
-        sb.w01 = q.sw[own][2];
-        sb.w11 = q.sw[own][3];
+        const uint32_t si = q.si[own];
+        sb.i00 = (int)(si & 0xffu);
+        sb.i10 = (int)((si >> 8) & 0xffu);
+        sb.i01 = (int)((si >> 16) & 0xffu);
+        sb.i11 = (int)(si >> 24);
+        sb.w00 = q.sw[0][own];
+        sb.w10 = q.sw[1][own];
+        sb.w01 = q.sw[2][own];
+        sb.w11 = q.sw[3][own];
         const uint32_t cell = q.cell[k];
         const f3 a = integ.tex.sample_diffuse(cell, db);
         const f3 b = integ.tex.sample_specular(cell, sb);
@@ -328,14 +329,11 @@ void infer_kernel(InferArgs a, uint32_t total_slots)
         float su, sv;
         oct_encode<RS>(mk(-integ.d.x, -integ.d.y, -integ.d.z), su, sv);
         const Bilinear sb = bilinear_setup<RS>(su, sv);
-        q.si[lane][0] = (uint8_t)sb.i00;
-        q.si[lane][1] = (uint8_t)sb.i10;
-        q.si[lane][2] = (uint8_t)sb.i01;
-        q.si[lane][3] = (uint8_t)sb.i11;
-        q.sw[lane][0] = sb.w00;
-        q.sw[lane][1] = sb.w10;
-        q.sw[lane][2] = sb.w01;
-        q.sw[lane][3] = sb.w11;
+        q.si[lane] = (uint32_t)sb.i00 | (uint32_t)sb.i10 << 8 | (uint32_t)sb.i01 << 16 | (uint32_t)sb.i11 << 24;
+        q.sw[0][lane] = sb.w00;
+        q.sw[1][lane] = sb.w10;
+        q.sw[2][lane] = sb.w01;
+        q.sw[3][lane] = sb.w11;
         walk_begin(w, a.points, a.offsets, start);
     }
     q.mask[lane] = 0ull;
