@@ -631,6 +631,7 @@ def train_c2(dev, log, cpu=False):
            "workload": "C2: TraceVoroTracing forward + backward, 262,144 sites (torus + background), 4x4 fp32 "
                        "textures, one 800x600 pinhole camera, upstream dL/dRGB ~ N(0,1), thr 0.001"}
     out["roofline_fwd"], out["roofline_bwd"] = train_rooflines(model, rays, sp, g, dev, log)
+    out["f16_storage"] = train_f16_storage(model, rays, sp, g, dev, log)
     out["full_step"] = train_step_c2(sc, dev, rays, sp, g, log)
     if cpu:
         out["cpu_baseline"] = train_c2_cpu(model, rays, sp, g, log)
@@ -683,6 +684,40 @@ def train_rooflines(model, rays, sp, g, dev, log, R=10):
     log(f"C2 fwd_kernel {t_fwd:.3f} ms, bwd_kernel {t_bwd:.3f} ms (prefetch {t_pre:.3f} ms); HBM fractions "
         f"{rf['frac']}, {rb['frac']}")
     return rf, rb
+
+
+def train_f16_storage(model, rays, sp, g, dev, log, R=10):
+    """The C2 forward and backward entries with f16 attribute storage (the reference's half-precision maps:
+    f16 textures, RGBA and its gradient; texture gradients summed with half-precision atomics), HIP events
+    around R calls of each _C entry, prefetch included."""
+    import torch
+
+    from vorotracing_amd import _C
+
+    dens = model.activated_density().detach()
+    scn = (model.primal_points.detach(), model.att_diffuse.detach().half(), model.att_specular.detach().half(),
+           dens, model.point_adjacency, model.point_adjacency_offsets)
+    gh = g.half()
+    fw = _C.trace_vorotracing_fwd(*scn, rays, sp, None, 0.001, 1024, False)
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(R):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / R
+
+    t_fwd = timed(lambda: _C.trace_vorotracing_fwd(*scn, rays, sp, None, 0.001, 1024, False))
+    t_bwd = timed(lambda: _C.trace_vorotracing_bwd(*scn, rays, sp, fw[0], gh, None, None, None, None, 0.0, fw[5],
+                                                   None, fw[6], fw[7], fw[8], 0.001, 1024))
+    log(f"C2 with f16 maps: forward entry {t_fwd:.3f} ms, backward entry {t_bwd:.3f} ms")
+    return {"forward_ms": round(t_fwd, 3), "backward_ms": round(t_bwd, 3),
+            "note": "f16 diffuse/specular storage, _C entries (prefetch included), HIP events over 10 calls"}
 
 
 def train_step_c2(sc, dev, rays, sp, g, log, K=10):
