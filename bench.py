@@ -6,7 +6,7 @@ over 32 poses, weight threshold 0.01, cell-skip 1e-3, fp16 inference.  A
 step is one ``VoroTracingInfer.render`` of one pose (start-cell LBVH query +
 traversal kernel), as timed by the reference's benchmark_eval.py:137-158;
 ``value`` = frames per second over ``--steps`` whole renders (rays resident in
-HBM) with three frames in flight on side streams, every frame checked
+HBM) with two frames in flight on side streams, every frame checked
 bit-identical to its serial render; the serial protocol is reported beside it.
 
 Also reported: the traversal kernel's duration from HIP events on its stream,
@@ -32,7 +32,7 @@ HBM_PEAK_GBS = 8000.0
 # vector peak is 256 CUs x 4 SIMDs x 32 lanes x 2 flops x 2.4 GHz, i.e. one
 # wave64 instruction per SIMD every 2 cycles.
 VALU_PEAK_PER_S = 256 * 4 * 2.4e9 / 2
-IN_FLIGHT = 3
+IN_FLIGHT = 2
 
 
 def log(*a):
@@ -219,8 +219,8 @@ def main():
     log(f"serial: {K} frames, {1000 * t_serial / K:.3f} ms/frame, {K / t_serial:.1f} FPS, "
         f"traversal kernel {kernel_avg_ms:.3f} ms")
 
-    # The same frames with three in flight (VoroTracingInfer.render_frames):
-    # frame k renders (start-cell query and traversal) on side stream k mod 3, so the
+    # The same frames with two in flight (VoroTracingInfer.render_frames):
+    # frame k renders (start-cell query and traversal) on side stream k mod 2, so the
     # end of one frame, when few waves are left, overlaps the start of the
     # next.  Every frame is a whole render, checked bit for bit against the
     # serial frames.
