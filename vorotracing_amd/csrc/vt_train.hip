@@ -80,8 +80,8 @@ template <typename A, int RD, int RS> struct TrainTex {
 // cell in the same step (all rays of a camera share the start cell and its
 // neighbours), and hardware atomics to one address serialise.  A scatter
 // therefore groups the active lanes by cell, leader by leader (the lowest
-// pending lane).  The forward's contribution adds a group of at least AGG_MIN
-// lanes in one LDS word and sends it with one atomic; the backward's records
+// pending lane).  The forward's contribution sums a group's weights with
+// v_readlane (FwdIntegrator::scatter_contribution); the backward's records
 // go through a per-wave LDS row table (BwdIntegrator::scatter).  Only the
 // order of the floating-point additions changes (atomics have no defined
 // order anyway).
@@ -90,8 +90,6 @@ constexpr int TRAIN_BLOCK = 64; // one wave per block: each wave's LDS is freed 
 constexpr int TRAIN_WAVES = TRAIN_BLOCK / 64;
 constexpr int TRAIN_CHUNK = 8; // face records read together per exit-face step
 constexpr uint32_t TRAIN_XCD_CHUNK = 32; // blocks per XCD turn (xcd_interleaved_block)
-constexpr int AGG_MIN = 2;     // forward contribution: smallest group combined
-constexpr int AGG_ROUNDS = 32; // forward contribution: groups combined per scatter
 
 // The backward's scatter record of one lane: 12 diffuse and 12 specular
 // values (tap-major, 3 channels each), dL/ds, the point_error term and the
@@ -105,27 +103,6 @@ constexpr int REC_DTAPS = 29, REC_STAPS = 30;
 constexpr int ROW_STRIDE = 36;
 constexpr int ROW_TABLE_FLOATS = 65 * ROW_STRIDE;
 
-// One combining round over the lanes still pending: the key of the lowest
-// pending lane leads; `mine` marks its group and `comb` (wave-uniform) says
-// whether the group is large enough to combine.  Returns false when no lane
-// is pending.  Up to AGG_ROUNDS groups are combined per scatter; lanes of
-// smaller groups and lanes left over scatter directly.
-struct AggRound {
-    uint32_t lead;
-    bool mine, comb;
-};
-
-__device__ __forceinline__ bool agg_round(uint32_t key, bool pending, AggRound &g)
-{
-    uint64_t pm = __ballot(pending);
-    if (pm == 0)
-        return false;
-    g.lead = __builtin_amdgcn_readlane(key, (int)__builtin_ctzll(pm));
-    g.mine = pending && key == g.lead;
-    g.comb = __popcll(__ballot(g.mine)) >= AGG_MIN;
-    return true;
-}
-
 // Ray of lane slot s: 8x8 screen tiles of row-major images, or ray order.
 constexpr uint32_t TRAIN_TILE = 8;
 
@@ -134,15 +111,6 @@ __device__ __forceinline__ uint32_t train_ray(uint32_t s, uint32_t num_rays, uin
     if (ni)
         return tiled_ray(s, ni, h, w, TRAIN_TILE, TRAIN_TILE);
     return s < num_rays ? s : NONE;
-}
-
-// Zero this wave's slice before first use (all lanes of the wave, before any
-// lane leaves the kernel).
-__device__ __forceinline__ void agg_clear(float *agg, int n)
-{
-    for (int k = threadIdx.x & 63; k < n; k += 64)
-        agg[k] = 0.0f;
-    wave_lds_sync();
 }
 
 // ---------------------------------------------------------------------------
@@ -186,34 +154,35 @@ template <typename A, int RD, int RS> struct FwdIntegrator {
     uint32_t *qidx;
     f3 acc;
     float T, W, S, D, self, tfar;
-    float *agg; // this wave's LDS slot (one float)
 
-    // contribution[cell] += w, same-cell lanes of the wave combined first
+    // contribution[cell] += w.  The lanes of one cell are summed first, in
+    // lane order, for the group's lowest lane (v_readlane over the members:
+    // scalar work, no LDS), and the groups' sums then leave in one atomic
+    // instruction.
     __device__ __forceinline__ void scatter_contribution(uint32_t cell, float w)
     {
-        bool pending = true, direct = false;
-        for (int round = 0; round < AGG_ROUNDS; ++round) {
-            AggRound g;
-            if (!agg_round(cell, pending, g))
-                break;
-            if (g.comb) {
-                if (g.mine)
-                    atomicAdd(agg, w);
-                wave_lds_sync();
-                if (lane_rank(__ballot(1)) == 0) {
-                    float x = *agg;
-                    *agg = 0.0f;
-                    Attr<A>::add(contribution, g.lead, x);
-                }
-                wave_lds_sync();
-            } else if (g.mine) {
-                direct = true;
+        const int lane = (int)(threadIdx.x & 63u);
+        uint64_t pend = __ballot(1);
+        float mine = 0.0f;
+        bool leader = false;
+        while (pend) {
+            const int ll = (int)__builtin_ctzll(pend);
+            const uint32_t lead = __builtin_amdgcn_readlane(cell, ll);
+            uint64_t m = __ballot(cell == lead) & pend;
+            pend &= ~m;
+            float sum = 0.0f;
+            do {
+                const int src = (int)__builtin_ctzll(m);
+                m &= m - 1;
+                sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), src));
+            } while (m);
+            if (lane == ll) {
+                mine = sum;
+                leader = true;
             }
-            if (g.mine)
-                pending = false;
         }
-        if (pending || direct)
-            Attr<A>::add(contribution, cell, w);
+        if (leader && mine != 0.0f) // weights are >= 0: a zero sum adds nothing
+            Attr<A>::add(contribution, cell, mine);
     }
 
     float pdens; // density of the current cell, loaded by begin_cell
@@ -267,15 +236,11 @@ template <typename A, int RD, int RS> struct FwdIntegrator {
 template <typename A, int RD, int RS, bool STATS>
 __global__ __launch_bounds__(TRAIN_BLOCK) __attribute__((amdgpu_waves_per_eu(6))) void fwd_kernel(FwdArgs a)
 {
-    __shared__ float agg_lds[TRAIN_WAVES];
-    float *agg = agg_lds + threadIdx.x / 64;
-    agg_clear(agg, 1);
     uint32_t r = train_ray(xcd_interleaved_block<TRAIN_XCD_CHUNK>() * blockDim.x + threadIdx.x, a.num_rays, a.num_images,
                            a.img_h, a.img_w);
     if (r == NONE)
         return;
     FwdIntegrator<A, RD, RS> it;
-    it.agg = agg;
     load_ray(a.rays, r, it.o, it.d);
     it.density = a.density;
     it.tex.diffuse = (const A *)a.diffuse;
