@@ -157,7 +157,7 @@ def main():
     _lib.load()
     dev = torch.device("cuda:0")
     if args.train_only:
-        print(json.dumps({"train_c2": train_c2(dev, log)}), flush=True)
+        print(json.dumps({"train_c2": train_c2(dev, log, random_batch=False)}), flush=True)
         return
     if args.c5_only:
         print(json.dumps({"train_c5": train_c5(dev, log, cpu=not args.no_cpu)}), flush=True)
@@ -581,7 +581,7 @@ def c1_forward(dev, log, cpu=False, K=20):
     return out
 
 
-def train_c2(dev, log, cpu=False):
+def train_c2(dev, log, cpu=False, random_batch=True):
     """Config-2 training step: TraceVoroTracing forward + backward (fp32), 262,144 sites, 800x600 rays.
     With ``cpu``, the oracle also runs one forward + backward on the same inputs (the CPU baseline of this
     config), checked against the GPU: forward bit for bit, gradients to 1e-3 of each tensor's scale."""
@@ -632,6 +632,8 @@ def train_c2(dev, log, cpu=False):
                        "textures, one 800x600 pinhole camera, upstream dL/dRGB ~ N(0,1), thr 0.001"}
     out["roofline_fwd"], out["roofline_bwd"] = train_rooflines(model, rays, sp, g, dev, log)
     out["f16_storage"] = train_f16_storage(model, rays, sp, g, dev, log)
+    if random_batch:  # left out of --train-only, whose traces average the C2 kernels
+        out["random_batch"] = train_random_batch(model, dev, log)
     out["full_step"] = train_step_c2(sc, dev, rays, sp, g, log)
     if cpu:
         out["cpu_baseline"] = train_c2_cpu(model, rays, sp, g, log)
@@ -718,6 +720,70 @@ def train_f16_storage(model, rays, sp, g, dev, log, R=10):
     log(f"C2 with f16 maps: forward entry {t_fwd:.3f} ms, backward entry {t_bwd:.3f} ms")
     return {"forward_ms": round(t_fwd, 3), "backward_ms": round(t_bwd, 3),
             "note": "f16 diffuse/specular storage, _C entries (prefetch included), HIP events over 10 calls"}
+
+
+def train_random_batch(model, dev, log, R=5, cams=32, W=800, H=600):
+    """The C2 scene trained on the batch the reference's default trainer draws (datasets.py:185-222 with
+    trainer.py:52): 480,000 random pixels of random images, here of 32 orbit cameras at 800x600.  Times the
+    _C entries in batch order (ray_perm=None) and in the default lane order (each entry sorts the batch with
+    vt_ray_order), and the model's forward + backward (one sort per step), HIP events over R calls."""
+    import numpy as np
+    import torch
+
+    from vorotracing_amd import _C, camera
+
+    n = W * H
+    rng = np.random.default_rng(5)
+    img = rng.integers(0, cams, n)
+    ys = rng.integers(0, H, n)
+    xs = rng.integers(0, W, n)
+    rays_np = np.empty((n, 6), np.float32)
+    start_np = np.empty(n, np.int32)
+    for k in range(cams):
+        sel = img == k
+        rk = camera.orbit_rays(k, W, H)
+        rays_np[sel] = rk[ys[sel], xs[sel]]
+        start_np[sel] = int(model.get_starting_point(torch.from_numpy(rk[:1, :1].copy()).to(dev)).view(torch.int32))
+    rays = torch.from_numpy(rays_np).to(dev)
+    sp = torch.from_numpy(start_np).to(dev).view(torch.uint32)
+    g = torch.from_numpy(rng.normal(size=(n, 4)).astype(np.float32)).to(dev)
+    g[:, 3] = 0
+    dens = model.activated_density().detach()
+    scn = (model.primal_points.detach(), model.att_diffuse.detach(), model.att_specular.detach(), dens,
+           model.point_adjacency, model.point_adjacency_offsets)
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(R):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / R
+
+    out = {"rays": n, "cameras": cams,
+           "workload": "C2 scene, 480,000 random pixels of 32 orbit cameras (800x600, radius 7), fp32, thr 0.001"}
+    for name, perm in (("batch_order", None), ("ray_order", "auto")):
+        fw = _C.trace_vorotracing_fwd(*scn, rays, sp, None, 0.001, 1024, False, ray_perm=perm)
+        t_fwd = timed(lambda: _C.trace_vorotracing_fwd(*scn, rays, sp, None, 0.001, 1024, False, ray_perm=perm))
+        t_bwd = timed(lambda: _C.trace_vorotracing_bwd(*scn, rays, sp, fw[0], g, None, None, None, None, 0.0, fw[5],
+                                                       None, fw[6], fw[7], fw[8], 0.001, 1024, ray_perm=perm))
+        out[name] = {"forward_ms": round(t_fwd, 3), "backward_ms": round(t_bwd, 3)}
+        log(f"C2 random batch, {name}: forward entry {t_fwd:.3f} ms, backward entry {t_bwd:.3f} ms")
+    out["order_ms"] = round(timed(lambda: _C.ray_order(rays, sp, scn[0].shape[0])), 3)
+
+    def step():
+        model.zero_grad(set_to_none=True)
+        rgba = model(rays, start_point=sp, weight_threshold=0.001)[0]
+        rgba.backward(g)
+
+    out["model_fwd_bwd_ms"] = round(timed(step), 3)
+    log(f"C2 random batch: vt_ray_order {out['order_ms']:.3f} ms; model forward + backward "
+        f"{out['model_fwd_bwd_ms']:.3f} ms/step (one order per step)")
+    return out
 
 
 def train_step_c2(sc, dev, rays, sp, g, log, K=10):

@@ -205,11 +205,16 @@ int vt_trace_infer_q8_camera(const float *points, const uint8_t *diffuse, const 
  *   size and each wave traces one 8x8 screen tile (neighbouring rays share
  *   cells, so same-cell gradient combining finds more partners); 0, 0 = ray
  *   order.  Outputs do not depend on it beyond the order of atomic adds.
+ *   ray_perm: u32 (num_rays) lane order or NULL (an extension, ABI version
+ *   5): lane t traces ray ray_perm[t], overriding image_h/image_w; it must
+ *   be a permutation of 0..num_rays-1 (an entry >= num_rays leaves its
+ *   lane idle).  vt_ray_order makes one for flat batches.
  */
 int vt_trace_fwd(int attr_dtype, const float *points, const void *diffuse, const void *specular, uint32_t diff_res,
                  uint32_t spec_res, const float *density, const uint32_t *adjacency, uint32_t adjacency_size,
                  const uint32_t *offsets, uint32_t num_points, const float *rays, uint32_t num_rays,
-                 uint32_t image_h, uint32_t image_w, const uint32_t *start_point, uint32_t num_quantiles, const float *depth_quantiles,
+                 uint32_t image_h, uint32_t image_w, const uint32_t *start_point, const uint32_t *ray_perm,
+                 uint32_t num_quantiles, const float *depth_quantiles,
                  float weight_threshold, uint32_t max_intersections, void *rgba, float *depth, uint32_t *depth_idx,
                  void *contribution, uint32_t *num_intersections, float *distortion, float *W_total,
                  float *S_total, float *t_far, uint16_t *adj_diff_workspace, vt_ray_stats *stats,
@@ -226,7 +231,7 @@ int vt_trace_fwd(int attr_dtype, const float *points, const void *diffuse, const
  *   Outputs (caller zero-initialises): points_grad f32 (num_points,3),
  *   diffuse_grad / specular_grad attr dtype, density_grad f32 (num_points),
  *   point_error attr dtype (num_points) or NULL.
- *   image_h, image_w: lane order, as for vt_trace_fwd.
+ *   image_h, image_w, ray_perm: lane order, as for vt_trace_fwd.
  *   cell_workspace: f32 (num_points, 4), 16-byte aligned, any contents (an
  *   extension, ABI version 4): the call accumulates each cell's point and
  *   density gradients there, in one 16-byte slot per cell, and adds the
@@ -237,13 +242,29 @@ int vt_trace_fwd(int attr_dtype, const float *points, const void *diffuse, const
 int vt_trace_bwd(int attr_dtype, const float *points, const void *diffuse, const void *specular, uint32_t diff_res,
                  uint32_t spec_res, const float *density, const uint32_t *adjacency, uint32_t adjacency_size,
                  const uint32_t *offsets, uint32_t num_points, const float *rays, uint32_t num_rays,
-                 uint32_t image_h, uint32_t image_w, const uint32_t *start_point, const void *rgba, const void *rgba_grad, uint32_t num_quantiles,
+                 uint32_t image_h, uint32_t image_w, const uint32_t *start_point, const uint32_t *ray_perm,
+                 const void *rgba, const void *rgba_grad, uint32_t num_quantiles,
                  const float *depth_quantiles, const uint32_t *depth_idx, const float *depth_grad,
                  const void *ray_error, float contribution_alpha_grad, const float *distortion,
                  const float *distortion_grad, const float *W_total, const float *S_total, const float *t_far,
                  float weight_threshold, uint32_t max_intersections, float *points_grad, void *diffuse_grad,
                  void *specular_grad, float *density_grad, void *point_error, uint16_t *adj_diff_workspace,
                  float *cell_workspace, vt_ray_stats *stats, vt_stream_t stream);
+
+/*
+ * Coherent lane order for a flat training batch (an extension: the reference
+ * traces rays in batch order, tracing_octmap.cu:175-179 and :264-268, and its default
+ * trainer batches random pixels of random images, datasets.py:185-222 with
+ * trainer.py:52).
+ *   ray_perm (num_rays) u32 out: the rays sorted by start cell, then by a
+ *   2-D Morton code of the direction's octahedral coordinates (a 256 x 256
+ *   grid), stable, so that a wave traces rays of one camera with neighbouring
+ *   directions.  Pass it as vt_trace_fwd / vt_trace_bwd's ray_perm.
+ *   workspace: vt_ray_order_workspace_size(num_rays) bytes, 4-byte aligned.
+ */
+size_t vt_ray_order_workspace_size(uint32_t num_rays);
+int vt_ray_order(const float *rays, const uint32_t *start_point, uint32_t num_rays, uint32_t num_points,
+                 uint32_t *ray_perm, void *workspace, vt_stream_t stream);
 
 /*
  * Start-cell lookup.  Replaces _C.NNBVH (nn_bvh.h:4-16, nn_bvh.cu:43-109):

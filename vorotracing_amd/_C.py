@@ -233,6 +233,68 @@ def _image_dims(rays):
     return 0, 0
 
 
+# Flat training batches of at least this many rays are traced in the
+# ray_order lane order by default; below it the sort's fixed cost (about
+# 0.2 ms) outweighs what coherent waves save.
+ORDER_MIN_RAYS = 1 << 16
+
+
+def ray_order(rays_in, start_point_in, num_points: int) -> torch.Tensor:
+    """(An extension.)  u32 (num_rays) lane order for a flat training batch:
+    the rays sorted by start cell, then by a Morton code of the direction
+    (vt_ray_order), so that each wave traces neighbouring rays of one camera.
+    The reference traces rays in batch order (tracing_octmap.cu:175-179) and
+    its default trainer batches random pixels of random images
+    (datasets.py:185-222); pass the result as ``ray_perm``."""
+    rays = rays_in.contiguous()
+    start_point = start_point_in.contiguous()
+    num_rays = rays.numel() // 6
+    _assert(rays.size(-1) == 6 and rays.dtype == torch.float32 and _is_gpu(rays),
+            "rays must be a float32 (..., 6) CUDA tensor")
+    _assert(start_point.dtype == torch.uint32 and start_point.numel() == num_rays and _is_gpu(start_point),
+            "start_point must be a uint32 CUDA tensor with one entry per ray")
+    perm = torch.empty(num_rays, dtype=torch.uint32, device=rays.device)
+    if num_rays == 0:
+        return perm
+    ws = torch.empty(int(_lib.load().vt_ray_order_workspace_size(num_rays)), dtype=torch.uint8, device=rays.device)
+    with torch.cuda.device(rays.device):
+        _lib.call("vt_ray_order", rays.data_ptr(), start_point.data_ptr(), num_rays, int(num_points), perm.data_ptr(),
+                  ws.data_ptr(), _stream(rays.device))
+    return perm
+
+
+def default_ray_perm(rays, start_point, num_points: int) -> Optional[torch.Tensor]:
+    """The lane order ``ray_perm="auto"`` picks: ray_order for a flat batch of
+    at least ORDER_MIN_RAYS rays, else None (image-shaped rays are traced in
+    8x8 screen tiles, small flat batches in batch order)."""
+    num_rays = rays.numel() // 6
+    if num_rays < ORDER_MIN_RAYS or _image_dims(rays) != (0, 0):
+        return None
+    if not (rays.size(-1) == 6 and rays.dtype == torch.float32 and _is_gpu(rays)
+            and start_point.dtype == torch.uint32 and start_point.numel() == num_rays and _is_gpu(start_point)):
+        return None  # the entry's own checks report these with the reference's messages
+    return ray_order(rays, start_point, num_points)
+
+
+def _lane_order(rays, start_point, num_points: int, ray_perm):
+    """(image_h, image_w, perm tensor or None) for the training entries."""
+    num_rays = rays.numel() // 6
+    if isinstance(ray_perm, torch.Tensor):
+        perm = _u32_view(ray_perm.contiguous())
+        _assert(perm.dtype == torch.uint32 and perm.numel() == num_rays and perm.device == rays.device,
+                "ray_perm must be a uint32 or int32 tensor with one entry per ray, on the rays' device")
+        return 0, 0, perm
+    if ray_perm is None:
+        h, w = _image_dims(rays)
+        return h, w, None
+    _assert(isinstance(ray_perm, str) and ray_perm == "auto", "ray_perm must be 'auto', None or a tensor")
+    perm = default_ray_perm(rays, start_point, num_points)
+    if perm is not None:
+        return 0, 0, perm
+    h, w = _image_dims(rays)
+    return h, w, None
+
+
 def _attr_code(dtype):
     if dtype == torch.float32:
         return 0
@@ -244,12 +306,15 @@ def _attr_code(dtype):
 def trace_vorotracing_fwd(points_in, diffuse_in, specular_in, density_in, point_adjacency_in,
                           point_adjacency_offsets_in, rays_in, start_point_in, depth_quantiles_in,
                           weight_threshold: float, max_intersections: int, return_contribution: bool,
-                          stats: Optional[torch.Tensor] = None):
+                          stats: Optional[torch.Tensor] = None, ray_perm: Union[str, torch.Tensor, None] = "auto"):
     """tracing_octmap.cu:346-546.  Returns (rgba, depth, depth_idx,
     contribution, n, distortion, W_total, S_total, t_far); absent outputs are
-    None.  ``stats`` (an extension): None, or a u32 (num_rays,
+    None.  Extensions: ``stats``, None or a u32 (num_rays,
     native.STATS_WORDS) tensor that receives the per-ray walk statistics
-    (vt_ray_stats)."""
+    (vt_ray_stats); ``ray_perm``, the lane order: "auto" (default_ray_perm),
+    None (screen tiles for image-shaped rays, else batch order) or a
+    permutation of the rays (ray_order).  Outputs stay indexed by ray; the
+    lane order changes only the order of atomic additions."""
     points = points_in.contiguous()
     diffuse = diffuse_in.contiguous()
     specular = specular_in.contiguous()
@@ -290,10 +355,11 @@ def trace_vorotracing_fwd(points_in, diffuse_in, specular_in, density_in, point_
     S_total = torch.empty(f1, dtype=torch.float32, device=dev)
     t_far = torch.empty(f1, dtype=torch.float32, device=dev)
     workspace = torch.empty((adjacency_size + 32, 4), dtype=torch.float16, device=dev)
+    img_h, img_w, perm = _lane_order(rays, start_point, num_points, ray_perm)
     with torch.cuda.device(dev):
         _lib.call("vt_trace_fwd", code, points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd, rs,
                   density.data_ptr(), adjacency.data_ptr(), adjacency_size, offsets.data_ptr(), num_points,
-                  rays.data_ptr(), num_rays, *_image_dims(rays), start_point.data_ptr(), K, _ptr(depth_quantiles),
+                  rays.data_ptr(), num_rays, img_h, img_w, start_point.data_ptr(), _ptr(perm), K, _ptr(depth_quantiles),
                   float(weight_threshold), int(max_intersections), rgba.data_ptr(), _ptr(depth), _ptr(depth_idx),
                   _ptr(contribution), n.data_ptr(), distortion.data_ptr(), W_total.data_ptr(), S_total.data_ptr(),
                   t_far.data_ptr(), workspace.data_ptr(), _stats_ptr(stats, num_rays), _stream(dev))
@@ -314,11 +380,11 @@ def trace_vorotracing_bwd(points_in, diffuse_in, specular_in, density_in, point_
                           depth_quantiles_in, depth_indices_in, depth_grad_in, ray_error_in,
                           contribution_alpha_grad: float, distortion_in, distortion_grad_in, W_total_in, S_total_in,
                           t_far_in, weight_threshold: float, max_intersections: int,
-                          stats: Optional[torch.Tensor] = None):
+                          stats: Optional[torch.Tensor] = None, ray_perm: Union[str, torch.Tensor, None] = "auto"):
     """tracing_octmap.cu:860-1103.  Returns (points_grad, diffuse_grad,
     specular_grad, density_grad, ray_grad, point_error).  ray_grad is zeros
     (the reference returns it uninitialised and the autograd wrapper drops
-    it).  ``stats`` as for trace_vorotracing_fwd (an extension)."""
+    it).  ``stats`` and ``ray_perm`` as for trace_vorotracing_fwd (extensions)."""
     points = points_in.contiguous()
     diffuse = diffuse_in.contiguous()
     specular = specular_in.contiguous()
@@ -397,10 +463,11 @@ def trace_vorotracing_bwd(points_in, diffuse_in, specular_in, density_in, point_
     ray_grad = torch.zeros_like(rays)
     workspace = torch.empty((adjacency_size + 32, 4), dtype=torch.float16, device=dev)
     cell_workspace = torch.empty((num_points, 4), dtype=torch.float32, device=dev)
+    img_h, img_w, perm = _lane_order(rays, start_point, num_points, ray_perm)
     with torch.cuda.device(dev):
         _lib.call("vt_trace_bwd", code, points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd, rs,
                   density.data_ptr(), adjacency.data_ptr(), adjacency_size, offsets.data_ptr(), num_points,
-                  rays.data_ptr(), num_rays, *_image_dims(rays), start_point.data_ptr(), rgb_out.data_ptr(),
+                  rays.data_ptr(), num_rays, img_h, img_w, start_point.data_ptr(), _ptr(perm), rgb_out.data_ptr(),
                   rgb_grad.data_ptr(), K,
                   _ptr(depth_quantiles), _ptr(depth_indices), _ptr(depth_grad), _ptr(ray_error),
                   float(contribution_alpha_grad), distortion.data_ptr(), _ptr(distortion_grad),

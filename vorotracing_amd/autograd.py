@@ -61,6 +61,7 @@ class TraceRecord:
     distortion: torch.Tensor
     totals: Tuple[torch.Tensor, torch.Tensor, torch.Tensor]  # W_total, S_total, t_far
     box: ErrorBox
+    perm: Optional[torch.Tensor] = None  # lane order of the forward, reused by the backward
 
 
 @dataclasses.dataclass
@@ -78,11 +79,12 @@ def run_forward(scene, rays, start, quantiles, weight_threshold: float, max_inte
     """One _C.trace_vorotracing_fwd; returns the six autograd outputs
     (rgba, depth, contribution, n, error box, distortion, as
     _wrapper.py:87) and the record a backward needs."""
+    perm = _C.default_ray_perm(rays, start, scene[0].shape[0])
     rgba, depth, depth_idx, contribution, n, distortion, w_tot, s_tot, t_far = _C.trace_vorotracing_fwd(
-        *scene, rays, start, quantiles, weight_threshold, max_intersections, want_contribution)
+        *scene, rays, start, quantiles, weight_threshold, max_intersections, want_contribution, ray_perm=perm)
     box = ErrorBox()
     rec = TraceRecord(tuple(scene), rays, start, quantiles, float(weight_threshold), int(max_intersections), rgba,
-                      depth_idx, distortion, (w_tot, s_tot, t_far), box)
+                      depth_idx, distortion, (w_tot, s_tot, t_far), box, perm)
     return (rgba, depth, contribution, n, box, distortion), rec
 
 
@@ -111,7 +113,7 @@ def _launch(rec: TraceRecord, up: Upstream):
     w_tot, s_tot, t_far = rec.totals
     return _C.trace_vorotracing_bwd(*rec.scene, rec.rays, rec.start, rec.rgba, up.rgba, rec.quantiles, rec.depth_idx,
                                     up.depth, up.ray_error, up.alpha_scalar, rec.distortion, up.distortion, w_tot,
-                                    s_tot, t_far, rec.weight_threshold, rec.max_intersections)
+                                    s_tot, t_far, rec.weight_threshold, rec.max_intersections, ray_perm=rec.perm)
 
 
 def scene_gradients(rec: TraceRecord, up: Upstream):

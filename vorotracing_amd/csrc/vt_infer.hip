@@ -264,14 +264,18 @@ struct InferArgs {
 constexpr int MAP_LINEAR = 0, MAP_TILED = 1, MAP_CAMERA = 2;
 
 // Lane s of a launch renders ray slot_to_ray(s): tiled, tile s/64 lane s%64
-// of the image batch; linear, ray s or ray_perm[s].
+// of the image batch; linear, ray s or ray_perm[s] (idle when that is not a
+// ray index).
 __device__ __forceinline__ uint32_t slot_to_ray(const InferArgs &a, uint32_t s, int map)
 {
     if (map == MAP_TILED || map == MAP_CAMERA)
         return tiled_ray(s, a.num_images, a.H, a.W, a.th, a.tw);
     if (s >= a.num_rays)
         return NONE;
-    return a.ray_perm ? a.ray_perm[s] : s;
+    if (!a.ray_perm)
+        return s;
+    const uint32_t r = a.ray_perm[s];
+    return r < a.num_rays ? r : NONE;
 }
 
 

@@ -137,6 +137,70 @@ __global__ void tile_perm_kernel(uint32_t H, uint32_t W, uint32_t TH, uint32_t T
     perm[rank] = (int32_t)p;
 }
 
+// --- coherent lane order for flat ray batches --------------------------------
+
+// Direction bits per octahedral axis of the order key: a 256 x 256 grid over
+// the sphere, cells of about 0.7 degrees.
+#ifndef VT_ORDER_DIR_BITS
+#define VT_ORDER_DIR_BITS 8
+#endif
+constexpr int ORDER_DIR_BITS = VT_ORDER_DIR_BITS;
+
+__device__ __forceinline__ uint32_t spread_bits(uint32_t x) // bit i -> bit 2i (x < 2^16)
+{
+    x &= 0xffffu;
+    x = (x | (x << 8)) & 0x00ff00ffu;
+    x = (x | (x << 4)) & 0x0f0f0f0fu;
+    x = (x | (x << 2)) & 0x33333333u;
+    x = (x | (x << 1)) & 0x55555555u;
+    return x;
+}
+
+// 2-D Morton code of the ray direction's octahedral coordinates: nearby
+// directions get nearby keys.  A NaN coordinate clamps to cell 0.
+__device__ __forceinline__ uint32_t direction_key(const float *__restrict__ rays, uint32_t i)
+{
+    const float dx = rays[6 * (size_t)i + 3], dy = rays[6 * (size_t)i + 4], dz = rays[6 * (size_t)i + 5];
+    const float l1 = __builtin_fmaxf(__builtin_fabsf(dx) + __builtin_fabsf(dy) + __builtin_fabsf(dz), 1e-30f);
+    float u = dx / l1, v = dy / l1;
+    if (dz < 0.0f) {
+        const float ou = (1.0f - __builtin_fabsf(v)) * __builtin_copysignf(1.0f, u);
+        const float ov = (1.0f - __builtin_fabsf(u)) * __builtin_copysignf(1.0f, v);
+        u = ou;
+        v = ov;
+    }
+    constexpr float cells = (float)(1u << ORDER_DIR_BITS);
+    const float top = cells - 1.0f;
+    const uint32_t qu = (uint32_t)__builtin_fminf(__builtin_fmaxf((u * 0.5f + 0.5f) * cells, 0.0f), top);
+    const uint32_t qv = (uint32_t)__builtin_fminf(__builtin_fmaxf((v * 0.5f + 0.5f) * cells, 0.0f), top);
+    return spread_bits(qu) | (spread_bits(qv) << 1);
+}
+
+// keys[i] = (start cell << 2*ORDER_DIR_BITS) | direction key when both fit
+// one word (cell_shift > 0), else the direction key alone; vals[i] = i.
+__global__ void ray_order_keys_kernel(const float *__restrict__ rays, const uint32_t *__restrict__ start_point,
+                                      uint32_t n, int cell_shift, uint32_t *__restrict__ keys,
+                                      uint32_t *__restrict__ vals)
+{
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n)
+        return;
+    uint32_t k = direction_key(rays, i);
+    if (cell_shift)
+        k |= start_point[i] << cell_shift;
+    keys[i] = k;
+    vals[i] = i;
+}
+
+// keys[j] = start cell of ray vals[j] (the second, stable pass of a two-pass order)
+__global__ void ray_order_cells_kernel(const uint32_t *__restrict__ start_point, const uint32_t *__restrict__ vals,
+                                       uint32_t n, uint32_t *__restrict__ keys)
+{
+    const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j < n)
+        keys[j] = start_point[vals[j]];
+}
+
 // --- q8 quantisation ---------------------------------------------------------
 
 // ws[0..2] min, ws[3..5] max (ordered ints), per channel or all in channel 0
@@ -325,6 +389,42 @@ extern "C" int vt_tile_perm(uint32_t height, uint32_t width, uint32_t tile_h, ui
     tile_perm_kernel<<<(n + 255) / 256, 256, 0, as_stream(stream)>>>(height, width, tile_h, tile_w, perm);
     VT_LAUNCH_CHECK("tile_perm_kernel");
     return VT_OK;
+}
+
+extern "C" size_t vt_ray_order_workspace_size(uint32_t num_rays)
+{
+    return ((size_t)num_rays + radix_sort_workspace_words(num_rays)) * 4;
+}
+
+extern "C" int vt_ray_order(const float *rays, const uint32_t *start_point, uint32_t num_rays, uint32_t num_points,
+                            uint32_t *ray_perm, void *workspace, vt_stream_t stream)
+{
+    clear_error();
+    if (num_rays == 0)
+        return VT_OK;
+    VT_REQUIRE(rays && start_point && ray_perm && workspace, "null pointer argument");
+    VT_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 4 == 0, "workspace must be 4-byte aligned");
+    hipStream_t s = as_stream(stream);
+    uint32_t *keys = static_cast<uint32_t *>(workspace);
+    uint32_t *sws = keys + num_rays;
+    const int dir_bits = 2 * ORDER_DIR_BITS;
+    const int cell_bits = num_points > 1 ? 32 - __builtin_clz(num_points - 1) : 0;
+    const uint32_t blocks = (num_rays + 255) / 256;
+    if (cell_bits + dir_bits <= 32) {
+        ray_order_keys_kernel<<<blocks, 256, 0, s>>>(rays, start_point, num_rays, cell_bits ? dir_bits : 0, keys,
+                                                     ray_perm);
+        VT_LAUNCH_CHECK("ray_order_keys_kernel");
+        return radix_sort_pairs(keys, ray_perm, num_rays, cell_bits + dir_bits, sws, s);
+    }
+    // Direction first, then a stable sort by start cell: cell-major order.
+    ray_order_keys_kernel<<<blocks, 256, 0, s>>>(rays, start_point, num_rays, 0, keys, ray_perm);
+    VT_LAUNCH_CHECK("ray_order_keys_kernel");
+    int rc = radix_sort_pairs(keys, ray_perm, num_rays, dir_bits, sws, s);
+    if (rc)
+        return rc;
+    ray_order_cells_kernel<<<blocks, 256, 0, s>>>(start_point, ray_perm, num_rays, keys);
+    VT_LAUNCH_CHECK("ray_order_cells_kernel");
+    return radix_sort_pairs(keys, ray_perm, num_rays, cell_bits, sws, s);
 }
 
 extern "C" size_t vt_quantize_workspace_size(void) { return 64; }

@@ -103,11 +103,20 @@ constexpr int REC_DTAPS = 29, REC_STAPS = 30;
 constexpr int ROW_STRIDE = 36;
 constexpr int ROW_TABLE_FLOATS = 65 * ROW_STRIDE;
 
-// Ray of lane slot s: 8x8 screen tiles of row-major images, or ray order.
+// Ray of lane slot s: perm[s] when a lane order is given (entries past
+// num_rays leave the lane idle), else 8x8 screen tiles of row-major images,
+// or ray order.
 constexpr uint32_t TRAIN_TILE = 8;
 
-__device__ __forceinline__ uint32_t train_ray(uint32_t s, uint32_t num_rays, uint32_t ni, uint32_t h, uint32_t w)
+__device__ __forceinline__ uint32_t train_ray(uint32_t s, uint32_t num_rays, const uint32_t *perm, uint32_t ni,
+                                              uint32_t h, uint32_t w)
 {
+    if (perm) {
+        if (s >= num_rays)
+            return NONE;
+        const uint32_t r = perm[s];
+        return r < num_rays ? r : NONE;
+    }
     if (ni)
         return tiled_ray(s, ni, h, w, TRAIN_TILE, TRAIN_TILE);
     return s < num_rays ? s : NONE;
@@ -124,7 +133,8 @@ struct FwdArgs {
     const uint2 *adj_diff;
     const float *rays;
     uint32_t num_rays;
-    uint32_t num_images, img_h, img_w; // tiled lane order when num_images > 0
+    const uint32_t *ray_perm;          // lane order, or null
+    uint32_t num_images, img_h, img_w; // tiled lane order when num_images > 0 and no ray_perm
     const uint32_t *start_point;
     uint32_t K;
     const float *quantiles;
@@ -236,8 +246,8 @@ template <typename A, int RD, int RS> struct FwdIntegrator {
 template <typename A, int RD, int RS, bool STATS>
 __global__ __launch_bounds__(TRAIN_BLOCK) __attribute__((amdgpu_waves_per_eu(6))) void fwd_kernel(FwdArgs a)
 {
-    uint32_t r = train_ray(xcd_interleaved_block<TRAIN_XCD_CHUNK>() * blockDim.x + threadIdx.x, a.num_rays, a.num_images,
-                           a.img_h, a.img_w);
+    uint32_t r = train_ray(xcd_interleaved_block<TRAIN_XCD_CHUNK>() * blockDim.x + threadIdx.x, a.num_rays, a.ray_perm,
+                           a.num_images, a.img_h, a.img_w);
     if (r == NONE)
         return;
     FwdIntegrator<A, RD, RS> it;
@@ -293,7 +303,8 @@ struct BwdArgs {
     const uint2 *adj_diff;
     const float *rays;
     uint32_t num_rays;
-    uint32_t num_images, img_h, img_w; // tiled lane order when num_images > 0
+    const uint32_t *ray_perm;          // lane order, or null
+    uint32_t num_images, img_h, img_w; // tiled lane order when num_images > 0 and no ray_perm
     const uint32_t *start_point;
     const void *rgba, *rgba_grad;
     uint32_t K;
@@ -713,8 +724,8 @@ __global__ __launch_bounds__(TRAIN_BLOCK) __attribute__((amdgpu_waves_per_eu(4))
     if ((threadIdx.x & 63u) < (uint32_t)ROW_STRIDE)
         rows[64 * ROW_STRIDE + (threadIdx.x & 63u)] = 0.0f; // the zero row
     wave_lds_sync();
-    uint32_t r = train_ray(xcd_interleaved_block<TRAIN_XCD_CHUNK>() * blockDim.x + threadIdx.x, a.num_rays, a.num_images,
-                           a.img_h, a.img_w);
+    uint32_t r = train_ray(xcd_interleaved_block<TRAIN_XCD_CHUNK>() * blockDim.x + threadIdx.x, a.num_rays, a.ray_perm,
+                           a.num_images, a.img_h, a.img_w);
     if (r == NONE)
         return;
     BwdIntegrator<A, RD, RS> it;
@@ -784,12 +795,14 @@ __global__ __launch_bounds__(TRAIN_BLOCK) __attribute__((amdgpu_waves_per_eu(4))
 int prefetch(const float *points, uint32_t num_points, const uint32_t *adjacency, uint32_t adjacency_size,
              const uint32_t *offsets, uint16_t *adj_diff, hipStream_t stream);
 
-template <typename Args> static void set_image_order(Args &a, uint32_t num_rays, uint32_t h, uint32_t w)
+template <typename Args>
+static void set_lane_order(Args &a, uint32_t num_rays, const uint32_t *ray_perm, uint32_t h, uint32_t w)
 {
+    a.ray_perm = ray_perm;
     a.num_images = 0;
     a.img_h = a.img_w = 0;
     uint64_t px = (uint64_t)h * w;
-    if (h && w && num_rays % px == 0) {
+    if (!ray_perm && h && w && num_rays % px == 0) {
         a.num_images = (uint32_t)(num_rays / px);
         a.img_h = h;
         a.img_w = w;
@@ -855,7 +868,7 @@ extern "C" int vt_trace_fwd(int attr_dtype, const float *points, const void *dif
                             uint32_t diff_res, uint32_t spec_res, const float *density, const uint32_t *adjacency,
                             uint32_t adjacency_size, const uint32_t *offsets, uint32_t num_points, const float *rays,
                             uint32_t num_rays, uint32_t image_h, uint32_t image_w,
-                            const uint32_t *start_point, uint32_t num_quantiles,
+                            const uint32_t *start_point, const uint32_t *ray_perm, uint32_t num_quantiles,
                             const float *depth_quantiles, float weight_threshold, uint32_t max_intersections,
                             void *rgba, float *depth, uint32_t *depth_idx, void *contribution,
                             uint32_t *num_intersections, float *distortion, float *W_total, float *S_total,
@@ -883,7 +896,7 @@ extern "C" int vt_trace_fwd(int attr_dtype, const float *points, const void *dif
     a.adj_diff = reinterpret_cast<const uint2 *>(adj_diff_workspace);
     a.rays = rays;
     a.num_rays = num_rays;
-    set_image_order(a, num_rays, image_h, image_w);
+    set_lane_order(a, num_rays, ray_perm, image_h, image_w);
     a.start_point = start_point;
     a.K = depth_quantiles ? num_quantiles : 0;
     a.quantiles = (depth_quantiles && num_quantiles) ? depth_quantiles : nullptr;
@@ -930,7 +943,8 @@ extern "C" int vt_trace_bwd(int attr_dtype, const float *points, const void *dif
                             uint32_t diff_res, uint32_t spec_res, const float *density, const uint32_t *adjacency,
                             uint32_t adjacency_size, const uint32_t *offsets, uint32_t num_points, const float *rays,
                             uint32_t num_rays, uint32_t image_h, uint32_t image_w,
-                            const uint32_t *start_point, const void *rgba, const void *rgba_grad,
+                            const uint32_t *start_point, const uint32_t *ray_perm, const void *rgba,
+                            const void *rgba_grad,
                             uint32_t num_quantiles, const float *depth_quantiles, const uint32_t *depth_idx,
                             const float *depth_grad, const void *ray_error, float contribution_alpha_grad,
                             const float *distortion, const float *distortion_grad, const float *W_total,
@@ -965,7 +979,7 @@ extern "C" int vt_trace_bwd(int attr_dtype, const float *points, const void *dif
     a.adj_diff = reinterpret_cast<const uint2 *>(adj_diff_workspace);
     a.rays = rays;
     a.num_rays = num_rays;
-    set_image_order(a, num_rays, image_h, image_w);
+    set_lane_order(a, num_rays, ray_perm, image_h, image_w);
     a.start_point = start_point;
     a.rgba = rgba;
     a.rgba_grad = rgba_grad;
