@@ -527,21 +527,30 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
 
     // The combining passes of one scatter; ONE: every column has its own
     // lane (at least REC_COLS lanes scatter), so the column is set up once;
-    // otherwise a lane takes several columns.
+    // otherwise a lane takes several columns.  With at least 2 * REC_COLS
+    // lanes, groups of a single lane are set aside and sent two per pass
+    // afterwards: lanes of rank k < REC_COLS send column k of the first,
+    // lanes of rank REC_COLS + k column k of the second.
     template <bool ONE>
     __device__ __forceinline__ void combine(uint32_t cell, uint64_t act, uint32_t nact, uint32_t arank, uint32_t lane)
     {
+        const bool pair = ONE && nact >= 2u * (uint32_t)REC_COLS;
+        const uint32_t half = arank >= (uint32_t)REC_COLS ? 1u : 0u;
         Column c1;
         if (ONE)
-            c1 = column(arank);
-        uint64_t pend = act;
+            c1 = column(arank - half * (uint32_t)REC_COLS);
+        uint64_t pend = act, singles = 0;
         while (pend) { // one group per pass, at most 64
             const int ll = (int)__builtin_ctzll(pend);
             const uint32_t lead = __builtin_amdgcn_readlane(cell, ll);
-            const uint32_t ldt = __builtin_amdgcn_readlane(held_taps, ll);
-            const uint32_t lst = __builtin_amdgcn_readlane(spec_taps, ll);
             const uint64_t mem = __ballot(cell == lead) & pend;
             pend &= ~mem;
+            if (pair && (mem & (mem - 1)) == 0) {
+                singles |= mem;
+                continue;
+            }
+            const uint32_t ldt = __builtin_amdgcn_readlane(held_taps, ll);
+            const uint32_t lst = __builtin_amdgcn_readlane(spec_taps, ll);
             // do all members share the leader's taps? (the usual case)
             const bool uniform =
                 (mem & (mem - 1)) == 0 || __ballot(((mem >> lane) & 1u) && (held_taps != ldt || spec_taps != lst)) == 0;
@@ -555,6 +564,22 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
                     column_send(c, lead, t0, acc);
                 if (acc1 != 0.0f)
                     column_send(c, lead, t1, acc1);
+            }
+        }
+        while (singles) { // (pair only) two lone lanes per pass
+            const int la = (int)__builtin_ctzll(singles);
+            singles &= singles - 1;
+            const int lb = singles ? (int)__builtin_ctzll(singles) : 64;
+            singles &= singles - 1;
+            const uint32_t ca = __builtin_amdgcn_readlane(cell, la), cb = __builtin_amdgcn_readlane(cell, lb & 63);
+            const uint32_t da = __builtin_amdgcn_readlane(held_taps, la), db = __builtin_amdgcn_readlane(held_taps, lb & 63);
+            const uint32_t sa = __builtin_amdgcn_readlane(spec_taps, la), sb = __builtin_amdgcn_readlane(spec_taps, lb & 63);
+            const int mine = half ? lb : la;
+            if (arank < 2u * (uint32_t)REC_COLS && mine < 64) {
+                const float x = rows[mine * ROW_STRIDE + (c1.k)];
+                const uint32_t t = (((c1.diffuse_taps ? (half ? db : da) : (half ? sb : sa))) >> c1.sh) & c1.tmask;
+                if (x != 0.0f)
+                    column_send(c1, half ? cb : ca, t, x);
             }
         }
     }
