@@ -163,3 +163,48 @@ def test_default_order_choice(gpu):
         _C.trace_vorotracing_fwd(*[H.to_dev(a, gpu) for a in (s.points, s.diffuse, s.specular, s.density,
                                                               s.adjacency, s.offsets)],
                                  flat, start.reshape(-1), None, 0.001, 1024, False, ray_perm=perm[:10])
+
+
+def _aa_rays(w, h, eye):
+    """Five rays per pixel, shaped (H, W, 5, 6) as the reference's full
+    antialiasing makes them: the pixel's ray and four perturbed directions."""
+    base = camera.pinhole_rays(w, h, eye=eye)
+    r = np.repeat(base[:, :, None, :], 5, axis=2)
+    r[:, :, 1:, 3:] += np.random.default_rng(4).normal(scale=2e-3, size=(h, w, 4, 3)).astype(np.float32)
+    return np.ascontiguousarray(r, np.float32)
+
+
+def test_antialiased_ray_shapes_equal_flat(gpu):
+    """(H, W, 5, 6) rays are traced as H x 5W images, in training and in
+    inference; every per-ray output equals the flat batch's in batch order,
+    bit for bit."""
+    from vorotracing_amd.infer import VoroTracingInfer
+    from vorotracing_amd.model import VoroTracing
+
+    s = H.small_random(1500, seed=5, R=8, Rs=4)
+    rays = _aa_rays(48, 40, (0.3, -3.2, 0.4))
+    assert _C._image_dims(torch.from_numpy(rays)) == (40, 240)
+    start = H.start_for(s, rays)
+    dev = lambda a: H.to_dev(a, gpu)  # noqa: E731
+    scene = (dev(s.points), dev(s.diffuse), dev(s.specular), dev(s.density), dev(s.adjacency), dev(s.offsets))
+    img = _C.trace_vorotracing_fwd(*scene, dev(rays), dev(start), None, 0.001, 1024, False)
+    flat = _C.trace_vorotracing_fwd(*scene, dev(rays.reshape(-1, 6)), dev(start.reshape(-1)), None, 0.001, 1024,
+                                    False, ray_perm=None)
+    torch.cuda.synchronize()
+    compared = 0
+    for a, b in zip(img, flat):
+        if a is None:
+            assert b is None
+            continue
+        assert torch.equal(a.reshape(-1).view(torch.int32), b.reshape(-1).view(torch.int32))
+        compared += 1
+    assert compared == 6  # rgba, n, distortion, W_total, S_total, t_far
+
+    inf = VoroTracingInfer(VoroTracing.from_scene(s, device=gpu), sort_morton=True, quantize="fp16")
+    r = dev(rays)
+    got = inf.render(r, weight_threshold=0.001, cell_skip_threshold=1e-3)
+    want = inf.render(r.reshape(-1, 6), weight_threshold=0.001, cell_skip_threshold=1e-3)
+    torch.cuda.synchronize()
+    assert tuple(got.shape) == (40, 48, 5, 4)
+    assert torch.equal(got.reshape(-1, 4).view(torch.int16), want.view(torch.int16))
+    assert (got[..., 3] > 0).any()

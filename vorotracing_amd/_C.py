@@ -226,11 +226,11 @@ def _check_train_common(points, diffuse, specular, density, rays, start_point, n
 
 
 def _image_dims(rays):
-    """(H, W) of image-shaped rays [..., H, W, 6] for the tiled lane order of
-    the training kernels; (0, 0) for flat ray batches."""
-    if rays.dim() >= 3 and rays.shape[-3] > 1 and rays.shape[-2] > 1:
-        return int(rays.shape[-3]), int(rays.shape[-2])
-    return 0, 0
+    """(H, W) of the images in the rays' leading shape (native.screen_layout)
+    for the tiled lane order of the training kernels; (0, 0) for a flat
+    batch."""
+    lay = native.screen_layout(rays.shape[:-1])
+    return (0, 0) if lay is None else (lay[1], lay[2])
 
 
 # Flat training batches of at least this many rays are traced in the

@@ -240,7 +240,7 @@ class VoroTracingInfer:
             start_point = self.get_starting_point(rays)
         else:
             start_point = torch.broadcast_to(start_point, rays.shape[:-1]).contiguous()
-        image = use_warp_perm and rays.ndim in (3, 4) and rays.shape[-1] == 6
+        image = use_warp_perm and rays.shape[-1] == 6 and native.screen_layout(rays.shape[:-1]) is not None
         if self.quantize == "q8":
             if not image and stats is None:
                 return ops.trace_octmap_infer_q8(
@@ -336,8 +336,7 @@ class VoroTracingInfer:
         rs = native.map_res(self.specular_q8.shape[-1], 3)
         sp = native._s(rays.device)
         if image:
-            shp = rays.shape[:-1]
-            B, H, W = (1, shp[0], shp[1]) if len(shp) == 2 else (shp[0], shp[1], shp[2])
+            B, H, W = native.image_dims(rays)
             _lib.call("vt_trace_infer_q8_tiled", self.primal_points.data_ptr(), self.diffuse_q8.data_ptr(),
                       self.specular_q8.data_ptr(), rd, rs, *keep, self.density.data_ptr(),
                       self.point_adjacency.data_ptr(), self.point_adjacency_offsets.data_ptr(),

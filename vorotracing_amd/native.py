@@ -7,13 +7,34 @@ callers pass contiguous device tensors of the documented dtypes.
 from __future__ import annotations
 
 import ctypes as C
-from typing import Optional
+import math
+from typing import Optional, Tuple
 
 import torch
 
 from . import _lib
 
 STATS_WORDS = 32  # vt_ray_stats: 8 counter words and the first 24 visited cells
+
+# Side of the 8x8 wave tiles: leading ray dimensions with at least this many
+# rows and columns are traced as images.
+IMAGE_MIN = 8
+
+
+def screen_layout(lead) -> Optional[Tuple[int, int, int]]:
+    """(images, rows, columns) of rays whose leading shape ``lead`` holds
+    images for the wave tiling, or None for a flat batch.  (..., H, W) with
+    H, W >= IMAGE_MIN is a batch of H x W images; (..., H, W, S) with
+    S < IMAGE_MIN rays per pixel (the reference's full antialiasing, five per
+    pixel, datasets.py:159-176) is a batch of H x (W*S) images, a pixel's rays
+    side by side."""
+    lead = tuple(int(x) for x in lead)
+    n = len(lead)
+    if n >= 2 and lead[-2] >= IMAGE_MIN and lead[-1] >= IMAGE_MIN:
+        return math.prod(lead[:-2]), lead[-2], lead[-1]
+    if n >= 3 and lead[-1] < IMAGE_MIN and lead[-3] >= IMAGE_MIN and lead[-2] >= IMAGE_MIN:
+        return math.prod(lead[:-3]), lead[-3], lead[-2] * lead[-1]
+    return None
 
 
 def _p(t: Optional[torch.Tensor]):
@@ -73,11 +94,22 @@ def prefetch(points, adjacency, offsets, out=None, stream=None):
     return out
 
 
+def image_dims(rays) -> Tuple[int, int, int]:
+    """(images, rows, columns) for the tiled entries: screen_layout of the
+    rays, else their last two leading dimensions."""
+    lead = rays.shape[:-1]
+    lay = screen_layout(lead)
+    if lay is None:
+        lay = (math.prod(lead[:-2]), int(lead[-2]), int(lead[-1]))
+    return lay
+
+
 def infer_f16(points, diffuse4, specular4, density, adjacency, offsets, adj_diff, rays, start_point, ray_perm=None,
               weight_threshold=0.001, max_intersections=1024, cell_skip_threshold=0.0, stats=None, out=None,
               tiled=None, stream=None):
     """fp16 inference.  ``tiled=(tile_h, tile_w)`` uses the in-kernel wave
-    tiling over rays shaped (B, H, W, 6) or (H, W, 6)."""
+    tiling over the images of screen_layout (any (..., H, W, 6) when the
+    layout finds none)."""
     rd = map_res(diffuse4.shape[-1], 4)
     rs = map_res(specular4.shape[-1], 4)
     nr = rays.numel() // 6
@@ -85,11 +117,7 @@ def infer_f16(points, diffuse4, specular4, density, adjacency, offsets, adj_diff
         out = torch.empty(list(rays.shape[:-1]) + [4], dtype=torch.float16, device=rays.device)
     dev = rays.device
     if tiled is not None:
-        shp = rays.shape[:-1]
-        if len(shp) == 2:
-            B, H, W = 1, shp[0], shp[1]
-        else:
-            B, H, W = shp[0], shp[1], shp[2]
+        B, H, W = image_dims(rays)
         _lib.call("vt_trace_infer_f16_tiled", points.data_ptr(), diffuse4.data_ptr(), specular4.data_ptr(), rd, rs,
                   density.data_ptr(), adjacency.data_ptr(), offsets.data_ptr(), points.size(0), adj_diff.data_ptr(),
                   rays.data_ptr(), B, H, W, tiled[0], tiled[1], start_point.data_ptr(), float(weight_threshold),
