@@ -78,6 +78,20 @@ class plant:
         return False
 
 
+class abs_sums:
+    """Context manager for oracle.h's absolute-sum mode: inside it, trace_bwd
+    returns per element the sum of |v| over the values scattered into it
+    (``with core.abs_sums(): cond = core.trace_bwd(...)``)."""
+
+    def __enter__(self):
+        lib().or_set_abs_sums(C.c_int(1))
+        return self
+
+    def __exit__(self, *exc):
+        lib().or_set_abs_sums(C.c_int(0))
+        return False
+
+
 PLANT_SPEC_PLUS_D = 1
 PLANT_INFER_NO_DENSITY_GATE = 2
 PLANT_SKIP_ON_ALPHA = 3

@@ -60,6 +60,15 @@ enum {
 void or_set_plant(int code);
 int or_get_plant(void);
 
+/* Absolute-sum mode: while on, every atomically accumulated output (the
+ * training backward's gradients, point_error, the forward's contribution)
+ * adds |v| instead of v, so a call returns per element the sum of the
+ * magnitudes scattered into it.  That sum bounds how far two summation
+ * orders of the element can differ (the conditioning of the sum); the
+ * parity tests scale their per-element tolerance by it.  Off in every other
+ * use. */
+void or_set_abs_sums(int on);
+
 float or_expf(float x);
 float or_logf(float x);
 uint16_t or_f32_to_f16(float x);

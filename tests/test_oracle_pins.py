@@ -492,3 +492,43 @@ def test_exit_face_rows_closed_forms():
     # exactly: face 0 of row 4 is -5e38 and face 1 is -1e39, both below -FLT_MAX
     x0 = (0.5 - 1e30) / dn[0].astype(np.float64) / 2
     assert x0 < -np.finfo(np.float32).max
+
+
+# --------------------------------------------------------------------------- absolute-sum mode
+
+def test_abs_sum_mode():
+    """The oracle's absolute-sum mode (the conditioning the GPU parity tests
+    scale their per-element tolerance by): single-threaded, so every sum has
+    one order.  The backward's terms are linear in the upstream gradient, so
+    their magnitudes do not change when it flips sign and double when it
+    doubles; the absolute sums bound the plain ones; and point_error's terms
+    w * ray_error >= 0 give absolute sums equal to the plain ones."""
+    s = scene.random_scene(400, seed=3, R=4)
+    rays = camera.pinhole_rays(24, 16, eye=(0.1, -3.3, 0.2))
+    o = rays[..., :3].reshape(-1, 3)
+    start = host_ops.nearest_site(s.points, o[:1]).astype(np.uint32)[0] * np.ones(rays.shape[:-1], np.uint32)
+    fw = core.trace_fwd(s.points, s.diffuse, s.specular, s.diff_res, s.spec_res, s.density, s.adjacency, s.offsets,
+                        rays, start, weight_threshold=0.001, threads=1)
+    g = np.random.default_rng(1).normal(size=rays.shape[:-1] + (4,)).astype(np.float32)
+    rerr = np.random.default_rng(2).uniform(0, 1, size=rays.shape[:-1]).astype(np.float32)
+
+    def bwd(gg):
+        return core.trace_bwd(s.points, s.diffuse, s.specular, s.diff_res, s.spec_res, s.density, s.adjacency,
+                              s.offsets, rays, start, fw["rgba"], gg, ray_error=rerr, distortion=fw["distortion"],
+                              W_total=fw["W_total"], S_total=fw["S_total"], t_far=fw["t_far"], threads=1)
+
+    plain = bwd(g)
+    with core.abs_sums():
+        a = bwd(g)
+        a_neg = bwd(-g)
+        a_two = bwd(2 * g)
+    again = bwd(g)  # the mode is off again after the context
+    keys = ("points_grad", "diffuse_grad", "specular_grad", "density_grad")
+    for k in keys:
+        assert np.array_equal(a[k], a_neg[k]), k
+        assert np.array_equal(a_two[k], 2 * a[k]), k
+        assert (a[k] >= 0).all() and (a[k] >= np.abs(plain[k]) * (1 - 1e-6)).all(), k
+        assert np.array_equal(again[k], plain[k]), k
+    assert np.abs(plain["diffuse_grad"]).max() > 0
+    assert (a["diffuse_grad"] > np.abs(plain["diffuse_grad"]) * 1.5).any()  # some texel sums cancel
+    assert np.array_equal(a["point_error"], plain["point_error"])
