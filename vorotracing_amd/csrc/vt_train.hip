@@ -35,15 +35,18 @@ template <> struct Attr<uint16_t> {
     // contribution buffers start at +0, which additions never turn into -0.
     // (A compare-and-swap loop on the 32-bit word took 70 times as long: the
     // lanes of a wave that add to one cell's texels serialise on its words.)
+    // The global-address form: a flat atomic also counts against the LDS
+    // wait counter, so the combining's LDS reads would wait for it.
     __device__ __forceinline__ static void add(uint16_t *p, size_t i, float v)
     {
         typedef _Float16 __attribute__((ext_vector_type(2))) half2_t;
+        typedef __attribute__((address_space(1))) half2_t global_half2_t;
         const uintptr_t addr = reinterpret_cast<uintptr_t>(p + i);
-        half2_t *pair = reinterpret_cast<half2_t *>(addr & ~(uintptr_t)3);
+        global_half2_t *pair = reinterpret_cast<global_half2_t *>(addr & ~(uintptr_t)3);
         const _Float16 h = __builtin_bit_cast(_Float16, f2h(v));
         const _Float16 z = __builtin_bit_cast(_Float16, (uint16_t)0);
         const half2_t val = (addr & 2) ? half2_t{z, h} : half2_t{h, z};
-        (void)__builtin_amdgcn_flat_atomic_fadd_v2f16(pair, val);
+        (void)__builtin_amdgcn_global_atomic_fadd_v2f16(pair, val);
     }
 };
 
@@ -388,46 +391,17 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
         held_perr = perr;
     }
 
-    // Global add of column k of a combined record (k in [0, REC_COLS)) of
-    // `cell`; for a texture column, `tap` is the texel of the column's tap.
-    __device__ __forceinline__ void column_add(uint32_t cell, uint32_t k, uint32_t tap, float x)
-    {
-        if (k == 25u && !point_error)
-            return; // no point_error output: its column has no target
-        if (k < 24u && tap >= (uint32_t)(k < 12u ? RD * RD : RS * RS))
-            return; // an unshaded cell: texture columns zero, taps unset
-        const uint32_t kt = k < 12u ? k : k - 12u;
-        const uint32_t texel = tap * 3u + (kt - 3u * (kt / 3u));
-        if constexpr (std::is_same<A, float>::value) {
-            // one atomic instruction for every target
-            float *q = k < 12u    ? diffuse_grad + (size_t)cell * ND + texel
-                       : k < 24u  ? specular_grad + (size_t)cell * NS + texel
-                       : k == 24u ? cell_grad + 4 * (size_t)cell + 3
-                       : k == 25u ? point_error + cell
-                                  : cell_grad + 4 * (size_t)cell + (k - 26u);
-            atomicAdd(q, x);
-        } else {
-            if (k < 12u)
-                Attr<A>::add(diffuse_grad + (size_t)cell * ND, texel, x);
-            else if (k < 24u)
-                Attr<A>::add(specular_grad + (size_t)cell * NS, texel, x);
-            else if (k == 24u)
-                atomicAdd(cell_grad + 4 * (size_t)cell + 3, x);
-            else if (k == 25u)
-                Attr<A>::add(point_error, cell, x);
-            else
-                atomicAdd(cell_grad + 4 * (size_t)cell + (k - 26u), x);
-        }
-    }
-
-    // What a lane needs to send column k of a combined record: the tap it
-    // reads (a byte of the diffuse or specular tap word; none for the other
-    // columns) and, for f32 outputs, the target as base + cell * stride +
-    // 3 * tap + off.  Set once per scatter, not per group.
+    // What a lane needs to send column k of a combined record (k in
+    // [0, REC_COLS)): the tap it reads (a byte of the diffuse or specular tap
+    // word; none for the other columns) and the target, element
+    // cell * stride + 3 * tap + off of base.  Set once per scatter, not per
+    // group.  A texture column of an unshaded cell (taps unset) and the
+    // point_error column without that output send nothing.
     struct Column {
         uint32_t k, sh, tmask;
         bool diffuse_taps, on;
-        float *base;
+        bool attr; // the target holds attribute values (textures, point_error), else f32
+        void *base;
         uint32_t stride, off, taps; // taps: texels of the map (1 for other columns)
     };
 
@@ -440,28 +414,27 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
         c.tmask = k < 24u ? 0xffu : 0u;
         c.diffuse_taps = k < 12u;
         c.on = k != 25u || point_error;
-        c.base = nullptr;
-        c.stride = 0;
-        c.off = 0;
         c.taps = k < 12u ? RD * RD : k < 24u ? RS * RS : 1u;
-        if constexpr (std::is_same<A, float>::value) {
-            c.base = k < 12u    ? diffuse_grad
-                     : k < 24u  ? specular_grad
-                     : k == 25u ? point_error
-                                : cell_grad;
-            c.stride = k < 12u ? (uint32_t)ND : k < 24u ? (uint32_t)NS : k == 25u ? 1u : 4u;
-            c.off = k < 24u ? kt - 3u * (kt / 3u) : k == 24u ? 3u : k == 25u ? 0u : k - 26u;
-        }
+        c.attr = k < 24u || k == 25u;
+        c.base = k < 12u    ? static_cast<void *>(diffuse_grad)
+                 : k < 24u  ? static_cast<void *>(specular_grad)
+                 : k == 25u ? static_cast<void *>(point_error)
+                            : static_cast<void *>(cell_grad);
+        c.stride = k < 12u ? (uint32_t)ND : k < 24u ? (uint32_t)NS : k == 25u ? 1u : 4u;
+        c.off = k < 24u ? kt - 3u * (kt / 3u) : k == 24u ? 3u : k == 25u ? 0u : k - 26u;
         return c;
     }
 
+    // One add of a combined column: one atomic instruction for every target
+    // (f32), or one per storage type (f16 attributes, f32 slots).
     __device__ __forceinline__ void column_send(const Column &c, uint32_t cell, uint32_t tap, float x)
     {
-        if constexpr (std::is_same<A, float>::value) {
-            if (c.on && tap < c.taps)
-                atomicAdd(c.base + (size_t)cell * c.stride + 3u * tap + c.off, x);
-        } else {
-            column_add(cell, c.k, tap, x);
+        if (c.on && tap < c.taps) {
+            const size_t i = (size_t)cell * c.stride + 3u * tap + c.off;
+            if (std::is_same<A, float>::value || !c.attr)
+                atomicAdd(static_cast<float *>(c.base) + i, x);
+            else
+                Attr<A>::add(static_cast<A *>(c.base), i, x);
         }
     }
 
