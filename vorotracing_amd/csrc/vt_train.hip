@@ -244,8 +244,9 @@ template <typename A, int RD, int RS> struct FwdIntegrator {
     }
 };
 
-// 6 waves per SIMD (80 VGPRs, 12 bytes spilled) beat the 5 that 86 VGPRs
-// allow: more waves hide more of the walk's load latency.
+// 6 waves per SIMD (80 VGPRs, 20 bytes spilled) beat the 5 that the
+// unspilled kernel allows (1.13-1.16 against 1.19-1.21 ms at C2): more waves
+// hide more of the walk's load latency.
 template <typename A, int RD, int RS, bool STATS>
 __global__ __launch_bounds__(TRAIN_BLOCK) __attribute__((amdgpu_waves_per_eu(6))) void fwd_kernel(FwdArgs a)
 {
