@@ -224,6 +224,10 @@ int vt_trace_fwd(int attr_dtype, const float *points, const void *diffuse, const
  * Training backward.  Replaces _C.trace_vorotracing_bwd
  * (tracing_octmap.cu:860-1103, kernel :232-340).  Prefetch into the
  * workspace as in vt_trace_fwd, then the re-walk with gradient scatter.
+ *   adj_diff_ready (an extension, ABI version 6): 0 = prefetch as the
+ *   reference does; 1 = adj_diff_workspace already holds the prefetch of
+ *   these points and adjacency (the forward of the same call filled it and
+ *   neither has changed since), which the call then skips.
  *   rgba / rgba_grad: attr dtype (num_rays, 4).  depth_quantiles, depth_idx,
  *   depth_grad (num_rays, K) or NULL.  ray_error: attr dtype (num_rays) or
  *   NULL.  distortion, W_total, S_total, t_far: f32 (num_rays);
@@ -249,7 +253,7 @@ int vt_trace_bwd(int attr_dtype, const float *points, const void *diffuse, const
                  const float *distortion_grad, const float *W_total, const float *S_total, const float *t_far,
                  float weight_threshold, uint32_t max_intersections, float *points_grad, void *diffuse_grad,
                  void *specular_grad, float *density_grad, void *point_error, uint16_t *adj_diff_workspace,
-                 float *cell_workspace, vt_ray_stats *stats, vt_stream_t stream);
+                 int adj_diff_ready, float *cell_workspace, vt_ray_stats *stats, vt_stream_t stream);
 
 /*
  * Coherent lane order for a flat training batch (an extension: the reference

@@ -92,6 +92,28 @@ def test_prefetch_bit_exact(gpu, which):
     assert not got[m:].view(np.uint16).any()  # padding rows zero-filled
 
 
+def test_prefetch_bit_exact_synthetic_csr(gpu):
+    """Face lists of every length the prefetch's two owner paths meet: blocks
+    of 256 cells whose entries fit its owner table, a block of 256 cells with
+    70 faces each (17,920 entries, past the table: binary search), a
+    900-face list, empty lists and a partial last block."""
+    rng = np.random.default_rng(12)
+    n = 1100
+    deg = rng.integers(0, 30, n)
+    deg[256:512] = 70
+    deg[600] = 900
+    deg[700:710] = 0
+    offsets = np.concatenate([[0], np.cumsum(deg)]).astype(np.uint32)
+    m = int(offsets[-1])
+    adjacency = np.concatenate([rng.integers(0, n, m), np.zeros(32)]).astype(np.uint32)
+    points = rng.normal(size=(n, 3)).astype(np.float32)
+    got = _C.trace_vorotracing_prefetch_adj(H.to_dev(points, gpu), H.to_dev(adjacency, gpu),
+                                            H.to_dev(offsets, gpu)).cpu().numpy()
+    want = core.prefetch_adj(points, adjacency, offsets)
+    assert np.array_equal(got[:m].view(np.uint16), want[:m].view(np.uint16))
+    assert not got[m:].view(np.uint16).any()
+
+
 def _c1_rays(W=128, Hh=128):
     return camera.pinhole_rays(W, Hh, eye=(0.0, -4.0, 0.0))
 

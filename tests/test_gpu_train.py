@@ -262,3 +262,35 @@ def test_start_cells_any_ray_order(gpu):
     # an image in order: one run per image
     img = camera.pinhole_rays(20, 12, eye=eyes[1])
     assert np.array_equal(model.get_starting_point(H.to_dev(img, gpu)).cpu().numpy(), H.start_for(s, img))
+
+
+def test_backward_reuses_the_forward_prefetch(gpu):
+    """adj_diff_out / adj_diff: the forward's face-offset prefetch (equal to
+    the oracle's) handed to the backward, which then skips its own; the
+    gradients are the oracle's."""
+    s, rays, start, thr = _case("r8")
+    rng = np.random.default_rng(6)
+    fw = core.trace_fwd(s.points, s.diffuse, s.specular, s.diff_res, s.spec_res, s.density, s.adjacency, s.offsets,
+                        rays, start, weight_threshold=thr)
+    g = rng.normal(size=rays.shape[:-1] + (4,)).astype(np.float32)
+    want = core.trace_bwd(s.points, s.diffuse, s.specular, s.diff_res, s.spec_res, s.density, s.adjacency,
+                          s.offsets, rays, start, fw["rgba"], g, distortion=fw["distortion"], W_total=fw["W_total"],
+                          S_total=fw["S_total"], t_far=fw["t_far"], weight_threshold=thr)
+    scene = _scene_tensors(s, gpu, False)
+    rd, sd = H.to_dev(rays, gpu), H.to_dev(start, gpu)
+    ad = torch.full((s.adjacency.shape[0] + 32, 4), float("nan"), dtype=torch.float16, device=gpu)
+    got = _C.trace_vorotracing_fwd(*scene, rd, sd, None, thr, 1024, False, adj_diff_out=ad)
+    torch.cuda.synchronize()
+    m = s.num_faces
+    pre = core.prefetch_adj(s.points, s.adjacency, s.offsets)
+    assert np.array_equal(ad.cpu().numpy()[:m].view(np.uint16), pre[:m].view(np.uint16))
+    assert np.array_equal(got[0].cpu().numpy(), fw["rgba"])
+    pg, dgd, sgd, deng, _, _ = _C.trace_vorotracing_bwd(
+        *scene, rd, sd, got[0], H.to_dev(g, gpu), None, None, None, None, 0.0, got[5], None, got[6], got[7], got[8],
+        thr, 1024, adj_diff=ad)
+    torch.cuda.synchronize()
+    for t, key in ((pg, "points_grad"), (deng, "density_grad"), (dgd, "diffuse_grad"), (sgd, "specular_grad")):
+        H.assert_grad_close(t.cpu().numpy(), want[key], key)
+    with pytest.raises(RuntimeError, match="adj_diff must be"):
+        _C.trace_vorotracing_bwd(*scene, rd, sd, got[0], H.to_dev(g, gpu), None, None, None, None, 0.0, got[5], None,
+                                 got[6], got[7], got[8], thr, 1024, adj_diff=ad[:-1])

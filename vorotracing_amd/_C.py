@@ -306,7 +306,8 @@ def _attr_code(dtype):
 def trace_vorotracing_fwd(points_in, diffuse_in, specular_in, density_in, point_adjacency_in,
                           point_adjacency_offsets_in, rays_in, start_point_in, depth_quantiles_in,
                           weight_threshold: float, max_intersections: int, return_contribution: bool,
-                          stats: Optional[torch.Tensor] = None, ray_perm: Union[str, torch.Tensor, None] = "auto"):
+                          stats: Optional[torch.Tensor] = None, ray_perm: Union[str, torch.Tensor, None] = "auto",
+                          adj_diff_out: Optional[torch.Tensor] = None):
     """tracing_octmap.cu:346-546.  Returns (rgba, depth, depth_idx,
     contribution, n, distortion, W_total, S_total, t_far); absent outputs are
     None.  Extensions: ``stats``, None or a u32 (num_rays,
@@ -314,7 +315,10 @@ def trace_vorotracing_fwd(points_in, diffuse_in, specular_in, density_in, point_
     (vt_ray_stats); ``ray_perm``, the lane order: "auto" (default_ray_perm),
     None (screen tiles for image-shaped rays, else batch order) or a
     permutation of the rays (ray_order).  Outputs stay indexed by ray; the
-    lane order changes only the order of atomic additions."""
+    lane order changes only the order of atomic additions.  ``adj_diff_out``:
+    an f16 (adjacency_size + 32, 4) device tensor the call's face-offset
+    prefetch goes to (else a temporary), for the backward of the same scene
+    to reuse (trace_vorotracing_bwd's ``adj_diff``)."""
     points = points_in.contiguous()
     diffuse = diffuse_in.contiguous()
     specular = specular_in.contiguous()
@@ -354,7 +358,7 @@ def trace_vorotracing_fwd(points_in, diffuse_in, specular_in, density_in, point_
     W_total = torch.empty(f1, dtype=torch.float32, device=dev)
     S_total = torch.empty(f1, dtype=torch.float32, device=dev)
     t_far = torch.empty(f1, dtype=torch.float32, device=dev)
-    workspace = torch.empty((adjacency_size + 32, 4), dtype=torch.float16, device=dev)
+    workspace = _adj_diff_buffer(adj_diff_out, adjacency_size, dev, "adj_diff_out")
     img_h, img_w, perm = _lane_order(rays, start_point, num_points, ray_perm)
     with torch.cuda.device(dev):
         _lib.call("vt_trace_fwd", code, points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd, rs,
@@ -364,6 +368,17 @@ def trace_vorotracing_fwd(points_in, diffuse_in, specular_in, density_in, point_
                   _ptr(contribution), n.data_ptr(), distortion.data_ptr(), W_total.data_ptr(), S_total.data_ptr(),
                   t_far.data_ptr(), workspace.data_ptr(), _stats_ptr(stats, num_rays), _stream(dev))
     return rgba, depth, depth_idx, contribution, n, distortion, W_total, S_total, t_far
+
+
+def _adj_diff_buffer(given: Optional[torch.Tensor], adjacency_size: int, dev, what: str) -> torch.Tensor:
+    """The f16 (adjacency_size + 32, 4) face-offset buffer of a training entry:
+    ``given`` (checked), else a new one."""
+    if given is None:
+        return torch.empty((adjacency_size + 32, 4), dtype=torch.float16, device=dev)
+    _assert(given.dtype == torch.float16 and tuple(given.shape) == (adjacency_size + 32, 4) and given.is_contiguous()
+            and given.device == dev, f"{what} must be a contiguous float16 (adjacency_size + 32, 4) tensor on the "
+                                     "rays' device")
+    return given
 
 
 def _stats_ptr(stats: Optional[torch.Tensor], num_rays: int):
@@ -380,11 +395,15 @@ def trace_vorotracing_bwd(points_in, diffuse_in, specular_in, density_in, point_
                           depth_quantiles_in, depth_indices_in, depth_grad_in, ray_error_in,
                           contribution_alpha_grad: float, distortion_in, distortion_grad_in, W_total_in, S_total_in,
                           t_far_in, weight_threshold: float, max_intersections: int,
-                          stats: Optional[torch.Tensor] = None, ray_perm: Union[str, torch.Tensor, None] = "auto"):
+                          stats: Optional[torch.Tensor] = None, ray_perm: Union[str, torch.Tensor, None] = "auto",
+                          adj_diff: Optional[torch.Tensor] = None):
     """tracing_octmap.cu:860-1103.  Returns (points_grad, diffuse_grad,
     specular_grad, density_grad, ray_grad, point_error).  ray_grad is zeros
     (the reference returns it uninitialised and the autograd wrapper drops
-    it).  ``stats`` and ``ray_perm`` as for trace_vorotracing_fwd (extensions)."""
+    it).  ``stats`` and ``ray_perm`` as for trace_vorotracing_fwd (extensions).
+    ``adj_diff`` (an extension): the forward's ``adj_diff_out`` for the same
+    points and adjacency, unchanged since; the call then skips its own
+    prefetch (the reference prefetches on every call)."""
     points = points_in.contiguous()
     diffuse = diffuse_in.contiguous()
     specular = specular_in.contiguous()
@@ -461,7 +480,7 @@ def trace_vorotracing_bwd(points_in, diffuse_in, specular_in, density_in, point_
     density_grad = torch.zeros_like(density, dtype=torch.float32)
     points_grad = torch.zeros((num_points, 3), dtype=rays.dtype, device=dev)
     ray_grad = torch.zeros_like(rays)
-    workspace = torch.empty((adjacency_size + 32, 4), dtype=torch.float16, device=dev)
+    workspace = _adj_diff_buffer(adj_diff, adjacency_size, dev, "adj_diff")
     cell_workspace = torch.empty((num_points, 4), dtype=torch.float32, device=dev)
     img_h, img_w, perm = _lane_order(rays, start_point, num_points, ray_perm)
     with torch.cuda.device(dev):
@@ -474,7 +493,7 @@ def trace_vorotracing_bwd(points_in, diffuse_in, specular_in, density_in, point_
                   W_total.data_ptr(), S_total.data_ptr(), t_far.data_ptr(), float(weight_threshold),
                   int(max_intersections), points_grad.data_ptr(), diffuse_grad.data_ptr(),
                   specular_grad.data_ptr(), density_grad.data_ptr(), _ptr(point_error), workspace.data_ptr(),
-                  cell_workspace.data_ptr(), _stats_ptr(stats, num_rays), _stream(dev))
+                  int(adj_diff is not None), cell_workspace.data_ptr(), _stats_ptr(stats, num_rays), _stream(dev))
     return points_grad, diffuse_grad, specular_grad, density_grad, ray_grad, point_error
 
 

@@ -43,7 +43,7 @@ SIGNATURES = {
         C.c_int),
     "vt_trace_bwd": (
         [I32, P, P, P, U32, U32, P, P, U32, P, U32, P, U32, U32, U32, P, P, P, P, U32, P, P, P, P, F32, P, P, P, P, P, F32,
-         U32, P, P, P, P, P, P, P, P, P], C.c_int),
+         U32, P, P, P, P, P, P, I32, P, P, P], C.c_int),
     "vt_ray_order_workspace_size": ([U32], C.c_size_t),
     "vt_ray_order": ([P, P, U32, U32, P, P, P], C.c_int),
     "vt_math_probe": ([I32, P, P, U32, P], C.c_int),

@@ -62,6 +62,7 @@ class TraceRecord:
     totals: Tuple[torch.Tensor, torch.Tensor, torch.Tensor]  # W_total, S_total, t_far
     box: ErrorBox
     perm: Optional[torch.Tensor] = None  # lane order of the forward, reused by the backward
+    adj_diff: Optional[torch.Tensor] = None  # the forward's face-offset prefetch, reused by the backward
 
 
 @dataclasses.dataclass
@@ -80,11 +81,16 @@ def run_forward(scene, rays, start, quantiles, weight_threshold: float, max_inte
     (rgba, depth, contribution, n, error box, distortion, as
     _wrapper.py:87) and the record a backward needs."""
     perm = _C.default_ray_perm(rays, start, scene[0].shape[0])
+    adjacency = scene[4]
+    ad = None
+    if rays.is_cuda:
+        ad = torch.empty((adjacency.shape[0] + 32, 4), dtype=torch.float16, device=rays.device)
     rgba, depth, depth_idx, contribution, n, distortion, w_tot, s_tot, t_far = _C.trace_vorotracing_fwd(
-        *scene, rays, start, quantiles, weight_threshold, max_intersections, want_contribution, ray_perm=perm)
+        *scene, rays, start, quantiles, weight_threshold, max_intersections, want_contribution, ray_perm=perm,
+        adj_diff_out=ad)
     box = ErrorBox()
     rec = TraceRecord(tuple(scene), rays, start, quantiles, float(weight_threshold), int(max_intersections), rgba,
-                      depth_idx, distortion, (w_tot, s_tot, t_far), box, perm)
+                      depth_idx, distortion, (w_tot, s_tot, t_far), box, perm, ad)
     return (rgba, depth, contribution, n, box, distortion), rec
 
 
@@ -113,7 +119,8 @@ def _launch(rec: TraceRecord, up: Upstream):
     w_tot, s_tot, t_far = rec.totals
     return _C.trace_vorotracing_bwd(*rec.scene, rec.rays, rec.start, rec.rgba, up.rgba, rec.quantiles, rec.depth_idx,
                                     up.depth, up.ray_error, up.alpha_scalar, rec.distortion, up.distortion, w_tot,
-                                    s_tot, t_far, rec.weight_threshold, rec.max_intersections, ray_perm=rec.perm)
+                                    s_tot, t_far, rec.weight_threshold, rec.max_intersections, ray_perm=rec.perm,
+                                    adj_diff=rec.adj_diff)
 
 
 def scene_gradients(rec: TraceRecord, up: Upstream):

@@ -63,32 +63,49 @@ __global__ void math_probe_kernel(int op, const float *__restrict__ in, uint32_t
 
 // Prefetch: one block per 256 consecutive cells.  The block stages the
 // cells' CSR offsets in LDS, then its lanes sweep the block's face entries
-// with unit stride (coalesced adjacency reads and adj_diff writes), finding
-// the owning cell by binary search in LDS.  Value per entry e of cell i:
+// with unit stride (coalesced adjacency reads and adj_diff writes).  The
+// owning cell of an entry comes from a byte table in LDS that each lane
+// fills for its cell's entries first (one LDS read per entry in the sweep);
+// a block with more entries than the table holds (long hull-cell lists)
+// finds it by binary search over the offsets.  Value per entry e of cell i:
 // half(site[adj[e]] - site[i]) per axis (f32 subtract, RNE cast), w = 0.
 constexpr int PF_CELLS = 256;
+constexpr uint32_t PF_OWNER = 16384; // entries of a block whose owners fit the byte table
 
 __global__ __launch_bounds__(PF_CELLS) void prefetch_kernel(const float *__restrict__ points, uint32_t num_points,
                                                              const uint32_t *__restrict__ adjacency,
                                                              const uint32_t *__restrict__ offsets,
                                                              uint2 *__restrict__ adj_diff)
 {
+    static_assert(PF_CELLS <= 256, "owners are stored as bytes");
     __shared__ uint32_t off[PF_CELLS + 1];
+    __shared__ uint8_t owner[PF_OWNER];
     uint32_t c0 = blockIdx.x * PF_CELLS;
     uint32_t cnt = min((uint32_t)PF_CELLS, num_points - c0);
     for (uint32_t i = threadIdx.x; i <= cnt; i += blockDim.x)
         off[i] = offsets[c0 + i];
     __syncthreads();
-    uint32_t e0 = off[0], e1 = off[cnt];
+    const uint32_t e0 = off[0], e1 = off[cnt];
+    const bool table = e1 - e0 <= PF_OWNER; // block-uniform
+    if (table) {
+        for (uint32_t c = threadIdx.x; c < cnt; c += blockDim.x)
+            for (uint32_t e = off[c]; e < off[c + 1]; ++e)
+                owner[e - e0] = (uint8_t)c;
+        __syncthreads();
+    }
     for (uint32_t e = e0 + threadIdx.x; e < e1; e += blockDim.x) {
-        // largest c with off[c] <= e (c < cnt)
-        uint32_t lo = 0, hi = cnt;
-        while (hi - lo > 1) {
-            uint32_t mid = (lo + hi) >> 1;
-            if (off[mid] <= e)
-                lo = mid;
-            else
-                hi = mid;
+        uint32_t lo = 0;
+        if (table) {
+            lo = owner[e - e0];
+        } else { // largest c with off[c] <= e (c < cnt)
+            uint32_t hi = cnt;
+            while (hi - lo > 1) {
+                uint32_t mid = (lo + hi) >> 1;
+                if (off[mid] <= e)
+                    lo = mid;
+                else
+                    hi = mid;
+            }
         }
         f3 p = load_site(points, c0 + lo);
         f3 q = load_site(points, adjacency[e]);
@@ -132,7 +149,7 @@ using namespace vt;
 
 extern "C" const char *vt_last_error(void) { return g_err; }
 
-extern "C" int vt_abi_version(void) { return 5; }
+extern "C" int vt_abi_version(void) { return 6; }
 
 extern "C" int vt_math_probe(int op, const float *in, uint32_t *out, uint32_t n, vt_stream_t stream)
 {

@@ -950,7 +950,7 @@ extern "C" int vt_trace_bwd(int attr_dtype, const float *points, const void *dif
                             const float *S_total, const float *t_far, float weight_threshold,
                             uint32_t max_intersections, float *points_grad, void *diffuse_grad, void *specular_grad,
                             float *density_grad, void *point_error, uint16_t *adj_diff_workspace,
-                            float *cell_workspace, vt_ray_stats *stats, vt_stream_t stream)
+                            int adj_diff_ready, float *cell_workspace, vt_ray_stats *stats, vt_stream_t stream)
 {
     clear_error();
     (void)t_far;
@@ -965,7 +965,9 @@ extern "C" int vt_trace_bwd(int attr_dtype, const float *points, const void *dif
     VT_REQUIRE(!ray_error || point_error, "point_error output required when ray_error is given");
     VT_REQUIRE(num_rays == 0 || num_points > 0, "rays need at least one site");
     hipStream_t s = as_stream(stream);
-    int rc = prefetch(points, num_points, adjacency, adjacency_size, offsets, adj_diff_workspace, s);
+    int rc = VT_OK;
+    if (!adj_diff_ready) // else the forward of the same scene filled it
+        rc = prefetch(points, num_points, adjacency, adjacency_size, offsets, adj_diff_workspace, s);
     if (rc)
         return rc;
     BwdArgs a{};
