@@ -110,6 +110,13 @@ constexpr int ROW_TABLE_FLOATS = 65 * ROW_STRIDE;
 // num_rays leave the lane idle), else 8x8 screen tiles of row-major images,
 // or ray order.
 constexpr uint32_t TRAIN_TILE = 8;
+// Tile strips of the training kernels, 2 tiles wide (C2: forward 1.13-1.15
+// against 1.15-1.18 ms, backward 3.98-4.03 against 4.04-4.09 with strips of
+// 4, which inference keeps).
+#ifndef VT_TRAIN_TILE_STRIP
+#define VT_TRAIN_TILE_STRIP 2
+#endif
+constexpr uint32_t TRAIN_TILE_STRIP = VT_TRAIN_TILE_STRIP;
 
 __device__ __forceinline__ uint32_t train_ray(uint32_t s, uint32_t num_rays, const uint32_t *perm, uint32_t ni,
                                               uint32_t h, uint32_t w)
@@ -121,7 +128,7 @@ __device__ __forceinline__ uint32_t train_ray(uint32_t s, uint32_t num_rays, con
         return r < num_rays ? r : NONE;
     }
     if (ni)
-        return tiled_ray(s, ni, h, w, TRAIN_TILE, TRAIN_TILE);
+        return tiled_ray<TRAIN_TILE_STRIP>(s, ni, h, w, TRAIN_TILE, TRAIN_TILE);
     return s < num_rays ? s : NONE;
 }
 

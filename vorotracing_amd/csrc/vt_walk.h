@@ -224,7 +224,9 @@ __device__ __forceinline__ uint32_t walk(f3 o, f3 d, const float *points,
 constexpr uint32_t TILE_STRIP = VT_TILE_STRIP;
 
 // Lane -> ray for a tiled image batch: one wave (64 lanes) per tile_w x
-// tile_h screen tile.  Returns NONE for lanes past the image edge.
+// tile_h screen tile, tiles in vertical strips STRIP tiles wide.  Returns
+// NONE for lanes past the image edge.
+template <uint32_t STRIP = TILE_STRIP>
 __device__ __forceinline__ uint32_t tiled_ray(uint32_t lane_global, uint32_t num_images, uint32_t H, uint32_t W,
                                               uint32_t th, uint32_t tw)
 {
@@ -236,18 +238,18 @@ __device__ __forceinline__ uint32_t tiled_ray(uint32_t lane_global, uint32_t num
     uint32_t img = tile / tpi;
     uint32_t ti = tile % tpi;
     uint32_t tx, ty;
-    if (TILE_STRIP == 0 || TILE_STRIP >= tiles_x) {
+    if (STRIP == 0 || STRIP >= tiles_x) {
         ty = ti / tiles_x;
         tx = ti % tiles_x;
     } else {
-        uint32_t per_strip = TILE_STRIP * tiles_y;
+        uint32_t per_strip = STRIP * tiles_y;
         uint32_t strip = ti / per_strip;
         uint32_t r = ti % per_strip;
-        uint32_t w = TILE_STRIP;
-        if ((strip + 1) * TILE_STRIP > tiles_x)
-            w = tiles_x - strip * TILE_STRIP;
+        uint32_t w = STRIP;
+        if ((strip + 1) * STRIP > tiles_x)
+            w = tiles_x - strip * STRIP;
         ty = r / w;
-        tx = strip * TILE_STRIP + r % w;
+        tx = strip * STRIP + r % w;
     }
     uint32_t y = ty * th + within / tw;
     uint32_t x = tx * tw + within % tw;
