@@ -261,7 +261,7 @@ int vt_trace_bwd(int attr_dtype, const float *points, const void *diffuse, const
  * trainer batches random pixels of random images, datasets.py:185-222 with
  * trainer.py:52).
  *   ray_perm (num_rays) u32 out: the rays sorted by start cell, then by a
- *   2-D Morton code of the direction's octahedral coordinates (a 256 x 256
+ *   2-D Morton code of the direction's octahedral coordinates (a 128 x 128
  *   grid), stable, so that a wave traces rays of one camera with neighbouring
  *   directions.  Pass it as vt_trace_fwd / vt_trace_bwd's ray_perm.
  *   workspace: vt_ray_order_workspace_size(num_rays) bytes, 4-byte aligned.

@@ -22,7 +22,7 @@ from vorotracing_amd import _C, camera
 
 pytestmark = pytest.mark.gpu
 
-DIR_BITS = 8  # octahedral grid bits per axis of vt_ray_order's direction key
+DIR_BITS = 7  # octahedral grid bits per axis of vt_ray_order's direction key
 
 
 def _spread(q):
@@ -49,8 +49,8 @@ def _grid_directions(rng, n):
 
 
 @pytest.mark.parametrize("num_points,num_rays,distinct", [
-    (1000, 70001, 7),        # cell and direction in one 26-bit key
-    (300000, 70001, 0),      # 19 + 16 bits: direction pass, then a stable cell pass
+    (1000, 70001, 7),        # cell and direction in one 24-bit key
+    (300000, 70001, 0),      # 19 + 14 bits: direction pass, then a stable cell pass
     (300000, 5000, 11),
     (1, 3000, 1),            # a single site: direction only
     (1000, 1, 1),
