@@ -441,10 +441,16 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
     {
         if (c.on && tap < c.taps) {
             const size_t i = (size_t)cell * c.stride + 3u * tap + c.off;
-            if (std::is_same<A, float>::value || !c.attr)
+            if (std::is_same<A, float>::value || !c.attr) {
                 atomicAdd(static_cast<float *>(c.base) + i, x);
-            else
-                Attr<A>::add(static_cast<A *>(c.base), i, x);
+            } else {
+                // halves of one 32-bit word in separate instructions: lanes
+                // adding to the same word in one atomic instruction serialise
+#pragma unroll 1
+                for (uint32_t half = 0; half < 2; ++half)
+                    if ((i & 1) == half)
+                        Attr<A>::add(static_cast<A *>(c.base), i, x);
+            }
         }
     }
 
