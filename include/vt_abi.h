@@ -293,12 +293,14 @@ int vt_bvh_num_nodes(void *handle);
 /*
  * The query of vt_bvh_query (nn_bvh.cu:91-109) without the handle's
  * workspace: when the all-sites scan is the faster path (num_queries *
- * num_points <= VT_NN_SCAN_PAIRS) its per-block partials go in `workspace`
+ * num_points <= VT_NN_SCAN_PAIRS and num_queries <= VT_NN_SCAN_MAX_QUERIES)
+ * its per-block partials go in `workspace`
  * (8-byte aligned, vt_nearest_scan_workspace_size(num_queries) bytes; with
  * less, or NULL, the tree is walked).  The handle is only read, so queries of
  * one built handle may run on several streams at once.
  */
 #define VT_NN_SCAN_PAIRS (1ull << 26)
+#define VT_NN_SCAN_MAX_QUERIES 64
 size_t vt_nearest_scan_workspace_size(uint32_t num_queries);
 int vt_bvh_query_ws(void *handle, const float *points, uint32_t num_points, const float *queries, uint32_t num_queries,
                     int32_t *out, void *workspace, size_t workspace_bytes, vt_stream_t stream);
@@ -318,7 +320,11 @@ int vt_bvh_debug_stack_limit(void *handle, uint32_t limit, int force_tree);
  * partials in a static device array that each GPU holds until the process
  * ends); more is rejected with VT_ERR_INVALID.  No hipMalloc or hipFree.
  * Every call on one GPU shares that array: calls that overlap on one GPU
- * (concurrent streams, threads) race; order them on one stream.
+ * (concurrent streams, threads) race; order them on one stream.  The first
+ * call on a device looks up the array's address there (hipGetSymbolAddress);
+ * a call with num_queries = 0 does only that, so a caller that captures the
+ * lookup into a HIP graph makes one such call first, outside the capture.
+ * Each call is then two kernel launches on `stream` and no memset.
  */
 int vt_nearest_sites_noalloc(const float *points, uint32_t num_points, const float *queries, uint32_t num_queries,
                              int32_t *out, vt_stream_t stream);
@@ -424,11 +430,14 @@ int vt_voronoi_build(const float *points, uint32_t num_points, uint32_t *offsets
  * reference's training refresh can pass to Paragram: initial_guesses,
  * cuda/__init__.py:16-37) cut each cell first; the result is the same
  * neighbour sets as without guesses (out-of-range ids are ignored), found
- * faster when the guesses are close.  NULL, NULL = vt_voronoi_build.
+ * faster when the guesses are close.  guess_adjacency holds num_guesses
+ * entries (an argument since ABI version 7); a cell whose guess range runs
+ * backwards or past them builds without guesses.  NULL, NULL, 0 =
+ * vt_voronoi_build.
  */
 int vt_voronoi_build_warm(const float *points, uint32_t num_points, const uint32_t *guess_offsets,
-                          const uint32_t *guess_adjacency, uint32_t *offsets, uint32_t *num_adjacency,
-                          void *workspace, vt_stream_t stream);
+                          const uint32_t *guess_adjacency, uint32_t num_guesses, uint32_t *offsets,
+                          uint32_t *num_adjacency, void *workspace, vt_stream_t stream);
 int vt_voronoi_adjacency(uint32_t num_points, const uint32_t *offsets, uint32_t *adjacency, const void *workspace,
                          vt_stream_t stream);
 
@@ -450,6 +459,16 @@ int vt_pad_3to4_f16(const float *x, uint32_t rows, uint32_t texels_per_row, uint
  * (0xffffffff = none) and t1 bits.
  */
 int vt_math_probe(int op, const float *in, uint32_t *out, uint32_t n, vt_stream_t stream);
+
+/*
+ * Self-test of the half-precision atomic add of the f16-storage backward (no
+ * reference counterpart; it stands in for the reference's atomicAdd on
+ * __half, ray_integrator_octmap.cuh:1004-1007,1021-1024): thread i adds
+ * values[i], rounded to half, to halves[index[i]] with the backward's own
+ * atomic.  Indices at or past num_halves (even) are skipped.
+ */
+int vt_debug_f16_atomic_add(uint16_t *halves, uint32_t num_halves, const uint32_t *index, const float *values,
+                            uint32_t n, vt_stream_t stream);
 
 #ifdef __cplusplus
 }

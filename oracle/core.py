@@ -81,10 +81,14 @@ class plant:
 class abs_sums:
     """Context manager for oracle.h's absolute-sum mode: inside it, trace_bwd
     returns per element the sum of |v| over the values scattered into it
-    (``with core.abs_sums(): cond = core.trace_bwd(...)``)."""
+    (``with core.abs_sums(): cond = core.trace_bwd(...)``); with
+    ``count=True`` the number of values scattered into it instead."""
+
+    def __init__(self, count: bool = False):
+        self.mode = 2 if count else 1
 
     def __enter__(self):
-        lib().or_set_abs_sums(C.c_int(1))
+        lib().or_set_abs_sums(C.c_int(self.mode))
         return self
 
     def __exit__(self, *exc):

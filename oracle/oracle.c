@@ -48,9 +48,10 @@ static int g_plant = OR_PLANT_NONE;
 void or_set_plant(int code) { g_plant = code; }
 int or_get_plant(void) { return g_plant; }
 
-/* absolute-sum mode (oracle.h): every atomic add adds |v|; 0 in every other use */
+/* absolute-sum mode (oracle.h): every atomic add adds |v| (1), or 1 (2); 0 in every other use */
 static int g_abs_sums = 0;
 void or_set_abs_sums(int on) { g_abs_sums = on; }
+static inline float sum_mode_value(float v) { return g_abs_sums == 2 ? 1.0f : fabsf(v); }
 
 /* ------------------------------------------------------------------------- */
 /* scalar math                                                                 */
@@ -616,7 +617,7 @@ void or_trace_infer_q8(const float *points, const uint8_t *diffuse, const uint8_
 static inline void atomic_add_f32(float *dst, float v)
 {
     if (g_abs_sums)
-        v = fabsf(v);
+        v = sum_mode_value(v);
 #pragma omp atomic
     *dst += v;
 }
@@ -625,7 +626,7 @@ static inline void atomic_add_f32(float *dst, float v)
 static inline void atomic_add_f16(uint16_t *dst, float v)
 {
     if (g_abs_sums)
-        v = fabsf(v);
+        v = sum_mode_value(v);
     uintptr_t a = (uintptr_t)dst;
     uint32_t *word = (uint32_t *)(a & ~(uintptr_t)3);
     int hi = (a & 2) != 0;

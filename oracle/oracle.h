@@ -65,8 +65,10 @@ int or_get_plant(void);
  * adds |v| instead of v, so a call returns per element the sum of the
  * magnitudes scattered into it.  That sum bounds how far two summation
  * orders of the element can differ (the conditioning of the sum); the
- * parity tests scale their per-element tolerance by it.  Off in every other
- * use. */
+ * parity tests scale their per-element tolerance by it.  With on = 2 every
+ * add adds 1 instead: the number of adds per element, which bounds the
+ * rounding of sums kept in half precision (one rounding per add).  Off (0) in
+ * every other use. */
 void or_set_abs_sums(int on);
 
 float or_expf(float x);

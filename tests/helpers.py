@@ -22,6 +22,13 @@ def mini_heightfield(n=40000, seed=3):
 
 
 @functools.lru_cache(maxsize=None)
+def mini_heightfield_r8(n=40000, seed=3):
+    """The mini height field with the reference's only compiled map
+    resolution, 8x8 diffuse and 8x8 specular (tracing_octmap.cu:27-28)."""
+    return scene.heightfield(seed=seed, n=n, R=8, name="mini_c3_r8")
+
+
+@functools.lru_cache(maxsize=None)
 def small_random(n=600, seed=7, R=4, Rs=None, grid=None):
     return scene.random_scene(n, seed=seed, R=R, Rs=Rs, grid=grid)
 
@@ -158,3 +165,85 @@ def assert_grad_close(got, want, name="", rtol=1e-3, atol_frac=1e-6, abs_sum=Non
     assert bad[0].size == 0, (f"{name}: {bad[0].size} elements outside {rtol} x |want| + {atol_frac} x scale"
                               f"{'' if abs_sum is None else f' + {COND_RTOL} x abs sum'}, first "
                               f"{list(zip(g[bad][:4], w[bad][:4]))}")
+
+
+def quant_ties(per_channel):
+    """q8 inputs whose quantised values land exactly on k + 0.5 steps, and the
+    codes torch.round (half to even) gives them (vorotracing.py:495-503).
+    Each channel spans exactly 255 (scale 1, reciprocal 1), shifted by an
+    exact offset, so (x - vmin) * (1 / scale) is the listed value exactly; a
+    half-away-from-zero rounding gives 1, 3, 5, ... where these give 0, 2, 4."""
+    vals = np.array([0.0, 255.0, 0.5, 1.5, 2.5, 3.5, 4.5, 126.5, 127.5, 128.5, 253.5, 254.5, 100.0, 7.25, 7.75,
+                     99.5], np.float32)
+    want = np.rint(vals).astype(np.uint8)  # numpy rounds half to even, like torch.round
+    assert list(want[2:7]) == [0, 2, 2, 4, 4]
+    shift = (-1.0, 0.0, 3.0) if per_channel else (0.0, 0.0, 0.0)
+    x = np.stack([vals + np.float32(shift[c]) for c in range(3)], axis=1).reshape(1, -1)  # texel-major
+    x = np.repeat(x, 4, axis=0)
+    q = np.repeat(np.stack([want] * 3, axis=1).reshape(1, -1), 4, axis=0)
+    return x.astype(np.float32), q
+
+
+# Half-precision accumulation (f16 attribute storage; the reference's
+# atomicAdd on __half, ray_integrator_octmap.cuh:1004-1007,1021-1024): each
+# term is rounded to half once and each add rounds the sum once, to nearest.
+F16_U = 2.0 ** -11      # unit roundoff of binary16
+F16_SUB = 2.0 ** -25    # largest rounding error in the subnormal range (half its spacing 2^-24)
+
+
+def f16_sum_bound(abs_sum, count):
+    """Per-element bound on |a - b| for two half-precision accumulations a, b
+    of the same ``count`` terms (absolute sum ``abs_sum``, both from the
+    oracle's sum modes) in any two orders and groupings.  Against the exact
+    sum each side is off by at most sum_i (u|v_i| + s) for the terms' rounding
+    plus sum_j (u|P_j| + s) for the adds, with |P_j| <= (1 + u) abs_sum (plus
+    the terms' own rounding): (k + 1) u (1 + 2u) A + 2 k s.  A side that
+    first sums some terms in f32 (the GPU's same-cell combining) adds at most
+    k 2^-23 A.  The bound is that of both sides added."""
+    A = np.asarray(abs_sum, np.float64)
+    k = np.asarray(count, np.float64)
+    one = (k + 1.0) * F16_U * (1.0 + 2.0 * F16_U) * A + 2.0 * k * F16_SUB
+    return 2.0 * one + k * 2.0 ** -23 * A
+
+
+def assert_f16_sum_close(got, want, abs_sum, count, name=""):
+    """Every element of a half-precision accumulation within f16_sum_bound of
+    the oracle's (same terms: the walks are bit-exact), elements nothing was
+    added to exactly zero on both sides."""
+    g = np.asarray(got, np.float32).astype(np.float64)
+    w = np.asarray(want, np.float32).astype(np.float64)
+    assert g.shape == w.shape, (name, g.shape, w.shape)
+    assert np.isfinite(g).all(), f"{name}: non-finite value"
+    k = np.asarray(count, np.float64)
+    assert k.shape == w.shape and (k >= 0).all() and (k == np.round(k)).all(), f"{name}: bad counts"
+    allow = f16_sum_bound(abs_sum, k)
+    d = np.abs(g - w)
+    bad = np.nonzero(d > allow)
+    assert bad[0].size == 0, (f"{name}: {bad[0].size} elements outside the half-precision accumulation bound, "
+                              f"first (got, want, allowed, adds) {list(zip(g[bad][:4], w[bad][:4], allow[bad][:4], k[bad][:4]))}")
+    none = k == 0
+    assert not g[none].any() and not w[none].any(), f"{name}: a value where nothing was added"
+
+
+def f16_train_sums(s, rays, start, thr, fw16, g16, contribution=False, **bwd_kw):
+    """Absolute sums and add counts (oracle sum modes) of the f16-storage
+    training call whose forward outputs are ``fw16`` and upstream gradient
+    ``g16``: the same terms, run with f32 copies of the f16 values (so no sum
+    is itself rounded to half).  Returns (abs_sums, counts), dicts of the
+    backward's outputs, plus "contribution" when asked for."""
+    f32 = lambda a: None if a is None else np.asarray(a).astype(np.float32)  # noqa: E731
+    d, sp = f32(s.diffuse.astype(np.float16)), f32(s.specular.astype(np.float16))
+    kw = {k: (f32(v) if isinstance(v, np.ndarray) and v.dtype == np.float16 else v) for k, v in bwd_kw.items()}
+    out = []
+    for count in (False, True):
+        with core.abs_sums(count=count):
+            r = core.trace_bwd(s.points, d, sp, s.diff_res, s.spec_res, s.density, s.adjacency, s.offsets, rays,
+                               start, f32(fw16["rgba"]), f32(g16), distortion=fw16["distortion"],
+                               W_total=fw16["W_total"], S_total=fw16["S_total"], t_far=fw16["t_far"],
+                               weight_threshold=thr, **kw)
+            if contribution:
+                r["contribution"] = core.trace_fwd(s.points, d, sp, s.diff_res, s.spec_res, s.density, s.adjacency,
+                                                   s.offsets, rays, start, weight_threshold=thr,
+                                                   return_contribution=True)["contribution"]
+        out.append(r)
+    return out[0], out[1]

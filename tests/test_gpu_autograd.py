@@ -102,3 +102,29 @@ def test_missing_rgba_gradient_is_zero(gpu):
     torch.cuda.synchronize()
     H.assert_grad_close(model.primal_points.grad.cpu().numpy(), want[0].cpu().numpy(), "points")
     assert not model.att_diffuse.grad.any()
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_retained_graph_backward_twice_doubles(gpu, fused):
+    """A graph kept with retain_graph=True runs backward again with the same
+    record: every gradient is accumulated twice (the reference keeps its ctx
+    state for the same reason, _wrapper.py:39-84)."""
+    s, rays = _setup(gpu)
+    model = VoroTracing.from_scene(s, device=gpu)
+    rng = np.random.default_rng(5)
+    g = torch.from_numpy(rng.normal(size=tuple(rays.shape[:-1]) + (4,)).astype(np.float32)).to(gpu)
+    run = fused_forward if fused else (lambda m, r, **kw: m(r, **kw))
+    rgba, *_ = run(model, rays)
+    loss = (rgba * g).sum()
+    loss.backward(retain_graph=True)
+    once = [p.grad.clone() for p in (model.primal_points, model.att_diffuse, model.att_specular, model.density)]
+    loss.backward(retain_graph=True)
+    torch.cuda.synchronize()
+    for name, p, g1 in zip(("points", "diffuse", "specular", "density"),
+                           (model.primal_points, model.att_diffuse, model.att_specular, model.density), once):
+        assert g1.abs().max() > 0, name
+        H.assert_grad_close(p.grad.cpu().numpy(), (2 * g1).cpu().numpy(), name)
+    # torch.autograd.grad through the same retained graph again
+    again = torch.autograd.grad(loss, [model.att_diffuse])
+    torch.cuda.synchronize()
+    H.assert_grad_close(again[0].cpu().numpy(), once[1].cpu().numpy(), "diffuse (autograd.grad)")

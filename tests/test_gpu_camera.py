@@ -47,8 +47,8 @@ def test_camera_rays_bit_exact(gpu, kind):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-def _infer(gpu, quantize):
-    s = H.mini_heightfield()
+def _infer(gpu, quantize, R=4):
+    s = H.mini_heightfield() if R == 4 else H.mini_heightfield_r8()
     model = VoroTracing.from_scene(s, device=gpu)
     return VoroTracingInfer(model, sort_morton=True, quantize=quantize)
 
@@ -77,12 +77,14 @@ def test_camera_render_equals_buffer_render(gpu, quantize, kind):
     assert (H.stats_np(st_cam)["integrated"] > 0).mean() > 0.3  # the cameras see the scene
 
 
-def test_camera_render_equals_oracle(gpu):
+@pytest.mark.parametrize("R", [4, 8])
+def test_camera_render_equals_oracle(gpu, R):
     """fp16 camera render of a fisheye rolling-shutter camera against the oracle
-    rendering the oracle's own rays from the oracle's start cells."""
+    rendering the oracle's own rays from the oracle's start cells; R = 8 has
+    the reference's 8x8 diffuse and specular maps."""
     W, Hh = 64, 40
     cams = _cams("fisheye_rolling", W, Hh)[:1]
-    inf = _infer(gpu, "fp16")
+    inf = _infer(gpu, "fp16", R)
     rays = oc.camera_rays(camera.pack_cameras(cams), 1, Hh, W)
     pts = inf.primal_points.cpu().numpy()
     row_origins = rays[0, :, 0, :3]
@@ -90,7 +92,7 @@ def test_camera_render_equals_oracle(gpu):
 
     start_rows = host_ops.nearest_site(pts, row_origins).astype(np.uint32)
     start_rays = np.broadcast_to(start_rows[None, :, None], (1, Hh, W)).copy()
-    want, wst, _ = oc.trace_infer_f16(pts, inf.diffuse_fp16.cpu().numpy(), inf.specular_fp16.cpu().numpy(), 4, 4,
+    want, wst, _ = oc.trace_infer_f16(pts, inf.diffuse_fp16.cpu().numpy(), inf.specular_fp16.cpu().numpy(), R, R,
                                       inf.density.reshape(-1).cpu().numpy(), inf.point_adjacency.cpu().numpy(),
                                       inf.point_adjacency_offsets.cpu().numpy(), inf.adjacent_diff.cpu().numpy(),
                                       rays, start_rays, weight_threshold=0.01, cell_skip_threshold=1e-3,

@@ -6,7 +6,9 @@ inputs (the oracle finishes each in seconds on the box's cores).
 - C2: 262,144-site torus scene, one 800x600 pinhole, fp32 forward + backward
   with every optional input (quantile depths and their gradient, distortion
   gradient, ray error, contribution_alpha_grad), upstream alpha gradient zero
-  and N(0, 1): forward bit for bit, gradients per element.
+  and N(0, 1): forward bit for bit, gradients per element; also with 8x8
+  maps and with f16 map storage (half-precision sums per element within
+  their accumulation bound).
 - C3 / C4: the 1,048,576-site height field, Morton-sorted, fp16 and q8
   inference of whole 1237x822 frames: walk statistics (visit hashes) and alpha
   bit for bit, RGB to one fp16 ulp.
@@ -46,14 +48,20 @@ def _heightfield(n, name):
     return scene.heightfield(0, n, 4, name=name, csr_fn=_gpu_csr)
 
 
-def _train_parity(s, rays, start, thr, gpu, extras, ga_random, label):
+def _train_parity(s, rays, start, thr, gpu, extras, ga_random, label, f16=False):
+    """``f16``: the maps stored as f16 (the reference's __half instantiation,
+    tracing_octmap.cu:474-535): the forward still bit for bit, the half-
+    precision sums (contribution, texture gradients, point_error) per element
+    within the half-precision accumulation bound (helpers.f16_sum_bound)."""
     rng = np.random.default_rng(7)
+    adt = np.float16 if f16 else np.float32
+    diffuse, specular = s.diffuse.astype(adt), s.specular.astype(adt)
     nq = 2 if extras else 0
     q = np.tile(np.float32([0.8, 0.35]), rays.shape[:-1] + (1,)) if extras else None
     _say(f"{label}: oracle forward ({rays.size // 6} rays)")
-    fw = core.trace_fwd(s.points, s.diffuse, s.specular, s.diff_res, s.spec_res, s.density, s.adjacency, s.offsets,
+    fw = core.trace_fwd(s.points, diffuse, specular, s.diff_res, s.spec_res, s.density, s.adjacency, s.offsets,
                         rays, start, depth_quantiles=q, weight_threshold=thr, return_contribution=True)
-    pts, dif, spe = H.to_dev(s.points, gpu), H.to_dev(s.diffuse, gpu), H.to_dev(s.specular, gpu)
+    pts, dif, spe = H.to_dev(s.points, gpu), H.to_dev(diffuse, gpu), H.to_dev(specular, gpu)
     den, adj, off = H.to_dev(s.density, gpu), H.to_dev(s.adjacency, gpu), H.to_dev(s.offsets, gpu)
     rd, sd = H.to_dev(rays, gpu), H.to_dev(start, gpu)
     _say(f"{label}: GPU forward")
@@ -61,7 +69,8 @@ def _train_parity(s, rays, start, thr, gpu, extras, ga_random, label):
         pts, dif, spe, den, adj, off, rd, sd, None if q is None else H.to_dev(q, gpu), thr, 1024, True)
     torch.cuda.synchronize()
     assert np.array_equal(n.cpu().numpy(), fw["n"])
-    assert np.array_equal(rgba.cpu().numpy().view(np.uint32), fw["rgba"].view(np.uint32))
+    bits = np.uint16 if f16 else np.uint32
+    assert np.array_equal(rgba.cpu().numpy().view(bits), fw["rgba"].view(bits))
     for got, key in ((dist, "distortion"), (W, "W_total"), (S, "S_total"), (tf, "t_far")):
         assert np.array_equal(got.cpu().numpy().view(np.uint32), fw[key].view(np.uint32)), key
     if extras:
@@ -72,39 +81,57 @@ def _train_parity(s, rays, start, thr, gpu, extras, ga_random, label):
     # and C5's start region sums tens of thousands of weights per cell (up to
     # 44,800), drifting by up to a few 1e-3 in either order: those sums get a
     # 5e-3 bound, every other cell the 1e-3 one.
-    cg, cw = contrib.cpu().numpy().astype(np.float64), fw["contribution"].astype(np.float64)
-    big = np.abs(cw) > 4096.0
-    H.assert_grad_close(np.where(big, cw, cg), cw, "contribution")
-    assert (np.abs(cg - cw)[big] <= 5e-3 * np.abs(cw[big])).all()
+    if not f16:
+        cg, cw = contrib.cpu().numpy().astype(np.float64), fw["contribution"].astype(np.float64)
+        big = np.abs(cw) > 4096.0
+        H.assert_grad_close(np.where(big, cw, cg), cw, "contribution")
+        assert (np.abs(cg - cw)[big] <= 5e-3 * np.abs(cw[big])).all()
     assert (fw["n"] > 1).mean() > 0.3  # the camera sees the scene
 
-    g = rng.normal(size=rays.shape[:-1] + (4,)).astype(np.float32)
+    g = rng.normal(size=rays.shape[:-1] + (4,)).astype(adt)
     if not ga_random:
         g[..., 3] = 0.0
     dg = rng.normal(size=rays.shape[:-1] + (nq,)).astype(np.float32) * 0.1 if extras else None
     distg = rng.uniform(0, 1, size=rays.shape[:-1] + (1,)).astype(np.float32) if extras else None
-    rerr = rng.uniform(0, 1, size=rays.shape[:-1]).astype(np.float32) if extras else None
+    rerr = rng.uniform(0, 1, size=rays.shape[:-1]).astype(adt) if extras else None
     cag = 0.25 if extras else 0.0
     _say(f"{label}: oracle backward")
-    bwd = functools.partial(core.trace_bwd, s.points, s.diffuse, s.specular, s.diff_res, s.spec_res, s.density,
-                            s.adjacency, s.offsets, rays, start, fw["rgba"], g, depth_quantiles=q,
-                            depth_idx=fw["depth_idx"], depth_grad=dg, ray_error=rerr,
-                            contribution_alpha_grad=cag, distortion=fw["distortion"], distortion_grad=distg,
-                            W_total=fw["W_total"], S_total=fw["S_total"], t_far=fw["t_far"], weight_threshold=thr)
-    want = bwd()
-    with core.abs_sums():  # each element's absolute sum: its summation-order tolerance
-        cond = bwd()
+    kw = dict(depth_quantiles=q, depth_idx=fw["depth_idx"], depth_grad=dg, ray_error=rerr,
+              contribution_alpha_grad=cag, distortion_grad=distg)
+    want = core.trace_bwd(s.points, diffuse, specular, s.diff_res, s.spec_res, s.density, s.adjacency, s.offsets,
+                          rays, start, fw["rgba"], g, distortion=fw["distortion"], W_total=fw["W_total"],
+                          S_total=fw["S_total"], t_far=fw["t_far"], weight_threshold=thr, **kw)
+    # each element's absolute sum (its summation-order tolerance) and, for
+    # half-precision sums, its number of adds
+    cond, count = H.f16_train_sums(s, rays, start, thr, fw, g, contribution=f16, **kw) if f16 else \
+        (_abs_sums(s, rays, start, thr, fw, g, **kw), None)
+    if f16:
+        H.assert_f16_sum_close(contrib.cpu().numpy(), fw["contribution"], cond["contribution"], count["contribution"],
+                               "contribution")
     d = lambda a: None if a is None else H.to_dev(a, gpu)  # noqa: E731
     _say(f"{label}: GPU backward")
     pg, dgd, sgd, deng, rayg, perr = _C.trace_vorotracing_bwd(
         pts, dif, spe, den, adj, off, rd, sd, rgba, d(g), d(q), depth_idx if extras else None, d(dg), d(rerr), cag,
         dist, d(distg), W, S, tf, thr, 1024)
     torch.cuda.synchronize()
-    for got, key in ((pg, "points_grad"), (deng, "density_grad"), (dgd, "diffuse_grad"), (sgd, "specular_grad")):
-        H.assert_grad_close(got.cpu().numpy(), want[key], key, abs_sum=cond[key])
-    assert not rayg.cpu().numpy().any()
+    half = ("diffuse_grad", "specular_grad", "point_error") if f16 else ()
+    outs = [(pg, "points_grad"), (deng, "density_grad"), (dgd, "diffuse_grad"), (sgd, "specular_grad")]
     if extras:
-        H.assert_grad_close(perr.cpu().numpy(), want["point_error"], "point_error", abs_sum=cond["point_error"])
+        outs.append((perr, "point_error"))
+    for got, key in outs:
+        if key in half:
+            H.assert_f16_sum_close(got.cpu().numpy(), want[key], cond[key], count[key], key)
+        else:
+            H.assert_grad_close(got.cpu().numpy(), want[key], key, abs_sum=cond[key])
+    assert not rayg.cpu().numpy().any()
+
+
+def _abs_sums(s, rays, start, thr, fw, g, **kw):
+    with core.abs_sums():
+        return core.trace_bwd(s.points, s.diffuse, s.specular, s.diff_res, s.spec_res, s.density, s.adjacency,
+                              s.offsets, rays, start, fw["rgba"], g, distortion=fw["distortion"],
+                              W_total=fw["W_total"], S_total=fw["S_total"], t_far=fw["t_far"], weight_threshold=thr,
+                              **kw)
 
 
 def test_c1_full_size(gpu):
@@ -122,6 +149,20 @@ def test_c2_full_size(gpu, ga_random):
     model = VoroTracing.from_scene(s, device=gpu)
     assert np.array_equal(model.get_starting_point(H.to_dev(rays, gpu)).cpu().numpy(), start)
     _train_parity(s, rays, start, 0.001, gpu, extras=ga_random, ga_random=ga_random, label="C2")
+
+
+@pytest.mark.parametrize("R,f16", [(8, False), (4, True), (8, True)])
+def test_c2_full_size_maps(gpu, R, f16):
+    """C2 at full size with the reference's 8x8 diffuse and specular maps
+    (its only compiled resolution, tracing_octmap.cu:27-28) and with f16 map
+    storage (the __half instantiation, tracing_octmap.cu:474-535), every
+    optional input on, upstream alpha gradient random."""
+    _say(f"C2: scene (262,144 sites, host qhull), {R}x{R} maps, {'f16' if f16 else 'f32'} storage")
+    s = scene.cached(scene.config2, 0, R=R)
+    assert s.diff_res == R and s.spec_res == R
+    rays = camera.pinhole_rays(800, 600, eye=(0.0, -4.0, 0.0))
+    _train_parity(s, rays, H.start_for(s, rays), 0.001, gpu, extras=True, ga_random=True,
+                  label=f"C2 R{R}{' f16' if f16 else ''}", f16=f16)
 
 
 @functools.lru_cache(maxsize=None)

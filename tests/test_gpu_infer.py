@@ -163,6 +163,21 @@ def test_infer_f16_reference_surface(gpu):
                                       adj.cpu().numpy(), rays, start, weight_threshold=0.01)
     assert got.shape == (64, 96, 4) and got.dtype == torch.float16
     H.assert_infer_rgba(got, want)
+    # the image above went through the in-kernel tiles; the same rays as a flat
+    # batch go through the linear kernel, lane t on ray perm[t]
+    flat = _C.trace_vorotracing_infer(d["points"], d["diffuse4"], d["specular4"], d["density"], d["adjacency"],
+                                      d["offsets"], H.to_dev(rays.reshape(-1, 6), gpu),
+                                      H.to_dev(start.reshape(-1), gpu), adj, perm, 0.01, 1024, 0.0)
+    torch.cuda.synchronize()
+    assert np.array_equal(flat.cpu().numpy().view(np.uint16).reshape(got.shape),
+                          got.cpu().numpy().view(np.uint16))
+    # a lane order that repeats a ray (so leaves another untraced) is refused
+    dup = perm.clone()
+    dup[7] = dup[8]
+    for r_, s_ in ((rays, start), (rays.reshape(-1, 6), start.reshape(-1))):
+        with pytest.raises(RuntimeError, match="ray_perm must be a permutation"):
+            _C.trace_vorotracing_infer(d["points"], d["diffuse4"], d["specular4"], d["density"], d["adjacency"],
+                                       d["offsets"], H.to_dev(r_, gpu), H.to_dev(s_, gpu), adj, dup, 0.01, 1024, 0.0)
 
 
 @pytest.mark.parametrize("R", [4, 8])
@@ -188,6 +203,61 @@ def test_infer_f16_mini_c3_skip(gpu, R):
         H.assert_infer_rgba(got, want)
 
 
+@pytest.mark.parametrize("quantize", ["fp16", "q8"])
+@pytest.mark.parametrize("lanes", ["linear", "tiled"])
+def test_infer_8x8_maps(gpu, quantize, lanes):
+    """The reference's only compiled map resolution, 8x8 diffuse and 8x8
+    specular (tracing_octmap.cu:27-28, vorotracing.py:12-18), on the mini
+    height field: fp16 and q8 through the _C entries, in ray order (no lane
+    order) and in in-kernel tiles (a lane order given), two orbit poses,
+    skip gate 1e-3.  Walk statistics and alpha bit for bit, RGB to one fp16
+    ulp of the oracle."""
+    s = H.mini_heightfield_r8()
+    assert s.diff_res == 8 and s.spec_res == 8
+    d = _dev_scene(s, gpu)
+    adj = _C.trace_vorotracing_prefetch_adj(d["points"], d["adjacency"], d["offsets"])
+    adj_np = adj.cpu().numpy()
+    if quantize == "q8":
+        dq, dsc, dof = host_ops.quantize_u8(s.diffuse, True)
+        sq, ssc, sof = host_ops.quantize_u8(s.specular, True)
+    else:
+        d4, s4 = H.f16_maps(s)
+    for k in (0, 9):
+        print(f"case: {quantize} {lanes} 8x8 maps, pose {k}", flush=True)
+        rays = camera.orbit_rays(k, 160, 120)
+        start = H.start_for(s, rays)
+        rd, sd = H.to_dev(rays, gpu), H.to_dev(start, gpu)
+        perm = torch.arange(rays.size // 6, dtype=torch.int32, device=gpu) if lanes == "tiled" else None
+        if quantize == "q8":
+            want, _ = core.trace_infer_q8(s.points, dq, sq, 8, 8, dsc, dof, ssc, sof, s.density, s.adjacency,
+                                          s.offsets, adj_np, rays, start, weight_threshold=0.01,
+                                          cell_skip_threshold=1e-3, want_stats=True)
+            got = _C.trace_vorotracing_infer_q8(d["points"], H.to_dev(dq, gpu), H.to_dev(sq, gpu), d["density"],
+                                                d["adjacency"], d["offsets"], rd, sd, adj, dsc, dof, ssc, sof, 0.01,
+                                                1024, 1e-3, ray_perm_in=perm)
+        else:
+            want, _, _ = core.trace_infer_f16(s.points, d4, s4, 8, 8, s.density, s.adjacency, s.offsets, adj_np,
+                                              rays, start, weight_threshold=0.01, cell_skip_threshold=1e-3,
+                                              want_stats=True)
+            empty = torch.empty(0, dtype=torch.int32, device=gpu)
+            got = _C.trace_vorotracing_infer(d["points"], d["diffuse4"], d["specular4"], d["density"],
+                                             d["adjacency"], d["offsets"], rd, sd, adj,
+                                             empty if perm is None else perm, 0.01, 1024, 1e-3)
+        torch.cuda.synchronize()
+        H.assert_infer_rgba(got, want)
+        assert (want[..., 3] > 0).mean() > 0.3  # the camera sees the surface
+    # the walk record of the last pose, through the tiled kernel with statistics
+    st = native.new_stats(rays.size // 6, gpu)
+    if quantize == "fp16":
+        want, wst, _ = core.trace_infer_f16(s.points, d4, s4, 8, 8, s.density, s.adjacency, s.offsets, adj_np, rays,
+                                            start, weight_threshold=0.01, cell_skip_threshold=1e-3, want_stats=True)
+        native.infer_f16(d["points"], d["diffuse4"], d["specular4"], d["density"], d["adjacency"], d["offsets"], adj,
+                         rd, sd, weight_threshold=0.01, cell_skip_threshold=1e-3, stats=st,
+                         tiled=(8, 8) if lanes == "tiled" else None)
+        torch.cuda.synchronize()
+        H.assert_stats_equal(H.stats_np(st), wst)
+
+
 @pytest.mark.parametrize("per_channel", [False, True])
 def test_infer_q8_parity(gpu, per_channel):
     s = H.mini_heightfield()
@@ -209,6 +279,15 @@ def test_infer_q8_parity(gpu, per_channel):
     torch.cuda.synchronize()
     H.assert_stats_equal(H.stats_np(stats), wst)
     H.assert_infer_rgba(got, want)
+    # _C with a lane order over these image-shaped rays renders them in
+    # in-kernel tiles: the same image bit for bit
+    perm = torch.from_numpy(np.random.default_rng(2).permutation(rays.size // 6).astype(np.int32)).to(gpu)
+    viac = _C.trace_vorotracing_infer_q8(d["points"], H.to_dev(dq, gpu),
+                                        H.to_dev(sq, gpu), d["density"], d["adjacency"], d["offsets"],
+                                        H.to_dev(rays, gpu), H.to_dev(start, gpu), adj, dsc, dof, ssc, sof, 0.01, 1024,
+                                        1e-3, ray_perm_in=perm)
+    torch.cuda.synchronize()
+    assert np.array_equal(viac.cpu().numpy().view(np.uint16), got.cpu().numpy().view(np.uint16))
 
 
 def test_infer_errors_reference_messages(gpu):

@@ -162,6 +162,11 @@ def test_quantize_and_pad(gpu, per_channel):
     assert np.array_equal(inf.diffuse_q8.cpu().numpy(), q)
     assert np.allclose(np.float32(inf.diff_scale), sc, rtol=0, atol=0)
     assert np.allclose(np.float32(inf.diff_offset), of, rtol=0, atol=0)
+    # values landing exactly on k + 0.5 steps take the even code (torch.round)
+    x, want = H.quant_ties(per_channel)
+    qt, sct, oft = inf._quantize_to_uint8(H.to_dev(x, gpu), per_channel)
+    assert np.all(np.asarray(sct, np.float32) == np.float32(1.0))
+    assert np.array_equal(qt.cpu().numpy(), want)
     f = VoroTracingInfer(model, sort_morton=False, quantize="fp16")
     d4, s4 = H.f16_maps(s)
     assert np.array_equal(f.diffuse_fp16.cpu().numpy().view(np.uint16), d4.view(np.uint16))

@@ -1,0 +1,62 @@
+"""Host-side argument checks that need no GPU: the warm-start guess CSR of
+build_voronoi_adjacency (cuda/__init__.py:16-37's initial_guesses) and the
+permutation check of explicit ray_perm lane orders (tracing_octmap.cu:642-717
+reads ray_perm[t] as the ray of thread t)."""
+import numpy as np
+import pytest
+import torch
+
+from vorotracing_amd import _C, ops
+
+
+def test_guess_csr_accepts_a_csr():
+    adj = torch.tensor([1, 2, 0, 2, 0, 1], dtype=torch.int32)
+    offs = torch.tensor([0, 2, 4, 6], dtype=torch.int64)
+    gofs, gadj = ops.guess_csr(adj, offs, 3, "cpu")
+    assert gofs.dtype == torch.uint32 and gadj.dtype == torch.uint32
+    assert gofs.tolist() == [0, 2, 4, 6] and gadj.tolist() == [1, 2, 0, 2, 0, 1]
+    assert ops.guess_csr(None, None, 3, "cpu") == (None, None)
+    # ids out of range are the builder's to skip, not an error
+    gofs, gadj = ops.guess_csr(torch.tensor([7, 99]), torch.tensor([0, 1, 2, 2]), 3, "cpu")
+    assert gadj.tolist() == [7, 99]
+
+
+@pytest.mark.parametrize("offs,msg", [
+    ([0, 3, 2, 6], "non-decreasing"),      # gofs[1] > gofs[2]: a reversed range reads past the list
+    ([0, 2, 4, 7], "offsets end at 7"),    # beyond the 6 guesses
+    ([0, 2, 4], "must have 4 entries"),
+    ([-1, 2, 4, 6], "non-negative"),
+])
+def test_guess_csr_rejects_bad_offsets(offs, msg):
+    adj = torch.tensor([1, 2, 0, 2, 0, 1])
+    with pytest.raises(ValueError, match=msg):
+        ops.guess_csr(adj, torch.tensor(offs), 3, "cpu")
+    with pytest.raises(ValueError, match="together"):
+        ops.guess_csr(adj, None, 3, "cpu")
+
+
+def test_is_permutation():
+    rng = np.random.default_rng(0)
+    p = torch.from_numpy(rng.permutation(5000).astype(np.int32))
+    assert _C.is_permutation(p, 5000)
+    assert _C.is_permutation(p.view(torch.uint32), 5000)
+    assert not _C.is_permutation(p, 4999)  # wrong length
+    dup = p.clone()
+    dup[10] = dup[11]
+    assert not _C.is_permutation(dup, 5000)
+    for bad in (5000, -1, 2 ** 31 - 1):
+        q = p.clone()
+        q[3] = bad
+        assert not _C.is_permutation(q, 5000), bad
+    assert _C.is_permutation(torch.empty(0, dtype=torch.int32), 0)
+    assert not _C.is_permutation(p.to(torch.int64), 5000)
+
+
+def test_is_permutation_sees_in_place_changes():
+    """The verdict is kept per tensor and re-checked after an in-place change."""
+    p = torch.arange(100, dtype=torch.int32)
+    assert _C.is_permutation(p, 100)
+    p[5] = 6
+    assert not _C.is_permutation(p, 100)
+    p[5] = 5
+    assert _C.is_permutation(p, 100)

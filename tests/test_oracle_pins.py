@@ -9,6 +9,7 @@ import numpy as np
 import pytest
 
 from oracle import core, host_ops
+from tests import helpers as H
 from vorotracing_amd import camera, scene
 
 
@@ -361,6 +362,16 @@ def test_quantize_error_bound(per_channel):
     err = np.abs(deq - x.reshape(500, 16, 3))
     assert (err <= scv[None, None, :] * 0.5 + 1e-6).all()
     assert q.min() == 0 and q.max() == 255
+
+
+@pytest.mark.parametrize("per_channel", [False, True])
+def test_quantize_rounds_ties_to_even(per_channel):
+    """torch.round is half to even (vorotracing.py:495-503): inputs landing
+    exactly on k + 0.5 steps take the even code."""
+    x, want = H.quant_ties(per_channel)
+    q, sc, of = host_ops.quantize_u8(x, per_channel)
+    assert np.all(np.asarray(sc) == np.float32(1.0))
+    assert np.array_equal(q, want)
 
 
 # --------------------------------------------------------------------------- backward vs finite differences

@@ -86,3 +86,38 @@ def test_noalloc_limits(gpu):
     got = _noalloc(one, H.to_dev(q[:5], gpu))
     torch.cuda.synchronize()
     assert got.cpu().numpy().tolist() == [0] * 5
+
+
+def test_noalloc_under_graph_capture(gpu):
+    """The entry captured into a graph (its device set up by a zero-query call
+    first, buffers allocated before the capture): every replay answers the
+    queries the buffer holds at that replay, with eager work and
+    synchronisations between replays."""
+    print("case: vt_nearest_sites_noalloc captured in a graph, 20000 sites, 48 queries", flush=True)
+    pts, q0 = _random_case(20000, 48, 9)
+    pd, qd = H.to_dev(pts, gpu), H.to_dev(q0, gpu)
+    out = torch.full((48,), -7, dtype=torch.int32, device=gpu)
+    _lib.call("vt_nearest_sites_noalloc", None, 0, None, 0, None, None)  # device set-up, no launch
+    side = torch.cuda.Stream(device=gpu)
+    side.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(side):  # eager call on the capture stream before capturing (torch's warm-up rule)
+        _lib.call("vt_nearest_sites_noalloc", pd.data_ptr(), pd.shape[0], qd.data_ptr(), 48, out.data_ptr(),
+                  side.cuda_stream)
+    torch.cuda.current_stream(gpu).wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _lib.call("vt_nearest_sites_noalloc", pd.data_ptr(), pd.shape[0], qd.data_ptr(), 48, out.data_ptr(),
+                  torch.cuda.current_stream(gpu).cuda_stream)
+    for k in range(4):
+        q = _random_case(20000, 48, 100 + k)[1]
+        qd.copy_(H.to_dev(q, gpu))
+        out.fill_(-7)
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        assert np.array_equal(got, host_ops.nearest_site(pts, q)), f"replay {k}"
+        # eager work between replays, on the same scratch array
+        eager = _noalloc(pd, H.to_dev(q[:5], gpu))
+        torch.cuda.synchronize()
+        assert np.array_equal(eager.cpu().numpy(), got[:5])

@@ -81,6 +81,55 @@ def _u32_view(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
+# Explicit ray_perm tensors already checked: id -> (weak reference, _version, num_rays, verdict).
+# Callers pass the same cached tensor every frame (the reference's _tile_perm,
+# vorotracing.py:606-625), so the device check and its host sync run once per
+# tensor and again only after an in-place change.
+_PERM_CHECKED: dict = {}
+
+
+def _remember_perm(t: torch.Tensor, num_rays: int, ok: bool) -> None:
+    import weakref
+
+    if len(_PERM_CHECKED) >= 64:
+        for k in [k for k, v in _PERM_CHECKED.items() if v[0]() is None]:
+            del _PERM_CHECKED[k]
+        if len(_PERM_CHECKED) >= 64:
+            _PERM_CHECKED.clear()
+    _PERM_CHECKED[id(t)] = (weakref.ref(t), t._version, int(num_rays), ok)
+
+
+def is_permutation(perm: torch.Tensor, num_rays: int) -> bool:
+    """Whether ``perm`` (int32 or uint32, read as uint32) holds every index
+    0..num_rays-1 exactly once.  With duplicates some rays would never be
+    traced (their outputs left unwritten) and lanes sharing a ray would race
+    on its outputs, so the entries reject such a ``ray_perm``."""
+    hit = _PERM_CHECKED.get(id(perm))
+    if hit is not None and hit[0]() is perm and hit[1] == perm._version and hit[2] == num_rays:
+        return hit[3]
+    flat = perm.reshape(-1)
+    if flat.numel() != num_rays or flat.dtype not in (torch.int32, torch.uint32):
+        return False
+    if num_rays == 0:
+        ok = True
+    else:
+        wide = flat.view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+        # entries >= num_rays land in the last bin; n entries fill bins 0..n-1
+        # once each only when none is out of range or repeated
+        counts = torch.bincount(wide.clamp_(max=num_rays), minlength=num_rays + 1)
+        ok = bool(counts[:num_rays].eq(1).all().item())
+    _remember_perm(perm, num_rays, ok)
+    return ok
+
+
+def _checked_perm(ray_perm_in: torch.Tensor, num_rays: int) -> torch.Tensor:
+    """uint32 view of an explicit lane order that is a permutation of the rays."""
+    _assert(ray_perm_in.numel() == num_rays, "ray_perm must be empty or have one entry per ray")
+    _assert(ray_perm_in.dtype in (torch.int32, torch.uint32), "ray_perm must have int32 or uint32 dtype")
+    _assert(is_permutation(ray_perm_in, num_rays), "ray_perm must be a permutation of the ray indices")
+    return _u32_view(ray_perm_in.contiguous())
+
+
 def trace_vorotracing_prefetch_adj(points_in, point_adjacency_in, point_adjacency_offsets_in):
     """tracing_octmap.cu:612-640: f16 (adjacency_size + 32, 4) per-face site offsets."""
     points = points_in.contiguous()
@@ -104,7 +153,6 @@ def trace_vorotracing_infer(points_in, diffuse_in, specular_in, density_in, poin
                             weight_threshold: float, max_intersections: int, cell_skip_threshold: float):
     """tracing_octmap.cu:642-717 (fp16 Half4Texel inference).  Returns f16 [..., 4]."""
     points = points_in.contiguous()
-    ray_perm = _u32_view(ray_perm_in.contiguous())
     diffuse = diffuse_in.contiguous()
     specular = specular_in.contiguous()
     density = density_in.contiguous()
@@ -124,18 +172,30 @@ def trace_vorotracing_infer(points_in, diffuse_in, specular_in, density_in, poin
     _check_infer_shapes(num_points, num_rays, diffuse, specular, density, start_point, adjacent_diff, adjacency)
     rd = _map_res(diffuse.shape[-1], 4, "diffuse")
     rs = _map_res(specular.shape[-1], 4, "specular")
-    if ray_perm.numel():
-        _assert(ray_perm.numel() == num_rays, "ray_perm must be empty or have one entry per ray")
-        _assert(ray_perm.dtype == torch.uint32, "ray_perm must have int32 or uint32 dtype")
+    ray_perm = _checked_perm(ray_perm_in, num_rays) if ray_perm_in.numel() else None
     out = torch.empty(_out_shape(rays, 4), dtype=torch.float16, device=rays.device)
     if num_rays == 0:
         return out
+    # A lane order asks for coherent waves.  For image-shaped rays the kernel
+    # tiles the screen itself (8x8 rays per wave64, blocks dealt to the XCDs
+    # in turns), and a ray's result does not depend on which lane traces it,
+    # so any permutation of an image (the reference's 4x8 warp tiles,
+    # vorotracing.py:606-625) renders the same image that way, with no
+    # permutation buffer read.
+    lay = native.screen_layout(rays.shape[:-1]) if ray_perm is not None else None
     with torch.cuda.device(rays.device):
-        _lib.call("vt_trace_infer_f16", points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd, rs,
-                  density.data_ptr(), adjacency.data_ptr(), offsets.data_ptr(), num_points,
-                  adjacent_diff.data_ptr(), rays.data_ptr(), num_rays, start_point.data_ptr(),
-                  ray_perm.data_ptr() if ray_perm.numel() else None, float(weight_threshold),
-                  int(max_intersections), float(cell_skip_threshold), out.data_ptr(), None, _stream(rays.device))
+        if lay is not None:
+            _lib.call("vt_trace_infer_f16_tiled", points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd,
+                      rs, density.data_ptr(), adjacency.data_ptr(), offsets.data_ptr(), num_points,
+                      adjacent_diff.data_ptr(), rays.data_ptr(), lay[0], lay[1], lay[2], native.IMAGE_MIN,
+                      native.IMAGE_MIN, start_point.data_ptr(), float(weight_threshold), int(max_intersections),
+                      float(cell_skip_threshold), out.data_ptr(), None, _stream(rays.device))
+        else:
+            _lib.call("vt_trace_infer_f16", points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd, rs,
+                      density.data_ptr(), adjacency.data_ptr(), offsets.data_ptr(), num_points,
+                      adjacent_diff.data_ptr(), rays.data_ptr(), num_rays, start_point.data_ptr(), _ptr(ray_perm),
+                      float(weight_threshold), int(max_intersections), float(cell_skip_threshold), out.data_ptr(),
+                      None, _stream(rays.device))
     return out
 
 
@@ -187,27 +247,34 @@ def trace_vorotracing_infer_q8(points_in, diffuse_in, specular_in, density_in, p
     rs = _map_res(specular.shape[-1], 3, "specular")
     perm = None
     if ray_perm_in is not None and ray_perm_in.numel():
-        perm = _u32_view(ray_perm_in.contiguous())
-        _assert(perm.numel() == num_rays and perm.dtype == torch.uint32, "ray_perm must have one entry per ray")
+        perm = _checked_perm(ray_perm_in, num_rays)
 
     import ctypes as C
 
     def v3(x):
-        vals = [float(x)] * 3 if isinstance(x, (int, float)) else [float(v) for v in torch.as_tensor(x).reshape(-1)]
-        _assert(len(vals) == 3, "dequantisation scale/offset must be a float or 3 values")
-        return (C.c_float * 3)(*vals)
+        vals = [float(v) for v in torch.as_tensor(x, dtype=torch.float64).reshape(-1)]
+        _assert(len(vals) in (1, 3), "dequantisation scale/offset must be a float or 3 values")
+        return (C.c_float * 3)(*(vals * 3 if len(vals) == 1 else vals))
 
     ds, do, ss, so = v3(diff_scale), v3(diff_offset), v3(spec_scale), v3(spec_offset)
     out = torch.empty(_out_shape(rays, 4), dtype=torch.float16, device=rays.device)
     if num_rays == 0:
         return out
+    scales = [C.cast(v, C.c_void_p) for v in (ds, do, ss, so)]
+    lay = native.screen_layout(rays.shape[:-1]) if perm is not None else None
     with torch.cuda.device(rays.device):
-        _lib.call("vt_trace_infer_q8", points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd, rs,
-                  C.cast(ds, C.c_void_p), C.cast(do, C.c_void_p), C.cast(ss, C.c_void_p), C.cast(so, C.c_void_p),
-                  density.data_ptr(), adjacency.data_ptr(), offsets.data_ptr(), num_points,
-                  adjacent_diff.data_ptr(), rays.data_ptr(), num_rays, start_point.data_ptr(), _ptr(perm),
-                  float(weight_threshold), int(max_intersections), float(cell_skip_threshold), out.data_ptr(), None,
-                  _stream(rays.device))
+        if lay is not None:  # a permuted image: in-kernel tiles, as trace_vorotracing_infer
+            _lib.call("vt_trace_infer_q8_tiled", points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd, rs,
+                      *scales, density.data_ptr(), adjacency.data_ptr(), offsets.data_ptr(), num_points,
+                      adjacent_diff.data_ptr(), rays.data_ptr(), lay[0], lay[1], lay[2], native.IMAGE_MIN,
+                      native.IMAGE_MIN, start_point.data_ptr(), float(weight_threshold), int(max_intersections),
+                      float(cell_skip_threshold), out.data_ptr(), None, _stream(rays.device))
+        else:
+            _lib.call("vt_trace_infer_q8", points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd, rs,
+                      *scales, density.data_ptr(), adjacency.data_ptr(), offsets.data_ptr(), num_points,
+                      adjacent_diff.data_ptr(), rays.data_ptr(), num_rays, start_point.data_ptr(), _ptr(perm),
+                      float(weight_threshold), int(max_intersections), float(cell_skip_threshold), out.data_ptr(),
+                      None, _stream(rays.device))
     return out
 
 
@@ -260,6 +327,7 @@ def ray_order(rays_in, start_point_in, num_points: int) -> torch.Tensor:
     with torch.cuda.device(rays.device):
         _lib.call("vt_ray_order", rays.data_ptr(), start_point.data_ptr(), num_rays, int(num_points), perm.data_ptr(),
                   ws.data_ptr(), _stream(rays.device))
+    _remember_perm(perm, num_rays, True)  # a sort's output order: a permutation by construction
     return perm
 
 
@@ -280,10 +348,11 @@ def _lane_order(rays, start_point, num_points: int, ray_perm):
     """(image_h, image_w, perm tensor or None) for the training entries."""
     num_rays = rays.numel() // 6
     if isinstance(ray_perm, torch.Tensor):
-        perm = _u32_view(ray_perm.contiguous())
-        _assert(perm.dtype == torch.uint32 and perm.numel() == num_rays and perm.device == rays.device,
+        _assert(ray_perm.dtype in (torch.int32, torch.uint32) and ray_perm.numel() == num_rays
+                and ray_perm.device == rays.device,
                 "ray_perm must be a uint32 or int32 tensor with one entry per ray, on the rays' device")
-        return 0, 0, perm
+        _assert(is_permutation(ray_perm, num_rays), "ray_perm must be a permutation of the ray indices")
+        return 0, 0, _u32_view(ray_perm.contiguous())
     if ray_perm is None:
         h, w = _image_dims(rays)
         return h, w, None
@@ -541,7 +610,7 @@ class NNBVH:
         # The scan path's partials come from torch's stream-ordered allocator,
         # not from the handle, so renders on several streams may query at once.
         ws = None
-        if nq * self._n <= _lib.NN_SCAN_PAIRS:
+        if nq <= _lib.NN_SCAN_MAX_QUERIES and nq * self._n <= _lib.NN_SCAN_PAIRS:
             ws = torch.empty(_lib.load().vt_nearest_scan_workspace_size(nq), dtype=torch.uint8, device=q.device)
         with torch.cuda.device(q.device):
             _lib.call("vt_bvh_query_ws", self._h, pts.data_ptr(), pts.size(0), q.data_ptr(), nq, out.data_ptr(),

@@ -47,12 +47,13 @@ SIGNATURES = {
     "vt_ray_order_workspace_size": ([U32], C.c_size_t),
     "vt_ray_order": ([P, P, U32, U32, P, P, P], C.c_int),
     "vt_math_probe": ([I32, P, P, U32, P], C.c_int),
+    "vt_debug_f16_atomic_add": ([P, U32, P, P, U32, P], C.c_int),
     "vt_grad_epilogue": ([P, C.c_uint64, P, C.c_uint64, P, C.c_uint64, P, P, F32, U32, P, P], C.c_int),
     "vt_adam_voro": ([P, P, P, P, P, P, P, P, P, P, P, P, U32, P, P, P, P, U32, U32, P, C.c_double, C.c_double, F32,
                       U32, F32, F32, F32, P], C.c_int),
     "vt_voronoi_workspace_size": ([U32], C.c_size_t),
     "vt_voronoi_build": ([P, U32, P, P, P, P], C.c_int),
-    "vt_voronoi_build_warm": ([P, U32, P, P, P, P, P, P], C.c_int),
+    "vt_voronoi_build_warm": ([P, U32, P, P, U32, P, P, P, P], C.c_int),
     "vt_voronoi_adjacency": ([U32, P, P, P, P], C.c_int),
     "vt_bvh_create": ([P], C.c_int),
     "vt_bvh_destroy": ([P], C.c_int),
@@ -73,9 +74,11 @@ SIGNATURES = {
 }
 
 
-# include/vt_abi.h VT_NN_SCAN_PAIRS: up to this many query-site pairs a start-cell
-# query scans all sites (vt_bvh_query_ws then needs its workspace)
+# include/vt_abi.h VT_NN_SCAN_PAIRS / VT_NN_SCAN_MAX_QUERIES: up to this many
+# query-site pairs, and this many queries, a start-cell query scans all sites
+# (vt_bvh_query_ws then needs its workspace); more queries walk the tree
 NN_SCAN_PAIRS = 1 << 26
+NN_SCAN_MAX_QUERIES = 64
 
 
 class VTError(RuntimeError):

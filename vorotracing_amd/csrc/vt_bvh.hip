@@ -297,12 +297,16 @@ __global__ __launch_bounds__(256) void bvh_query_kernel(const BvhNode *__restric
     out[qi] = (int32_t)best_i;
 }
 
-// Few queries (num_queries * num_points <= NN_SCAN_PAIRS, e.g. the one camera
-// origin of a pinhole frame): the tree walk is a chain of dependent loads on
-// one lane (about 37 us for 1M sites), while a scan of all sites by the whole
-// GPU reads 12 bytes per site once.  Same squared distance and the same
-// lowest-index rule as the tree, so the answer is the same site.
+// Few queries (num_queries * num_points <= NN_SCAN_PAIRS and at most
+// NN_SCAN_MAX_QUERIES, e.g. the one camera origin of a pinhole frame): the
+// tree walk is a chain of dependent loads on one lane (about 37 us for 1M
+// sites), while a scan of all sites by the whole GPU reads 12 bytes per site
+// once.  Same squared distance and the same lowest-index rule as the tree, so
+// the answer is the same site.  The scan launches NN_SCAN_BLOCKS blocks per
+// query whatever the site count, so many queries over few sites walk the tree
+// (each then costs one lane, not 1024 blocks and 8 KiB of partials).
 constexpr uint64_t NN_SCAN_PAIRS = 1ull << 26;
+constexpr uint32_t NN_SCAN_MAX_QUERIES = 64;
 constexpr int NN_SCAN_BLOCK = 256;
 constexpr uint32_t NN_SCAN_BLOCKS = 1024; // per query
 
@@ -500,7 +504,7 @@ static int launch_scan(const float *points, uint32_t num_points, const float *qu
 
 static bool scan_is_faster(const BvhHandle *h, uint32_t num_queries)
 {
-    return !h->force_tree && (uint64_t)num_queries * h->n <= NN_SCAN_PAIRS && num_queries <= 65535u;
+    return !h->force_tree && (uint64_t)num_queries * h->n <= NN_SCAN_PAIRS && num_queries <= NN_SCAN_MAX_QUERIES;
 }
 
 static int query_common(BvhHandle *h, const float *points, uint32_t num_points, const float *queries,
@@ -593,18 +597,23 @@ extern "C" int vt_nearest_sites_noalloc(const float *points, uint32_t num_points
                                         uint32_t num_queries, int32_t *out, vt_stream_t stream)
 {
     clear_error();
-    if (num_queries == 0)
-        return VT_OK;
     VT_REQUIRE(num_queries <= NN_NOALLOC_MAX_QUERIES,
                "vt_nearest_sites_noalloc: %u queries exceed its scratch capacity of %u queries", num_queries,
                NN_NOALLOC_MAX_QUERIES);
-    VT_REQUIRE(num_points > 0, "no points to search");
-    VT_REQUIRE(num_points < 0x7fffffffu, "too many points");
-    VT_REQUIRE(points && queries && out, "null pointer argument");
+    if (num_queries) {
+        VT_REQUIRE(num_points > 0, "no points to search");
+        VT_REQUIRE(num_points < 0x7fffffffu, "too many points");
+        VT_REQUIRE(points && queries && out, "null pointer argument");
+    }
+    // the address lookup comes before the zero-query return, so that a call
+    // with no queries sets the device up (outside a graph capture) and
+    // launches nothing
     uint2 *partial = nullptr;
     int rc = scratch_ptr_current_device(&partial);
     if (rc)
         return rc;
+    if (num_queries == 0)
+        return VT_OK;
     return launch_scan(points, num_points, queries, num_queries, partial, out, as_stream(stream));
 }
 

@@ -5,7 +5,8 @@
 // Attribute maps are (num_points, 3*R*R), texel-major / channel-minor.  The
 // backward scatters 28 gradient values per integrated cell (29 with
 // point_error), lanes of one cell combined in LDS first, with global atomics
-// (f32: hardware global_atomic_add_f32; f16: 32-bit CAS).
+// (f32: hardware global_atomic_add_f32; f16: the packed-f16 global atomic
+// add on the aligned pair holding the half, +0 into the other half).
 #include <type_traits>
 
 #include "vt_internal.h"
@@ -1027,5 +1028,33 @@ extern "C" int vt_trace_bwd(int attr_dtype, const float *points, const void *dif
     cell_grad_out_kernel<<<cblocks, 256, 0, s>>>(reinterpret_cast<const float4 *>(cell_workspace), points_grad,
                                                   density_grad, num_points);
     VT_LAUNCH_CHECK("cell_grad_out_kernel");
+    return VT_OK;
+}
+
+// ---- self-test of the half-precision atomic --------------------------------
+
+namespace vt {
+
+__global__ void f16_atomic_probe_kernel(uint16_t *halves, uint32_t num_halves, const uint32_t *__restrict__ index,
+                                        const float *__restrict__ values, uint32_t n)
+{
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n && index[i] < num_halves)
+        Attr<uint16_t>::add(halves, index[i], values[i]);
+}
+
+} // namespace vt
+
+extern "C" int vt_debug_f16_atomic_add(uint16_t *halves, uint32_t num_halves, const uint32_t *index,
+                                       const float *values, uint32_t n, vt_stream_t stream)
+{
+    clear_error();
+    VT_REQUIRE(num_halves % 2 == 0, "num_halves must be even (whole 32-bit words), got %u", num_halves);
+    if (n == 0)
+        return VT_OK;
+    VT_REQUIRE(halves && index && values, "null pointer argument");
+    VT_REQUIRE(((uintptr_t)halves & 3u) == 0, "halves must be 4-byte aligned");
+    f16_atomic_probe_kernel<<<(n + 255) / 256, 256, 0, as_stream(stream)>>>(halves, num_halves, index, values, n);
+    VT_LAUNCH_CHECK("f16_atomic_probe_kernel");
     return VT_OK;
 }

@@ -826,7 +826,7 @@ __global__ __launch_bounds__(VOR_BLOCK) __attribute__((amdgpu_waves_per_eu(LARGE
     const uint32_t *__restrict__ sorted, const uint32_t *__restrict__ cells, uint32_t ncells,
     uint32_t *__restrict__ lists, uint32_t *__restrict__ big_lists, uint32_t big_cap, uint32_t *__restrict__ big_slot,
     uint32_t *__restrict__ counts, uint32_t *__restrict__ retry, uint32_t *fails, uint32_t n,
-    const uint32_t *__restrict__ gofs, const uint32_t *__restrict__ gadj)
+    const uint32_t *__restrict__ gofs, const uint32_t *__restrict__ gadj, uint32_t gcount)
 {
     __shared__ WaveCell<Cap> c;
     __shared__ uint32_t pick;
@@ -846,8 +846,13 @@ __global__ __launch_bounds__(VOR_BLOCK) __attribute__((amdgpu_waves_per_eu(LARGE
         // them (one nearest-first group): a longer list cut group by group can
         // hold more vertices on the way than the cold band order, and the
         // retry with the large tables runs cold, so guesses never cause a
-        // capacity failure.
-        const bool warm = WARM && !LARGE && gofs[i + 1] - gofs[i] <= 64u;
+        // capacity failure.  A range that runs backwards or past the gcount
+        // guesses is not read (the cell builds cold).
+        bool warm = false;
+        if (WARM && !LARGE) {
+            const uint32_t gb = gofs[i], ge = gofs[i + 1];
+            warm = gb <= ge && ge <= gcount && ge - gb <= 64u;
+        }
         int full = 0;
         int status = wave_voronoi_cell<Cap, WARM>(c, i, points, g, cell_start, sorted, n, warm ? gofs : nullptr,
                                                   gadj, lane, &m, &full);
@@ -1003,11 +1008,12 @@ extern "C" size_t vt_voronoi_workspace_size(uint32_t num_points)
 extern "C" int vt_voronoi_build(const float *points, uint32_t num_points, uint32_t *offsets,
                                 uint32_t *num_adjacency, void *workspace, vt_stream_t stream)
 {
-    return vt_voronoi_build_warm(points, num_points, nullptr, nullptr, offsets, num_adjacency, workspace, stream);
+    return vt_voronoi_build_warm(points, num_points, nullptr, nullptr, 0, offsets, num_adjacency, workspace, stream);
 }
 
 extern "C" int vt_voronoi_build_warm(const float *points, uint32_t num_points, const uint32_t *guess_offsets,
-                                     const uint32_t *guess_adjacency, uint32_t *offsets, uint32_t *num_adjacency,
+                                     const uint32_t *guess_adjacency, uint32_t num_guesses, uint32_t *offsets,
+                                     uint32_t *num_adjacency,
                                      void *workspace, vt_stream_t stream)
 {
     clear_error();
@@ -1077,11 +1083,11 @@ extern "C" int vt_voronoi_build_warm(const float *points, uint32_t num_points, c
     if (guess_offsets)
         voronoi_cells_kernel<VorSmall, false, true><<<wave_blocks(n), VOR_BLOCK, 0, s>>>(
             points, g, w.cell_start, w.vals, w.order, n, w.lists, w.big_lists, bcap, w.big_slot, w.counts, w.retry,
-            w.fails, n, guess_offsets, guess_adjacency);
+            w.fails, n, guess_offsets, guess_adjacency, num_guesses);
     else
         voronoi_cells_kernel<VorSmall, false, false><<<wave_blocks(n), VOR_BLOCK, 0, s>>>(
             points, g, w.cell_start, w.vals, w.order, n, w.lists, w.big_lists, bcap, w.big_slot, w.counts, w.retry,
-            w.fails, n, nullptr, nullptr);
+            w.fails, n, nullptr, nullptr, 0u);
     VT_LAUNCH_CHECK("voronoi_cells_kernel (small)");
     uint32_t f[F_WORDS];
     VT_HIP_CHECK(hipMemcpyAsync(f, w.fails, sizeof(f), hipMemcpyDeviceToHost, s));
@@ -1090,7 +1096,7 @@ extern "C" int vt_voronoi_build_warm(const float *points, uint32_t num_points, c
         // the retry pass runs cold (guesses never cause a capacity failure)
         voronoi_cells_kernel<VorLarge, true, false><<<wave_blocks(f[F_RETRY]), VOR_BLOCK, 0, s>>>(
             points, g, w.cell_start, w.vals, w.retry, f[F_RETRY], w.lists, w.big_lists, bcap, w.big_slot, w.counts,
-            w.retry, w.fails, n, nullptr, nullptr);
+            w.retry, w.fails, n, nullptr, nullptr, 0u);
         VT_LAUNCH_CHECK("voronoi_cells_kernel (large)");
     }
     rc = exclusive_scan_u32(w.counts, offsets, n + 1, w.scan_ws, s);

@@ -148,6 +148,13 @@ class VoroTracing(nn.Module):
         new = torch.ones(o.shape[0], dtype=torch.bool, device=o.device)
         new[1:] = (o[1:] != o[:-1]).any(dim=1)
         run = torch.cumsum(new, 0) - 1
+        runs = int(run[-1].item()) + 1
+        if runs > 1024 and 4 * runs > o.shape[0]:
+            # a shuffled batch of a few cameras (random pixels of random
+            # images): runs are about as many as rays, the distinct origins
+            # few, so query each distinct origin once
+            uniq, inverse = torch.unique(o, dim=0, return_inverse=True)
+            return self.bvh.query(self.primal_points, uniq.contiguous())[inverse].reshape(lead).view(torch.uint32)
         nearest = self.bvh.query(self.primal_points, o[new].contiguous())
         return nearest[run].reshape(lead).view(torch.uint32)
 

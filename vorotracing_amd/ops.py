@@ -36,8 +36,9 @@ class TraceVoroTracing(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_rgba, grad_depth, grad_contribution, _grad_n, _grad_box, grad_distortion):
+        # the record stays on ctx (as the reference keeps its state), so a graph
+        # retained for a second backward gives the same gradients again
         rec = ctx.record
-        ctx.record = None  # the record holds the scene and the forward outputs: drop them with the graph
         up = autograd.upstream_of(rec, grad_rgba, grad_depth, grad_contribution, grad_distortion)
         grads = autograd.clean_(autograd.scene_gradients(rec, up))
         return (*grads, None, None, None, None, None, None, None, None)
@@ -63,6 +64,31 @@ def trace_octmap_infer_q8(points, diffuse_q8, specular_q8, density, adjacency, o
                                          spec_offset, weight_threshold, max_intersections, cell_skip_threshold)
 
 
+def guess_csr(initial_guesses, initial_guesses_offsets, num_sites: int, device):
+    """Checked warm-start CSR for ``build_voronoi_adjacency``: (offsets,
+    adjacency) as contiguous uint32 on ``device``, or (None, None).  The
+    offsets must have ``num_sites + 1`` non-decreasing entries that end
+    within the guess list; ids themselves may be anything (out-of-range ids
+    are skipped by the builder)."""
+    if (initial_guesses is None) != (initial_guesses_offsets is None):
+        raise ValueError("initial_guesses and initial_guesses_offsets are given together or not at all")
+    if initial_guesses is None:
+        return None, None
+    gofs = torch.as_tensor(initial_guesses_offsets, device=device).reshape(-1)
+    gadj = torch.as_tensor(initial_guesses, device=device).reshape(-1)
+    if gofs.numel() != num_sites + 1:
+        raise ValueError(f"initial_guesses_offsets must have {num_sites + 1} entries, got {gofs.numel()}")
+    wide = gofs.to(torch.int64)
+    if bool((wide < 0).any()) or bool((wide[1:] < wide[:-1]).any()):
+        raise ValueError("initial_guesses_offsets must be non-negative and non-decreasing")
+    last = int(wide[-1].item())
+    if last > gadj.numel():
+        raise ValueError(f"initial_guesses has {gadj.numel()} entries, its offsets end at {last}")
+    gofs = wide.to(torch.uint32).contiguous() if gofs.dtype != torch.uint32 else gofs.contiguous()
+    gadj = gadj.to(torch.int64).to(torch.uint32).contiguous() if gadj.dtype != torch.uint32 else gadj.contiguous()
+    return gofs, gadj
+
+
 def build_voronoi_adjacency(points: torch.Tensor, *, debug: bool = False, initial_guesses=None,
                             initial_guesses_offsets=None, chunk_padding: int = 32):
     """cuda/__init__.py:16-46: uint32 CSR (adjacency padded by ``chunk_padding``
@@ -80,19 +106,7 @@ def build_voronoi_adjacency(points: torch.Tensor, *, debug: bool = False, initia
     if dev.type != "cuda":
         raise RuntimeError("build_voronoi_adjacency needs the sites on the GPU")
     n = pts.shape[0]
-    if (initial_guesses is None) != (initial_guesses_offsets is None):
-        raise ValueError("initial_guesses and initial_guesses_offsets are given together or not at all")
-    gofs = gadj = None
-    if initial_guesses is not None:
-        gofs = torch.as_tensor(initial_guesses_offsets, device=dev).reshape(-1)
-        gadj = torch.as_tensor(initial_guesses, device=dev).reshape(-1)
-        if gofs.numel() != n + 1:
-            raise ValueError(f"initial_guesses_offsets must have {n + 1} entries, got {gofs.numel()}")
-        gofs = gofs.to(torch.int64).to(torch.uint32).contiguous() if gofs.dtype != torch.uint32 else gofs.contiguous()
-        gadj = gadj.to(torch.int64).to(torch.uint32).contiguous() if gadj.dtype != torch.uint32 else gadj.contiguous()
-        last = int(gofs[-1].item())
-        if last > gadj.numel():
-            raise ValueError(f"initial_guesses has {gadj.numel()} entries, its offsets end at {last}")
+    gofs, gadj = guess_csr(initial_guesses, initial_guesses_offsets, n, dev)
     lib = _lib.load()
     ws = torch.empty(lib.vt_voronoi_workspace_size(n), dtype=torch.uint8, device=dev)
     offsets = torch.empty(n + 1, dtype=torch.uint32, device=dev)
@@ -100,8 +114,8 @@ def build_voronoi_adjacency(points: torch.Tensor, *, debug: bool = False, initia
     stream = torch.cuda.current_stream(dev).cuda_stream
     with torch.cuda.device(dev):
         _lib.call("vt_voronoi_build_warm", pts.data_ptr(), n, None if gofs is None else gofs.data_ptr(),
-                  None if gadj is None else gadj.data_ptr(), offsets.data_ptr(), ctypes.addressof(m), ws.data_ptr(),
-                  stream)
+                  None if gadj is None else gadj.data_ptr(), 0 if gadj is None else gadj.numel(), offsets.data_ptr(),
+                  ctypes.addressof(m), ws.data_ptr(), stream)
         adjacency = torch.zeros(m.value + chunk_padding, dtype=torch.uint32, device=dev)
         _lib.call("vt_voronoi_adjacency", n, offsets.data_ptr(), adjacency.data_ptr(), ws.data_ptr(), stream)
     return adjacency, offsets, torch.zeros(1, dtype=torch.int32, device=dev)

@@ -44,14 +44,14 @@ class FusedTraceVoroTracing(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_rgba, grad_depth, grad_contribution, _grad_n, _grad_box, grad_distortion):
-        rec, e = ctx.record, ctx.exp_raw
-        ctx.record = ctx.exp_raw = None
+        rec, e = ctx.record, ctx.exp_raw  # kept on ctx: a retained graph can run backward again
         up = autograd.upstream_of(rec, grad_rgba, grad_depth, grad_contribution, grad_distortion)
         pg, dg, sg, ds = autograd.scene_gradients(rec, up)
         raw_grad = torch.empty_like(e)
+        ds = ds.contiguous()
         _lib.call("vt_grad_epilogue", pg.data_ptr(), pg.numel(), dg.data_ptr(), dg.numel(), sg.data_ptr(),
-                  sg.numel(), ds.contiguous().data_ptr(), e.data_ptr(), ctx.activation_scale, e.numel(),
-                  raw_grad.data_ptr(), native._s(e.device))
+                  sg.numel(), ds.data_ptr(), e.data_ptr(), ctx.activation_scale, e.numel(), raw_grad.data_ptr(),
+                  native._s(e.device))
         return (pg, dg, sg, raw_grad, None, None, None, None, None, None, None, None, None)
 
 
