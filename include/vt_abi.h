@@ -86,6 +86,10 @@ int vt_trace_infer_f16(const float *points, const uint16_t *diffuse, const uint1
  * tile_w x tile_h screen tile (tile_w * tile_h == 64), so no permutation
  * buffer is read.  Results are identical to vt_trace_infer_f16 (the lane
  * assignment never changes per-ray results, vorotracing.py:606-625).
+ * tile_order: NULL (tiles in screen order) or the launch order of the
+ * ceil(W/tile_w) * ceil(H/tile_h) * num_images tiles (vt_tile_order);
+ * tile_cost: NULL or one u32 per tile, written with each tile's cost for
+ * vt_tile_order (both extensions).
  */
 int vt_trace_infer_f16_tiled(const float *points, const uint16_t *diffuse, const uint16_t *specular,
                              uint32_t diff_res, uint32_t spec_res, const float *density, const uint32_t *adjacency,
@@ -93,7 +97,7 @@ int vt_trace_infer_f16_tiled(const float *points, const uint16_t *diffuse, const
                              const float *rays, uint32_t num_images, uint32_t image_h, uint32_t image_w,
                              uint32_t tile_h, uint32_t tile_w, const uint32_t *start_point, float weight_threshold,
                              uint32_t max_intersections, float cell_skip_threshold, uint16_t *rgba,
-                             vt_ray_stats *stats, vt_stream_t stream);
+                             const uint32_t *tile_order, uint32_t *tile_cost, vt_ray_stats *stats, vt_stream_t stream);
 
 /*
  * q8 inference render.  Replaces _C.trace_vorotracing_infer_q8
@@ -121,7 +125,8 @@ int vt_trace_infer_q8_tiled(const float *points, const uint8_t *diffuse, const u
                             const uint16_t *adj_diff, const float *rays, uint32_t num_images, uint32_t image_h,
                             uint32_t image_w, uint32_t tile_h, uint32_t tile_w, const uint32_t *start_point,
                             float weight_threshold, uint32_t max_intersections, float cell_skip_threshold,
-                            uint16_t *rgba, vt_ray_stats *stats, vt_stream_t stream);
+                            uint16_t *rgba, const uint32_t *tile_order, uint32_t *tile_cost, vt_ray_stats *stats,
+                            vt_stream_t stream);
 
 /*
  * Cameras for in-kernel ray generation.  Replaces the rays buffer that the
@@ -178,7 +183,8 @@ int vt_trace_infer_f16_camera(const float *points, const uint16_t *diffuse, cons
                               const vt_camera *cameras, uint32_t num_images, uint32_t image_h, uint32_t image_w,
                               uint32_t tile_h, uint32_t tile_w, const uint32_t *start_point, int start_per_row,
                               float weight_threshold, uint32_t max_intersections, float cell_skip_threshold,
-                              uint16_t *rgba, vt_ray_stats *stats, vt_stream_t stream);
+                              uint16_t *rgba, const uint32_t *tile_order, uint32_t *tile_cost, vt_ray_stats *stats,
+                              vt_stream_t stream);
 int vt_trace_infer_q8_camera(const float *points, const uint8_t *diffuse, const uint8_t *specular, uint32_t diff_res,
                              uint32_t spec_res, const float diff_scale[3], const float diff_offset[3],
                              const float spec_scale[3], const float spec_offset[3], const float *density,
@@ -187,7 +193,7 @@ int vt_trace_infer_q8_camera(const float *points, const uint8_t *diffuse, const 
                              uint32_t image_h, uint32_t image_w, uint32_t tile_h, uint32_t tile_w,
                              const uint32_t *start_point, int start_per_row, float weight_threshold,
                              uint32_t max_intersections, float cell_skip_threshold, uint16_t *rgba,
-                             vt_ray_stats *stats, vt_stream_t stream);
+                             const uint32_t *tile_order, uint32_t *tile_cost, vt_ray_stats *stats, vt_stream_t stream);
 
 /*
  * Training forward.  Replaces _C.trace_vorotracing_fwd
@@ -355,6 +361,22 @@ int vt_permute_rows(const void *src, uint32_t rows, uint32_t row_bytes, const ui
  */
 int vt_tile_perm(uint32_t height, uint32_t width, uint32_t tile_h, uint32_t tile_w, int32_t *perm,
                  vt_stream_t stream);
+
+/*
+ * Launch order of the screen tiles of the tiled and camera inference
+ * entries (an extension; the reference launches blocks in screen order).
+ * tile_cost (u32, one per tile) is what such a call wrote to its tile_cost
+ * argument: 18 x the longest walk's steps + the most face records searched by
+ * one ray of the tile.  tile_order (u32, one per tile) receives the tiles by
+ * decreasing cost, equal costs in screen order; a call given it launches
+ * tile tile_order[s] in slot s.  Launched longest first, a frame no longer
+ * ends with a few long tiles running on an otherwise idle GPU.  Any order
+ * gives bit-identical images (a ray's result does not depend on its lane).
+ * workspace: vt_tile_order_workspace_size(tiles) bytes, 4-byte aligned.
+ */
+size_t vt_tile_order_workspace_size(uint32_t tiles);
+int vt_tile_order(const uint32_t *tile_cost, uint32_t tiles, uint32_t *tile_order, void *workspace,
+                  vt_stream_t stream);
 
 /*
  * q8 quantisation.  Replaces VoroTracingInfer._quantize_to_uint8

@@ -12,7 +12,7 @@ import torch
 
 from oracle import core, host_ops
 from tests import helpers as H
-from vorotracing_amd import _C, camera, native
+from vorotracing_amd import _C, _lib, camera, native
 from vorotracing_amd.infer import VoroTracingInfer
 from vorotracing_amd.model import VoroTracing
 
@@ -401,3 +401,73 @@ def test_render_frames_overlapped_equal_serial(gpu, in_flight):
     assert len(got) == len(want)
     for a, b in zip(got, want):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def _strip_tiles(Hh, W, strip=4):
+    """Tile index (4-wide vertical strips of 8x8 tiles, row by row inside a
+    strip, as the tiled kernels number them) of every pixel of an H x W image."""
+    TX, TY = (W + 7) // 8, (Hh + 7) // 8
+    yy, xx = np.meshgrid(np.arange(Hh), np.arange(W), indexing="ij")
+    tx, ty = xx // 8, yy // 8
+    s = tx // strip
+    w = np.where((s + 1) * strip <= TX, strip, TX - s * strip)
+    return (s * strip * TY + ty * w + (tx - s * strip)).reshape(-1), TX * TY
+
+
+def test_tile_order_sorts_by_cost(gpu):
+    """vt_tile_order: tiles by decreasing cost (quantised to cost >> 2),
+    equal costs in tile order, against numpy's stable argsort."""
+    rng = np.random.default_rng(3)
+    for tiles, hi in ((1, 10), (777, 50), (16095, 40000), (70000, 1 << 20)):
+        cost = rng.integers(0, hi, tiles).astype(np.uint32)
+        cost[: tiles // 3] = cost[0]  # many ties
+        c = H.to_dev(cost, gpu)
+        order = torch.empty(tiles, dtype=torch.uint32, device=gpu)
+        ws = torch.empty(int(_lib.load().vt_tile_order_workspace_size(tiles)), dtype=torch.uint8, device=gpu)
+        _lib.call("vt_tile_order", c.data_ptr(), tiles, order.data_ptr(), ws.data_ptr(),
+                  torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        key = 65535 - np.minimum(cost >> 2, 65535)
+        assert np.array_equal(order.cpu().numpy().astype(np.int64), np.argsort(key, kind="stable")), tiles
+
+
+def test_tile_order_and_costs_of_a_render(gpu):
+    """A tiled render launched in any tile order gives the same image bit for
+    bit; the tile costs it writes are 18 x the longest walk + the most face
+    records of a ray of the tile (from the same launch's walk statistics)."""
+    s = H.mini_heightfield()
+    d = _dev_scene(s, gpu)
+    adj = native.prefetch(d["points"], d["adjacency"], d["offsets"])
+    Hh, W = 100, 132
+    rays = H.to_dev(camera.orbit_rays(3, W, Hh), gpu)
+    start = H.to_dev(H.start_for(s, rays.cpu().numpy()), gpu)
+    tile_of, tiles = _strip_tiles(Hh, W)
+    args = (d["points"], d["diffuse4"], d["specular4"], d["density"], d["adjacency"], d["offsets"], adj, rays, start)
+    ref = native.infer_f16(*args, weight_threshold=0.01, cell_skip_threshold=1e-3, tiled=(8, 8))
+    sch = native.TileSchedule(tiles, gpu)
+    st = native.new_stats(Hh * W, gpu)
+    got = native.infer_f16(*args, weight_threshold=0.01, cell_skip_threshold=1e-3, tiled=(8, 8), schedule=sch,
+                           stats=st)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    stn = H.stats_np(st)
+    nmax, fmax = np.zeros(tiles, np.int64), np.zeros(tiles, np.int64)
+    np.maximum.at(nmax, tile_of, stn["n"].astype(np.int64))
+    np.maximum.at(fmax, tile_of, stn["faces"].astype(np.int64))
+    assert np.array_equal(sch.cost.cpu().numpy().astype(np.int64), 18 * nmax + fmax)
+    # the same rays again: launched by decreasing cost, same image
+    for _ in range(2):
+        again = native.infer_f16(*args, weight_threshold=0.01, cell_skip_threshold=1e-3, tiled=(8, 8), schedule=sch)
+        torch.cuda.synchronize()
+        assert torch.equal(again.view(torch.int16), ref.view(torch.int16))
+    want = np.argsort(65535 - np.minimum((18 * nmax + fmax) >> 2, 65535), kind="stable")
+    assert np.array_equal(sch.order.cpu().numpy().astype(np.int64), want)
+    # a random launch order through the C ABI: same image
+    order = H.to_dev(np.random.default_rng(5).permutation(tiles).astype(np.uint32), gpu)
+    out = torch.empty_like(ref)
+    _lib.call("vt_trace_infer_f16_tiled", d["points"].data_ptr(), d["diffuse4"].data_ptr(), d["specular4"].data_ptr(),
+              4, 4, d["density"].data_ptr(), d["adjacency"].data_ptr(), d["offsets"].data_ptr(), s.num_points,
+              adj.data_ptr(), rays.data_ptr(), 1, Hh, W, 8, 8, start.data_ptr(), 0.01, 1024, 1e-3, out.data_ptr(),
+              order.data_ptr(), None, None, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))

@@ -122,6 +122,17 @@ def is_permutation(perm: torch.Tensor, num_rays: int) -> bool:
     return ok
 
 
+# Tile launch schedules of the drop-in inference entries (native.TileSchedule),
+# keyed by the caller's ray_perm tensor (the reference caches one per
+# resolution, vorotracing.py:606-625), the image shape and the stream.
+_SCHEDULES: dict = {}
+
+
+def _drop_in_schedule(ray_perm_in: torch.Tensor, lay, device) -> "native.TileSchedule":
+    key = (id(ray_perm_in), tuple(lay), _stream(device))
+    return native.schedule_for(_SCHEDULES, key, native.num_tiles(*lay), device)
+
+
 def _checked_perm(ray_perm_in: torch.Tensor, num_rays: int) -> torch.Tensor:
     """uint32 view of an explicit lane order that is a permutation of the rays."""
     _assert(ray_perm_in.numel() == num_rays, "ray_perm must be empty or have one entry per ray")
@@ -185,11 +196,13 @@ def trace_vorotracing_infer(points_in, diffuse_in, specular_in, density_in, poin
     lay = native.screen_layout(rays.shape[:-1]) if ray_perm is not None else None
     with torch.cuda.device(rays.device):
         if lay is not None:
+            order, cost = _drop_in_schedule(ray_perm_in, lay, rays.device).launch_args(
+                _stream(rays.device), native.frame_key(rays_in))
             _lib.call("vt_trace_infer_f16_tiled", points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd,
                       rs, density.data_ptr(), adjacency.data_ptr(), offsets.data_ptr(), num_points,
                       adjacent_diff.data_ptr(), rays.data_ptr(), lay[0], lay[1], lay[2], native.IMAGE_MIN,
                       native.IMAGE_MIN, start_point.data_ptr(), float(weight_threshold), int(max_intersections),
-                      float(cell_skip_threshold), out.data_ptr(), None, _stream(rays.device))
+                      float(cell_skip_threshold), out.data_ptr(), order, cost, None, _stream(rays.device))
         else:
             _lib.call("vt_trace_infer_f16", points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd, rs,
                       density.data_ptr(), adjacency.data_ptr(), offsets.data_ptr(), num_points,
@@ -264,11 +277,13 @@ def trace_vorotracing_infer_q8(points_in, diffuse_in, specular_in, density_in, p
     lay = native.screen_layout(rays.shape[:-1]) if perm is not None else None
     with torch.cuda.device(rays.device):
         if lay is not None:  # a permuted image: in-kernel tiles, as trace_vorotracing_infer
+            order, cost = _drop_in_schedule(ray_perm_in, lay, rays.device).launch_args(
+                _stream(rays.device), native.frame_key(rays_in))
             _lib.call("vt_trace_infer_q8_tiled", points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd, rs,
                       *scales, density.data_ptr(), adjacency.data_ptr(), offsets.data_ptr(), num_points,
                       adjacent_diff.data_ptr(), rays.data_ptr(), lay[0], lay[1], lay[2], native.IMAGE_MIN,
                       native.IMAGE_MIN, start_point.data_ptr(), float(weight_threshold), int(max_intersections),
-                      float(cell_skip_threshold), out.data_ptr(), None, _stream(rays.device))
+                      float(cell_skip_threshold), out.data_ptr(), order, cost, None, _stream(rays.device))
         else:
             _lib.call("vt_trace_infer_q8", points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd, rs,
                       *scales, density.data_ptr(), adjacency.data_ptr(), offsets.data_ptr(), num_points,

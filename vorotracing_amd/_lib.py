@@ -25,17 +25,17 @@ SIGNATURES = {
     "vt_prefetch_adj": ([P, U32, P, U32, P, P, P], C.c_int),
     "vt_trace_infer_f16": ([P, P, P, U32, U32, P, P, P, U32, P, P, U32, P, P, F32, U32, F32, P, P, P], C.c_int),
     "vt_trace_infer_f16_tiled": (
-        [P, P, P, U32, U32, P, P, P, U32, P, P, U32, U32, U32, U32, U32, P, F32, U32, F32, P, P, P], C.c_int),
+        [P, P, P, U32, U32, P, P, P, U32, P, P, U32, U32, U32, U32, U32, P, F32, U32, F32, P, P, P, P, P], C.c_int),
     "vt_trace_infer_q8": (
         [P, P, P, U32, U32, P, P, P, P, P, P, P, U32, P, P, U32, P, P, F32, U32, F32, P, P, P], C.c_int),
     "vt_trace_infer_q8_tiled": (
-        [P, P, P, U32, U32, P, P, P, P, P, P, P, U32, P, P, U32, U32, U32, U32, U32, P, F32, U32, F32, P, P, P],
+        [P, P, P, U32, U32, P, P, P, P, P, P, P, U32, P, P, U32, U32, U32, U32, U32, P, F32, U32, F32, P, P, P, P, P],
         C.c_int),
     "vt_camera_rays": ([P, U32, U32, U32, P, P], C.c_int),
     "vt_trace_infer_f16_camera": (
-        [P, P, P, U32, U32, P, P, P, U32, P, P, U32, U32, U32, U32, U32, P, I32, F32, U32, F32, P, P, P], C.c_int),
+        [P, P, P, U32, U32, P, P, P, U32, P, P, U32, U32, U32, U32, U32, P, I32, F32, U32, F32, P, P, P, P, P], C.c_int),
     "vt_trace_infer_q8_camera": (
-        [P, P, P, U32, U32, P, P, P, P, P, P, P, U32, P, P, U32, U32, U32, U32, U32, P, I32, F32, U32, F32, P, P, P],
+        [P, P, P, U32, U32, P, P, P, P, P, P, P, U32, P, P, U32, U32, U32, U32, U32, P, I32, F32, U32, F32, P, P, P, P, P],
         C.c_int),
     "vt_trace_fwd": (
         [I32, P, P, P, U32, U32, P, P, U32, P, U32, P, U32, U32, U32, P, P, U32, P, F32, U32, P, P, P, P, P, P, P, P, P, P, P,
@@ -65,6 +65,8 @@ SIGNATURES = {
     "vt_bvh_debug_stack_limit": ([P, U32, I32], C.c_int),
     "vt_nearest_sites_noalloc": ([P, U32, P, U32, P, P], C.c_int),
     "vt_tile_perm": ([U32, U32, U32, U32, P, P], C.c_int),
+    "vt_tile_order_workspace_size": ([U32], C.c_size_t),
+    "vt_tile_order": ([P, U32, P, P, P], C.c_int),
     "vt_morton_workspace_size": ([U32, U32], C.c_size_t),
     "vt_morton_reorder": ([P, U32, P, U32, P, P, P, P, P, P, P], C.c_int),
     "vt_permute_rows": ([P, U32, U32, P, P, P], C.c_int),

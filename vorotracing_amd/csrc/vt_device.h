@@ -115,6 +115,15 @@ __device__ __forceinline__ void wave_lds_sync()
     __builtin_amdgcn_wave_barrier();
 }
 
+// Largest x over the 64 lanes of the wave (every lane must be active).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x)
+{
+#pragma unroll
+    for (int k = 32; k >= 1; k >>= 1)
+        x = max(x, (uint32_t)__shfl_xor((int)x, k));
+    return x;
+}
+
 // Number of set bits of m below the calling lane.
 __device__ __forceinline__ uint32_t lane_rank(uint64_t m)
 {
@@ -271,8 +280,10 @@ constexpr uint32_t STATS_WORDS = sizeof(vt_ray_stats) / 4;
 static_assert(sizeof(vt_ray_stats) == 4 * (8 + VT_STATS_LOG), "vt_ray_stats is 8 counter words and the log");
 
 template <bool ON> struct StatsAcc {
+    uint32_t faces = 0; // face records searched (a launch-order cost; dropped when unread)
     __device__ __forceinline__ void begin(void *, uint32_t) {}
-    __device__ __forceinline__ void visit(uint32_t, uint32_t) {}
+    __device__ __forceinline__ void visit(uint32_t, uint32_t nf) { faces += nf; }
+    __device__ __forceinline__ uint32_t face_count() const { return faces; }
     __device__ __forceinline__ void exit() {}
     __device__ __forceinline__ void integrate() {}
     __device__ __forceinline__ void shade() {}
@@ -296,6 +307,7 @@ template <> struct StatsAcc<true> {
         s.faces += nf;
         s.hash = (s.hash ^ (uint64_t)cell) * 1099511628211ull;
     }
+    __device__ __forceinline__ uint32_t face_count() const { return s.faces; }
     __device__ __forceinline__ void exit() { s.exits++; }
     __device__ __forceinline__ void integrate() { s.integrated++; }
     __device__ __forceinline__ void shade() { s.shaded++; }

@@ -395,6 +395,48 @@ extern "C" int vt_tile_perm(uint32_t height, uint32_t width, uint32_t tile_h, ui
     return VT_OK;
 }
 
+// ---- launch order of screen tiles ------------------------------------------
+
+namespace vt {
+
+// keys of the stable ascending sort that lists tiles by decreasing cost
+// (costs quantised to 16 bits: 4 units, far below the spread of a frame's
+// tile costs, which run in the thousands)
+constexpr uint32_t TILE_ORDER_BITS = 16;
+
+__global__ void tile_order_keys_kernel(const uint32_t *__restrict__ cost, uint32_t tiles, uint32_t *__restrict__ keys,
+                                       uint32_t *__restrict__ order)
+{
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= tiles)
+        return;
+    const uint32_t top = (1u << TILE_ORDER_BITS) - 1u;
+    keys[t] = top - min(cost[t] >> 2, top);
+    order[t] = t;
+}
+
+} // namespace vt
+
+extern "C" size_t vt_tile_order_workspace_size(uint32_t tiles)
+{
+    return ((size_t)tiles + radix_sort_workspace_words(tiles)) * 4;
+}
+
+extern "C" int vt_tile_order(const uint32_t *tile_cost, uint32_t tiles, uint32_t *tile_order, void *workspace,
+                             vt_stream_t stream)
+{
+    clear_error();
+    if (tiles == 0)
+        return VT_OK;
+    VT_REQUIRE(tile_cost && tile_order && workspace, "null pointer argument");
+    VT_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 4 == 0, "workspace must be 4-byte aligned");
+    hipStream_t s = as_stream(stream);
+    uint32_t *keys = static_cast<uint32_t *>(workspace);
+    tile_order_keys_kernel<<<(tiles + 255) / 256, 256, 0, s>>>(tile_cost, tiles, keys, tile_order);
+    VT_LAUNCH_CHECK("tile_order_keys_kernel");
+    return radix_sort_pairs(keys, tile_order, tiles, (int)TILE_ORDER_BITS, keys + tiles, s);
+}
+
 extern "C" size_t vt_ray_order_workspace_size(uint32_t num_rays)
 {
     return ((size_t)num_rays + radix_sort_workspace_words(num_rays)) * 4;

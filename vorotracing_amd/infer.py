@@ -16,7 +16,7 @@ from typing import Literal, Optional
 import numpy as np
 import torch
 
-from . import _C, _lib, native, ops
+from . import _C, _lib, camera, native, ops
 
 
 class VoroTracingInfer:
@@ -24,6 +24,9 @@ class VoroTracingInfer:
     ``vorotracing_amd.model.VoroTracing`` (or any object with its attributes)."""
 
     TILE = (8, 8)
+    # launch the tiles of a repeated image shape by the previous frame's tile
+    # costs (native.TileSchedule; images are bit-identical either way)
+    adaptive_tile_order = True
 
     def __init__(self, model, sort_morton: bool = True, quantize: Literal["fp16", "q8"] = "fp16",
                  per_channel_q8: bool = False):
@@ -95,6 +98,14 @@ class VoroTracingInfer:
 
     def _stream(self):
         return torch.cuda.current_stream(self.device).cuda_stream
+
+    def _schedule(self, images: int, H: int, W: int) -> Optional[native.TileSchedule]:
+        """The tile launch schedule of this image shape on the current stream."""
+        if not self.adaptive_tile_order:
+            return None
+        cache = self.__dict__.setdefault("_schedules", {})
+        return native.schedule_for(cache, (int(images), int(H), int(W), self._stream()),
+                                   native.num_tiles(images, H, W, *self.TILE), self.device)
 
     def _quantize_to_uint8(self, tensor, per_channel=False):
         """vorotracing.py:495-503 -> (q u8, scale, offset); per-channel returns 3-lists."""
@@ -262,7 +273,8 @@ class VoroTracingInfer:
                                 self.point_adjacency, self.point_adjacency_offsets, self.adjacent_diff, rays,
                                 start_point, weight_threshold=weight_threshold, max_intersections=max_intersections,
                                 cell_skip_threshold=cell_skip_threshold, stats=stats,
-                                tiled=self.TILE if image else None)
+                                tiled=self.TILE if image else None,
+                                schedule=self._schedule(*native.image_dims(rays)) if image else None)
 
     def camera_start_points(self, cameras, camera_buffer=None):
         """Start cells of a camera batch: one LBVH query on each camera's centre, or
@@ -295,8 +307,11 @@ class VoroTracingInfer:
             per_row = start_point.numel() == B * H and any(c.rolling_shutter for c in cams)
         out = torch.empty((B, H, W, 4), dtype=torch.float16, device=self.device)
         sp = native._s(self.device)
-        common = (float(weight_threshold), int(max_intersections), float(cell_skip_threshold), out.data_ptr(),
-                  native._p(stats), sp)
+        sch = self._schedule(B, H, W)
+        frame = camera.pack_cameras(cams)  # host-side records: no device read
+        order, cost = sch.launch_args(sp, frame) if sch is not None else (None, None)
+        common = (float(weight_threshold), int(max_intersections), float(cell_skip_threshold), out.data_ptr(), order,
+                  cost, native._p(stats), sp)
         if self.quantize == "q8":
             def v3(x):
                 vals = [float(x)] * 3 if isinstance(x, (int, float)) else [float(v) for v in x]
@@ -337,12 +352,15 @@ class VoroTracingInfer:
         sp = native._s(rays.device)
         if image:
             B, H, W = native.image_dims(rays)
+            sch = self._schedule(B, H, W)
+            frame = native.frame_key(rays)
+            order, cost = sch.launch_args(sp, frame) if sch is not None else (None, None)
             _lib.call("vt_trace_infer_q8_tiled", self.primal_points.data_ptr(), self.diffuse_q8.data_ptr(),
                       self.specular_q8.data_ptr(), rd, rs, *keep, self.density.data_ptr(),
                       self.point_adjacency.data_ptr(), self.point_adjacency_offsets.data_ptr(),
                       self.primal_points.shape[0], self.adjacent_diff.data_ptr(), rays.data_ptr(), B, H, W,
                       self.TILE[0], self.TILE[1], start_point.data_ptr(), float(thr), int(max_int), float(skip),
-                      out.data_ptr(), native._p(stats), sp)
+                      out.data_ptr(), order, cost, native._p(stats), sp)
         else:
             _lib.call("vt_trace_infer_q8", self.primal_points.data_ptr(), self.diffuse_q8.data_ptr(),
                       self.specular_q8.data_ptr(), rd, rs, *keep, self.density.data_ptr(),

@@ -104,12 +104,68 @@ def image_dims(rays) -> Tuple[int, int, int]:
     return lay
 
 
+def num_tiles(images: int, H: int, W: int, tile_h: int = IMAGE_MIN, tile_w: int = IMAGE_MIN) -> int:
+    return int(images) * ((int(H) + tile_h - 1) // tile_h) * ((int(W) + tile_w - 1) // tile_w)
+
+
+class TileSchedule:
+    """Launch order of the screen tiles of a frame rendered again (the same
+    rays or cameras on one stream; vt_tile_order): each launch records its
+    tiles' costs, and the next render of the same frame launches the tiles
+    by decreasing cost, so that it does not end with a few long tiles on an
+    otherwise idle GPU (C3, one view rendered repeatedly: 2-7 % per frame).
+    A different frame launches in screen order: the costs of the previous
+    view mispredict a moved camera's (a 32-pose orbit ran 10 % slower with
+    them).  Images are bit-identical in any order.  One schedule per stream:
+    a launch reads the costs the previous launch on its stream wrote."""
+
+    def __init__(self, tiles: int, device):
+        self.tiles = int(tiles)
+        self.cost = torch.zeros(self.tiles, dtype=torch.uint32, device=device)
+        self.order = torch.empty(self.tiles, dtype=torch.uint32, device=device)
+        self.ws = torch.empty(int(_lib.load().vt_tile_order_workspace_size(self.tiles)), dtype=torch.uint8,
+                              device=device)
+        self.frame = None  # the frame whose costs self.cost holds
+
+    def launch_args(self, stream: int, frame):
+        """(tile_order, tile_cost) pointers for the next launch on ``stream``
+        of ``frame`` (a hashable identity of the launch's rays or cameras)."""
+        order = None
+        if frame is not None and frame == self.frame:
+            _lib.call("vt_tile_order", self.cost.data_ptr(), self.tiles, self.order.data_ptr(), self.ws.data_ptr(),
+                      stream)
+            order = self.order.data_ptr()
+        self.frame = frame
+        return order, self.cost.data_ptr()
+
+
+def frame_key(t: torch.Tensor):
+    """Identity of a frame's rays: the tensor object, its storage and its
+    in-place version (rays rendered again unchanged keep all three).  The
+    schedule only moves work between lanes, so a stale key costs time, not
+    correctness."""
+    return (id(t), t.data_ptr(), t._version)
+
+
+def schedule_for(cache: dict, key, tiles: int, device, limit: int = 16) -> TileSchedule:
+    """The TileSchedule of ``key`` in ``cache`` (created on first use; the
+    cache keeps the ``limit`` most recent)."""
+    sch = cache.pop(key, None)
+    if sch is None or sch.tiles != tiles:
+        sch = TileSchedule(tiles, device)
+    cache[key] = sch
+    while len(cache) > limit:
+        cache.pop(next(iter(cache)))
+    return sch
+
+
 def infer_f16(points, diffuse4, specular4, density, adjacency, offsets, adj_diff, rays, start_point, ray_perm=None,
               weight_threshold=0.001, max_intersections=1024, cell_skip_threshold=0.0, stats=None, out=None,
-              tiled=None, stream=None):
+              tiled=None, stream=None, schedule: Optional[TileSchedule] = None):
     """fp16 inference.  ``tiled=(tile_h, tile_w)`` uses the in-kernel wave
     tiling over the images of screen_layout (any (..., H, W, 6) when the
-    layout finds none)."""
+    layout finds none), with ``schedule`` (a TileSchedule of this image
+    shape and stream) the tiles' launch order."""
     rd = map_res(diffuse4.shape[-1], 4)
     rs = map_res(specular4.shape[-1], 4)
     nr = rays.numel() // 6
@@ -118,10 +174,12 @@ def infer_f16(points, diffuse4, specular4, density, adjacency, offsets, adj_diff
     dev = rays.device
     if tiled is not None:
         B, H, W = image_dims(rays)
+        sp = _s(dev, stream)
+        order, cost = schedule.launch_args(sp, frame_key(rays)) if schedule is not None else (None, None)
         _lib.call("vt_trace_infer_f16_tiled", points.data_ptr(), diffuse4.data_ptr(), specular4.data_ptr(), rd, rs,
                   density.data_ptr(), adjacency.data_ptr(), offsets.data_ptr(), points.size(0), adj_diff.data_ptr(),
                   rays.data_ptr(), B, H, W, tiled[0], tiled[1], start_point.data_ptr(), float(weight_threshold),
-                  int(max_intersections), float(cell_skip_threshold), out.data_ptr(), _p(stats), _s(dev, stream))
+                  int(max_intersections), float(cell_skip_threshold), out.data_ptr(), order, cost, _p(stats), sp)
     else:
         _lib.call("vt_trace_infer_f16", points.data_ptr(), diffuse4.data_ptr(), specular4.data_ptr(), rd, rs,
                   density.data_ptr(), adjacency.data_ptr(), offsets.data_ptr(), points.size(0), adj_diff.data_ptr(),
