@@ -223,8 +223,8 @@ int vt_trace_fwd(int attr_dtype, const float *points, const void *diffuse, const
                  uint32_t num_quantiles, const float *depth_quantiles,
                  float weight_threshold, uint32_t max_intersections, void *rgba, float *depth, uint32_t *depth_idx,
                  void *contribution, uint32_t *num_intersections, float *distortion, float *W_total,
-                 float *S_total, float *t_far, uint16_t *adj_diff_workspace, vt_ray_stats *stats,
-                 vt_stream_t stream);
+                 float *S_total, float *t_far, uint16_t *adj_diff_workspace, const uint32_t *tile_order,
+                 uint32_t *tile_cost, vt_ray_stats *stats, vt_stream_t stream);
 
 /*
  * Training backward.  Replaces _C.trace_vorotracing_bwd
@@ -259,7 +259,8 @@ int vt_trace_bwd(int attr_dtype, const float *points, const void *diffuse, const
                  const float *distortion_grad, const float *W_total, const float *S_total, const float *t_far,
                  float weight_threshold, uint32_t max_intersections, float *points_grad, void *diffuse_grad,
                  void *specular_grad, float *density_grad, void *point_error, uint16_t *adj_diff_workspace,
-                 int adj_diff_ready, float *cell_workspace, vt_ray_stats *stats, vt_stream_t stream);
+                 int adj_diff_ready, float *cell_workspace, const uint32_t *tile_order, vt_ray_stats *stats,
+                 vt_stream_t stream);
 
 /*
  * Coherent lane order for a flat training batch (an extension: the reference

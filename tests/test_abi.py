@@ -45,7 +45,7 @@ def test_binding_matches_header_arity():
 
 def test_host_only_entries():
     lib = _lib.load()
-    assert lib.vt_abi_version() == 8
+    assert lib.vt_abi_version() == 9
     assert isinstance(lib.vt_last_error(), bytes)
     assert lib.vt_quantize_workspace_size() > 0
     assert lib.vt_morton_workspace_size(1000, 16000) >= lib.vt_morton_workspace_size(10, 160) > 0

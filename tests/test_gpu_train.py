@@ -391,3 +391,57 @@ def test_f16_atomic_same_half_exact_in_any_order(gpu):
     want = (k.sum(axis=1) * 2.0 ** -24)
     assert (want < 2.0 ** -13).all()
     assert np.array_equal(got.astype(np.float64), want), f"{got[:6]} vs {want[:6]}"
+
+
+def test_backward_in_forward_cost_order(gpu):
+    """The backward of a forward over the same rays tensor launches its tiles
+    by the forward's recorded costs (18 x longest walk + most face records per
+    tile): per-ray walk statistics equal the screen-order backward's, and the
+    gradients agree with it and with the oracle."""
+    s, rays, start, thr = _case("hf8")
+    scene_t = _scene_tensors(s, gpu, False)
+    rd, sd = H.to_dev(rays, gpu), H.to_dev(start, gpu)
+    g = H.to_dev(np.random.default_rng(8).normal(size=rays.shape[:-1] + (4,)).astype(np.float32), gpu)
+    saved = _C.TRAIN_TILE_ORDER
+    try:
+        res = {}
+        for flag in (False, True):
+            _C.TRAIN_TILE_ORDER = flag
+            _C._TRAIN_SCHEDULES.clear()
+            fst = native.new_stats(rays.size // 6, gpu)
+            out = _C.trace_vorotracing_fwd(*scene_t, rd, sd, None, thr, 1024, False, stats=fst)
+            st = native.new_stats(rays.size // 6, gpu)
+            grads = _C.trace_vorotracing_bwd(*scene_t, rd, sd, out[0], g, None, None, None, None, 0.0, out[5], None,
+                                             out[6], out[7], out[8], thr, 1024, stats=st)
+            torch.cuda.synchronize()
+            res[flag] = (out[0].cpu().numpy(), [x.cpu().numpy() for x in grads[:4]], H.stats_np(st), H.stats_np(fst))
+        sch = next(iter(_C._TRAIN_SCHEDULES.values()))
+    finally:
+        _C.TRAIN_TILE_ORDER = saved
+    assert np.array_equal(res[True][0], res[False][0])
+    H.assert_stats_equal(res[True][2], res[False][2])
+    for a, b, name in zip(res[True][1], res[False][1], ("points", "diffuse", "specular", "density")):
+        H.assert_grad_close(a, b, name)
+    # the order the backward used: tiles by the forward's costs (2-wide strips)
+    Hh, W = rays.shape[:2]
+    TX, TY = (W + 7) // 8, (Hh + 7) // 8
+    yy, xx = np.meshgrid(np.arange(Hh), np.arange(W), indexing="ij")
+    tx, ty = xx // 8, yy // 8
+    sp = tx // 2
+    wd = np.where((sp + 1) * 2 <= TX, 2, TX - sp * 2)
+    tile_of = (sp * 2 * TY + ty * wd + (tx - sp * 2)).reshape(-1)
+    fs = res[True][3]
+    nmax, fmax = np.zeros(TX * TY, np.int64), np.zeros(TX * TY, np.int64)
+    np.maximum.at(nmax, tile_of, fs["n"].astype(np.int64))
+    np.maximum.at(fmax, tile_of, fs["faces"].astype(np.int64))
+    cost = 18 * nmax + fmax
+    assert np.array_equal(sch.cost.cpu().numpy().astype(np.int64), cost)
+    assert np.array_equal(sch.order.cpu().numpy().astype(np.int64),
+                          np.argsort(65535 - np.minimum(cost >> 2, 65535), kind="stable"))
+    fw = core.trace_fwd(s.points, s.diffuse, s.specular, s.diff_res, s.spec_res, s.density, s.adjacency, s.offsets,
+                        rays, start, weight_threshold=thr)
+    want = core.trace_bwd(s.points, s.diffuse, s.specular, s.diff_res, s.spec_res, s.density, s.adjacency, s.offsets,
+                          rays, start, fw["rgba"], g.cpu().numpy(), distortion=fw["distortion"],
+                          W_total=fw["W_total"], S_total=fw["S_total"], t_far=fw["t_far"], weight_threshold=thr)
+    for a, key in zip(res[True][1], ("points_grad", "diffuse_grad", "specular_grad", "density_grad")):
+        H.assert_grad_close(a, want[key], key)

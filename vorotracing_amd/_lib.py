@@ -38,12 +38,12 @@ SIGNATURES = {
         [P, P, P, U32, U32, P, P, P, P, P, P, P, U32, P, P, U32, U32, U32, U32, U32, P, I32, F32, U32, F32, P, P, P, P, P],
         C.c_int),
     "vt_trace_fwd": (
-        [I32, P, P, P, U32, U32, P, P, U32, P, U32, P, U32, U32, U32, P, P, U32, P, F32, U32, P, P, P, P, P, P, P, P, P, P, P,
-         P],
+        [I32, P, P, P, U32, U32, P, P, U32, P, U32, P, U32, U32, U32, P, P, U32, P, F32, U32, P, P, P, P, P, P, P, P,
+         P, P, P, P, P, P],
         C.c_int),
     "vt_trace_bwd": (
-        [I32, P, P, P, U32, U32, P, P, U32, P, U32, P, U32, U32, U32, P, P, P, P, U32, P, P, P, P, F32, P, P, P, P, P, F32,
-         U32, P, P, P, P, P, P, I32, P, P, P], C.c_int),
+        [I32, P, P, P, U32, U32, P, P, U32, P, U32, P, U32, U32, U32, P, P, P, P, U32, P, P, P, P, F32, P, P, P, P,
+         P, F32, U32, P, P, P, P, P, P, I32, P, P, P, P], C.c_int),
     "vt_ray_order_workspace_size": ([U32], C.c_size_t),
     "vt_ray_order": ([P, P, U32, U32, P, P, P], C.c_int),
     "vt_math_probe": ([I32, P, P, U32, P], C.c_int),

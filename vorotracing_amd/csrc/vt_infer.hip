@@ -82,11 +82,7 @@ constexpr int INFER_CHUNK = 8;
 // Blocks per XCD turn (xcd_interleaved_block): with contiguous ranges per XCD
 // (xcd_block) one XCD got the costliest screen region and finished last.
 constexpr uint32_t INFER_XCD_CHUNK = 32;
-// Tile cost = TILE_COST_STEP x the longest walk's steps + the most face
-// records one ray of the tile searched.  Launching tiles by decreasing cost
-// (vt_tile_order, from the previous frame's costs) measured 14 % shorter C3
-// frames than screen order; the walk steps alone gave 7-10 %.
-constexpr uint32_t TILE_COST_STEP = 18;
+
 
 
 // The pending shades of one wave: a ring of SQ_RING entries.  Lanes append
@@ -380,7 +376,7 @@ void infer_kernel(InferArgs a, uint32_t total_slots)
         const uint32_t nmax = wave_max_u32(r == NONE ? 0u : w.n);
         const uint32_t fmax = wave_max_u32(r == NONE ? 0u : st.face_count());
         if (lane == 0)
-            a.tile_cost[tile_of_slot(a, s)] = TILE_COST_STEP * nmax + fmax;
+            a.tile_cost[tile_of_slot(a, s)] = tile_cost_of(nmax, fmax);
     }
     if (r == NONE)
         return;

@@ -121,8 +121,15 @@ constexpr uint32_t TRAIN_TILE = 8;
 #endif
 constexpr uint32_t TRAIN_TILE_STRIP = VT_TRAIN_TILE_STRIP;
 
+// Tile of launch slot s in the tiled order: the tile in screen order, or
+// the one tile_order places at the slot's wave.
+__device__ __forceinline__ uint32_t train_tile(uint32_t s, const uint32_t *tile_order)
+{
+    return tile_order ? tile_order[s >> 6] : s >> 6;
+}
+
 __device__ __forceinline__ uint32_t train_ray(uint32_t s, uint32_t num_rays, const uint32_t *perm, uint32_t ni,
-                                              uint32_t h, uint32_t w)
+                                              uint32_t h, uint32_t w, const uint32_t *tile_order)
 {
     if (perm) {
         if (s >= num_rays)
@@ -131,7 +138,8 @@ __device__ __forceinline__ uint32_t train_ray(uint32_t s, uint32_t num_rays, con
         return r < num_rays ? r : NONE;
     }
     if (ni)
-        return tiled_ray<TRAIN_TILE_STRIP>(s, ni, h, w, TRAIN_TILE, TRAIN_TILE);
+        return tiled_ray<TRAIN_TILE_STRIP>(train_tile(s, tile_order) * 64u + (s & 63u), ni, h, w, TRAIN_TILE,
+                                           TRAIN_TILE);
     return s < num_rays ? s : NONE;
 }
 
@@ -160,6 +168,8 @@ struct FwdArgs {
     uint32_t *n_out;
     float *distortion, *W_total, *S_total, *t_far;
     uint32_t *stats;
+    const uint32_t *tile_order; // tiled lane order: launch order of the tiles, or null (screen order)
+    uint32_t *tile_cost;        // tiled lane order: each tile's cost (tile_cost_of), or null
 };
 
 // RayIntegratorOctMap::integrate_cell (ray_integrator_octmap.cuh:102-152)
@@ -257,13 +267,11 @@ template <typename A, int RD, int RS> struct FwdIntegrator {
 // 6 waves per SIMD (80 VGPRs, 20 bytes spilled) beat the 5 that the
 // unspilled kernel allows (1.13-1.16 against 1.19-1.21 ms at C2): more waves
 // hide more of the walk's load latency.
+// The forward of ray r; returns the walk's step count, and in faces the face
+// records it searched.
 template <typename A, int RD, int RS, bool STATS>
-__global__ __launch_bounds__(TRAIN_BLOCK) __attribute__((amdgpu_waves_per_eu(6))) void fwd_kernel(FwdArgs a)
+__device__ __forceinline__ uint32_t fwd_ray(const FwdArgs &a, uint32_t r, uint32_t &faces)
 {
-    uint32_t r = train_ray(xcd_interleaved_block<TRAIN_XCD_CHUNK>() * blockDim.x + threadIdx.x, a.num_rays, a.ray_perm,
-                           a.num_images, a.img_h, a.img_w);
-    if (r == NONE)
-        return;
     FwdIntegrator<A, RD, RS> it;
     load_ray(a.rays, r, it.o, it.d);
     it.density = a.density;
@@ -304,6 +312,24 @@ __global__ __launch_bounds__(TRAIN_BLOCK) __attribute__((amdgpu_waves_per_eu(6))
     a.S_total[r] = it.S;
     a.t_far[r] = it.tfar;
     st.store(a.stats, r, n);
+    faces = st.face_count();
+    return n;
+}
+
+template <typename A, int RD, int RS, bool STATS>
+__global__ __launch_bounds__(TRAIN_BLOCK) __attribute__((amdgpu_waves_per_eu(6))) void fwd_kernel(FwdArgs a)
+{
+    const uint32_t s = xcd_interleaved_block<TRAIN_XCD_CHUNK>() * blockDim.x + threadIdx.x;
+    const uint32_t r = train_ray(s, a.num_rays, a.ray_perm, a.num_images, a.img_h, a.img_w, a.tile_order);
+    uint32_t n = 0, faces = 0;
+    if (r != NONE)
+        n = fwd_ray<A, RD, RS, STATS>(a, r, faces);
+    if (a.tile_cost && a.num_images) {
+        // tiled launches are whole waves, and every lane is here
+        const uint32_t nmax = wave_max_u32(n), fmax = wave_max_u32(faces);
+        if ((threadIdx.x & 63u) == 0)
+            a.tile_cost[train_tile(s, a.tile_order)] = tile_cost_of(nmax, fmax);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -334,6 +360,7 @@ struct BwdArgs {
     void *diffuse_grad, *specular_grad;
     void *point_error;
     uint32_t *stats;
+    const uint32_t *tile_order; // tiled lane order: launch order of the tiles, or null (screen order)
 };
 
 // ray_integrator.cuh:39-53
@@ -740,7 +767,7 @@ __global__ __launch_bounds__(TRAIN_BLOCK) __attribute__((amdgpu_waves_per_eu(4))
         rows[64 * ROW_STRIDE + (threadIdx.x & 63u)] = 0.0f; // the zero row
     wave_lds_sync();
     uint32_t r = train_ray(xcd_interleaved_block<TRAIN_XCD_CHUNK>() * blockDim.x + threadIdx.x, a.num_rays, a.ray_perm,
-                           a.num_images, a.img_h, a.img_w);
+                           a.num_images, a.img_h, a.img_w, a.tile_order);
     if (r == NONE)
         return;
     BwdIntegrator<A, RD, RS> it;
@@ -887,7 +914,8 @@ extern "C" int vt_trace_fwd(int attr_dtype, const float *points, const void *dif
                             const float *depth_quantiles, float weight_threshold, uint32_t max_intersections,
                             void *rgba, float *depth, uint32_t *depth_idx, void *contribution,
                             uint32_t *num_intersections, float *distortion, float *W_total, float *S_total,
-                            float *t_far, uint16_t *adj_diff_workspace, vt_ray_stats *stats, vt_stream_t stream)
+                            float *t_far, uint16_t *adj_diff_workspace, const uint32_t *tile_order,
+                            uint32_t *tile_cost, vt_ray_stats *stats, vt_stream_t stream)
 {
     clear_error();
     VT_REQUIRE(points && diffuse && specular && density && adjacency && offsets && adj_diff_workspace,
@@ -927,6 +955,8 @@ extern "C" int vt_trace_fwd(int attr_dtype, const float *points, const void *dif
     a.S_total = S_total;
     a.t_far = t_far;
     a.stats = reinterpret_cast<uint32_t *>(stats);
+    a.tile_order = a.num_images ? tile_order : nullptr;
+    a.tile_cost = a.num_images ? tile_cost : nullptr;
     return launch_train<FwdK>(attr_dtype, a, diff_res, spec_res, stats != nullptr, s);
 }
 
@@ -966,7 +996,8 @@ extern "C" int vt_trace_bwd(int attr_dtype, const float *points, const void *dif
                             const float *S_total, const float *t_far, float weight_threshold,
                             uint32_t max_intersections, float *points_grad, void *diffuse_grad, void *specular_grad,
                             float *density_grad, void *point_error, uint16_t *adj_diff_workspace,
-                            int adj_diff_ready, float *cell_workspace, vt_ray_stats *stats, vt_stream_t stream)
+                            int adj_diff_ready, float *cell_workspace, const uint32_t *tile_order,
+                            vt_ray_stats *stats, vt_stream_t stream)
 {
     clear_error();
     (void)t_far;
@@ -1017,6 +1048,7 @@ extern "C" int vt_trace_bwd(int attr_dtype, const float *points, const void *dif
     a.specular_grad = specular_grad;
     a.point_error = point_error;
     a.stats = reinterpret_cast<uint32_t *>(stats);
+    a.tile_order = a.num_images ? tile_order : nullptr;
     if (num_rays == 0)
         return VT_OK;
     const uint32_t cblocks = (num_points + 255) / 256;

@@ -213,6 +213,19 @@ __device__ __forceinline__ uint32_t walk(f3 o, f3 d, const float *points,
     return w.n;
 }
 
+// Cost of a screen tile for the launch order of the next launch over the
+// same rays (vt_tile_order): TILE_COST_STEP x the longest walk's steps + the
+// most face records one ray of the tile searched, both maxima over the
+// tile's rays (a wave takes about as long as its longest lane).  Of the keys
+// tried on C3 frames this one ordered the launch best; walk steps alone
+// recovered about half as much.
+constexpr uint32_t TILE_COST_STEP = 18;
+
+__device__ __forceinline__ uint32_t tile_cost_of(uint32_t steps_max, uint32_t faces_max)
+{
+    return TILE_COST_STEP * steps_max + faces_max;
+}
+
 // Screen tiles are visited in vertical strips TILE_STRIP tiles wide (the last
 // strip takes the remainder), row by row inside a strip; 0 = row-major over
 // the whole image.  Consecutive waves then cover a compact screen region

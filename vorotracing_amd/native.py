@@ -138,6 +138,21 @@ class TileSchedule:
         self.frame = frame
         return order, self.cost.data_ptr()
 
+    def record(self, frame):
+        """tile_cost pointer for a launch of ``frame`` in screen order that
+        records its tiles' costs (the training forward)."""
+        self.frame = frame
+        return self.cost.data_ptr()
+
+    def order_for(self, stream: int, frame):
+        """Launch order from the costs the last launch of ``frame`` recorded
+        (the training backward after the forward over the same rays), or
+        None when the costs are of another frame."""
+        if frame is None or frame != self.frame:
+            return None
+        _lib.call("vt_tile_order", self.cost.data_ptr(), self.tiles, self.order.data_ptr(), self.ws.data_ptr(), stream)
+        return self.order.data_ptr()
+
 
 def frame_key(t: torch.Tensor):
     """Identity of a frame's rays: the tensor object, its storage and its
