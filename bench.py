@@ -33,6 +33,7 @@ HBM_PEAK_GBS = 8000.0
 # wave64 instruction per SIMD every 2 cycles.
 VALU_PEAK_PER_S = 256 * 4 * 2.4e9 / 2
 IN_FLIGHT = 2
+REPEATS = 4  # timed renders per view in the reference's protocol (it uses 20 per test image)
 
 
 def log(*a):
@@ -192,17 +193,55 @@ def main():
     thr, skip = 0.01, 1e-3
     stream = torch.cuda.current_stream(dev)
 
-    # warmup
-    for i in range(args.warmup):
-        inf.render(poses[i % args.poses], weight_threshold=thr, cell_skip_threshold=skip)
-    torch.cuda.synchronize()
-
     kw = dict(weight_threshold=thr, cell_skip_threshold=skip)
     K = args.steps
+    P = args.poses
 
-    # Serial frames, the reference's protocol (benchmark_eval.py:137-158): one
-    # render after the other on one stream.  HIP events on that stream around
-    # each traversal launch give the kernel's duration.
+    # warm-up over the orbit (the GPU's clocks and caches, the allocator)
+    for i in range(args.warmup):
+        inf.render(poses[i % args.poses], **kw)
+    torch.cuda.synchronize()
+
+    # The reference's protocol (benchmark_eval.py:137-158): each view rendered
+    # `warmup` times, then timed over repeated renders of that view with
+    # events on the render stream, the per-view times averaged.  Here K renders
+    # in all: REPEATS per view over K / REPEATS views spread evenly over the
+    # orbit, each after W / views warm-up renders (at least one: a render of a
+    # view seen before launches its tiles by the costs it recorded).
+    R = min(REPEATS, K)
+    P = max(1, min(P, K // R))
+    view_poses = [(i * args.poses) // P for i in range(P)]
+    Wp = max(1, args.warmup // P)
+    view_ms = []
+    t_ref = 0.0
+    # (--profile renders the orbit only: every traced traversal launch is then
+    # one the roofline's kernel_ms averages)
+    for p in (view_poses if not args.profile else []):
+        for _ in range(Wp):
+            inf.render(poses[p], **kw)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        tw = time.perf_counter()
+        e0.record(stream)
+        for _ in range(R):
+            inf.render(poses[p], **kw)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t_ref += time.perf_counter() - tw
+        view_ms.append(e0.elapsed_time(e1) / R)
+    if args.profile:
+        view_ms = [float("nan")]
+    ref_steps = R * P
+    ms_per_step = float(np.mean(view_ms))
+    fps = 1000.0 / ms_per_step
+    log(f"reference protocol: {P} views x {R} timed renders after {Wp} warm-up each: {ms_per_step:.3f} ms/frame, "
+        f"{fps:.1f} FPS (views {', '.join(f'{x:.3f}' for x in view_ms)} ms; wall clock "
+        f"{1000 * t_ref / max(ref_steps, 1):.3f} ms/frame)")
+
+
+    # The orbit, serial: one render after the other on one stream, a new pose
+    # every frame (a moving camera).  HIP events on that stream around each
+    # traversal launch give the kernel's duration.
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
     frames = []
     torch.cuda.synchronize()
@@ -216,7 +255,7 @@ def main():
     torch.cuda.synchronize()
     t_serial = time.perf_counter() - t_start
     kernel_avg_ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
-    log(f"serial: {K} frames, {1000 * t_serial / K:.3f} ms/frame, {K / t_serial:.1f} FPS, "
+    log(f"orbit serial: {K} frames, {1000 * t_serial / K:.3f} ms/frame, {K / t_serial:.1f} FPS, "
         f"traversal kernel {kernel_avg_ms:.3f} ms")
 
     # The same frames with two in flight (VoroTracingInfer.render_frames):
@@ -236,9 +275,8 @@ def main():
     t_total = time.perf_counter() - t_start
     same_frames = all(torch.equal(a.view(torch.int16), b.view(torch.int16)) for a, b in zip(piped, frames))
     del piped
-    ms_per_step = 1000.0 * t_total / K
-    fps = K / t_total
-    log(f"timed {K} frames, {in_flight} in flight: {ms_per_step:.3f} ms/frame, {fps:.1f} FPS; "
+    fly_ms = 1000.0 * t_total / K
+    log(f"orbit, {in_flight} frames in flight: {fly_ms:.3f} ms/frame, {K / t_total:.1f} FPS; "
         f"frames bit-identical to the serial renders: {same_frames}")
 
     result = {
@@ -246,8 +284,8 @@ def main():
         "value": round(fps, 2),
         "unit": "frames/s",
         "n_gpus": 1,
-        "steps": K,
-        "warmup": args.warmup,
+        "steps": ref_steps,
+        "warmup": Wp * P,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -257,15 +295,22 @@ def main():
         "config": {"workload": "C3: fp16 inference render, 1,048,576 sites (Morton-sorted), 4x4 octahedral "
                                "textures, 1237x822 pinhole orbit x32 poses, thr 0.01, skip 1e-3",
                    "sites": sc.num_points, "faces": sc.num_faces, "width": W, "height": H, "poses": args.poses,
-                   "tiling": "8x8 wave64 tiles in-kernel", "parallelism": "single GPU",
-                   "frames_in_flight": in_flight,
-                   "timing": f"{K} whole renders (start-cell query + traversal each), frame k on side stream k mod "
-                             f"{in_flight} (VoroTracingInfer.render_frames), wall clock between synchronizations; "
-                             "every frame complete and bit-identical to the serial render"},
-        "serial": {"fps": round(K / t_serial, 2), "ms_per_frame": round(1000 * t_serial / K, 4),
-                   "kernel_ms": round(kernel_avg_ms, 4),
-                   "note": "one render after the other on one stream (benchmark_eval.py:137-158)"},
-        "frames_identical_to_serial": same_frames,
+                   "tiling": "8x8 wave64 tiles in-kernel", "parallelism": "single GPU", "frames_in_flight": 1,
+                   "timing": f"benchmark_eval.py:137-158's protocol: {P} poses spread over the orbit, each rendered "
+                             f"{Wp}x untimed, then {R}x between HIP events on the render stream (whole renders: "
+                             "start-cell query + tile order + traversal), serially on one stream; ms/frame = mean "
+                             "over the poses"},
+        "views_ms": {"poses": view_poses, "ms": [round(x, 4) for x in view_ms],
+                     "wall_clock_ms_per_frame": round(1000 * t_ref / max(ref_steps, 1), 4)},
+        "orbit_serial": {"fps": round(K / t_serial, 2), "ms_per_frame": round(1000 * t_serial / K, 4),
+                         "kernel_ms": round(kernel_avg_ms, 4),
+                         "note": f"{K} renders of the orbit, a new pose every frame, one after the other on one "
+                                 "stream"},
+        "two_in_flight": {"fps": round(K / t_total, 2), "ms_per_frame": round(fly_ms, 4), "frames_in_flight": in_flight,
+                          "frames_identical_to_serial": same_frames,
+                          "note": f"the same {K} orbit renders, frame k on side stream k mod {in_flight} "
+                                  "(VoroTracingInfer.render_frames): one frame's last tiles overlap the next "
+                                  "frame's start; wall clock between synchronizations"},
     }
 
     if not args.profile:
@@ -290,6 +335,7 @@ def main():
             "shaded_per_ray": round(float(tot_s[5]) / (nr * args.poses), 2),
             "mrays_per_s": round(nr * fps / 1e6, 1),
         }
+        result["dropin_c"] = dropin_c(inf, poses[0], kw, dev, log)
         r = result["roofline"]
         log(f"HBM {r['achieved']:.0f} GB/s ({r['frac']:.1%} of peak); logical bytes {bytes_per_frame / 1e9:.2f} "
             f"GB/frame; VALU issue {r.get('valu', {}).get('frac', float('nan')):.1%}")
@@ -381,6 +427,52 @@ def compulsory_bytes(oc, pts, d4, s4, den, adj, off, ad, rays, inf, thr, skip, c
                                "8 per face record); textures excluded; walks from the CPU oracle's visit log"}
 
 
+def dropin_c(inf, rays, kw, dev, log, R=20):
+    """C3 pose 0 through the drop-in _C.trace_vorotracing_infer with the
+    reference's own arguments (its 4x8 int32 warp permutation,
+    vorotracing.py:606-642) against VoroTracingInfer.render, both after a
+    warm-up render, R renders each between HIP events, alternated three
+    times (the best of each is kept)."""
+    import torch
+
+    from vorotracing_amd import _C, _lib
+
+    H, W = rays.shape[0], rays.shape[1]
+    perm = torch.empty(H * W, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    _lib.call("vt_tile_perm", H, W, 4, 8, perm.data_ptr(), stream.cuda_stream)
+    sp = inf.get_starting_point(rays)
+
+    def dropin():
+        return _C.trace_vorotracing_infer(inf.primal_points, inf.diffuse_fp16, inf.specular_fp16, inf.density,
+                                          inf.point_adjacency, inf.point_adjacency_offsets, rays, sp,
+                                          inf.adjacent_diff, perm, kw["weight_threshold"], 1024,
+                                          kw["cell_skip_threshold"])
+
+    def render():
+        return inf.render(rays, start_point=sp, **kw)
+
+    out = {"dropin_ms": float("inf"), "render_ms": float("inf")}
+    imgs = {}
+    for _ in range(3):  # alternated, so neither path is timed colder than the other; best of three
+        for name, fn in (("dropin_ms", dropin), ("render_ms", render)):
+            imgs[name] = fn()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for _ in range(R):
+                fn()
+            b.record(stream)
+            torch.cuda.synchronize()
+            out[name] = min(out[name], round(a.elapsed_time(b) / R, 4))
+    out["identical"] = bool(torch.equal(imgs["dropin_ms"].view(torch.int16), imgs["render_ms"].view(torch.int16)))
+    out["note"] = ("pose 0, start cells given; _C sees an image-shaped rays tensor and a permutation of it, and "
+                   "renders with in-kernel 8x8 tiles (a ray's result does not depend on its lane)")
+    log(f"drop-in _C.trace_vorotracing_infer with the 4x8 perm: {out['dropin_ms']:.3f} ms against render "
+        f"{out['render_ms']:.3f} ms; identical {out['identical']}")
+    return out
+
+
 def voronoi_c3(sc, dev, log, reps=5):
     """The Voronoi adjacency of the C3 sites built on the GPU (the step the
     reference hands to Paragram, cuda/__init__.py:16-46): wall time of
@@ -467,7 +559,7 @@ def c3_camera(inf, W, H, n_poses, kw, dev, log, K=64):
     return {"fps": round(K / dt, 2), "ms_per_frame": round(1000 * dt / K, 4), "frames": K,
             "identical_to_buffer_render": same,
             "note": "serial renders from vt_camera records (whole renders: start-cell query + traversal), no rays "
-                    "buffer; compare serial.ms_per_frame"}
+                    "buffer; compare orbit_serial.ms_per_frame"}
 
 
 def c4_q8(model, poses, dev, log, thr, skip, cpu=False):
@@ -631,12 +723,110 @@ def train_c2(dev, log, cpu=False, random_batch=True):
            "workload": "C2: TraceVoroTracing forward + backward, 262,144 sites (torus + background), 4x4 fp32 "
                        "textures, one 800x600 pinhole camera, upstream dL/dRGB ~ N(0,1), thr 0.001"}
     out["roofline_fwd"], out["roofline_bwd"] = train_rooflines(model, rays, sp, g, dev, log)
+    if random_batch:  # left out of --train-only: its traces average the default (ordered) backward
+        out["backward_tile_order"] = train_tile_order(model, rays, sp, g, dev, log)
     out["f16_storage"] = train_f16_storage(model, rays, sp, g, dev, log)
     if random_batch:  # left out of --train-only, whose traces average the C2 kernels
         out["random_batch"] = train_random_batch(model, dev, log)
     out["full_step"] = train_step_c2(sc, dev, rays, sp, g, log)
     if cpu:
         out["cpu_baseline"] = train_c2_cpu(model, rays, sp, g, log)
+    if random_batch:
+        del model
+        out["maps_8x8"] = train_maps8(dev, rays, sp, g, log)
+    return out
+
+
+def _entry_times(scn, rays, sp, g, dev, R=10):
+    """HIP-event means of R calls of the forward and of the backward _C entry
+    (prefetch included; the backward after a forward over the same rays)."""
+    import torch
+
+    from vorotracing_amd import _C
+
+    fw = _C.trace_vorotracing_fwd(*scn, rays, sp, None, 0.001, 1024, False)
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(R):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / R
+
+    t_fwd = timed(lambda: _C.trace_vorotracing_fwd(*scn, rays, sp, None, 0.001, 1024, False))
+    t_bwd = timed(lambda: _C.trace_vorotracing_bwd(*scn, rays, sp, fw[0], g.to(fw[0].dtype), None, None, None, None,
+                                                   0.0, fw[5], None, fw[6], fw[7], fw[8], 0.001, 1024))
+    return round(t_fwd, 3), round(t_bwd, 3)
+
+
+def train_tile_order(model, rays, sp, g, dev, log):
+    """The C2 backward entry with its tiles in screen order and in the order of
+    the forward's tile costs (the default: _C.TRAIN_TILE_ORDER)."""
+    from vorotracing_amd import _C
+
+    dens = model.activated_density().detach()
+    scn = (model.primal_points.detach(), model.att_diffuse.detach(), model.att_specular.detach(), dens,
+           model.point_adjacency, model.point_adjacency_offsets)
+    out = {}
+    saved = _C.TRAIN_TILE_ORDER
+    try:
+        for name, flag in (("screen_order", False), ("forward_cost_order", True)):
+            _C.TRAIN_TILE_ORDER = flag
+            _C._TRAIN_SCHEDULES.clear()
+            t_fwd, t_bwd = _entry_times(scn, rays, sp, g, dev)
+            out[name] = {"forward_ms": t_fwd, "backward_ms": t_bwd}
+    finally:
+        _C.TRAIN_TILE_ORDER = saved
+    out["note"] = ("_C entries, prefetch included; the backward of a forward over the same rays launches its tiles "
+                   "by the forward's per-tile costs (vt_tile_order) instead of screen order")
+    log(f"C2 backward entry: screen order {out['screen_order']['backward_ms']:.3f} ms, forward-cost order "
+        f"{out['forward_cost_order']['backward_ms']:.3f} ms")
+    return out
+
+
+def train_maps8(dev, rays, sp, g, log):
+    """C2 with the reference's compiled map resolution, 8x8 diffuse and 8x8
+    specular (tracing_octmap.cu:27-28): the model's forward + backward step
+    and the entries with f32 and f16 map storage."""
+    import torch
+
+    from vorotracing_amd import scene
+    from vorotracing_amd.model import VoroTracing
+
+    sc = scene.cached(scene.config2, 0, R=8)
+    model = VoroTracing.from_scene(sc, device=dev)
+    dens = model.activated_density().detach()
+    out = {"workload": "C2 scene with 8x8 diffuse + 8x8 specular maps (random), one 800x600 pinhole"}
+    for name, cast in (("f32", lambda t: t), ("f16_storage", lambda t: t.half())):
+        scn = (model.primal_points.detach(), cast(model.att_diffuse.detach()), cast(model.att_specular.detach()),
+               dens, model.point_adjacency, model.point_adjacency_offsets)
+        t_fwd, t_bwd = _entry_times(scn, rays, sp, g, dev)
+        out[name] = {"forward_ms": t_fwd, "backward_ms": t_bwd}
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        model.zero_grad(set_to_none=True)
+        rgba = model(rays, start_point=sp, weight_threshold=0.001)[0]
+        rgba.backward(g)
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(10):
+        step()
+    b.record(stream)
+    torch.cuda.synchronize()
+    out["model_fwd_bwd_ms"] = round(a.elapsed_time(b) / 10, 3)
+    log(f"C2 8x8 maps: f32 entries {out['f32']['forward_ms']:.3f} / {out['f32']['backward_ms']:.3f} ms, f16 "
+        f"{out['f16_storage']['forward_ms']:.3f} / {out['f16_storage']['backward_ms']:.3f} ms; model step "
+        f"{out['model_fwd_bwd_ms']:.3f} ms")
     return out
 
 
@@ -774,6 +964,11 @@ def train_random_batch(model, dev, log, R=5, cams=32, W=800, H=600):
         out[name] = {"forward_ms": round(t_fwd, 3), "backward_ms": round(t_bwd, 3)}
         log(f"C2 random batch, {name}: forward entry {t_fwd:.3f} ms, backward entry {t_bwd:.3f} ms")
     out["order_ms"] = round(timed(lambda: _C.ray_order(rays, sp, scn[0].shape[0])), 3)
+    # the start cells of the shuffled batch (VoroTracing.get_starting_point:
+    # runs of equal origins are as many as rays here, so it queries the 32
+    # distinct origins)
+    out["start_cells_ms"] = round(timed(lambda: model.get_starting_point(rays)), 3)
+    assert bool((model.get_starting_point(rays).view(torch.int32) == sp.view(torch.int32)).all())
 
     def step():
         model.zero_grad(set_to_none=True)
@@ -781,7 +976,8 @@ def train_random_batch(model, dev, log, R=5, cams=32, W=800, H=600):
         rgba.backward(g)
 
     out["model_fwd_bwd_ms"] = round(timed(step), 3)
-    log(f"C2 random batch: vt_ray_order {out['order_ms']:.3f} ms; model forward + backward "
+    log(f"C2 random batch: start cells {out['start_cells_ms']:.3f} ms, vt_ray_order {out['order_ms']:.3f} ms; "
+        f"model forward + backward "
         f"{out['model_fwd_bwd_ms']:.3f} ms/step (one order per step)")
     return out
 
@@ -943,18 +1139,33 @@ def train_c5(dev, log, cpu=False, K=5):
             ev[3].record(stream)
         holder["sp"] = sp
 
-    for _ in range(2):
-        step()
+    def timed_steps():
+        for _ in range(2):
+            step()
+        torch.cuda.synchronize()
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(K)]
+        t = time.perf_counter()
+        for i in range(K):
+            step(evs[i])
+        torch.cuda.synchronize()
+        part = lambda j: round(float(np.mean([e[j].elapsed_time(e[j + 1]) for e in evs])), 3)  # noqa: E731
+        return 1000 * (time.perf_counter() - t) / K, part(0), part(1), part(2)
+
+    # the sites in the order the scene generator drew them, then in Morton
+    # order (VoroTracing.sort_morton, a preparation step like
+    # VoroTracingInfer's reorder; neighbouring cells in neighbouring rows)
+    ms0, _, f0, b0 = timed_steps()
+    log(f"C5 step, sites in generation order: {ms0:.2f} ms (forward {f0} ms, backward {b0} ms)")
+    t_sort = time.perf_counter()
+    model.sort_morton()
     torch.cuda.synchronize()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(K)]
-    t = time.perf_counter()
-    for i in range(K):
-        step(evs[i])
-    torch.cuda.synchronize()
-    ms = 1000 * (time.perf_counter() - t) / K
-    part = lambda j: round(float(np.mean([e[j].elapsed_time(e[j + 1]) for e in evs])), 3)
-    out = {"fwd_bwd_ms_per_step": round(ms, 3), "start_lookup_ms": part(0), "forward_ms": part(1),
-           "backward_ms": part(2), "rays": int(rays.numel() // 6), "sites": sc.num_points, "faces": sc.num_faces,
+    t_sort = 1000 * (time.perf_counter() - t_sort)
+    ms, s_ms, f_ms, b_ms = timed_steps()
+    out = {"fwd_bwd_ms_per_step": round(ms, 3), "start_lookup_ms": s_ms, "forward_ms": f_ms,
+           "backward_ms": b_ms, "sites_order": "Morton (VoroTracing.sort_morton, done once before the timed steps)",
+           "generation_order": {"fwd_bwd_ms_per_step": round(ms0, 3), "forward_ms": f0, "backward_ms": b0},
+           "sort_morton_ms": round(t_sort, 1),
+           "rays": int(rays.numel() // 6), "sites": sc.num_points, "faces": sc.num_faces,
            "distinct_origins": int(torch.unique(rays[..., :3].reshape(-1, 3), dim=0).shape[0]), "dtype": "fp32",
            "adjacency": f"GPU Voronoi builder ({vor['ms']} ms)",
            "workload": "C5: TraceVoroTracing forward + backward, 3,145,728 height-field sites, 4x4 fp32 textures, "

