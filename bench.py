@@ -19,6 +19,7 @@ configs[1]: fwd + bwd ms/step, 262,144 sites, 800x600 rays).
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -38,6 +39,16 @@ REPEATS = 4  # timed renders per view in the reference's protocol (it uses 20 pe
 
 def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def settle():
+    """Collect garbage and freeze what survives (gc.freeze) before a timed
+    phase: a full collection rescans every long-lived object (scene arrays,
+    models, torch's modules) and takes about 40 ms of host time here, enough
+    to starve the GPU inside a timed render.  Collection stays enabled; it
+    just no longer rescans the setup's objects."""
+    gc.collect()
+    gc.freeze()
 
 
 def b_alg(st, tex_bytes=64, per_ray_extra=0):
@@ -190,6 +201,7 @@ def main():
         poses.append(torch.from_numpy(camera.orbit_rays(k, W, H, n=args.poses)).to(dev))
     torch.cuda.synchronize()
     log(f"{args.poses} poses of {W}x{H} rays resident ({time.time() - t0:.1f}s)")
+    settle()
     thr, skip = 0.01, 1e-3
     stream = torch.cuda.current_stream(dev)
 
@@ -229,14 +241,13 @@ def main():
         torch.cuda.synchronize()
         t_ref += time.perf_counter() - tw
         view_ms.append(e0.elapsed_time(e1) / R)
-    if args.profile:
-        view_ms = [float("nan")]
     ref_steps = R * P
-    ms_per_step = float(np.mean(view_ms))
+    ms_per_step = float(np.mean(view_ms)) if view_ms else float("nan")
     fps = 1000.0 / ms_per_step
-    log(f"reference protocol: {P} views x {R} timed renders after {Wp} warm-up each: {ms_per_step:.3f} ms/frame, "
-        f"{fps:.1f} FPS (views {', '.join(f'{x:.3f}' for x in view_ms)} ms; wall clock "
-        f"{1000 * t_ref / max(ref_steps, 1):.3f} ms/frame)")
+    if view_ms:
+        log(f"reference protocol: {P} views x {R} timed renders after {Wp} warm-up each: {ms_per_step:.3f} ms/frame, "
+            f"{fps:.1f} FPS (views {', '.join(f'{x:.3f}' for x in view_ms)} ms; wall clock "
+            f"{1000 * t_ref / max(ref_steps, 1):.3f} ms/frame)")
 
 
     # The orbit, serial: one render after the other on one stream, a new pose
@@ -279,6 +290,12 @@ def main():
     log(f"orbit, {in_flight} frames in flight: {fly_ms:.3f} ms/frame, {K / t_total:.1f} FPS; "
         f"frames bit-identical to the serial renders: {same_frames}")
 
+    timing = (f"benchmark_eval.py:137-158's protocol: {P} poses spread over the orbit, each rendered {Wp}x untimed, "
+              f"then {R}x between HIP events on the render stream (whole renders: start-cell query + tile order + "
+              "traversal), serially on one stream; ms/frame = mean over the poses")
+    if args.profile:  # no views: the serial orbit is the figure of a profiling run
+        ms_per_step, fps, ref_steps, Wp, P = 1000 * t_serial / K, K / t_serial, K, args.warmup, 0
+        timing = f"--profile: {K} serial renders of the orbit, a new pose every frame (wall clock)"
     result = {
         "metric": "FPS @1237x822 1M cells fp16; fwd+bwd ms/step; achieved HBM GB/s",
         "value": round(fps, 2),
@@ -296,22 +313,21 @@ def main():
                                "textures, 1237x822 pinhole orbit x32 poses, thr 0.01, skip 1e-3",
                    "sites": sc.num_points, "faces": sc.num_faces, "width": W, "height": H, "poses": args.poses,
                    "tiling": "8x8 wave64 tiles in-kernel", "parallelism": "single GPU", "frames_in_flight": 1,
-                   "timing": f"benchmark_eval.py:137-158's protocol: {P} poses spread over the orbit, each rendered "
-                             f"{Wp}x untimed, then {R}x between HIP events on the render stream (whole renders: "
-                             "start-cell query + tile order + traversal), serially on one stream; ms/frame = mean "
-                             "over the poses"},
+                   "timing": timing},
         "views_ms": {"poses": view_poses, "ms": [round(x, 4) for x in view_ms],
                      "wall_clock_ms_per_frame": round(1000 * t_ref / max(ref_steps, 1), 4)},
         "orbit_serial": {"fps": round(K / t_serial, 2), "ms_per_frame": round(1000 * t_serial / K, 4),
                          "kernel_ms": round(kernel_avg_ms, 4),
                          "note": f"{K} renders of the orbit, a new pose every frame, one after the other on one "
                                  "stream"},
-        "two_in_flight": {"fps": round(K / t_total, 2), "ms_per_frame": round(fly_ms, 4), "frames_in_flight": in_flight,
-                          "frames_identical_to_serial": same_frames,
-                          "note": f"the same {K} orbit renders, frame k on side stream k mod {in_flight} "
-                                  "(VoroTracingInfer.render_frames): one frame's last tiles overlap the next "
-                                  "frame's start; wall clock between synchronizations"},
     }
+    if not args.profile:
+        result["two_in_flight"] = {
+            "fps": round(K / t_total, 2), "ms_per_frame": round(fly_ms, 4), "frames_in_flight": in_flight,
+            "frames_identical_to_serial": same_frames,
+            "note": f"the same {K} orbit renders, frame k on side stream k mod {in_flight} "
+                    "(VoroTracingInfer.render_frames): one frame's last tiles overlap the next frame's start; wall "
+                    "clock between synchronizations"}
 
     if not args.profile:
         # algorithmic bytes from the kernel's walk counters (every pose once)
@@ -575,6 +591,7 @@ def c4_q8(model, poses, dev, log, thr, skip, cpu=False):
     inf8 = VoroTracingInfer(model, sort_morton=True, quantize="q8", per_channel_q8=True)
     batch = torch.stack([poses[k] for k in range(0, len(poses), 4)][:8]).contiguous()
     sp = inf8.get_starting_point(batch)
+    settle()
     for _ in range(3):
         inf8.render(batch, start_point=sp, weight_threshold=thr, cell_skip_threshold=skip)
     torch.cuda.synchronize()
@@ -634,6 +651,7 @@ def c1_forward(dev, log, cpu=False, K=20):
     model = VoroTracing.from_scene(sc, device=dev)
     rays = torch.from_numpy(camera.pinhole_rays(128, 128, eye=(0.0, -4.0, 0.0))).to(dev)
     sp = model.get_starting_point(rays)
+    settle()
     with torch.no_grad():
         for _ in range(10):
             model(rays, start_point=sp, weight_threshold=0.01)
@@ -691,6 +709,7 @@ def train_c2(dev, log, cpu=False, random_batch=True):
     g = torch.from_numpy(np.random.default_rng(0).normal(size=(600, 800, 4)).astype(np.float32)).to(dev)
     g[..., 3] = 0
     sp = model.get_starting_point(rays)
+    settle()
 
     stream = torch.cuda.current_stream(dev)
 
@@ -1121,6 +1140,7 @@ def train_c5(dev, log, cpu=False, K=5):
     rays = torch.from_numpy(camera.fisheye_rolling_rays(1558, 1039)).to(dev)
     g = torch.from_numpy(np.random.default_rng(5).normal(size=(1039, 1558, 4)).astype(np.float32)).to(dev)
     g[..., 3] = 0
+    settle()
     stream = torch.cuda.current_stream(dev)
     holder = {}
 

@@ -59,6 +59,15 @@ def stats_np(t: torch.Tensor):
     return np.ascontiguousarray(a).view(core.STATS_DTYPE).reshape(-1)
 
 
+def tile_order_keys(cost):
+    """Ascending sort key of the tile launch order: 4 buckets per octave of the
+    tile cost (cost 0 counts as 1), costliest bucket first."""
+    c = np.maximum(np.asarray(cost, dtype=np.int64), 1)
+    lb = np.frexp(c.astype(np.float64))[1].astype(np.int64) - 1  # floor(log2 c), exact below 2**53
+    frac = np.where(lb >= 2, c >> np.maximum(lb - 2, 0), c << np.maximum(2 - lb, 0)) & 3
+    return 127 - (4 * lb + frac)
+
+
 def assert_stats_equal(got, want):
     for k in ("n", "visits", "faces", "exits", "integrated", "shaded", "visit_hash", "first_cells"):
         diff = got[k] != want[k]

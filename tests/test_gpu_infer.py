@@ -415,20 +415,21 @@ def _strip_tiles(Hh, W, strip=4):
 
 
 def test_tile_order_sorts_by_cost(gpu):
-    """vt_tile_order: tiles by decreasing cost (quantised to cost >> 2),
-    equal costs in tile order, against numpy's stable argsort."""
+    """vt_tile_order: tiles by decreasing cost bucket (4 per octave), equal
+    buckets in tile order, against numpy's stable argsort of the bucket key."""
     rng = np.random.default_rng(3)
-    for tiles, hi in ((1, 10), (777, 50), (16095, 40000), (70000, 1 << 20)):
+    for tiles, hi in ((1, 10), (777, 50), (16095, 40000), (70000, 1 << 20), (5000, 1 << 32)):
         cost = rng.integers(0, hi, tiles).astype(np.uint32)
         cost[: tiles // 3] = cost[0]  # many ties
+        cost[-3:] = (0, 1, 0xFFFFFFFF)[: min(3, tiles)]
         c = H.to_dev(cost, gpu)
         order = torch.empty(tiles, dtype=torch.uint32, device=gpu)
         ws = torch.empty(int(_lib.load().vt_tile_order_workspace_size(tiles)), dtype=torch.uint8, device=gpu)
         _lib.call("vt_tile_order", c.data_ptr(), tiles, order.data_ptr(), ws.data_ptr(),
                   torch.cuda.current_stream().cuda_stream)
         torch.cuda.synchronize()
-        key = 65535 - np.minimum(cost >> 2, 65535)
-        assert np.array_equal(order.cpu().numpy().astype(np.int64), np.argsort(key, kind="stable")), tiles
+        want = np.argsort(H.tile_order_keys(cost), kind="stable")
+        assert np.array_equal(order.cpu().numpy().astype(np.int64), want), tiles
 
 
 def test_tile_order_and_costs_of_a_render(gpu):
@@ -460,7 +461,7 @@ def test_tile_order_and_costs_of_a_render(gpu):
         again = native.infer_f16(*args, weight_threshold=0.01, cell_skip_threshold=1e-3, tiled=(8, 8), schedule=sch)
         torch.cuda.synchronize()
         assert torch.equal(again.view(torch.int16), ref.view(torch.int16))
-    want = np.argsort(65535 - np.minimum((18 * nmax + fmax) >> 2, 65535), kind="stable")
+    want = np.argsort(H.tile_order_keys(18 * nmax + fmax), kind="stable")
     assert np.array_equal(sch.order.cpu().numpy().astype(np.int64), want)
     # a random launch order through the C ABI: same image
     order = H.to_dev(np.random.default_rng(5).permutation(tiles).astype(np.uint32), gpu)

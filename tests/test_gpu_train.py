@@ -439,7 +439,7 @@ def test_backward_in_forward_cost_order(gpu):
     cost = 18 * nmax + fmax
     assert np.array_equal(sch.cost.cpu().numpy().astype(np.int64), cost)
     assert np.array_equal(sch.order.cpu().numpy().astype(np.int64),
-                          np.argsort(65535 - np.minimum(cost >> 2, 65535), kind="stable"))
+                          np.argsort(H.tile_order_keys(cost), kind="stable"))
     fw = core.trace_fwd(s.points, s.diffuse, s.specular, s.diff_res, s.spec_res, s.density, s.adjacency, s.offsets,
                         rays, start, weight_threshold=thr)
     want = core.trace_bwd(s.points, s.diffuse, s.specular, s.diff_res, s.spec_res, s.density, s.adjacency, s.offsets,

@@ -1,12 +1,15 @@
 """Host-side argument checks that need no GPU: the warm-start guess CSR of
 build_voronoi_adjacency (cuda/__init__.py:16-37's initial_guesses) and the
 permutation check of explicit ray_perm lane orders (tracing_octmap.cu:642-717
-reads ray_perm[t] as the ray of thread t)."""
+reads ray_perm[t] as the ray of thread t), and the key of the tile launch
+order."""
 import numpy as np
 import pytest
 import torch
 
 from vorotracing_amd import _C, ops
+
+from tests import helpers as H
 
 
 def test_guess_csr_accepts_a_csr():
@@ -60,3 +63,23 @@ def test_is_permutation_sees_in_place_changes():
     assert not _C.is_permutation(p, 100)
     p[5] = 5
     assert _C.is_permutation(p, 100)
+
+
+def test_tile_order_key_buckets():
+    """The tile launch order's key: costs 0 and 1 share the last bucket, the
+    largest u32 cost sorts first, the key never rises with the cost, and each
+    octave [2^k, 2^(k+1)) from k = 2 on splits into 4 equal buckets."""
+    k = H.tile_order_keys
+    assert k([0, 1, 0xFFFFFFFF]).tolist() == [127, 127, 0]
+    c = np.arange(1, 1 << 17)
+    keys = k(c)
+    assert np.all(np.diff(keys) <= 0)
+    for e in range(2, 16):
+        seg = keys[(1 << e) - 1:(1 << (e + 1)) - 1]
+        vals, counts = np.unique(seg, return_counts=True)
+        assert len(vals) == 4 and np.all(counts == (1 << e) // 4), e
+    rng = np.random.default_rng(0)
+    for x in rng.integers(1, 1 << 32, 2000).tolist() + [2, 3, 5, 6, 7]:
+        lb = x.bit_length() - 1
+        frac = (x >> (lb - 2)) & 3 if lb >= 2 else (x << (2 - lb)) & 3
+        assert k([x])[0] == 127 - (4 * lb + frac), x

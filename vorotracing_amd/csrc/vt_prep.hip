@@ -399,27 +399,44 @@ extern "C" int vt_tile_perm(uint32_t height, uint32_t width, uint32_t tile_h, ui
 
 namespace vt {
 
-// keys of the stable ascending sort that lists tiles by decreasing cost
-// (costs quantised to 16 bits: 4 units, far below the spread of a frame's
-// tile costs, which run in the thousands)
-constexpr uint32_t TILE_ORDER_BITS = 16;
+// Key of the stable ascending sort that lists tiles by decreasing cost: the
+// cost's octave and its next two bits, 4 buckets per doubling (7 bits for any
+// u32 cost), inverted.  Only the costliest tiles need to start first; within
+// a bucket tiles keep screen order, so the blocks an XCD takes in one turn
+// still cover neighbouring tiles and share their cells in that XCD's L2.
+constexpr uint32_t TILE_ORDER_FRAC = 2;
+constexpr uint32_t TILE_ORDER_TOP = (32u << TILE_ORDER_FRAC) - 1u;
+
+__host__ __device__ constexpr uint32_t tile_order_key(uint32_t cost)
+{
+    const uint32_t c = cost > 1u ? cost : 1u;
+    const uint32_t lb = 31u - (uint32_t)__builtin_clz(c);
+    const uint32_t frac = (lb >= TILE_ORDER_FRAC ? c >> (lb - TILE_ORDER_FRAC) : c << (TILE_ORDER_FRAC - lb)) &
+                          ((1u << TILE_ORDER_FRAC) - 1u);
+    return TILE_ORDER_TOP - ((lb << TILE_ORDER_FRAC) | frac);
+}
+static_assert(TILE_ORDER_TOP < 256, "the tile order sorts on one 8-bit digit");
+static_assert(tile_order_key(1) == TILE_ORDER_TOP && tile_order_key(0) == TILE_ORDER_TOP, "");
+static_assert(tile_order_key(0xffffffffu) == 0, "");
+static_assert(tile_order_key(7) < tile_order_key(6) && tile_order_key(6) < tile_order_key(5), "");
+static_assert(tile_order_key(1000) == tile_order_key(1023) && tile_order_key(1023) > tile_order_key(1024), "");
 
 __global__ void tile_order_keys_kernel(const uint32_t *__restrict__ cost, uint32_t tiles, uint32_t *__restrict__ keys,
-                                       uint32_t *__restrict__ order)
+                                       uint32_t *__restrict__ ids)
 {
     const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= tiles)
         return;
-    const uint32_t top = (1u << TILE_ORDER_BITS) - 1u;
-    keys[t] = top - min(cost[t] >> 2, top);
-    order[t] = t;
+    keys[t] = tile_order_key(cost[t]);
+    ids[t] = t;
 }
 
 } // namespace vt
 
+// workspace: keys, tile ids, sorted keys (tiles words each), then one radix pass
 extern "C" size_t vt_tile_order_workspace_size(uint32_t tiles)
 {
-    return ((size_t)tiles + radix_sort_workspace_words(tiles)) * 4;
+    return (3 * (size_t)tiles + radix_pass_workspace_words(tiles)) * 4;
 }
 
 extern "C" int vt_tile_order(const uint32_t *tile_cost, uint32_t tiles, uint32_t *tile_order, void *workspace,
@@ -432,9 +449,11 @@ extern "C" int vt_tile_order(const uint32_t *tile_cost, uint32_t tiles, uint32_t
     VT_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 4 == 0, "workspace must be 4-byte aligned");
     hipStream_t s = as_stream(stream);
     uint32_t *keys = static_cast<uint32_t *>(workspace);
-    tile_order_keys_kernel<<<(tiles + 255) / 256, 256, 0, s>>>(tile_cost, tiles, keys, tile_order);
+    uint32_t *ids = keys + tiles;
+    uint32_t *sorted_keys = ids + tiles;
+    tile_order_keys_kernel<<<(tiles + 255) / 256, 256, 0, s>>>(tile_cost, tiles, keys, ids);
     VT_LAUNCH_CHECK("tile_order_keys_kernel");
-    return radix_sort_pairs(keys, tile_order, tiles, (int)TILE_ORDER_BITS, keys + tiles, s);
+    return radix_sort_pass(keys, ids, sorted_keys, tile_order, tiles, 0, sorted_keys + tiles, s);
 }
 
 extern "C" size_t vt_ray_order_workspace_size(uint32_t num_rays)

@@ -13,6 +13,14 @@ size_t scan_workspace_words(uint32_t n);
 // out[i] = sum(in[0..i)), u32 wrap-around; in == out allowed.
 int exclusive_scan_u32(const uint32_t *in, uint32_t *out, uint32_t n, uint32_t *ws, hipStream_t s);
 
+// Words of scratch (u32) needed by radix_sort_pass for n elements.
+size_t radix_pass_workspace_words(uint32_t n);
+// One stable counting-sort pass on the 8-bit digit (key >> shift) & 255:
+// (kin, vin)[0..n) scattered to (kout, vout) in ascending digit order, equal
+// digits in input order.  Outputs must not alias the inputs.
+int radix_sort_pass(const uint32_t *kin, const uint32_t *vin, uint32_t *kout, uint32_t *vout, uint32_t n, int shift,
+                    uint32_t *ws, hipStream_t s);
+
 // Words of scratch (u32) needed by radix_sort_pairs for n elements.
 size_t radix_sort_workspace_words(uint32_t n);
 // Stable ascending sort of keys[0..n) (the low `bits` bits are compared),

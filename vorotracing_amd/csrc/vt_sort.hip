@@ -189,32 +189,48 @@ __global__ __launch_bounds__(P_THREADS) void radix_scatter_kernel(const uint32_t
     }
 }
 
-size_t radix_sort_workspace_words(uint32_t n)
+size_t radix_pass_workspace_words(uint32_t n)
 {
     uint32_t tiles = (n + P_TILE - 1) / P_TILE;
-    return 2 * (size_t)n + 256 * (size_t)tiles + scan_workspace_words(256 * tiles);
+    return 256 * (size_t)tiles + scan_workspace_words(256 * tiles);
+}
+
+int radix_sort_pass(const uint32_t *kin, const uint32_t *vin, uint32_t *kout, uint32_t *vout, uint32_t n, int shift,
+                    uint32_t *ws, hipStream_t s)
+{
+    if (n == 0)
+        return VT_OK;
+    uint32_t tiles = (n + P_TILE - 1) / P_TILE;
+    uint32_t *hist = ws;
+    uint32_t *sws = hist + 256 * (size_t)tiles;
+    radix_hist_kernel<<<tiles, P_THREADS, 0, s>>>(kin, n, shift, hist, tiles);
+    VT_LAUNCH_CHECK("radix_hist_kernel");
+    int rc = exclusive_scan_u32(hist, hist, 256 * tiles, sws, s);
+    if (rc)
+        return rc;
+    radix_scatter_kernel<<<tiles, P_THREADS, 0, s>>>(kin, vin, kout, vout, n, shift, hist, tiles);
+    VT_LAUNCH_CHECK("radix_scatter_kernel");
+    return VT_OK;
+}
+
+size_t radix_sort_workspace_words(uint32_t n)
+{
+    return 2 * (size_t)n + radix_pass_workspace_words(n);
 }
 
 int radix_sort_pairs(uint32_t *keys, uint32_t *vals, uint32_t n, int bits, uint32_t *ws, hipStream_t s)
 {
     if (n <= 1)
         return VT_OK;
-    uint32_t tiles = (n + P_TILE - 1) / P_TILE;
     uint32_t *k2 = ws;
     uint32_t *v2 = ws + n;
-    uint32_t *hist = ws + 2 * (size_t)n;
-    uint32_t *sws = hist + 256 * (size_t)tiles;
+    uint32_t *pws = ws + 2 * (size_t)n;
     int passes = (bits + 7) / 8;
     uint32_t *ka = keys, *va = vals, *kb = k2, *vb = v2;
     for (int p = 0; p < passes; ++p) {
-        int shift = 8 * p;
-        radix_hist_kernel<<<tiles, P_THREADS, 0, s>>>(ka, n, shift, hist, tiles);
-        VT_LAUNCH_CHECK("radix_hist_kernel");
-        int rc = exclusive_scan_u32(hist, hist, 256 * tiles, sws, s);
+        int rc = radix_sort_pass(ka, va, kb, vb, n, 8 * p, pws, s);
         if (rc)
             return rc;
-        radix_scatter_kernel<<<tiles, P_THREADS, 0, s>>>(ka, va, kb, vb, n, shift, hist, tiles);
-        VT_LAUNCH_CHECK("radix_scatter_kernel");
         uint32_t *t = ka;
         ka = kb;
         kb = t;
