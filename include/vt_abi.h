@@ -215,6 +215,10 @@ int vt_trace_infer_q8_camera(const float *points, const uint8_t *diffuse, const 
  *   5): lane t traces ray ray_perm[t], overriding image_h/image_w; it must
  *   be a permutation of 0..num_rays-1 (an entry >= num_rays leaves its
  *   lane idle).  vt_ray_order makes one for flat batches.
+ *   tile_order, tile_cost (extensions, ABI version 9): with image lanes,
+ *   NULL or the launch order of the tiles (vt_tile_order; the forward
+ *   ignores its split count), and NULL or one u32 per tile receiving each
+ *   tile's cost for vt_tile_order, as for the tiled inference entries.
  */
 int vt_trace_fwd(int attr_dtype, const float *points, const void *diffuse, const void *specular, uint32_t diff_res,
                  uint32_t spec_res, const float *density, const uint32_t *adjacency, uint32_t adjacency_size,
@@ -248,6 +252,11 @@ int vt_trace_fwd(int attr_dtype, const float *points, const void *diffuse, const
  *   slots into points_grad and density_grad at its end.
  *   Gradient scatters of lanes that integrate the same cell in the same step
  *   are combined in LDS before the global atomics.
+ *   tile_order (an extension, ABI version 10): with image lanes, NULL or
+ *   the tiles + 1 words of vt_tile_order over the costs the forward of these
+ *   rays recorded.  Tiles launch in that order, and the first
+ *   tile_order[tiles] of them (at most vt_train_bwd_resident_waves()) run as
+ *   two half-waves of 32 rays each.
  */
 int vt_trace_bwd(int attr_dtype, const float *points, const void *diffuse, const void *specular, uint32_t diff_res,
                  uint32_t spec_res, const float *density, const uint32_t *adjacency, uint32_t adjacency_size,
@@ -368,18 +377,31 @@ int vt_tile_perm(uint32_t height, uint32_t width, uint32_t tile_h, uint32_t tile
  * entries (an extension; the reference launches blocks in screen order).
  * tile_cost (u32, one per tile) is what such a call wrote to its tile_cost
  * argument: 18 x the longest walk's steps + the most face records searched by
- * one ray of the tile.  tile_order (u32, one per tile) receives the tiles by
- * decreasing cost bucket (4 buckets per octave of the cost: floor(log2 c) and
- * the next two bits of c, cost 0 counted as 1), tiles of one bucket in screen
- * order, which keeps neighbouring tiles together; a call given it launches
- * tile tile_order[s] in slot s.  Launched longest first, a frame no longer
- * ends with a few long tiles running on an otherwise idle GPU.  Any order
- * gives bit-identical images (a ray's result does not depend on its lane).
+ * one ray of the tile.  tile_order (u32, tiles + 1 words) receives the tiles
+ * by decreasing cost bucket (4 buckets per octave of the cost: floor(log2 c)
+ * and the next two bits of c, cost 0 counted as 1), tiles of one bucket in
+ * screen order, which keeps neighbouring tiles together; a call given it
+ * launches tile tile_order[s] in slot s.  Launched longest first, a frame no
+ * longer ends with a few long tiles running on an otherwise idle GPU.  Any
+ * order gives bit-identical images (a ray's result does not depend on its
+ * lane).
+ * tile_order[tiles] receives the split count (ABI version 10): the number of
+ * tiles whose cost exceeds 4/5 of sum(cost) / split_waves, 0 when
+ * split_waves is 0.  split_waves is the number of waves the consuming launch
+ * holds at once (below 2^24): a tile costing more than one such wave's mean
+ * share still runs when the rest has drained.  The training backward runs
+ * the first tile_order[tiles] tiles of its order as two half-waves each (pass
+ * vt_train_bwd_resident_waves()); the inference entries ignore the count
+ * (pass 0).
  * workspace: vt_tile_order_workspace_size(tiles) bytes, 4-byte aligned.
  */
 size_t vt_tile_order_workspace_size(uint32_t tiles);
-int vt_tile_order(const uint32_t *tile_cost, uint32_t tiles, uint32_t *tile_order, void *workspace,
-                  vt_stream_t stream);
+int vt_tile_order(const uint32_t *tile_cost, uint32_t tiles, uint32_t split_waves, uint32_t *tile_order,
+                  void *workspace, vt_stream_t stream);
+/* Waves of the training backward that the current device holds at once
+ * (16 per CU), the split_waves of its tile orders; 0 if the device query
+ * fails. */
+uint32_t vt_train_bwd_resident_waves(void);
 
 /*
  * q8 quantisation.  Replaces VoroTracingInfer._quantize_to_uint8

@@ -17,7 +17,7 @@ def _declarations():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     decls = {}
-    for m in re.finditer(r"\b(?:int|size_t|const char \*)\s*(vt_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
+    for m in re.finditer(r"\b(?:int|size_t|uint32_t|const char \*)\s*(vt_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
         params = m.group(2).strip()
         n = 0 if params in ("", "void") else params.count(",") + 1
         decls[m.group(1)] = n
@@ -26,7 +26,7 @@ def _declarations():
 
 def test_header_declarations_parsed():
     d = _declarations()
-    assert len(d) == 40, sorted(d)
+    assert len(d) == 41, sorted(d)
     for name in ("vt_trace_infer_f16", "vt_trace_fwd", "vt_trace_bwd", "vt_bvh_query", "vt_morton_reorder"):
         assert name in d
 
@@ -45,10 +45,16 @@ def test_binding_matches_header_arity():
 
 def test_host_only_entries():
     lib = _lib.load()
-    assert lib.vt_abi_version() == 9
+    assert lib.vt_abi_version() == 10
     assert isinstance(lib.vt_last_error(), bytes)
     assert lib.vt_quantize_workspace_size() > 0
     assert lib.vt_morton_workspace_size(1000, 16000) >= lib.vt_morton_workspace_size(10, 160) > 0
+    # 16 backward waves per CU; 0 where no device answers
+    assert lib.vt_train_bwd_resident_waves() % 16 == 0
+    # split_waves is range-checked before any launch; no tiles is no work
+    assert lib.vt_tile_order(None, 0, 0, None, None, None) == 0
+    assert lib.vt_tile_order(C.c_void_p(16), 10, 1 << 24, C.c_void_p(16), C.c_void_p(16), None) == 1
+    assert b"split_waves" in lib.vt_last_error()
 
 
 def test_argument_errors_need_no_gpu():

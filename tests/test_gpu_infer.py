@@ -423,13 +423,19 @@ def test_tile_order_sorts_by_cost(gpu):
         cost[: tiles // 3] = cost[0]  # many ties
         cost[-3:] = (0, 1, 0xFFFFFFFF)[: min(3, tiles)]
         c = H.to_dev(cost, gpu)
-        order = torch.empty(tiles, dtype=torch.uint32, device=gpu)
+        order = torch.empty(tiles + 1, dtype=torch.uint32, device=gpu)
         ws = torch.empty(int(_lib.load().vt_tile_order_workspace_size(tiles)), dtype=torch.uint8, device=gpu)
-        _lib.call("vt_tile_order", c.data_ptr(), tiles, order.data_ptr(), ws.data_ptr(),
-                  torch.cuda.current_stream().cuda_stream)
-        torch.cuda.synchronize()
         want = np.argsort(H.tile_order_keys(cost), kind="stable")
-        assert np.array_equal(order.cpu().numpy().astype(np.int64), want), tiles
+        for split_waves in (0, 1, 4096, tiles, (1 << 24) - 1):
+            _lib.call("vt_tile_order", c.data_ptr(), tiles, split_waves, order.data_ptr(), ws.data_ptr(),
+                      torch.cuda.current_stream().cuda_stream)
+            torch.cuda.synchronize()
+            got = order.cpu().numpy().astype(np.int64)
+            assert np.array_equal(got[:tiles], want), tiles
+            # the split count: tiles costing more than 4/5 of the mean share of one of split_waves waves
+            c64, total = cost.astype(np.int64), int(cost.astype(np.int64).sum())
+            k = int(np.sum(5 * c64 * split_waves > 4 * total)) if split_waves else 0
+            assert got[tiles] == k, (tiles, split_waves)
 
 
 def test_tile_order_and_costs_of_a_render(gpu):
@@ -462,7 +468,7 @@ def test_tile_order_and_costs_of_a_render(gpu):
         torch.cuda.synchronize()
         assert torch.equal(again.view(torch.int16), ref.view(torch.int16))
     want = np.argsort(H.tile_order_keys(18 * nmax + fmax), kind="stable")
-    assert np.array_equal(sch.order.cpu().numpy().astype(np.int64), want)
+    assert np.array_equal(sch.order[:tiles].cpu().numpy().astype(np.int64), want)
     # a random launch order through the C ABI: same image
     order = H.to_dev(np.random.default_rng(5).permutation(tiles).astype(np.uint32), gpu)
     out = torch.empty_like(ref)

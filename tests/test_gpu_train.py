@@ -438,7 +438,7 @@ def test_backward_in_forward_cost_order(gpu):
     np.maximum.at(fmax, tile_of, fs["faces"].astype(np.int64))
     cost = 18 * nmax + fmax
     assert np.array_equal(sch.cost.cpu().numpy().astype(np.int64), cost)
-    assert np.array_equal(sch.order.cpu().numpy().astype(np.int64),
+    assert np.array_equal(sch.order[:TX * TY].cpu().numpy().astype(np.int64),
                           np.argsort(H.tile_order_keys(cost), kind="stable"))
     fw = core.trace_fwd(s.points, s.diffuse, s.specular, s.diff_res, s.spec_res, s.density, s.adjacency, s.offsets,
                         rays, start, weight_threshold=thr)
@@ -447,6 +447,67 @@ def test_backward_in_forward_cost_order(gpu):
                           W_total=fw["W_total"], S_total=fw["S_total"], t_far=fw["t_far"], weight_threshold=thr)
     for a, key in zip(res[True][1], ("points_grad", "diffuse_grad", "specular_grad", "density_grad")):
         H.assert_grad_close(a, want[key], key)
+
+
+@pytest.mark.parametrize("split,f16", [("all", False), ("all", True), ("part", False)])
+def test_backward_split_tiles(gpu, split, f16):
+    """The backward's costliest tiles run as two half-waves (vt_tile_order's
+    split count; TRAIN_SPLIT_WAVES forces it on a small frame: every tile,
+    or the tiles above 4/5 of the mean cost): per-ray walk statistics equal
+    the screen-order backward's, and the gradients agree with it and with
+    the oracle."""
+    s, rays, start, thr = _case("hf8")
+    scene_t = _scene_tensors(s, gpu, f16)
+    rd, sd = H.to_dev(rays, gpu), H.to_dev(start, gpu)
+    gn = np.random.default_rng(12).normal(size=rays.shape[:-1] + (4,)).astype(np.float16 if f16 else np.float32)
+    g = H.to_dev(gn, gpu)
+    Hh, W = rays.shape[:2]
+    tiles = ((W + 7) // 8) * ((Hh + 7) // 8)
+    saved = (_C.TRAIN_TILE_ORDER, _C.TRAIN_SPLIT_WAVES)
+    try:
+        res = {}
+        for flag in (False, True):
+            _C.TRAIN_TILE_ORDER = flag
+            _C.TRAIN_SPLIT_WAVES = (1 << 23) if split == "all" else tiles
+            _C._TRAIN_SCHEDULES.clear()
+            out = _C.trace_vorotracing_fwd(*scene_t, rd, sd, None, thr, 1024, False)
+            st = native.new_stats(rays.size // 6, gpu)
+            grads = _C.trace_vorotracing_bwd(*scene_t, rd, sd, out[0], g, None, None, None, None, 0.0, out[5], None,
+                                             out[6], out[7], out[8], thr, 1024, stats=st)
+            torch.cuda.synchronize()
+            res[flag] = ([x.float().cpu().numpy() for x in grads[:4]], H.stats_np(st))
+        sch = next(iter(_C._TRAIN_SCHEDULES.values()))
+    finally:
+        _C.TRAIN_TILE_ORDER, _C.TRAIN_SPLIT_WAVES = saved
+        _C._TRAIN_SCHEDULES.clear()
+    cost = sch.cost.cpu().numpy().astype(np.int64)
+    k = int(sch.order[tiles].item())
+    want_k = tiles if split == "all" else int(np.sum(5 * cost * tiles > 4 * cost.sum()))
+    assert k == want_k and 0 < k, (k, want_k)
+    resident = int(_lib.load().vt_train_bwd_resident_waves())
+    assert resident >= tiles  # every counted tile was split (the launch adds min(tiles, resident) waves)
+    H.assert_stats_equal(res[True][1], res[False][1])
+    adt = np.float16 if f16 else np.float32
+    fw = core.trace_fwd(s.points, s.diffuse.astype(adt), s.specular.astype(adt), s.diff_res, s.spec_res, s.density,
+                        s.adjacency, s.offsets, rays, start, weight_threshold=thr)
+    want = core.trace_bwd(s.points, s.diffuse.astype(adt), s.specular.astype(adt), s.diff_res, s.spec_res,
+                          s.density, s.adjacency, s.offsets, rays, start, fw["rgba"], gn, distortion=fw["distortion"],
+                          W_total=fw["W_total"], S_total=fw["S_total"], t_far=fw["t_far"], weight_threshold=thr)
+    keys = ("points_grad", "diffuse_grad", "specular_grad", "density_grad")
+    if not f16:
+        for a, b, key in zip(res[True][0], res[False][0], keys):
+            H.assert_grad_close(a, b, key)
+            H.assert_grad_close(a, want[key], key)
+    else:
+        # half-precision texture sums: each run within the accumulation bound
+        # of the oracle's absolute sums and add counts
+        A, K = H.f16_train_sums(s, rays, start, thr, fw, gn)
+        for flag in (False, True):
+            for a, key in zip(res[flag][0], keys):
+                if key in ("points_grad", "density_grad"):
+                    H.assert_grad_close(a, want[key], key, abs_sum=A[key])
+                else:
+                    H.assert_f16_sum_close(a, want[key], A[key], K[key], key)
 
 
 def test_model_sort_morton(gpu):

@@ -140,8 +140,15 @@ def _drop_in_schedule(ray_perm_in: torch.Tensor, lay, device) -> "native.TileSch
 # for 4,096 backward wave slots; in screen order its backward lost about a
 # quarter of its time to the tiles that run last (C2 backward 3.95 -> 3.40
 # ms).  A forward launched by the previous step's costs ran slower (1.16 ->
-# 1.18 ms), so the forward keeps screen order.
+# 1.18 ms), so the forward keeps screen order.  The backward also runs its
+# costliest tiles as two half-waves each (vt_tile_order's split count over
+# the waves the device holds at once): at C2 the launch otherwise ends with
+# the few costliest tiles, started first and still running alone (3.38 ->
+# 2.88 ms); at C5 (25,350 tiles) no tile exceeds the share and nothing is
+# split.  TRAIN_SPLIT_WAVES overrides the resident-wave count (0: no split;
+# tests use large values to split small frames).
 TRAIN_TILE_ORDER = True
+TRAIN_SPLIT_WAVES: Optional[int] = None
 _TRAIN_SCHEDULES: dict = {}
 
 
@@ -150,7 +157,9 @@ def _train_schedule(rays, img_h: int, img_w: int, num_rays: int, device) -> Opti
         return None
     images = num_rays // (img_h * img_w)
     key = (images, img_h, img_w, _stream(device))
-    return native.schedule_for(_TRAIN_SCHEDULES, key, native.num_tiles(images, img_h, img_w), device)
+    return native.schedule_for(_TRAIN_SCHEDULES, key, native.num_tiles(images, img_h, img_w), device,
+                               split_waves=TRAIN_SPLIT_WAVES if TRAIN_SPLIT_WAVES is not None
+                               else int(_lib.load().vt_train_bwd_resident_waves()))
 
 
 def _checked_perm(ray_perm_in: torch.Tensor, num_rays: int) -> torch.Tensor:

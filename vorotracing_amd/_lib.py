@@ -66,7 +66,8 @@ SIGNATURES = {
     "vt_nearest_sites_noalloc": ([P, U32, P, U32, P, P], C.c_int),
     "vt_tile_perm": ([U32, U32, U32, U32, P, P], C.c_int),
     "vt_tile_order_workspace_size": ([U32], C.c_size_t),
-    "vt_tile_order": ([P, U32, P, P, P], C.c_int),
+    "vt_tile_order": ([P, U32, U32, P, P, P], C.c_int),
+    "vt_train_bwd_resident_waves": ([], U32),
     "vt_morton_workspace_size": ([U32, U32], C.c_size_t),
     "vt_morton_reorder": ([P, U32, P, U32, P, P, P, P, P, P, P], C.c_int),
     "vt_permute_rows": ([P, U32, U32, P, P, P], C.c_int),

@@ -431,6 +431,47 @@ __global__ void tile_order_keys_kernel(const uint32_t *__restrict__ cost, uint32
     ids[t] = t;
 }
 
+// A tile is split when its cost exceeds SPLIT_NUM / SPLIT_DEN of the mean
+// load of one resident wave (total cost / split_waves): such a tile, started
+// first, still runs when the launch's other work has drained, and the
+// launch ends with it.  Tiles below that are covered by the other waves.
+constexpr uint64_t SPLIT_NUM = 4, SPLIT_DEN = 5;
+constexpr uint32_t SPLIT_THREADS = 1024;
+
+__device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, uint64_t *red)
+{
+    red[threadIdx.x] = v;
+    __syncthreads();
+    for (uint32_t h = SPLIT_THREADS / 2; h > 0; h >>= 1) {
+        if (threadIdx.x < h)
+            red[threadIdx.x] += red[threadIdx.x + h];
+        __syncthreads();
+    }
+    const uint64_t total = red[0];
+    __syncthreads();
+    return total;
+}
+
+// out = the number of tiles to split (one block; tiles are few)
+__global__ __launch_bounds__(SPLIT_THREADS) void tile_split_kernel(const uint32_t *__restrict__ cost, uint32_t tiles,
+                                                                   uint32_t split_waves, uint32_t *__restrict__ out)
+{
+    __shared__ uint64_t red[SPLIT_THREADS];
+    uint64_t sum = 0;
+    for (uint32_t t = threadIdx.x; t < tiles; t += SPLIT_THREADS)
+        sum += cost[t];
+    const uint64_t total = block_sum_u64(sum, red);
+    // (the left side stays below 2^59: cost < 2^32, split_waves < 2^24; a
+    // total of 2^57 or more splits nothing and would overflow on the right)
+    uint64_t n = 0;
+    if (total < (1ull << 57))
+        for (uint32_t t = threadIdx.x; t < tiles; t += SPLIT_THREADS)
+            n += SPLIT_DEN * (uint64_t)cost[t] * split_waves > SPLIT_NUM * total;
+    const uint64_t k = block_sum_u64(n, red);
+    if (threadIdx.x == 0)
+        *out = split_waves ? (uint32_t)k : 0u;
+}
+
 } // namespace vt
 
 // workspace: keys, tile ids, sorted keys (tiles words each), then one radix pass
@@ -439,21 +480,27 @@ extern "C" size_t vt_tile_order_workspace_size(uint32_t tiles)
     return (3 * (size_t)tiles + radix_pass_workspace_words(tiles)) * 4;
 }
 
-extern "C" int vt_tile_order(const uint32_t *tile_cost, uint32_t tiles, uint32_t *tile_order, void *workspace,
-                             vt_stream_t stream)
+extern "C" int vt_tile_order(const uint32_t *tile_cost, uint32_t tiles, uint32_t split_waves, uint32_t *tile_order,
+                             void *workspace, vt_stream_t stream)
 {
     clear_error();
     if (tiles == 0)
         return VT_OK;
     VT_REQUIRE(tile_cost && tile_order && workspace, "null pointer argument");
     VT_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 4 == 0, "workspace must be 4-byte aligned");
+    VT_REQUIRE(split_waves < (1u << 24), "split_waves (%u) must be below 2^24", split_waves);
     hipStream_t s = as_stream(stream);
     uint32_t *keys = static_cast<uint32_t *>(workspace);
     uint32_t *ids = keys + tiles;
     uint32_t *sorted_keys = ids + tiles;
     tile_order_keys_kernel<<<(tiles + 255) / 256, 256, 0, s>>>(tile_cost, tiles, keys, ids);
     VT_LAUNCH_CHECK("tile_order_keys_kernel");
-    return radix_sort_pass(keys, ids, sorted_keys, tile_order, tiles, 0, sorted_keys + tiles, s);
+    int rc = radix_sort_pass(keys, ids, sorted_keys, tile_order, tiles, 0, sorted_keys + tiles, s);
+    if (rc)
+        return rc;
+    tile_split_kernel<<<1, SPLIT_THREADS, 0, s>>>(tile_cost, tiles, split_waves, tile_order + tiles);
+    VT_LAUNCH_CHECK("tile_split_kernel");
+    return VT_OK;
 }
 
 extern "C" size_t vt_ray_order_workspace_size(uint32_t num_rays)

@@ -7,6 +7,7 @@
 // point_error), lanes of one cell combined in LDS first, with global atomics
 // (f32: hardware global_atomic_add_f32; f16: the packed-f16 global atomic
 // add on the aligned pair holding the half, +0 into the other half).
+#include <algorithm>
 #include <type_traits>
 
 #include "vt_internal.h"
@@ -128,6 +129,14 @@ __device__ __forceinline__ uint32_t train_tile(uint32_t s, const uint32_t *tile_
     return tile_order ? tile_order[s >> 6] : s >> 6;
 }
 
+// Ray of launch slot s.  Tiled rays with a tile order: wave j runs tile
+// tile_order[j].  With SPLIT (the backward), the first k tiles of the order,
+// k = tile_order[tiles] clamped to the waves the launch added for them, run
+// as two half-waves each: waves 2i and 2i + 1 take rows 0-3 and rows 4-7 of
+// tile tile_order[i] on lanes 0-31 (lanes 32-63 idle), and wave 2k + j
+// takes tile tile_order[k + j].  A long tile, which the launch would
+// otherwise end waiting for, then ends about as early as the rest.
+template <bool SPLIT>
 __device__ __forceinline__ uint32_t train_ray(uint32_t s, uint32_t num_rays, const uint32_t *perm, uint32_t ni,
                                               uint32_t h, uint32_t w, const uint32_t *tile_order)
 {
@@ -137,9 +146,29 @@ __device__ __forceinline__ uint32_t train_ray(uint32_t s, uint32_t num_rays, con
         const uint32_t r = perm[s];
         return r < num_rays ? r : NONE;
     }
-    if (ni)
-        return tiled_ray<TRAIN_TILE_STRIP>(train_tile(s, tile_order) * 64u + (s & 63u), ni, h, w, TRAIN_TILE,
-                                           TRAIN_TILE);
+    if (ni) {
+        uint32_t t = s >> 6, within = s & 63u;
+        if (tile_order) {
+            const uint32_t tiles = ni * ((w + TRAIN_TILE - 1) / TRAIN_TILE) * ((h + TRAIN_TILE - 1) / TRAIN_TILE);
+            if (SPLIT) {
+                const uint32_t waves = gridDim.x * (blockDim.x / 64u);
+                const uint32_t extra = waves > tiles ? waves - tiles : 0u;
+                const uint32_t k = min(min(tile_order[tiles], tiles), extra);
+                if (t < 2u * k) {
+                    if (within >= 32u)
+                        return NONE;
+                    within += (t & 1u) * 32u;
+                    t >>= 1;
+                } else {
+                    t -= k;
+                }
+            }
+            if (t >= tiles)
+                return NONE;
+            t = tile_order[t];
+        }
+        return tiled_ray<TRAIN_TILE_STRIP>(t * 64u + within, ni, h, w, TRAIN_TILE, TRAIN_TILE);
+    }
     return s < num_rays ? s : NONE;
 }
 
@@ -320,7 +349,7 @@ template <typename A, int RD, int RS, bool STATS>
 __global__ __launch_bounds__(TRAIN_BLOCK) __attribute__((amdgpu_waves_per_eu(6))) void fwd_kernel(FwdArgs a)
 {
     const uint32_t s = xcd_interleaved_block<TRAIN_XCD_CHUNK>() * blockDim.x + threadIdx.x;
-    const uint32_t r = train_ray(s, a.num_rays, a.ray_perm, a.num_images, a.img_h, a.img_w, a.tile_order);
+    const uint32_t r = train_ray<false>(s, a.num_rays, a.ray_perm, a.num_images, a.img_h, a.img_w, a.tile_order);
     uint32_t n = 0, faces = 0;
     if (r != NONE)
         n = fwd_ray<A, RD, RS, STATS>(a, r, faces);
@@ -766,8 +795,8 @@ __global__ __launch_bounds__(TRAIN_BLOCK) __attribute__((amdgpu_waves_per_eu(4))
     if ((threadIdx.x & 63u) < (uint32_t)ROW_STRIDE)
         rows[64 * ROW_STRIDE + (threadIdx.x & 63u)] = 0.0f; // the zero row
     wave_lds_sync();
-    uint32_t r = train_ray(xcd_interleaved_block<TRAIN_XCD_CHUNK>() * blockDim.x + threadIdx.x, a.num_rays, a.ray_perm,
-                           a.num_images, a.img_h, a.img_w, a.tile_order);
+    uint32_t r = train_ray<true>(xcd_interleaved_block<TRAIN_XCD_CHUNK>() * blockDim.x + threadIdx.x, a.num_rays,
+                                 a.ray_perm, a.num_images, a.img_h, a.img_w, a.tile_order);
     if (r == NONE)
         return;
     BwdIntegrator<A, RD, RS> it;
@@ -851,13 +880,40 @@ static void set_lane_order(Args &a, uint32_t num_rays, const uint32_t *ray_perm,
     }
 }
 
+template <typename A, int RD, int RS, bool ST> struct FwdK {
+    static constexpr auto fn = fwd_kernel<A, RD, RS, ST>;
+    static constexpr bool split = false;
+};
+template <typename A, int RD, int RS, bool ST> struct BwdK {
+    static constexpr auto fn = bwd_kernel<A, RD, RS, ST>;
+    static constexpr bool split = true;
+};
+
+// Waves of the training backward resident at once on the current device: 4
+// per SIMD (its register budget, amdgpu_waves_per_eu(4)), 4 SIMDs per CU.
+static uint32_t bwd_resident_waves()
+{
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        return 0;
+    return (uint32_t)cus * 16u;
+}
+
 template <template <typename, int, int, bool> class K, typename Args, typename A, int RD, int RS>
 static int launch_train_rs(const Args &a, bool stats, hipStream_t s)
 {
     uint64_t slots = a.num_rays;
-    if (a.num_images)
-        slots = (uint64_t)a.num_images * ((a.img_h + TRAIN_TILE - 1) / TRAIN_TILE) *
-                ((a.img_w + TRAIN_TILE - 1) / TRAIN_TILE) * (TRAIN_TILE * TRAIN_TILE);
+    if (a.num_images) {
+        const uint64_t tiles = (uint64_t)a.num_images * ((a.img_h + TRAIN_TILE - 1) / TRAIN_TILE) *
+                               ((a.img_w + TRAIN_TILE - 1) / TRAIN_TILE);
+        slots = tiles * (TRAIN_TILE * TRAIN_TILE);
+        // the waves that run split tiles' second halves (at most one per
+        // resident wave: the split count stays below 1.25x that; see
+        // vt_tile_order)
+        if (K<A, RD, RS, false>::split && a.tile_order)
+            slots += std::min<uint64_t>(tiles, bwd_resident_waves()) * 64;
+    }
     dim3 grid((uint32_t)((slots + TRAIN_BLOCK - 1) / TRAIN_BLOCK)), block(TRAIN_BLOCK);
     if (stats)
         hipLaunchKernelGGL((K<A, RD, RS, true>::fn), grid, block, 0, s, a);
@@ -867,12 +923,6 @@ static int launch_train_rs(const Args &a, bool stats, hipStream_t s)
     return VT_OK;
 }
 
-template <typename A, int RD, int RS, bool ST> struct FwdK {
-    static constexpr auto fn = fwd_kernel<A, RD, RS, ST>;
-};
-template <typename A, int RD, int RS, bool ST> struct BwdK {
-    static constexpr auto fn = bwd_kernel<A, RD, RS, ST>;
-};
 
 template <template <typename, int, int, bool> class K, typename Args, typename A>
 static int launch_train_a(const Args &a, uint32_t rd, uint32_t rs, bool stats, hipStream_t s)
@@ -1076,6 +1126,11 @@ __global__ void f16_atomic_probe_kernel(uint16_t *halves, uint32_t num_halves, c
 }
 
 } // namespace vt
+
+extern "C" uint32_t vt_train_bwd_resident_waves(void)
+{
+    return vt::bwd_resident_waves();
+}
 
 extern "C" int vt_debug_f16_atomic_add(uint16_t *halves, uint32_t num_halves, const uint32_t *index,
                                        const float *values, uint32_t n, vt_stream_t stream)

@@ -119,22 +119,29 @@ class TileSchedule:
     them).  Images are bit-identical in any order.  One schedule per stream:
     a launch reads the costs the previous launch on its stream wrote."""
 
-    def __init__(self, tiles: int, device):
+    def __init__(self, tiles: int, device, split_waves: int = 0):
         self.tiles = int(tiles)
+        # waves the consuming launch holds at once (vt_tile_order's split
+        # count; 0: the inference entries, which ignore it)
+        self.split_waves = int(split_waves)
         self.cost = torch.zeros(self.tiles, dtype=torch.uint32, device=device)
-        self.order = torch.empty(self.tiles, dtype=torch.uint32, device=device)
+        # the order, then the split count
+        self.order = torch.empty(self.tiles + 1, dtype=torch.uint32, device=device)
         self.ws = torch.empty(int(_lib.load().vt_tile_order_workspace_size(self.tiles)), dtype=torch.uint8,
                               device=device)
         self.frame = None  # the frame whose costs self.cost holds
+
+    def _sort(self, stream: int):
+        _lib.call("vt_tile_order", self.cost.data_ptr(), self.tiles, self.split_waves, self.order.data_ptr(),
+                  self.ws.data_ptr(), stream)
+        return self.order.data_ptr()
 
     def launch_args(self, stream: int, frame):
         """(tile_order, tile_cost) pointers for the next launch on ``stream``
         of ``frame`` (a hashable identity of the launch's rays or cameras)."""
         order = None
         if frame is not None and frame == self.frame:
-            _lib.call("vt_tile_order", self.cost.data_ptr(), self.tiles, self.order.data_ptr(), self.ws.data_ptr(),
-                      stream)
-            order = self.order.data_ptr()
+            order = self._sort(stream)
         self.frame = frame
         return order, self.cost.data_ptr()
 
@@ -150,8 +157,7 @@ class TileSchedule:
         None when the costs are of another frame."""
         if frame is None or frame != self.frame:
             return None
-        _lib.call("vt_tile_order", self.cost.data_ptr(), self.tiles, self.order.data_ptr(), self.ws.data_ptr(), stream)
-        return self.order.data_ptr()
+        return self._sort(stream)
 
 
 def frame_key(t: torch.Tensor):
@@ -162,12 +168,12 @@ def frame_key(t: torch.Tensor):
     return (id(t), t.data_ptr(), t._version)
 
 
-def schedule_for(cache: dict, key, tiles: int, device, limit: int = 16) -> TileSchedule:
+def schedule_for(cache: dict, key, tiles: int, device, limit: int = 16, split_waves: int = 0) -> TileSchedule:
     """The TileSchedule of ``key`` in ``cache`` (created on first use; the
     cache keeps the ``limit`` most recent)."""
     sch = cache.pop(key, None)
-    if sch is None or sch.tiles != tiles:
-        sch = TileSchedule(tiles, device)
+    if sch is None or sch.tiles != tiles or sch.split_waves != split_waves:
+        sch = TileSchedule(tiles, device, split_waves)
     cache[key] = sch
     while len(cache) > limit:
         cache.pop(next(iter(cache)))
