@@ -215,10 +215,17 @@ int vt_trace_infer_q8_camera(const float *points, const uint8_t *diffuse, const 
  *   5): lane t traces ray ray_perm[t], overriding image_h/image_w; it must
  *   be a permutation of 0..num_rays-1 (an entry >= num_rays leaves its
  *   lane idle).  vt_ray_order makes one for flat batches.
- *   tile_order, tile_cost (extensions, ABI version 9): with image lanes,
- *   NULL or the launch order of the tiles (vt_tile_order; the forward
- *   ignores its split count), and NULL or one u32 per tile receiving each
- *   tile's cost for vt_tile_order, as for the tiled inference entries.
+ *   tile_order, tile_cost (extensions, ABI versions 9-10): with image lanes,
+ *   NULL or the tiles + 1 words of vt_tile_order (split_waves =
+ *   vt_train_fwd_resident_waves()) over the costs a forward of the same rays
+ *   recorded, and NULL or one u32 per tile receiving each tile's cost for
+ *   vt_tile_order, as for the tiled inference entries.  Given an order with a
+ *   non-zero split count, the launch takes the tiles in that order and runs
+ *   the first tile_order[tiles] as two half-waves each (rows 0-3, rows 4-7);
+ *   a split tile's cost is then the larger of its halves' costs (each
+ *   half's longest walk and most face records), recorded with an atomic max:
+ *   clear tile_cost before such a call.  With a split count of 0 the order
+ *   is ignored (screen order).
  */
 int vt_trace_fwd(int attr_dtype, const float *points, const void *diffuse, const void *specular, uint32_t diff_res,
                  uint32_t spec_res, const float *density, const uint32_t *adjacency, uint32_t adjacency_size,
@@ -320,6 +327,19 @@ int vt_bvh_num_nodes(void *handle);
 size_t vt_nearest_scan_workspace_size(uint32_t num_queries);
 int vt_bvh_query_ws(void *handle, const float *points, uint32_t num_points, const float *queries, uint32_t num_queries,
                     int32_t *out, void *workspace, size_t workspace_bytes, vt_stream_t stream);
+/*
+ * Start cells of a ray batch: start[i] = the site nearest the origin of ray
+ * i (rays (num_rays, 6) f32, origin first; the reference's per-ray query of
+ * vorotracing.py:323-344, nn_bvh.cu:91-109), with the tree's distance and
+ * tie rule.  One tree query per run of equal consecutive origins (a
+ * camera's rays share one, a rolling shutter has one per row), counted and
+ * compacted on the device, so the call never waits for the GPU (an
+ * extension, ABI version 10).  workspace: vt_start_cells_workspace_size(
+ * num_rays) bytes, 4-byte aligned.  The handle is only read.
+ */
+size_t vt_start_cells_workspace_size(uint32_t num_rays);
+int vt_start_cells(void *handle, const float *points, uint32_t num_points, const float *rays, uint32_t num_rays,
+                   uint32_t *start, void *workspace, vt_stream_t stream);
 /* Test hook (no reference counterpart): caps the tree walk's stack at `limit`
  * entries (1..64; 0 restores 64) and, if force_tree, makes every query walk
  * the tree.  A query whose stack would overflow answers by a scan of all
@@ -391,16 +411,18 @@ int vt_tile_perm(uint32_t height, uint32_t width, uint32_t tile_h, uint32_t tile
  * holds at once (below 2^24): a tile costing more than one such wave's mean
  * share still runs when the rest has drained.  The training backward runs
  * the first tile_order[tiles] tiles of its order as two half-waves each (pass
- * vt_train_bwd_resident_waves()); the inference entries ignore the count
- * (pass 0).
+ * vt_train_bwd_resident_waves()), and so does the forward when the count is
+ * non-zero (pass vt_train_fwd_resident_waves()); the inference entries
+ * ignore the count (pass 0).
  * workspace: vt_tile_order_workspace_size(tiles) bytes, 4-byte aligned.
  */
 size_t vt_tile_order_workspace_size(uint32_t tiles);
 int vt_tile_order(const uint32_t *tile_cost, uint32_t tiles, uint32_t split_waves, uint32_t *tile_order,
                   void *workspace, vt_stream_t stream);
-/* Waves of the training backward that the current device holds at once
- * (16 per CU), the split_waves of its tile orders; 0 if the device query
- * fails. */
+/* Waves of the training forward (24 per CU) and backward (16 per CU) that
+ * the current device holds at once, the split_waves of their tile orders; 0
+ * if the device query fails. */
+uint32_t vt_train_fwd_resident_waves(void);
 uint32_t vt_train_bwd_resident_waves(void);
 
 /*

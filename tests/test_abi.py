@@ -26,7 +26,7 @@ def _declarations():
 
 def test_header_declarations_parsed():
     d = _declarations()
-    assert len(d) == 41, sorted(d)
+    assert len(d) == 44, sorted(d)
     for name in ("vt_trace_infer_f16", "vt_trace_fwd", "vt_trace_bwd", "vt_bvh_query", "vt_morton_reorder"):
         assert name in d
 
@@ -49,7 +49,8 @@ def test_host_only_entries():
     assert isinstance(lib.vt_last_error(), bytes)
     assert lib.vt_quantize_workspace_size() > 0
     assert lib.vt_morton_workspace_size(1000, 16000) >= lib.vt_morton_workspace_size(10, 160) > 0
-    # 16 backward waves per CU; 0 where no device answers
+    # 24 forward and 16 backward waves per CU; 0 where no device answers
+    assert lib.vt_train_fwd_resident_waves() * 2 == lib.vt_train_bwd_resident_waves() * 3
     assert lib.vt_train_bwd_resident_waves() % 16 == 0
     # split_waves is range-checked before any launch; no tiles is no work
     assert lib.vt_tile_order(None, 0, 0, None, None, None) == 0

@@ -31,6 +31,36 @@ def test_bvh_exact_nearest(gpu, n, nq, seed):
     assert np.array_equal(got, want)
 
 
+def test_start_cells_runs(gpu):
+    """NNBVH.start_cells (vt_start_cells): the nearest site of every ray's
+    origin, against the brute-force oracle, for runs of equal consecutive
+    origins of lengths 300, 1, 2 and 7, an origin repeated after other runs,
+    origins on duplicated sites (lowest index), and 600,000 single-ray runs
+    (more than one pass of the grid-stride query: 2048 blocks x 256 lanes);
+    the batch's shape is kept, and an empty batch gives an empty result."""
+    rng = np.random.default_rng(21)
+    n = 5000
+    pts = rng.normal(size=(n, 3)).astype(np.float32)
+    pts[20] = pts[30] = pts[10]  # duplicates: the lowest index wins
+    a, b, c = rng.normal(size=(3, 3)).astype(np.float32)
+    runs = [(a, 300), (b, 1), (c, 2), (pts[30], 7), (a, 5), (b, 3)]
+    o = np.concatenate([np.repeat(x[None], k, 0) for x, k in runs] +
+                       [rng.normal(size=(600000, 3)).astype(np.float32) * 1.5])
+    rays = np.concatenate([o, rng.normal(size=o.shape).astype(np.float32)], axis=1)
+    assert rays.shape[0] % 256 != 0
+    bvh = ops.NNBVH()
+    pd = H.to_dev(pts, gpu)
+    bvh.build(pd)
+    got = bvh.start_cells(pd, H.to_dev(rays, gpu))
+    assert got.dtype == torch.uint32 and tuple(got.shape) == (rays.shape[0],)
+    want = host_ops.nearest_site(pts, o)
+    assert np.array_equal(got.cpu().numpy().astype(np.int64), want.astype(np.int64))
+    assert int(got[300 + 1 + 2].item()) == 10
+    img = H.to_dev(rays[:12 * 20].reshape(12, 20, 6), gpu)
+    assert np.array_equal(bvh.start_cells(pd, img).cpu().numpy().astype(np.int64).reshape(-1), want[:240])
+    assert bvh.start_cells(pd, torch.empty((0, 6), device=gpu)).numel() == 0
+
+
 def test_bvh_ties_lowest_index(gpu):
     """Duplicate sites and equidistant sites: lowest index wins (brute force rule)."""
     base = np.array([[0, 0, 0], [1, 0, 0], [0, 1, 0], [1, 1, 0]], np.float32)

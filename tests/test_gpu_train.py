@@ -290,8 +290,7 @@ def test_start_cells_any_ray_order(gpu):
     rays = rays[np.random.default_rng(3).permutation(rays.shape[0])]
     got = model.get_starting_point(H.to_dev(rays, gpu)).cpu().numpy()
     assert np.array_equal(got, H.start_for(s, rays))
-    # a larger shuffled batch: runs about as many as rays, so the distinct
-    # origins are queried once each (torch.unique)
+    # a larger shuffled batch: runs about as many as rays, one query each
     big = np.concatenate([camera.pinhole_rays(48, 32, eye=e).reshape(-1, 6) for e in eyes])
     big = big[np.random.default_rng(4).permutation(big.shape[0])]
     assert np.array_equal(model.get_starting_point(H.to_dev(big, gpu)).cpu().numpy(), H.start_for(s, big))
@@ -447,6 +446,71 @@ def test_backward_in_forward_cost_order(gpu):
                           W_total=fw["W_total"], S_total=fw["S_total"], t_far=fw["t_far"], weight_threshold=thr)
     for a, key in zip(res[True][1], ("points_grad", "diffuse_grad", "specular_grad", "density_grad")):
         H.assert_grad_close(a, want[key], key)
+
+
+@pytest.mark.parametrize("split", ["all", "part"])
+def test_forward_split_tiles(gpu, split):
+    """A forward of rays rendered again launches by the previous forward's
+    tile costs and runs the tiles above the split share as two half-waves
+    (TRAIN_SPLIT_WAVES forces splits on a small frame): every per-ray output
+    and walk statistic equals the screen-order forward's, bit for bit; the
+    split count follows from the previous costs; a whole tile records 18 x
+    its longest walk + its most face records, a split tile the larger of its
+    halves' (rows 0-3, rows 4-7) such costs (an atomic max into cleared
+    costs)."""
+    s, rays, start, thr = _case("hf8")
+    scene_t = _scene_tensors(s, gpu, False)
+    rd, sd = H.to_dev(rays, gpu), H.to_dev(start, gpu)
+    q = H.to_dev(np.tile(np.array([0.7, 0.2], np.float32), rays.shape[:-1] + (1,)), gpu)
+    Hh, W = rays.shape[:2]
+    TX, TY = (W + 7) // 8, (Hh + 7) // 8
+    tiles = TX * TY
+    waves = (1 << 23) if split == "all" else tiles
+    saved = (_C.TRAIN_TILE_ORDER, _C.TRAIN_SPLIT_WAVES)
+    try:
+        _C.TRAIN_TILE_ORDER = True
+        _C.TRAIN_SPLIT_WAVES = waves
+        _C._TRAIN_SCHEDULES.clear()
+        runs = []
+        for _ in range(3):  # screen order, then twice by the recorded costs
+            st = native.new_stats(rays.size // 6, gpu)
+            out = _C.trace_vorotracing_fwd(*scene_t, rd, sd, q, thr, 1024, False, stats=st)
+            sch = next(iter(_C._TRAIN_SCHEDULES.values()))
+            torch.cuda.synchronize()
+            runs.append(([None if x is None else x.cpu().numpy() for x in out], H.stats_np(st),
+                         sch.cost.cpu().numpy().astype(np.int64), sch.order.cpu().numpy().astype(np.int64)))
+    finally:
+        _C.TRAIN_TILE_ORDER, _C.TRAIN_SPLIT_WAVES = saved
+        _C._TRAIN_SCHEDULES.clear()
+    assert int(_lib.load().vt_train_fwd_resident_waves()) >= tiles  # the launch had a wave for every half
+    # per-tile and per-half maxima of the walk statistics (2-wide tile strips)
+    yy, xx = np.meshgrid(np.arange(Hh), np.arange(W), indexing="ij")
+    tx, ty = xx // 8, yy // 8
+    sp = tx // 2
+    wd = np.where((sp + 1) * 2 <= TX, 2, TX - sp * 2)
+    tile_of = (sp * 2 * TY + ty * wd + (tx - sp * 2)).reshape(-1)
+    half_of = ((yy % 8) // 4).reshape(-1)
+    st0 = runs[0][1]
+    def cost_of(sel):
+        nmax, fmax = np.zeros(tiles, np.int64), np.zeros(tiles, np.int64)
+        np.maximum.at(nmax, tile_of[sel], st0["n"][sel].astype(np.int64))
+        np.maximum.at(fmax, tile_of[sel], st0["faces"][sel].astype(np.int64))
+        return 18 * nmax + fmax
+    whole = cost_of(np.ones(tile_of.size, bool))
+    halves = np.maximum(cost_of(half_of == 0), cost_of(half_of == 1))
+    assert np.array_equal(runs[0][2], whole)
+    for i in (1, 2):
+        out, stats, cost, order = runs[i]
+        for a, b in zip(out, runs[0][0]):
+            assert (a is None and b is None) or np.array_equal(a, b)
+        H.assert_stats_equal(stats, runs[0][1])
+        prev = runs[i - 1][2]
+        k = int(np.sum(5 * prev * waves > 4 * prev.sum()))
+        assert 0 < k == order[tiles], (k, order[tiles])
+        assert np.array_equal(order[:tiles], np.argsort(H.tile_order_keys(prev), kind="stable"))
+        split_set = np.zeros(tiles, bool)
+        split_set[order[:k]] = True
+        assert np.array_equal(cost, np.where(split_set, halves, whole)), i
 
 
 @pytest.mark.parametrize("split,f16", [("all", False), ("all", True), ("part", False)])

@@ -139,14 +139,15 @@ def _drop_in_schedule(ray_perm_in: torch.Tensor, lay, device) -> "native.TileSch
 # launches its tiles by decreasing cost.  A single C2 camera has 7,500 tiles
 # for 4,096 backward wave slots; in screen order its backward lost about a
 # quarter of its time to the tiles that run last (C2 backward 3.95 -> 3.40
-# ms).  A forward launched by the previous step's costs ran slower (1.16 ->
-# 1.18 ms), so the forward keeps screen order.  The backward also runs its
-# costliest tiles as two half-waves each (vt_tile_order's split count over
-# the waves the device holds at once): at C2 the launch otherwise ends with
-# the few costliest tiles, started first and still running alone (3.38 ->
-# 2.88 ms); at C5 (25,350 tiles) no tile exceeds the share and nothing is
-# split.  TRAIN_SPLIT_WAVES overrides the resident-wave count (0: no split;
-# tests use large values to split small frames).
+# ms).  Both passes also run their costliest tiles as two half-waves each
+# (vt_tile_order's split count over the waves the device holds of that
+# kernel at once): at C2 each launch otherwise ends with the few costliest
+# tiles, started first and still running alone (backward 3.38 -> 2.84 ms).
+# The forward takes the previous forward's costs of the same rays, and only
+# when it splits (an order alone made it slower, 1.16 -> 1.18 ms; with the
+# split 1.15 -> 1.06 ms).  At C5 (25,350 tiles) no tile exceeds the share
+# and nothing is split.  TRAIN_SPLIT_WAVES overrides the resident-wave counts
+# of both (0: no split; tests use large values to split small frames).
 TRAIN_TILE_ORDER = True
 TRAIN_SPLIT_WAVES: Optional[int] = None
 _TRAIN_SCHEDULES: dict = {}
@@ -158,8 +159,13 @@ def _train_schedule(rays, img_h: int, img_w: int, num_rays: int, device) -> Opti
     images = num_rays // (img_h * img_w)
     key = (images, img_h, img_w, _stream(device))
     return native.schedule_for(_TRAIN_SCHEDULES, key, native.num_tiles(images, img_h, img_w), device,
-                               split_waves=TRAIN_SPLIT_WAVES if TRAIN_SPLIT_WAVES is not None
-                               else int(_lib.load().vt_train_bwd_resident_waves()))
+                               split_waves=_split_waves("bwd"))
+
+
+def _split_waves(kernel: str) -> int:
+    if TRAIN_SPLIT_WAVES is not None:
+        return int(TRAIN_SPLIT_WAVES)
+    return int(getattr(_lib.load(), f"vt_train_{kernel}_resident_waves")())
 
 
 def _checked_perm(ray_perm_in: torch.Tensor, num_rays: int) -> torch.Tensor:
@@ -475,13 +481,14 @@ def trace_vorotracing_fwd(points_in, diffuse_in, specular_in, density_in, point_
     img_h, img_w, perm = _lane_order(rays, start_point, num_points, ray_perm)
     with torch.cuda.device(dev):
         sch = _train_schedule(rays, img_h, img_w, num_rays, dev) if perm is None else None
-        cost = sch.record(native.frame_key(rays_in)) if sch is not None else None
+        order, cost = (sch.launch_args(_stream(dev), native.frame_key(rays_in), split_waves=_split_waves("fwd"))
+                       if sch is not None else (None, None))
         _lib.call("vt_trace_fwd", code, points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd, rs,
                   density.data_ptr(), adjacency.data_ptr(), adjacency_size, offsets.data_ptr(), num_points,
                   rays.data_ptr(), num_rays, img_h, img_w, start_point.data_ptr(), _ptr(perm), K, _ptr(depth_quantiles),
                   float(weight_threshold), int(max_intersections), rgba.data_ptr(), _ptr(depth), _ptr(depth_idx),
                   _ptr(contribution), n.data_ptr(), distortion.data_ptr(), W_total.data_ptr(), S_total.data_ptr(),
-                  t_far.data_ptr(), workspace.data_ptr(), None, cost, _stats_ptr(stats, num_rays), _stream(dev))
+                  t_far.data_ptr(), workspace.data_ptr(), order, cost, _stats_ptr(stats, num_rays), _stream(dev))
     return rgba, depth, depth_idx, contribution, n, distortion, W_total, S_total, t_far
 
 
@@ -664,6 +671,27 @@ class NNBVH:
         with torch.cuda.device(q.device):
             _lib.call("vt_bvh_query_ws", self._h, pts.data_ptr(), pts.size(0), q.data_ptr(), nq, out.data_ptr(),
                       None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), _stream(q.device))
+        return out
+
+
+    def start_cells(self, points, rays):
+        """u32 nearest site of every ray's origin (rays (..., 6) f32), one
+        tree query per run of equal consecutive origins, counted on the GPU
+        (vt_start_cells: no wait for the device)."""
+        _assert(self._built, "BVH must be built before querying")
+        _assert(rays.device.type == "cuda" and rays.dtype == torch.float32 and rays.shape[-1] == 6,
+                "rays must be (..., 6) float32 on CUDA")
+        pts = points.detach().contiguous()
+        _assert(pts.size(0) == self._n, "points must be the point set the BVH was built on")
+        r = rays.detach().contiguous()
+        n = r.numel() // 6
+        out = torch.empty(r.shape[:-1], dtype=torch.uint32, device=r.device)
+        if n == 0:
+            return out
+        ws = torch.empty(int(_lib.load().vt_start_cells_workspace_size(n)), dtype=torch.uint8, device=r.device)
+        with torch.cuda.device(r.device):
+            _lib.call("vt_start_cells", self._h, pts.data_ptr(), pts.size(0), r.data_ptr(), n, out.data_ptr(),
+                      ws.data_ptr(), _stream(r.device))
         return out
 
 

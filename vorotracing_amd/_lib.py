@@ -62,11 +62,14 @@ SIGNATURES = {
     "vt_bvh_num_nodes": ([P], C.c_int),
     "vt_nearest_scan_workspace_size": ([U32], C.c_size_t),
     "vt_bvh_query_ws": ([P, P, U32, P, U32, P, P, C.c_size_t, P], C.c_int),
+    "vt_start_cells_workspace_size": ([U32], C.c_size_t),
+    "vt_start_cells": ([P, P, U32, P, U32, P, P, P], C.c_int),
     "vt_bvh_debug_stack_limit": ([P, U32, I32], C.c_int),
     "vt_nearest_sites_noalloc": ([P, U32, P, U32, P, P], C.c_int),
     "vt_tile_perm": ([U32, U32, U32, U32, P, P], C.c_int),
     "vt_tile_order_workspace_size": ([U32], C.c_size_t),
     "vt_tile_order": ([P, U32, U32, P, P, P], C.c_int),
+    "vt_train_fwd_resident_waves": ([], U32),
     "vt_train_bwd_resident_waves": ([], U32),
     "vt_morton_workspace_size": ([U32, U32], C.c_size_t),
     "vt_morton_reorder": ([P, U32, P, U32, P, P, P, P, P, P, P], C.c_int),

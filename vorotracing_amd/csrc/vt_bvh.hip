@@ -205,16 +205,12 @@ __device__ __forceinline__ bool box_may_hold(float bd2, float best) { return bd2
 
 constexpr int BVH_STACK = 64;
 
-__global__ __launch_bounds__(256) void bvh_query_kernel(const BvhNode *__restrict__ nodes,
-                                                        const uint32_t *__restrict__ leaf_idx, uint32_t n,
-                                                        const float *__restrict__ points,
-                                                        const float *__restrict__ queries, uint32_t nq,
-                                                        int32_t *__restrict__ out, uint32_t stack_limit)
+// Nearest site of q: the smallest squared distance, the lowest site index
+// among equal distances.
+__device__ __forceinline__ uint32_t bvh_nearest(f3 q, const BvhNode *__restrict__ nodes,
+                                                const uint32_t *__restrict__ leaf_idx, uint32_t n,
+                                                const float *__restrict__ points, uint32_t stack_limit)
 {
-    uint32_t qi = xcd_block_linear();
-    if (qi >= nq)
-        return;
-    f3 q = load_site(queries, qi);
     float best = __builtin_huge_valf();
     uint32_t best_i = NONE;
     auto visit_leaf = [&](uint32_t k) {
@@ -294,7 +290,87 @@ __global__ __launch_bounds__(256) void bvh_query_kernel(const BvhNode *__restric
             }
         }
     }
-    out[qi] = (int32_t)best_i;
+    return best_i;
+}
+
+__global__ __launch_bounds__(256) void bvh_query_kernel(const BvhNode *__restrict__ nodes,
+                                                        const uint32_t *__restrict__ leaf_idx, uint32_t n,
+                                                        const float *__restrict__ points,
+                                                        const float *__restrict__ queries, uint32_t nq,
+                                                        int32_t *__restrict__ out, uint32_t stack_limit)
+{
+    uint32_t qi = xcd_block_linear();
+    if (qi >= nq)
+        return;
+    out[qi] = (int32_t)bvh_nearest(load_site(queries, qi), nodes, leaf_idx, n, points, stack_limit);
+}
+
+// ---- start cells of a ray batch --------------------------------------------
+//
+// The nearest site of every ray's origin, one tree query per run of equal
+// consecutive origins (the rays of a camera share one origin, or one per
+// row under a rolling shutter), without the host learning the number of
+// runs: flags, a scan, the runs' origins compacted, a grid-stride query over
+// the device-side run count, and a gather.
+
+constexpr uint32_t RUN_QUERY_BLOCKS = 2048;
+
+__device__ __forceinline__ f3 ray_origin(const float *__restrict__ rays, uint32_t i)
+{
+    return mk(rays[6 * (size_t)i], rays[6 * (size_t)i + 1], rays[6 * (size_t)i + 2]);
+}
+
+// flags[i] = 1 where ray i starts a run (its origin differs from ray i-1's)
+__global__ void run_flags_kernel(const float *__restrict__ rays, uint32_t num_rays, uint32_t *__restrict__ flags)
+{
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= num_rays)
+        return;
+    bool start = i == 0;
+    if (!start) {
+        const f3 a = ray_origin(rays, i), b = ray_origin(rays, i - 1);
+        start = a.x != b.x || a.y != b.y || a.z != b.z;
+    }
+    flags[i] = start ? 1u : 0u;
+}
+
+// runs' origins packed in run order; count = the number of runs
+__global__ void run_compact_kernel(const float *__restrict__ rays, const uint32_t *__restrict__ flags,
+                                   const uint32_t *__restrict__ first, uint32_t num_rays, float *__restrict__ origins,
+                                   uint32_t *__restrict__ count)
+{
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= num_rays)
+        return;
+    if (flags[i]) {
+        const f3 o = ray_origin(rays, i);
+        origins[3 * (size_t)first[i]] = o.x;
+        origins[3 * (size_t)first[i] + 1] = o.y;
+        origins[3 * (size_t)first[i] + 2] = o.z;
+    }
+    if (i == num_rays - 1)
+        *count = first[i] + flags[i];
+}
+
+__global__ __launch_bounds__(256) void run_query_kernel(const BvhNode *__restrict__ nodes,
+                                                        const uint32_t *__restrict__ leaf_idx, uint32_t n,
+                                                        const float *__restrict__ points,
+                                                        const float *__restrict__ origins,
+                                                        const uint32_t *__restrict__ count,
+                                                        uint32_t *__restrict__ nearest, uint32_t stack_limit)
+{
+    const uint32_t runs = *count;
+    for (uint32_t j = blockIdx.x * blockDim.x + threadIdx.x; j < runs; j += gridDim.x * blockDim.x)
+        nearest[j] = bvh_nearest(load_site(origins, j), nodes, leaf_idx, n, points, stack_limit);
+}
+
+// start[i] = the nearest site of ray i's run
+__global__ void run_gather_kernel(const uint32_t *__restrict__ flags, const uint32_t *__restrict__ first,
+                                  uint32_t num_rays, const uint32_t *__restrict__ nearest, uint32_t *__restrict__ start)
+{
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < num_rays)
+        start[i] = nearest[first[i] + flags[i] - 1u];
 }
 
 // Few queries (num_queries * num_points <= NN_SCAN_PAIRS and at most
@@ -552,6 +628,50 @@ extern "C" int vt_bvh_query_ws(void *handle, const float *points, uint32_t num_p
     VT_REQUIRE(((uintptr_t)workspace & 7u) == 0, "workspace must be 8-byte aligned");
     return query_common((BvhHandle *)handle, points, num_points, queries, num_queries, out,
                         reinterpret_cast<uint2 *>(workspace), workspace_bytes / sizeof(uint2), as_stream(stream));
+}
+
+// workspace (u32 words): flags, first ray of each run (num_rays each), the
+// runs' origins (3 num_rays floats), their nearest sites (num_rays), the run
+// count, then the scan's workspace
+extern "C" size_t vt_start_cells_workspace_size(uint32_t num_rays)
+{
+    return (6 * (size_t)num_rays + 1 + scan_workspace_words(num_rays)) * 4;
+}
+
+extern "C" int vt_start_cells(void *handle, const float *points, uint32_t num_points, const float *rays,
+                              uint32_t num_rays, uint32_t *start, void *workspace, vt_stream_t stream)
+{
+    clear_error();
+    BvhHandle *h = (BvhHandle *)handle;
+    VT_REQUIRE(h, "null BVH handle");
+    VT_REQUIRE(h->n > 0, "BVH must be built before querying");
+    VT_REQUIRE(num_points == h->n, "points must be the point set the BVH was built on (%u vs %u)", num_points, h->n);
+    if (num_rays == 0)
+        return VT_OK;
+    VT_REQUIRE(points && rays && start && workspace, "null pointer argument");
+    VT_REQUIRE(((uintptr_t)workspace & 3u) == 0, "workspace must be 4-byte aligned");
+    hipStream_t s = as_stream(stream);
+    uint32_t *flags = static_cast<uint32_t *>(workspace);
+    uint32_t *first = flags + num_rays;
+    float *origins = reinterpret_cast<float *>(first + num_rays);
+    uint32_t *nearest = reinterpret_cast<uint32_t *>(origins + 3 * (size_t)num_rays);
+    uint32_t *count = nearest + num_rays;
+    uint32_t *sws = count + 1;
+    const uint32_t blocks = (num_rays + 255) / 256;
+    run_flags_kernel<<<blocks, 256, 0, s>>>(rays, num_rays, flags);
+    VT_LAUNCH_CHECK("run_flags_kernel");
+    int rc = exclusive_scan_u32(flags, first, num_rays, sws, s);
+    if (rc)
+        return rc;
+    run_compact_kernel<<<blocks, 256, 0, s>>>(rays, flags, first, num_rays, origins, count);
+    VT_LAUNCH_CHECK("run_compact_kernel");
+    run_query_kernel<<<blocks < RUN_QUERY_BLOCKS ? blocks : RUN_QUERY_BLOCKS, 256, 0, s>>>(
+        h->nodes, h->leaf_idx, h->n, points, origins, count, nearest,
+        h->stack_limit < (uint32_t)BVH_STACK ? h->stack_limit : (uint32_t)BVH_STACK);
+    VT_LAUNCH_CHECK("run_query_kernel");
+    run_gather_kernel<<<blocks, 256, 0, s>>>(flags, first, num_rays, nearest, start);
+    VT_LAUNCH_CHECK("run_gather_kernel");
+    return VT_OK;
 }
 
 // ---- allocation-free nearest-site scan -------------------------------------

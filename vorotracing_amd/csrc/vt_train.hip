@@ -92,6 +92,9 @@ template <typename A, int RD, int RS> struct TrainTex {
 // order anyway).
 
 constexpr int TRAIN_BLOCK = 64; // one wave per block: each wave's LDS is freed when it ends
+// waves per SIMD the training kernels' register budgets allow (the
+// forward spills 20 bytes at 6; the backward keeps 112 VGPRs at 4)
+constexpr uint32_t TRAIN_FWD_WAVES = 6, TRAIN_BWD_WAVES = 4;
 constexpr int TRAIN_WAVES = TRAIN_BLOCK / 64;
 constexpr int TRAIN_CHUNK = 8;      // face records read together per exit-face step (forward)
 constexpr int TRAIN_BWD_CHUNK = 12; // the same in the backward (C2: 3.93-3.98 against 4.04-4.07 ms with 8;
@@ -122,21 +125,51 @@ constexpr uint32_t TRAIN_TILE = 8;
 #endif
 constexpr uint32_t TRAIN_TILE_STRIP = VT_TRAIN_TILE_STRIP;
 
-// Tile of launch slot s in the tiled order: the tile in screen order, or
-// the one tile_order places at the slot's wave.
-__device__ __forceinline__ uint32_t train_tile(uint32_t s, const uint32_t *tile_order)
+// Slot s of a tiled training launch: the tile its wave runs (NONE past the
+// last), the lane's ray within the tile's 64 (NONE for the idle lanes of a
+// half-wave) and whether the wave runs half a tile.  With a tile order,
+// wave j runs tile tile_order[j], except that the first k tiles of the
+// order, k = tile_order[tiles] clamped to the waves the launch added for
+// them, run as two half-waves each: waves 2i and 2i + 1 take rows 0-3 and
+// rows 4-7 of tile tile_order[i] on lanes 0-31, and wave 2k + j takes tile
+// tile_order[k + j].  A long tile, which the launch would otherwise end
+// waiting for, then ends about as early as the rest.  The forward
+// (ORDER_ONLY_TO_SPLIT) keeps screen order when k is 0: an order alone made
+// it slower.
+struct TrainSlot {
+    uint32_t tile, within;
+    bool half;
+};
+
+template <bool ORDER_ONLY_TO_SPLIT>
+__device__ __forceinline__ TrainSlot train_slot(uint32_t s, uint32_t ni, uint32_t h, uint32_t w,
+                                                const uint32_t *tile_order)
 {
-    return tile_order ? tile_order[s >> 6] : s >> 6;
+    TrainSlot r{s >> 6, s & 63u, false};
+    if (!tile_order)
+        return r;
+    const uint32_t tiles = ni * ((w + TRAIN_TILE - 1) / TRAIN_TILE) * ((h + TRAIN_TILE - 1) / TRAIN_TILE);
+    const uint32_t waves = gridDim.x * (blockDim.x / 64u);
+    const uint32_t extra = waves > tiles ? waves - tiles : 0u;
+    const uint32_t k = min(min(tile_order[tiles], tiles), extra);
+    if (ORDER_ONLY_TO_SPLIT && k == 0) {
+        if (r.tile >= tiles)
+            r.tile = NONE;
+        return r;
+    }
+    uint32_t t = r.tile;
+    if (t < 2u * k) {
+        r.half = true;
+        r.within = r.within < 32u ? r.within + (t & 1u) * 32u : NONE;
+        t >>= 1;
+    } else {
+        t -= k;
+    }
+    r.tile = t < tiles ? tile_order[t] : NONE;
+    return r;
 }
 
-// Ray of launch slot s.  Tiled rays with a tile order: wave j runs tile
-// tile_order[j].  With SPLIT (the backward), the first k tiles of the order,
-// k = tile_order[tiles] clamped to the waves the launch added for them, run
-// as two half-waves each: waves 2i and 2i + 1 take rows 0-3 and rows 4-7 of
-// tile tile_order[i] on lanes 0-31 (lanes 32-63 idle), and wave 2k + j
-// takes tile tile_order[k + j].  A long tile, which the launch would
-// otherwise end waiting for, then ends about as early as the rest.
-template <bool SPLIT>
+template <bool ORDER_ONLY_TO_SPLIT>
 __device__ __forceinline__ uint32_t train_ray(uint32_t s, uint32_t num_rays, const uint32_t *perm, uint32_t ni,
                                               uint32_t h, uint32_t w, const uint32_t *tile_order)
 {
@@ -147,27 +180,10 @@ __device__ __forceinline__ uint32_t train_ray(uint32_t s, uint32_t num_rays, con
         return r < num_rays ? r : NONE;
     }
     if (ni) {
-        uint32_t t = s >> 6, within = s & 63u;
-        if (tile_order) {
-            const uint32_t tiles = ni * ((w + TRAIN_TILE - 1) / TRAIN_TILE) * ((h + TRAIN_TILE - 1) / TRAIN_TILE);
-            if (SPLIT) {
-                const uint32_t waves = gridDim.x * (blockDim.x / 64u);
-                const uint32_t extra = waves > tiles ? waves - tiles : 0u;
-                const uint32_t k = min(min(tile_order[tiles], tiles), extra);
-                if (t < 2u * k) {
-                    if (within >= 32u)
-                        return NONE;
-                    within += (t & 1u) * 32u;
-                    t >>= 1;
-                } else {
-                    t -= k;
-                }
-            }
-            if (t >= tiles)
-                return NONE;
-            t = tile_order[t];
-        }
-        return tiled_ray<TRAIN_TILE_STRIP>(t * 64u + within, ni, h, w, TRAIN_TILE, TRAIN_TILE);
+        const TrainSlot t = train_slot<ORDER_ONLY_TO_SPLIT>(s, ni, h, w, tile_order);
+        if (t.tile == NONE || t.within == NONE)
+            return NONE;
+        return tiled_ray<TRAIN_TILE_STRIP>(t.tile * 64u + t.within, ni, h, w, TRAIN_TILE, TRAIN_TILE);
     }
     return s < num_rays ? s : NONE;
 }
@@ -346,18 +362,29 @@ __device__ __forceinline__ uint32_t fwd_ray(const FwdArgs &a, uint32_t r, uint32
 }
 
 template <typename A, int RD, int RS, bool STATS>
-__global__ __launch_bounds__(TRAIN_BLOCK) __attribute__((amdgpu_waves_per_eu(6))) void fwd_kernel(FwdArgs a)
+__global__ __launch_bounds__(TRAIN_BLOCK) __attribute__((amdgpu_waves_per_eu(TRAIN_FWD_WAVES)))
+void fwd_kernel(FwdArgs a)
 {
     const uint32_t s = xcd_interleaved_block<TRAIN_XCD_CHUNK>() * blockDim.x + threadIdx.x;
-    const uint32_t r = train_ray<false>(s, a.num_rays, a.ray_perm, a.num_images, a.img_h, a.img_w, a.tile_order);
+    const uint32_t r = train_ray<true>(s, a.num_rays, a.ray_perm, a.num_images, a.img_h, a.img_w, a.tile_order);
     uint32_t n = 0, faces = 0;
     if (r != NONE)
         n = fwd_ray<A, RD, RS, STATS>(a, r, faces);
     if (a.tile_cost && a.num_images) {
-        // tiled launches are whole waves, and every lane is here
+        // tiled launches are whole waves, and every lane is here; a split
+        // tile records the larger of its halves' costs (the slower half is
+        // what bounds it), in an atomic max (the caller cleared the costs
+        // before an ordered launch)
         const uint32_t nmax = wave_max_u32(n), fmax = wave_max_u32(faces);
-        if ((threadIdx.x & 63u) == 0)
-            a.tile_cost[train_tile(s, a.tile_order)] = tile_cost_of(nmax, fmax);
+        if ((threadIdx.x & 63u) == 0) {
+            const TrainSlot t = train_slot<true>(s, a.num_images, a.img_h, a.img_w, a.tile_order);
+            if (t.tile != NONE) {
+                if (t.half)
+                    atomicMax(a.tile_cost + t.tile, tile_cost_of(nmax, fmax));
+                else
+                    a.tile_cost[t.tile] = tile_cost_of(nmax, fmax);
+            }
+        }
     }
 }
 
@@ -788,15 +815,16 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
 };
 
 template <typename A, int RD, int RS, bool STATS>
-__global__ __launch_bounds__(TRAIN_BLOCK) __attribute__((amdgpu_waves_per_eu(4))) void bwd_kernel(BwdArgs a)
+__global__ __launch_bounds__(TRAIN_BLOCK) __attribute__((amdgpu_waves_per_eu(TRAIN_BWD_WAVES)))
+void bwd_kernel(BwdArgs a)
 {
     __shared__ __align__(16) float rows_lds[TRAIN_WAVES][ROW_TABLE_FLOATS];
     float *rows = rows_lds[threadIdx.x / 64];
     if ((threadIdx.x & 63u) < (uint32_t)ROW_STRIDE)
         rows[64 * ROW_STRIDE + (threadIdx.x & 63u)] = 0.0f; // the zero row
     wave_lds_sync();
-    uint32_t r = train_ray<true>(xcd_interleaved_block<TRAIN_XCD_CHUNK>() * blockDim.x + threadIdx.x, a.num_rays,
-                                 a.ray_perm, a.num_images, a.img_h, a.img_w, a.tile_order);
+    uint32_t r = train_ray<false>(xcd_interleaved_block<TRAIN_XCD_CHUNK>() * blockDim.x + threadIdx.x, a.num_rays,
+                                  a.ray_perm, a.num_images, a.img_h, a.img_w, a.tile_order);
     if (r == NONE)
         return;
     BwdIntegrator<A, RD, RS> it;
@@ -880,25 +908,25 @@ static void set_lane_order(Args &a, uint32_t num_rays, const uint32_t *ray_perm,
     }
 }
 
-template <typename A, int RD, int RS, bool ST> struct FwdK {
-    static constexpr auto fn = fwd_kernel<A, RD, RS, ST>;
-    static constexpr bool split = false;
-};
-template <typename A, int RD, int RS, bool ST> struct BwdK {
-    static constexpr auto fn = bwd_kernel<A, RD, RS, ST>;
-    static constexpr bool split = true;
-};
-
-// Waves of the training backward resident at once on the current device: 4
-// per SIMD (its register budget, amdgpu_waves_per_eu(4)), 4 SIMDs per CU.
-static uint32_t bwd_resident_waves()
+// Waves of a training kernel resident at once on the current device:
+// waves_per_simd (its register budget, amdgpu_waves_per_eu) x 4 SIMDs per CU.
+static uint32_t resident_waves(uint32_t waves_per_simd)
 {
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
         return 0;
-    return (uint32_t)cus * 16u;
+    return (uint32_t)cus * 4u * waves_per_simd;
 }
+
+template <typename A, int RD, int RS, bool ST> struct FwdK {
+    static constexpr auto fn = fwd_kernel<A, RD, RS, ST>;
+    static uint32_t resident() { return resident_waves(TRAIN_FWD_WAVES); }
+};
+template <typename A, int RD, int RS, bool ST> struct BwdK {
+    static constexpr auto fn = bwd_kernel<A, RD, RS, ST>;
+    static uint32_t resident() { return resident_waves(TRAIN_BWD_WAVES); }
+};
 
 template <template <typename, int, int, bool> class K, typename Args, typename A, int RD, int RS>
 static int launch_train_rs(const Args &a, bool stats, hipStream_t s)
@@ -911,8 +939,8 @@ static int launch_train_rs(const Args &a, bool stats, hipStream_t s)
         // the waves that run split tiles' second halves (at most one per
         // resident wave: the split count stays below 1.25x that; see
         // vt_tile_order)
-        if (K<A, RD, RS, false>::split && a.tile_order)
-            slots += std::min<uint64_t>(tiles, bwd_resident_waves()) * 64;
+        if (a.tile_order)
+            slots += std::min<uint64_t>(tiles, K<A, RD, RS, false>::resident()) * 64;
     }
     dim3 grid((uint32_t)((slots + TRAIN_BLOCK - 1) / TRAIN_BLOCK)), block(TRAIN_BLOCK);
     if (stats)
@@ -1127,9 +1155,14 @@ __global__ void f16_atomic_probe_kernel(uint16_t *halves, uint32_t num_halves, c
 
 } // namespace vt
 
+extern "C" uint32_t vt_train_fwd_resident_waves(void)
+{
+    return vt::resident_waves(vt::TRAIN_FWD_WAVES);
+}
+
 extern "C" uint32_t vt_train_bwd_resident_waves(void)
 {
-    return vt::bwd_resident_waves();
+    return vt::resident_waves(vt::TRAIN_BWD_WAVES);
 }
 
 extern "C" int vt_debug_f16_atomic_add(uint16_t *halves, uint32_t num_halves, const uint32_t *index,

@@ -194,25 +194,10 @@ class VoroTracing(nn.Module):
     def get_starting_point(self, rays: torch.Tensor) -> torch.Tensor:
         """u32 start cell of every ray: the nearest site of its origin
         (vorotracing.py:323-344), one LBVH query per run of equal consecutive
-        origins.  Rays of an image share one origin, or one per row under a
-        rolling shutter, so the runs are the distinct origins without sorting
-        them; any order of rays gives the same cells."""
-        lead = rays.shape[:-1]
-        o = rays[..., :3].reshape(-1, 3)
-        if o.shape[0] == 0:
-            return torch.empty(lead, dtype=torch.uint32, device=rays.device)
-        new = torch.ones(o.shape[0], dtype=torch.bool, device=o.device)
-        new[1:] = (o[1:] != o[:-1]).any(dim=1)
-        run = torch.cumsum(new, 0) - 1
-        runs = int(run[-1].item()) + 1
-        if runs > 1024 and 4 * runs > o.shape[0]:
-            # a shuffled batch of a few cameras (random pixels of random
-            # images): runs are about as many as rays, the distinct origins
-            # few, so query each distinct origin once
-            uniq, inverse = torch.unique(o, dim=0, return_inverse=True)
-            return self.bvh.query(self.primal_points, uniq.contiguous())[inverse].reshape(lead).view(torch.uint32)
-        nearest = self.bvh.query(self.primal_points, o[new].contiguous())
-        return nearest[run].reshape(lead).view(torch.uint32)
+        origins, counted on the GPU (NNBVH.start_cells: the call does not wait
+        for the device).  Rays of an image share one origin, or one per row
+        under a rolling shutter; any order of rays gives the same cells."""
+        return self.bvh.start_cells(self.primal_points, rays)
 
     def start_cells(self, rays: torch.Tensor, start_point: Optional[torch.Tensor] = None) -> torch.Tensor:
         """``start_point`` broadcast over the ray batch, or the nearest sites."""

@@ -121,8 +121,8 @@ class TileSchedule:
 
     def __init__(self, tiles: int, device, split_waves: int = 0):
         self.tiles = int(tiles)
-        # waves the consuming launch holds at once (vt_tile_order's split
-        # count; 0: the inference entries, which ignore it)
+        # waves the training backward holds at once (the split count of the
+        # orders order_for makes; 0: none)
         self.split_waves = int(split_waves)
         self.cost = torch.zeros(self.tiles, dtype=torch.uint32, device=device)
         # the order, then the split count
@@ -131,25 +131,25 @@ class TileSchedule:
                               device=device)
         self.frame = None  # the frame whose costs self.cost holds
 
-    def _sort(self, stream: int):
-        _lib.call("vt_tile_order", self.cost.data_ptr(), self.tiles, self.split_waves, self.order.data_ptr(),
+    def _sort(self, stream: int, split_waves: int):
+        _lib.call("vt_tile_order", self.cost.data_ptr(), self.tiles, split_waves, self.order.data_ptr(),
                   self.ws.data_ptr(), stream)
         return self.order.data_ptr()
 
-    def launch_args(self, stream: int, frame):
+    def launch_args(self, stream: int, frame, split_waves: int = 0):
         """(tile_order, tile_cost) pointers for the next launch on ``stream``
-        of ``frame`` (a hashable identity of the launch's rays or cameras)."""
+        of ``frame`` (a hashable identity of the launch's rays or cameras).
+        ``split_waves``: 0 for the inference entries; the waves the training
+        forward holds at once for it, which may then split its costliest
+        tiles and record their costs with an atomic max, into costs cleared
+        here after the sort has read them."""
         order = None
         if frame is not None and frame == self.frame:
-            order = self._sort(stream)
+            order = self._sort(stream, split_waves)
+            if split_waves:
+                self.cost.zero_()
         self.frame = frame
         return order, self.cost.data_ptr()
-
-    def record(self, frame):
-        """tile_cost pointer for a launch of ``frame`` in screen order that
-        records its tiles' costs (the training forward)."""
-        self.frame = frame
-        return self.cost.data_ptr()
 
     def order_for(self, stream: int, frame):
         """Launch order from the costs the last launch of ``frame`` recorded
@@ -157,7 +157,7 @@ class TileSchedule:
         None when the costs are of another frame."""
         if frame is None or frame != self.frame:
             return None
-        return self._sort(stream)
+        return self._sort(stream, self.split_waves)
 
 
 def frame_key(t: torch.Tensor):
