@@ -743,7 +743,7 @@ def train_c2(dev, log, cpu=False, random_batch=True):
                        "textures, one 800x600 pinhole camera, upstream dL/dRGB ~ N(0,1), thr 0.001"}
     out["roofline_fwd"], out["roofline_bwd"] = train_rooflines(model, rays, sp, g, dev, log)
     if random_batch:  # left out of --train-only: its traces average the default (ordered) backward
-        out["backward_tile_order"] = train_tile_order(model, rays, sp, g, dev, log)
+        out["tile_order"] = train_tile_order(model, rays, sp, g, dev, log)
     out["f16_storage"] = train_f16_storage(model, rays, sp, g, dev, log)
     if random_batch:  # left out of --train-only, whose traces average the C2 kernels
         out["random_batch"] = train_random_batch(model, dev, log)
@@ -784,27 +784,40 @@ def _entry_times(scn, rays, sp, g, dev, R=10):
 
 
 def train_tile_order(model, rays, sp, g, dev, log):
-    """The C2 backward entry with its tiles in screen order and in the order of
-    the forward's tile costs (the default: _C.TRAIN_TILE_ORDER)."""
+    """The C2 forward and backward entries with their tiles in screen order,
+    in the order of the recorded tile costs without splitting, and in that
+    order with the costliest tiles run as two half-waves (the default:
+    _C.TRAIN_TILE_ORDER, split counts over the resident waves)."""
     from vorotracing_amd import _C
 
     dens = model.activated_density().detach()
     scn = (model.primal_points.detach(), model.att_diffuse.detach(), model.att_specular.detach(), dens,
            model.point_adjacency, model.point_adjacency_offsets)
     out = {}
-    saved = _C.TRAIN_TILE_ORDER
+    saved = (_C.TRAIN_TILE_ORDER, _C.TRAIN_SPLIT_WAVES)
     try:
-        for name, flag in (("screen_order", False), ("forward_cost_order", True)):
-            _C.TRAIN_TILE_ORDER = flag
+        for name, flag, split in (("screen_order", False, None), ("cost_order", True, 0),
+                                  ("cost_order_split", True, None)):
+            _C.TRAIN_TILE_ORDER, _C.TRAIN_SPLIT_WAVES = flag, split
             _C._TRAIN_SCHEDULES.clear()
             t_fwd, t_bwd = _entry_times(scn, rays, sp, g, dev)
             out[name] = {"forward_ms": t_fwd, "backward_ms": t_bwd}
+            if flag:
+                sch = next(iter(_C._TRAIN_SCHEDULES.values()))
+                out[name]["tiles"] = sch.tiles
+                out[name]["backward_split_tiles"] = int(sch.order[sch.tiles].item())  # the last sort: the backward's
     finally:
-        _C.TRAIN_TILE_ORDER = saved
-    out["note"] = ("_C entries, prefetch included; the backward of a forward over the same rays launches its tiles "
-                   "by the forward's per-tile costs (vt_tile_order) instead of screen order")
-    log(f"C2 backward entry: screen order {out['screen_order']['backward_ms']:.3f} ms, forward-cost order "
-        f"{out['forward_cost_order']['backward_ms']:.3f} ms")
+        _C.TRAIN_TILE_ORDER, _C.TRAIN_SPLIT_WAVES = saved
+        _C._TRAIN_SCHEDULES.clear()
+    out["note"] = ("_C entries, prefetch included, the same rays every call. cost_order: the backward launches its "
+                   "tiles by the forward's per-tile costs (vt_tile_order), the forward keeps screen order. "
+                   "cost_order_split: both passes also run the tiles above 4/5 of one resident wave's mean share as "
+                   "two half-waves (the forward by the previous forward's costs)")
+    log(f"C2 entries: screen order fwd {out['screen_order']['forward_ms']:.3f} / bwd "
+        f"{out['screen_order']['backward_ms']:.3f} ms; cost order bwd {out['cost_order']['backward_ms']:.3f} ms; "
+        f"with split tiles fwd {out['cost_order_split']['forward_ms']:.3f} / bwd "
+        f"{out['cost_order_split']['backward_ms']:.3f} ms ({out['cost_order_split']['backward_split_tiles']} of "
+        f"{out['cost_order_split']['tiles']} tiles split in the backward)")
     return out
 
 
