@@ -414,7 +414,7 @@ int vt_tile_perm(uint32_t height, uint32_t width, uint32_t tile_h, uint32_t tile
  * vt_train_bwd_resident_waves()), and so does the forward when the count is
  * non-zero (pass vt_train_fwd_resident_waves()); the inference entries
  * ignore the count (pass 0).
- * workspace: vt_tile_order_workspace_size(tiles) bytes, 4-byte aligned.
+ * workspace: vt_tile_order_workspace_size(tiles) bytes, 8-byte aligned.
  */
 size_t vt_tile_order_workspace_size(uint32_t tiles);
 int vt_tile_order(const uint32_t *tile_cost, uint32_t tiles, uint32_t split_waves, uint32_t *tile_order,

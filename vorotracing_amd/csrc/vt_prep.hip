@@ -415,34 +415,27 @@ __host__ __device__ constexpr uint32_t tile_order_key(uint32_t cost)
                           ((1u << TILE_ORDER_FRAC) - 1u);
     return TILE_ORDER_TOP - ((lb << TILE_ORDER_FRAC) | frac);
 }
-static_assert(TILE_ORDER_TOP < 256, "the tile order sorts on one 8-bit digit");
+static_assert(TILE_ORDER_TOP < 128, "keys fit 7 bits: the scatter ranks them by 7 ballots");
 static_assert(tile_order_key(1) == TILE_ORDER_TOP && tile_order_key(0) == TILE_ORDER_TOP, "");
 static_assert(tile_order_key(0xffffffffu) == 0, "");
 static_assert(tile_order_key(7) < tile_order_key(6) && tile_order_key(6) < tile_order_key(5), "");
 static_assert(tile_order_key(1000) == tile_order_key(1023) && tile_order_key(1023) > tile_order_key(1024), "");
 
-__global__ void tile_order_keys_kernel(const uint32_t *__restrict__ cost, uint32_t tiles, uint32_t *__restrict__ keys,
-                                       uint32_t *__restrict__ ids)
-{
-    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= tiles)
-        return;
-    keys[t] = tile_order_key(cost[t]);
-    ids[t] = t;
-}
-
-// A tile is split when its cost exceeds SPLIT_NUM / SPLIT_DEN of the mean
-// load of one resident wave (total cost / split_waves): such a tile, started
-// first, still runs when the launch's other work has drained, and the
-// launch ends with it.  Tiles below that are covered by the other waves.
-constexpr uint64_t SPLIT_NUM = 4, SPLIT_DEN = 5;
-constexpr uint32_t SPLIT_THREADS = 1024;
+// The order is a stable counting sort of the keys (TILE_ORDER_TOP + 1 bins)
+// in three launches: per-block key histograms and cost sums; one block that
+// scans the histograms bin-major (each block's first position per key) and
+// totals the costs; and a stable scatter, in which each block also counts
+// its tiles above the split share into tile_order[tiles].
+constexpr uint32_t TO_BLOCK = 256; // tiles per block
+constexpr uint32_t TO_BINS = TILE_ORDER_TOP + 1;
+constexpr uint32_t TO_SCAN_THREADS = 1024;
+static_assert(TO_BINS <= TO_BLOCK, "one thread per bin");
 
 __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, uint64_t *red)
 {
     red[threadIdx.x] = v;
     __syncthreads();
-    for (uint32_t h = SPLIT_THREADS / 2; h > 0; h >>= 1) {
+    for (uint32_t h = blockDim.x / 2; h > 0; h >>= 1) {
         if (threadIdx.x < h)
             red[threadIdx.x] += red[threadIdx.x + h];
         __syncthreads();
@@ -452,32 +445,138 @@ __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, uint64_t *red)
     return total;
 }
 
-// out = the number of tiles to split (one block; tiles are few)
-__global__ __launch_bounds__(SPLIT_THREADS) void tile_split_kernel(const uint32_t *__restrict__ cost, uint32_t tiles,
-                                                                   uint32_t split_waves, uint32_t *__restrict__ out)
+// hist[bin * blocks + block] = tiles of the block with that key; psum[block]
+// = the block's cost sum
+__global__ __launch_bounds__(TO_BLOCK) void tile_hist_kernel(const uint32_t *__restrict__ cost, uint32_t tiles,
+                                                             uint32_t *__restrict__ hist, uint64_t *__restrict__ psum)
 {
-    __shared__ uint64_t red[SPLIT_THREADS];
+    __shared__ uint32_t h[TO_BINS];
+    __shared__ uint64_t red[TO_BLOCK];
+    if (threadIdx.x < TO_BINS)
+        h[threadIdx.x] = 0;
+    __syncthreads();
+    const uint32_t t = blockIdx.x * TO_BLOCK + threadIdx.x;
+    const uint32_t c = t < tiles ? cost[t] : 0u;
+    if (t < tiles)
+        atomicAdd(&h[tile_order_key(c)], 1u);
+    const uint64_t sum = block_sum_u64(c, red);
+    if (threadIdx.x < TO_BINS)
+        hist[threadIdx.x * gridDim.x + blockIdx.x] = h[threadIdx.x];
+    if (threadIdx.x == 0)
+        psum[blockIdx.x] = sum;
+}
+
+// One block: hist scanned in place (exclusive, bin-major), *total = the sum
+// of psum, *split = 0
+__global__ __launch_bounds__(TO_SCAN_THREADS) void tile_scan_kernel(uint32_t *__restrict__ hist, uint32_t n,
+                                                                    const uint64_t *__restrict__ psum, uint32_t blocks,
+                                                                    uint64_t *__restrict__ total,
+                                                                    uint32_t *__restrict__ split)
+{
+    __shared__ uint32_t wsum[TO_SCAN_THREADS / 64];
+    __shared__ uint64_t red[TO_SCAN_THREADS];
+    const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+    uint32_t carry = 0;
+    for (uint32_t base = 0; base < n; base += TO_SCAN_THREADS) {
+        const uint32_t i = base + threadIdx.x;
+        const uint32_t v = i < n ? hist[i] : 0u;
+        uint32_t x = v; // inclusive scan within the wave
+#pragma unroll
+        for (uint32_t o = 1; o < 64; o <<= 1) {
+            const uint32_t y = __shfl_up(x, o, 64);
+            if (lane >= o)
+                x += y;
+        }
+        if (lane == 63)
+            wsum[w] = x;
+        __syncthreads();
+        uint32_t before = carry;
+        for (uint32_t j = 0; j < w; ++j)
+            before += wsum[j];
+        uint32_t chunk = 0;
+        for (uint32_t j = 0; j < TO_SCAN_THREADS / 64; ++j)
+            chunk += wsum[j];
+        if (i < n)
+            hist[i] = before + x - v;
+        carry += chunk;
+        __syncthreads();
+    }
     uint64_t sum = 0;
-    for (uint32_t t = threadIdx.x; t < tiles; t += SPLIT_THREADS)
-        sum += cost[t];
-    const uint64_t total = block_sum_u64(sum, red);
+    for (uint32_t b = threadIdx.x; b < blocks; b += TO_SCAN_THREADS)
+        sum += psum[b];
+    sum = block_sum_u64(sum, red);
+    if (threadIdx.x == 0) {
+        *total = sum;
+        *split = 0u;
+    }
+}
+
+// Stable scatter: tile t to its key's next position, tiles of a block in
+// order (lanes, then waves, through 7 key-bit ballots and per-wave counts).
+// A tile is split when its cost exceeds SPLIT_NUM / SPLIT_DEN of the mean
+// load of one resident wave (total cost / split_waves): such a tile, started
+// first, still runs when the launch's other work has drained, and the
+// launch ends with it.  Tiles below that are covered by the other waves.
+constexpr uint64_t SPLIT_NUM = 4, SPLIT_DEN = 5;
+
+__global__ __launch_bounds__(TO_BLOCK) void tile_scatter_kernel(const uint32_t *__restrict__ cost, uint32_t tiles,
+                                                                const uint32_t *__restrict__ hist,
+                                                                const uint64_t *__restrict__ total,
+                                                                uint32_t split_waves, uint32_t *__restrict__ order)
+{
+    __shared__ uint32_t base[TO_BINS];
+    __shared__ uint32_t wcnt[TO_BLOCK / 64][TO_BINS];
+    __shared__ uint32_t nsplit;
+    if (threadIdx.x < TO_BINS) {
+        base[threadIdx.x] = hist[threadIdx.x * gridDim.x + blockIdx.x];
+#pragma unroll
+        for (uint32_t j = 0; j < TO_BLOCK / 64; ++j)
+            wcnt[j][threadIdx.x] = 0;
+    }
+    if (threadIdx.x == 0)
+        nsplit = 0;
+    __syncthreads();
+    const uint32_t t = blockIdx.x * TO_BLOCK + threadIdx.x;
+    const bool valid = t < tiles;
+    const uint32_t c = valid ? cost[t] : 0u;
+    const uint32_t key = tile_order_key(c);
+    const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+    uint64_t m = __ballot(valid);
+#pragma unroll
+    for (uint32_t b = 0; b < 7; ++b) {
+        const bool bit = (key >> b) & 1u;
+        const uint64_t bb = __ballot(bit);
+        m &= bit ? bb : ~bb;
+    }
+    const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
+    const uint32_t rank = (uint32_t)__popcll(m & lt);
+    if (valid && rank == 0)
+        wcnt[w][key] = (uint32_t)__popcll(m);
     // (the left side stays below 2^59: cost < 2^32, split_waves < 2^24; a
     // total of 2^57 or more splits nothing and would overflow on the right)
-    uint64_t n = 0;
-    if (total < (1ull << 57))
-        for (uint32_t t = threadIdx.x; t < tiles; t += SPLIT_THREADS)
-            n += SPLIT_DEN * (uint64_t)cost[t] * split_waves > SPLIT_NUM * total;
-    const uint64_t k = block_sum_u64(n, red);
-    if (threadIdx.x == 0)
-        *out = split_waves ? (uint32_t)k : 0u;
+    const uint64_t tot = *total;
+    if (valid && split_waves && tot < (1ull << 57) && SPLIT_DEN * (uint64_t)c * split_waves > SPLIT_NUM * tot)
+        atomicAdd(&nsplit, 1u);
+    __syncthreads();
+    if (valid) {
+        uint32_t pos = base[key] + rank;
+        for (uint32_t j = 0; j < w; ++j)
+            pos += wcnt[j][key];
+        order[pos] = t;
+    }
+    if (threadIdx.x == 0 && nsplit)
+        atomicAdd(order + tiles, nsplit);
 }
 
 } // namespace vt
 
-// workspace: keys, tile ids, sorted keys (tiles words each), then one radix pass
+static uint32_t tile_order_blocks(uint32_t tiles) { return (tiles + TO_BLOCK - 1) / TO_BLOCK; }
+
+// workspace: hist (TO_BINS words per block), psum (one u64 per block), total (u64)
 extern "C" size_t vt_tile_order_workspace_size(uint32_t tiles)
 {
-    return (3 * (size_t)tiles + radix_pass_workspace_words(tiles)) * 4;
+    const size_t blocks = tile_order_blocks(tiles);
+    return (blocks * TO_BINS * 4 + 7) / 8 * 8 + (blocks + 1) * 8;
 }
 
 extern "C" int vt_tile_order(const uint32_t *tile_cost, uint32_t tiles, uint32_t split_waves, uint32_t *tile_order,
@@ -487,19 +586,20 @@ extern "C" int vt_tile_order(const uint32_t *tile_cost, uint32_t tiles, uint32_t
     if (tiles == 0)
         return VT_OK;
     VT_REQUIRE(tile_cost && tile_order && workspace, "null pointer argument");
-    VT_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 4 == 0, "workspace must be 4-byte aligned");
+    VT_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 8 == 0, "workspace must be 8-byte aligned");
     VT_REQUIRE(split_waves < (1u << 24), "split_waves (%u) must be below 2^24", split_waves);
     hipStream_t s = as_stream(stream);
-    uint32_t *keys = static_cast<uint32_t *>(workspace);
-    uint32_t *ids = keys + tiles;
-    uint32_t *sorted_keys = ids + tiles;
-    tile_order_keys_kernel<<<(tiles + 255) / 256, 256, 0, s>>>(tile_cost, tiles, keys, ids);
-    VT_LAUNCH_CHECK("tile_order_keys_kernel");
-    int rc = radix_sort_pass(keys, ids, sorted_keys, tile_order, tiles, 0, sorted_keys + tiles, s);
-    if (rc)
-        return rc;
-    tile_split_kernel<<<1, SPLIT_THREADS, 0, s>>>(tile_cost, tiles, split_waves, tile_order + tiles);
-    VT_LAUNCH_CHECK("tile_split_kernel");
+    const uint32_t blocks = tile_order_blocks(tiles);
+    uint32_t *hist = static_cast<uint32_t *>(workspace);
+    uint64_t *psum = reinterpret_cast<uint64_t *>(static_cast<char *>(workspace) +
+                                                  ((size_t)blocks * TO_BINS * 4 + 7) / 8 * 8);
+    uint64_t *total = psum + blocks;
+    tile_hist_kernel<<<blocks, TO_BLOCK, 0, s>>>(tile_cost, tiles, hist, psum);
+    VT_LAUNCH_CHECK("tile_hist_kernel");
+    tile_scan_kernel<<<1, TO_SCAN_THREADS, 0, s>>>(hist, blocks * TO_BINS, psum, blocks, total, tile_order + tiles);
+    VT_LAUNCH_CHECK("tile_scan_kernel");
+    tile_scatter_kernel<<<blocks, TO_BLOCK, 0, s>>>(tile_cost, tiles, hist, total, split_waves, tile_order);
+    VT_LAUNCH_CHECK("tile_scatter_kernel");
     return VT_OK;
 }
 
