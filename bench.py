@@ -85,18 +85,22 @@ def train_bytes(st, fwd=True, attr_bytes=4):
 
 
 def roofline_record(kernel_ms, logical_bytes, profile_name, kernel_key=None):
-    """Roofline of a traversal kernel against MI355X's 8 TB/s HBM: achieved =
-    the kernel's memory traffic per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE,
-    each scaled by what it reads for a 1 GiB copy; profiles/<profile_name>)
-    over its mean duration measured here.  The logical bytes (every record as
-    the walk reads it) are reported beside it: L2 and the MALL serve most of
-    them, so their rate is no fraction of the DRAM peak.  When the profile
-    holds the kernel's VALU instruction count, its issue rate is reported
-    against MI355X's VALU issue peak."""
+    """Roofline of a traversal kernel against MI355X's 8 TB/s HBM, as the
+    measurement contract defines it: achieved = the algorithmic bytes of one
+    launch (every reference-layout record the walks read and write, summed
+    from the kernel's own walk counters) over the kernel's mean duration
+    measured here, frac = achieved / peak.  L2 and the MALL serve repeated
+    cell reads, so frac can exceed 1.  Beside it, the physical DRAM rate:
+    traffic = the kernel's memory traffic per launch (rocprofv3 FETCH_SIZE +
+    WRITE_SIZE, each scaled by what it reads for a 1 GiB copy;
+    profiles/<profile_name>) over the same duration, and, when the profile
+    holds the kernel's VALU instruction count, its issue rate against
+    MI355X's VALU issue peak."""
     sec = kernel_ms * 1e-3
-    rec = {"bound": "hbm", "achieved": None, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": None, "traffic": None,
-           "kernel_ms": round(kernel_ms, 4), "logical_bytes_per_launch": int(logical_bytes),
-           "logical_gbs": round(logical_bytes / sec / 1e9, 1)}
+    alg = logical_bytes / sec / 1e9
+    rec = {"bound": "hbm", "achieved": round(alg, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+           "frac": round(alg / HBM_PEAK_GBS, 4), "traffic": None, "kernel_ms": round(kernel_ms, 4),
+           "algorithmic_bytes_per_launch": int(logical_bytes)}
     path = os.path.join(ROOT, "profiles", profile_name)
     if not os.path.exists(path):
         return rec
@@ -106,8 +110,8 @@ def roofline_record(kernel_ms, logical_bytes, profile_name, kernel_key=None):
         tr = tr[kernel_key]
     traffic = int(tr["hbm_bytes_per_launch"])
     rec["traffic"] = traffic
-    rec["achieved"] = round(traffic / sec / 1e9, 1)
-    rec["frac"] = round(traffic / sec / 1e9 / HBM_PEAK_GBS, 4)
+    rec["hbm_gbs"] = round(traffic / sec / 1e9, 1)
+    rec["hbm_frac"] = round(traffic / sec / 1e9 / HBM_PEAK_GBS, 4)
     rec["traffic_source"] = f"profiles/{profile_name} (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)"
     if "valu_insts_per_launch" in tr:
         rate = tr["valu_insts_per_launch"] / sec
@@ -353,8 +357,9 @@ def main():
         }
         result["dropin_c"] = dropin_c(inf, poses[0], kw, dev, log)
         r = result["roofline"]
-        log(f"HBM {r['achieved']:.0f} GB/s ({r['frac']:.1%} of peak); logical bytes {bytes_per_frame / 1e9:.2f} "
-            f"GB/frame; VALU issue {r.get('valu', {}).get('frac', float('nan')):.1%}")
+        log(f"algorithmic bytes {bytes_per_frame / 1e9:.2f} GB/frame: {r['achieved']:.0f} GB/s ({r['frac']:.2f} of the "
+            f"HBM peak); HBM traffic {r.get('hbm_gbs', float('nan')):.0f} GB/s ({r.get('hbm_frac', float('nan')):.1%}); "
+            f"VALU issue {r.get('valu', {}).get('frac', float('nan')):.1%}")
         result["c4_q8"] = c4_q8(model, poses, dev, log, thr, skip, cpu=not args.no_cpu)
         result["c3_camera"] = c3_camera(inf, W, H, args.poses, kw, dev, log)
 
@@ -905,8 +910,8 @@ def train_rooflines(model, rays, sp, g, dev, log, R=10):
     rb = roofline_record(t_bwd, train_bytes(st_b, False), "traffic_train_c2.json", "bwd_kernel")
     for r in (rf, rb):
         r["timing"] = "HIP events around the _C entry minus the face-offset prefetch timed alone"
-    log(f"C2 fwd_kernel {t_fwd:.3f} ms, bwd_kernel {t_bwd:.3f} ms (prefetch {t_pre:.3f} ms); HBM fractions "
-        f"{rf['frac']}, {rb['frac']}")
+    log(f"C2 fwd_kernel {t_fwd:.3f} ms, bwd_kernel {t_bwd:.3f} ms (prefetch {t_pre:.3f} ms); algorithmic fractions "
+        f"{rf['frac']}, {rb['frac']}; HBM fractions {rf.get('hbm_frac')}, {rb.get('hbm_frac')}")
     return rf, rb
 
 
