@@ -50,6 +50,17 @@ template <> struct Attr<uint16_t> {
         const half2_t val = (addr & 2) ? half2_t{z, h} : half2_t{h, z};
         (void)__builtin_amdgcn_global_atomic_fadd_v2f16(pair, val);
     }
+    // Both halves of the 32-bit word at p + i (p + i 4-byte aligned): lo to
+    // the half at p + i, hi to the one after it, in one packed add, each
+    // half rounded once as by two separate adds.
+    __device__ __forceinline__ static void add_pair(uint16_t *p, size_t i, float lo, float hi)
+    {
+        typedef _Float16 __attribute__((ext_vector_type(2))) half2_t;
+        typedef __attribute__((address_space(1))) half2_t global_half2_t;
+        global_half2_t *pair = reinterpret_cast<global_half2_t *>(reinterpret_cast<uintptr_t>(p + i));
+        const half2_t val = {__builtin_bit_cast(_Float16, f2h(lo)), __builtin_bit_cast(_Float16, f2h(hi))};
+        (void)__builtin_amdgcn_global_atomic_fadd_v2f16(pair, val);
+    }
 };
 
 template <typename A, int RD, int RS> struct TrainTex {
@@ -538,6 +549,56 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
         }
     }
 
+    // The sends of one combining pass.  Every lane of the pass calls it
+    // (a converged region), and a lane's column is the next one after the
+    // column of the lane below it in the pass.  f32: one atomic per lane.
+    // f16 attributes: the two halves of a 32-bit word usually belong to a
+    // column and the next one (a tap's channels, or one tap's last channel
+    // and the next tap's first); the lane of the first then adds both in one
+    // packed atomic and the next lane skips, and every other lane adds its
+    // half alone, all in one instruction (lanes that add to one word in one
+    // instruction serialise; here no two do unless a wrapped tap repeats a
+    // texel).  Each value is still added exactly once.
+    __device__ __forceinline__ void column_send_pass(const Column &c, uint32_t cell, uint32_t tap, float x,
+                                                     uint32_t lane)
+    {
+        const bool send = x != 0.0f && c.on && tap < c.taps;
+        const size_t i = (size_t)cell * c.stride + 3u * tap + c.off;
+        if constexpr (std::is_same<A, float>::value) {
+            if (send)
+                atomicAdd(static_cast<float *>(c.base) + i, x);
+        } else {
+            if (!c.attr) {
+                if (send)
+                    atomicAdd(static_cast<float *>(c.base) + i, x);
+                return;
+            }
+            column_send_f16(c, i, x, send, lane);
+        }
+    }
+
+    __device__ __forceinline__ void column_send_f16(const Column &c, size_t i, float x, bool send, uint32_t lane)
+    {
+        const uint64_t here = __ballot(1);
+        const uint64_t above = lane < 63u ? here & (~0ull << (lane + 1u)) : 0ull;
+        const uint64_t below = here & ((1ull << lane) - 1ull);
+        const uint32_t next = above ? (uint32_t)__builtin_ctzll(above) : lane;
+        // a texture column and the next column of the same map
+        const bool pairs_up = c.k < 24u && c.k != 11u && c.k != 23u;
+        const uint32_t a_lo = (uint32_t)reinterpret_cast<uintptr_t>(static_cast<A *>(c.base) + i);
+        const uint64_t sending = __ballot(send && c.k < 24u);
+        const uint32_t a_next = __shfl(a_lo, (int)next, 64);
+        const float x_next = __shfl(x, (int)next, 64);
+        const bool owner = send && pairs_up && above && ((sending >> next) & 1u) && (a_lo & 3u) == 0 &&
+                           a_next == a_lo + 2u;
+        const uint64_t owners = __ballot(owner);
+        const bool taken = below && ((owners >> (63 - __builtin_clzll(below))) & 1u);
+        if (owner)
+            Attr<A>::add_pair(static_cast<A *>(c.base), i, x, x_next);
+        else if (send && !taken)
+            Attr<A>::add(static_cast<A *>(c.base), i, x);
+    }
+
     // Sum of column c (column k of the row table) over the members `mem` of
     // one cell's group (ll: the lowest member; uniform: every member has the
     // leader's taps).  acc is the sum for tap t0, the leader's; when taps
@@ -633,10 +694,9 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
                 uint32_t t1 = 0xffffffffu;
                 float acc = 0.0f, acc1 = 0.0f;
                 column_sum(c, k, lead, mem, ll, uniform, t0, acc, t1, acc1);
-                if (acc != 0.0f)
-                    column_send(c, lead, t0, acc);
-                if (acc1 != 0.0f)
-                    column_send(c, lead, t1, acc1);
+                column_send_pass(c, lead, t0, acc, lane);
+                if (__ballot(acc1 != 0.0f)) // second sums: only where some member's taps differ
+                    column_send_pass(c, lead, t1, acc1, lane);
             }
         }
         while (singles) { // (pair only) two lone lanes per pass
@@ -651,8 +711,7 @@ template <typename A, int RD, int RS> struct BwdIntegrator {
             if (arank < 2u * (uint32_t)REC_COLS && mine < 64) {
                 const float x = rows[mine * ROW_STRIDE + (c1.k)];
                 const uint32_t t = (((c1.diffuse_taps ? (half ? db : da) : (half ? sb : sa))) >> c1.sh) & c1.tmask;
-                if (x != 0.0f)
-                    column_send(c1, half ? cb : ca, t, x);
+                column_send_pass(c1, half ? cb : ca, t, x, lane);
             }
         }
     }
