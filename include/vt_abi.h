@@ -215,7 +215,9 @@ int vt_trace_infer_q8_camera(const float *points, const uint8_t *diffuse, const 
  *   5): lane t traces ray ray_perm[t], overriding image_h/image_w; it must
  *   be a permutation of 0..num_rays-1 (an entry >= num_rays leaves its
  *   lane idle).  vt_ray_order makes one for flat batches.
- *   tile_order, tile_cost (extensions, ABI versions 9-10): with image lanes,
+ *   tile_order, tile_cost (extensions, ABI versions 9-10): with image lanes
+ *   (tiles: screen tiles) or a ray_perm (tiles: waves of 64 consecutive
+ *   ray_perm entries, a half-wave taking 32 of them),
  *   NULL or the tiles + 1 words of vt_tile_order (split_waves =
  *   vt_train_fwd_resident_waves()) over the costs a forward of the same rays
  *   recorded, and NULL or one u32 per tile receiving each tile's cost for
@@ -259,9 +261,9 @@ int vt_trace_fwd(int attr_dtype, const float *points, const void *diffuse, const
  *   slots into points_grad and density_grad at its end.
  *   Gradient scatters of lanes that integrate the same cell in the same step
  *   are combined in LDS before the global atomics.
- *   tile_order (an extension, ABI version 10): with image lanes, NULL or
- *   the tiles + 1 words of vt_tile_order over the costs the forward of these
- *   rays recorded.  Tiles launch in that order, and the first
+ *   tile_order (an extension, ABI version 10): with image lanes or a
+ *   ray_perm (tiles as for vt_trace_fwd), NULL or the tiles + 1 words of
+ *   vt_tile_order over the costs the forward of these rays recorded.  Tiles launch in that order, and the first
  *   tile_order[tiles] of them (at most vt_train_bwd_resident_waves()) run as
  *   two half-waves of 32 rays each.
  */

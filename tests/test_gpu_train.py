@@ -574,6 +574,57 @@ def test_backward_split_tiles(gpu, split, f16):
                     H.assert_f16_sum_close(a, want[key], A[key], K[key], key)
 
 
+@pytest.mark.parametrize("split", ["all", "part"])
+def test_backward_split_waves_ray_perm(gpu, split):
+    """A flat batch in a ray_perm lane order: the forward records the cost of
+    each wave of 64 consecutive ray_perm entries, and the backward of the same
+    rays and permutation tensors launches those waves by cost, the ones above
+    the split share (forced by TRAIN_SPLIT_WAVES) as two half-waves of 32
+    entries.  Per-ray walk statistics equal the batch-order backward's and
+    the gradients agree with it and with the oracle."""
+    s, rays, start, thr = _case("hf8")
+    flat = rays.reshape(-1, 6)
+    shuffle = np.random.default_rng(13).permutation(flat.shape[0])
+    flat, fstart = np.ascontiguousarray(flat[shuffle]), np.ascontiguousarray(start.reshape(-1)[shuffle])
+    scene_t = _scene_tensors(s, gpu, False)
+    rd, sd = H.to_dev(flat, gpu), H.to_dev(fstart, gpu)
+    perm = _C.ray_order(rd, sd, s.points.shape[0])
+    gn = np.random.default_rng(14).normal(size=(flat.shape[0], 4)).astype(np.float32)
+    g = H.to_dev(gn, gpu)
+    tiles = (flat.shape[0] + 63) // 64
+    saved = (_C.TRAIN_TILE_ORDER, _C.TRAIN_SPLIT_WAVES)
+    try:
+        res = {}
+        for flag in (False, True):
+            _C.TRAIN_TILE_ORDER = flag
+            _C.TRAIN_SPLIT_WAVES = (1 << 23) if split == "all" else tiles
+            _C._TRAIN_SCHEDULES.clear()
+            out = _C.trace_vorotracing_fwd(*scene_t, rd, sd, None, thr, 1024, False, ray_perm=perm)
+            st = native.new_stats(flat.shape[0], gpu)
+            grads = _C.trace_vorotracing_bwd(*scene_t, rd, sd, out[0], g, None, None, None, None, 0.0, out[5], None,
+                                             out[6], out[7], out[8], thr, 1024, stats=st, ray_perm=perm)
+            torch.cuda.synchronize()
+            res[flag] = ([x.cpu().numpy() for x in grads[:4]], H.stats_np(st))
+        sch = next(iter(_C._TRAIN_SCHEDULES.values()))
+        cost = sch.cost.cpu().numpy().astype(np.int64)
+        k = int(sch.order[tiles].item())
+    finally:
+        _C.TRAIN_TILE_ORDER, _C.TRAIN_SPLIT_WAVES = saved
+        _C._TRAIN_SCHEDULES.clear()
+    assert sch.tiles == tiles
+    want_k = tiles if split == "all" else int(np.sum(5 * cost * tiles > 4 * cost.sum()))
+    assert 0 < k == want_k, (k, want_k)
+    H.assert_stats_equal(res[True][1], res[False][1])
+    fw = core.trace_fwd(s.points, s.diffuse, s.specular, s.diff_res, s.spec_res, s.density, s.adjacency, s.offsets,
+                        flat, fstart, weight_threshold=thr)
+    want = core.trace_bwd(s.points, s.diffuse, s.specular, s.diff_res, s.spec_res, s.density, s.adjacency,
+                          s.offsets, flat, fstart, fw["rgba"], gn, distortion=fw["distortion"], W_total=fw["W_total"],
+                          S_total=fw["S_total"], t_far=fw["t_far"], weight_threshold=thr)
+    for a, b, key in zip(res[True][0], res[False][0], ("points_grad", "diffuse_grad", "specular_grad", "density_grad")):
+        H.assert_grad_close(a, b, key)
+        H.assert_grad_close(a, want[key], key)
+
+
 def test_model_sort_morton(gpu):
     """VoroTracing.sort_morton: the model's rows and CSR in Morton order (the
     oracle's morton_reorder permutation), the LBVH rebuilt, gradients and

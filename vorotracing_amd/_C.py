@@ -153,13 +153,29 @@ TRAIN_SPLIT_WAVES: Optional[int] = None
 _TRAIN_SCHEDULES: dict = {}
 
 
-def _train_schedule(rays, img_h: int, img_w: int, num_rays: int, device) -> Optional["native.TileSchedule"]:
-    if not TRAIN_TILE_ORDER or not img_h:
-        return None
-    images = num_rays // (img_h * img_w)
-    key = (images, img_h, img_w, _stream(device))
-    return native.schedule_for(_TRAIN_SCHEDULES, key, native.num_tiles(images, img_h, img_w), device,
-                               split_waves=_split_waves("bwd"))
+def _train_schedule(rays_in, img_h: int, img_w: int, num_rays: int, perm, ray_perm_arg, device):
+    """(schedule, frame) of a training launch, or (None, None) without tiles.
+    Image lanes: screen tiles, one schedule per image shape and stream, the
+    frame being the rays tensor.  A ray_perm lane order (a sorted flat
+    batch): waves of 64 consecutive ray_perm entries, one schedule per ray
+    count and stream, the frame being the rays and the permutation tensors
+    (the autograd path hands the forward's permutation to the backward; a
+    permutation made inside each entry, "auto", has no frame)."""
+    if not TRAIN_TILE_ORDER:
+        return None, None
+    if perm is not None:
+        tiles = (num_rays + 63) // 64
+        key = ("perm", tiles, _stream(device))
+        frame = ((native.frame_key(rays_in), native.frame_key(ray_perm_arg))
+                 if isinstance(ray_perm_arg, torch.Tensor) else None)
+    elif img_h:
+        images = num_rays // (img_h * img_w)
+        tiles = native.num_tiles(images, img_h, img_w)
+        key = (images, img_h, img_w, _stream(device))
+        frame = native.frame_key(rays_in)
+    else:
+        return None, None
+    return native.schedule_for(_TRAIN_SCHEDULES, key, tiles, device, split_waves=_split_waves("bwd")), frame
 
 
 def _split_waves(kernel: str) -> int:
@@ -480,8 +496,8 @@ def trace_vorotracing_fwd(points_in, diffuse_in, specular_in, density_in, point_
     workspace = _adj_diff_buffer(adj_diff_out, adjacency_size, dev, "adj_diff_out")
     img_h, img_w, perm = _lane_order(rays, start_point, num_points, ray_perm)
     with torch.cuda.device(dev):
-        sch = _train_schedule(rays, img_h, img_w, num_rays, dev) if perm is None else None
-        order, cost = (sch.launch_args(_stream(dev), native.frame_key(rays_in), split_waves=_split_waves("fwd"))
+        sch, frame = _train_schedule(rays_in, img_h, img_w, num_rays, perm, ray_perm, dev)
+        order, cost = (sch.launch_args(_stream(dev), frame, split_waves=_split_waves("fwd"))
                        if sch is not None else (None, None))
         _lib.call("vt_trace_fwd", code, points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd, rs,
                   density.data_ptr(), adjacency.data_ptr(), adjacency_size, offsets.data_ptr(), num_points,
@@ -606,8 +622,8 @@ def trace_vorotracing_bwd(points_in, diffuse_in, specular_in, density_in, point_
     cell_workspace = torch.empty((num_points, 4), dtype=torch.float32, device=dev)
     img_h, img_w, perm = _lane_order(rays, start_point, num_points, ray_perm)
     with torch.cuda.device(dev):
-        sch = _train_schedule(rays, img_h, img_w, num_rays, dev) if perm is None else None
-        order = sch.order_for(_stream(dev), native.frame_key(rays_in)) if sch is not None else None
+        sch, frame = _train_schedule(rays_in, img_h, img_w, num_rays, perm, ray_perm, dev)
+        order = sch.order_for(_stream(dev), frame) if sch is not None else None
         _lib.call("vt_trace_bwd", code, points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd, rs,
                   density.data_ptr(), adjacency.data_ptr(), adjacency_size, offsets.data_ptr(), num_points,
                   rays.data_ptr(), num_rays, img_h, img_w, start_point.data_ptr(), _ptr(perm), rgb_out.data_ptr(),

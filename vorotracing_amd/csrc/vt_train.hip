@@ -136,30 +136,41 @@ constexpr uint32_t TRAIN_TILE = 8;
 #endif
 constexpr uint32_t TRAIN_TILE_STRIP = VT_TRAIN_TILE_STRIP;
 
+// Tiles of a training launch: the screen tiles of image lanes, or the waves
+// of 64 consecutive ray_perm entries of a sorted flat batch; 0 for rays in
+// batch order.
+__host__ __device__ inline uint32_t train_tiles(uint32_t num_rays, bool perm, uint32_t ni, uint32_t h, uint32_t w)
+{
+    if (perm)
+        return (num_rays + 63u) / 64u;
+    return ni * ((w + TRAIN_TILE - 1) / TRAIN_TILE) * ((h + TRAIN_TILE - 1) / TRAIN_TILE);
+}
+
 // Slot s of a tiled training launch: the tile its wave runs (NONE past the
 // last), the lane's ray within the tile's 64 (NONE for the idle lanes of a
 // half-wave) and whether the wave runs half a tile.  With a tile order,
 // wave j runs tile tile_order[j], except that the first k tiles of the
 // order, k = tile_order[tiles] clamped to the waves the launch added for
-// them, run as two half-waves each: waves 2i and 2i + 1 take rows 0-3 and
-// rows 4-7 of tile tile_order[i] on lanes 0-31, and wave 2k + j takes tile
-// tile_order[k + j].  A long tile, which the launch would otherwise end
-// waiting for, then ends about as early as the rest.  The forward
-// (ORDER_ONLY_TO_SPLIT) keeps screen order when k is 0: an order alone made
-// it slower.
+// them, run as two half-waves each: waves 2i and 2i + 1 take the first and
+// the last 32 rays of tile tile_order[i] (rows 0-3 and 4-7 of a screen
+// tile) on lanes 0-31, and wave 2k + j takes tile tile_order[k + j].  A long
+// tile, which the launch would otherwise end waiting for, then ends about as
+// early as the rest.  The forward (ORDER_ONLY_TO_SPLIT) keeps its own order
+// when k is 0: an order alone made it slower.
 struct TrainSlot {
     uint32_t tile, within;
     bool half;
 };
 
 template <bool ORDER_ONLY_TO_SPLIT>
-__device__ __forceinline__ TrainSlot train_slot(uint32_t s, uint32_t ni, uint32_t h, uint32_t w,
-                                                const uint32_t *tile_order)
+__device__ __forceinline__ TrainSlot train_slot(uint32_t s, uint32_t tiles, const uint32_t *tile_order)
 {
     TrainSlot r{s >> 6, s & 63u, false};
-    if (!tile_order)
+    if (!tile_order) {
+        if (r.tile >= tiles)
+            r.tile = NONE;
         return r;
-    const uint32_t tiles = ni * ((w + TRAIN_TILE - 1) / TRAIN_TILE) * ((h + TRAIN_TILE - 1) / TRAIN_TILE);
+    }
     const uint32_t waves = gridDim.x * (blockDim.x / 64u);
     const uint32_t extra = waves > tiles ? waves - tiles : 0u;
     const uint32_t k = min(min(tile_order[tiles], tiles), extra);
@@ -185,13 +196,20 @@ __device__ __forceinline__ uint32_t train_ray(uint32_t s, uint32_t num_rays, con
                                               uint32_t h, uint32_t w, const uint32_t *tile_order)
 {
     if (perm) {
-        if (s >= num_rays)
+        uint32_t q = s;
+        if (tile_order) {
+            const TrainSlot t = train_slot<ORDER_ONLY_TO_SPLIT>(s, train_tiles(num_rays, true, 0, 0, 0), tile_order);
+            if (t.tile == NONE || t.within == NONE)
+                return NONE;
+            q = t.tile * 64u + t.within;
+        }
+        if (q >= num_rays)
             return NONE;
-        const uint32_t r = perm[s];
+        const uint32_t r = perm[q];
         return r < num_rays ? r : NONE;
     }
     if (ni) {
-        const TrainSlot t = train_slot<ORDER_ONLY_TO_SPLIT>(s, ni, h, w, tile_order);
+        const TrainSlot t = train_slot<ORDER_ONLY_TO_SPLIT>(s, train_tiles(num_rays, false, ni, h, w), tile_order);
         if (t.tile == NONE || t.within == NONE)
             return NONE;
         return tiled_ray<TRAIN_TILE_STRIP>(t.tile * 64u + t.within, ni, h, w, TRAIN_TILE, TRAIN_TILE);
@@ -381,14 +399,15 @@ void fwd_kernel(FwdArgs a)
     uint32_t n = 0, faces = 0;
     if (r != NONE)
         n = fwd_ray<A, RD, RS, STATS>(a, r, faces);
-    if (a.tile_cost && a.num_images) {
+    if (a.tile_cost && (a.num_images || a.ray_perm)) {
         // tiled launches are whole waves, and every lane is here; a split
         // tile records the larger of its halves' costs (the slower half is
         // what bounds it), in an atomic max (the caller cleared the costs
         // before an ordered launch)
         const uint32_t nmax = wave_max_u32(n), fmax = wave_max_u32(faces);
         if ((threadIdx.x & 63u) == 0) {
-            const TrainSlot t = train_slot<true>(s, a.num_images, a.img_h, a.img_w, a.tile_order);
+            const TrainSlot t = train_slot<true>(
+                s, train_tiles(a.num_rays, a.ray_perm != nullptr, a.num_images, a.img_h, a.img_w), a.tile_order);
             if (t.tile != NONE) {
                 if (t.half)
                     atomicMax(a.tile_cost + t.tile, tile_cost_of(nmax, fmax));
@@ -991,10 +1010,9 @@ template <template <typename, int, int, bool> class K, typename Args, typename A
 static int launch_train_rs(const Args &a, bool stats, hipStream_t s)
 {
     uint64_t slots = a.num_rays;
-    if (a.num_images) {
-        const uint64_t tiles = (uint64_t)a.num_images * ((a.img_h + TRAIN_TILE - 1) / TRAIN_TILE) *
-                               ((a.img_w + TRAIN_TILE - 1) / TRAIN_TILE);
-        slots = tiles * (TRAIN_TILE * TRAIN_TILE);
+    if (a.num_images || a.ray_perm) {
+        const uint64_t tiles = train_tiles(a.num_rays, a.ray_perm != nullptr, a.num_images, a.img_h, a.img_w);
+        slots = tiles * 64;
         // the waves that run split tiles' second halves (at most one per
         // resident wave: the split count stays below 1.25x that; see
         // vt_tile_order)
@@ -1092,8 +1110,10 @@ extern "C" int vt_trace_fwd(int attr_dtype, const float *points, const void *dif
     a.S_total = S_total;
     a.t_far = t_far;
     a.stats = reinterpret_cast<uint32_t *>(stats);
-    a.tile_order = a.num_images ? tile_order : nullptr;
-    a.tile_cost = a.num_images ? tile_cost : nullptr;
+    // tiles exist for image lanes and for the waves of a ray_perm lane order
+    const bool tiled = a.num_images || a.ray_perm;
+    a.tile_order = tiled ? tile_order : nullptr;
+    a.tile_cost = tiled ? tile_cost : nullptr;
     return launch_train<FwdK>(attr_dtype, a, diff_res, spec_res, stats != nullptr, s);
 }
 
@@ -1185,7 +1205,7 @@ extern "C" int vt_trace_bwd(int attr_dtype, const float *points, const void *dif
     a.specular_grad = specular_grad;
     a.point_error = point_error;
     a.stats = reinterpret_cast<uint32_t *>(stats);
-    a.tile_order = a.num_images ? tile_order : nullptr;
+    a.tile_order = (a.num_images || a.ray_perm) ? tile_order : nullptr;
     if (num_rays == 0)
         return VT_OK;
     const uint32_t cblocks = (num_points + 255) / 256;
