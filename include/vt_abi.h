@@ -65,6 +65,52 @@ int vt_prefetch_adj(const float *points, uint32_t num_points, const uint32_t *ad
                     const uint32_t *offsets, uint16_t *adj_diff, vt_stream_t stream);
 
 /*
+ * Packed walk layout (extension; no counterpart in the reference).  The
+ * scene's face records regrouped so that a traversal step issues fewer
+ * vector loads, which bound the traversal kernels:
+ *   chunks: u32 (num_chunks, 12).  Each cell's face list in chunks of 8
+ *     faces, 24 halves each: x, y, z of the chunk's first face, then of its
+ *     second, ... (the adj_diff halves).  A list is padded to a multiple of 8
+ *     with zero offsets, never an exit face (n.d = 0).
+ *   links: u32 (8 * num_chunks, 2).  Per padded face slot k of cell c, at
+ *     8 * first_chunk[c] + k: {neighbour | its chunk count << 24, its first
+ *     chunk}.
+ *   heads: u32 (num_points, 2): the same pair for each cell itself.
+ *   cells: f32 (num_points, 4): {site xyz, density}.
+ * The walk reads the same offsets, sites and densities as through adjacency,
+ * offsets and adj_diff, and renders the same images bit for bit.  Limits:
+ * num_points < 2^24, at most 255 chunks (2,040 faces) per cell and
+ * 8 * num_chunks < 2^32.
+ */
+typedef struct vt_walk_layout {
+    const uint32_t *chunks;
+    const uint32_t *links;
+    const uint32_t *heads;
+    const float *cells;
+    uint32_t num_chunks;
+} vt_walk_layout;
+
+/* Bytes of workspace for vt_walk_layout_count. */
+size_t vt_walk_layout_count_workspace_size(uint32_t num_points);
+/*
+ * Chunk ranges of the layout.  first_chunk out: u32 (num_points + 2):
+ * first_chunk[c] = chunks of the cells before c, [num_points] = the total
+ * (num_chunks), [num_points + 1] = the largest chunk count of one cell; the
+ * caller checks the limits on the last two before vt_walk_layout_fill.
+ */
+int vt_walk_layout_count(const uint32_t *offsets, uint32_t num_points, uint32_t *first_chunk, void *ws,
+                         vt_stream_t stream);
+/*
+ * Fill the layout (arrays sized for num_chunks = first_chunk[num_points]).
+ * density: the f32 per-cell density the renders integrate; adj_diff from
+ * vt_prefetch_adj.
+ */
+int vt_walk_layout_fill(const float *points, const float *density, const uint32_t *adjacency,
+                        const uint32_t *offsets, uint32_t num_points, const uint16_t *adj_diff,
+                        const uint32_t *first_chunk, uint32_t num_chunks, uint32_t *chunks, uint32_t *links,
+                        uint32_t *heads, float *cells, vt_stream_t stream);
+
+/*
  * fp16 inference render.  Replaces _C.trace_vorotracing_infer
  * (tracing_octmap.cu:642-717, kernel :552-610).
  *   diffuse/specular: Half4Texel maps, f16 (num_points, 4*R*R), R = diff_res /
@@ -89,7 +135,9 @@ int vt_trace_infer_f16(const float *points, const uint16_t *diffuse, const uint1
  * tile_order: NULL (tiles in screen order) or the launch order of the
  * ceil(W/tile_w) * ceil(H/tile_h) * num_images tiles (vt_tile_order);
  * tile_cost: NULL or one u32 per tile, written with each tile's cost for
- * vt_tile_order (both extensions).
+ * vt_tile_order (both extensions).  walk: NULL, or the scene's packed walk
+ * layout (vt_walk_layout; extension), which the kernel then walks in place of
+ * adjacency / adj_diff (same results; offsets still serve stats).
  */
 int vt_trace_infer_f16_tiled(const float *points, const uint16_t *diffuse, const uint16_t *specular,
                              uint32_t diff_res, uint32_t spec_res, const float *density, const uint32_t *adjacency,
@@ -97,7 +145,8 @@ int vt_trace_infer_f16_tiled(const float *points, const uint16_t *diffuse, const
                              const float *rays, uint32_t num_images, uint32_t image_h, uint32_t image_w,
                              uint32_t tile_h, uint32_t tile_w, const uint32_t *start_point, float weight_threshold,
                              uint32_t max_intersections, float cell_skip_threshold, uint16_t *rgba,
-                             const uint32_t *tile_order, uint32_t *tile_cost, vt_ray_stats *stats, vt_stream_t stream);
+                             const uint32_t *tile_order, uint32_t *tile_cost, vt_ray_stats *stats,
+                             const vt_walk_layout *walk, vt_stream_t stream);
 
 /*
  * q8 inference render.  Replaces _C.trace_vorotracing_infer_q8
@@ -116,7 +165,8 @@ int vt_trace_infer_q8(const float *points, const uint8_t *diffuse, const uint8_t
 
 /*
  * q8 inference over image batches with in-kernel wave tiling (as
- * vt_trace_infer_f16_tiled; per-ray results identical to vt_trace_infer_q8).
+ * vt_trace_infer_f16_tiled, walk included; per-ray results identical to
+ * vt_trace_infer_q8).
  */
 int vt_trace_infer_q8_tiled(const float *points, const uint8_t *diffuse, const uint8_t *specular, uint32_t diff_res,
                             uint32_t spec_res, const float diff_scale[3], const float diff_offset[3],
@@ -126,7 +176,7 @@ int vt_trace_infer_q8_tiled(const float *points, const uint8_t *diffuse, const u
                             uint32_t image_w, uint32_t tile_h, uint32_t tile_w, const uint32_t *start_point,
                             float weight_threshold, uint32_t max_intersections, float cell_skip_threshold,
                             uint16_t *rgba, const uint32_t *tile_order, uint32_t *tile_cost, vt_ray_stats *stats,
-                            vt_stream_t stream);
+                            const vt_walk_layout *walk, vt_stream_t stream);
 
 /*
  * Cameras for in-kernel ray generation.  Replaces the rays buffer that the
@@ -175,7 +225,7 @@ int vt_camera_rays(const vt_camera *cameras, uint32_t num_images, uint32_t image
  * vt_camera_rays.  start_point: u32 start cell per image, or per image row
  * ((num_images, image_h)) when start_per_row is non-zero (rolling shutter:
  * every row has its own origin).  rgba (num_images, image_h, image_w, 4) f16;
- * stats in the same ray order.
+ * stats in the same ray order.  walk: as for vt_trace_infer_f16_tiled.
  */
 int vt_trace_infer_f16_camera(const float *points, const uint16_t *diffuse, const uint16_t *specular,
                               uint32_t diff_res, uint32_t spec_res, const float *density, const uint32_t *adjacency,
@@ -184,7 +234,7 @@ int vt_trace_infer_f16_camera(const float *points, const uint16_t *diffuse, cons
                               uint32_t tile_h, uint32_t tile_w, const uint32_t *start_point, int start_per_row,
                               float weight_threshold, uint32_t max_intersections, float cell_skip_threshold,
                               uint16_t *rgba, const uint32_t *tile_order, uint32_t *tile_cost, vt_ray_stats *stats,
-                              vt_stream_t stream);
+                              const vt_walk_layout *walk, vt_stream_t stream);
 int vt_trace_infer_q8_camera(const float *points, const uint8_t *diffuse, const uint8_t *specular, uint32_t diff_res,
                              uint32_t spec_res, const float diff_scale[3], const float diff_offset[3],
                              const float spec_scale[3], const float spec_offset[3], const float *density,
@@ -193,7 +243,8 @@ int vt_trace_infer_q8_camera(const float *points, const uint8_t *diffuse, const 
                              uint32_t image_h, uint32_t image_w, uint32_t tile_h, uint32_t tile_w,
                              const uint32_t *start_point, int start_per_row, float weight_threshold,
                              uint32_t max_intersections, float cell_skip_threshold, uint16_t *rgba,
-                             const uint32_t *tile_order, uint32_t *tile_cost, vt_ray_stats *stats, vt_stream_t stream);
+                             const uint32_t *tile_order, uint32_t *tile_cost, vt_ray_stats *stats,
+                             const vt_walk_layout *walk, vt_stream_t stream);
 
 /*
  * Training forward.  Replaces _C.trace_vorotracing_fwd

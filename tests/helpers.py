@@ -256,3 +256,32 @@ def f16_train_sums(s, rays, start, thr, fw16, g16, contribution=False, **bwd_kw)
                                                    return_contribution=True)["contribution"]
         out.append(r)
     return out[0], out[1]
+
+
+def walk_layout_np(points, density, adjacency, offsets, adj_diff):
+    """The packed walk layout (vt_walk_layout) built on the host with numpy:
+    (first_chunk (n + 2), chunks (C, 12) u32, links (8C, 2) u32, heads (n, 2)
+    u32, cells (n, 4) f32).  adj_diff: the f16 records (rows of 4 halves)."""
+    offsets = np.asarray(offsets, np.int64)
+    n = offsets.size - 1
+    nf = np.diff(offsets)
+    nch = (nf + 7) // 8
+    first = np.zeros(n + 2, np.int64)
+    first[1:n + 1] = np.cumsum(nch)
+    total = int(first[n])
+    first[n + 1] = nch.max() if n else 0
+    F = int(offsets[n])
+    halves = np.ascontiguousarray(adj_diff).view(np.uint16).reshape(-1, 4)[:F]
+    cell_of = np.repeat(np.arange(n), nf)
+    slot = 8 * first[cell_of] + (np.arange(F) - offsets[cell_of])
+    rows = np.zeros((max(total, 0), 8, 3), np.uint16)
+    for axis in range(3):
+        rows[slot // 8, slot % 8, axis] = halves[:, axis]
+    nb = np.asarray(adjacency, np.int64)[:F]
+    links = np.zeros((8 * total, 2), np.uint32)
+    links[slot, 0] = (nb | (nch[nb] << 24)).astype(np.uint32)
+    links[slot, 1] = first[nb].astype(np.uint32)
+    heads = np.stack([np.arange(n) | (nch << 24), first[:n]], 1).astype(np.uint32)
+    cells = np.concatenate([np.asarray(points, np.float32).reshape(n, 3),
+                            np.asarray(density, np.float32).reshape(n, 1)], 1)
+    return first.astype(np.uint32), rows.reshape(total, 24).view(np.uint32), links, heads, cells

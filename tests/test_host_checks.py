@@ -83,3 +83,36 @@ def test_tile_order_key_buckets():
         lb = x.bit_length() - 1
         frac = (x >> (lb - 2)) & 3 if lb >= 2 else (x << (2 - lb)) & 3
         assert k([x])[0] == 127 - (4 * lb + frac), x
+
+
+def test_walk_layout_np_round_trip():
+    """The numpy construction of the packed walk layout (the checker of the
+    GPU build) decodes back to the CSR it came from: every face record and
+    neighbour at its list position, zero records in the pads, and each link
+    carrying its neighbour's own head."""
+    rng = np.random.default_rng(2)
+    nf = np.array([0, 1, 7, 8, 9, 15, 16, 17, 0, 40], np.int64)
+    n = nf.size
+    offsets = np.concatenate([[0], np.cumsum(nf)])
+    F = int(offsets[-1])
+    adjacency = rng.integers(0, n, F + 32)
+    adj_diff = rng.integers(1, 1 << 15, (F + 32, 4)).astype(np.uint16)
+    points = rng.standard_normal((n, 3)).astype(np.float32)
+    density = rng.random(n).astype(np.float32)
+    first, chunks, links, heads, cells = H.walk_layout_np(points, density, adjacency, offsets, adj_diff)
+    nch = (nf + 7) // 8
+    assert first[n] == nch.sum() and first[n + 1] == nch.max() and chunks.shape == (nch.sum(), 12)
+    halves = chunks.view(np.uint16).reshape(-1, 8, 3)
+    for c in range(n):
+        assert heads[c, 0] == (c | nch[c] << 24) and heads[c, 1] == first[c]
+        assert np.array_equal(cells[c], np.append(points[c], density[c]))
+        for f in range(8 * nch[c]):
+            q, j = divmod(f, 8)
+            rec = halves[first[c] + q, j]
+            lk = links[8 * (first[c] + q) + j]
+            if f < nf[c]:
+                assert np.array_equal(rec, adj_diff[offsets[c] + f, :3])
+                nb = adjacency[offsets[c] + f]
+                assert np.array_equal(lk, heads[nb])
+            else:
+                assert not rec.any() and not lk.any()

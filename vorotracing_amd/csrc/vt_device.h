@@ -280,6 +280,8 @@ constexpr uint32_t STATS_WORDS = sizeof(vt_ray_stats) / 4;
 static_assert(sizeof(vt_ray_stats) == 4 * (8 + VT_STATS_LOG), "vt_ray_stats is 8 counter words and the log");
 
 template <bool ON> struct StatsAcc {
+    // visit() takes a cell's face count, or any cost-like count when false
+    static constexpr bool EXACT_FACES = false;
     uint32_t faces = 0; // face records searched (a launch-order cost; dropped when unread)
     __device__ __forceinline__ void begin(void *, uint32_t) {}
     __device__ __forceinline__ void visit(uint32_t, uint32_t nf) { faces += nf; }
@@ -291,6 +293,7 @@ template <bool ON> struct StatsAcc {
 };
 
 template <> struct StatsAcc<true> {
+    static constexpr bool EXACT_FACES = true;
     Stats s{0, 0, 0, 0, 0, 0, 1469598103934665603ull};
     uint32_t *log = nullptr; // first_cells of this ray's record
     // the record of ray r (NONE: no record)

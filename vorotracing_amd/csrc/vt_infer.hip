@@ -116,6 +116,8 @@ template <int RD, int RS, class Tex> struct InferIntegrator {
     float pdens; // density of the current cell, loaded by begin_cell
 
     __device__ __forceinline__ void begin_cell(uint32_t cell) { pdens = density[cell]; }
+    // the density when the walk state carries it (packed walk layout)
+    __device__ __forceinline__ void begin_cell_value(float dens) { pdens = dens; }
 
     template <class S>
     __device__ __forceinline__ bool integrate(uint32_t cell, float t0, float t1, f3 p, f3, S &st)
@@ -261,6 +263,12 @@ struct InferArgs {
     // and each tile's cost, written by the call (NULL = not recorded)
     const uint32_t *tile_order;
     uint32_t *tile_cost;
+    // packed walk layout (vt_walk_layout), or wl_chunks = NULL to walk
+    // adjacency / offsets / adj_diff
+    const uint4 *wl_chunks;
+    const uint2 *wl_links;
+    const uint2 *wl_heads;
+    const float4 *wl_cells;
 };
 
 // MAP_CAMERA: tiled lanes whose rays come from cameras instead of a buffer.
@@ -290,7 +298,7 @@ __device__ __forceinline__ uint32_t slot_to_ray(const InferArgs &a, uint32_t s, 
 }
 
 
-template <int RD, int RS, bool Q8, bool STATS, int MAP, int CHUNK>
+template <int RD, int RS, bool Q8, bool STATS, int MAP, int CHUNK, bool PACKED>
 // 8 waves per SIMD need at most 64 VGPRs.  The fp16 kernel fits them; the q8
 // kernel spills 12 bytes per lane and is still faster than at 7 waves
 // (C4: 16.6 against 17.2 ms).  The statistics variants (tests and counters
@@ -327,7 +335,7 @@ void infer_kernel(InferArgs a, uint32_t total_slots)
     integ.T = 1.0f;
     StatsAcc<STATS> st;
     st.begin(a.stats, r);
-    WalkState w;
+    typename std::conditional<PACKED, PackedWalk, WalkState>::type w;
     if (active) {
         uint32_t start;
         if constexpr (MAP == MAP_CAMERA) {
@@ -349,7 +357,10 @@ void infer_kernel(InferArgs a, uint32_t total_slots)
         q.sw[1][lane] = sb.w10;
         q.sw[2][lane] = sb.w01;
         q.sw[3][lane] = sb.w11;
-        walk_begin(w, a.points, a.offsets, start);
+        if constexpr (PACKED)
+            walk_begin_packed(w, a.wl_heads, a.wl_cells, start);
+        else
+            walk_begin(w, a.points, a.offsets, start);
     }
     q.mask[lane] = 0ull;
     if (lane == 0)
@@ -357,9 +368,14 @@ void infer_kernel(InferArgs a, uint32_t total_slots)
     wave_lds_sync();
     uint32_t head = 0; // wave-uniform: entries shaded so far
     while (__ballot(active)) {
-        if (active)
-            active = walk_step<CHUNK>(w, integ.o, integ.d, a.points, a.adjacency, a.offsets, a.adj_diff,
-                                      a.max_steps, integ, st);
+        if (active) {
+            if constexpr (PACKED)
+                active = walk_step_packed(w, integ.o, integ.d, a.wl_chunks, a.wl_links, a.wl_cells, a.offsets,
+                                          a.max_steps, integ, st);
+            else
+                active = walk_step<CHUNK>(w, integ.o, integ.d, a.points, a.adjacency, a.offsets, a.adj_diff,
+                                          a.max_steps, integ, st);
+        }
         wave_lds_sync();
         if (__builtin_amdgcn_readfirstlane(q.tail) - head >= 64u) {
             shade_batch<RD, RS>(q, head, 64, integ, lane);
@@ -391,7 +407,10 @@ template <int RD, int RS, bool Q8, bool STATS, int MAP>
 static int launch_one(const InferArgs &a, hipStream_t stream, uint32_t slots)
 {
     uint32_t blocks = (slots + INFER_BLOCK - 1) / INFER_BLOCK;
-    infer_kernel<RD, RS, Q8, STATS, MAP, INFER_CHUNK><<<blocks, INFER_BLOCK, 0, stream>>>(a, slots);
+    if (a.wl_chunks)
+        infer_kernel<RD, RS, Q8, STATS, MAP, INFER_CHUNK, true><<<blocks, INFER_BLOCK, 0, stream>>>(a, slots);
+    else
+        infer_kernel<RD, RS, Q8, STATS, MAP, INFER_CHUNK, false><<<blocks, INFER_BLOCK, 0, stream>>>(a, slots);
     VT_LAUNCH_CHECK("infer_kernel");
     return VT_OK;
 }
@@ -434,6 +453,19 @@ static int check_common(const void *points, const void *diffuse, const void *spe
     VT_REQUIRE(points && diffuse && specular && density && adjacency && offsets && adj_diff && rays &&
                    start_point && rgba,
                "null pointer argument");
+    return VT_OK;
+}
+
+// The packed walk layout of a call, or the general walk when walk is NULL.
+static int set_walk_layout(InferArgs &a, const vt_walk_layout *walk)
+{
+    if (!walk)
+        return VT_OK;
+    VT_REQUIRE(walk->chunks && walk->links && walk->heads && walk->cells, "null array in the walk layout");
+    a.wl_chunks = reinterpret_cast<const uint4 *>(walk->chunks);
+    a.wl_links = reinterpret_cast<const uint2 *>(walk->links);
+    a.wl_heads = reinterpret_cast<const uint2 *>(walk->heads);
+    a.wl_cells = reinterpret_cast<const float4 *>(walk->cells);
     return VT_OK;
 }
 
@@ -484,7 +516,7 @@ extern "C" int vt_trace_infer_f16_tiled(const float *points, const uint16_t *dif
                                         const uint32_t *start_point, float weight_threshold,
                                         uint32_t max_intersections, float cell_skip_threshold, uint16_t *rgba,
                                         const uint32_t *tile_order, uint32_t *tile_cost,
-                                        vt_ray_stats *stats, vt_stream_t stream)
+                                        vt_ray_stats *stats, const vt_walk_layout *walk, vt_stream_t stream)
 {
     clear_error();
     if (num_images == 0 || image_h == 0 || image_w == 0)
@@ -517,6 +549,9 @@ extern "C" int vt_trace_infer_f16_tiled(const float *points, const uint16_t *dif
     a.stats = reinterpret_cast<uint32_t *>(stats);
     a.tile_order = tile_order;
     a.tile_cost = tile_cost;
+    rc = set_walk_layout(a, walk);
+    if (rc)
+        return rc;
     a.num_images = num_images;
     a.H = image_h;
     a.W = image_w;
@@ -578,7 +613,7 @@ extern "C" int vt_trace_infer_q8_tiled(const float *points, const uint8_t *diffu
                                        uint32_t tile_h, uint32_t tile_w, const uint32_t *start_point,
                                        float weight_threshold, uint32_t max_intersections, float cell_skip_threshold,
                                        uint16_t *rgba, const uint32_t *tile_order, uint32_t *tile_cost,
-                                       vt_ray_stats *stats, vt_stream_t stream)
+                                       vt_ray_stats *stats, const vt_walk_layout *walk, vt_stream_t stream)
 {
     clear_error();
     if (num_images == 0 || image_h == 0 || image_w == 0)
@@ -611,6 +646,9 @@ extern "C" int vt_trace_infer_q8_tiled(const float *points, const uint8_t *diffu
     a.stats = reinterpret_cast<uint32_t *>(stats);
     a.tile_order = tile_order;
     a.tile_cost = tile_cost;
+    rc = set_walk_layout(a, walk);
+    if (rc)
+        return rc;
     a.num_images = num_images;
     a.H = image_h;
     a.W = image_w;
@@ -688,7 +726,7 @@ extern "C" int vt_trace_infer_f16_camera(const float *points, const uint16_t *di
                                          const uint32_t *start_point, int start_per_row, float weight_threshold,
                                          uint32_t max_intersections, float cell_skip_threshold, uint16_t *rgba,
                                          const uint32_t *tile_order, uint32_t *tile_cost,
-                                         vt_ray_stats *stats, vt_stream_t stream)
+                                         vt_ray_stats *stats, const vt_walk_layout *walk, vt_stream_t stream)
 {
     clear_error();
     if (num_images == 0 || image_h == 0 || image_w == 0)
@@ -714,6 +752,9 @@ extern "C" int vt_trace_infer_f16_camera(const float *points, const uint16_t *di
     a.stats = reinterpret_cast<uint32_t *>(stats);
     a.tile_order = tile_order;
     a.tile_cost = tile_cost;
+    rc = set_walk_layout(a, walk);
+    if (rc)
+        return rc;
     a.H = image_h;
     a.W = image_w;
     a.th = tile_h;
@@ -732,7 +773,7 @@ extern "C" int vt_trace_infer_q8_camera(const float *points, const uint8_t *diff
                                         const uint32_t *start_point, int start_per_row, float weight_threshold,
                                         uint32_t max_intersections, float cell_skip_threshold, uint16_t *rgba,
                                         const uint32_t *tile_order, uint32_t *tile_cost,
-                                        vt_ray_stats *stats, vt_stream_t stream)
+                                        vt_ray_stats *stats, const vt_walk_layout *walk, vt_stream_t stream)
 {
     clear_error();
     if (num_images == 0 || image_h == 0 || image_w == 0)
@@ -759,6 +800,9 @@ extern "C" int vt_trace_infer_q8_camera(const float *points, const uint8_t *diff
     a.stats = reinterpret_cast<uint32_t *>(stats);
     a.tile_order = tile_order;
     a.tile_cost = tile_cost;
+    rc = set_walk_layout(a, walk);
+    if (rc)
+        return rc;
     a.H = image_h;
     a.W = image_w;
     a.th = tile_h;

@@ -6,6 +6,7 @@
 #include "vt_internal.h"
 #include "vt_prims.h"
 #include "vt_device.h"
+#include "vt_walk.h"
 
 namespace vt {
 
@@ -677,5 +678,120 @@ extern "C" int vt_pad_3to4_f16(const float *x, uint32_t rows, uint32_t texels_pe
         return VT_OK;
     pad34_kernel<<<grid_for(t), 256, 0, as_stream(stream)>>>(x, t, reinterpret_cast<uint2 *>(out));
     VT_LAUNCH_CHECK("pad34_kernel");
+    return VT_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Packed walk layout (vt_walk_layout): the inference walk's arrays regrouped
+// so that a step issues fewer vector loads (the walk side is in vt_walk.h).
+
+namespace vt {
+
+__global__ void wl_init_kernel(uint32_t *first_chunk, uint32_t n)
+{
+    if (blockIdx.x == 0 && threadIdx.x == 0)
+        first_chunk[n + 1] = 0;
+}
+
+// chunk count of each cell (8 faces per chunk); [n] = 0 so that the scan
+// leaves the total there; [n + 1] = the largest count
+__global__ void wl_count_kernel(const uint32_t *offsets, uint32_t n, uint32_t *first_chunk)
+{
+    const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c > n)
+        return;
+    if (c == n) {
+        first_chunk[n] = 0;
+        return;
+    }
+    const uint32_t k = (uint32_t)(((uint64_t)offsets[c + 1] - offsets[c] + 7u) >> 3);
+    first_chunk[c] = k;
+    atomicMax(first_chunk + n + 1, k);
+}
+
+// One lane per cell: its cell record, its head, and its chunks and links.
+__global__ void wl_fill_kernel(const float *__restrict__ points, const float *__restrict__ density,
+                               const uint32_t *__restrict__ adjacency, const uint32_t *__restrict__ offsets,
+                               uint32_t n, const uint2 *__restrict__ adj_diff, const uint32_t *__restrict__ fc,
+                               uint4 *__restrict__ chunks, uint2 *__restrict__ links, uint2 *__restrict__ heads,
+                               float4 *__restrict__ cells)
+{
+    const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= n)
+        return;
+    const uint32_t b = offsets[c], nf = offsets[c + 1] - b;
+    const uint32_t cb = fc[c], nch = fc[c + 1] - cb;
+    const f3 p = load_site(points, c);
+    cells[c] = make_float4(p.x, p.y, p.z, density[c]);
+    heads[c] = make_uint2(c | nch << WL_ID_BITS, cb);
+    for (uint32_t q = 0; q < nch; ++q) {
+        // the chunk's 24 halves: x, y, z of face 0, then of face 1, ...
+        uint32_t w[12] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t f = 8 * q + j;
+            uint2 lk = make_uint2(0u, 0u);
+            if (f < nf) {
+                const uint2 r = adj_diff[b + f];
+                const uint32_t h[3] = {r.x & 0xffffu, r.x >> 16, r.y & 0xffffu};
+#pragma unroll
+                for (int a = 0; a < 3; ++a) {
+                    const int k = 3 * j + a;
+                    w[k >> 1] |= h[a] << (16 * (k & 1));
+                }
+                const uint32_t nb = adjacency[b + f];
+                const uint32_t ncb = fc[nb];
+                lk = make_uint2(nb | (fc[nb + 1] - ncb) << WL_ID_BITS, ncb);
+            }
+            links[8 * (size_t)(cb + q) + j] = lk;
+        }
+        uint4 *row = chunks + 3 * (size_t)(cb + q);
+        row[0] = make_uint4(w[0], w[1], w[2], w[3]);
+        row[1] = make_uint4(w[4], w[5], w[6], w[7]);
+        row[2] = make_uint4(w[8], w[9], w[10], w[11]);
+    }
+}
+
+} // namespace vt
+
+extern "C" size_t vt_walk_layout_count_workspace_size(uint32_t num_points)
+{
+    return 4 * scan_workspace_words(num_points + 1);
+}
+
+extern "C" int vt_walk_layout_count(const uint32_t *offsets, uint32_t num_points, uint32_t *first_chunk, void *ws,
+                                    vt_stream_t stream)
+{
+    clear_error();
+    VT_REQUIRE(offsets && first_chunk && ws, "null pointer argument");
+    VT_REQUIRE(num_points < 0xffffffffu, "too many points");
+    hipStream_t s = as_stream(stream);
+    wl_init_kernel<<<1, 64, 0, s>>>(first_chunk, num_points);
+    VT_LAUNCH_CHECK("wl_init_kernel");
+    wl_count_kernel<<<(uint32_t)(((size_t)num_points + 256) / 256), 256, 0, s>>>(offsets, num_points,
+                                                                              first_chunk);
+    VT_LAUNCH_CHECK("wl_count_kernel");
+    return exclusive_scan_u32(first_chunk, first_chunk, num_points + 1, (uint32_t *)ws, s);
+}
+
+extern "C" int vt_walk_layout_fill(const float *points, const float *density, const uint32_t *adjacency,
+                                   const uint32_t *offsets, uint32_t num_points, const uint16_t *adj_diff,
+                                   const uint32_t *first_chunk, uint32_t num_chunks, uint32_t *chunks,
+                                   uint32_t *links, uint32_t *heads, float *cells, vt_stream_t stream)
+{
+    clear_error();
+    VT_REQUIRE(points && density && adjacency && offsets && adj_diff && first_chunk && chunks && links && heads &&
+                   cells,
+               "null pointer argument");
+    VT_REQUIRE(num_points < (1u << WL_ID_BITS), "the walk layout holds cell ids below 2^24, got %u points",
+               num_points);
+    VT_REQUIRE(num_chunks < (1u << 29), "the walk layout holds fewer than 2^29 chunks, got %u", num_chunks);
+    if (num_points == 0)
+        return VT_OK;
+    wl_fill_kernel<<<(num_points + 255) / 256, 256, 0, as_stream(stream)>>>(
+        points, density, adjacency, offsets, num_points, reinterpret_cast<const uint2 *>(adj_diff), first_chunk,
+        reinterpret_cast<uint4 *>(chunks), reinterpret_cast<uint2 *>(links), reinterpret_cast<uint2 *>(heads),
+        reinterpret_cast<float4 *>(cells));
+    VT_LAUNCH_CHECK("wl_fill_kernel");
     return VT_OK;
 }

@@ -213,6 +213,174 @@ __device__ __forceinline__ uint32_t walk(f3 o, f3 d, const float *points,
     return w.n;
 }
 
+// ---------------------------------------------------------------------------
+// The same walk over the packed walk layout (vt_walk_layout, built by
+// vt_walk_layout_fill).  The traversal kernels are bound by the number of
+// vector memory instructions they issue, so the layout regroups the scene's
+// arrays to need fewer of them per step:
+//  - chunks: a cell's face records in chunks of 8, 16-byte aligned, each
+//    face's x, y, z halves in turn (48 bytes, three uint4 rows): three loads
+//    per 8 faces instead of four, and no per-face bound test, since a list is
+//    padded to a multiple of 8 with zero offsets (n.d = 0 is never an exit
+//    face);
+//  - links: per padded face slot, the neighbour behind it with its own chunk
+//    range, so the next cell's face records can be loaded as soon as the exit
+//    face is known, in parallel with its site;
+//  - cells: site and density in one 16-byte record.
+// A step reads the same offsets, sites and densities as walk_step, so it
+// picks the same exit faces and hands the integrator the same values.
+constexpr uint32_t WL_ID_BITS = 24;
+constexpr uint32_t WL_ID_MASK = (1u << WL_ID_BITS) - 1u;
+constexpr uint32_t WL_MAX_CHUNKS = 255; // chunks of one cell (8 bits beside the id)
+
+struct PackedWalk {
+    uint32_t cur; // cell
+    uint32_t nch; // chunks of its face list
+    uint32_t cb;  // its first chunk
+    f3 p;
+    float dens;
+    float t0;
+    uint32_t n;
+};
+
+__device__ __forceinline__ void walk_begin_packed(PackedWalk &w, const uint2 *heads, const float4 *cells,
+                                                  uint32_t start)
+{
+    const uint2 h = heads[start];
+    const float4 c = cells[start];
+    w.cur = start;
+    w.nch = h.x >> WL_ID_BITS;
+    w.cb = h.y;
+    w.p = mk(c.x, c.y, c.z);
+    w.dens = c.w;
+    w.t0 = 0.0f;
+    w.n = 0;
+}
+
+__device__ __forceinline__ uint32_t chunk_word(uint4 r0, uint4 r1, uint4 r2, int k)
+{
+    const uint4 r = k < 4 ? r0 : k < 8 ? r1 : r2;
+    k &= 3;
+    return k == 0 ? r.x : k == 1 ? r.y : k == 2 ? r.z : r.w;
+}
+
+__device__ __forceinline__ float chunk_half(uint4 r0, uint4 r1, uint4 r2, int h)
+{
+    const uint32_t w = chunk_word(r0, r1, r2, h >> 1);
+    return (h & 1) ? half_hi(w) : half_lo(w);
+}
+
+// Offset of face j (0..7) of a chunk whose 24 halves (x, y, z of face 0, then
+// of face 1, ...) are the rows R0, R1, R2: faces 0-1 lie in R0, 2-4 end in
+// R1 and 5-7 in R2, so the search starts as the first row arrives.
+__device__ __forceinline__ void chunk_face(uint4 R0, uint4 R1, uint4 R2, int j, float &ox, float &oy, float &oz)
+{
+    ox = chunk_half(R0, R1, R2, 3 * j);
+    oy = chunk_half(R0, R1, R2, 3 * j + 1);
+    oz = chunk_half(R0, R1, R2, 3 * j + 2);
+}
+
+// exit_face over the nch chunks at ch (3 uint4 rows each): the same choice,
+// ties to the lowest slot, and a slot is the face's index in the cell's list.
+__device__ __forceinline__ uint32_t exit_face_packed(const uint4 *ch, uint32_t nch, f3 p, f3 o, f3 d, float &t1)
+{
+    uint32_t best = NONE;
+    float bnum = FIRST_BNUM, bdp = FIRST_BDP;
+    for (uint32_t q = 0; q < nch; ++q) {
+        const uint4 *c = ch + 3 * q;
+        const uint4 R0 = c[0], R1 = c[1], R2 = c[2];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            float ox, oy, oz;
+            chunk_face(R0, R1, R2, j, ox, oy, oz);
+            // as in exit_face: keep the widening out of v_fma_mix operands
+            asm("" : "+v"(ox), "+v"(oy), "+v"(oz));
+            float dp = fma_(oz, d.z, fma_(oy, d.y, ox * d.x));
+            if (dp > 0.0f) {
+                float ex = fma_(ox, 0.5f, p.x) - o.x;
+                float ey = fma_(oy, 0.5f, p.y) - o.y;
+                float ez = fma_(oz, 0.5f, p.z) - o.z;
+                float num = fma_(ez, oz, fma_(ey, oy, ex * ox));
+                if (exit_before(num, dp, bnum, bdp)) {
+                    bnum = num;
+                    bdp = dp;
+                    best = 8 * q + j;
+                }
+            }
+        }
+    }
+    if (best == NONE)
+        return NONE;
+    t1 = bnum / bdp;
+    if (t1 == -__builtin_huge_valf()) {
+        // the IEEE redo of exit_face
+        float bt = __builtin_huge_valf();
+        best = NONE;
+        for (uint32_t q = 0; q < nch; ++q) {
+            const uint4 R0 = ch[3 * q], R1 = ch[3 * q + 1], R2 = ch[3 * q + 2];
+            for (int j = 0; j < 8; ++j) {
+                float ox, oy, oz;
+                chunk_face(R0, R1, R2, j, ox, oy, oz);
+                const float dp = fma_(oz, d.z, fma_(oy, d.y, ox * d.x));
+                if (dp > 0.0f) {
+                    const float ex = fma_(ox, 0.5f, p.x) - o.x;
+                    const float ey = fma_(oy, 0.5f, p.y) - o.y;
+                    const float ez = fma_(oz, 0.5f, p.z) - o.z;
+                    const float t = fma_(ez, oz, fma_(ey, oy, ex * ox)) / dp;
+                    if (t < bt) {
+                        bt = t;
+                        best = 8 * q + j;
+                    }
+                }
+            }
+        }
+        t1 = bt;
+    }
+    return best;
+}
+
+// walk_step over the packed layout.  The integrator takes the cell's density
+// from the walk state (begin_cell_value) instead of loading it.  Statistics
+// that record face counts read them from offsets; otherwise a visit counts
+// the cell's padded slots.
+template <class Integrator, class StatsT>
+__device__ __forceinline__ bool walk_step_packed(PackedWalk &w, f3 o, f3 d, const uint4 *chunks, const uint2 *links,
+                                                 const float4 *cells, const uint32_t *offsets, uint32_t max_steps,
+                                                 Integrator &integ, StatsT &st)
+{
+    w.n++;
+    if (w.n > max_steps)
+        return false;
+    const f3 p = w.p;
+    integ.begin_cell_value(w.dens);
+    if constexpr (StatsT::EXACT_FACES)
+        st.visit(w.cur, offsets[w.cur + 1] - offsets[w.cur]);
+    else
+        st.visit(w.cur, 8 * w.nch);
+    float t1;
+    const uint32_t best = exit_face_packed(chunks + 3 * (size_t)w.cb, w.nch, p, o, d, t1);
+    if (best == NONE)
+        return false;
+    st.exit();
+    const uint2 lk = links[8 * (size_t)w.cb + best];
+    const uint32_t nxt = lk.x & WL_ID_MASK;
+    const float4 c = cells[nxt];
+    const f3 np = mk(c.x, c.y, c.z);
+    // no early return inside the integrate branch (see walk_step)
+    bool go = true;
+    if (t1 > w.t0) {
+        st.integrate();
+        go = integ.integrate(w.cur, w.t0, t1, p, np, st);
+    }
+    w.t0 = __builtin_fmaxf(w.t0, t1);
+    w.cur = nxt;
+    w.nch = lk.x >> WL_ID_BITS;
+    w.cb = lk.y;
+    w.p = np;
+    w.dens = c.w;
+    return go;
+}
+
 // Cost of a screen tile for the launch order of the next launch over the
 // same rays (vt_tile_order): TILE_COST_STEP x the longest walk's steps + the
 // most face records one ray of the tile searched, both maxima over the

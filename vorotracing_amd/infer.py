@@ -27,6 +27,9 @@ class VoroTracingInfer:
     # launch the tiles of a repeated image shape by the previous frame's tile
     # costs (native.TileSchedule; images are bit-identical either way)
     adaptive_tile_order = True
+    # walk the packed layout (native.WalkLayout) in the tiled and camera
+    # renders; images are bit-identical either way
+    packed_walk = True
 
     def __init__(self, model, sort_morton: bool = True, quantize: Literal["fp16", "q8"] = "fp16",
                  per_channel_q8: bool = False):
@@ -64,6 +67,22 @@ class VoroTracingInfer:
             self.bvh.build(self.primal_points)
         self.adjacent_diff = ops.prefetch_octmap_adj(self.primal_points, self.point_adjacency,
                                                      self.point_adjacency_offsets)
+        self._walk_layout = None
+
+    def walk_layout(self) -> Optional[native.WalkLayout]:
+        """The scene's packed walk layout (built on first use, and again when
+        the sites, density, adjacency or face records have been replaced or
+        changed in place), or None when ``packed_walk`` is off or the scene
+        exceeds the layout's limits."""
+        if not self.packed_walk:
+            return None
+        src = (self.primal_points, self.density, self.point_adjacency, self.point_adjacency_offsets,
+               self.adjacent_diff)
+        entry = self._walk_layout
+        if entry is None or not entry[0].matches(*src):
+            entry = (native.SourceKey(*src), native.WalkLayout.build(*src))
+            self._walk_layout = entry
+        return entry[1]
 
     @classmethod
     def from_foam(cls, path, device=torch.device("cuda"), quantize: Literal["fp16", "q8"] = "fp16",
@@ -274,7 +293,8 @@ class VoroTracingInfer:
                                 start_point, weight_threshold=weight_threshold, max_intersections=max_intersections,
                                 cell_skip_threshold=cell_skip_threshold, stats=stats,
                                 tiled=self.TILE if image else None,
-                                schedule=self._schedule(*native.image_dims(rays)) if image else None)
+                                schedule=self._schedule(*native.image_dims(rays)) if image else None,
+                                walk=self.walk_layout() if image else None)
 
     def camera_start_points(self, cameras, camera_buffer=None):
         """Start cells of a camera batch: one LBVH query on each camera's centre, or
@@ -311,7 +331,7 @@ class VoroTracingInfer:
         frame = camera.pack_cameras(cams)  # host-side records: no device read
         order, cost = sch.launch_args(sp, frame) if sch is not None else (None, None)
         common = (float(weight_threshold), int(max_intersections), float(cell_skip_threshold), out.data_ptr(), order,
-                  cost, native._p(stats), sp)
+                  cost, native._p(stats), native._walk_ptr(self.walk_layout()), sp)
         if self.quantize == "q8":
             def v3(x):
                 vals = [float(x)] * 3 if isinstance(x, (int, float)) else [float(v) for v in x]
@@ -360,7 +380,7 @@ class VoroTracingInfer:
                       self.point_adjacency.data_ptr(), self.point_adjacency_offsets.data_ptr(),
                       self.primal_points.shape[0], self.adjacent_diff.data_ptr(), rays.data_ptr(), B, H, W,
                       self.TILE[0], self.TILE[1], start_point.data_ptr(), float(thr), int(max_int), float(skip),
-                      out.data_ptr(), order, cost, native._p(stats), sp)
+                      out.data_ptr(), order, cost, native._p(stats), native._walk_ptr(self.walk_layout()), sp)
         else:
             _lib.call("vt_trace_infer_q8", self.primal_points.data_ptr(), self.diffuse_q8.data_ptr(),
                       self.specular_q8.data_ptr(), rd, rs, *keep, self.density.data_ptr(),

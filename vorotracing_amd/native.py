@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import ctypes as C
 import math
+import weakref
 from typing import Optional, Tuple
 
 import torch
@@ -180,13 +181,97 @@ def schedule_for(cache: dict, key, tiles: int, device, limit: int = 16, split_wa
     return sch
 
 
+class SourceKey:
+    """Identity of a set of source tensors for data derived from them: the
+    tensors themselves (weak references, so a freed source never matches),
+    their storage and their in-place version."""
+
+    def __init__(self, *sources):
+        self._refs = [weakref.ref(t) for t in sources]
+        self._state = [(t.data_ptr(), t._version) for t in sources]
+
+    def matches(self, *sources) -> bool:
+        return len(sources) == len(self._refs) and all(
+            r() is t and (t.data_ptr(), t._version) == st for r, t, st in zip(self._refs, sources, self._state))
+
+
+class _WalkLayoutC(C.Structure):
+    _fields_ = [("chunks", C.c_void_p), ("links", C.c_void_p), ("heads", C.c_void_p), ("cells", C.c_void_p),
+                ("num_chunks", C.c_uint32)]
+
+
+class WalkLayout:
+    """The packed walk layout of a scene (vt_walk_layout): face records in
+    16-byte-aligned chunks of 8 (6 bytes each, no pad half), a link per
+    padded face slot carrying the neighbour's chunk range, and a {site,
+    density} record per cell.  The inference kernels walk it with fewer
+    vector loads per step and render the same images bit for bit.
+
+    ``build`` returns None for a scene beyond the layout's limits (2^24 cells,
+    255 chunks per cell); the renders then walk the reference's arrays.
+    ``source`` (a SourceKey) tells whether the arrays it was built from are
+    still the given tensors, unchanged."""
+
+    MAX_POINTS = 1 << 24
+    MAX_CHUNKS_PER_CELL = 255
+
+    def __init__(self, chunks, links, heads, cells, num_chunks: int, sources=()):
+        self.chunks, self.links, self.heads, self.cells = chunks, links, heads, cells
+        self.num_chunks = int(num_chunks)
+        self.source = SourceKey(*sources)
+        self._c = _WalkLayoutC(chunks.data_ptr(), links.data_ptr(), heads.data_ptr(), cells.data_ptr(),
+                               self.num_chunks)
+
+    @property
+    def ptr(self) -> int:
+        """Address of the vt_walk_layout struct (host memory) for the C ABI."""
+        return C.addressof(self._c)
+
+
+    @classmethod
+    def build(cls, points, density, adjacency, offsets, adj_diff, stream=None) -> Optional["WalkLayout"]:
+        """The layout of a scene (density: f32 per cell, as the renders take
+        it; adj_diff from vt_prefetch_adj), or None beyond the limits.  Reads
+        two counts back to the host to size the arrays."""
+        n = int(points.shape[0])
+        if n >= cls.MAX_POINTS:
+            return None
+        dev = points.device
+        sources = (points, density, adjacency, offsets, adj_diff)
+        density = density.reshape(-1)
+        sp = _s(dev, stream)
+        lib = _lib.load()
+        first = torch.empty(n + 2, dtype=torch.int32, device=dev)
+        ws = torch.empty(max(int(lib.vt_walk_layout_count_workspace_size(n)), 1), dtype=torch.uint8, device=dev)
+        with torch.cuda.device(dev):
+            _lib.call("vt_walk_layout_count", offsets.data_ptr(), n, first.data_ptr(), ws.data_ptr(), sp)
+            torch.cuda.synchronize(dev)
+            total, most = (int(v) & 0xFFFFFFFF for v in first[n:].cpu().tolist())
+        if most > cls.MAX_CHUNKS_PER_CELL or total >= (1 << 29):
+            return None
+        chunks = torch.empty((max(total, 1), 12), dtype=torch.int32, device=dev)
+        links = torch.empty((max(8 * total, 1), 2), dtype=torch.int32, device=dev)
+        heads = torch.empty((max(n, 1), 2), dtype=torch.int32, device=dev)
+        cells = torch.empty((max(n, 1), 4), dtype=torch.float32, device=dev)
+        with torch.cuda.device(dev):
+            _lib.call("vt_walk_layout_fill", points.data_ptr(), density.data_ptr(), adjacency.data_ptr(),
+                      offsets.data_ptr(), n, adj_diff.data_ptr(), first.data_ptr(), total, chunks.data_ptr(),
+                      links.data_ptr(), heads.data_ptr(), cells.data_ptr(), sp)
+        return cls(chunks, links, heads, cells, total, sources)
+
+
+def _walk_ptr(walk: Optional[WalkLayout]):
+    return walk.ptr if walk is not None else None
+
+
 def infer_f16(points, diffuse4, specular4, density, adjacency, offsets, adj_diff, rays, start_point, ray_perm=None,
               weight_threshold=0.001, max_intersections=1024, cell_skip_threshold=0.0, stats=None, out=None,
-              tiled=None, stream=None, schedule: Optional[TileSchedule] = None):
+              tiled=None, stream=None, schedule: Optional[TileSchedule] = None, walk: Optional[WalkLayout] = None):
     """fp16 inference.  ``tiled=(tile_h, tile_w)`` uses the in-kernel wave
     tiling over the images of screen_layout (any (..., H, W, 6) when the
     layout finds none), with ``schedule`` (a TileSchedule of this image
-    shape and stream) the tiles' launch order."""
+    shape and stream) the tiles' launch order and ``walk`` (a WalkLayout of
+    the scene) the packed walk."""
     rd = map_res(diffuse4.shape[-1], 4)
     rs = map_res(specular4.shape[-1], 4)
     nr = rays.numel() // 6
@@ -200,7 +285,8 @@ def infer_f16(points, diffuse4, specular4, density, adjacency, offsets, adj_diff
         _lib.call("vt_trace_infer_f16_tiled", points.data_ptr(), diffuse4.data_ptr(), specular4.data_ptr(), rd, rs,
                   density.data_ptr(), adjacency.data_ptr(), offsets.data_ptr(), points.size(0), adj_diff.data_ptr(),
                   rays.data_ptr(), B, H, W, tiled[0], tiled[1], start_point.data_ptr(), float(weight_threshold),
-                  int(max_intersections), float(cell_skip_threshold), out.data_ptr(), order, cost, _p(stats), sp)
+                  int(max_intersections), float(cell_skip_threshold), out.data_ptr(), order, cost, _p(stats),
+                  _walk_ptr(walk), sp)
     else:
         _lib.call("vt_trace_infer_f16", points.data_ptr(), diffuse4.data_ptr(), specular4.data_ptr(), rd, rs,
                   density.data_ptr(), adjacency.data_ptr(), offsets.data_ptr(), points.size(0), adj_diff.data_ptr(),
