@@ -304,10 +304,14 @@ __device__ __forceinline__ uint32_t exit_face_packed(const uint4 *ch, uint32_t n
                 if (exit_before(num, dp, bnum, bdp)) {
                     bnum = num;
                     bdp = dp;
-                    best = 8 * q + j;
+                    // j - 16 (an inline constant: no move per face), made
+                    // the list index 8q + j after the chunk
+                    best = (uint32_t)(j - 16);
                 }
             }
         }
+        if ((int32_t)best < -8)
+            best += 16 + 8 * q;
     }
     if (best == NONE)
         return NONE;
@@ -372,7 +376,9 @@ __device__ __forceinline__ bool walk_step_packed(PackedWalk &w, f3 o, f3 d, cons
         st.integrate();
         go = integ.integrate(w.cur, w.t0, t1, p, np, st);
     }
-    w.t0 = __builtin_fmaxf(w.t0, t1);
+    // max(t0, t1) as a select: neither is NaN, and fmaxf would add two
+    // canonicalising moves
+    w.t0 = t1 > w.t0 ? t1 : w.t0;
     w.cur = nxt;
     w.nch = lk.x >> WL_ID_BITS;
     w.cb = lk.y;
