@@ -68,10 +68,12 @@ int vt_prefetch_adj(const float *points, uint32_t num_points, const uint32_t *ad
  * Packed walk layout (extension; no counterpart in the reference).  The
  * scene's face records regrouped so that a traversal step issues fewer
  * vector loads, which bound the traversal kernels:
- *   chunks: u32 (num_chunks, 12).  Each cell's face list in chunks of 8
+ *   chunks: u32 (num_chunks + 1, 12).  Each cell's face list in chunks of 8
  *     faces, 24 halves each: x, y, z of the chunk's first face, then of its
  *     second, ... (the adj_diff halves).  A list is padded to a multiple of 8
- *     with zero offsets, never an exit face (n.d = 0).
+ *     with zero offsets, never an exit face (n.d = 0).  The walk loads a
+ *     cell's first chunk before it knows the list is not empty, so the array
+ *     holds one chunk more (any contents).
  *   links: u32 (8 * num_chunks, 2).  Per padded face slot k of cell c, at
  *     8 * first_chunk[c] + k: {neighbour | its chunk count << 24, its first
  *     chunk}.

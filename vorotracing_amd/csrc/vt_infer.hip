@@ -358,7 +358,7 @@ void infer_kernel(InferArgs a, uint32_t total_slots)
         q.sw[2][lane] = sb.w01;
         q.sw[3][lane] = sb.w11;
         if constexpr (PACKED)
-            walk_begin_packed(w, a.wl_heads, a.wl_cells, start);
+            walk_begin_packed(w, a.wl_heads, a.wl_cells, a.wl_chunks, start);
         else
             walk_begin(w, a.points, a.offsets, start);
     }

@@ -241,10 +241,18 @@ struct PackedWalk {
     float dens;
     float t0;
     uint32_t n;
+    uint4 r0; // the first row of its first chunk (faces 0-1), loaded with its site
 };
 
+// The first row of a cell's first chunk (the chunk array holds one chunk
+// past its last, so an empty list reads in bounds too).
+__device__ __forceinline__ void load_first_chunk(PackedWalk &w, const uint4 *chunks)
+{
+    w.r0 = chunks[3 * (size_t)w.cb];
+}
+
 __device__ __forceinline__ void walk_begin_packed(PackedWalk &w, const uint2 *heads, const float4 *cells,
-                                                  uint32_t start)
+                                                  const uint4 *chunks, uint32_t start)
 {
     const uint2 h = heads[start];
     const float4 c = cells[start];
@@ -255,6 +263,7 @@ __device__ __forceinline__ void walk_begin_packed(PackedWalk &w, const uint2 *he
     w.dens = c.w;
     w.t0 = 0.0f;
     w.n = 0;
+    load_first_chunk(w, chunks);
 }
 
 __device__ __forceinline__ uint32_t chunk_word(uint4 r0, uint4 r1, uint4 r2, int k)
@@ -280,73 +289,70 @@ __device__ __forceinline__ void chunk_face(uint4 R0, uint4 R1, uint4 R2, int j, 
     oz = chunk_half(R0, R1, R2, 3 * j + 2);
 }
 
-// exit_face over the nch chunks at ch (3 uint4 rows each): the same choice,
-// ties to the lowest slot, and a slot is the face's index in the cell's list.
-__device__ __forceinline__ uint32_t exit_face_packed(const uint4 *ch, uint32_t nch, f3 p, f3 o, f3 d, float &t1)
+// The faces of one chunk (rows R0-R2, slots 8q..8q+7) against the running
+// best (exit_face's order); an accepted slot is kept as j - 16 (an inline
+// constant, no move per face) and made 8q + j after the chunk.
+__device__ __forceinline__ void search_chunk(uint4 R0, uint4 R1, uint4 R2, uint32_t q, f3 p, f3 o, f3 d,
+                                             float &bnum, float &bdp, uint32_t &best)
 {
-    uint32_t best = NONE;
-    float bnum = FIRST_BNUM, bdp = FIRST_BDP;
-    for (uint32_t q = 0; q < nch; ++q) {
-        const uint4 *c = ch + 3 * q;
-        const uint4 R0 = c[0], R1 = c[1], R2 = c[2];
 #pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        float ox, oy, oz;
+        chunk_face(R0, R1, R2, j, ox, oy, oz);
+        // as in exit_face: keep the widening out of v_fma_mix operands
+        asm("" : "+v"(ox), "+v"(oy), "+v"(oz));
+        float dp = fma_(oz, d.z, fma_(oy, d.y, ox * d.x));
+        if (dp > 0.0f) {
+            float ex = fma_(ox, 0.5f, p.x) - o.x;
+            float ey = fma_(oy, 0.5f, p.y) - o.y;
+            float ez = fma_(oz, 0.5f, p.z) - o.z;
+            float num = fma_(ez, oz, fma_(ey, oy, ex * ox));
+            if (exit_before(num, dp, bnum, bdp)) {
+                bnum = num;
+                bdp = dp;
+                best = (uint32_t)(j - 16);
+            }
+        }
+    }
+    if ((int32_t)best < -8)
+        best += 16 + 8 * q;
+}
+
+// The IEEE redo of exit_face over the nch chunks at ch (a best quotient that
+// rounded to -inf); returns the slot and sets t1.
+__device__ __forceinline__ uint32_t exit_face_packed_ieee(const uint4 *ch, uint32_t nch, f3 p, f3 o, f3 d, float &t1)
+{
+    float bt = __builtin_huge_valf();
+    uint32_t best = NONE;
+    for (uint32_t q = 0; q < nch; ++q) {
+        const uint4 R0 = ch[3 * q], R1 = ch[3 * q + 1], R2 = ch[3 * q + 2];
         for (int j = 0; j < 8; ++j) {
             float ox, oy, oz;
             chunk_face(R0, R1, R2, j, ox, oy, oz);
-            // as in exit_face: keep the widening out of v_fma_mix operands
-            asm("" : "+v"(ox), "+v"(oy), "+v"(oz));
-            float dp = fma_(oz, d.z, fma_(oy, d.y, ox * d.x));
+            const float dp = fma_(oz, d.z, fma_(oy, d.y, ox * d.x));
             if (dp > 0.0f) {
-                float ex = fma_(ox, 0.5f, p.x) - o.x;
-                float ey = fma_(oy, 0.5f, p.y) - o.y;
-                float ez = fma_(oz, 0.5f, p.z) - o.z;
-                float num = fma_(ez, oz, fma_(ey, oy, ex * ox));
-                if (exit_before(num, dp, bnum, bdp)) {
-                    bnum = num;
-                    bdp = dp;
-                    // j - 16 (an inline constant: no move per face), made
-                    // the list index 8q + j after the chunk
-                    best = (uint32_t)(j - 16);
+                const float ex = fma_(ox, 0.5f, p.x) - o.x;
+                const float ey = fma_(oy, 0.5f, p.y) - o.y;
+                const float ez = fma_(oz, 0.5f, p.z) - o.z;
+                const float t = fma_(ez, oz, fma_(ey, oy, ex * ox)) / dp;
+                if (t < bt) {
+                    bt = t;
+                    best = 8 * q + j;
                 }
             }
         }
-        if ((int32_t)best < -8)
-            best += 16 + 8 * q;
     }
-    if (best == NONE)
-        return NONE;
-    t1 = bnum / bdp;
-    if (t1 == -__builtin_huge_valf()) {
-        // the IEEE redo of exit_face
-        float bt = __builtin_huge_valf();
-        best = NONE;
-        for (uint32_t q = 0; q < nch; ++q) {
-            const uint4 R0 = ch[3 * q], R1 = ch[3 * q + 1], R2 = ch[3 * q + 2];
-            for (int j = 0; j < 8; ++j) {
-                float ox, oy, oz;
-                chunk_face(R0, R1, R2, j, ox, oy, oz);
-                const float dp = fma_(oz, d.z, fma_(oy, d.y, ox * d.x));
-                if (dp > 0.0f) {
-                    const float ex = fma_(ox, 0.5f, p.x) - o.x;
-                    const float ey = fma_(oy, 0.5f, p.y) - o.y;
-                    const float ez = fma_(oz, 0.5f, p.z) - o.z;
-                    const float t = fma_(ez, oz, fma_(ey, oy, ex * ox)) / dp;
-                    if (t < bt) {
-                        bt = t;
-                        best = 8 * q + j;
-                    }
-                }
-            }
-        }
-        t1 = bt;
-    }
+    t1 = bt;
     return best;
 }
 
-// walk_step over the packed layout.  The integrator takes the cell's density
-// from the walk state (begin_cell_value) instead of loading it.  Statistics
-// that record face counts read them from offsets; otherwise a visit counts
-// the cell's padded slots.
+// walk_step over the packed layout, with the loads of the next cell moved
+// ahead: the exit face's link is loaded before the exit distance is divided
+// out, and the next cell's site, density and first chunk as soon as the link
+// arrives, so that their latency overlaps the integrator's work.  The
+// integrator takes the density from the walk state (begin_cell_value).
+// Statistics that record face counts read them from offsets; otherwise a
+// visit counts the cell's padded slots.
 template <class Integrator, class StatsT>
 __device__ __forceinline__ bool walk_step_packed(PackedWalk &w, f3 o, f3 d, const uint4 *chunks, const uint2 *links,
                                                  const float4 *cells, const uint32_t *offsets, uint32_t max_steps,
@@ -361,28 +367,40 @@ __device__ __forceinline__ bool walk_step_packed(PackedWalk &w, f3 o, f3 d, cons
         st.visit(w.cur, offsets[w.cur + 1] - offsets[w.cur]);
     else
         st.visit(w.cur, 8 * w.nch);
-    float t1;
-    const uint32_t best = exit_face_packed(chunks + 3 * (size_t)w.cb, w.nch, p, o, d, t1);
+    const uint4 *ch = chunks + 3 * (size_t)w.cb;
+    uint32_t best = NONE;
+    float bnum = FIRST_BNUM, bdp = FIRST_BDP;
+    if (w.nch > 0)
+        search_chunk(w.r0, ch[1], ch[2], 0, p, o, d, bnum, bdp, best);
+    for (uint32_t q = 1; q < w.nch; ++q) {
+        const uint4 *c = ch + 3 * q;
+        search_chunk(c[0], c[1], c[2], q, p, o, d, bnum, bdp, best);
+    }
     if (best == NONE)
         return false;
     st.exit();
-    const uint2 lk = links[8 * (size_t)w.cb + best];
-    const uint32_t nxt = lk.x & WL_ID_MASK;
-    const float4 c = cells[nxt];
-    const f3 np = mk(c.x, c.y, c.z);
+    uint2 lk = links[8 * (size_t)w.cb + best];
+    float t1 = bnum / bdp;
+    if (t1 == -__builtin_huge_valf()) {
+        best = exit_face_packed_ieee(ch, w.nch, p, o, d, t1);
+        lk = links[8 * (size_t)w.cb + best];
+    }
+    const uint32_t cur = w.cur;
+    w.cur = lk.x & WL_ID_MASK;
+    w.nch = lk.x >> WL_ID_BITS;
+    w.cb = lk.y;
+    const float4 c = cells[w.cur];
+    load_first_chunk(w, chunks);
     // no early return inside the integrate branch (see walk_step)
     bool go = true;
     if (t1 > w.t0) {
         st.integrate();
-        go = integ.integrate(w.cur, w.t0, t1, p, np, st);
+        go = integ.integrate(cur, w.t0, t1, p, mk(c.x, c.y, c.z), st);
     }
     // max(t0, t1) as a select: neither is NaN, and fmaxf would add two
     // canonicalising moves
     w.t0 = t1 > w.t0 ? t1 : w.t0;
-    w.cur = nxt;
-    w.nch = lk.x >> WL_ID_BITS;
-    w.cb = lk.y;
-    w.p = np;
+    w.p = mk(c.x, c.y, c.z);
     w.dens = c.w;
     return go;
 }

@@ -249,7 +249,8 @@ class WalkLayout:
             total, most = (int(v) & 0xFFFFFFFF for v in first[n:].cpu().tolist())
         if most > cls.MAX_CHUNKS_PER_CELL or total >= (1 << 29):
             return None
-        chunks = torch.empty((max(total, 1), 12), dtype=torch.int32, device=dev)
+        # one chunk past the last: the walk loads a cell's first chunk before it knows the list is not empty
+        chunks = torch.zeros((total + 1, 12), dtype=torch.int32, device=dev)
         links = torch.empty((max(8 * total, 1), 2), dtype=torch.int32, device=dev)
         heads = torch.empty((max(n, 1), 2), dtype=torch.int32, device=dev)
         cells = torch.empty((max(n, 1), 4), dtype=torch.float32, device=dev)
