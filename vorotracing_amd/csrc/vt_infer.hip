@@ -370,8 +370,9 @@ void infer_kernel(InferArgs a, uint32_t total_slots)
     while (__ballot(active)) {
         if (active) {
             if constexpr (PACKED)
-                active = walk_step_packed(w, integ.o, integ.d, a.wl_chunks, a.wl_links, a.wl_cells, a.offsets,
-                                          a.max_steps, integ, st);
+                // the q8 integrator leaves no register room for the preloaded row
+                active = walk_step_packed<!Q8>(w, integ.o, integ.d, a.wl_chunks, a.wl_links, a.wl_cells,
+                                               a.offsets, a.max_steps, integ, st);
             else
                 active = walk_step<CHUNK>(w, integ.o, integ.d, a.points, a.adjacency, a.offsets, a.adj_diff,
                                           a.max_steps, integ, st);

@@ -348,12 +348,14 @@ __device__ __forceinline__ uint32_t exit_face_packed_ieee(const uint4 *ch, uint3
 
 // walk_step over the packed layout, with the loads of the next cell moved
 // ahead: the exit face's link is loaded before the exit distance is divided
-// out, and the next cell's site, density and first chunk as soon as the link
-// arrives, so that their latency overlaps the integrator's work.  The
+// out, and the next cell's site, density and (PRELOAD) the first row of its
+// first chunk as soon as the link arrives, so that their latency overlaps the
+// integrator's work.  Without PRELOAD that row is loaded with the rest of the
+// chunk (for integrators with too little register room to hold it).  The
 // integrator takes the density from the walk state (begin_cell_value).
 // Statistics that record face counts read them from offsets; otherwise a
 // visit counts the cell's padded slots.
-template <class Integrator, class StatsT>
+template <bool PRELOAD, class Integrator, class StatsT>
 __device__ __forceinline__ bool walk_step_packed(PackedWalk &w, f3 o, f3 d, const uint4 *chunks, const uint2 *links,
                                                  const float4 *cells, const uint32_t *offsets, uint32_t max_steps,
                                                  Integrator &integ, StatsT &st)
@@ -371,7 +373,7 @@ __device__ __forceinline__ bool walk_step_packed(PackedWalk &w, f3 o, f3 d, cons
     uint32_t best = NONE;
     float bnum = FIRST_BNUM, bdp = FIRST_BDP;
     if (w.nch > 0)
-        search_chunk(w.r0, ch[1], ch[2], 0, p, o, d, bnum, bdp, best);
+        search_chunk(PRELOAD ? w.r0 : ch[0], ch[1], ch[2], 0, p, o, d, bnum, bdp, best);
     for (uint32_t q = 1; q < w.nch; ++q) {
         const uint4 *c = ch + 3 * q;
         search_chunk(c[0], c[1], c[2], q, p, o, d, bnum, bdp, best);
@@ -390,7 +392,8 @@ __device__ __forceinline__ bool walk_step_packed(PackedWalk &w, f3 o, f3 d, cons
     w.nch = lk.x >> WL_ID_BITS;
     w.cb = lk.y;
     const float4 c = cells[w.cur];
-    load_first_chunk(w, chunks);
+    if constexpr (PRELOAD)
+        load_first_chunk(w, chunks);
     // no early return inside the integrate branch (see walk_step)
     bool go = true;
     if (t1 > w.t0) {

@@ -118,7 +118,13 @@ class TileSchedule:
     A different frame launches in screen order: the costs of the previous
     view mispredict a moved camera's (a 32-pose orbit ran 10 % slower with
     them).  Images are bit-identical in any order.  One schedule per stream:
-    a launch reads the costs the previous launch on its stream wrote."""
+    a launch reads the costs the previous launch on its stream wrote.
+
+    The walk is deterministic, so every render of unchanged rays records the
+    same costs and their sort gives the same order: without a split
+    (``split_waves`` 0, the inference entries) the order sorted for a frame
+    is kept for its further renders instead of being sorted again.  Each
+    render still records its costs."""
 
     def __init__(self, tiles: int, device, split_waves: int = 0):
         self.tiles = int(tiles)
@@ -131,6 +137,7 @@ class TileSchedule:
         self.ws = torch.empty(int(_lib.load().vt_tile_order_workspace_size(self.tiles)), dtype=torch.uint8,
                               device=device)
         self.frame = None  # the frame whose costs self.cost holds
+        self.sorted = None  # the frame self.order was sorted for (split_waves 0)
 
     def _sort(self, stream: int, split_waves: int):
         _lib.call("vt_tile_order", self.cost.data_ptr(), self.tiles, split_waves, self.order.data_ptr(),
@@ -146,9 +153,14 @@ class TileSchedule:
         here after the sort has read them."""
         order = None
         if frame is not None and frame == self.frame:
-            order = self._sort(stream, split_waves)
             if split_waves:
+                order = self._sort(stream, split_waves)
                 self.cost.zero_()
+            elif frame == self.sorted:
+                order = self.order.data_ptr()
+            else:
+                order = self._sort(stream, 0)
+                self.sorted = frame
         self.frame = frame
         return order, self.cost.data_ptr()
 
@@ -158,6 +170,7 @@ class TileSchedule:
         None when the costs are of another frame."""
         if frame is None or frame != self.frame:
             return None
+        self.sorted = None
         return self._sort(stream, self.split_waves)
 
 
