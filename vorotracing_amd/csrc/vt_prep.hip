@@ -698,15 +698,17 @@ __global__ void wl_init_kernel(uint32_t *first_chunk, uint32_t n)
 __global__ void wl_count_kernel(const uint32_t *offsets, uint32_t n, uint32_t *first_chunk)
 {
     const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c > n)
-        return;
-    if (c == n) {
+    uint32_t k = 0;
+    if (c < n) {
+        k = (uint32_t)(((uint64_t)offsets[c + 1] - offsets[c] + 7u) >> 3);
+        first_chunk[c] = k;
+    } else if (c == n) {
         first_chunk[n] = 0;
-        return;
     }
-    const uint32_t k = (uint32_t)(((uint64_t)offsets[c + 1] - offsets[c] + 7u) >> 3);
-    first_chunk[c] = k;
-    atomicMax(first_chunk + n + 1, k);
+    // one atomic per wave for the largest count
+    k = wave_max_u32(k);
+    if ((threadIdx.x & 63u) == 0 && k)
+        atomicMax(first_chunk + n + 1, k);
 }
 
 // One lane per cell: its cell record, its head, and its chunks and links.
