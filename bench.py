@@ -261,7 +261,7 @@ def main():
     t_start = time.perf_counter()
     for i in range(K):
         rays = poses[i % args.poses]
-        sp = inf.get_starting_point(rays)
+        sp = inf.start_cells(rays)
         ev[i][0].record(stream)
         frames.append(inf.render(rays, start_point=sp, **kw))
         ev[i][1].record(stream)

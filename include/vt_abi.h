@@ -137,7 +137,10 @@ int vt_trace_infer_f16(const float *points, const uint16_t *diffuse, const uint1
  * tile_order: NULL (tiles in screen order) or the launch order of the
  * ceil(W/tile_w) * ceil(H/tile_h) * num_images tiles (vt_tile_order);
  * tile_cost: NULL or one u32 per tile, written with each tile's cost for
- * vt_tile_order (both extensions).  walk: NULL, or the scene's packed walk
+ * vt_tile_order (both extensions).  rays_per_start: 0 when start_point holds
+ * one cell per ray, else the number of consecutive rays that share one start
+ * cell (ray r starts at start_point[r / rays_per_start]; H * W for one cell
+ * per pinhole image; extension).  walk: NULL, or the scene's packed walk
  * layout (vt_walk_layout; extension), which the kernel then walks in place of
  * adjacency / adj_diff (same results; offsets still serve stats).
  */
@@ -145,7 +148,8 @@ int vt_trace_infer_f16_tiled(const float *points, const uint16_t *diffuse, const
                              uint32_t diff_res, uint32_t spec_res, const float *density, const uint32_t *adjacency,
                              const uint32_t *offsets, uint32_t num_points, const uint16_t *adj_diff,
                              const float *rays, uint32_t num_images, uint32_t image_h, uint32_t image_w,
-                             uint32_t tile_h, uint32_t tile_w, const uint32_t *start_point, float weight_threshold,
+                             uint32_t tile_h, uint32_t tile_w, const uint32_t *start_point, uint32_t rays_per_start,
+                             float weight_threshold,
                              uint32_t max_intersections, float cell_skip_threshold, uint16_t *rgba,
                              const uint32_t *tile_order, uint32_t *tile_cost, vt_ray_stats *stats,
                              const vt_walk_layout *walk, vt_stream_t stream);
@@ -176,7 +180,8 @@ int vt_trace_infer_q8_tiled(const float *points, const uint8_t *diffuse, const u
                             const uint32_t *adjacency, const uint32_t *offsets, uint32_t num_points,
                             const uint16_t *adj_diff, const float *rays, uint32_t num_images, uint32_t image_h,
                             uint32_t image_w, uint32_t tile_h, uint32_t tile_w, const uint32_t *start_point,
-                            float weight_threshold, uint32_t max_intersections, float cell_skip_threshold,
+                            uint32_t rays_per_start, float weight_threshold, uint32_t max_intersections,
+                            float cell_skip_threshold,
                             uint16_t *rgba, const uint32_t *tile_order, uint32_t *tile_cost, vt_ray_stats *stats,
                             const vt_walk_layout *walk, vt_stream_t stream);
 

@@ -67,7 +67,7 @@ def test_host_only_entries():
 def test_argument_errors_need_no_gpu():
     """Null pointers and bad sizes are rejected on the host, with a message."""
     lib = _lib.load()
-    rc = lib.vt_trace_infer_f16_tiled(None, None, None, 4, 4, None, None, None, 10, None, None, 1, 8, 8, 8, 8, None,
+    rc = lib.vt_trace_infer_f16_tiled(None, None, None, 4, 4, None, None, None, 10, None, None, 1, 8, 8, 8, 8, None, 0,
                                       0.01, 1024, 0.0, None, None, None, None, None, None)
     assert rc == 1
     assert b"null pointer" in lib.vt_last_error()

@@ -143,3 +143,33 @@ def test_packed_walk_q8_drop_in(gpu):
         assert torch.equal(packed.view(torch.int16), general.view(torch.int16))
     finally:
         _C.DROP_IN_WALK = True
+
+
+@pytest.mark.parametrize("quantize", ["fp16", "q8"])
+def test_render_start_cell_forms(gpu, quantize):
+    """render() with start cells given per ray, per camera ((B, 1, 1)), as one
+    cell for all rays, or not given: the tiled kernels read a per-camera array
+    through rays_per_start, and every form renders the same image bit for bit
+    (one camera, and a batch of two cameras)."""
+    from vorotracing_amd.infer import VoroTracingInfer
+    from vorotracing_amd.model import VoroTracing
+    s = H.mini_heightfield()
+    inf = VoroTracingInfer(VoroTracing.from_scene(s, device=gpu), sort_morton=True, quantize=quantize)
+    kw = dict(weight_threshold=0.01, cell_skip_threshold=1e-3)
+    one = H.to_dev(camera.orbit_rays(2, 96, 72), gpu)
+    two = torch.stack([one, H.to_dev(camera.orbit_rays(11, 96, 72), gpu)])
+    for rays in (one, two):
+        print(f"case: {quantize} start cell forms, rays {tuple(rays.shape)}", flush=True)
+        per_ray = inf.get_starting_point(rays)
+        cells = inf.start_cells(rays)
+        assert cells.numel() == (rays.shape[0] if rays.dim() == 4 else 1)
+        assert inf._rays_per_start(rays, cells) > 0
+        outs = [inf.render(rays, **kw), inf.render(rays, start_point=per_ray, **kw),
+                inf.render(rays, start_point=cells, **kw)]
+        if rays.dim() == 3:
+            outs.append(inf.render(rays, start_point=cells.reshape(1), **kw))
+        # the same cells through the general path (no lane order): the reference's per-ray form
+        outs.append(inf.render(rays, start_point=per_ray, use_warp_perm=False, **kw))
+        torch.cuda.synchronize()
+        for o in outs[1:]:
+            assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16))

@@ -277,7 +277,7 @@ def trace_vorotracing_infer(points_in, diffuse_in, specular_in, density_in, poin
             _lib.call("vt_trace_infer_f16_tiled", points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd,
                       rs, density.data_ptr(), adjacency.data_ptr(), offsets.data_ptr(), num_points,
                       adjacent_diff.data_ptr(), rays.data_ptr(), lay[0], lay[1], lay[2], native.IMAGE_MIN,
-                      native.IMAGE_MIN, start_point.data_ptr(), float(weight_threshold), int(max_intersections),
+                      native.IMAGE_MIN, start_point.data_ptr(), 0, float(weight_threshold), int(max_intersections),
                       float(cell_skip_threshold), out.data_ptr(), order, cost, None,
                       native._walk_ptr(_drop_in_walk(
                           (points_in, density_in, point_adjacency_in, point_adjacency_offsets_in, adjacent_diff_in),
@@ -362,7 +362,7 @@ def trace_vorotracing_infer_q8(points_in, diffuse_in, specular_in, density_in, p
             _lib.call("vt_trace_infer_q8_tiled", points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd, rs,
                       *scales, density.data_ptr(), adjacency.data_ptr(), offsets.data_ptr(), num_points,
                       adjacent_diff.data_ptr(), rays.data_ptr(), lay[0], lay[1], lay[2], native.IMAGE_MIN,
-                      native.IMAGE_MIN, start_point.data_ptr(), float(weight_threshold), int(max_intersections),
+                      native.IMAGE_MIN, start_point.data_ptr(), 0, float(weight_threshold), int(max_intersections),
                       float(cell_skip_threshold), out.data_ptr(), order, cost, None,
                       native._walk_ptr(_drop_in_walk(
                           (points_in, density_in, point_adjacency_in, point_adjacency_offsets_in, adjacent_diff_in),

@@ -385,6 +385,7 @@ constexpr uint64_t NN_SCAN_PAIRS = 1ull << 26;
 constexpr uint32_t NN_SCAN_MAX_QUERIES = 64;
 constexpr int NN_SCAN_BLOCK = 256;
 constexpr uint32_t NN_SCAN_BLOCKS = 1024; // per query
+constexpr uint32_t NN_SCAN_UNROLL = 4;    // sites per lane and pass of nn_scan_kernel
 
 __device__ __forceinline__ bool nn_better(float d, uint32_t i, float bd, uint32_t bi)
 {
@@ -403,12 +404,24 @@ __global__ __launch_bounds__(NN_SCAN_BLOCK) void nn_scan_kernel(const float *__r
     const f3 q = load_site(queries, qi);
     float best = __builtin_huge_valf();
     uint32_t bi = NONE;
-    for (uint32_t i = blockIdx.x * NN_SCAN_BLOCK + threadIdx.x; i < n; i += NN_SCAN_BLOCKS * NN_SCAN_BLOCK) {
-        const f3 df = sub(q, load_site(points, i));
-        const float d2 = dot(df, df);
-        if (d2 < best) { // i increases along the stride, so ties keep the lower index
-            best = d2;
-            bi = i;
+    // NN_SCAN_UNROLL sites per pass, their loads issued together
+    constexpr uint32_t stride = NN_SCAN_BLOCKS * NN_SCAN_BLOCK;
+    for (uint32_t i0 = blockIdx.x * NN_SCAN_BLOCK + threadIdx.x; i0 < n; i0 += NN_SCAN_UNROLL * stride) {
+        f3 site[NN_SCAN_UNROLL];
+#pragma unroll
+        for (uint32_t u = 0; u < NN_SCAN_UNROLL; ++u) {
+            const uint32_t i = i0 + u * stride;
+            site[u] = load_site(points, i < n ? i : i0);
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < NN_SCAN_UNROLL; ++u) {
+            const uint32_t i = i0 + u * stride;
+            const f3 df = sub(q, site[u]);
+            const float d2 = dot(df, df);
+            if (i < n && d2 < best) { // i increases along the stride, so ties keep the lower index
+                best = d2;
+                bi = i;
+            }
         }
     }
     for (int o = 32; o >= 1; o >>= 1) {
@@ -441,8 +454,11 @@ __global__ __launch_bounds__(64) void nn_pick_kernel(const uint2 *__restrict__ p
     const uint32_t qi = blockIdx.x;
     float best = __builtin_huge_valf();
     uint32_t bi = NONE;
-    for (uint32_t k = threadIdx.x; k < NN_SCAN_BLOCKS; k += 64) {
-        const uint2 p = partial[(size_t)qi * NN_SCAN_BLOCKS + k];
+    // the partials' loads issued together (a loop of dependent round trips took 7 us)
+    static_assert(NN_SCAN_BLOCKS % 64 == 0, "partials per lane");
+#pragma unroll
+    for (uint32_t j = 0; j < NN_SCAN_BLOCKS / 64; ++j) {
+        const uint2 p = partial[(size_t)qi * NN_SCAN_BLOCKS + threadIdx.x + 64 * j];
         if (nn_better(bits_f(p.x), p.y, best, bi)) {
             best = bits_f(p.x);
             bi = p.y;

@@ -269,6 +269,8 @@ struct InferArgs {
     const uint2 *wl_links;
     const uint2 *wl_heads;
     const float4 *wl_cells;
+    // rays per start cell (0: one start cell per ray)
+    uint32_t rays_per_start;
 };
 
 // MAP_CAMERA: tiled lanes whose rays come from cameras instead of a buffer.
@@ -347,7 +349,7 @@ void infer_kernel(InferArgs a, uint32_t total_slots)
             start = a.start_point[a.start_rows ? img * a.H + v : img];
         } else {
             load_ray(a.rays, r, integ.o, integ.d);
-            start = a.start_point[r];
+            start = a.start_point[a.rays_per_start ? r / a.rays_per_start : r];
         }
         float su, sv;
         oct_encode<RS>(mk(-integ.d.x, -integ.d.y, -integ.d.z), su, sv);
@@ -514,7 +516,8 @@ extern "C" int vt_trace_infer_f16_tiled(const float *points, const uint16_t *dif
                                         const uint32_t *adjacency, const uint32_t *offsets, uint32_t num_points,
                                         const uint16_t *adj_diff, const float *rays, uint32_t num_images,
                                         uint32_t image_h, uint32_t image_w, uint32_t tile_h, uint32_t tile_w,
-                                        const uint32_t *start_point, float weight_threshold,
+                                        const uint32_t *start_point, uint32_t rays_per_start,
+                                        float weight_threshold,
                                         uint32_t max_intersections, float cell_skip_threshold, uint16_t *rgba,
                                         const uint32_t *tile_order, uint32_t *tile_cost,
                                         vt_ray_stats *stats, const vt_walk_layout *walk, vt_stream_t stream)
@@ -542,6 +545,7 @@ extern "C" int vt_trace_infer_f16_tiled(const float *points, const uint16_t *dif
     a.rays = rays;
     a.num_rays = num_images * image_h * image_w;
     a.start_point = start_point;
+    a.rays_per_start = rays_per_start;
     a.ray_perm = nullptr;
     a.thr = weight_threshold;
     a.skip = cell_skip_threshold;
@@ -612,7 +616,7 @@ extern "C" int vt_trace_infer_q8_tiled(const float *points, const uint8_t *diffu
                                        const uint32_t *offsets, uint32_t num_points, const uint16_t *adj_diff,
                                        const float *rays, uint32_t num_images, uint32_t image_h, uint32_t image_w,
                                        uint32_t tile_h, uint32_t tile_w, const uint32_t *start_point,
-                                       float weight_threshold, uint32_t max_intersections, float cell_skip_threshold,
+                                       uint32_t rays_per_start, float weight_threshold, uint32_t max_intersections, float cell_skip_threshold,
                                        uint16_t *rgba, const uint32_t *tile_order, uint32_t *tile_cost,
                                        vt_ray_stats *stats, const vt_walk_layout *walk, vt_stream_t stream)
 {
@@ -640,6 +644,7 @@ extern "C" int vt_trace_infer_q8_tiled(const float *points, const uint8_t *diffu
     a.rays = rays;
     a.num_rays = num_images * image_h * image_w;
     a.start_point = start_point;
+    a.rays_per_start = rays_per_start;
     a.thr = weight_threshold;
     a.skip = cell_skip_threshold;
     a.max_steps = max_intersections;

@@ -207,12 +207,47 @@ class VoroTracingInfer:
         of a camera's first ray is every ray's origin for a pinhole image (the
         reference queries the batch's first ray only, vorotracing.py:585-604).
         An image batch (B, H, W, 6) is B cameras, any other shape one."""
+        return self.start_cells(rays).expand(rays.shape[:-1]).contiguous()
+
+    def start_cells(self, rays):
+        """get_starting_point's cells, one per camera, shaped to broadcast
+        over the rays' leading dimensions ((B, 1, 1) or all ones): the form
+        ``render`` passes to the tiled kernels without expanding it."""
         lead = rays.shape[:-1]
         cams = lead[0] if rays.dim() == 4 else 1
         first = rays.reshape(cams, -1, 6)[:, 0, :3].contiguous()
         cells = self.bvh.query(self.primal_points, first).view(torch.uint32)
-        spread = (cams,) + (1,) * (len(lead) - 1) if rays.dim() == 4 else (1,) * len(lead)
-        return cells.reshape(spread).expand(lead).contiguous()
+        return cells.reshape((cams,) + (1,) * (len(lead) - 1) if rays.dim() == 4 else (1,) * len(lead))
+
+    @staticmethod
+    def _rays_per_start(rays, start_point) -> int:
+        """For the tiled kernels: the rays that share one entry of a
+        broadcastable ``start_point`` when it holds one cell for all rays or
+        one per image of the batch (ray r then starts at r // this); 0 when it
+        must be expanded to one cell per ray."""
+        lead = tuple(rays.shape[:-1])
+        shape = (1,) * (len(lead) - start_point.dim()) + tuple(start_point.shape)
+        if len(shape) != len(lead):
+            return 0
+        B, H, W = native.image_dims(rays)
+        if all(x == 1 for x in shape):
+            return B * H * W
+        if len(lead) == 3 and shape == (lead[0], 1, 1) and B == lead[0]:
+            return H * W
+        return 0
+
+    def _render_start(self, rays, start_point, image: bool):
+        """(start cells, rays per start cell) of a render: for the tiled
+        kernels a per-camera (or single) cell array as is, with the rays that
+        share each cell; otherwise one cell per ray and 0."""
+        if start_point is None:
+            start_point = self.start_cells(rays)
+        else:
+            start_point = torch.as_tensor(start_point, device=rays.device)
+        k = self._rays_per_start(rays, start_point) if image else 0
+        if k:
+            return start_point.reshape(-1).contiguous(), k
+        return torch.broadcast_to(start_point, rays.shape[:-1]).contiguous(), 0
 
     def render_frames(self, frames, in_flight: int = 2, **render_kw):
         """``render`` of a sequence of frames (each a rays tensor as ``render``
@@ -266,11 +301,8 @@ class VoroTracingInfer:
     def render(self, rays, start_point=None, weight_threshold=0.001, max_intersections=1024,
                cell_skip_threshold=0.0, use_warp_perm: bool = True, stats: Optional[torch.Tensor] = None):
         """vorotracing.py:627-683.  Returns f16 [..., 4]."""
-        if start_point is None:
-            start_point = self.get_starting_point(rays)
-        else:
-            start_point = torch.broadcast_to(start_point, rays.shape[:-1]).contiguous()
         image = use_warp_perm and rays.shape[-1] == 6 and native.screen_layout(rays.shape[:-1]) is not None
+        start_point, rays_per_start = self._render_start(rays, start_point, image)
         if self.quantize == "q8":
             if not image and stats is None:
                 return ops.trace_octmap_infer_q8(
@@ -279,7 +311,7 @@ class VoroTracingInfer:
                     self.diff_offset, self.spec_scale, self.spec_offset, weight_threshold, max_intersections,
                     cell_skip_threshold)
             return self._render_q8_native(rays, start_point, weight_threshold, max_intersections,
-                                          cell_skip_threshold, image, stats)
+                                          cell_skip_threshold, image, stats, rays_per_start)
         if not image and stats is None:
             empty = torch.empty(0, dtype=torch.int32, device=self.device)
             return ops.trace_octmap_infer(self.primal_points, self.diffuse_fp16, self.specular_fp16, self.density,
@@ -287,14 +319,14 @@ class VoroTracingInfer:
                                           self.adjacent_diff, empty, weight_threshold, max_intersections,
                                           cell_skip_threshold)
         rays = rays.contiguous()
-        _check_render_args(self, rays, start_point, self.diffuse_fp16)
+        _check_render_args(self, rays, start_point, self.diffuse_fp16, rays_per_start)
         return native.infer_f16(self.primal_points, self.diffuse_fp16, self.specular_fp16, self.density.reshape(-1),
                                 self.point_adjacency, self.point_adjacency_offsets, self.adjacent_diff, rays,
                                 start_point, weight_threshold=weight_threshold, max_intersections=max_intersections,
                                 cell_skip_threshold=cell_skip_threshold, stats=stats,
                                 tiled=self.TILE if image else None,
                                 schedule=self._schedule(*native.image_dims(rays)) if image else None,
-                                walk=self.walk_layout() if image else None)
+                                walk=self.walk_layout() if image else None, rays_per_start=rays_per_start)
 
     def camera_start_points(self, cameras, camera_buffer=None):
         """Start cells of a camera batch: one LBVH query on each camera's centre, or
@@ -355,11 +387,11 @@ class VoroTracingInfer:
                       self.TILE[0], self.TILE[1], start_point.data_ptr(), int(per_row), *common)
         return out
 
-    def _render_q8_native(self, rays, start_point, thr, max_int, skip, image, stats):
+    def _render_q8_native(self, rays, start_point, thr, max_int, skip, image, stats, rays_per_start=0):
         import ctypes as C
 
         rays = rays.contiguous()
-        _check_render_args(self, rays, start_point, self.diffuse_q8)
+        _check_render_args(self, rays, start_point, self.diffuse_q8, rays_per_start)
 
         def v3(x):
             vals = [float(x)] * 3 if isinstance(x, (int, float)) else [float(v) for v in x]
@@ -379,8 +411,9 @@ class VoroTracingInfer:
                       self.specular_q8.data_ptr(), rd, rs, *keep, self.density.data_ptr(),
                       self.point_adjacency.data_ptr(), self.point_adjacency_offsets.data_ptr(),
                       self.primal_points.shape[0], self.adjacent_diff.data_ptr(), rays.data_ptr(), B, H, W,
-                      self.TILE[0], self.TILE[1], start_point.data_ptr(), float(thr), int(max_int), float(skip),
-                      out.data_ptr(), order, cost, native._p(stats), native._walk_ptr(self.walk_layout()), sp)
+                      self.TILE[0], self.TILE[1], start_point.data_ptr(), int(rays_per_start), float(thr),
+                      int(max_int), float(skip), out.data_ptr(), order, cost, native._p(stats),
+                      native._walk_ptr(self.walk_layout()), sp)
         else:
             _lib.call("vt_trace_infer_q8", self.primal_points.data_ptr(), self.diffuse_q8.data_ptr(),
                       self.specular_q8.data_ptr(), rd, rs, *keep, self.density.data_ptr(),
@@ -391,10 +424,12 @@ class VoroTracingInfer:
         return out
 
 
-def _check_render_args(inf, rays, start_point, diffuse):
-    """Shape/dtype checks of the native render paths (same rules as _C)."""
+def _check_render_args(inf, rays, start_point, diffuse, rays_per_start=0):
+    """Shape/dtype checks of the native render paths (same rules as _C).
+    With rays_per_start, start_point holds one cell per that many rays."""
     _C.validate_scene_data(inf.primal_points, diffuse, inf.point_adjacency, inf.point_adjacency_offsets)
     if rays.dtype != torch.float32 or rays.shape[-1] != 6:
         raise RuntimeError("rays must have float32 dtype and 6 as the last dimension")
-    if start_point.dtype != torch.uint32 or start_point.numel() != rays.numel() // 6:
+    want = rays.numel() // 6 // rays_per_start if rays_per_start else rays.numel() // 6
+    if start_point.dtype != torch.uint32 or start_point.numel() != want:
         raise RuntimeError("start_point must have uint32 dtype and the same batch size as rays")

@@ -280,12 +280,14 @@ def _walk_ptr(walk: Optional[WalkLayout]):
 
 def infer_f16(points, diffuse4, specular4, density, adjacency, offsets, adj_diff, rays, start_point, ray_perm=None,
               weight_threshold=0.001, max_intersections=1024, cell_skip_threshold=0.0, stats=None, out=None,
-              tiled=None, stream=None, schedule: Optional[TileSchedule] = None, walk: Optional[WalkLayout] = None):
+              tiled=None, stream=None, schedule: Optional[TileSchedule] = None, walk: Optional[WalkLayout] = None,
+              rays_per_start: int = 0):
     """fp16 inference.  ``tiled=(tile_h, tile_w)`` uses the in-kernel wave
     tiling over the images of screen_layout (any (..., H, W, 6) when the
     layout finds none), with ``schedule`` (a TileSchedule of this image
-    shape and stream) the tiles' launch order and ``walk`` (a WalkLayout of
-    the scene) the packed walk."""
+    shape and stream) the tiles' launch order, ``walk`` (a WalkLayout of
+    the scene) the packed walk, and ``rays_per_start`` the rays that share
+    each entry of ``start_point`` (0: one per ray)."""
     rd = map_res(diffuse4.shape[-1], 4)
     rs = map_res(specular4.shape[-1], 4)
     nr = rays.numel() // 6
@@ -298,7 +300,8 @@ def infer_f16(points, diffuse4, specular4, density, adjacency, offsets, adj_diff
         order, cost = schedule.launch_args(sp, frame_key(rays)) if schedule is not None else (None, None)
         _lib.call("vt_trace_infer_f16_tiled", points.data_ptr(), diffuse4.data_ptr(), specular4.data_ptr(), rd, rs,
                   density.data_ptr(), adjacency.data_ptr(), offsets.data_ptr(), points.size(0), adj_diff.data_ptr(),
-                  rays.data_ptr(), B, H, W, tiled[0], tiled[1], start_point.data_ptr(), float(weight_threshold),
+                  rays.data_ptr(), B, H, W, tiled[0], tiled[1], start_point.data_ptr(), int(rays_per_start),
+                  float(weight_threshold),
                   int(max_intersections), float(cell_skip_threshold), out.data_ptr(), order, cost, _p(stats),
                   _walk_ptr(walk), sp)
     else:
