@@ -458,9 +458,10 @@ int vt_tile_perm(uint32_t height, uint32_t width, uint32_t tile_h, uint32_t tile
  * tile_cost (u32, one per tile) is what such a call wrote to its tile_cost
  * argument: 18 x the longest walk's steps + the most face records searched by
  * one ray of the tile.  tile_order (u32, tiles + 1 words) receives the tiles
- * by decreasing cost bucket (4 buckets per octave of the cost: floor(log2 c)
- * and the next two bits of c, cost 0 counted as 1), tiles of one bucket in
- * screen order, which keeps neighbouring tiles together; a call given it
+ * by decreasing cost bucket (8 buckets per octave of the cost over
+ * [16, 2^20): floor(log2 c) and the next three bits of c; costs below 16 in
+ * the last bucket, from 2^20 in the first), tiles of one bucket in screen
+ * order, which keeps neighbouring tiles together; a call given it
  * launches tile tile_order[s] in slot s.  Launched longest first, a frame no
  * longer ends with a few long tiles running on an otherwise idle GPU.  Any
  * order gives bit-identical images (a ray's result does not depend on its

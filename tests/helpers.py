@@ -60,12 +60,14 @@ def stats_np(t: torch.Tensor):
 
 
 def tile_order_keys(cost):
-    """Ascending sort key of the tile launch order: 4 buckets per octave of the
-    tile cost (cost 0 counts as 1), costliest bucket first."""
+    """Ascending sort key of the tile launch order: 8 buckets per octave of the
+    tile cost over [16, 2^20) (below: the last bucket, above: the first),
+    costliest bucket first."""
     c = np.maximum(np.asarray(cost, dtype=np.int64), 1)
     lb = np.frexp(c.astype(np.float64))[1].astype(np.int64) - 1  # floor(log2 c), exact below 2**53
-    frac = np.where(lb >= 2, c >> np.maximum(lb - 2, 0), c << np.maximum(2 - lb, 0)) & 3
-    return 127 - (4 * lb + frac)
+    frac = (c >> np.maximum(lb - 3, 0)) & 7
+    key = 127 - (((lb - 4) << 3) | frac)
+    return np.where(lb < 4, 127, np.where(lb >= 20, 0, key))
 
 
 def assert_stats_equal(got, want):

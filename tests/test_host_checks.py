@@ -66,23 +66,23 @@ def test_is_permutation_sees_in_place_changes():
 
 
 def test_tile_order_key_buckets():
-    """The tile launch order's key: costs 0 and 1 share the last bucket, the
-    largest u32 cost sorts first, the key never rises with the cost, and each
-    octave [2^k, 2^(k+1)) from k = 2 on splits into 4 equal buckets."""
+    """The tile launch order's key: costs below 16 fall in the last bucket, costs
+    from 2^20 the first, the key never rises with the cost, and each octave
+    [2^k, 2^(k+1)) for k = 4..19 splits into 8 equal buckets."""
     k = H.tile_order_keys
-    assert k([0, 1, 0xFFFFFFFF]).tolist() == [127, 127, 0]
-    c = np.arange(1, 1 << 17)
+    assert k([0, 1, 15, 16, 31, 1 << 20, 0xFFFFFFFF]).tolist() == [127, 127, 127, 127, 120, 0, 0]
+    c = np.arange(1, 1 << 21)
     keys = k(c)
     assert np.all(np.diff(keys) <= 0)
-    for e in range(2, 16):
+    for e in range(4, 20):
         seg = keys[(1 << e) - 1:(1 << (e + 1)) - 1]
         vals, counts = np.unique(seg, return_counts=True)
-        assert len(vals) == 4 and np.all(counts == (1 << e) // 4), e
+        assert len(vals) == 8 and np.all(counts == (1 << e) // 8), e
+        assert vals.max() == 127 - 8 * (e - 4) and vals.min() == 120 - 8 * (e - 4), e
     rng = np.random.default_rng(0)
-    for x in rng.integers(1, 1 << 32, 2000).tolist() + [2, 3, 5, 6, 7]:
+    for x in rng.integers(16, 1 << 20, 2000).tolist() + [16, 17, 23, 24, 1023, 1024]:
         lb = x.bit_length() - 1
-        frac = (x >> (lb - 2)) & 3 if lb >= 2 else (x << (2 - lb)) & 3
-        assert k([x])[0] == 127 - (4 * lb + frac), x
+        assert k([x])[0] == 127 - (8 * (lb - 4) + ((x >> (lb - 3)) & 7)), x
 
 
 def test_walk_layout_np_round_trip():
