@@ -79,8 +79,16 @@ int vt_prefetch_adj(const float *points, uint32_t num_points, const uint32_t *ad
  *     chunk}.
  *   heads: u32 (num_points, 2): the same pair for each cell itself.
  *   cells: f32 (num_points, 4): {site xyz, density}.
+ *   orig: u16 (8 * num_chunks): each slot's index in the cell's original
+ *     list (0xffff for pads).  A list of at most 64 faces is laid out in the
+ *     order of one component of its offsets (face_order 1, 2, 3: x, y, z;
+ *     equal values in list order; 0 keeps the list order): the lanes of a
+ *     wave, whose rays point alike, then meet forward-facing faces at the same
+ *     slots, and the wave skips the plane test of slots that no lane faces.
+ *     Quotients that tie go to the lower original index, as in the reference.
  * The walk reads the same offsets, sites and densities as through adjacency,
- * offsets and adj_diff, and renders the same images bit for bit.  Limits:
+ * offsets and adj_diff and picks the same exit faces, so it renders the same
+ * images bit for bit.  Limits:
  * num_points < 2^24, at most 255 chunks (2,040 faces) per cell and
  * 8 * num_chunks < 2^32.
  */
@@ -89,6 +97,7 @@ typedef struct vt_walk_layout {
     const uint32_t *links;
     const uint32_t *heads;
     const float *cells;
+    const uint16_t *orig;
     uint32_t num_chunks;
 } vt_walk_layout;
 
@@ -109,8 +118,8 @@ int vt_walk_layout_count(const uint32_t *offsets, uint32_t num_points, uint32_t 
  */
 int vt_walk_layout_fill(const float *points, const float *density, const uint32_t *adjacency,
                         const uint32_t *offsets, uint32_t num_points, const uint16_t *adj_diff,
-                        const uint32_t *first_chunk, uint32_t num_chunks, uint32_t *chunks, uint32_t *links,
-                        uint32_t *heads, float *cells, vt_stream_t stream);
+                        const uint32_t *first_chunk, uint32_t num_chunks, int face_order, uint32_t *chunks,
+                        uint32_t *links, uint32_t *heads, float *cells, uint16_t *orig, vt_stream_t stream);
 
 /*
  * fp16 inference render.  Replaces _C.trace_vorotracing_infer
@@ -586,7 +595,11 @@ int vt_pad_3to4_f16(const float *x, uint32_t rows, uint32_t texels_per_row, uint
  * op 6 = the walk's exit-face search on n rows of 26 floats (site, origin,
  * unit direction, face count <= 8 as u32 bits, 8 half4 face records as 16
  * u32; counts above 8 read as 8), out = 2 words per row: face index
- * (0xffffffff = none) and t1 bits.
+ * (0xffffffff = none) and t1 bits; op 7 = the packed walk's search over one
+ * chunk whose faces are reordered, on n rows of 30 floats (an op 6 row with
+ * the records in slot order and zero records past the count, then the 8
+ * slots' original indices as u16 in 4 words), out = the original index of
+ * the exit face (0xffffffff = none) and t1 bits.
  */
 int vt_math_probe(int op, const float *in, uint32_t *out, uint32_t n, vt_stream_t stream);
 

@@ -75,3 +75,32 @@ def face_rows(rng, m=1 << 14):
     # NaN site
     rows.append(_row((np.nan, 0, 0), (0, 0, 0), F([0, 0, 1]), [(0, 0, 1), (0, 0, 2)]))
     return np.ascontiguousarray(np.stack(rows))
+
+
+def packed_rows(rows, rng):
+    """Op 6 rows reordered into the packed walk's slots: (n, 30) float32, the
+    records of each row put in a new slot order (by the z half, stably, as
+    vt_walk_layout_fill's face order 3 lays a list out; reversed; or at
+    random), zero records past the count, then the slots' original indices
+    as 8 u16 (0xffff for empty slots)."""
+    n = rows.shape[0]
+    out = np.zeros((n, 30), F)
+    out[:, :10] = rows[:, :10]
+    recs = np.ascontiguousarray(rows[:, 10:26]).view(np.uint16).reshape(n, 8, 4)
+    nf = np.minimum(rows[:, 9].view(np.uint32), 8)
+    slots = np.zeros((n, 8, 4), np.uint16)
+    orig = np.full((n, 8), 0xffff, np.uint16)
+    kind = rng.integers(0, 3, n)
+    for i in range(n):
+        k = int(nf[i])
+        if kind[i] == 0:
+            perm = np.argsort(recs[i, :k, 2].view(np.float16).astype(np.float32), kind="stable")
+        elif kind[i] == 1:
+            perm = np.arange(k)[::-1]
+        else:
+            perm = rng.permutation(k)
+        slots[i, :k] = recs[i, perm]
+        orig[i, :k] = perm
+    out[:, 10:26] = slots.reshape(n, 16 * 2).view(F)
+    out[:, 26:30] = orig.view(F)
+    return np.ascontiguousarray(out)

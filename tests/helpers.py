@@ -260,10 +260,12 @@ def f16_train_sums(s, rays, start, thr, fw16, g16, contribution=False, **bwd_kw)
     return out[0], out[1]
 
 
-def walk_layout_np(points, density, adjacency, offsets, adj_diff):
+def walk_layout_np(points, density, adjacency, offsets, adj_diff, face_order=0):
     """The packed walk layout (vt_walk_layout) built on the host with numpy:
     (first_chunk (n + 2), chunks (C, 12) u32, links (8C, 2) u32, heads (n, 2)
-    u32, cells (n, 4) f32).  adj_diff: the f16 records (rows of 4 halves)."""
+    u32, cells (n, 4) f32, orig (8C,) u16).  adj_diff: the f16 records (rows
+    of 4 halves).  face_order 1..3 lays out lists of at most 64 faces in the
+    stable order of the x, y or z half of their offsets."""
     offsets = np.asarray(offsets, np.int64)
     n = offsets.size - 1
     nf = np.diff(offsets)
@@ -274,16 +276,26 @@ def walk_layout_np(points, density, adjacency, offsets, adj_diff):
     first[n + 1] = nch.max() if n else 0
     F = int(offsets[n])
     halves = np.ascontiguousarray(adj_diff).view(np.uint16).reshape(-1, 4)[:F]
+    # the face of each slot of each cell (list position within the cell)
+    src = np.arange(F) - np.repeat(offsets[:-1], nf)
+    if face_order:
+        key = halves[:, face_order - 1].view(np.float16).astype(np.float32)
+        for c in np.nonzero((nf > 1) & (nf <= 64))[0]:
+            b, e = offsets[c], offsets[c + 1]
+            src[b:e] = np.argsort(key[b:e], kind="stable")
     cell_of = np.repeat(np.arange(n), nf)
     slot = 8 * first[cell_of] + (np.arange(F) - offsets[cell_of])
+    face = offsets[cell_of] + src  # the face record placed at each slot
     rows = np.zeros((max(total, 0), 8, 3), np.uint16)
     for axis in range(3):
-        rows[slot // 8, slot % 8, axis] = halves[:, axis]
-    nb = np.asarray(adjacency, np.int64)[:F]
+        rows[slot // 8, slot % 8, axis] = halves[face, axis]
+    nb = np.asarray(adjacency, np.int64)[face]
     links = np.zeros((8 * total, 2), np.uint32)
     links[slot, 0] = (nb | (nch[nb] << 24)).astype(np.uint32)
     links[slot, 1] = first[nb].astype(np.uint32)
+    orig = np.full(8 * total, 0xFFFF, np.uint16)
+    orig[slot] = src.astype(np.uint16)
     heads = np.stack([np.arange(n) | (nch << 24), first[:n]], 1).astype(np.uint32)
     cells = np.concatenate([np.asarray(points, np.float32).reshape(n, 3),
                             np.asarray(density, np.float32).reshape(n, 1)], 1)
-    return first.astype(np.uint32), rows.reshape(total, 24).view(np.uint32), links, heads, cells
+    return first.astype(np.uint32), rows.reshape(total, 24).view(np.uint32), links, heads, cells, orig

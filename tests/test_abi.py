@@ -58,9 +58,12 @@ def test_host_only_entries():
     assert b"split_waves" in lib.vt_last_error()
     # the walk layout's limits are checked before any launch
     big = 1 << 24
-    assert lib.vt_walk_layout_fill(*[C.c_void_p(16)] * 4, big, C.c_void_p(16), C.c_void_p(16), 1,
-                                   *[C.c_void_p(16)] * 4, None) == 1
+    assert lib.vt_walk_layout_fill(*[C.c_void_p(16)] * 4, big, C.c_void_p(16), C.c_void_p(16), 1, 3,
+                                   *[C.c_void_p(16)] * 5, None) == 1
     assert b"below 2^24" in lib.vt_last_error()
+    assert lib.vt_walk_layout_fill(*[C.c_void_p(16)] * 4, 10, C.c_void_p(16), C.c_void_p(16), 1, 4,
+                                   *[C.c_void_p(16)] * 5, None) == 1
+    assert b"face_order" in lib.vt_last_error()
     assert lib.vt_walk_layout_count_workspace_size(10 ** 7) >= lib.vt_walk_layout_count_workspace_size(1000) >= 0
 
 

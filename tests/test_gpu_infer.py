@@ -49,6 +49,20 @@ def test_exit_face_probe(gpu):
     assert (want[-13:-1, 1] == np.float32(-np.inf).view(np.uint32)).all()
 
 
+def test_packed_exit_face_probe(gpu):
+    """The packed walk's search over a reordered chunk (exact ties noted and
+    settled by original index in the IEEE redo, the -inf redo) picks the face
+    the oracle's plain search over the original list picks: original index and
+    t1 bits, with the faces sorted by z, reversed and shuffled."""
+    from tests import exit_rows as X
+    rows = X.face_rows(np.random.default_rng(11))
+    packed = X.packed_rows(rows, np.random.default_rng(12))
+    got = native.math_probe(7, torch.from_numpy(packed).to(gpu)).cpu().numpy()
+    want = core.exit_face_rows(rows)
+    bad = np.nonzero((got != want).any(axis=1))[0]
+    assert bad.size == 0, f"{bad.size} of {len(rows)} rows differ, first {bad[:5]}: {got[bad[:5]]} vs {want[bad[:5]]}"
+
+
 def _dev_scene(s, dev):
     d4, s4 = H.f16_maps(s)
     return dict(points=H.to_dev(s.points, dev), diffuse4=H.to_dev(d4, dev), specular4=H.to_dev(s4, dev),

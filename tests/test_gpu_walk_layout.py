@@ -23,12 +23,14 @@ def _dev(s, gpu):
 
 
 def _check_arrays(wl, points, density, adjacency, offsets, adj_diff):
-    first, chunks, links, heads, cells = H.walk_layout_np(points, density, adjacency, offsets, adj_diff)
+    first, chunks, links, heads, cells, orig = H.walk_layout_np(points, density, adjacency, offsets, adj_diff,
+                                                                face_order=wl.face_order)
     assert wl.num_chunks == int(first[len(offsets) - 1])
     assert np.array_equal(wl.chunks.cpu().numpy().view(np.uint32)[:wl.num_chunks], chunks)
     assert np.array_equal(wl.links.cpu().numpy().view(np.uint32)[:8 * wl.num_chunks], links)
     assert np.array_equal(wl.heads.cpu().numpy().view(np.uint32), heads)
     assert np.array_equal(wl.cells.cpu().numpy().view(np.uint32), cells.view(np.uint32))
+    assert np.array_equal(wl.orig.cpu().numpy().view(np.uint16)[:8 * wl.num_chunks], orig)
 
 
 def test_walk_layout_arrays(gpu):
@@ -36,10 +38,12 @@ def test_walk_layout_arrays(gpu):
     length it has, several chunks each)."""
     s = H.mini_heightfield()
     d = _dev(s, gpu)
-    wl = native.WalkLayout.build(d["points"], d["density"], d["adjacency"], d["offsets"], d["adj"])
-    assert wl is not None
-    torch.cuda.synchronize()
-    _check_arrays(wl, s.points, s.density, s.adjacency, s.offsets, d["adj"].cpu().numpy())
+    for order in (0, 1, 2, 3):
+        wl = native.WalkLayout.build(d["points"], d["density"], d["adjacency"], d["offsets"], d["adj"],
+                                     face_order=order)
+        assert wl is not None
+        torch.cuda.synchronize()
+        _check_arrays(wl, s.points, s.density, s.adjacency, s.offsets, d["adj"].cpu().numpy())
     nf = np.diff(s.offsets)
     assert nf.min() < 8 < nf.max() and (nf % 8 == 0).any()
 

@@ -87,32 +87,47 @@ def test_tile_order_key_buckets():
 
 def test_walk_layout_np_round_trip():
     """The numpy construction of the packed walk layout (the checker of the
-    GPU build) decodes back to the CSR it came from: every face record and
-    neighbour at its list position, zero records in the pads, and each link
-    carrying its neighbour's own head."""
+    GPU build) decodes back to the CSR it came from, in list order and with
+    the faces laid out by their z: every slot's face record and neighbour are
+    those of its original index, each cell's original indices are a
+    permutation of its list (in z order when the layout sorts), pads are zero
+    records with no index, and each link carries its neighbour's own head."""
     rng = np.random.default_rng(2)
-    nf = np.array([0, 1, 7, 8, 9, 15, 16, 17, 0, 40], np.int64)
+    nf = np.array([0, 1, 7, 8, 9, 15, 16, 17, 0, 40, 65], np.int64)
     n = nf.size
     offsets = np.concatenate([[0], np.cumsum(nf)])
     F = int(offsets[-1])
     adjacency = rng.integers(0, n, F + 32)
-    adj_diff = rng.integers(1, 1 << 15, (F + 32, 4)).astype(np.uint16)
+    adj_diff = rng.integers(1, 1 << 14, (F + 32, 4)).astype(np.uint16)
+    adj_diff[3:6, 2] = adj_diff[2, 2]  # equal z values: list order among them
     points = rng.standard_normal((n, 3)).astype(np.float32)
     density = rng.random(n).astype(np.float32)
-    first, chunks, links, heads, cells = H.walk_layout_np(points, density, adjacency, offsets, adj_diff)
-    nch = (nf + 7) // 8
-    assert first[n] == nch.sum() and first[n + 1] == nch.max() and chunks.shape == (nch.sum(), 12)
-    halves = chunks.view(np.uint16).reshape(-1, 8, 3)
-    for c in range(n):
-        assert heads[c, 0] == (c | nch[c] << 24) and heads[c, 1] == first[c]
-        assert np.array_equal(cells[c], np.append(points[c], density[c]))
-        for f in range(8 * nch[c]):
-            q, j = divmod(f, 8)
-            rec = halves[first[c] + q, j]
-            lk = links[8 * (first[c] + q) + j]
-            if f < nf[c]:
-                assert np.array_equal(rec, adj_diff[offsets[c] + f, :3])
-                nb = adjacency[offsets[c] + f]
-                assert np.array_equal(lk, heads[nb])
+    for order in (0, 3):
+        first, chunks, links, heads, cells, orig = H.walk_layout_np(points, density, adjacency, offsets, adj_diff,
+                                                                    face_order=order)
+        nch = (nf + 7) // 8
+        assert first[n] == nch.sum() and first[n + 1] == nch.max() and chunks.shape == (nch.sum(), 12)
+        halves = chunks.view(np.uint16).reshape(-1, 8, 3)
+        for c in range(n):
+            assert heads[c, 0] == (c | nch[c] << 24) and heads[c, 1] == first[c]
+            assert np.array_equal(cells[c], np.append(points[c], density[c]))
+            seen = []
+            for f in range(8 * nch[c]):
+                q, j = divmod(f, 8)
+                rec = halves[first[c] + q, j]
+                lk = links[8 * (first[c] + q) + j]
+                og = int(orig[8 * (first[c] + q) + j])
+                if f < nf[c]:
+                    assert np.array_equal(rec, adj_diff[offsets[c] + og, :3])
+                    assert np.array_equal(lk, heads[adjacency[offsets[c] + og]])
+                    seen.append(og)
+                else:
+                    assert not rec.any() and not lk.any() and og == 0xFFFF
+            assert sorted(seen) == list(range(nf[c]))
+            if order == 0 or nf[c] > 64:
+                assert seen == list(range(nf[c]))
             else:
-                assert not rec.any() and not lk.any()
+                z = adj_diff[offsets[c] + np.array(seen, np.int64), 2].view(np.float16).astype(np.float32)
+                assert np.all(np.diff(z) >= 0)
+                ties = np.diff(z) == 0
+                assert np.all(np.diff(np.array(seen))[ties] > 0)

@@ -505,6 +505,33 @@ def test_exit_face_rows_closed_forms():
     assert x0 < -np.finfo(np.float32).max
 
 
+def test_packed_rows_need_the_tie_rule():
+    """The reordered rows of the packed-search probe keep each row's faces
+    (de-permuted through their original indices they are the row's records),
+    and the reordering matters: searched plainly in slot order (first of equal
+    quotients wins), many rows take a face other than the one the original
+    order takes, so the probe's agreement with the oracle checks the
+    original-index tie rule and does not hold by construction."""
+    from tests import exit_rows as X
+    rows = X.face_rows(np.random.default_rng(11), m=4096)
+    packed = X.packed_rows(rows, np.random.default_rng(12))
+    n = rows.shape[0]
+    recs = np.ascontiguousarray(rows[:, 10:26]).view(np.uint16).reshape(n, 8, 4)
+    slots = np.ascontiguousarray(packed[:, 10:26]).view(np.uint16).reshape(n, 8, 4)
+    orig = np.ascontiguousarray(packed[:, 26:30]).view(np.uint16)
+    nf = np.minimum(rows[:, 9].view(np.uint32), 8)
+    for i in range(n):
+        k = int(nf[i])
+        assert sorted(orig[i, :k]) == list(range(k)) and np.all(orig[i, k:] == 0xFFFF)
+        assert np.array_equal(slots[i, :k], recs[i, orig[i, :k]]) and not slots[i, k:].any()
+    want = core.exit_face_rows(rows)
+    plain = core.exit_face_rows(np.ascontiguousarray(packed[:, :26]))
+    hit = plain[:, 0] != 0xFFFFFFFF
+    mapped = np.where(hit, orig[np.arange(n), np.where(hit, plain[:, 0], 0)], 0xFFFFFFFF)
+    assert np.array_equal(plain[:, 1], want[:, 1])  # the same quotient wins
+    assert (mapped != want[:, 0]).sum() >= 500  # of 4109 rows; about a quarter hold a duplicated face
+
+
 # --------------------------------------------------------------------------- absolute-sum mode
 
 def test_abs_sum_mode():

@@ -138,6 +138,7 @@ def _drop_in_schedule(ray_perm_in: torch.Tensor, lay, device) -> "native.TileSch
 # caller's five scene arrays are the same tensors, unchanged (native.SourceKey).
 # The layout walks with fewer vector loads per step and renders the same image.
 DROP_IN_WALK = True
+DROP_IN_FACE_ORDER = 3
 _WALK_LAYOUTS: list = []
 
 
@@ -149,10 +150,10 @@ def _drop_in_walk(srcs_in, srcs) -> Optional["native.WalkLayout"]:
     if not DROP_IN_WALK:
         return None
     for i, (key, wl) in enumerate(_WALK_LAYOUTS):
-        if key.matches(*srcs_in):
+        if key.matches(*srcs_in) and (wl is None or wl.face_order == DROP_IN_FACE_ORDER):
             _WALK_LAYOUTS.append(_WALK_LAYOUTS.pop(i))
             return wl
-    entry = (native.SourceKey(*srcs_in), native.WalkLayout.build(*srcs))
+    entry = (native.SourceKey(*srcs_in), native.WalkLayout.build(*srcs, face_order=DROP_IN_FACE_ORDER))
     _WALK_LAYOUTS.append(entry)
     del _WALK_LAYOUTS[:-2]
     return entry[1]

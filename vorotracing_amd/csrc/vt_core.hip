@@ -26,6 +26,9 @@ void clear_error() { g_err[0] = 0; }
 // read as one chunk
 constexpr int PROBE_FACE_ROW = 26;
 constexpr int INFER_PROBE_CHUNK = 8;
+// op 7 rows: an op 6 row whose records are in slot order (faces past nf are
+// zero), then the slots' original indices as 8 u16 (4 words)
+constexpr int PROBE_PACKED_ROW = 30;
 
 __global__ void math_probe_kernel(int op, const float *__restrict__ in, uint32_t *__restrict__ out, uint32_t n)
 {
@@ -45,6 +48,39 @@ __global__ void math_probe_kernel(int op, const float *__restrict__ in, uint32_t
                                                              mk(r[0], r[1], r[2]), mk(r[3], r[4], r[5]),
                                                              mk(r[6], r[7], r[8]), t1);
         out[2 * (size_t)i] = best;
+        out[2 * (size_t)i + 1] = best == NONE ? 0u : f_bits(t1);
+        return;
+    }
+    if (op == 7) { // the packed walk's search (walk_step_packed) over one reordered chunk; out (orig, t1 bits)
+        const float *r = in + PROBE_PACKED_ROW * (size_t)i;
+        const uint32_t *rec = reinterpret_cast<const uint32_t *>(r + 10);
+        uint32_t h[24];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            h[3 * j] = rec[2 * j] & 0xffffu;
+            h[3 * j + 1] = rec[2 * j] >> 16;
+            h[3 * j + 2] = rec[2 * j + 1] & 0xffffu;
+        }
+        uint4 ch[3];
+        uint32_t *cw = reinterpret_cast<uint32_t *>(ch);
+#pragma unroll
+        for (int k = 0; k < 12; ++k)
+            cw[k] = h[2 * k] | h[2 * k + 1] << 16;
+        uint16_t orig[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            orig[j] = (uint16_t)(f_bits(r[26 + j / 2]) >> (16 * (j & 1)));
+        const f3 p = mk(r[0], r[1], r[2]), o = mk(r[3], r[4], r[5]), d = mk(r[6], r[7], r[8]);
+        float bnum = FIRST_BNUM, bdp = FIRST_BDP;
+        uint32_t best = NONE;
+        search_chunk(ch[0], ch[1], ch[2], 0, p, o, d, bnum, bdp, best);
+        float t1 = 0.0f;
+        if (best != NONE) {
+            t1 = bnum / bdp;
+            if (!(t1 > -__builtin_huge_valf()))
+                best = exit_face_packed_ieee(ch, 1, p, o, d, orig, t1);
+        }
+        out[2 * (size_t)i] = best == NONE ? NONE : orig[best];
         out[2 * (size_t)i + 1] = best == NONE ? 0u : f_bits(t1);
         return;
     }
@@ -154,8 +190,9 @@ extern "C" int vt_abi_version(void) { return 11; }
 extern "C" int vt_math_probe(int op, const float *in, uint32_t *out, uint32_t n, vt_stream_t stream)
 {
     clear_error();
-    VT_REQUIRE(op >= 0 && op <= 6,
-               "op must be 0 (exp), 1 (log), 2 (f16), 3 (sin), 4 (cos), 5 (exit order) or 6 (exit face)");
+    VT_REQUIRE(op >= 0 && op <= 7,
+               "op must be 0 (exp), 1 (log), 2 (f16), 3 (sin), 4 (cos), 5 (exit order), 6 (exit face) or 7 "
+               "(packed exit face)");
     if (n == 0)
         return VT_OK;
     VT_REQUIRE(in && out, "null pointer argument");

@@ -269,6 +269,7 @@ struct InferArgs {
     const uint2 *wl_links;
     const uint2 *wl_heads;
     const float4 *wl_cells;
+    const uint16_t *wl_orig;
     // rays per start cell (0: one start cell per ray)
     uint32_t rays_per_start;
 };
@@ -374,7 +375,7 @@ void infer_kernel(InferArgs a, uint32_t total_slots)
             if constexpr (PACKED)
                 // the q8 integrator leaves no register room for the preloaded row
                 active = walk_step_packed<!Q8>(w, integ.o, integ.d, a.wl_chunks, a.wl_links, a.wl_cells,
-                                               a.offsets, a.max_steps, integ, st);
+                                               a.wl_orig, a.offsets, a.max_steps, integ, st);
             else
                 active = walk_step<CHUNK>(w, integ.o, integ.d, a.points, a.adjacency, a.offsets, a.adj_diff,
                                           a.max_steps, integ, st);
@@ -464,11 +465,13 @@ static int set_walk_layout(InferArgs &a, const vt_walk_layout *walk)
 {
     if (!walk)
         return VT_OK;
-    VT_REQUIRE(walk->chunks && walk->links && walk->heads && walk->cells, "null array in the walk layout");
+    VT_REQUIRE(walk->chunks && walk->links && walk->heads && walk->cells && walk->orig,
+               "null array in the walk layout");
     a.wl_chunks = reinterpret_cast<const uint4 *>(walk->chunks);
     a.wl_links = reinterpret_cast<const uint2 *>(walk->links);
     a.wl_heads = reinterpret_cast<const uint2 *>(walk->heads);
     a.wl_cells = reinterpret_cast<const float4 *>(walk->cells);
+    a.wl_orig = walk->orig;
     return VT_OK;
 }
 

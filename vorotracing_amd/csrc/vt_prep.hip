@@ -721,12 +721,19 @@ __global__ void wl_count_kernel(const uint32_t *offsets, uint32_t n, uint32_t *f
         atomicMax(first_chunk + n + 1, k);
 }
 
-// One lane per cell: its cell record, its head, and its chunks and links.
+// Lists of up to WL_SORT_MAX faces are laid out in the face order; longer
+// ones (hull cells) keep theirs.
+constexpr uint32_t WL_SORT_MAX = 64;
+
+// One lane per cell: its cell record, its head, and its chunks, links and
+// original indices.  face_order 1..3 sorts the cell's faces by the x, y or z
+// half of their offsets (stable: equal values keep list order), 0 keeps the
+// list order.
 __global__ void wl_fill_kernel(const float *__restrict__ points, const float *__restrict__ density,
                                const uint32_t *__restrict__ adjacency, const uint32_t *__restrict__ offsets,
                                uint32_t n, const uint2 *__restrict__ adj_diff, const uint32_t *__restrict__ fc,
-                               uint4 *__restrict__ chunks, uint2 *__restrict__ links, uint2 *__restrict__ heads,
-                               float4 *__restrict__ cells)
+                               int face_order, uint4 *__restrict__ chunks, uint2 *__restrict__ links,
+                               uint2 *__restrict__ heads, float4 *__restrict__ cells, uint16_t *__restrict__ origs)
 {
     const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
     if (c >= n)
@@ -736,14 +743,35 @@ __global__ void wl_fill_kernel(const float *__restrict__ points, const float *__
     const f3 p = load_site(points, c);
     cells[c] = make_float4(p.x, p.y, p.z, density[c]);
     heads[c] = make_uint2(c | nch << WL_ID_BITS, cb);
+    uint16_t ord[WL_SORT_MAX];
+    const bool sorted = face_order >= 1 && face_order <= 3 && nf <= WL_SORT_MAX;
+    if (sorted) {
+        // the sort key: one component of the offset, as the walk widens it
+        auto key = [&](uint32_t f) {
+            const uint2 r = adj_diff[b + f];
+            const uint32_t hbits = face_order == 1 ? (r.x & 0xffffu) : face_order == 2 ? (r.x >> 16) : (r.y & 0xffffu);
+            return h2f((uint16_t)hbits);
+        };
+        for (uint32_t f = 0; f < nf; ++f) {
+            const float kf = key(f);
+            uint32_t k = f;
+            while (k > 0 && key(ord[k - 1]) > kf) {
+                ord[k] = ord[k - 1];
+                --k;
+            }
+            ord[k] = (uint16_t)f;
+        }
+    }
     for (uint32_t q = 0; q < nch; ++q) {
         // the chunk's 24 halves: x, y, z of face 0, then of face 1, ...
         uint32_t w[12] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const uint32_t f = 8 * q + j;
+            const uint32_t slot = 8 * q + j;
             uint2 lk = make_uint2(0u, 0u);
-            if (f < nf) {
+            uint16_t og = 0xffffu;
+            if (slot < nf) {
+                const uint32_t f = sorted ? ord[slot] : slot;
                 const uint2 r = adj_diff[b + f];
                 const uint32_t h[3] = {r.x & 0xffffu, r.x >> 16, r.y & 0xffffu};
 #pragma unroll
@@ -754,8 +782,10 @@ __global__ void wl_fill_kernel(const float *__restrict__ points, const float *__
                 const uint32_t nb = adjacency[b + f];
                 const uint32_t ncb = fc[nb];
                 lk = make_uint2(nb | (fc[nb + 1] - ncb) << WL_ID_BITS, ncb);
+                og = (uint16_t)f;
             }
             links[8 * (size_t)(cb + q) + j] = lk;
+            origs[8 * (size_t)(cb + q) + j] = og;
         }
         uint4 *row = chunks + 3 * (size_t)(cb + q);
         row[0] = make_uint4(w[0], w[1], w[2], w[3]);
@@ -788,13 +818,16 @@ extern "C" int vt_walk_layout_count(const uint32_t *offsets, uint32_t num_points
 
 extern "C" int vt_walk_layout_fill(const float *points, const float *density, const uint32_t *adjacency,
                                    const uint32_t *offsets, uint32_t num_points, const uint16_t *adj_diff,
-                                   const uint32_t *first_chunk, uint32_t num_chunks, uint32_t *chunks,
-                                   uint32_t *links, uint32_t *heads, float *cells, vt_stream_t stream)
+                                   const uint32_t *first_chunk, uint32_t num_chunks, int face_order,
+                                   uint32_t *chunks, uint32_t *links, uint32_t *heads, float *cells, uint16_t *orig,
+                                   vt_stream_t stream)
 {
     clear_error();
     VT_REQUIRE(points && density && adjacency && offsets && adj_diff && first_chunk && chunks && links && heads &&
-                   cells,
+                   cells && orig,
                "null pointer argument");
+    VT_REQUIRE(face_order >= 0 && face_order <= 3, "face_order must be 0 (list order), 1, 2 or 3 (x, y, z), got %d",
+               face_order);
     VT_REQUIRE(num_points < (1u << WL_ID_BITS), "the walk layout holds cell ids below 2^24, got %u points",
                num_points);
     VT_REQUIRE(num_chunks < (1u << 29), "the walk layout holds fewer than 2^29 chunks, got %u", num_chunks);
@@ -802,8 +835,8 @@ extern "C" int vt_walk_layout_fill(const float *points, const float *density, co
         return VT_OK;
     wl_fill_kernel<<<(num_points + 255) / 256, 256, 0, as_stream(stream)>>>(
         points, density, adjacency, offsets, num_points, reinterpret_cast<const uint2 *>(adj_diff), first_chunk,
-        reinterpret_cast<uint4 *>(chunks), reinterpret_cast<uint2 *>(links), reinterpret_cast<uint2 *>(heads),
-        reinterpret_cast<float4 *>(cells));
+        face_order, reinterpret_cast<uint4 *>(chunks), reinterpret_cast<uint2 *>(links),
+        reinterpret_cast<uint2 *>(heads), reinterpret_cast<float4 *>(cells), orig);
     VT_LAUNCH_CHECK("wl_fill_kernel");
     return VT_OK;
 }

@@ -226,7 +226,12 @@ __device__ __forceinline__ uint32_t walk(f3 o, f3 d, const float *points,
 //  - links: per padded face slot, the neighbour behind it with its own chunk
 //    range, so the next cell's face records can be loaded as soon as the exit
 //    face is known, in parallel with its site;
-//  - cells: site and density in one 16-byte record.
+//  - cells: site and density in one 16-byte record;
+//  - a cell's faces may be reordered (vt_walk_layout_fill's face order: by one
+//    component of their offsets, so that the lanes of a wave, whose rays point
+//    alike, meet forward-facing faces at the same slots and the wave skips the
+//    plane test of slots that no lane faces); orig[slot] keeps each slot's
+//    index in the original list for the exact-tie rule (exit_before_tie).
 // A step reads the same offsets, sites and densities as walk_step, so it
 // picks the same exit faces and hands the integrator the same values.
 constexpr uint32_t WL_ID_BITS = 24;
@@ -289,9 +294,35 @@ __device__ __forceinline__ void chunk_face(uint4 R0, uint4 R1, uint4 R2, int j, 
     oz = chunk_half(R0, R1, R2, 3 * j + 2);
 }
 
+// exit_before for the packed layout, whose face lists may be reordered
+// (vt_walk_layout_fill's face order): two quotients that round to the same
+// float go to the face of lower index in the cell's original list, as the
+// reference's strict t < t_1 over that list keeps the first
+// (tracing_octmap.cu:90-94).  Such ties only occur on the IEEE path (a
+// decided comparison separates the quotients by 2^-19 of their size, and two
+// that both round to -inf take the -inf redo), where a tie with a face
+// (bt < inf: only the virtual first best has quotient +inf) sets bnum to NaN.
+// No later face is then accepted (a NaN quotient compares false), t1 comes
+// out NaN, and the step settles the cell by exit_face_packed_ieee, which
+// compares original indices.  A face's own quotient is never NaN when
+// accepted, so NaN marks a tie and nothing else.
+__device__ __forceinline__ bool exit_before_tie(float num, float dp, float &bnum, float bdp)
+{
+    float Q = bnum * dp;
+    float gap = fma_(num, bdp, -Q);
+    float h = fma_(__builtin_fabsf(gap), -0x1p18f, __builtin_fabsf(Q));
+    if (h < -1e-26f)
+        return gap < 0.0f;
+    const float t = num / dp, bt = bnum / bdp;
+    if (t == bt && bt < __builtin_huge_valf())
+        bnum = __builtin_nanf("");
+    return t < bt;
+}
+
 // The faces of one chunk (rows R0-R2, slots 8q..8q+7) against the running
-// best (exit_face's order); an accepted slot is kept as j - 16 (an inline
-// constant, no move per face) and made 8q + j after the chunk.
+// best (exit_face's order; an exact tie turns bnum into NaN); an accepted
+// slot is kept as j - 16 (an inline constant, no move per face) and made
+// 8q + j after the chunk.
 __device__ __forceinline__ void search_chunk(uint4 R0, uint4 R1, uint4 R2, uint32_t q, f3 p, f3 o, f3 d,
                                              float &bnum, float &bdp, uint32_t &best)
 {
@@ -307,7 +338,7 @@ __device__ __forceinline__ void search_chunk(uint4 R0, uint4 R1, uint4 R2, uint3
             float ey = fma_(oy, 0.5f, p.y) - o.y;
             float ez = fma_(oz, 0.5f, p.z) - o.z;
             float num = fma_(ez, oz, fma_(ey, oy, ex * ox));
-            if (exit_before(num, dp, bnum, bdp)) {
+            if (exit_before_tie(num, dp, bnum, bdp)) {
                 bnum = num;
                 bdp = dp;
                 best = (uint32_t)(j - 16);
@@ -318,9 +349,11 @@ __device__ __forceinline__ void search_chunk(uint4 R0, uint4 R1, uint4 R2, uint3
         best += 16 + 8 * q;
 }
 
-// The IEEE redo of exit_face over the nch chunks at ch (a best quotient that
-// rounded to -inf); returns the slot and sets t1.
-__device__ __forceinline__ uint32_t exit_face_packed_ieee(const uint4 *ch, uint32_t nch, f3 p, f3 o, f3 d, float &t1)
+// The IEEE search over the nch chunks at ch, for a best quotient that rounded
+// to -inf or an exact tie (t1 NaN): the lowest RN(num / dp), ties to the
+// lowest orig[slot].  Returns the slot and sets t1.
+__device__ __forceinline__ uint32_t exit_face_packed_ieee(const uint4 *ch, uint32_t nch, f3 p, f3 o, f3 d,
+                                                          const uint16_t *orig, float &t1)
 {
     float bt = __builtin_huge_valf();
     uint32_t best = NONE;
@@ -335,9 +368,10 @@ __device__ __forceinline__ uint32_t exit_face_packed_ieee(const uint4 *ch, uint3
                 const float ey = fma_(oy, 0.5f, p.y) - o.y;
                 const float ez = fma_(oz, 0.5f, p.z) - o.z;
                 const float t = fma_(ez, oz, fma_(ey, oy, ex * ox)) / dp;
-                if (t < bt) {
+                const uint32_t slot = 8 * q + j;
+                if (t < bt || (t == bt && best != NONE && orig[slot] < orig[best])) {
                     bt = t;
-                    best = 8 * q + j;
+                    best = slot;
                 }
             }
         }
@@ -357,8 +391,9 @@ __device__ __forceinline__ uint32_t exit_face_packed_ieee(const uint4 *ch, uint3
 // visit counts the cell's padded slots.
 template <bool PRELOAD, class Integrator, class StatsT>
 __device__ __forceinline__ bool walk_step_packed(PackedWalk &w, f3 o, f3 d, const uint4 *chunks, const uint2 *links,
-                                                 const float4 *cells, const uint32_t *offsets, uint32_t max_steps,
-                                                 Integrator &integ, StatsT &st)
+                                                 const float4 *cells, const uint16_t *origs,
+                                                 const uint32_t *offsets, uint32_t max_steps, Integrator &integ,
+                                                 StatsT &st)
 {
     w.n++;
     if (w.n > max_steps)
@@ -383,8 +418,8 @@ __device__ __forceinline__ bool walk_step_packed(PackedWalk &w, f3 o, f3 d, cons
     st.exit();
     uint2 lk = links[8 * (size_t)w.cb + best];
     float t1 = bnum / bdp;
-    if (t1 == -__builtin_huge_valf()) {
-        best = exit_face_packed_ieee(ch, w.nch, p, o, d, t1);
+    if (!(t1 > -__builtin_huge_valf())) { // -inf, or NaN after a tie
+        best = exit_face_packed_ieee(ch, w.nch, p, o, d, origs + 8 * (size_t)w.cb, t1);
         lk = links[8 * (size_t)w.cb + best];
     }
     const uint32_t cur = w.cur;

@@ -28,8 +28,10 @@ class VoroTracingInfer:
     # costs (native.TileSchedule; images are bit-identical either way)
     adaptive_tile_order = True
     # walk the packed layout (native.WalkLayout) in the tiled and camera
-    # renders; images are bit-identical either way
+    # renders, each cell's faces laid out by the z of their offsets
+    # (face_order 3; 0 keeps the list order); images are bit-identical either way
     packed_walk = True
+    face_order = 3
 
     def __init__(self, model, sort_morton: bool = True, quantize: Literal["fp16", "q8"] = "fp16",
                  per_channel_q8: bool = False):
@@ -79,8 +81,9 @@ class VoroTracingInfer:
         src = (self.primal_points, self.density, self.point_adjacency, self.point_adjacency_offsets,
                self.adjacent_diff)
         entry = self._walk_layout
-        if entry is None or not entry[0].matches(*src):
-            entry = (native.SourceKey(*src), native.WalkLayout.build(*src))
+        if entry is None or not entry[0].matches(*src) or entry[2] != self.face_order:
+            entry = (native.SourceKey(*src), native.WalkLayout.build(*src, face_order=self.face_order),
+                     self.face_order)
             self._walk_layout = entry
         return entry[1]
 

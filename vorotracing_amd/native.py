@@ -66,16 +66,19 @@ def math_probe(op: int, x: torch.Tensor) -> torch.Tensor:
     order on the rows (num, dp, bnum, bdp) of an (n, 4) float32 tensor; for
     op 6 the walk's exit-face search on the rows of an (n, 26) float32 tensor
     (site, origin, direction, face count as int32 bits, 8 half4 records as
-    16 words), giving (face index, t1 bits) per row."""
+    16 words), giving (face index, t1 bits) per row; for op 7 the packed
+    walk's search on (n, 30) rows (an op 6 row in slot order, then the slots'
+    original indices as 8 u16), giving (original index, t1 bits)."""
     x = x.contiguous()
     if op == 5:
         if x.dim() != 2 or x.size(1) != 4 or x.dtype != torch.float32:
             raise ValueError("op 5 takes an (n, 4) float32 tensor of (num, dp, bnum, bdp)")
         n = x.size(0)
         out = torch.empty(n, dtype=torch.uint32, device=x.device)
-    elif op == 6:
-        if x.dim() != 2 or x.size(1) != 26 or x.dtype != torch.float32:
-            raise ValueError("op 6 takes an (n, 26) float32 tensor of exit-face rows")
+    elif op in (6, 7):
+        width = 26 if op == 6 else 30
+        if x.dim() != 2 or x.size(1) != width or x.dtype != torch.float32:
+            raise ValueError(f"op {op} takes an (n, {width}) float32 tensor of exit-face rows")
         n = x.size(0)
         out = torch.empty((n, 2), dtype=torch.uint32, device=x.device)
     else:
@@ -210,7 +213,7 @@ class SourceKey:
 
 class _WalkLayoutC(C.Structure):
     _fields_ = [("chunks", C.c_void_p), ("links", C.c_void_p), ("heads", C.c_void_p), ("cells", C.c_void_p),
-                ("num_chunks", C.c_uint32)]
+                ("orig", C.c_void_p), ("num_chunks", C.c_uint32)]
 
 
 class WalkLayout:
@@ -219,6 +222,10 @@ class WalkLayout:
     padded face slot carrying the neighbour's chunk range, and a {site,
     density} record per cell.  The inference kernels walk it with fewer
     vector loads per step and render the same images bit for bit.
+    ``face_order`` (0: list order; 1, 2, 3: by the x, y or z of the offsets)
+    lays out each cell's faces so that the lanes of a wave meet
+    forward-facing faces at the same slots (``orig`` keeps the original
+    indices for exact ties); 3 suits scenes whose views look up or down.
 
     ``build`` returns None for a scene beyond the layout's limits (2^24 cells,
     255 chunks per cell); the renders then walk the reference's arrays.
@@ -228,12 +235,13 @@ class WalkLayout:
     MAX_POINTS = 1 << 24
     MAX_CHUNKS_PER_CELL = 255
 
-    def __init__(self, chunks, links, heads, cells, num_chunks: int, sources=()):
-        self.chunks, self.links, self.heads, self.cells = chunks, links, heads, cells
+    def __init__(self, chunks, links, heads, cells, orig, num_chunks: int, face_order: int = 0, sources=()):
+        self.chunks, self.links, self.heads, self.cells, self.orig = chunks, links, heads, cells, orig
         self.num_chunks = int(num_chunks)
+        self.face_order = int(face_order)
         self.source = SourceKey(*sources)
         self._c = _WalkLayoutC(chunks.data_ptr(), links.data_ptr(), heads.data_ptr(), cells.data_ptr(),
-                               self.num_chunks)
+                               orig.data_ptr(), self.num_chunks)
 
     @property
     def ptr(self) -> int:
@@ -242,7 +250,8 @@ class WalkLayout:
 
 
     @classmethod
-    def build(cls, points, density, adjacency, offsets, adj_diff, stream=None) -> Optional["WalkLayout"]:
+    def build(cls, points, density, adjacency, offsets, adj_diff, stream=None,
+              face_order: int = 3) -> Optional["WalkLayout"]:
         """The layout of a scene (density: f32 per cell, as the renders take
         it; adj_diff from vt_prefetch_adj), or None beyond the limits.  Reads
         two counts back to the host to size the arrays."""
@@ -267,11 +276,12 @@ class WalkLayout:
         links = torch.empty((max(8 * total, 1), 2), dtype=torch.int32, device=dev)
         heads = torch.empty((max(n, 1), 2), dtype=torch.int32, device=dev)
         cells = torch.empty((max(n, 1), 4), dtype=torch.float32, device=dev)
+        orig = torch.empty(max(8 * total, 1), dtype=torch.int16, device=dev)
         with torch.cuda.device(dev):
             _lib.call("vt_walk_layout_fill", points.data_ptr(), density.data_ptr(), adjacency.data_ptr(),
-                      offsets.data_ptr(), n, adj_diff.data_ptr(), first.data_ptr(), total, chunks.data_ptr(),
-                      links.data_ptr(), heads.data_ptr(), cells.data_ptr(), sp)
-        return cls(chunks, links, heads, cells, total, sources)
+                      offsets.data_ptr(), n, adj_diff.data_ptr(), first.data_ptr(), total, int(face_order),
+                      chunks.data_ptr(), links.data_ptr(), heads.data_ptr(), cells.data_ptr(), orig.data_ptr(), sp)
+        return cls(chunks, links, heads, cells, orig, total, face_order, sources)
 
 
 def _walk_ptr(walk: Optional[WalkLayout]):
