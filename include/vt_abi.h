@@ -82,7 +82,9 @@ int vt_prefetch_adj(const float *points, uint32_t num_points, const uint32_t *ad
  *   orig: u16 (8 * num_chunks): each slot's index in the cell's original
  *     list (0xffff for pads).  A list of at most 64 faces is laid out in the
  *     order of one component of its offsets (face_order 1, 2, 3: x, y, z;
- *     equal values in list order; 0 keeps the list order): the lanes of a
+ *     0 keeps the list order), compared as f16 values with -0 taken as +0
+ *     and NaNs past the infinities of their sign, equal values in list
+ *     order: the lanes of a
  *     wave, whose rays point alike, then meet forward-facing faces at the same
  *     slots, and the wave skips the plane test of slots that no lane faces.
  *     Quotients that tie go to the lower original index, as in the reference.

@@ -260,12 +260,22 @@ def f16_train_sums(s, rays, start, thr, fw16, g16, contribution=False, **bwd_kw)
     return out[0], out[1]
 
 
+def face_order_key(h):
+    """The walk layout's sort key of f16 bits h: a total order that is the
+    numeric one on non-NaN values, -0 taken as +0, NaNs past the infinities
+    of their sign."""
+    h = np.asarray(h, np.uint32)
+    h = np.where(h == 0x8000, 0, h)
+    return np.where(h & 0x8000, 0x7FFF - (h & 0x7FFF), h | 0x8000)
+
+
 def walk_layout_np(points, density, adjacency, offsets, adj_diff, face_order=0):
     """The packed walk layout (vt_walk_layout) built on the host with numpy:
     (first_chunk (n + 2), chunks (C, 12) u32, links (8C, 2) u32, heads (n, 2)
     u32, cells (n, 4) f32, orig (8C,) u16).  adj_diff: the f16 records (rows
     of 4 halves).  face_order 1..3 lays out lists of at most 64 faces in the
-    stable order of the x, y or z half of their offsets."""
+    order of the x, y or z half of their offsets (face_order_key, ties in list
+    order)."""
     offsets = np.asarray(offsets, np.int64)
     n = offsets.size - 1
     nf = np.diff(offsets)
@@ -279,7 +289,7 @@ def walk_layout_np(points, density, adjacency, offsets, adj_diff, face_order=0):
     # the face of each slot of each cell (list position within the cell)
     src = np.arange(F) - np.repeat(offsets[:-1], nf)
     if face_order:
-        key = halves[:, face_order - 1].view(np.float16).astype(np.float32)
+        key = face_order_key(halves[:, face_order - 1])
         for c in np.nonzero((nf > 1) & (nf <= 64))[0]:
             b, e = offsets[c], offsets[c + 1]
             src[b:e] = np.argsort(key[b:e], kind="stable")

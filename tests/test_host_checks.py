@@ -85,6 +85,19 @@ def test_tile_order_key_buckets():
         assert k([x])[0] == 127 - (8 * (lb - 4) + ((x >> (lb - 3)) & 7)), x
 
 
+def test_face_order_key():
+    """The walk layout's face-order key orders f16 values numerically, takes
+    -0 as +0, and puts NaNs past the infinities of their sign; every bit
+    pattern gets a key, so the sort is a total order."""
+    vals = np.float16([-np.inf, -65504, -1, -2.0 ** -24, -0.0, 0.0, 2.0 ** -24, 1, 65504, np.inf])
+    k = H.face_order_key(vals.view(np.uint16))
+    assert k[4] == k[5] and np.all(np.diff(np.delete(k, 4)) > 0)
+    nan_pos, nan_neg = H.face_order_key(np.uint16([0x7E00, 0xFE00]))
+    assert nan_pos > k[-1] and nan_neg < k[0]
+    allk = H.face_order_key(np.arange(1 << 16, dtype=np.uint32))
+    assert allk.max() < 1 << 16 and np.unique(allk).size == (1 << 16) - 1  # only -0 and +0 share a key
+
+
 def test_walk_layout_np_round_trip():
     """The numpy construction of the packed walk layout (the checker of the
     GPU build) decodes back to the CSR it came from, in list order and with
@@ -100,6 +113,7 @@ def test_walk_layout_np_round_trip():
     adjacency = rng.integers(0, n, F + 32)
     adj_diff = rng.integers(1, 1 << 14, (F + 32, 4)).astype(np.uint16)
     adj_diff[3:6, 2] = adj_diff[2, 2]  # equal z values: list order among them
+    adj_diff[10:14, 2] = [0x8000, 0x0000, 0x8001, 0x0001]  # -0 and +0 tie; -2^-24 below them, 2^-24 above
     points = rng.standard_normal((n, 3)).astype(np.float32)
     density = rng.random(n).astype(np.float32)
     for order in (0, 3):

@@ -725,10 +725,20 @@ __global__ void wl_count_kernel(const uint32_t *offsets, uint32_t n, uint32_t *f
 // ones (hull cells) keep theirs.
 constexpr uint32_t WL_SORT_MAX = 64;
 
+// The face order's key of f16 bits h: a total order that is the numeric one
+// on non-NaN values, with -0 taken as +0 and NaNs past the infinities of
+// their sign.
+__device__ __forceinline__ uint32_t face_order_key(uint32_t h)
+{
+    h = h == 0x8000u ? 0u : h;
+    return (h & 0x8000u) ? 0x7fffu - (h & 0x7fffu) : (h | 0x8000u);
+}
+
 // One lane per cell: its cell record, its head, and its chunks, links and
-// original indices.  face_order 1..3 sorts the cell's faces by the x, y or z
-// half of their offsets (stable: equal values keep list order), 0 keeps the
-// list order.
+// original indices.  face_order 1..3 sorts the cell's faces by the
+// face_order_key of the x, y or z half of their offsets (equal keys keep list
+// order), 0 keeps the list order.  The sort ranks (key, index) pairs, which
+// are distinct, so the ranks are a permutation of the list.
 __global__ void wl_fill_kernel(const float *__restrict__ points, const float *__restrict__ density,
                                const uint32_t *__restrict__ adjacency, const uint32_t *__restrict__ offsets,
                                uint32_t n, const uint2 *__restrict__ adj_diff, const uint32_t *__restrict__ fc,
@@ -746,20 +756,19 @@ __global__ void wl_fill_kernel(const float *__restrict__ points, const float *__
     uint16_t ord[WL_SORT_MAX];
     const bool sorted = face_order >= 1 && face_order <= 3 && nf <= WL_SORT_MAX;
     if (sorted) {
-        // the sort key: one component of the offset, as the walk widens it
-        auto key = [&](uint32_t f) {
-            const uint2 r = adj_diff[b + f];
-            const uint32_t hbits = face_order == 1 ? (r.x & 0xffffu) : face_order == 2 ? (r.x >> 16) : (r.y & 0xffffu);
-            return h2f((uint16_t)hbits);
-        };
+        // (key << 8 | index) per face, loaded once; a face's slot is the
+        // number of smaller pairs
+        uint32_t kv[WL_SORT_MAX];
         for (uint32_t f = 0; f < nf; ++f) {
-            const float kf = key(f);
-            uint32_t k = f;
-            while (k > 0 && key(ord[k - 1]) > kf) {
-                ord[k] = ord[k - 1];
-                --k;
-            }
-            ord[k] = (uint16_t)f;
+            const uint2 r = adj_diff[b + f];
+            const uint32_t h = face_order == 1 ? (r.x & 0xffffu) : face_order == 2 ? (r.x >> 16) : (r.y & 0xffffu);
+            kv[f] = face_order_key(h) << 8 | f;
+        }
+        for (uint32_t f = 0; f < nf; ++f) {
+            uint32_t rank = 0;
+            for (uint32_t g = 0; g < nf; ++g)
+                rank += kv[g] < kv[f] ? 1u : 0u;
+            ord[rank] = (uint16_t)f;
         }
     }
     for (uint32_t q = 0; q < nch; ++q) {
