@@ -26,7 +26,7 @@ def _declarations():
 
 def test_header_declarations_parsed():
     d = _declarations()
-    assert len(d) == 47, sorted(d)
+    assert len(d) == 48, sorted(d)
     for name in ("vt_trace_infer_f16", "vt_trace_fwd", "vt_trace_bwd", "vt_bvh_query", "vt_morton_reorder"):
         assert name in d
 
@@ -45,7 +45,7 @@ def test_binding_matches_header_arity():
 
 def test_host_only_entries():
     lib = _lib.load()
-    assert lib.vt_abi_version() == 11
+    assert lib.vt_abi_version() == 12
     assert isinstance(lib.vt_last_error(), bytes)
     assert lib.vt_quantize_workspace_size() > 0
     assert lib.vt_morton_workspace_size(1000, 16000) >= lib.vt_morton_workspace_size(10, 160) > 0
@@ -71,11 +71,16 @@ def test_argument_errors_need_no_gpu():
     """Null pointers and bad sizes are rejected on the host, with a message."""
     lib = _lib.load()
     rc = lib.vt_trace_infer_f16_tiled(None, None, None, 4, 4, None, None, None, 10, None, None, 1, 8, 8, 8, 8, None, 0,
-                                      0.01, 1024, 0.0, None, None, None, None, None, None)
+                                      0.01, 1024, 0.0, None, None, None, None, None, None, None)
     assert rc == 1
     assert b"null pointer" in lib.vt_last_error()
     with pytest.raises(_lib.VTError, match="null"):
         _lib.check(rc, "vt_trace_infer_f16_tiled")
+    # footprint tables: the map resolution and alignment are checked before any launch
+    assert lib.vt_quad_maps_f16(C.c_void_p(16), 10, 6, C.c_void_p(16), None) == 1
+    assert b"res must be 4 or 8" in lib.vt_last_error()
+    assert lib.vt_quad_maps_f16(C.c_void_p(16), 10, 4, C.c_void_p(8), None) == 1
+    assert b"16-byte aligned" in lib.vt_last_error()
     # the allocation-free lookup rejects more queries than its scratch holds before touching a device
     rc = lib.vt_nearest_sites_noalloc(None, 1000, None, 65, None, None)
     assert rc == 1

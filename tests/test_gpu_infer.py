@@ -489,6 +489,6 @@ def test_tile_order_and_costs_of_a_render(gpu):
     _lib.call("vt_trace_infer_f16_tiled", d["points"].data_ptr(), d["diffuse4"].data_ptr(), d["specular4"].data_ptr(),
               4, 4, d["density"].data_ptr(), d["adjacency"].data_ptr(), d["offsets"].data_ptr(), s.num_points,
               adj.data_ptr(), rays.data_ptr(), 1, Hh, W, 8, 8, start.data_ptr(), 0, 0.01, 1024, 1e-3, out.data_ptr(),
-              order.data_ptr(), None, None, None, torch.cuda.current_stream().cuda_stream)
+              order.data_ptr(), None, None, None, None, torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16))

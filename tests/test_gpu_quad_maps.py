@@ -1,0 +1,128 @@
+"""Footprint tables of the fp16 maps (vt_quad_maps, native.QuadMaps): the
+tables against a numpy construction through the oracle's octahedral wrap, and
+renders that read them, which must equal the renders that read the maps'
+texels bit for bit (buffer, camera and drop-in renders, 4x4 and 8x8 maps) and
+stay within the oracle's bound."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import core
+from tests import helpers as H
+from vorotracing_amd import _C, _lib, camera, native
+
+pytestmark = pytest.mark.gpu
+
+
+def _table_np(maps4, R):
+    """The footprint table of Half4Texel maps (N, 4 R^2) f16: entry
+    (ex, ey) = the texels at (ex - 1, ey - 1), (ex, ey - 1), (ex - 1, ey),
+    (ex, ey), each through the oracle's oct_wrap_index."""
+    tex = np.ascontiguousarray(maps4).view(np.uint16).reshape(maps4.shape[0], R * R, 4)
+    idx = np.array([[core.oct_wrap_index(ex + du - 1, ey + dv - 1, R) for dv in (0, 1) for du in (0, 1)]
+                    for ey in range(R + 1) for ex in range(R + 1)], np.int64)
+    return tex[:, idx, :].reshape(maps4.shape[0], -1)
+
+
+@pytest.mark.parametrize("R", [4, 8])
+def test_quad_tables(gpu, R):
+    """The GPU tables equal the numpy construction for random texel bits
+    (every half pattern, NaNs included: the tables copy bits)."""
+    rng = np.random.default_rng(R)
+    n = 777
+    maps = rng.integers(0, 1 << 16, (n, 4 * R * R), dtype=np.uint16).view(np.float16)
+    got = native.QuadMaps.table(H.to_dev(maps, gpu))
+    torch.cuda.synchronize()
+    assert got.shape == (n, 16 * (R + 1) ** 2)
+    assert np.array_equal(got.cpu().numpy().view(np.uint16), _table_np(maps, R))
+
+
+@pytest.mark.parametrize("scene", ["heightfield", "random_r8"])
+def test_quad_render_parity(gpu, scene):
+    """Tiled fp16 renders reading the tables: within the oracle's bound and
+    bit-identical to the renders reading the maps, with the packed walk and
+    with the reference's arrays, with and without statistics."""
+    s = H.mini_heightfield() if scene == "heightfield" else H.small_random(3000, seed=11, R=8, Rs=8)
+    d4, s4 = H.f16_maps(s)
+    d = dict(points=H.to_dev(s.points, gpu), diffuse4=H.to_dev(d4, gpu), specular4=H.to_dev(s4, gpu),
+             density=H.to_dev(s.density.reshape(-1), gpu), adjacency=H.to_dev(s.adjacency, gpu),
+             offsets=H.to_dev(s.offsets, gpu))
+    d["adj"] = native.prefetch(d["points"], d["adjacency"], d["offsets"])
+    wl = native.WalkLayout.build(d["points"], d["density"], d["adjacency"], d["offsets"], d["adj"])
+    qm = native.QuadMaps.build(d["diffuse4"], d["specular4"])
+    adj_np = d["adj"].cpu().numpy()
+    for k in (0, 9):
+        print(f"case: quad maps, {scene}, pose {k}", flush=True)
+        rays = camera.orbit_rays(k, 160, 120)
+        start = H.start_for(s, rays)
+        want, _, _ = core.trace_infer_f16(s.points, d4, s4, s.diff_res, s.spec_res, s.density, s.adjacency,
+                                          s.offsets, adj_np, rays, start, weight_threshold=0.01,
+                                          cell_skip_threshold=1e-3, want_stats=True)
+        outs = []
+        for walk in (wl, None):
+            for quads in (qm, None):
+                for stats in (True, False):
+                    st = native.new_stats(rays.shape[0] * rays.shape[1], gpu) if stats else None
+                    outs.append(native.infer_f16(d["points"], d["diffuse4"], d["specular4"], d["density"],
+                                                 d["adjacency"], d["offsets"], d["adj"], H.to_dev(rays, gpu),
+                                                 H.to_dev(start, gpu), weight_threshold=0.01,
+                                                 cell_skip_threshold=1e-3, stats=st, tiled=(8, 8), walk=walk,
+                                                 quads=quads))
+        torch.cuda.synchronize()
+        H.assert_infer_rgba(outs[0], want)
+        for o in outs[1:]:
+            assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16))
+    # tables of another scene (fewer cells) are refused before any launch
+    few = native.QuadMaps.build(d["diffuse4"][:100], d["specular4"][:100])
+    with pytest.raises(_lib.VTError, match="quad maps of 100 cells"):
+        native.infer_f16(d["points"], d["diffuse4"], d["specular4"], d["density"], d["adjacency"], d["offsets"],
+                         d["adj"], H.to_dev(rays, gpu), H.to_dev(start, gpu), tiled=(8, 8), quads=few)
+
+
+def test_quad_renders_infer_camera_drop_in(gpu):
+    """VoroTracingInfer's buffer and camera renders and the fp16 drop-in with
+    a lane order: the same image with the tables on and off; the drop-in's
+    cached tables are rebuilt after an in-place change of the maps."""
+    from vorotracing_amd.infer import VoroTracingInfer
+    from vorotracing_amd.model import VoroTracing
+    s = H.mini_heightfield_r8()
+    inf = VoroTracingInfer(VoroTracing.from_scene(s, device=gpu), sort_morton=True, quantize="fp16")
+    assert inf.quad_tables() is not None
+    kw = dict(weight_threshold=0.01, cell_skip_threshold=1e-3)
+    rays = H.to_dev(camera.orbit_rays(3, 128, 96), gpu)
+    cams = [camera.Camera.orbit(3, 128, 96)]
+    outs = {}
+    try:
+        for on in (True, False):
+            VoroTracingInfer.quad_maps = on
+            print(f"case: VoroTracingInfer renders, quad maps {on}", flush=True)
+            outs[on] = (inf.render(rays, **kw), inf.render_cameras(cams, **kw))
+    finally:
+        VoroTracingInfer.quad_maps = True
+    torch.cuda.synchronize()
+    for a, b in zip(outs[True], outs[False]):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+    sp = inf.get_starting_point(rays)
+    perm = torch.arange(rays.numel() // 6, dtype=torch.int32, device=gpu)
+    diffuse = inf.diffuse_fp16.clone()
+
+    def render():
+        return _C.trace_vorotracing_infer(inf.primal_points, diffuse, inf.specular_fp16, inf.density,
+                                          inf.point_adjacency, inf.point_adjacency_offsets, rays, sp,
+                                          inf.adjacent_diff, perm, 0.01, 1024, 1e-3)
+
+    try:
+        for step in range(2):
+            print(f"case: fp16 drop-in, quad maps on/off, maps changed {bool(step)}", flush=True)
+            _C.DROP_IN_QUADS = False
+            plain = render()
+            _C.DROP_IN_QUADS = True
+            quad = render()
+            torch.cuda.synchronize()
+            assert torch.equal(quad.view(torch.int16), plain.view(torch.int16))
+            if step == 0:
+                assert torch.equal(quad.view(torch.int16), outs[True][0].view(torch.int16))
+                diffuse.mul_(0.5)  # in place: the cached tables must not be reused
+    finally:
+        _C.DROP_IN_QUADS = True

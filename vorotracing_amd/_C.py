@@ -159,6 +159,31 @@ def _drop_in_walk(srcs_in, srcs) -> Optional["native.WalkLayout"]:
     return entry[1]
 
 
+# Footprint tables (native.QuadMaps) of the fp16 maps the tiled drop-in
+# renders read: built on a scene's first image render and reused while the
+# caller's two map tensors are the same, unchanged.  A bilinear tap then reads
+# its four texels with two 16-byte loads; the image is the same.
+DROP_IN_QUADS = True
+_QUAD_MAPS: list = []
+
+
+def _drop_in_quads(maps_in, maps) -> Optional["native.QuadMaps"]:
+    """The footprint tables of the maps ``maps_in`` (diffuse, specular as the
+    caller passed them), built from their contiguous forms ``maps``; None
+    when off."""
+    if not DROP_IN_QUADS:
+        return None
+    for i, qm in enumerate(_QUAD_MAPS):
+        if qm.source.matches(*maps_in):
+            _QUAD_MAPS.append(_QUAD_MAPS.pop(i))
+            return qm
+    qm = native.QuadMaps.build(*maps)
+    qm.source = native.SourceKey(*maps_in)
+    _QUAD_MAPS.append(qm)
+    del _QUAD_MAPS[:-2]
+    return qm
+
+
 # Tile launch schedules of the training entries for tiled rays, keyed by the
 # image shape and stream: the forward (in screen order) records its tiles'
 # costs, and the backward of the same rays (the same tensor, unchanged)
@@ -283,6 +308,7 @@ def trace_vorotracing_infer(points_in, diffuse_in, specular_in, density_in, poin
                       native._walk_ptr(_drop_in_walk(
                           (points_in, density_in, point_adjacency_in, point_adjacency_offsets_in, adjacent_diff_in),
                           (points, density, adjacency, offsets, adjacent_diff))),
+                      native._quads_ptr(_drop_in_quads((diffuse_in, specular_in), (diffuse, specular))),
                       _stream(rays.device))
         else:
             _lib.call("vt_trace_infer_f16", points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd, rs,

@@ -27,8 +27,9 @@ SIGNATURES = {
     "vt_walk_layout_count_workspace_size": ([U32], C.c_size_t),
     "vt_walk_layout_count": ([P, U32, P, P, P], C.c_int),
     "vt_walk_layout_fill": ([P, P, P, P, U32, P, P, U32, I32, P, P, P, P, P, P], C.c_int),
+    "vt_quad_maps_f16": ([P, U32, U32, P, P], C.c_int),
     "vt_trace_infer_f16_tiled": (
-        [P, P, P, U32, U32, P, P, P, U32, P, P, U32, U32, U32, U32, U32, P, U32, F32, U32, F32, P, P, P, P, P, P],
+        [P, P, P, U32, U32, P, P, P, U32, P, P, U32, U32, U32, U32, U32, P, U32, F32, U32, F32, P, P, P, P, P, P, P],
         C.c_int),
     "vt_trace_infer_q8": (
         [P, P, P, U32, U32, P, P, P, P, P, P, P, U32, P, P, U32, P, P, F32, U32, F32, P, P, P], C.c_int),
@@ -37,7 +38,7 @@ SIGNATURES = {
          P, P], C.c_int),
     "vt_camera_rays": ([P, U32, U32, U32, P, P], C.c_int),
     "vt_trace_infer_f16_camera": (
-        [P, P, P, U32, U32, P, P, P, U32, P, P, U32, U32, U32, U32, U32, P, I32, F32, U32, F32, P, P, P, P, P, P],
+        [P, P, P, U32, U32, P, P, P, U32, P, P, U32, U32, U32, U32, U32, P, I32, F32, U32, F32, P, P, P, P, P, P, P],
         C.c_int),
     "vt_trace_infer_q8_camera": (
         [P, P, P, U32, U32, P, P, P, P, P, P, P, U32, P, P, U32, U32, U32, U32, U32, P, I32, F32, U32, F32, P, P, P, P, P,

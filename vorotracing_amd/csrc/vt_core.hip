@@ -185,7 +185,7 @@ using namespace vt;
 
 extern "C" const char *vt_last_error(void) { return g_err; }
 
-extern "C" int vt_abi_version(void) { return 11; }
+extern "C" int vt_abi_version(void) { return 12; }
 
 extern "C" int vt_math_probe(int op, const float *in, uint32_t *out, uint32_t n, vt_stream_t stream)
 {

@@ -221,6 +221,30 @@ template <int R> __device__ __forceinline__ Bilinear bilinear_setup(float u, flo
     return b;
 }
 
+// The bilinear tap of (u, v) as an entry of a footprint table (vt_quad_maps:
+// entry (ex, ey), 0 <= ex, ey <= R, holds the four wrapped texels of the
+// taps with floor coordinates (ex - 1, ey - 1)): q = (v0 + 1) (R + 1) + u0 + 1
+// and the weights of bilinear_setup.  u0, v0 lie in [-1, R - 1] for every
+// encoded direction (see oct_wrap_edge; a NaN converts to 0); the clamp keeps
+// any other input inside the table.
+template <int R> __device__ __forceinline__ Bilinear bilinear_quad(float u, float v)
+{
+    Bilinear b;
+    int u0 = (int)__builtin_floorf(u);
+    int v0 = (int)__builtin_floorf(v);
+    float fu = u - (float)u0;
+    float fv = v - (float)v0;
+    const int cu = u0 < -1 ? -1 : (u0 > R - 1 ? R - 1 : u0);
+    const int cv = v0 < -1 ? -1 : (v0 > R - 1 ? R - 1 : v0);
+    b.i00 = (cv + 1) * (R + 1) + cu + 1;
+    b.i10 = b.i01 = b.i11 = 0;
+    b.w00 = (1.0f - fu) * (1.0f - fv);
+    b.w10 = fu * (1.0f - fv);
+    b.w01 = (1.0f - fu) * fv;
+    b.w11 = fu * fv;
+    return b;
+}
+
 // w00*a + w10*b + w01*c + w11*d, left to right, contracted
 __device__ __forceinline__ float bil_mix(const Bilinear &b, float a, float bb, float c, float d)
 {

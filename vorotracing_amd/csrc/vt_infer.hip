@@ -21,26 +21,50 @@
 
 namespace vt {
 
-// fp16 Half4Texel maps: texel = 8 bytes (r, g, b, pad) halves
-template <int RD, int RS> struct TexF16 {
-    const uint2 *diffuse;
+// fp16 Half4Texel maps: texel = 8 bytes (r, g, b, pad) halves.  QUADS: the
+// maps' footprint tables (vt_quad_maps) are read instead, a tap's four texels
+// as one 32-byte entry (two 16-byte loads in one cache line) instead of four
+// 8-byte texels; the texels and weights are the same, so is the colour.
+template <int RD, int RS, bool QUADS> struct TexF16 {
+    const uint2 *diffuse;  // maps, or footprint tables (QUADS)
     const uint2 *specular;
 
+    __device__ __forceinline__ static constexpr bool quads() { return QUADS; }
     __device__ __forceinline__ f3 sample_diffuse(uint32_t cell, const Bilinear &b) const
     {
-        return sample(diffuse + (size_t)cell * (RD * RD), b);
+        if constexpr (QUADS)
+            return sample_quad(reinterpret_cast<const uint4 *>(diffuse) +
+                                   2 * ((size_t)cell * ((RD + 1) * (RD + 1)) + (uint32_t)b.i00),
+                               b);
+        else
+            return sample(diffuse + (size_t)cell * (RD * RD), b);
     }
     __device__ __forceinline__ f3 sample_specular(uint32_t cell, const Bilinear &b) const
     {
-        return sample(specular + (size_t)cell * (RS * RS), b);
+        if constexpr (QUADS)
+            return sample_quad(reinterpret_cast<const uint4 *>(specular) +
+                                   2 * ((size_t)cell * ((RS + 1) * (RS + 1)) + (uint32_t)b.i00),
+                               b);
+        else
+            return sample(specular + (size_t)cell * (RS * RS), b);
     }
-    __device__ __forceinline__ static f3 sample(const uint2 *m, const Bilinear &b)
+    __device__ __forceinline__ static f3 mix(const Bilinear &b, uint2 a, uint2 c, uint2 e, uint2 g)
     {
-        uint2 a = m[b.i00], c = m[b.i10], e = m[b.i01], g = m[b.i11];
         float r = bil_mix(b, h2f(a.x & 0xffffu), h2f(c.x & 0xffffu), h2f(e.x & 0xffffu), h2f(g.x & 0xffffu));
         float gg = bil_mix(b, h2f(a.x >> 16), h2f(c.x >> 16), h2f(e.x >> 16), h2f(g.x >> 16));
         float bl = bil_mix(b, h2f(a.y & 0xffffu), h2f(c.y & 0xffffu), h2f(e.y & 0xffffu), h2f(g.y & 0xffffu));
         return mk(r, gg, bl);
+    }
+    __device__ __forceinline__ static f3 sample(const uint2 *m, const Bilinear &b)
+    {
+        return mix(b, m[b.i00], m[b.i10], m[b.i01], m[b.i11]);
+    }
+    // entry: texels (u0, v0), (u0 + 1, v0) | (u0, v0 + 1), (u0 + 1, v0 + 1)
+    __device__ __forceinline__ static f3 sample_quad(const uint4 *m, const Bilinear &b)
+    {
+        const uint4 p0 = m[0], p1 = m[1];
+        return mix(b, make_uint2(p0.x, p0.y), make_uint2(p0.z, p0.w), make_uint2(p1.x, p1.y),
+                   make_uint2(p1.z, p1.w));
     }
 };
 
@@ -50,6 +74,7 @@ template <int RD, int RS> struct TexQ8 {
     const uint8_t *specular;
     float ds[3], dof[3], ss[3], sof[3];
 
+    __device__ __forceinline__ static constexpr bool quads() { return false; }
     __device__ __forceinline__ f3 sample_diffuse(uint32_t cell, const Bilinear &b) const
     {
         return sample(diffuse + (size_t)cell * (3 * RD * RD), b, ds, dof);
@@ -107,6 +132,7 @@ __device__ __forceinline__ ShadeQueue &wave_queue() { return infer_queues[thread
 // :487-515, colour :437-460).  A cell to shade goes to the wave's queue as
 // (cell, weight, probe offset); shade_batch computes its colour.
 template <int RD, int RS, class Tex> struct InferIntegrator {
+    using TexType = Tex;
     f3 o, d;
     const float *density;
     Tex tex;
@@ -202,13 +228,22 @@ __device__ __forceinline__ void shade_batch(ShadeQueue &q, uint32_t head, uint32
         const f3 pd = mk(dv.x * il, dv.y * il, dv.z * il);
         float u, v;
         shade_oct_encode<RD>(pd, u, v);
-        const Bilinear db = bilinear_setup<RD>(u, v);
+        Bilinear db;
+        if constexpr (Integ::TexType::quads())
+            db = bilinear_quad<RD>(u, v);
+        else
+            db = bilinear_setup<RD>(u, v);
         Bilinear sb;
         const uint32_t si = q.si[own];
-        sb.i00 = (int)(si & 0xffu);
-        sb.i10 = (int)((si >> 8) & 0xffu);
-        sb.i01 = (int)((si >> 16) & 0xffu);
-        sb.i11 = (int)(si >> 24);
+        if constexpr (Integ::TexType::quads()) { // the footprint entry
+            sb.i00 = (int)si;
+            sb.i10 = sb.i01 = sb.i11 = 0;
+        } else {
+            sb.i00 = (int)(si & 0xffu);
+            sb.i10 = (int)((si >> 8) & 0xffu);
+            sb.i01 = (int)((si >> 16) & 0xffu);
+            sb.i11 = (int)(si >> 24);
+        }
         sb.w00 = q.sw[0][own];
         sb.w10 = q.sw[1][own];
         sb.w01 = q.sw[2][own];
@@ -272,6 +307,9 @@ struct InferArgs {
     const uint16_t *wl_orig;
     // rays per start cell (0: one start cell per ray)
     uint32_t rays_per_start;
+    // fp16 footprint tables (vt_quad_maps), or NULL to read the maps' texels
+    const void *quad_d;
+    const void *quad_s;
 };
 
 // MAP_CAMERA: tiled lanes whose rays come from cameras instead of a buffer.
@@ -301,7 +339,7 @@ __device__ __forceinline__ uint32_t slot_to_ray(const InferArgs &a, uint32_t s, 
 }
 
 
-template <int RD, int RS, bool Q8, bool STATS, int MAP, int CHUNK, bool PACKED>
+template <int RD, int RS, bool Q8, bool STATS, int MAP, int CHUNK, bool PACKED, bool QUADS>
 // 8 waves per SIMD need at most 64 VGPRs.  The fp16 kernel fits them; the q8
 // kernel spills 12 bytes per lane and is still faster than at 7 waves
 // (C4: 16.6 against 17.2 ms).  The statistics variants (tests and counters
@@ -315,7 +353,8 @@ void infer_kernel(InferArgs a, uint32_t total_slots)
     const uint32_t s = xcd_interleaved_block<INFER_XCD_CHUNK>() * blockDim.x + threadIdx.x;
     const uint32_t r = s < total_slots ? slot_to_ray(a, s, MAP) : NONE;
     bool active = r != NONE;
-    using Tex = typename std::conditional<Q8, TexQ8<RD, RS>, TexF16<RD, RS>>::type;
+    static_assert(!(Q8 && QUADS), "footprint tables hold fp16 texels");
+    using Tex = typename std::conditional<Q8, TexQ8<RD, RS>, TexF16<RD, RS, QUADS>>::type;
     InferIntegrator<RD, RS, Tex> integ;
     integ.density = a.density;
     if constexpr (Q8) {
@@ -329,8 +368,8 @@ void infer_kernel(InferArgs a, uint32_t total_slots)
             integ.tex.sof[c] = a.sof[c];
         }
     } else {
-        integ.tex.diffuse = (const uint2 *)a.diffuse;
-        integ.tex.specular = (const uint2 *)a.specular;
+        integ.tex.diffuse = (const uint2 *)(QUADS ? a.quad_d : a.diffuse);
+        integ.tex.specular = (const uint2 *)(QUADS ? a.quad_s : a.specular);
     }
     integ.thr = a.thr;
     integ.skip = a.skip;
@@ -354,8 +393,14 @@ void infer_kernel(InferArgs a, uint32_t total_slots)
         }
         float su, sv;
         oct_encode<RS>(mk(-integ.d.x, -integ.d.y, -integ.d.z), su, sv);
-        const Bilinear sb = bilinear_setup<RS>(su, sv);
-        q.si[lane] = (uint32_t)sb.i00 | (uint32_t)sb.i10 << 8 | (uint32_t)sb.i01 << 16 | (uint32_t)sb.i11 << 24;
+        Bilinear sb;
+        if constexpr (QUADS) {
+            sb = bilinear_quad<RS>(su, sv);
+            q.si[lane] = (uint32_t)sb.i00;
+        } else {
+            sb = bilinear_setup<RS>(su, sv);
+            q.si[lane] = (uint32_t)sb.i00 | (uint32_t)sb.i10 << 8 | (uint32_t)sb.i01 << 16 | (uint32_t)sb.i11 << 24;
+        }
         q.sw[0][lane] = sb.w00;
         q.sw[1][lane] = sb.w10;
         q.sw[2][lane] = sb.w01;
@@ -411,10 +456,22 @@ template <int RD, int RS, bool Q8, bool STATS, int MAP>
 static int launch_one(const InferArgs &a, hipStream_t stream, uint32_t slots)
 {
     uint32_t blocks = (slots + INFER_BLOCK - 1) / INFER_BLOCK;
+    if constexpr (!Q8) {
+        if (a.quad_d) {
+            if (a.wl_chunks)
+                infer_kernel<RD, RS, false, STATS, MAP, INFER_CHUNK, true, true>
+                    <<<blocks, INFER_BLOCK, 0, stream>>>(a, slots);
+            else
+                infer_kernel<RD, RS, false, STATS, MAP, INFER_CHUNK, false, true>
+                    <<<blocks, INFER_BLOCK, 0, stream>>>(a, slots);
+            VT_LAUNCH_CHECK("infer_kernel");
+            return VT_OK;
+        }
+    }
     if (a.wl_chunks)
-        infer_kernel<RD, RS, Q8, STATS, MAP, INFER_CHUNK, true><<<blocks, INFER_BLOCK, 0, stream>>>(a, slots);
+        infer_kernel<RD, RS, Q8, STATS, MAP, INFER_CHUNK, true, false><<<blocks, INFER_BLOCK, 0, stream>>>(a, slots);
     else
-        infer_kernel<RD, RS, Q8, STATS, MAP, INFER_CHUNK, false><<<blocks, INFER_BLOCK, 0, stream>>>(a, slots);
+        infer_kernel<RD, RS, Q8, STATS, MAP, INFER_CHUNK, false, false><<<blocks, INFER_BLOCK, 0, stream>>>(a, slots);
     VT_LAUNCH_CHECK("infer_kernel");
     return VT_OK;
 }
@@ -475,6 +532,21 @@ static int set_walk_layout(InferArgs &a, const vt_walk_layout *walk)
     return VT_OK;
 }
 
+// The footprint tables of a call, or the maps' texels when quads is NULL.
+static int set_quad_maps(InferArgs &a, const vt_quad_maps *quads, uint32_t num_points, uint32_t diff_res,
+                         uint32_t spec_res)
+{
+    if (!quads)
+        return VT_OK;
+    VT_REQUIRE(quads->diffuse && quads->specular, "null table in the quad maps");
+    VT_REQUIRE(quads->num_points == num_points && quads->diff_res == diff_res && quads->spec_res == spec_res,
+               "quad maps of %u cells at %u/%u texels per side, the render has %u cells at %u/%u",
+               quads->num_points, quads->diff_res, quads->spec_res, num_points, diff_res, spec_res);
+    a.quad_d = quads->diffuse;
+    a.quad_s = quads->specular;
+    return VT_OK;
+}
+
 } // namespace vt
 
 using namespace vt;
@@ -523,7 +595,8 @@ extern "C" int vt_trace_infer_f16_tiled(const float *points, const uint16_t *dif
                                         float weight_threshold,
                                         uint32_t max_intersections, float cell_skip_threshold, uint16_t *rgba,
                                         const uint32_t *tile_order, uint32_t *tile_cost,
-                                        vt_ray_stats *stats, const vt_walk_layout *walk, vt_stream_t stream)
+                                        vt_ray_stats *stats, const vt_walk_layout *walk,
+                                        const vt_quad_maps *quads, vt_stream_t stream)
 {
     clear_error();
     if (num_images == 0 || image_h == 0 || image_w == 0)
@@ -558,6 +631,9 @@ extern "C" int vt_trace_infer_f16_tiled(const float *points, const uint16_t *dif
     a.tile_order = tile_order;
     a.tile_cost = tile_cost;
     rc = set_walk_layout(a, walk);
+    if (rc)
+        return rc;
+    rc = set_quad_maps(a, quads, num_points, diff_res, spec_res);
     if (rc)
         return rc;
     a.num_images = num_images;
@@ -735,7 +811,8 @@ extern "C" int vt_trace_infer_f16_camera(const float *points, const uint16_t *di
                                          const uint32_t *start_point, int start_per_row, float weight_threshold,
                                          uint32_t max_intersections, float cell_skip_threshold, uint16_t *rgba,
                                          const uint32_t *tile_order, uint32_t *tile_cost,
-                                         vt_ray_stats *stats, const vt_walk_layout *walk, vt_stream_t stream)
+                                         vt_ray_stats *stats, const vt_walk_layout *walk,
+                                         const vt_quad_maps *quads, vt_stream_t stream)
 {
     clear_error();
     if (num_images == 0 || image_h == 0 || image_w == 0)
@@ -762,6 +839,9 @@ extern "C" int vt_trace_infer_f16_camera(const float *points, const uint16_t *di
     a.tile_order = tile_order;
     a.tile_cost = tile_cost;
     rc = set_walk_layout(a, walk);
+    if (rc)
+        return rc;
+    rc = set_quad_maps(a, quads, num_points, diff_res, spec_res);
     if (rc)
         return rc;
     a.H = image_h;

@@ -803,6 +803,28 @@ __global__ void wl_fill_kernel(const float *__restrict__ points, const float *__
     }
 }
 
+// Footprint tables of fp16 octahedral maps (vt_quad_maps): one lane per
+// (cell, entry); entry (ex, ey) holds the wrapped texels of the taps
+// (ex - 1, ey - 1), (ex, ey - 1), (ex - 1, ey), (ex, ey), the ones
+// bilinear_setup reads for floor coordinates (ex - 1, ey - 1).  Coordinates
+// stay in [-1, R], the range oct_wrap_edge reduces.
+template <int R>
+__global__ void quad_maps_kernel(const uint2 *__restrict__ maps, uint32_t n, uint4 *__restrict__ quads)
+{
+    constexpr uint32_t E = (R + 1) * (R + 1);
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (uint64_t)n * E)
+        return;
+    const uint64_t c = i / E;
+    const int e = (int)(i - c * E);
+    const int ex = e % (R + 1), ey = e / (R + 1);
+    const uint2 *m = maps + c * (R * R);
+    const uint2 t00 = m[oct_wrap_edge<R>(ex - 1, ey - 1)], t10 = m[oct_wrap_edge<R>(ex, ey - 1)];
+    const uint2 t01 = m[oct_wrap_edge<R>(ex - 1, ey)], t11 = m[oct_wrap_edge<R>(ex, ey)];
+    quads[2 * i] = make_uint4(t00.x, t00.y, t10.x, t10.y);
+    quads[2 * i + 1] = make_uint4(t01.x, t01.y, t11.x, t11.y);
+}
+
 } // namespace vt
 
 extern "C" size_t vt_walk_layout_count_workspace_size(uint32_t num_points)
@@ -847,5 +869,28 @@ extern "C" int vt_walk_layout_fill(const float *points, const float *density, co
         face_order, reinterpret_cast<uint4 *>(chunks), reinterpret_cast<uint2 *>(links),
         reinterpret_cast<uint2 *>(heads), reinterpret_cast<float4 *>(cells), orig);
     VT_LAUNCH_CHECK("wl_fill_kernel");
+    return VT_OK;
+}
+
+extern "C" int vt_quad_maps_f16(const uint16_t *maps, uint32_t num_points, uint32_t res, uint16_t *quads,
+                                vt_stream_t stream)
+{
+    clear_error();
+    VT_REQUIRE(res == 4 || res == 8, "res must be 4 or 8, got %u", res);
+    if (num_points == 0)
+        return VT_OK;
+    VT_REQUIRE(maps && quads, "null pointer argument");
+    VT_REQUIRE((reinterpret_cast<uintptr_t>(maps) & 7u) == 0 && (reinterpret_cast<uintptr_t>(quads) & 15u) == 0,
+               "maps must be 8-byte and quads 16-byte aligned");
+    const uint64_t lanes = (uint64_t)num_points * (res + 1) * (res + 1);
+    const uint64_t blocks = (lanes + 255) / 256;
+    VT_REQUIRE(blocks < (1ull << 31), "too many cells for one launch: %u", num_points);
+    if (res == 4)
+        quad_maps_kernel<4><<<(uint32_t)blocks, 256, 0, as_stream(stream)>>>(
+            reinterpret_cast<const uint2 *>(maps), num_points, reinterpret_cast<uint4 *>(quads));
+    else
+        quad_maps_kernel<8><<<(uint32_t)blocks, 256, 0, as_stream(stream)>>>(
+            reinterpret_cast<const uint2 *>(maps), num_points, reinterpret_cast<uint4 *>(quads));
+    VT_LAUNCH_CHECK("quad_maps_kernel");
     return VT_OK;
 }

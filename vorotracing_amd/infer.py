@@ -32,6 +32,10 @@ class VoroTracingInfer:
     # (face_order 3; 0 keeps the list order); images are bit-identical either way
     packed_walk = True
     face_order = 3
+    # read the fp16 maps through their footprint tables (native.QuadMaps: a
+    # bilinear tap's four texels in one 32-byte entry) in the tiled and
+    # camera renders; images are bit-identical either way
+    quad_maps = True
 
     def __init__(self, model, sort_morton: bool = True, quantize: Literal["fp16", "q8"] = "fp16",
                  per_channel_q8: bool = False):
@@ -70,6 +74,20 @@ class VoroTracingInfer:
         self.adjacent_diff = ops.prefetch_octmap_adj(self.primal_points, self.point_adjacency,
                                                      self.point_adjacency_offsets)
         self._walk_layout = None
+        self._quad_maps = None
+
+    def quad_tables(self) -> Optional[native.QuadMaps]:
+        """The footprint tables of the fp16 maps (built on first use, and
+        again when the maps have been replaced or changed in place), or None
+        for q8 maps or when ``quad_maps`` is off."""
+        if not self.quad_maps or self.quantize != "fp16":
+            return None
+        src = (self.diffuse_fp16, self.specular_fp16)
+        entry = self.__dict__.get("_quad_maps")
+        if entry is None or not entry.source.matches(*src):
+            entry = native.QuadMaps.build(*src)
+            self._quad_maps = entry
+        return entry
 
     def walk_layout(self) -> Optional[native.WalkLayout]:
         """The scene's packed walk layout (built on first use, and again when
@@ -329,7 +347,8 @@ class VoroTracingInfer:
                                 cell_skip_threshold=cell_skip_threshold, stats=stats,
                                 tiled=self.TILE if image else None,
                                 schedule=self._schedule(*native.image_dims(rays)) if image else None,
-                                walk=self.walk_layout() if image else None, rays_per_start=rays_per_start)
+                                walk=self.walk_layout() if image else None, rays_per_start=rays_per_start,
+                                quads=self.quad_tables() if image else None)
 
     def camera_start_points(self, cameras, camera_buffer=None):
         """Start cells of a camera batch: one LBVH query on each camera's centre, or
@@ -366,7 +385,7 @@ class VoroTracingInfer:
         frame = camera.pack_cameras(cams)  # host-side records: no device read
         order, cost = sch.launch_args(sp, frame) if sch is not None else (None, None)
         common = (float(weight_threshold), int(max_intersections), float(cell_skip_threshold), out.data_ptr(), order,
-                  cost, native._p(stats), native._walk_ptr(self.walk_layout()), sp)
+                  cost, native._p(stats), native._walk_ptr(self.walk_layout()))
         if self.quantize == "q8":
             def v3(x):
                 vals = [float(x)] * 3 if isinstance(x, (int, float)) else [float(v) for v in x]
@@ -379,7 +398,7 @@ class VoroTracingInfer:
                       self.specular_q8.data_ptr(), rd, rs, *keep, self.density.data_ptr(),
                       self.point_adjacency.data_ptr(), self.point_adjacency_offsets.data_ptr(),
                       self.primal_points.shape[0], self.adjacent_diff.data_ptr(), camera_buffer.data_ptr(), B, H, W,
-                      self.TILE[0], self.TILE[1], start_point.data_ptr(), int(per_row), *common)
+                      self.TILE[0], self.TILE[1], start_point.data_ptr(), int(per_row), *common, sp)
         else:
             rd = native.map_res(self.diffuse_fp16.shape[-1], 4)
             rs = native.map_res(self.specular_fp16.shape[-1], 4)
@@ -387,7 +406,8 @@ class VoroTracingInfer:
                       self.specular_fp16.data_ptr(), rd, rs, self.density.data_ptr(),
                       self.point_adjacency.data_ptr(), self.point_adjacency_offsets.data_ptr(),
                       self.primal_points.shape[0], self.adjacent_diff.data_ptr(), camera_buffer.data_ptr(), B, H, W,
-                      self.TILE[0], self.TILE[1], start_point.data_ptr(), int(per_row), *common)
+                      self.TILE[0], self.TILE[1], start_point.data_ptr(), int(per_row), *common,
+                      native._quads_ptr(self.quad_tables()), sp)
         return out
 
     def _render_q8_native(self, rays, start_point, thr, max_int, skip, image, stats, rays_per_start=0):

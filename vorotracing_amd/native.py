@@ -288,16 +288,67 @@ def _walk_ptr(walk: Optional[WalkLayout]):
     return walk.ptr if walk is not None else None
 
 
+class _QuadMapsC(C.Structure):
+    _fields_ = [("diffuse", C.c_void_p), ("specular", C.c_void_p), ("num_points", C.c_uint32),
+                ("diff_res", C.c_uint32), ("spec_res", C.c_uint32)]
+
+
+class QuadMaps:
+    """Footprint tables of a scene's fp16 octahedral maps (vt_quad_maps): per
+    cell, (R + 1)^2 entries of 32 bytes, each the four wrapped texels of one
+    bilinear tap, so that the fp16 inference kernels read a tap with two
+    16-byte loads instead of four 8-byte ones and render the same images bit
+    for bit.  The tables take (R + 1)^2 / R^2 x 4 the bytes of the maps.
+    ``source`` (a SourceKey) tells whether the maps they were built from are
+    still the given tensors, unchanged."""
+
+    def __init__(self, diffuse, specular, num_points: int, diff_res: int, spec_res: int, sources=()):
+        self.diffuse, self.specular = diffuse, specular
+        self.num_points, self.diff_res, self.spec_res = int(num_points), int(diff_res), int(spec_res)
+        self.source = SourceKey(*sources)
+        self._c = _QuadMapsC(diffuse.data_ptr(), specular.data_ptr(), self.num_points, self.diff_res,
+                             self.spec_res)
+
+    @property
+    def ptr(self) -> int:
+        """Address of the vt_quad_maps struct (host memory) for the C ABI."""
+        return C.addressof(self._c)
+
+    @staticmethod
+    def table(maps4, stream=None):
+        """The footprint table of one Half4Texel map (f16 (N, 4 R^2))."""
+        maps4 = maps4.contiguous()
+        res = map_res(maps4.shape[-1], 4)
+        n = maps4.numel() // (4 * res * res)
+        out = torch.empty((max(n, 1), 16 * (res + 1) ** 2), dtype=torch.float16, device=maps4.device)
+        with torch.cuda.device(maps4.device):
+            _lib.call("vt_quad_maps_f16", maps4.data_ptr(), n, res, out.data_ptr(), _s(maps4.device, stream))
+        return out
+
+    @classmethod
+    def build(cls, diffuse4, specular4, stream=None) -> "QuadMaps":
+        """The tables of a scene's two Half4Texel maps (one row per cell)."""
+        if diffuse4.shape[0] != specular4.shape[0]:
+            raise ValueError(f"the maps have {diffuse4.shape[0]} and {specular4.shape[0]} rows")
+        return cls(cls.table(diffuse4, stream), cls.table(specular4, stream), diffuse4.shape[0],
+                   map_res(diffuse4.shape[-1], 4), map_res(specular4.shape[-1], 4), (diffuse4, specular4))
+
+
+def _quads_ptr(quads: Optional[QuadMaps]):
+    return quads.ptr if quads is not None else None
+
+
 def infer_f16(points, diffuse4, specular4, density, adjacency, offsets, adj_diff, rays, start_point, ray_perm=None,
               weight_threshold=0.001, max_intersections=1024, cell_skip_threshold=0.0, stats=None, out=None,
               tiled=None, stream=None, schedule: Optional[TileSchedule] = None, walk: Optional[WalkLayout] = None,
-              rays_per_start: int = 0):
+              rays_per_start: int = 0, quads: Optional[QuadMaps] = None):
     """fp16 inference.  ``tiled=(tile_h, tile_w)`` uses the in-kernel wave
     tiling over the images of screen_layout (any (..., H, W, 6) when the
     layout finds none), with ``schedule`` (a TileSchedule of this image
     shape and stream) the tiles' launch order, ``walk`` (a WalkLayout of
-    the scene) the packed walk, and ``rays_per_start`` the rays that share
-    each entry of ``start_point`` (0: one per ray)."""
+    the scene) the packed walk, ``rays_per_start`` the rays that share
+    each entry of ``start_point`` (0: one per ray), and ``quads`` (the
+    QuadMaps of the maps) the footprint tables read in place of the maps."""
     rd = map_res(diffuse4.shape[-1], 4)
     rs = map_res(specular4.shape[-1], 4)
     nr = rays.numel() // 6
@@ -313,8 +364,10 @@ def infer_f16(points, diffuse4, specular4, density, adjacency, offsets, adj_diff
                   rays.data_ptr(), B, H, W, tiled[0], tiled[1], start_point.data_ptr(), int(rays_per_start),
                   float(weight_threshold),
                   int(max_intersections), float(cell_skip_threshold), out.data_ptr(), order, cost, _p(stats),
-                  _walk_ptr(walk), sp)
+                  _walk_ptr(walk), _quads_ptr(quads), sp)
     else:
+        if quads is not None:
+            raise ValueError("quads (footprint tables) are read by the tiled fp16 renders only")
         _lib.call("vt_trace_infer_f16", points.data_ptr(), diffuse4.data_ptr(), specular4.data_ptr(), rd, rs,
                   density.data_ptr(), adjacency.data_ptr(), offsets.data_ptr(), points.size(0), adj_diff.data_ptr(),
                   rays.data_ptr(), nr, start_point.data_ptr(), _p(ray_perm), float(weight_threshold),
