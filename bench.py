@@ -251,6 +251,26 @@ def main():
             f"{fps:.1f} FPS (views {', '.join(f'{x:.3f}' for x in view_ms)} ms; wall clock "
             f"{1000 * t_ref / max(ref_steps, 1):.3f} ms/frame)")
 
+    # The traversal's share of those frames: each view rendered twice untimed
+    # (its second render launches by the recorded costs, as the protocol's
+    # timed renders do), then 5 renders with their start cells given, each
+    # between HIP events on the render stream.
+    ref_kernel_ms = []
+    for p in (view_poses if view_ms else []):
+        sp = inf.start_cells(poses[p])
+        for _ in range(2):
+            inf.render(poses[p], start_point=sp, **kw)
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(5)]
+        for a, b in evs:
+            a.record(stream)
+            inf.render(poses[p], start_point=sp, **kw)
+            b.record(stream)
+        torch.cuda.synchronize()
+        ref_kernel_ms.append(float(np.mean([a.elapsed_time(b) for a, b in evs])))
+    ref_kernel_avg = float(np.mean(ref_kernel_ms)) if ref_kernel_ms else float("nan")
+    if ref_kernel_ms:
+        log(f"reference protocol, traversal alone (start cells given): {ref_kernel_avg:.3f} ms/frame")
+
 
     # The orbit, serial: one render after the other on one stream, a new pose
     # every frame (a moving camera).  HIP events on that stream around each
@@ -318,6 +338,11 @@ def main():
                    "timing": timing},
         "views_ms": {"poses": view_poses, "ms": [round(x, 4) for x in view_ms],
                      "wall_clock_ms_per_frame": round(1000 * t_ref / max(ref_steps, 1), 4)},
+        "serial": {"fps": round(fps, 2), "ms_per_frame": round(ms_per_step, 4),
+                   "kernel_ms": round(ref_kernel_avg, 4) if ref_kernel_ms else None,
+                   "note": "the value's protocol (benchmark_eval.py:137-158: one stream, one frame at a time); "
+                           "kernel_ms: the traversal of the same views launched by their costs, start cells "
+                           "given, mean over 5 renders per view between HIP events"},
         "orbit_serial": {"fps": round(K / t_serial, 2), "ms_per_frame": round(1000 * t_serial / K, 4),
                          "kernel_ms": round(kernel_avg_ms, 4),
                          "note": f"{K} renders of the orbit, a new pose every frame, one after the other on one "
