@@ -108,11 +108,14 @@ size_t vt_walk_layout_count_workspace_size(uint32_t num_points);
 /*
  * Chunk ranges of the layout.  first_chunk out: u32 (num_points + 2):
  * first_chunk[c] = chunks of the cells before c, [num_points] = the total
- * (num_chunks), [num_points + 1] = the largest chunk count of one cell; the
- * caller checks the limits on the last two before vt_walk_layout_fill.
+ * (num_chunks), [num_points + 1] = the largest chunk count of one cell, with
+ * bit 31 set when an adjacency entry is num_points or more; the caller checks
+ * the limits and the flag on the last two before vt_walk_layout_fill (which
+ * links a cell to itself in place of such an entry, and never reads out of
+ * bounds).
  */
-int vt_walk_layout_count(const uint32_t *offsets, uint32_t num_points, uint32_t *first_chunk, void *ws,
-                         vt_stream_t stream);
+int vt_walk_layout_count(const uint32_t *offsets, const uint32_t *adjacency, uint32_t num_points,
+                         uint32_t *first_chunk, void *ws, vt_stream_t stream);
 /*
  * Fill the layout (arrays sized for num_chunks = first_chunk[num_points]).
  * density: the f32 per-cell density the renders integrate; adj_diff from
@@ -156,6 +159,9 @@ int vt_quad_maps_f16(const uint16_t *maps, uint32_t num_points, uint32_t res, ui
  *   vt_prefetch_adj.  rays f32 (num_rays, 6).  start_point u32 (num_rays).
  *   ray_perm u32 (num_rays) or NULL: lane t renders ray ray_perm[t].
  *   rgba out: f16 (num_rays, 4) in ray order.  stats: NULL or (num_rays).
+ * A start cell at or past num_points (which the reference would read out of
+ * bounds) gives its ray no step: rgba (0, 0, 0, 0), n = 0.  This holds for
+ * every inference and training entry; the other rays are unchanged.
  */
 int vt_trace_infer_f16(const float *points, const uint16_t *diffuse, const uint16_t *specular, uint32_t diff_res,
                        uint32_t spec_res, const float *density, const uint32_t *adjacency, const uint32_t *offsets,

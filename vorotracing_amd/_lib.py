@@ -25,7 +25,7 @@ SIGNATURES = {
     "vt_prefetch_adj": ([P, U32, P, U32, P, P, P], C.c_int),
     "vt_trace_infer_f16": ([P, P, P, U32, U32, P, P, P, U32, P, P, U32, P, P, F32, U32, F32, P, P, P], C.c_int),
     "vt_walk_layout_count_workspace_size": ([U32], C.c_size_t),
-    "vt_walk_layout_count": ([P, U32, P, P, P], C.c_int),
+    "vt_walk_layout_count": ([P, P, U32, P, P, P], C.c_int),
     "vt_walk_layout_fill": ([P, P, P, P, U32, P, P, U32, I32, P, P, P, P, P, P], C.c_int),
     "vt_quad_maps_f16": ([P, U32, U32, P, P], C.c_int),
     "vt_trace_infer_f16_tiled": (

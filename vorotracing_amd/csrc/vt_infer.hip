@@ -282,6 +282,7 @@ struct InferArgs {
     const float *rays;
     uint32_t num_rays;
     const uint32_t *start_point;
+    uint32_t num_points; // a start cell at or past it: the ray takes no step
     const uint32_t *ray_perm;
     float thr, skip;
     uint32_t max_steps;
@@ -405,10 +406,14 @@ void infer_kernel(InferArgs a, uint32_t total_slots)
         q.sw[1][lane] = sb.w10;
         q.sw[2][lane] = sb.w01;
         q.sw[3][lane] = sb.w11;
-        if constexpr (PACKED)
+        if (start >= a.num_points) { // out of range: no step, rgba (0, 0, 0, 0)
+            active = false;
+            w.n = 0;
+        } else if constexpr (PACKED) {
             walk_begin_packed(w, a.wl_heads, a.wl_cells, a.wl_chunks, start);
-        else
+        } else {
             walk_begin(w, a.points, a.offsets, start);
+        }
     }
     q.mask[lane] = 0ull;
     if (lane == 0)
@@ -565,8 +570,8 @@ extern "C" int vt_trace_infer_f16(const float *points, const uint16_t *diffuse, 
     int rc = check_common(points, diffuse, specular, density, adjacency, offsets, adj_diff, rays, start_point, rgba);
     if (rc)
         return rc;
-    (void)num_points;
     InferArgs a{};
+    a.num_points = num_points;
     a.points = points;
     a.diffuse = diffuse;
     a.specular = specular;
@@ -606,11 +611,11 @@ extern "C" int vt_trace_infer_f16_tiled(const float *points, const uint16_t *dif
         return rc;
     VT_REQUIRE(tile_h * tile_w == 64, "tile_h * tile_w must be 64 (one wave64 per tile), got %u x %u", tile_h,
                tile_w);
-    (void)num_points;
     uint64_t tiles = (uint64_t)((image_w + tile_w - 1) / tile_w) * ((image_h + tile_h - 1) / tile_h) * num_images;
     VT_REQUIRE(tiles * 64 < (1ull << 32), "image batch too large");
     VT_REQUIRE((uint64_t)num_images * image_h * image_w < (1ull << 32), "image batch too large");
     InferArgs a{};
+    a.num_points = num_points;
     a.points = points;
     a.diffuse = diffuse;
     a.specular = specular;
@@ -661,8 +666,8 @@ extern "C" int vt_trace_infer_q8(const float *points, const uint8_t *diffuse, co
     if (rc)
         return rc;
     VT_REQUIRE(diff_scale && diff_offset && spec_scale && spec_offset, "null dequantisation parameters");
-    (void)num_points;
     InferArgs a{};
+    a.num_points = num_points;
     a.points = points;
     a.diffuse = diffuse;
     a.specular = specular;
@@ -708,11 +713,11 @@ extern "C" int vt_trace_infer_q8_tiled(const float *points, const uint8_t *diffu
     VT_REQUIRE(diff_scale && diff_offset && spec_scale && spec_offset, "null dequantisation parameters");
     VT_REQUIRE(tile_h * tile_w == 64, "tile_h * tile_w must be 64 (one wave64 per tile), got %u x %u", tile_h,
                tile_w);
-    (void)num_points;
     uint64_t tiles = (uint64_t)((image_w + tile_w - 1) / tile_w) * ((image_h + tile_h - 1) / tile_h) * num_images;
     VT_REQUIRE(tiles * 64 < (1ull << 32), "image batch too large");
     VT_REQUIRE((uint64_t)num_images * image_h * image_w < (1ull << 32), "image batch too large");
     InferArgs a{};
+    a.num_points = num_points;
     a.points = points;
     a.diffuse = diffuse;
     a.specular = specular;
@@ -821,8 +826,8 @@ extern "C" int vt_trace_infer_f16_camera(const float *points, const uint16_t *di
                           rgba);
     if (rc)
         return rc;
-    (void)num_points;
     InferArgs a{};
+    a.num_points = num_points;
     a.points = points;
     a.diffuse = diffuse;
     a.specular = specular;
@@ -872,8 +877,8 @@ extern "C" int vt_trace_infer_q8_camera(const float *points, const uint8_t *diff
     if (rc)
         return rc;
     VT_REQUIRE(diff_scale && diff_offset && spec_scale && spec_offset, "null dequantisation parameters");
-    (void)num_points;
     InferArgs a{};
+    a.num_points = num_points;
     a.points = points;
     a.diffuse = diffuse;
     a.specular = specular;

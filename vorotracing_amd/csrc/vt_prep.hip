@@ -705,18 +705,25 @@ __global__ void wl_init_kernel(uint32_t *first_chunk, uint32_t n)
 
 // chunk count of each cell (8 faces per chunk); [n] = 0 so that the scan
 // leaves the total there; [n + 1] = the largest count
-__global__ void wl_count_kernel(const uint32_t *offsets, uint32_t n, uint32_t *first_chunk)
+// One lane per cell: its chunk count, and whether its list holds a
+// neighbour id at or past n (bit 31 of first_chunk[n + 1], which no count
+// reaches).
+__global__ void wl_count_kernel(const uint32_t *offsets, const uint32_t *adjacency, uint32_t n,
+                                uint32_t *first_chunk)
 {
     const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
-    uint32_t k = 0;
+    uint32_t k = 0, bad = 0;
     if (c < n) {
-        k = (uint32_t)(((uint64_t)offsets[c + 1] - offsets[c] + 7u) >> 3);
+        const uint32_t b = offsets[c], e = offsets[c + 1];
+        k = (uint32_t)(((uint64_t)e - b + 7u) >> 3);
         first_chunk[c] = k;
+        for (uint32_t f = b; f < e; ++f)
+            bad |= adjacency[f] >= n ? 1u : 0u;
     } else if (c == n) {
         first_chunk[n] = 0;
     }
-    // one atomic per wave for the largest count
-    k = wave_max_u32(k);
+    // one atomic per wave for the largest count (and the flag)
+    k = wave_max_u32(k | bad << 31);
     if ((threadIdx.x & 63u) == 0 && k)
         atomicMax(first_chunk + n + 1, k);
 }
@@ -788,7 +795,8 @@ __global__ void wl_fill_kernel(const float *__restrict__ points, const float *__
                     const int k = 3 * j + a;
                     w[k >> 1] |= h[a] << (16 * (k & 1));
                 }
-                const uint32_t nb = adjacency[b + f];
+                // an id out of range (flagged by vt_walk_layout_count) links the cell to itself
+                const uint32_t nb = adjacency[b + f] < n ? adjacency[b + f] : c;
                 const uint32_t ncb = fc[nb];
                 lk = make_uint2(nb | (fc[nb + 1] - ncb) << WL_ID_BITS, ncb);
                 og = (uint16_t)f;
@@ -832,16 +840,16 @@ extern "C" size_t vt_walk_layout_count_workspace_size(uint32_t num_points)
     return 4 * scan_workspace_words(num_points + 1);
 }
 
-extern "C" int vt_walk_layout_count(const uint32_t *offsets, uint32_t num_points, uint32_t *first_chunk, void *ws,
-                                    vt_stream_t stream)
+extern "C" int vt_walk_layout_count(const uint32_t *offsets, const uint32_t *adjacency, uint32_t num_points,
+                                    uint32_t *first_chunk, void *ws, vt_stream_t stream)
 {
     clear_error();
-    VT_REQUIRE(offsets && first_chunk && ws, "null pointer argument");
+    VT_REQUIRE(offsets && adjacency && first_chunk && ws, "null pointer argument");
     VT_REQUIRE(num_points < 0xffffffffu, "too many points");
     hipStream_t s = as_stream(stream);
     wl_init_kernel<<<1, 64, 0, s>>>(first_chunk, num_points);
     VT_LAUNCH_CHECK("wl_init_kernel");
-    wl_count_kernel<<<(uint32_t)(((size_t)num_points + 256) / 256), 256, 0, s>>>(offsets, num_points,
+    wl_count_kernel<<<(uint32_t)(((size_t)num_points + 256) / 256), 256, 0, s>>>(offsets, adjacency, num_points,
                                                                               first_chunk);
     VT_LAUNCH_CHECK("wl_count_kernel");
     return exclusive_scan_u32(first_chunk, first_chunk, num_points + 1, (uint32_t *)ws, s);

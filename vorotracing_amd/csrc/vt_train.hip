@@ -231,6 +231,7 @@ struct FwdArgs {
     const uint32_t *ray_perm;          // lane order, or null
     uint32_t num_images, img_h, img_w; // tiled lane order when num_images > 0 and no ray_perm
     const uint32_t *start_point;
+    uint32_t num_points; // a start cell at or past it: the ray takes no step
     uint32_t K;
     const float *quantiles;
     float thr;
@@ -368,8 +369,10 @@ __device__ __forceinline__ uint32_t fwd_ray(const FwdArgs &a, uint32_t r, uint32
     it.W = it.S = it.D = it.self = it.tfar = 0.0f;
     StatsAcc<STATS> st;
     st.begin(a.stats, r);
-    uint32_t n = walk<TRAIN_CHUNK>(it.o, it.d, a.points, a.adjacency, a.offsets, a.adj_diff, a.start_point[r], a.max_steps,
-                         it, st);
+    const uint32_t start = a.start_point[r];
+    const uint32_t n = start < a.num_points ? walk<TRAIN_CHUNK>(it.o, it.d, a.points, a.adjacency, a.offsets,
+                                                                a.adj_diff, start, a.max_steps, it, st)
+                                            : 0u;
     for (uint32_t i = it.qi; i < K; ++i) {
         a.depth[(size_t)r * K + i] = -1.0f;
         a.depth_idx[(size_t)r * K + i] = NONE;
@@ -432,6 +435,7 @@ struct BwdArgs {
     const uint32_t *ray_perm;          // lane order, or null
     uint32_t num_images, img_h, img_w; // tiled lane order when num_images > 0 and no ray_perm
     const uint32_t *start_point;
+    uint32_t num_points; // a start cell at or past it: the ray takes no step
     const void *rgba, *rgba_grad;
     uint32_t K;
     const float *quantiles;
@@ -963,8 +967,10 @@ void bwd_kernel(BwdArgs a)
     it.D_total = (2.0f * fd) * it.dist_grad;
     StatsAcc<STATS> st;
     st.begin(a.stats, r);
-    uint32_t n = walk<TRAIN_BWD_CHUNK>(it.o, it.d, a.points, a.adjacency, a.offsets, a.adj_diff, a.start_point[r], a.max_steps,
-                         it, st);
+    const uint32_t start = a.start_point[r];
+    const uint32_t n = start < a.num_points ? walk<TRAIN_BWD_CHUNK>(it.o, it.d, a.points, a.adjacency, a.offsets,
+                                                                    a.adj_diff, start, a.max_steps, it, st)
+                                            : 0u;
     it.finish();
     st.store(a.stats, r, n);
 }
@@ -1096,6 +1102,7 @@ extern "C" int vt_trace_fwd(int attr_dtype, const float *points, const void *dif
     a.num_rays = num_rays;
     set_lane_order(a, num_rays, ray_perm, image_h, image_w);
     a.start_point = start_point;
+    a.num_points = num_points;
     a.K = depth_quantiles ? num_quantiles : 0;
     a.quantiles = (depth_quantiles && num_quantiles) ? depth_quantiles : nullptr;
     a.thr = weight_threshold;
@@ -1186,6 +1193,7 @@ extern "C" int vt_trace_bwd(int attr_dtype, const float *points, const void *dif
     a.num_rays = num_rays;
     set_lane_order(a, num_rays, ray_perm, image_h, image_w);
     a.start_point = start_point;
+    a.num_points = num_points;
     a.rgba = rgba;
     a.rgba_grad = rgba_grad;
     a.K = depth_quantiles ? num_quantiles : 0;

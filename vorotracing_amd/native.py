@@ -254,7 +254,8 @@ class WalkLayout:
               face_order: int = 3) -> Optional["WalkLayout"]:
         """The layout of a scene (density: f32 per cell, as the renders take
         it; adj_diff from vt_prefetch_adj), or None beyond the limits.  Reads
-        two counts back to the host to size the arrays."""
+        two counts back to the host to size the arrays; raises ValueError when
+        the adjacency names a cell past the scene's last."""
         n = int(points.shape[0])
         if n >= cls.MAX_POINTS:
             return None
@@ -266,9 +267,12 @@ class WalkLayout:
         first = torch.empty(n + 2, dtype=torch.int32, device=dev)
         ws = torch.empty(max(int(lib.vt_walk_layout_count_workspace_size(n)), 1), dtype=torch.uint8, device=dev)
         with torch.cuda.device(dev):
-            _lib.call("vt_walk_layout_count", offsets.data_ptr(), n, first.data_ptr(), ws.data_ptr(), sp)
+            _lib.call("vt_walk_layout_count", offsets.data_ptr(), adjacency.data_ptr(), n, first.data_ptr(),
+                      ws.data_ptr(), sp)
             torch.cuda.synchronize(dev)
             total, most = (int(v) & 0xFFFFFFFF for v in first[n:].cpu().tolist())
+        if most >> 31:
+            raise ValueError(f"the adjacency holds a neighbour id of {n} or more (the scene has {n} cells)")
         if most > cls.MAX_CHUNKS_PER_CELL or total >= (1 << 29):
             return None
         # one chunk past the last: the walk loads a cell's first chunk before it knows the list is not empty
