@@ -127,29 +127,35 @@ int vt_walk_layout_fill(const float *points, const float *density, const uint32_
                         uint32_t *links, uint32_t *heads, float *cells, uint16_t *orig, vt_stream_t stream);
 
 /*
- * Footprint tables of fp16 octahedral maps (extension; no counterpart in the
- * reference: a layout of the Half4Texel maps that vt_trace_infer_f16_tiled
- * and vt_trace_infer_f16_camera can read in place of the maps' texels).  For
- * maps of res x res texels (res 4 or 8), a cell's table has (res + 1)^2
- * entries of 32 bytes.  Entry ey * (res + 1) + ex holds the four Half4Texels
- * that a bilinear tap with floor coordinates (ex - 1, ey - 1) reads, at
- * (ex - 1, ey - 1), (ex, ey - 1), (ex - 1, ey) and (ex, ey), each through the
- * octahedral wrap (oct_wrap_index, ray_integrator_octmap.cuh:36-55).  A tap
- * then reads one entry (two 16-byte loads in one cache line) instead of four
- * 8-byte texels, with the same texels and weights: the images are the same
- * bit for bit.  The tables take (res + 1)^2 / res^2 x 4 the bytes of the maps.
- *   maps: Half4Texel f16 (num_points, 4 * res * res).
- *   quads out: f16 (num_points, 16 * (res + 1)^2), 16-byte aligned.
+ * Footprint tables of octahedral maps (extension; no counterpart in the
+ * reference: a layout of the maps that the tiled and camera inference entries
+ * can read in place of the maps' texels).  For maps of res x res texels
+ * (res 4 or 8), a cell's table has (res + 1)^2 entries.  Entry
+ * ey * (res + 1) + ex holds the four texels that a bilinear tap with floor
+ * coordinates (ex - 1, ey - 1) reads, at (ex - 1, ey - 1), (ex, ey - 1),
+ * (ex - 1, ey) and (ex, ey), each through the octahedral wrap
+ * (oct_wrap_index, ray_integrator_octmap.cuh:36-55), with the same texels and
+ * weights as the maps: the images are the same bit for bit.
+ *   fp16 (vt_quad_maps_f16): maps Half4Texel f16 (num_points, 4 * res * res);
+ *   quads out f16 (num_points, 16 * (res + 1)^2): 32-byte entries, two
+ *   16-byte loads per tap in one cache line instead of four 8-byte texels.
+ *   q8 (vt_quad_maps_q8): maps u8 (num_points, 3 * res * res); quads out u8
+ *   (num_points, 16 * (res + 1)^2): 16-byte entries of four (r, g, b, 0)
+ *   texels, one load per tap instead of twelve single bytes.
+ * quads is 16-byte aligned.
  */
+enum { VT_QUAD_F16 = 0, VT_QUAD_Q8 = 1 };
 typedef struct vt_quad_maps {
-    const uint16_t *diffuse;  /* table of the diffuse map (diff_res) */
-    const uint16_t *specular; /* table of the specular map (spec_res) */
-    uint32_t num_points;      /* cells of the tables; a render checks them */
-    uint32_t diff_res;        /* against its num_points, diff_res and */
-    uint32_t spec_res;        /* spec_res */
+    const void *diffuse;  /* table of the diffuse map (diff_res) */
+    const void *specular; /* table of the specular map (spec_res) */
+    uint32_t num_points;  /* cells of the tables; a render checks them */
+    uint32_t diff_res;    /* against its num_points, diff_res and */
+    uint32_t spec_res;    /* spec_res */
+    uint32_t format;      /* VT_QUAD_F16 or VT_QUAD_Q8, checked against the entry */
 } vt_quad_maps;
 
 int vt_quad_maps_f16(const uint16_t *maps, uint32_t num_points, uint32_t res, uint16_t *quads, vt_stream_t stream);
+int vt_quad_maps_q8(const uint8_t *maps, uint32_t num_points, uint32_t res, uint8_t *quads, vt_stream_t stream);
 
 /*
  * fp16 inference render.  Replaces _C.trace_vorotracing_infer
@@ -215,8 +221,8 @@ int vt_trace_infer_q8(const float *points, const uint8_t *diffuse, const uint8_t
 
 /*
  * q8 inference over image batches with in-kernel wave tiling (as
- * vt_trace_infer_f16_tiled, walk included; per-ray results identical to
- * vt_trace_infer_q8).
+ * vt_trace_infer_f16_tiled, walk and quads (q8 tables) included; per-ray
+ * results identical to vt_trace_infer_q8).
  */
 int vt_trace_infer_q8_tiled(const float *points, const uint8_t *diffuse, const uint8_t *specular, uint32_t diff_res,
                             uint32_t spec_res, const float diff_scale[3], const float diff_offset[3],
@@ -227,7 +233,7 @@ int vt_trace_infer_q8_tiled(const float *points, const uint8_t *diffuse, const u
                             uint32_t rays_per_start, float weight_threshold, uint32_t max_intersections,
                             float cell_skip_threshold,
                             uint16_t *rgba, const uint32_t *tile_order, uint32_t *tile_cost, vt_ray_stats *stats,
-                            const vt_walk_layout *walk, vt_stream_t stream);
+                            const vt_walk_layout *walk, const vt_quad_maps *quads, vt_stream_t stream);
 
 /*
  * Cameras for in-kernel ray generation.  Replaces the rays buffer that the
@@ -276,8 +282,8 @@ int vt_camera_rays(const vt_camera *cameras, uint32_t num_images, uint32_t image
  * vt_camera_rays.  start_point: u32 start cell per image, or per image row
  * ((num_images, image_h)) when start_per_row is non-zero (rolling shutter:
  * every row has its own origin).  rgba (num_images, image_h, image_w, 4) f16;
- * stats in the same ray order.  walk (and quads, fp16): as for
- * vt_trace_infer_f16_tiled.
+ * stats in the same ray order.  walk and quads: as for
+ * vt_trace_infer_f16_tiled (quads of the entry's format).
  */
 int vt_trace_infer_f16_camera(const float *points, const uint16_t *diffuse, const uint16_t *specular,
                               uint32_t diff_res, uint32_t spec_res, const float *density, const uint32_t *adjacency,
@@ -296,7 +302,7 @@ int vt_trace_infer_q8_camera(const float *points, const uint8_t *diffuse, const 
                              const uint32_t *start_point, int start_per_row, float weight_threshold,
                              uint32_t max_intersections, float cell_skip_threshold, uint16_t *rgba,
                              const uint32_t *tile_order, uint32_t *tile_cost, vt_ray_stats *stats,
-                             const vt_walk_layout *walk, vt_stream_t stream);
+                             const vt_walk_layout *walk, const vt_quad_maps *quads, vt_stream_t stream);
 
 /*
  * Training forward.  Replaces _C.trace_vorotracing_fwd

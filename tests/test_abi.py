@@ -26,7 +26,7 @@ def _declarations():
 
 def test_header_declarations_parsed():
     d = _declarations()
-    assert len(d) == 48, sorted(d)
+    assert len(d) == 49, sorted(d)
     for name in ("vt_trace_infer_f16", "vt_trace_fwd", "vt_trace_bwd", "vt_bvh_query", "vt_morton_reorder"):
         assert name in d
 

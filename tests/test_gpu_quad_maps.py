@@ -1,13 +1,13 @@
-"""Footprint tables of the fp16 maps (vt_quad_maps, native.QuadMaps): the
-tables against a numpy construction through the oracle's octahedral wrap, and
-renders that read them, which must equal the renders that read the maps'
+"""Footprint tables of the maps (vt_quad_maps, native.QuadMaps; fp16 and q8):
+the tables against a numpy construction through the oracle's octahedral wrap,
+and renders that read them, which must equal the renders that read the maps'
 texels bit for bit (buffer, camera and drop-in renders, 4x4 and 8x8 maps) and
 stay within the oracle's bound."""
 import numpy as np
 import pytest
 import torch
 
-from oracle import core
+from oracle import core, host_ops
 from tests import helpers as H
 from vorotracing_amd import _C, _lib, camera, native
 
@@ -22,6 +22,27 @@ def _table_np(maps4, R):
     idx = np.array([[core.oct_wrap_index(ex + du - 1, ey + dv - 1, R) for dv in (0, 1) for du in (0, 1)]
                     for ey in range(R + 1) for ex in range(R + 1)], np.int64)
     return tex[:, idx, :].reshape(maps4.shape[0], -1)
+
+
+def _table_q8_np(maps, R):
+    """The q8 table of u8 maps (N, 3 R^2): per entry the four wrapped texels as
+    (r, g, b, 0) bytes."""
+    tex = np.zeros((maps.shape[0], R * R, 4), np.uint8)
+    tex[..., :3] = np.ascontiguousarray(maps).reshape(maps.shape[0], R * R, 3)
+    idx = np.array([[core.oct_wrap_index(ex + du - 1, ey + dv - 1, R) for dv in (0, 1) for du in (0, 1)]
+                    for ey in range(R + 1) for ex in range(R + 1)], np.int64)
+    return tex[:, idx, :].reshape(maps.shape[0], -1)
+
+
+@pytest.mark.parametrize("R", [4, 8])
+def test_quad_tables_q8(gpu, R):
+    rng = np.random.default_rng(10 + R)
+    n = 555
+    maps = rng.integers(0, 256, (n, 3 * R * R), dtype=np.uint8)
+    got = native.QuadMaps.table_q8(H.to_dev(maps, gpu))
+    torch.cuda.synchronize()
+    assert got.shape == (n, 16 * (R + 1) ** 2)
+    assert np.array_equal(got.cpu().numpy(), _table_q8_np(maps, R))
 
 
 @pytest.mark.parametrize("R", [4, 8])
@@ -72,11 +93,17 @@ def test_quad_render_parity(gpu, scene):
         H.assert_infer_rgba(outs[0], want)
         for o in outs[1:]:
             assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16))
-    # tables of another scene (fewer cells) are refused before any launch
+    # tables of another scene (fewer cells) or of the other format are refused before any launch
     few = native.QuadMaps.build(d["diffuse4"][:100], d["specular4"][:100])
     with pytest.raises(_lib.VTError, match="quad maps of 100 cells"):
         native.infer_f16(d["points"], d["diffuse4"], d["specular4"], d["density"], d["adjacency"], d["offsets"],
                          d["adj"], H.to_dev(rays, gpu), H.to_dev(start, gpu), tiled=(8, 8), quads=few)
+    dq = H.to_dev(host_ops.quantize_u8(s.diffuse, True)[0], gpu)
+    sq = H.to_dev(host_ops.quantize_u8(s.specular, True)[0], gpu)
+    with pytest.raises(_lib.VTError, match="format 1"):
+        native.infer_f16(d["points"], d["diffuse4"], d["specular4"], d["density"], d["adjacency"], d["offsets"],
+                         d["adj"], H.to_dev(rays, gpu), H.to_dev(start, gpu), tiled=(8, 8),
+                         quads=native.QuadMaps.build(dq, sq))
 
 
 def test_quad_renders_infer_camera_drop_in(gpu):
@@ -126,3 +153,51 @@ def test_quad_renders_infer_camera_drop_in(gpu):
                 diffuse.mul_(0.5)  # in place: the cached tables must not be reused
     finally:
         _C.DROP_IN_QUADS = True
+
+
+@pytest.mark.parametrize("res", ["r4", "r8"])
+def test_quad_q8_renders(gpu, res):
+    """q8 renders of VoroTracingInfer (buffer and camera) and the q8 drop-in
+    with a lane order: the same image with the q8 tables on and off (the q8
+    parity tests against the oracle run with the tables on, the default)."""
+    from vorotracing_amd.infer import VoroTracingInfer
+    from vorotracing_amd.model import VoroTracing
+    s = H.mini_heightfield() if res == "r4" else H.mini_heightfield_r8()
+    inf = VoroTracingInfer(VoroTracing.from_scene(s, device=gpu), sort_morton=True, quantize="q8",
+                           per_channel_q8=True)
+    qt = inf.quad_tables()
+    assert qt is not None and qt.format == native.QUAD_Q8
+    kw = dict(weight_threshold=0.01, cell_skip_threshold=1e-3)
+    rays = H.to_dev(camera.orbit_rays(5, 128, 96), gpu)
+    cams = [camera.Camera.orbit(5, 128, 96)]
+    outs = {}
+    try:
+        for on in (True, False):
+            VoroTracingInfer.quad_maps = on
+            print(f"case: q8 {res} renders, quad maps {on}", flush=True)
+            outs[on] = (inf.render(rays, **kw), inf.render_cameras(cams, **kw))
+    finally:
+        VoroTracingInfer.quad_maps = True
+    torch.cuda.synchronize()
+    for a, b in zip(outs[True], outs[False]):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    sp = inf.get_starting_point(rays)
+    perm = torch.arange(rays.numel() // 6, dtype=torch.int32, device=gpu)
+
+    def render():
+        return _C.trace_vorotracing_infer_q8(inf.primal_points, inf.diffuse_q8, inf.specular_q8, inf.density,
+                                             inf.point_adjacency, inf.point_adjacency_offsets, rays, sp,
+                                             inf.adjacent_diff, inf.diff_scale, inf.diff_offset, inf.spec_scale,
+                                             inf.spec_offset, 0.01, 1024, 1e-3, ray_perm_in=perm)
+
+    try:
+        print(f"case: q8 {res} drop-in, quad maps on/off", flush=True)
+        _C.DROP_IN_QUADS = False
+        plain = render()
+        _C.DROP_IN_QUADS = True
+        quad = render()
+        torch.cuda.synchronize()
+    finally:
+        _C.DROP_IN_QUADS = True
+    assert torch.equal(quad.view(torch.int16), plain.view(torch.int16))
+    assert torch.equal(quad.view(torch.int16), outs[True][0].view(torch.int16))

@@ -159,10 +159,11 @@ def _drop_in_walk(srcs_in, srcs) -> Optional["native.WalkLayout"]:
     return entry[1]
 
 
-# Footprint tables (native.QuadMaps) of the fp16 maps the tiled drop-in
-# renders read: built on a scene's first image render and reused while the
-# caller's two map tensors are the same, unchanged.  A bilinear tap then reads
-# its four texels with two 16-byte loads; the image is the same.
+# Footprint tables (native.QuadMaps) of the maps the tiled drop-in renders
+# read (fp16 or q8): built on a scene's first image render and reused while
+# the caller's two map tensors are the same, unchanged.  A bilinear tap then
+# reads its four texels with two 16-byte loads (fp16) or one (q8); the image
+# is the same.
 DROP_IN_QUADS = True
 _QUAD_MAPS: list = []
 
@@ -394,6 +395,7 @@ def trace_vorotracing_infer_q8(points_in, diffuse_in, specular_in, density_in, p
                       native._walk_ptr(_drop_in_walk(
                           (points_in, density_in, point_adjacency_in, point_adjacency_offsets_in, adjacent_diff_in),
                           (points, density, adjacency, offsets, adjacent_diff))),
+                      native._quads_ptr(_drop_in_quads((diffuse_in, specular_in), (diffuse, specular))),
                       _stream(rays.device))
         else:
             _lib.call("vt_trace_infer_q8", points.data_ptr(), diffuse.data_ptr(), specular.data_ptr(), rd, rs,

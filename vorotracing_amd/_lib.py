@@ -28,6 +28,7 @@ SIGNATURES = {
     "vt_walk_layout_count": ([P, P, U32, P, P, P], C.c_int),
     "vt_walk_layout_fill": ([P, P, P, P, U32, P, P, U32, I32, P, P, P, P, P, P], C.c_int),
     "vt_quad_maps_f16": ([P, U32, U32, P, P], C.c_int),
+    "vt_quad_maps_q8": ([P, U32, U32, P, P], C.c_int),
     "vt_trace_infer_f16_tiled": (
         [P, P, P, U32, U32, P, P, P, U32, P, P, U32, U32, U32, U32, U32, P, U32, F32, U32, F32, P, P, P, P, P, P, P],
         C.c_int),
@@ -35,14 +36,14 @@ SIGNATURES = {
         [P, P, P, U32, U32, P, P, P, P, P, P, P, U32, P, P, U32, P, P, F32, U32, F32, P, P, P], C.c_int),
     "vt_trace_infer_q8_tiled": (
         [P, P, P, U32, U32, P, P, P, P, P, P, P, U32, P, P, U32, U32, U32, U32, U32, P, U32, F32, U32, F32, P, P, P, P,
-         P, P], C.c_int),
+         P, P, P], C.c_int),
     "vt_camera_rays": ([P, U32, U32, U32, P, P], C.c_int),
     "vt_trace_infer_f16_camera": (
         [P, P, P, U32, U32, P, P, P, U32, P, P, U32, U32, U32, U32, U32, P, I32, F32, U32, F32, P, P, P, P, P, P, P],
         C.c_int),
     "vt_trace_infer_q8_camera": (
         [P, P, P, U32, U32, P, P, P, P, P, P, P, U32, P, P, U32, U32, U32, U32, U32, P, I32, F32, U32, F32, P, P, P, P, P,
-         P], C.c_int),
+         P, P], C.c_int),
     "vt_trace_fwd": (
         [I32, P, P, P, U32, U32, P, P, U32, P, U32, P, U32, U32, U32, P, P, U32, P, F32, U32, P, P, P, P, P, P, P, P,
          P, P, P, P, P, P],

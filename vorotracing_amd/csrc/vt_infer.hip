@@ -68,20 +68,47 @@ template <int RD, int RS, bool QUADS> struct TexF16 {
     }
 };
 
-// q8 maps: texel = 3 bytes, dequant = scale[c] * q + offset[c]
-template <int RD, int RS> struct TexQ8 {
-    const uint8_t *diffuse;
+// q8 maps: texel = 3 bytes, dequant = scale[c] * q + offset[c].  QUADS: the
+// maps' q8 footprint tables (vt_quad_maps) are read instead, a tap's four
+// texels (r, g, b, 0 bytes each) as one 16-byte entry instead of twelve single
+// bytes; the bytes and weights are the same, so is the colour.
+template <int RD, int RS, bool QUADS> struct TexQ8 {
+    const uint8_t *diffuse; // maps, or footprint tables (QUADS)
     const uint8_t *specular;
     float ds[3], dof[3], ss[3], sof[3];
 
-    __device__ __forceinline__ static constexpr bool quads() { return false; }
+    __device__ __forceinline__ static constexpr bool quads() { return QUADS; }
     __device__ __forceinline__ f3 sample_diffuse(uint32_t cell, const Bilinear &b) const
     {
-        return sample(diffuse + (size_t)cell * (3 * RD * RD), b, ds, dof);
+        if constexpr (QUADS)
+            return sample_quad(reinterpret_cast<const uint4 *>(diffuse)[(size_t)cell * ((RD + 1) * (RD + 1)) +
+                                                                         (uint32_t)b.i00],
+                               b, ds, dof);
+        else
+            return sample(diffuse + (size_t)cell * (3 * RD * RD), b, ds, dof);
     }
     __device__ __forceinline__ f3 sample_specular(uint32_t cell, const Bilinear &b) const
     {
-        return sample(specular + (size_t)cell * (3 * RS * RS), b, ss, sof);
+        if constexpr (QUADS)
+            return sample_quad(reinterpret_cast<const uint4 *>(specular)[(size_t)cell * ((RS + 1) * (RS + 1)) +
+                                                                          (uint32_t)b.i00],
+                               b, ss, sof);
+        else
+            return sample(specular + (size_t)cell * (3 * RS * RS), b, ss, sof);
+    }
+    // entry words: texels (u0, v0), (u0 + 1, v0), (u0, v0 + 1), (u0 + 1, v0 + 1)
+    __device__ __forceinline__ static f3 sample_quad(uint4 e, const Bilinear &b, const float *sc, const float *of)
+    {
+        float v[3];
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            float a = fma_(sc[c], (float)((e.x >> (8 * c)) & 0xffu), of[c]);
+            float bb = fma_(sc[c], (float)((e.y >> (8 * c)) & 0xffu), of[c]);
+            float cc = fma_(sc[c], (float)((e.z >> (8 * c)) & 0xffu), of[c]);
+            float d = fma_(sc[c], (float)((e.w >> (8 * c)) & 0xffu), of[c]);
+            v[c] = bil_mix(b, a, bb, cc, d);
+        }
+        return mk(v[0], v[1], v[2]);
     }
     __device__ __forceinline__ static f3 sample(const uint8_t *m, const Bilinear &b, const float *sc,
                                                 const float *of)
@@ -354,13 +381,12 @@ void infer_kernel(InferArgs a, uint32_t total_slots)
     const uint32_t s = xcd_interleaved_block<INFER_XCD_CHUNK>() * blockDim.x + threadIdx.x;
     const uint32_t r = s < total_slots ? slot_to_ray(a, s, MAP) : NONE;
     bool active = r != NONE;
-    static_assert(!(Q8 && QUADS), "footprint tables hold fp16 texels");
-    using Tex = typename std::conditional<Q8, TexQ8<RD, RS>, TexF16<RD, RS, QUADS>>::type;
+    using Tex = typename std::conditional<Q8, TexQ8<RD, RS, QUADS>, TexF16<RD, RS, QUADS>>::type;
     InferIntegrator<RD, RS, Tex> integ;
     integ.density = a.density;
     if constexpr (Q8) {
-        integ.tex.diffuse = (const uint8_t *)a.diffuse;
-        integ.tex.specular = (const uint8_t *)a.specular;
+        integ.tex.diffuse = (const uint8_t *)(QUADS ? a.quad_d : a.diffuse);
+        integ.tex.specular = (const uint8_t *)(QUADS ? a.quad_s : a.specular);
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
             integ.tex.ds[c] = a.ds[c];
@@ -461,17 +487,14 @@ template <int RD, int RS, bool Q8, bool STATS, int MAP>
 static int launch_one(const InferArgs &a, hipStream_t stream, uint32_t slots)
 {
     uint32_t blocks = (slots + INFER_BLOCK - 1) / INFER_BLOCK;
-    if constexpr (!Q8) {
-        if (a.quad_d) {
-            if (a.wl_chunks)
-                infer_kernel<RD, RS, false, STATS, MAP, INFER_CHUNK, true, true>
-                    <<<blocks, INFER_BLOCK, 0, stream>>>(a, slots);
-            else
-                infer_kernel<RD, RS, false, STATS, MAP, INFER_CHUNK, false, true>
-                    <<<blocks, INFER_BLOCK, 0, stream>>>(a, slots);
-            VT_LAUNCH_CHECK("infer_kernel");
-            return VT_OK;
-        }
+    if (a.quad_d) {
+        if (a.wl_chunks)
+            infer_kernel<RD, RS, Q8, STATS, MAP, INFER_CHUNK, true, true><<<blocks, INFER_BLOCK, 0, stream>>>(a, slots);
+        else
+            infer_kernel<RD, RS, Q8, STATS, MAP, INFER_CHUNK, false, true><<<blocks, INFER_BLOCK, 0, stream>>>(a,
+                                                                                                            slots);
+        VT_LAUNCH_CHECK("infer_kernel");
+        return VT_OK;
     }
     if (a.wl_chunks)
         infer_kernel<RD, RS, Q8, STATS, MAP, INFER_CHUNK, true, false><<<blocks, INFER_BLOCK, 0, stream>>>(a, slots);
@@ -539,11 +562,13 @@ static int set_walk_layout(InferArgs &a, const vt_walk_layout *walk)
 
 // The footprint tables of a call, or the maps' texels when quads is NULL.
 static int set_quad_maps(InferArgs &a, const vt_quad_maps *quads, uint32_t num_points, uint32_t diff_res,
-                         uint32_t spec_res)
+                         uint32_t spec_res, uint32_t format)
 {
     if (!quads)
         return VT_OK;
     VT_REQUIRE(quads->diffuse && quads->specular, "null table in the quad maps");
+    VT_REQUIRE(quads->format == format, "quad maps of format %u (0 fp16, 1 q8) given to a %s render", quads->format,
+               format == VT_QUAD_Q8 ? "q8" : "fp16");
     VT_REQUIRE(quads->num_points == num_points && quads->diff_res == diff_res && quads->spec_res == spec_res,
                "quad maps of %u cells at %u/%u texels per side, the render has %u cells at %u/%u",
                quads->num_points, quads->diff_res, quads->spec_res, num_points, diff_res, spec_res);
@@ -638,7 +663,7 @@ extern "C" int vt_trace_infer_f16_tiled(const float *points, const uint16_t *dif
     rc = set_walk_layout(a, walk);
     if (rc)
         return rc;
-    rc = set_quad_maps(a, quads, num_points, diff_res, spec_res);
+    rc = set_quad_maps(a, quads, num_points, diff_res, spec_res, VT_QUAD_F16);
     if (rc)
         return rc;
     a.num_images = num_images;
@@ -702,7 +727,8 @@ extern "C" int vt_trace_infer_q8_tiled(const float *points, const uint8_t *diffu
                                        uint32_t tile_h, uint32_t tile_w, const uint32_t *start_point,
                                        uint32_t rays_per_start, float weight_threshold, uint32_t max_intersections, float cell_skip_threshold,
                                        uint16_t *rgba, const uint32_t *tile_order, uint32_t *tile_cost,
-                                       vt_ray_stats *stats, const vt_walk_layout *walk, vt_stream_t stream)
+                                       vt_ray_stats *stats, const vt_walk_layout *walk,
+                                       const vt_quad_maps *quads, vt_stream_t stream)
 {
     clear_error();
     if (num_images == 0 || image_h == 0 || image_w == 0)
@@ -737,6 +763,9 @@ extern "C" int vt_trace_infer_q8_tiled(const float *points, const uint8_t *diffu
     a.tile_order = tile_order;
     a.tile_cost = tile_cost;
     rc = set_walk_layout(a, walk);
+    if (rc)
+        return rc;
+    rc = set_quad_maps(a, quads, num_points, diff_res, spec_res, VT_QUAD_Q8);
     if (rc)
         return rc;
     a.num_images = num_images;
@@ -846,7 +875,7 @@ extern "C" int vt_trace_infer_f16_camera(const float *points, const uint16_t *di
     rc = set_walk_layout(a, walk);
     if (rc)
         return rc;
-    rc = set_quad_maps(a, quads, num_points, diff_res, spec_res);
+    rc = set_quad_maps(a, quads, num_points, diff_res, spec_res, VT_QUAD_F16);
     if (rc)
         return rc;
     a.H = image_h;
@@ -867,7 +896,8 @@ extern "C" int vt_trace_infer_q8_camera(const float *points, const uint8_t *diff
                                         const uint32_t *start_point, int start_per_row, float weight_threshold,
                                         uint32_t max_intersections, float cell_skip_threshold, uint16_t *rgba,
                                         const uint32_t *tile_order, uint32_t *tile_cost,
-                                        vt_ray_stats *stats, const vt_walk_layout *walk, vt_stream_t stream)
+                                        vt_ray_stats *stats, const vt_walk_layout *walk,
+                                        const vt_quad_maps *quads, vt_stream_t stream)
 {
     clear_error();
     if (num_images == 0 || image_h == 0 || image_w == 0)
@@ -895,6 +925,9 @@ extern "C" int vt_trace_infer_q8_camera(const float *points, const uint8_t *diff
     a.tile_order = tile_order;
     a.tile_cost = tile_cost;
     rc = set_walk_layout(a, walk);
+    if (rc)
+        return rc;
+    rc = set_quad_maps(a, quads, num_points, diff_res, spec_res, VT_QUAD_Q8);
     if (rc)
         return rc;
     a.H = image_h;

@@ -816,6 +816,26 @@ __global__ void wl_fill_kernel(const float *__restrict__ points, const float *__
 // (ex - 1, ey - 1), (ex, ey - 1), (ex - 1, ey), (ex, ey), the ones
 // bilinear_setup reads for floor coordinates (ex - 1, ey - 1).  Coordinates
 // stay in [-1, R], the range oct_wrap_edge reduces.
+// The q8 footprint tables: as quad_maps_kernel below, each texel's three bytes
+// widened to one (r, g, b, 0) word, an entry one 16-byte word.
+template <int R>
+__global__ void quad_maps_q8_kernel(const uint8_t *__restrict__ maps, uint32_t n, uint4 *__restrict__ quads)
+{
+    constexpr uint32_t E = (R + 1) * (R + 1);
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (uint64_t)n * E)
+        return;
+    const uint64_t c = i / E;
+    const int e = (int)(i - c * E);
+    const int ex = e % (R + 1), ey = e / (R + 1);
+    const uint8_t *m = maps + c * (3 * R * R);
+    auto texel = [&](int t) {
+        return (uint32_t)m[3 * t] | (uint32_t)m[3 * t + 1] << 8 | (uint32_t)m[3 * t + 2] << 16;
+    };
+    quads[i] = make_uint4(texel(oct_wrap_edge<R>(ex - 1, ey - 1)), texel(oct_wrap_edge<R>(ex, ey - 1)),
+                          texel(oct_wrap_edge<R>(ex - 1, ey)), texel(oct_wrap_edge<R>(ex, ey)));
+}
+
 template <int R>
 __global__ void quad_maps_kernel(const uint2 *__restrict__ maps, uint32_t n, uint4 *__restrict__ quads)
 {
@@ -900,5 +920,27 @@ extern "C" int vt_quad_maps_f16(const uint16_t *maps, uint32_t num_points, uint3
         quad_maps_kernel<8><<<(uint32_t)blocks, 256, 0, as_stream(stream)>>>(
             reinterpret_cast<const uint2 *>(maps), num_points, reinterpret_cast<uint4 *>(quads));
     VT_LAUNCH_CHECK("quad_maps_kernel");
+    return VT_OK;
+}
+
+extern "C" int vt_quad_maps_q8(const uint8_t *maps, uint32_t num_points, uint32_t res, uint8_t *quads,
+                               vt_stream_t stream)
+{
+    clear_error();
+    VT_REQUIRE(res == 4 || res == 8, "res must be 4 or 8, got %u", res);
+    if (num_points == 0)
+        return VT_OK;
+    VT_REQUIRE(maps && quads, "null pointer argument");
+    VT_REQUIRE((reinterpret_cast<uintptr_t>(quads) & 15u) == 0, "quads must be 16-byte aligned");
+    const uint64_t lanes = (uint64_t)num_points * (res + 1) * (res + 1);
+    const uint64_t blocks = (lanes + 255) / 256;
+    VT_REQUIRE(blocks < (1ull << 31), "too many cells for one launch: %u", num_points);
+    if (res == 4)
+        quad_maps_q8_kernel<4><<<(uint32_t)blocks, 256, 0, as_stream(stream)>>>(maps, num_points,
+                                                                               reinterpret_cast<uint4 *>(quads));
+    else
+        quad_maps_q8_kernel<8><<<(uint32_t)blocks, 256, 0, as_stream(stream)>>>(maps, num_points,
+                                                                               reinterpret_cast<uint4 *>(quads));
+    VT_LAUNCH_CHECK("quad_maps_q8_kernel");
     return VT_OK;
 }

@@ -32,9 +32,9 @@ class VoroTracingInfer:
     # (face_order 3; 0 keeps the list order); images are bit-identical either way
     packed_walk = True
     face_order = 3
-    # read the fp16 maps through their footprint tables (native.QuadMaps: a
-    # bilinear tap's four texels in one 32-byte entry) in the tiled and
-    # camera renders; images are bit-identical either way
+    # read the maps through their footprint tables (native.QuadMaps: a
+    # bilinear tap's four texels in one entry, 32 bytes for fp16 maps, 16 for
+    # q8) in the tiled and camera renders; images are bit-identical either way
     quad_maps = True
 
     def __init__(self, model, sort_morton: bool = True, quantize: Literal["fp16", "q8"] = "fp16",
@@ -77,12 +77,13 @@ class VoroTracingInfer:
         self._quad_maps = None
 
     def quad_tables(self) -> Optional[native.QuadMaps]:
-        """The footprint tables of the fp16 maps (built on first use, and
-        again when the maps have been replaced or changed in place), or None
-        for q8 maps or when ``quad_maps`` is off."""
-        if not self.quad_maps or self.quantize != "fp16":
+        """The footprint tables of the maps (fp16 or q8; built on first use,
+        and again when the maps have been replaced or changed in place), or
+        None when ``quad_maps`` is off."""
+        if not self.quad_maps:
             return None
-        src = (self.diffuse_fp16, self.specular_fp16)
+        src = (self.diffuse_q8, self.specular_q8) if self.quantize == "q8" else (self.diffuse_fp16,
+                                                                                  self.specular_fp16)
         entry = self.__dict__.get("_quad_maps")
         if entry is None or not entry.source.matches(*src):
             entry = native.QuadMaps.build(*src)
@@ -398,7 +399,8 @@ class VoroTracingInfer:
                       self.specular_q8.data_ptr(), rd, rs, *keep, self.density.data_ptr(),
                       self.point_adjacency.data_ptr(), self.point_adjacency_offsets.data_ptr(),
                       self.primal_points.shape[0], self.adjacent_diff.data_ptr(), camera_buffer.data_ptr(), B, H, W,
-                      self.TILE[0], self.TILE[1], start_point.data_ptr(), int(per_row), *common, sp)
+                      self.TILE[0], self.TILE[1], start_point.data_ptr(), int(per_row), *common,
+                      native._quads_ptr(self.quad_tables()), sp)
         else:
             rd = native.map_res(self.diffuse_fp16.shape[-1], 4)
             rs = native.map_res(self.specular_fp16.shape[-1], 4)
@@ -436,7 +438,7 @@ class VoroTracingInfer:
                       self.primal_points.shape[0], self.adjacent_diff.data_ptr(), rays.data_ptr(), B, H, W,
                       self.TILE[0], self.TILE[1], start_point.data_ptr(), int(rays_per_start), float(thr),
                       int(max_int), float(skip), out.data_ptr(), order, cost, native._p(stats),
-                      native._walk_ptr(self.walk_layout()), sp)
+                      native._walk_ptr(self.walk_layout()), native._quads_ptr(self.quad_tables()), sp)
         else:
             _lib.call("vt_trace_infer_q8", self.primal_points.data_ptr(), self.diffuse_q8.data_ptr(),
                       self.specular_q8.data_ptr(), rd, rs, *keep, self.density.data_ptr(),

@@ -294,24 +294,29 @@ def _walk_ptr(walk: Optional[WalkLayout]):
 
 class _QuadMapsC(C.Structure):
     _fields_ = [("diffuse", C.c_void_p), ("specular", C.c_void_p), ("num_points", C.c_uint32),
-                ("diff_res", C.c_uint32), ("spec_res", C.c_uint32)]
+                ("diff_res", C.c_uint32), ("spec_res", C.c_uint32), ("format", C.c_uint32)]
+
+
+QUAD_F16, QUAD_Q8 = 0, 1
 
 
 class QuadMaps:
-    """Footprint tables of a scene's fp16 octahedral maps (vt_quad_maps): per
-    cell, (R + 1)^2 entries of 32 bytes, each the four wrapped texels of one
-    bilinear tap, so that the fp16 inference kernels read a tap with two
-    16-byte loads instead of four 8-byte ones and render the same images bit
-    for bit.  The tables take (R + 1)^2 / R^2 x 4 the bytes of the maps.
-    ``source`` (a SourceKey) tells whether the maps they were built from are
-    still the given tensors, unchanged."""
+    """Footprint tables of a scene's octahedral maps (vt_quad_maps): per cell,
+    (R + 1)^2 entries, each the four wrapped texels of one bilinear tap, so
+    that the inference kernels read a tap with two 16-byte loads (fp16 maps:
+    32-byte entries, instead of four 8-byte texels) or one (q8 maps: 16-byte
+    entries, instead of twelve bytes) and render the same images bit for bit.
+    ``format`` is QUAD_F16 or QUAD_Q8.  ``source`` (a SourceKey) tells whether
+    the maps they were built from are still the given tensors, unchanged."""
 
-    def __init__(self, diffuse, specular, num_points: int, diff_res: int, spec_res: int, sources=()):
+    def __init__(self, diffuse, specular, num_points: int, diff_res: int, spec_res: int, sources=(),
+                 format: int = QUAD_F16):
         self.diffuse, self.specular = diffuse, specular
         self.num_points, self.diff_res, self.spec_res = int(num_points), int(diff_res), int(spec_res)
+        self.format = int(format)
         self.source = SourceKey(*sources)
         self._c = _QuadMapsC(diffuse.data_ptr(), specular.data_ptr(), self.num_points, self.diff_res,
-                             self.spec_res)
+                             self.spec_res, self.format)
 
     @property
     def ptr(self) -> int:
@@ -329,13 +334,28 @@ class QuadMaps:
             _lib.call("vt_quad_maps_f16", maps4.data_ptr(), n, res, out.data_ptr(), _s(maps4.device, stream))
         return out
 
+    @staticmethod
+    def table_q8(maps_q8, stream=None):
+        """The footprint table of one q8 map (u8 (N, 3 R^2))."""
+        maps_q8 = maps_q8.contiguous()
+        res = map_res(maps_q8.shape[-1], 3)
+        n = maps_q8.numel() // (3 * res * res)
+        out = torch.empty((max(n, 1), 16 * (res + 1) ** 2), dtype=torch.uint8, device=maps_q8.device)
+        with torch.cuda.device(maps_q8.device):
+            _lib.call("vt_quad_maps_q8", maps_q8.data_ptr(), n, res, out.data_ptr(), _s(maps_q8.device, stream))
+        return out
+
     @classmethod
-    def build(cls, diffuse4, specular4, stream=None) -> "QuadMaps":
-        """The tables of a scene's two Half4Texel maps (one row per cell)."""
-        if diffuse4.shape[0] != specular4.shape[0]:
-            raise ValueError(f"the maps have {diffuse4.shape[0]} and {specular4.shape[0]} rows")
-        return cls(cls.table(diffuse4, stream), cls.table(specular4, stream), diffuse4.shape[0],
-                   map_res(diffuse4.shape[-1], 4), map_res(specular4.shape[-1], 4), (diffuse4, specular4))
+    def build(cls, diffuse, specular, stream=None) -> "QuadMaps":
+        """The tables of a scene's two maps (one row per cell): Half4Texel f16
+        maps give fp16 tables, u8 maps q8 tables."""
+        if diffuse.shape[0] != specular.shape[0]:
+            raise ValueError(f"the maps have {diffuse.shape[0]} and {specular.shape[0]} rows")
+        if diffuse.dtype == torch.uint8:
+            return cls(cls.table_q8(diffuse, stream), cls.table_q8(specular, stream), diffuse.shape[0],
+                       map_res(diffuse.shape[-1], 3), map_res(specular.shape[-1], 3), (diffuse, specular), QUAD_Q8)
+        return cls(cls.table(diffuse, stream), cls.table(specular, stream), diffuse.shape[0],
+                   map_res(diffuse.shape[-1], 4), map_res(specular.shape[-1], 4), (diffuse, specular), QUAD_F16)
 
 
 def _quads_ptr(quads: Optional[QuadMaps]):
