@@ -201,3 +201,27 @@ def test_quad_q8_renders(gpu, res):
         _C.DROP_IN_QUADS = True
     assert torch.equal(quad.view(torch.int16), plain.view(torch.int16))
     assert torch.equal(quad.view(torch.int16), outs[True][0].view(torch.int16))
+
+
+def test_quad_tables_memory_guard(gpu):
+    """Tables that would take more than QuadMaps.MAX_FREE_SHARE of the free
+    memory are not built; the renders then read the maps, with the same image."""
+    from vorotracing_amd.infer import VoroTracingInfer
+    from vorotracing_amd.model import VoroTracing
+    s = H.mini_heightfield()
+    model = VoroTracing.from_scene(s, device=gpu)
+    kw = dict(weight_threshold=0.01, cell_skip_threshold=1e-3)
+    rays = H.to_dev(camera.orbit_rays(7, 96, 64), gpu)
+    inf = VoroTracingInfer(model, sort_morton=True, quantize="fp16")
+    assert inf.quad_tables() is not None
+    with_tables = inf.render(rays, **kw)
+    share = native.QuadMaps.MAX_FREE_SHARE
+    try:
+        native.QuadMaps.MAX_FREE_SHARE = 0.0
+        lean = VoroTracingInfer(model, sort_morton=True, quantize="fp16")
+        assert lean.quad_tables() is None
+        without = lean.render(rays, **kw)
+    finally:
+        native.QuadMaps.MAX_FREE_SHARE = share
+    torch.cuda.synchronize()
+    assert torch.equal(with_tables.view(torch.int16), without.view(torch.int16))

@@ -145,3 +145,15 @@ def test_walk_layout_np_round_trip():
                 assert np.all(np.diff(z) >= 0)
                 ties = np.diff(z) == 0
                 assert np.all(np.diff(np.array(seen))[ties] > 0)
+
+
+def test_quad_table_bytes():
+    """The footprint tables' size: (R + 1)^2 entries per map and cell, 32
+    bytes for fp16 maps, 16 for q8."""
+    from vorotracing_amd import native
+    f16 = torch.zeros((10, 4 * 16), dtype=torch.float16)
+    f16_8 = torch.zeros((10, 4 * 64), dtype=torch.float16)
+    q8 = torch.zeros((10, 3 * 16), dtype=torch.uint8)
+    assert native.QuadMaps.table_bytes(f16, f16) == 10 * 32 * 25 * 2
+    assert native.QuadMaps.table_bytes(f16_8, f16) == 10 * 32 * (81 + 25)
+    assert native.QuadMaps.table_bytes(q8, q8) == 10 * 16 * 25 * 2

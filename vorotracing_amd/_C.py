@@ -171,18 +171,18 @@ _QUAD_MAPS: list = []
 def _drop_in_quads(maps_in, maps) -> Optional["native.QuadMaps"]:
     """The footprint tables of the maps ``maps_in`` (diffuse, specular as the
     caller passed them), built from their contiguous forms ``maps``; None
-    when off."""
+    when off or when they would take too much of the free memory."""
     if not DROP_IN_QUADS:
         return None
-    for i, qm in enumerate(_QUAD_MAPS):
-        if qm.source.matches(*maps_in):
+    for i, (key, qm) in enumerate(_QUAD_MAPS):
+        if key.matches(*maps_in):
             _QUAD_MAPS.append(_QUAD_MAPS.pop(i))
             return qm
-    qm = native.QuadMaps.build(*maps)
-    qm.source = native.SourceKey(*maps_in)
-    _QUAD_MAPS.append(qm)
+    # None when the tables would take too much of the free memory (native.QuadMaps.MAX_FREE_SHARE)
+    entry = (native.SourceKey(*maps_in), native.QuadMaps.build_within(*maps))
+    _QUAD_MAPS.append(entry)
     del _QUAD_MAPS[:-2]
-    return qm
+    return entry[1]
 
 
 # Tile launch schedules of the training entries for tiled rays, keyed by the

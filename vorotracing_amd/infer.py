@@ -79,16 +79,18 @@ class VoroTracingInfer:
     def quad_tables(self) -> Optional[native.QuadMaps]:
         """The footprint tables of the maps (fp16 or q8; built on first use,
         and again when the maps have been replaced or changed in place), or
-        None when ``quad_maps`` is off."""
+        None when ``quad_maps`` is off or the tables would take more than a
+        quarter of the device's free memory (the renders then read the maps)."""
         if not self.quad_maps:
             return None
         src = (self.diffuse_q8, self.specular_q8) if self.quantize == "q8" else (self.diffuse_fp16,
                                                                                   self.specular_fp16)
         entry = self.__dict__.get("_quad_maps")
-        if entry is None or not entry.source.matches(*src):
-            entry = native.QuadMaps.build(*src)
+        if entry is None or not entry[0].matches(*src):
+            # None when the tables would take too much of the free memory (QuadMaps.MAX_FREE_SHARE)
+            entry = (native.SourceKey(*src), native.QuadMaps.build_within(*src))
             self._quad_maps = entry
-        return entry
+        return entry[1]
 
     def walk_layout(self) -> Optional[native.WalkLayout]:
         """The scene's packed walk layout (built on first use, and again when

@@ -345,6 +345,28 @@ class QuadMaps:
             _lib.call("vt_quad_maps_q8", maps_q8.data_ptr(), n, res, out.data_ptr(), _s(maps_q8.device, stream))
         return out
 
+    # the share of the device's free memory the tables may take; beyond it
+    # build_within returns None and the renders read the maps themselves
+    MAX_FREE_SHARE = 0.25
+
+    @staticmethod
+    def table_bytes(diffuse, specular) -> int:
+        """Bytes of the two tables of these maps."""
+        q8 = diffuse.dtype == torch.uint8
+        per = 16 if q8 else 32
+        rd = map_res(diffuse.shape[-1], 3 if q8 else 4)
+        rs = map_res(specular.shape[-1], 3 if q8 else 4)
+        return int(diffuse.shape[0]) * per * ((rd + 1) ** 2 + (rs + 1) ** 2)
+
+    @classmethod
+    def build_within(cls, diffuse, specular, stream=None) -> Optional["QuadMaps"]:
+        """build(), or None when the tables would take more than
+        MAX_FREE_SHARE of the device's free memory."""
+        free, _ = torch.cuda.mem_get_info(diffuse.device)
+        if cls.table_bytes(diffuse, specular) > cls.MAX_FREE_SHARE * free:
+            return None
+        return cls.build(diffuse, specular, stream)
+
     @classmethod
     def build(cls, diffuse, specular, stream=None) -> "QuadMaps":
         """The tables of a scene's two maps (one row per cell): Half4Texel f16
