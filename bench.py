@@ -154,6 +154,9 @@ def main():
     ap.add_argument("--no-c5", action="store_true", help="skip the config-5 fisheye rolling-shutter training step")
     ap.add_argument("--c5-only", action="store_true", help="only the config-5 training step")
     ap.add_argument("--voronoi-only", action="store_true", help="only the GPU Voronoi build (profiling)")
+    ap.add_argument("--compare-layouts", action="store_true",
+                    help="only 4 serial C3 frames (poses 0, 8, 21, 5) through the packed walk layout and footprint "
+                         "tables, then through the reference's arrays and texels, in screen order (rocprofv3 --pmc)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run 8 device copies of 1 GiB (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
@@ -198,6 +201,17 @@ def main():
     inf = VoroTracingInfer(model, sort_morton=True, quantize="fp16")
     torch.cuda.synchronize()
     log(f"inference prep done ({time.time() - t0:.1f}s)")
+    if args.compare_layouts:
+        inf.adaptive_tile_order = False
+        views = [torch.from_numpy(camera.orbit_rays(k, args.width, args.height)).to(dev) for k in (0, 8, 21, 5)]
+        frames = {}
+        for layouts in (True, False):
+            inf.packed_walk = inf.quad_maps = layouts
+            frames[layouts] = [inf.render(r, weight_threshold=0.01, cell_skip_threshold=1e-3) for r in views]
+        torch.cuda.synchronize()
+        same = all(torch.equal(a.view(torch.int16), b.view(torch.int16)) for a, b in zip(frames[True], frames[False]))
+        print(json.dumps({"compare_layouts": {"poses": [0, 8, 21, 5], "frames_identical": same}}), flush=True)
+        return
 
     W, H = args.width, args.height
     poses = []
