@@ -154,6 +154,9 @@ def main():
     ap.add_argument("--no-c5", action="store_true", help="skip the config-5 fisheye rolling-shutter training step")
     ap.add_argument("--c5-only", action="store_true", help="only the config-5 training step")
     ap.add_argument("--voronoi-only", action="store_true", help="only the GPU Voronoi build (profiling)")
+    ap.add_argument("--c4-only", action="store_true",
+                    help="only the config-4 q8 launch (8 cameras), with the q8 footprint tables and then without "
+                         "(profiling; no CPU leg)")
     ap.add_argument("--compare-layouts", action="store_true",
                     help="only 4 serial C3 frames (poses 0, 8, 21, 5) through the packed walk layout and footprint "
                          "tables, then through the reference's arrays and texels, in screen order (rocprofv3 --pmc)")
@@ -201,6 +204,16 @@ def main():
     inf = VoroTracingInfer(model, sort_morton=True, quantize="fp16")
     torch.cuda.synchronize()
     log(f"inference prep done ({time.time() - t0:.1f}s)")
+    if args.c4_only:
+        poses = [torch.from_numpy(camera.orbit_rays(k, args.width, args.height, n=args.poses)).to(dev)
+                 for k in range(args.poses)]
+        out = {}
+        for tables in (True, False):
+            VoroTracingInfer.quad_maps = tables
+            out["with_tables" if tables else "without_tables"] = c4_q8(model, poses, dev, log, 0.01, 1e-3, cpu=False)
+        VoroTracingInfer.quad_maps = True
+        print(json.dumps({"c4_q8": out}), flush=True)
+        return
     if args.compare_layouts:
         inf.adaptive_tile_order = False
         views = [torch.from_numpy(camera.orbit_rays(k, args.width, args.height)).to(dev) for k in (0, 8, 21, 5)]
