@@ -157,3 +157,11 @@ def test_quad_table_bytes():
     assert native.QuadMaps.table_bytes(f16, f16) == 10 * 32 * 25 * 2
     assert native.QuadMaps.table_bytes(f16_8, f16) == 10 * 32 * (81 + 25)
     assert native.QuadMaps.table_bytes(q8, q8) == 10 * 16 * 25 * 2
+
+
+def test_quad_maps_reject_mismatched_maps():
+    """The footprint tables are built for one scene: maps with different row
+    counts are refused on the host, before any launch."""
+    from vorotracing_amd import native
+    with pytest.raises(ValueError, match="rows"):
+        native.QuadMaps.build(torch.zeros((10, 64), dtype=torch.float16), torch.zeros((9, 64), dtype=torch.float16))
